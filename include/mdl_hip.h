@@ -1,0 +1,316 @@
+/*
+ * mdl_hip.h -- C ABI of the MI355X (gfx950) sparse-feature path.
+ *
+ * The library libmdl_hip.so implements, as hand-written HIP kernels, the
+ * single-GPU sparse hot path of an MDL/RankMixer-style ranker:
+ *
+ *   raw int64 hashes --bucketize--> ids --lookup/pool--> per-feature slots
+ *   upstream grads  --sort/unique/segment-reduce--> per-row grads
+ *                   --row-wise Adagrad--> updated rows + accumulators
+ *
+ * Every pointer argument is a device address unless its comment says "host".
+ * `stream` is a hipStream_t passed as void*; every kernel of a call runs on it
+ * in order and no call synchronises the device.  All calls return MDL_OK (0)
+ * or a negative MDL_ERR_* code; mdl_last_error() gives the message of the
+ * calling thread's last failure.
+ *
+ * Reference interfaces (paths relative to the wcrmu/MDL source tree) are
+ * named next to each entry point.
+ */
+#ifndef MDL_HIP_H
+#define MDL_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+enum {
+  MDL_OK = 0,
+  MDL_ERR_INVALID = -1,     /* bad argument (shape, dtype, alignment, size) */
+  MDL_ERR_HIP = -2,         /* a HIP runtime call failed */
+  MDL_ERR_WORKSPACE = -3,   /* workspace smaller than the *_workspace_bytes query */
+  MDL_ERR_UNSUPPORTED = -4  /* legal input outside what this build implements */
+};
+
+enum { MDL_F32 = 0, MDL_BF16 = 1 };
+
+/* Pooling of one feature's bags. NONE: every id is its own output row. */
+enum { MDL_POOL_NONE = 0, MDL_POOL_SUM = 1, MDL_POOL_MEAN = 2 };
+
+/* Feature flags. EXCLUDE_NULL is the "exclude" null policy: ids equal to 0
+ * carry weight 0 in the pooled sum and in the mean's denominator
+ * (src/model.py:554-557); without it ("include_as_padding") every id counts. */
+enum { MDL_FLAG_EXCLUDE_NULL = 1 };
+
+enum { MDL_BUCKET_PRE_HASHED = 0, MDL_BUCKET_MOD = 1 };
+
+/* Sequence output order (src/model.py:3074-3100). */
+enum { MDL_SEQ_OLDEST_TO_NEWEST = 0, MDL_SEQ_NEWEST_TO_OLDEST = 1 };
+
+/*
+ * One feature (lookup request) of a grouped call.  The array of descriptors
+ * lives in device memory.  Features that alias one table (shared embeddings)
+ * carry the same weight/state/row_base/table.
+ *
+ * Ids of feature f are ids[ids_begin, ids_begin + num_ids).  A pooled feature
+ * has num_bags bags whose bounds are offsets[bag_base .. bag_base+num_bags]
+ * (absolute indices into ids, non-decreasing).  A MDL_POOL_NONE feature has
+ * one output row per id and ignores bag_base/num_bags.
+ *
+ * Output row r of feature f is out + r*out_stride (elements of odtype); the
+ * upstream gradient has the same layout at grad.  For the backward, output
+ * row r of feature f is the sort payload payload_base + r.
+ */
+typedef struct mdl_feature {
+  uint64_t weight;        /* table rows [num_rows, dim], row-major, contiguous */
+  uint64_t state;         /* fp32 row-wise Adagrad accumulator [num_rows], 0 if unused */
+  uint64_t out;           /* output row 0 */
+  uint64_t grad;          /* upstream gradient row 0, 0 when no backward */
+  int64_t num_rows;
+  int64_t out_stride;     /* elements between consecutive output/gradient rows */
+  int64_t row_base;       /* first sort key of the table: key = row_base + id */
+  int64_t payload_base;   /* first sort payload of this feature's output rows */
+  int64_t ids_begin;
+  int64_t num_ids;
+  int64_t bag_base;
+  int64_t num_bags;
+  int32_t dim;
+  int32_t wdtype;         /* MDL_F32 / MDL_BF16: weight rows */
+  int32_t odtype;         /* MDL_F32 / MDL_BF16: out and grad rows */
+  int32_t pooling;        /* MDL_POOL_* */
+  int32_t flags;          /* MDL_FLAG_* */
+  int32_t padding_idx;    /* ids equal to it get no gradient (F.embedding padding_idx) */
+  int32_t table;          /* index into the mdl_table array of the backward */
+  int32_t reserved;
+} mdl_feature;            /* 128 bytes */
+
+/* A unit of forward work: bags [first, first+count) of one pooled feature, or
+ * ids [first, first+count) (relative to ids_begin) of a MDL_POOL_NONE feature. */
+typedef struct mdl_chunk {
+  int32_t feature;
+  int32_t count;
+  int64_t first;
+} mdl_chunk;              /* 16 bytes */
+
+/*
+ * One table of a grouped backward.  Sort keys of the table are
+ * [row_base, row_base + num_rows); tables are ordered by row_base.
+ * `feature` is the only feature reading the table, or -1 when several alias it.
+ */
+typedef struct mdl_table {
+  uint64_t weight;
+  uint64_t state;
+  int64_t num_rows;
+  int64_t row_base;
+  int32_t dim;
+  int32_t wdtype;
+  int32_t feature;
+  int32_t gdtype;         /* MDL_F32 / MDL_BF16: gradient rows of every feature reading it */
+} mdl_table;              /* 48 bytes */
+
+/* ---------------------------------------------------------------- misc --- */
+
+const char* mdl_last_error(void);
+int32_t mdl_abi_version(void);
+
+/* ------------------------------------------------------------ bucketing --- */
+
+/*
+ * out[i] = bucket of raw[i].  MDL_BUCKET_PRE_HASHED: (uint64(raw) & (B-1)) + 1
+ * with B = num_buckets a power of two, null (valid[i]==0) -> 0, and a non-null 0
+ * counted in *error_count when validate_nonzero (the id is still (0&(B-1))+1).
+ * Replaces src/features.py:360-376 and the vectorised src/dataloader.py:8463-8493,
+ * src/dataloader.py:10173-10186.
+ * MDL_BUCKET_MOD: 1 + floormod(raw - 1, num_buckets - 1) (Python floor-mod),
+ * null -> 0.  Replaces the id rule of src/benchmark.py:1246-1250.
+ * valid may be NULL (all non-null).  error_count may be NULL.
+ */
+int mdl_bucketize(const int64_t* raw, const uint8_t* valid, int64_t n,
+                  int64_t num_buckets, int32_t mode, int32_t validate_nonzero,
+                  int64_t* out, int32_t* error_count, void* stream);
+
+/* --------------------------------------------------------------- offsets --- */
+
+/* offsets[0] = 0, offsets[i+1] = offsets[i] + lengths[i]; n+1 outputs.
+ * Replaces the segment layout of repeat_interleave(arange(B), lengths) in
+ * src/model.py:560-563,666-669 (CSR values+lengths, src/dataloader.py:8607-8665). */
+size_t mdl_offsets_workspace_bytes(int64_t n);
+int mdl_lengths_to_offsets(const int64_t* lengths, int64_t n, int64_t* offsets,
+                           void* workspace, size_t workspace_bytes, void* stream);
+
+/* -------------------------------------------------------------- planning --- */
+
+/* Host helper: split every feature into forward chunks of about target_ids ids.
+ * feats_host: host copy of the descriptors.  Writes at most `capacity`
+ * chunks to chunks_host (host, may be NULL) and returns the number needed,
+ * or a negative MDL_ERR_* code. */
+int64_t mdl_plan_chunks(const mdl_feature* feats_host, int32_t num_features,
+                        int32_t target_ids, mdl_chunk* chunks_host, int64_t capacity);
+
+/* ------------------------------------------------------------- forward --- */
+
+/*
+ * Grouped lookup + pooling of every chunk, one launch for all features.
+ *   MDL_POOL_NONE : out row r = weight[ids[ids_begin + r]]      (F.embedding,
+ *                   src/embeddings.py:438-473, grouped :1646-1709)
+ *   MDL_POOL_SUM  : out row b = sum_i w_i * weight[id_i]      (embedding_bag sum)
+ *   MDL_POOL_MEAN : out row b = sum_i w_i * weight[id_i] / max(sum_i w_i, 1)
+ *                   (src/model.py:509-570, batched :590-678)
+ * with w_i = 0 for id 0 under MDL_FLAG_EXCLUDE_NULL and 1 otherwise; sums in
+ * fp32, one rounding to odtype.  Empty bags give 0.  Ids outside
+ * [0, num_rows) contribute 0 and are counted in *error_count (may be NULL);
+ * so are bag offsets outside the feature's id range (clamped into it) and
+ * pooled chunks of more than 256 bags (skipped).
+ *
+ * When sort_keys is not NULL the call also writes, for every id position i of
+ * every feature, the backward sort key and payload:
+ *   sort_keys[i]    = row_base + id, or `sentinel` when id is padding_idx,
+ *                     invalid, or 0 under MDL_FLAG_EXCLUDE_NULL (no gradient
+ *                     reaches it);
+ *   sort_payload[i] = payload_base + output row of the id.
+ * and, when bag_count is not NULL, bag_count[payload_base + b] = sum_i w_i for
+ * every pooled bag.  sort_keys/sort_payload have one entry per position of
+ * the concatenated ids array.
+ */
+int mdl_forward(const mdl_feature* feats, int32_t num_features,
+                const mdl_chunk* chunks, int64_t num_chunks,
+                const int64_t* ids, const int64_t* offsets,
+                uint32_t* sort_keys, uint32_t* sort_payload, uint32_t sentinel,
+                float* bag_count, int32_t* error_count, void* stream);
+
+/*
+ * Sequence gather without pooling, right-aligned into a padded window
+ * (src/model.py:3022-3072, alignment :2989-3020, order :3074-3100).
+ * ids: [batch, in_len] right-padded; lengths: [batch] (clamped to out_len).
+ * out: [batch, out_len, dim] (odtype); mask: [batch, out_len] bytes.
+ * Position p of row b is valid when p >= out_len - len_b; it holds
+ * weight[ids[b, p - start]] (oldest_to_newest) or weight[ids[b, len_b-1-(p-start)]]
+ * (newest_to_oldest); invalid positions hold 0.
+ * feature->out is ignored (out is passed here); feature->payload_base and
+ * row_base are used when sort_keys is not NULL: for input position (b, k),
+ * sort_keys[k + b*in_len] = row_base + id (sentinel when k >= len_b or padding),
+ * payload = payload_base + b*out_len + p(k).
+ */
+int mdl_sequence_forward(const mdl_feature* feature_host, const int64_t* ids,
+                         const int64_t* lengths, int64_t batch, int64_t in_len,
+                         int64_t out_len, int32_t order, void* out, uint8_t* mask,
+                         uint32_t* sort_keys, uint32_t* sort_payload,
+                         uint32_t sentinel, int32_t* error_count, void* stream);
+
+/* ---------------------------------------------------------------- sort --- */
+
+/*
+ * Stable LSD radix sort of (key, payload) pairs on the low key_bits bits,
+ * 8 bits per pass, ping-ponging between (keys, payload) and (keys_alt,
+ * payload_alt).  *result_in_alt (host) is set to 1 when the sorted pairs end
+ * in the _alt buffers.  Equal keys keep input order, so the segment reduction
+ * that follows sums duplicates in a fixed order (deterministic), unlike the
+ * fp32-atomic index_add_ of the reference (src/optim.py:321-324 coalesce).
+ */
+size_t mdl_sort_workspace_bytes(int64_t n);
+int mdl_sort_pairs(uint32_t* keys, uint32_t* payload, uint32_t* keys_alt,
+                   uint32_t* payload_alt, int64_t n, int32_t key_bits,
+                   void* workspace, size_t workspace_bytes, int32_t* result_in_alt,
+                   void* stream);
+
+/* torch.unique(sorted=True, return_inverse=True, return_counts=True) of
+ * ids in [0, 2^key_bits): unique_out[U], inverse_out[n], counts_out[U] (counts
+ * may be NULL), *num_unique written to device memory.  Replaces the
+ * world>1 dedup of src/embeddings.py:514-519,549-553. */
+size_t mdl_unique_workspace_bytes(int64_t n);
+int mdl_unique(const int64_t* ids, int64_t n, int32_t key_bits, int64_t* unique_out,
+               int64_t* inverse_out, int64_t* counts_out, int64_t* num_unique,
+               void* workspace, size_t workspace_bytes, void* stream);
+
+/* ------------------------------------------------------------ backward --- */
+
+/*
+ * The backward of a grouped call consumes the sort keys/payloads written by
+ * mdl_forward / mdl_sequence_forward (n entries, keys < 2^key_bits; the
+ * sentinel must be < 2^key_bits too).  It sorts them in place (keys/payload
+ * and the workspace are clobbered), cuts the sorted array into chunks of
+ * <= 1024 entries that never straddle two tables and reduces every run of
+ * equal keys.  The num_tables tables (device array) are ordered by row_base,
+ * cover every non-sentinel key, and their gradients are 16-byte aligned with
+ * row strides that are multiples of 16 bytes whenever dim*sizeof(weight) is.
+ * dim <= 64*16/sizeof(weight) (256 fp32, 512 bf16) and max_dim >= every dim.
+ * The per-id gradient of a pooled id is grad[row b] / max(bag_count, 1) (mean)
+ * or grad[row b] (sum, none); padding ids get none (src/model.py:564-570 and
+ * the F.embedding sparse backward).  Duplicate ids are summed in input order
+ * in fp32, deterministically.
+ */
+size_t mdl_backward_workspace_bytes(int64_t n, int32_t num_tables, int32_t max_dim);
+
+/*
+ * Sort keys/payloads of a plain row-index list, for coalescing an uncoalesced
+ * COO gradient (indices [n], values [n, dim]) with the calls below as one
+ * MDL_POOL_NONE feature whose gradient rows are the values
+ * (sparse coalesce of src/optim.py:323-324, src/train.py:5388-5396):
+ * keys[i] = row_base + ids[i] (sentinel when ids[i] == padding_idx, pass -1
+ * for none, or outside [0, num_rows), counted in *error_count),
+ * payload[i] = payload_base + i.
+ */
+int mdl_sparse_keys(const int64_t* ids, int64_t n, int64_t num_rows, int64_t row_base,
+                    int64_t payload_base, int64_t padding_idx, uint32_t* keys,
+                    uint32_t* payload, uint32_t sentinel, int32_t* error_count,
+                    void* stream);
+
+/*
+ * Fused backward + row-wise Adagrad: every distinct (table, row) is updated
+ * once from its summed gradient g:
+ *   acc += sum(g^2)/dim;  w = w - lr * (g / (sqrt(acc) + eps))
+ * rounded once to the weight dtype (round-to-nearest-even for bf16).
+ * Semantics of src/optim.py:31-62 (Triton kernel) and :299-357 (step).
+ */
+int mdl_backward_adagrad(const mdl_feature* feats, int32_t num_features,
+                         const mdl_table* tables, int32_t num_tables, int32_t max_dim,
+                         uint32_t* sort_keys, uint32_t* sort_payload, int64_t n,
+                         int32_t key_bits, const float* bag_count, float lr, float eps,
+                         void* workspace, size_t workspace_bytes, void* stream);
+
+/*
+ * Coalesced sparse gradients, the autograd contract of src/optim.py:317-329 and
+ * src/train.py:5730-5742 (rows ascending and unique), in two calls:
+ * mdl_backward_count sorts and writes unique_range[2t], unique_range[2t+1]
+ * (device int64), the global distinct-row index range of table t, so
+ * U_t = unique_range[2t+1] - unique_range[2t];  mdl_backward_coalesce, with the
+ * same keys/payload/key_bits/workspace, then writes rows (int64 [U_t]) and
+ * values ([U_t, dim], weight dtype) at the device addresses rows_addr[t] and
+ * values_addr[t] (device arrays of num_tables addresses).
+ */
+int mdl_backward_count(const mdl_table* tables, int32_t num_tables, int32_t max_dim,
+                       uint32_t* sort_keys, uint32_t* sort_payload, int64_t n,
+                       int32_t key_bits, int64_t* unique_range,
+                       void* workspace, size_t workspace_bytes, void* stream);
+int mdl_backward_coalesce(const mdl_feature* feats, int32_t num_features,
+                          const mdl_table* tables, int32_t num_tables, int32_t max_dim,
+                          uint32_t* sort_keys, uint32_t* sort_payload, int64_t n,
+                          int32_t key_bits, const float* bag_count,
+                          const int64_t* unique_range, const uint64_t* rows_addr,
+                          const uint64_t* values_addr, void* workspace,
+                          size_t workspace_bytes, void* stream);
+
+/* ------------------------------------------------------------- update --- */
+
+/*
+ * Row-wise Adagrad on unique rows of one table (fused_rowwise_adagrad_update,
+ * src/optim.py:68-108, kernel :31-62): for every i,
+ *   acc[rows[i]] += sum_j values[i,j]^2 / dim
+ *   weight[rows[i]] = weight[rows[i]] - lr * values[i] / (sqrt(acc) + eps).
+ * rows must be unique and inside [0, num_rows) (rows outside are skipped and
+ * counted in *error_count, may be NULL).  values_stride in elements.
+ */
+int mdl_rowwise_adagrad(void* weight, int32_t wdtype, int64_t num_rows, int32_t dim,
+                        int64_t weight_stride, float* acc, const int64_t* rows,
+                        int64_t num_touched, const void* values, int32_t vdtype,
+                        int64_t values_stride, float lr, float eps,
+                        int32_t* error_count, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* MDL_HIP_H */

@@ -1,0 +1,534 @@
+// Grouped embedding lookup and bag pooling for gfx950.
+//
+// One wavefront owns one chunk (a run of whole bags of one feature, or a run
+// of ids of an unpooled feature).  A row of `dim` elements is spread over L
+// lanes (L = next_pow2(dim / C), C elements = 16 bytes per lane), so a wave
+// gathers G = 64 / L rows per pass; four passes are issued before any is
+// reduced to keep 4*G row loads in flight per wave.
+//
+// Pooling walks the chunk's ids as one flat stream (bags are consecutive
+// segments of it).  Each pass forms an inclusive segmented scan over the G
+// slots (bag index is the segment key) with cross-lane permutes, adds the
+// carry of a bag that began in an earlier pass, and the slot holding a bag's
+// last id writes that bag's pooled row.  Every id costs the same regardless
+// of how the bag lengths are distributed, so ragged bags (lengths 1..32 in
+// the RankMixer workload) keep all lanes busy, and the summation order is
+// fixed by the chunk layout alone (deterministic).  Bag bounds are staged in
+// LDS once per chunk.
+#include "common.cuh"
+
+namespace mdl {
+
+constexpr int kFwdWaves = 4;
+constexpr int kMaxBagsPerChunk = 256;
+constexpr int kUnroll = 4;
+
+struct FwdArgs {
+  const mdl_feature* feats;
+  const mdl_chunk* chunks;
+  int64_t num_chunks;
+  const int64_t* ids;
+  const int64_t* offsets;
+  uint32_t* keys;
+  uint32_t* payload;
+  float* bag_count;
+  int32_t* error_count;
+  uint32_t sentinel;
+};
+
+// Wave-uniform copy of the descriptor fields a chunk needs.
+struct Feat {
+  const void* weight;
+  void* out;
+  int64_t num_rows, out_stride, row_base, payload_base, ids_begin, num_ids, bag_base;
+  int dim, wdtype, odtype, pooling, flags, padding_idx;
+};
+
+__device__ __forceinline__ int64_t uni64(int64_t v) {
+  int lo = __builtin_amdgcn_readfirstlane((int)(v & 0xffffffff));
+  int hi = __builtin_amdgcn_readfirstlane((int)(v >> 32));
+  return (int64_t)(((uint64_t)(uint32_t)hi << 32) | (uint32_t)lo);
+}
+__device__ __forceinline__ int uni32(int v) { return __builtin_amdgcn_readfirstlane(v); }
+
+__device__ __forceinline__ Feat load_feat(const mdl_feature* p) {
+  Feat f;
+  f.weight = (const void*)uni64((int64_t)p->weight);
+  f.out = (void*)uni64((int64_t)p->out);
+  f.num_rows = uni64(p->num_rows);
+  f.out_stride = uni64(p->out_stride);
+  f.row_base = uni64(p->row_base);
+  f.payload_base = uni64(p->payload_base);
+  f.ids_begin = uni64(p->ids_begin);
+  f.num_ids = uni64(p->num_ids);
+  f.bag_base = uni64(p->bag_base);
+  f.dim = uni32(p->dim);
+  f.wdtype = uni32(p->wdtype);
+  f.odtype = uni32(p->odtype);
+  f.pooling = uni32(p->pooling);
+  f.flags = uni32(p->flags);
+  f.padding_idx = uni32(p->padding_idx);
+  return f;
+}
+
+// Whether every row access of the feature can use 16-byte vectors.
+__device__ __forceinline__ bool vec_ok(const Feat& f) {
+  const int wsz = f.wdtype == MDL_BF16 ? 2 : 4;
+  const int osz = f.odtype == MDL_BF16 ? 2 : 4;
+  const int c = 16 / wsz;
+  return ((uint64_t)f.weight % 16 == 0) && ((uint64_t)f.out % 16 == 0) &&
+         ((int64_t)f.dim * wsz) % 16 == 0 && (f.out_stride * osz) % 16 == 0 &&
+         ((int64_t)c * osz) % 16 == 0;
+}
+
+__device__ __forceinline__ void wave_sync() { __builtin_amdgcn_wave_barrier(); __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront"); }
+
+// ------------------------------------------------------------ unpooled --
+
+template <typename TW, typename TO, int C>
+__device__ __forceinline__ void gather_chunk(const Feat& f, int64_t first, int count, const FwdArgs& a) {
+  const int lane = lane_id();
+  const int L = lanes_for(f.dim, C);
+  const int G = kWave / L;
+  const int slot = lane / L, sub = lane % L;
+  const int ncb = (f.dim + L * C - 1) / (L * C);
+  const TW* W = static_cast<const TW*>(f.weight);
+  TO* out = static_cast<TO*>(f.out);
+  int bad = 0;
+  for (int cb = 0; cb < ncb; ++cb) {
+    const int col = (cb * L + sub) * C;
+    const bool col_ok = col < f.dim;
+    for (int base = 0; base < count; base += G * kUnroll) {
+      float v[kUnroll][C];
+      int64_t id[kUnroll];
+#pragma unroll
+      for (int u = 0; u < kUnroll; ++u) {
+        const int i = base + u * G + slot;
+        const bool valid = i < count;
+        id[u] = valid ? a.ids[f.ids_begin + first + i] : 0;
+        const bool in_range = (uint64_t)id[u] < (uint64_t)f.num_rows;
+#pragma unroll
+        for (int k = 0; k < C; ++k) v[u][k] = 0.f;
+        if (valid && in_range && col_ok) RowIO<TW, C>::load(W + id[u] * f.dim + col, v[u]);
+        if (cb == 0 && sub == 0 && valid) {
+          bad += !in_range;
+          if (a.keys != nullptr) {
+            const int64_t e = f.ids_begin + first + i;
+            a.keys[e] = (in_range && id[u] != f.padding_idx) ? (uint32_t)(f.row_base + id[u]) : a.sentinel;
+            a.payload[e] = (uint32_t)(f.payload_base + first + i);
+          }
+        }
+      }
+#pragma unroll
+      for (int u = 0; u < kUnroll; ++u) {
+        const int i = base + u * G + slot;
+        if (i < count && col_ok) RowIO<TO, C>::store(out + (first + i) * f.out_stride + col, v[u]);
+      }
+    }
+  }
+  if (bad && a.error_count) atomicAdd(a.error_count, bad);
+}
+
+// -------------------------------------------------------------- pooled --
+
+template <typename TW, typename TO, int C>
+__device__ __forceinline__ void pooled_chunk(const Feat& f, int64_t first_bag, int nb, int64_t* s_off, const FwdArgs& a) {
+  const int lane = lane_id();
+  // Offsets are clamped into the feature's own id range, so lengths that do
+  // not add up to the ids passed can only give wrong sums (and an error
+  // count), never an out-of-bounds read.
+  const int64_t lo = f.ids_begin, hi = f.ids_begin + f.num_ids;
+  int clamped = 0;
+  for (int i = lane; i <= nb; i += kWave) {
+    int64_t o = a.offsets[f.bag_base + first_bag + i];
+    const int64_t oc = o < lo ? lo : (o > hi ? hi : o);
+    clamped += oc != o;
+    s_off[i] = oc;
+  }
+  if (clamped && a.error_count) atomicAdd(a.error_count, clamped);
+  wave_sync();
+  const int64_t e_begin = s_off[0], e_end = s_off[nb];
+  const int L = lanes_for(f.dim, C);
+  const int G = kWave / L;
+  const int slot = lane / L, sub = lane % L;
+  const int ncb = (f.dim + L * C - 1) / (L * C);
+  const bool exclude = (f.flags & MDL_FLAG_EXCLUDE_NULL) != 0;
+  const bool mean = f.pooling == MDL_POOL_MEAN;
+  const TW* W = static_cast<const TW*>(f.weight);
+  TO* out = static_cast<TO*>(f.out);
+  const int last_lane_base = (G - 1) * L;
+  int bad = 0;
+
+  for (int cb = 0; cb < ncb; ++cb) {
+    const int col = (cb * L + sub) * C;
+    const bool col_ok = col < f.dim;
+    float carry[C];
+#pragma unroll
+    for (int k = 0; k < C; ++k) carry[k] = 0.f;
+    float carry_w = 0.f;
+    int carry_seg = -2;
+    int bag = 0;  // cursor: bag (relative to the chunk) of this slot's current id
+    for (int64_t base = e_begin; base < e_end; base += (int64_t)G * kUnroll) {
+      float v[kUnroll][C];
+      float wt[kUnroll];
+      int seg[kUnroll];
+      bool tail[kUnroll];
+#pragma unroll
+      for (int u = 0; u < kUnroll; ++u) {
+        const int64_t e = base + (int64_t)u * G + slot;
+        const bool valid = e < e_end;
+        const int64_t id = valid ? a.ids[e] : 0;
+        if (valid) {
+          while (s_off[bag + 1] <= e) ++bag;
+        }
+        const bool in_range = (uint64_t)id < (uint64_t)f.num_rows;
+        float w = (exclude && id == 0) ? 0.f : 1.f;
+        if (!in_range) w = 0.f;
+        seg[u] = valid ? bag : -1;
+        wt[u] = valid ? w : 0.f;
+        tail[u] = valid && (e + 1 == s_off[bag + 1]);
+#pragma unroll
+        for (int k = 0; k < C; ++k) v[u][k] = 0.f;
+        if (valid && w != 0.f && col_ok) RowIO<TW, C>::load(W + id * f.dim + col, v[u]);
+        if (cb == 0 && sub == 0 && valid) {
+          bad += !in_range;
+          if (a.keys != nullptr) {
+            // w == 0 covers invalid ids and nulls under "exclude": their
+            // gradient is exactly zero, so they take no part in the backward.
+            a.keys[e] = (w != 0.f && id != f.padding_idx) ? (uint32_t)(f.row_base + id) : a.sentinel;
+            a.payload[e] = (uint32_t)(f.payload_base + first_bag + bag);
+          }
+        }
+      }
+#pragma unroll
+      for (int u = 0; u < kUnroll; ++u) {
+        // Inclusive segmented scan over the G slots of this pass.
+        for (int d = 1; d < G; d <<= 1) {
+          const int src = slot >= d ? lane - d * L : lane;
+          const int oseg = shfl_i(seg[u], src);
+          const float ow = shfl_f(wt[u], src);
+          float ov[C];
+#pragma unroll
+          for (int k = 0; k < C; ++k) ov[k] = shfl_f(v[u][k], src);
+          if (slot >= d && oseg == seg[u]) {
+            wt[u] += ow;
+#pragma unroll
+            for (int k = 0; k < C; ++k) v[u][k] += ov[k];
+          }
+        }
+        if (seg[u] == carry_seg) {
+          wt[u] += carry_w;
+#pragma unroll
+          for (int k = 0; k < C; ++k) v[u][k] += carry[k];
+        }
+        if (tail[u]) {
+          const int64_t b = first_bag + seg[u];
+          if (col_ok) {
+            float r[C];
+            const float den = fmaxf(wt[u], 1.f);
+#pragma unroll
+            for (int k = 0; k < C; ++k) r[k] = mean ? v[u][k] / den : v[u][k];
+            RowIO<TO, C>::store(out + b * f.out_stride + col, r);
+          }
+          if (cb == 0 && sub == 0 && a.bag_count != nullptr) a.bag_count[f.payload_base + b] = wt[u];
+        }
+        const int src = last_lane_base + sub;
+        const int lseg = shfl_i(seg[u], src);
+        const int ltail = shfl_i((int)tail[u], src);
+        carry_w = shfl_f(wt[u], src);
+#pragma unroll
+        for (int k = 0; k < C; ++k) carry[k] = shfl_f(v[u][k], src);
+        carry_seg = (lseg >= 0 && !ltail) ? lseg : -2;
+      }
+    }
+  }
+  // Empty bags pool to zero.
+  for (int b = slot; b < nb; b += G) {
+    if (s_off[b] == s_off[b + 1]) {
+      float z[C];
+#pragma unroll
+      for (int k = 0; k < C; ++k) z[k] = 0.f;
+      for (int cb = 0; cb < ncb; ++cb) {
+        const int col = (cb * L + sub) * C;
+        if (col < f.dim) RowIO<TO, C>::store(out + (first_bag + b) * f.out_stride + col, z);
+      }
+      if (sub == 0 && a.bag_count != nullptr) a.bag_count[f.payload_base + first_bag + b] = 0.f;
+    }
+  }
+  if (bad && a.error_count) atomicAdd(a.error_count, bad);
+}
+
+template <typename TW, typename TO, int C>
+__device__ __forceinline__ void run_chunk(const Feat& f, const mdl_chunk& ch, int64_t* s_off, const FwdArgs& a) {
+  if (f.pooling == MDL_POOL_NONE)
+    gather_chunk<TW, TO, C>(f, ch.first, ch.count, a);
+  else
+    pooled_chunk<TW, TO, C>(f, ch.first, ch.count, s_off, a);
+}
+
+__global__ __launch_bounds__(kFwdWaves * kWave) void forward_kernel(FwdArgs a) {
+  __shared__ int64_t s_off[kFwdWaves][kMaxBagsPerChunk + 1];
+  const int w = threadIdx.x / kWave;
+  const int64_t blk = xcd_block(blockIdx.x, gridDim.x);
+  const int64_t c = uni64(blk * kFwdWaves + w);
+  if (c >= a.num_chunks) return;
+  mdl_chunk ch;
+  ch.feature = uni32(a.chunks[c].feature);
+  ch.count = uni32(a.chunks[c].count);
+  ch.first = uni64(a.chunks[c].first);
+  const Feat f = load_feat(a.feats + ch.feature);
+  if (f.pooling != MDL_POOL_NONE && (ch.count > kMaxBagsPerChunk || ch.count < 0)) {
+    if (lane_id() == 0 && a.error_count) atomicAdd(a.error_count, 1);
+    return;
+  }
+  const bool v = vec_ok(f);
+  if (f.wdtype == MDL_F32) {
+    if (v) run_chunk<float, float, 4>(f, ch, s_off[w], a);
+    else run_chunk<float, float, 1>(f, ch, s_off[w], a);
+  } else if (f.odtype == MDL_BF16) {
+    if (v) run_chunk<bf16_t, bf16_t, 8>(f, ch, s_off[w], a);
+    else run_chunk<bf16_t, bf16_t, 1>(f, ch, s_off[w], a);
+  } else {
+    if (v) run_chunk<bf16_t, float, 8>(f, ch, s_off[w], a);
+    else run_chunk<bf16_t, float, 1>(f, ch, s_off[w], a);
+  }
+}
+
+// ------------------------------------------------------------ sequences --
+
+struct SeqArgs {
+  Feat f;
+  const int64_t* ids;
+  const int64_t* lengths;
+  int64_t batch, in_len, out_len;
+  int order;
+  void* out;
+  uint8_t* mask;
+  uint32_t* keys;
+  uint32_t* payload;
+  uint32_t sentinel;
+  int32_t* error_count;
+};
+
+__device__ __forceinline__ int64_t seq_len(const SeqArgs& a, int64_t b) {
+  int64_t n = a.lengths[b];
+  n = n < 0 ? 0 : n;
+  n = n > a.out_len ? a.out_len : n;
+  return n > a.in_len ? a.in_len : n;
+}
+
+// One slot per output row (b, p) of [batch, out_len].
+template <typename TW, typename TO, int C>
+__device__ __forceinline__ void seq_rows(const SeqArgs& a, int64_t row0, int64_t nrows) {
+  const Feat& f = a.f;
+  const int lane = lane_id();
+  const int L = lanes_for(f.dim, C);
+  const int G = kWave / L;
+  const int slot = lane / L, sub = lane % L;
+  const int ncb = (f.dim + L * C - 1) / (L * C);
+  const TW* W = static_cast<const TW*>(f.weight);
+  TO* out = static_cast<TO*>(a.out);
+  int bad = 0;
+  for (int cb = 0; cb < ncb; ++cb) {
+    const int col = (cb * L + sub) * C;
+    const bool col_ok = col < f.dim;
+    for (int64_t base = 0; base < nrows; base += (int64_t)G * kUnroll) {
+      float v[kUnroll][C];
+#pragma unroll
+      for (int u = 0; u < kUnroll; ++u) {
+        const int64_t r = row0 + base + u * G + slot;
+        const bool in_chunk = base + u * G + slot < nrows;
+        int64_t b = in_chunk ? r / a.out_len : 0;
+        int64_t p = in_chunk ? r - b * a.out_len : 0;
+        const int64_t len = in_chunk ? seq_len(a, b) : 0;
+        const int64_t start = a.out_len - len;
+        const bool valid = in_chunk && p >= start;
+        const int64_t k = a.order == MDL_SEQ_OLDEST_TO_NEWEST ? p - start : len - 1 - (p - start);
+        const int64_t id = valid ? a.ids[b * a.in_len + k] : 0;
+        const bool in_range = (uint64_t)id < (uint64_t)f.num_rows;
+#pragma unroll
+        for (int q = 0; q < C; ++q) v[u][q] = 0.f;
+        if (valid && in_range && col_ok) RowIO<TW, C>::load(W + id * f.dim + col, v[u]);
+        if (cb == 0 && sub == 0 && in_chunk) {
+          bad += valid && !in_range;
+          if (a.mask) a.mask[r] = valid ? 1 : 0;
+        }
+      }
+#pragma unroll
+      for (int u = 0; u < kUnroll; ++u) {
+        const int64_t i = base + u * G + slot;
+        if (i < nrows && col_ok) RowIO<TO, C>::store(out + (row0 + i) * f.out_stride + col, v[u]);
+      }
+    }
+  }
+  if (bad && a.error_count) atomicAdd(a.error_count, bad);
+}
+
+constexpr int kSeqRowsPerWave = 256;
+
+__global__ __launch_bounds__(kFwdWaves * kWave) void sequence_kernel(SeqArgs a) {
+  const int w = threadIdx.x / kWave;
+  const int64_t blk = xcd_block(blockIdx.x, gridDim.x);
+  const int64_t total = a.batch * a.out_len;
+  const int64_t row0 = uni64((blk * kFwdWaves + w) * kSeqRowsPerWave);
+  if (row0 >= total) return;
+  const int64_t nrows = total - row0 < kSeqRowsPerWave ? total - row0 : kSeqRowsPerWave;
+  Feat f = a.f;
+  const bool v = ((uint64_t)f.weight % 16 == 0) && ((uint64_t)a.out % 16 == 0) &&
+                 ((int64_t)f.dim * (f.wdtype == MDL_BF16 ? 2 : 4)) % 16 == 0 &&
+                 (f.wdtype == MDL_F32 || f.odtype == MDL_BF16 || f.dim % 8 == 0);
+  if (f.wdtype == MDL_F32) {
+    if (v) seq_rows<float, float, 4>(a, row0, nrows);
+    else seq_rows<float, float, 1>(a, row0, nrows);
+  } else if (f.odtype == MDL_BF16) {
+    if (v) seq_rows<bf16_t, bf16_t, 8>(a, row0, nrows);
+    else seq_rows<bf16_t, bf16_t, 1>(a, row0, nrows);
+  } else {
+    if (v) seq_rows<bf16_t, float, 8>(a, row0, nrows);
+    else seq_rows<bf16_t, float, 1>(a, row0, nrows);
+  }
+}
+
+// Sort keys/payloads of the input positions (b, k) of a sequence feature.
+__global__ void sequence_keys_kernel(SeqArgs a) {
+  const int64_t n = a.batch * a.in_len;
+  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n;
+       i += (int64_t)gridDim.x * blockDim.x) {
+    const int64_t b = i / a.in_len;
+    const int64_t k = i - b * a.in_len;
+    const int64_t len = seq_len(a, b);
+    const int64_t id = a.ids[i];
+    const bool valid = k < len && (uint64_t)id < (uint64_t)a.f.num_rows && id != a.f.padding_idx;
+    const int64_t start = a.out_len - len;
+    const int64_t p = a.order == MDL_SEQ_OLDEST_TO_NEWEST ? start + k : start + (len - 1 - k);
+    a.keys[i] = valid ? (uint32_t)(a.f.row_base + id) : a.sentinel;
+    a.payload[i] = valid ? (uint32_t)(a.f.payload_base + b * a.out_len + p) : 0u;
+  }
+}
+
+}  // namespace mdl
+
+using namespace mdl;
+
+extern "C" {
+
+int64_t mdl_plan_chunks(const mdl_feature* feats, int32_t num_features, int32_t target_ids,
+                        mdl_chunk* chunks, int64_t capacity) {
+  if (num_features < 0 || target_ids <= 0) return fail(MDL_ERR_INVALID, "mdl_plan_chunks: bad arguments");
+  int64_t n = 0;
+  for (int32_t fi = 0; fi < num_features; ++fi) {
+    const mdl_feature& f = feats[fi];
+    if (f.pooling == MDL_POOL_NONE) {
+      const int64_t step = target_ids;
+      for (int64_t s = 0; s < f.num_ids; s += step) {
+        if (chunks && n < capacity) {
+          chunks[n].feature = fi;
+          chunks[n].first = s;
+          chunks[n].count = (int32_t)(f.num_ids - s < step ? f.num_ids - s : step);
+        }
+        ++n;
+      }
+    } else {
+      const double avg = f.num_bags > 0 ? (double)f.num_ids / (double)f.num_bags : 1.0;
+      int64_t nb = 1;
+      while (nb * 2 <= kMaxBagsPerChunk && (double)(nb * 2) * (avg > 1.0 ? avg : 1.0) <= (double)target_ids) nb *= 2;
+      for (int64_t s = 0; s < f.num_bags; s += nb) {
+        if (chunks && n < capacity) {
+          chunks[n].feature = fi;
+          chunks[n].first = s;
+          chunks[n].count = (int32_t)(f.num_bags - s < nb ? f.num_bags - s : nb);
+        }
+        ++n;
+      }
+    }
+  }
+  return n;
+}
+
+int mdl_forward(const mdl_feature* feats, int32_t num_features, const mdl_chunk* chunks,
+                int64_t num_chunks, const int64_t* ids, const int64_t* offsets, uint32_t* sort_keys,
+                uint32_t* sort_payload, uint32_t sentinel, float* bag_count, int32_t* error_count,
+                void* stream) {
+  if (num_features < 0 || num_chunks < 0) return fail(MDL_ERR_INVALID, "mdl_forward: negative count");
+  if (num_chunks == 0) return MDL_OK;
+  if (!feats || !chunks || !ids) return fail(MDL_ERR_INVALID, "mdl_forward: null pointer");
+  if ((sort_keys == nullptr) != (sort_payload == nullptr))
+    return fail(MDL_ERR_INVALID, "mdl_forward: sort_keys and sort_payload go together");
+  FwdArgs a;
+  a.feats = feats;
+  a.chunks = chunks;
+  a.num_chunks = num_chunks;
+  a.ids = ids;
+  a.offsets = offsets;
+  a.keys = sort_keys;
+  a.payload = sort_payload;
+  a.bag_count = bag_count;
+  a.error_count = error_count;
+  a.sentinel = sentinel;
+  const int64_t blocks = (num_chunks + kFwdWaves - 1) / kFwdWaves;
+  if (blocks > 0x7fffffff) return fail(MDL_ERR_UNSUPPORTED, "mdl_forward: too many chunks");
+  hipLaunchKernelGGL(forward_kernel, dim3((unsigned)blocks), dim3(kFwdWaves * kWave), 0,
+                     as_stream(stream), a);
+  MDL_CHECK_LAUNCH("forward_kernel");
+  return MDL_OK;
+}
+
+int mdl_sequence_forward(const mdl_feature* feature, const int64_t* ids, const int64_t* lengths,
+                         int64_t batch, int64_t in_len, int64_t out_len, int32_t order, void* out,
+                         uint8_t* mask, uint32_t* sort_keys, uint32_t* sort_payload, uint32_t sentinel,
+                         int32_t* error_count, void* stream) {
+  if (!feature || batch < 0 || in_len < 0 || out_len < 0)
+    return fail(MDL_ERR_INVALID, "mdl_sequence_forward: bad arguments");
+  if (order != MDL_SEQ_OLDEST_TO_NEWEST && order != MDL_SEQ_NEWEST_TO_OLDEST)
+    return fail(MDL_ERR_INVALID, "mdl_sequence_forward: bad order");
+  if ((sort_keys == nullptr) != (sort_payload == nullptr))
+    return fail(MDL_ERR_INVALID, "mdl_sequence_forward: sort_keys and sort_payload go together");
+  SeqArgs a;
+  const mdl_feature& d = *feature;
+  a.f.weight = (const void*)d.weight;
+  a.f.out = out;
+  a.f.num_rows = d.num_rows;
+  a.f.out_stride = d.dim;
+  a.f.row_base = d.row_base;
+  a.f.payload_base = d.payload_base;
+  a.f.ids_begin = 0;
+  a.f.bag_base = 0;
+  a.f.dim = d.dim;
+  a.f.wdtype = d.wdtype;
+  a.f.odtype = d.odtype;
+  a.f.pooling = MDL_POOL_NONE;
+  a.f.flags = d.flags;
+  a.f.padding_idx = d.padding_idx;
+  if (d.dim <= 0) return fail(MDL_ERR_INVALID, "mdl_sequence_forward: dim must be positive");
+  if (d.wdtype == MDL_F32 && d.odtype != MDL_F32)
+    return fail(MDL_ERR_UNSUPPORTED, "mdl_sequence_forward: fp32 weights need fp32 output");
+  a.ids = ids;
+  a.lengths = lengths;
+  a.batch = batch;
+  a.in_len = in_len;
+  a.out_len = out_len;
+  a.order = order;
+  a.out = out;
+  a.mask = mask;
+  a.keys = sort_keys;
+  a.payload = sort_payload;
+  a.sentinel = sentinel;
+  a.error_count = error_count;
+  hipStream_t s = as_stream(stream);
+  const int64_t total = batch * out_len;
+  if (total > 0) {
+    const int64_t waves = (total + kSeqRowsPerWave - 1) / kSeqRowsPerWave;
+    const int64_t blocks = (waves + kFwdWaves - 1) / kFwdWaves;
+    hipLaunchKernelGGL(sequence_kernel, dim3((unsigned)blocks), dim3(kFwdWaves * kWave), 0, s, a);
+    MDL_CHECK_LAUNCH("sequence_kernel");
+  }
+  if (sort_keys != nullptr && batch * in_len > 0) {
+    int64_t blocks = (batch * in_len + 255) / 256;
+    if (blocks > 65536) blocks = 65536;
+    hipLaunchKernelGGL(sequence_keys_kernel, dim3((unsigned)blocks), dim3(256), 0, s, a);
+    MDL_CHECK_LAUNCH("sequence_keys_kernel");
+  }
+  return MDL_OK;
+}
+
+}  // extern "C"

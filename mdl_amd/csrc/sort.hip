@@ -1,0 +1,338 @@
+// Stable LSD radix sort of (uint32 key, uint32 payload) pairs and the
+// torch.unique-style dedup built on it.
+//
+// Each 8-bit pass is three launches:
+//   upsweep   - per-tile digit histogram  -> counts[digit][tile]
+//   scan      - one block per digit scans its row of counts (tile order)
+//   downsweep - ranks the tile's keys stably, stages them in LDS in digit
+//               order and writes each digit's run to its global slot.
+// Ranking inside a wavefront uses ballots: the lanes that share a digit are
+// found by intersecting one ballot per digit bit, and a key's rank is the
+// popcount of its peers on lower lanes plus the wave's running count of that
+// digit.  Keys are visited in index order (item-major, then lane), so equal
+// keys keep their input order; that stability is what makes the later
+// segment reduction of duplicate rows deterministic.
+#include "common.cuh"
+
+namespace mdl {
+
+constexpr int kSortThreads = 256;
+constexpr int kSortWaves = kSortThreads / kWave;
+constexpr int kSortItems = 16;
+constexpr int kSortTile = kSortThreads * kSortItems;
+constexpr int kRadix = 256;
+
+__device__ uint32_t block_exclusive_scan_u32(uint32_t v, uint32_t* smem) {
+  const int tid = threadIdx.x;
+  smem[tid] = v;
+  __syncthreads();
+  for (int d = 1; d < kSortThreads; d <<= 1) {
+    uint32_t o = tid >= d ? smem[tid - d] : 0u;
+    __syncthreads();
+    smem[tid] += o;
+    __syncthreads();
+  }
+  uint32_t incl = smem[tid];
+  __syncthreads();
+  return incl - v;
+}
+
+__global__ __launch_bounds__(kSortThreads) void radix_upsweep(const uint32_t* __restrict__ keys, int64_t n,
+                                                              int shift, uint32_t mask,
+                                                              uint32_t* __restrict__ counts, int ntiles) {
+  __shared__ uint32_t hist[kSortWaves][kRadix];
+  const int tid = threadIdx.x, w = tid / kWave;
+  for (int i = tid; i < kSortWaves * kRadix; i += kSortThreads) (&hist[0][0])[i] = 0u;
+  __syncthreads();
+  const int64_t base = (int64_t)blockIdx.x * kSortTile;
+#pragma unroll
+  for (int i = 0; i < kSortItems; ++i) {
+    const int64_t idx = base + (int64_t)i * kSortThreads + tid;
+    if (idx < n) atomicAdd(&hist[w][(keys[idx] >> shift) & mask], 1u);
+  }
+  __syncthreads();
+  uint32_t s = 0;
+#pragma unroll
+  for (int q = 0; q < kSortWaves; ++q) s += hist[q][tid];
+  counts[(int64_t)tid * ntiles + blockIdx.x] = s;
+}
+
+// Exclusive scan of counts[d][0..ntiles) for digit d = blockIdx.x.
+__global__ __launch_bounds__(kSortThreads) void radix_scan(uint32_t* __restrict__ counts, int ntiles,
+                                                           uint32_t* __restrict__ digit_total) {
+  __shared__ uint32_t smem[kSortThreads];
+  uint32_t* row = counts + (int64_t)blockIdx.x * ntiles;
+  uint32_t carry = 0;
+  constexpr int kPer = 4;
+  for (int base = 0; base < ntiles; base += kSortThreads * kPer) {
+    uint32_t v[kPer];
+    uint32_t s = 0;
+#pragma unroll
+    for (int k = 0; k < kPer; ++k) {
+      const int i = base + threadIdx.x * kPer + k;
+      v[k] = i < ntiles ? row[i] : 0u;
+      s += v[k];
+    }
+    const uint32_t ex = block_exclusive_scan_u32(s, smem);
+    __shared__ uint32_t s_total;
+    if (threadIdx.x == kSortThreads - 1) s_total = ex + s;
+    __syncthreads();
+    uint32_t run = carry + ex;
+#pragma unroll
+    for (int k = 0; k < kPer; ++k) {
+      const int i = base + threadIdx.x * kPer + k;
+      if (i < ntiles) row[i] = run;
+      run += v[k];
+    }
+    carry += s_total;
+    __syncthreads();
+  }
+  if (threadIdx.x == 0) digit_total[blockIdx.x] = carry;
+}
+
+__global__ __launch_bounds__(kSortThreads) void radix_downsweep(
+    const uint32_t* __restrict__ keys_in, const uint32_t* __restrict__ vals_in,
+    uint32_t* __restrict__ keys_out, uint32_t* __restrict__ vals_out, int64_t n, int shift, int bits,
+    const uint32_t* __restrict__ counts, const uint32_t* __restrict__ digit_total, int ntiles) {
+  __shared__ uint32_t s_keys[kSortTile];
+  __shared__ uint32_t s_vals[kSortTile];
+  __shared__ uint32_t s_wh[kSortWaves][kRadix];
+  __shared__ uint32_t s_tile[kRadix];
+  __shared__ uint32_t s_gbase[kRadix];
+  __shared__ uint32_t s_scan[kSortThreads];
+
+  const int tid = threadIdx.x, w = tid / kWave, lane = tid % kWave;
+  const uint32_t mask = (bits >= 32) ? 0xffffffffu : ((1u << bits) - 1u);
+  for (int i = tid; i < kSortWaves * kRadix; i += kSortThreads) (&s_wh[0][0])[i] = 0u;
+  __syncthreads();
+
+  const int64_t tile_base = (int64_t)blockIdx.x * kSortTile;
+  const int64_t wave_base = tile_base + (int64_t)w * (kWave * kSortItems);
+  const uint64_t lt_mask = (lane == 0) ? 0ull : (~0ull >> (64 - lane));
+  uint32_t k[kSortItems], v[kSortItems], rank[kSortItems];
+#pragma unroll
+  for (int i = 0; i < kSortItems; ++i) {
+    const int64_t idx = wave_base + (int64_t)i * kWave + lane;
+    const bool valid = idx < n;
+    k[i] = valid ? keys_in[idx] : 0u;
+    v[i] = valid ? vals_in[idx] : 0u;
+  }
+#pragma unroll
+  for (int i = 0; i < kSortItems; ++i) {
+    const int64_t idx = wave_base + (int64_t)i * kWave + lane;
+    const bool valid = idx < n;
+    const uint32_t d = (k[i] >> shift) & mask;
+    uint64_t m = __ballot(valid);
+    for (int b = 0; b < bits; ++b) {
+      const bool bit = (d >> b) & 1u;
+      const uint64_t bb = __ballot(bit);
+      m &= bit ? bb : ~bb;
+    }
+    const uint32_t r = (uint32_t)__popcll(m & lt_mask);
+    const uint32_t cnt = (uint32_t)__popcll(m);
+    const uint32_t old = s_wh[w][d];
+    __builtin_amdgcn_wave_barrier();
+    if (valid && r == 0) s_wh[w][d] = old + cnt;
+    __builtin_amdgcn_wave_barrier();
+    rank[i] = old + r;
+  }
+  __syncthreads();
+  {
+    const int d = tid;  // kSortThreads == kRadix
+    uint32_t run = 0;
+#pragma unroll
+    for (int q = 0; q < kSortWaves; ++q) {
+      const uint32_t c = s_wh[q][d];
+      s_wh[q][d] = run;
+      run += c;
+    }
+    const uint32_t tile_prefix = block_exclusive_scan_u32(run, s_scan);
+    const uint32_t global_prefix = block_exclusive_scan_u32(digit_total[d], s_scan);
+    s_tile[d] = tile_prefix;
+    s_gbase[d] = global_prefix + counts[(int64_t)d * ntiles + blockIdx.x] - tile_prefix;
+  }
+  __syncthreads();
+#pragma unroll
+  for (int i = 0; i < kSortItems; ++i) {
+    const int64_t idx = wave_base + (int64_t)i * kWave + lane;
+    if (idx < n) {
+      const uint32_t d = (k[i] >> shift) & mask;
+      const uint32_t pos = s_tile[d] + s_wh[w][d] + rank[i];
+      s_keys[pos] = k[i];
+      s_vals[pos] = v[i];
+    }
+  }
+  __syncthreads();
+  const int64_t rem = n - tile_base;
+  const int tile_n = rem < kSortTile ? (int)rem : kSortTile;
+  for (int j = tid; j < tile_n; j += kSortThreads) {
+    const uint32_t kk = s_keys[j];
+    const uint32_t d = (kk >> shift) & mask;
+    const uint32_t g = s_gbase[d] + (uint32_t)j;
+    keys_out[g] = kk;
+    vals_out[g] = s_vals[j];
+  }
+}
+
+size_t sort_ws_bytes(int64_t n) {
+  const int64_t ntiles = (n + kSortTile - 1) / kSortTile;
+  return (size_t)(kRadix * (ntiles > 0 ? ntiles : 1) + kRadix) * sizeof(uint32_t) + 256;
+}
+
+int sort_pairs(uint32_t* keys, uint32_t* vals, uint32_t* keys_alt, uint32_t* vals_alt, int64_t n,
+               int key_bits, void* ws, size_t ws_bytes, int* in_alt, hipStream_t s) {
+  *in_alt = 0;
+  if (n <= 0 || key_bits <= 0) return MDL_OK;
+  if (n > 0xffffffffll) return fail(MDL_ERR_UNSUPPORTED, "radix sort: more than 2^32-1 keys");
+  if (key_bits > 32) return fail(MDL_ERR_INVALID, "radix sort: key_bits > 32");
+  if (ws_bytes < sort_ws_bytes(n)) return fail(MDL_ERR_WORKSPACE, "radix sort: workspace too small");
+  const int ntiles = (int)((n + kSortTile - 1) / kSortTile);
+  uint32_t* counts = static_cast<uint32_t*>(ws);
+  uint32_t* digit_total = counts + (size_t)kRadix * ntiles;
+  uint32_t* ki = keys;
+  uint32_t* vi = vals;
+  uint32_t* ko = keys_alt;
+  uint32_t* vo = vals_alt;
+  int passes = 0;
+  for (int shift = 0; shift < key_bits; shift += 8) {
+    const int bits = key_bits - shift < 8 ? key_bits - shift : 8;
+    const uint32_t mask = (1u << bits) - 1u;
+    hipLaunchKernelGGL(radix_upsweep, dim3(ntiles), dim3(kSortThreads), 0, s, ki, n, shift, mask, counts,
+                       ntiles);
+    MDL_CHECK_LAUNCH("radix_upsweep");
+    hipLaunchKernelGGL(radix_scan, dim3(kRadix), dim3(kSortThreads), 0, s, counts, ntiles, digit_total);
+    MDL_CHECK_LAUNCH("radix_scan");
+    hipLaunchKernelGGL(radix_downsweep, dim3(ntiles), dim3(kSortThreads), 0, s, ki, vi, ko, vo, n, shift,
+                       bits, counts, digit_total, ntiles);
+    MDL_CHECK_LAUNCH("radix_downsweep");
+    uint32_t* t;
+    t = ki; ki = ko; ko = t;
+    t = vi; vi = vo; vo = t;
+    ++passes;
+  }
+  *in_alt = passes & 1;
+  return MDL_OK;
+}
+
+// --------------------------------------------------------------- unique --
+
+__global__ void unique_init(const int64_t* __restrict__ ids, int64_t n, uint32_t* __restrict__ keys,
+                            uint32_t* __restrict__ pos) {
+  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (int64_t)gridDim.x * blockDim.x) {
+    keys[i] = (uint32_t)ids[i];
+    pos[i] = (uint32_t)i;
+  }
+}
+
+__global__ void unique_flags(const uint32_t* __restrict__ keys, int64_t n, int64_t* __restrict__ flags) {
+  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (int64_t)gridDim.x * blockDim.x)
+    flags[i] = (i == 0 || keys[i] != keys[i - 1]) ? 1 : 0;
+}
+
+// offs = inclusive positions (n+1 entries, offs[i+1] = heads in [0, i]).
+__global__ void unique_scatter(const uint32_t* __restrict__ keys, const uint32_t* __restrict__ pos, int64_t n,
+                               const int64_t* __restrict__ offs, int64_t* __restrict__ uniq,
+                               int64_t* __restrict__ inverse, int64_t* __restrict__ starts,
+                               int64_t* __restrict__ num_unique) {
+  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (int64_t)gridDim.x * blockDim.x) {
+    const int64_t s = offs[i + 1] - 1;
+    if (i == 0 || keys[i] != keys[i - 1]) {
+      uniq[s] = keys[i];
+      if (starts) starts[s] = i;
+    }
+    inverse[pos[i]] = s;
+    if (i == n - 1) *num_unique = offs[n];
+  }
+}
+
+__global__ void unique_counts(const uint32_t* __restrict__ keys, int64_t n, const int64_t* __restrict__ offs,
+                              int64_t* __restrict__ counts) {
+  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (int64_t)gridDim.x * blockDim.x) {
+    if (i == n - 1 || keys[i + 1] != keys[i]) {
+      const int64_t s = offs[i + 1] - 1;
+      counts[s] = i + 1 - counts[s];
+    }
+  }
+}
+
+__global__ void write_zero_i64(int64_t* p) { *p = 0; }
+
+static inline unsigned grid_for(int64_t n) {
+  int64_t b = (n + 255) / 256;
+  if (b < 1) b = 1;
+  if (b > 65536) b = 65536;
+  return (unsigned)b;
+}
+
+}  // namespace mdl
+
+using namespace mdl;
+
+extern "C" {
+
+size_t mdl_sort_workspace_bytes(int64_t n) { return sort_ws_bytes(n); }
+
+int mdl_sort_pairs(uint32_t* keys, uint32_t* payload, uint32_t* keys_alt, uint32_t* payload_alt, int64_t n,
+                   int32_t key_bits, void* workspace, size_t workspace_bytes, int32_t* result_in_alt,
+                   void* stream) {
+  int in_alt = 0;
+  int rc = sort_pairs(keys, payload, keys_alt, payload_alt, n, key_bits, workspace, workspace_bytes, &in_alt,
+                      as_stream(stream));
+  if (result_in_alt) *result_in_alt = in_alt;
+  return rc;
+}
+
+size_t mdl_unique_workspace_bytes(int64_t n) {
+  const size_t nn = (size_t)(n > 0 ? n : 1);
+  return 4 * nn * sizeof(uint32_t) + nn * sizeof(int64_t) + (nn + 1) * sizeof(int64_t) +
+         mdl_offsets_workspace_bytes((int64_t)nn) + sort_ws_bytes((int64_t)nn) + 4 * 256;
+}
+
+int mdl_unique(const int64_t* ids, int64_t n, int32_t key_bits, int64_t* unique_out, int64_t* inverse_out,
+               int64_t* counts_out, int64_t* num_unique, void* workspace, size_t workspace_bytes,
+               void* stream) {
+  hipStream_t s = as_stream(stream);
+  if (n < 0 || key_bits < 0 || key_bits > 32) return fail(MDL_ERR_INVALID, "mdl_unique: bad arguments");
+  if (n == 0) {
+    hipLaunchKernelGGL(write_zero_i64, dim3(1), dim3(1), 0, s, num_unique);
+    MDL_CHECK_LAUNCH("write_zero_i64");
+    return MDL_OK;
+  }
+  if (workspace_bytes < mdl_unique_workspace_bytes(n)) return fail(MDL_ERR_WORKSPACE, "mdl_unique: workspace too small");
+  char* p = static_cast<char*>(workspace);
+  auto take = [&](size_t bytes) {
+    char* r = p;
+    p += (bytes + 255) & ~size_t(255);
+    return r;
+  };
+  uint32_t* k0 = (uint32_t*)take(n * 4);
+  uint32_t* v0 = (uint32_t*)take(n * 4);
+  uint32_t* k1 = (uint32_t*)take(n * 4);
+  uint32_t* v1 = (uint32_t*)take(n * 4);
+  int64_t* flags = (int64_t*)take(n * 8);
+  int64_t* offs = (int64_t*)take((n + 1) * 8);
+  void* scan_ws = take(mdl_offsets_workspace_bytes(n));
+  void* sort_ws = take(sort_ws_bytes(n));
+  (void)workspace_bytes;
+  hipLaunchKernelGGL(unique_init, dim3(grid_for(n)), dim3(256), 0, s, ids, n, k0, v0);
+  MDL_CHECK_LAUNCH("unique_init");
+  int in_alt = 0;
+  int rc = sort_pairs(k0, v0, k1, v1, n, key_bits, sort_ws, sort_ws_bytes(n), &in_alt, s);
+  if (rc) return rc;
+  uint32_t* ks = in_alt ? k1 : k0;
+  uint32_t* vs = in_alt ? v1 : v0;
+  hipLaunchKernelGGL(unique_flags, dim3(grid_for(n)), dim3(256), 0, s, ks, n, flags);
+  MDL_CHECK_LAUNCH("unique_flags");
+  rc = mdl_lengths_to_offsets(flags, n, offs, scan_ws, mdl_offsets_workspace_bytes(n), stream);
+  if (rc) return rc;
+  hipLaunchKernelGGL(unique_scatter, dim3(grid_for(n)), dim3(256), 0, s, ks, vs, n, offs, unique_out,
+                     inverse_out, counts_out, num_unique);
+  MDL_CHECK_LAUNCH("unique_scatter");
+  if (counts_out) {
+    hipLaunchKernelGGL(unique_counts, dim3(grid_for(n)), dim3(256), 0, s, ks, n, offs, counts_out);
+    MDL_CHECK_LAUNCH("unique_counts");
+  }
+  return MDL_OK;
+}
+
+}  // extern "C"

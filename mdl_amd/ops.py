@@ -1,0 +1,833 @@
+"""Tensor-level entry points over the libmdl_hip C ABI.
+
+PyTorch supplies device memory and the current HIP stream; every computation
+below is a launch of a hand-written gfx950 kernel in ``libmdl_hip.so``.  All
+launches go to ``torch.cuda.current_stream()`` and none of these functions
+synchronises the device unless its docstring says so.
+"""
+
+from __future__ import annotations
+
+import ctypes
+from dataclasses import dataclass, field
+from typing import Sequence
+
+import numpy as np
+import torch
+from torch import Tensor
+
+from . import _lib
+from ._lib import (
+    CHUNK_DTYPE,
+    FEATURE_DTYPE,
+    MDL_BF16,
+    MDL_F32,
+    MDL_FLAG_EXCLUDE_NULL,
+    MDL_POOL_MEAN,
+    MDL_POOL_NONE,
+    MDL_POOL_SUM,
+    TABLE_DTYPE,
+    check,
+    lib,
+)
+
+POOLING_CODES = {"none": MDL_POOL_NONE, "sum": MDL_POOL_SUM, "mean": MDL_POOL_MEAN}
+NULL_POLICIES = ("exclude", "include_as_padding")
+FORWARD_TARGET_IDS = 512
+
+
+def _require_device(t: Tensor, what: str) -> None:
+    if t.device.type != "cuda":
+        raise RuntimeError(
+            f"{what} must live on a ROCm device; libmdl_hip has no host implementation"
+        )
+
+
+def _ptr(t: Tensor | None) -> int | None:
+    return None if t is None else t.data_ptr()
+
+
+def _stream(device: torch.device) -> int:
+    return torch.cuda.current_stream(device).cuda_stream
+
+
+def dtype_code(dtype: torch.dtype) -> int:
+    if dtype == torch.float32:
+        return MDL_F32
+    if dtype == torch.bfloat16:
+        return MDL_BF16
+    raise TypeError(f"unsupported embedding dtype {dtype}; expected float32 or bfloat16")
+
+
+def upload(host: np.ndarray, device: torch.device) -> Tensor:
+    """Copy a host array to the device through pinned memory, without a sync."""
+
+    raw = np.ascontiguousarray(host).view(np.uint8).reshape(-1)
+    staged = torch.empty(raw.size, dtype=torch.uint8, pin_memory=True)
+    staged.numpy()[:] = raw
+    return staged.to(device, non_blocking=True)
+
+
+def _workspace(nbytes: int, device: torch.device) -> Tensor:
+    return torch.empty(max(int(nbytes), 1), dtype=torch.uint8, device=device)
+
+
+def _aligned16(t: Tensor) -> bool:
+    return t.data_ptr() % 16 == 0
+
+
+def _row_major_aligned(t: Tensor) -> Tensor:
+    """Contiguous rows whose start is 16-byte aligned (copies only if needed)."""
+
+    if not t.is_contiguous():
+        t = t.contiguous()
+    if not _aligned16(t):
+        t = t.clone()
+    return t
+
+
+# ------------------------------------------------------------- bucketing --
+
+
+def bucketize(
+    raw: Tensor,
+    num_buckets: int,
+    *,
+    mode: str = "pre_hashed",
+    valid: Tensor | None = None,
+    validate_nonzero: bool = True,
+    error_count: Tensor | None = None,
+) -> Tensor:
+    """Bucket raw int64 hashes on the device (src/features.py:360-376 rule).
+
+    ``mode="pre_hashed"``: ``(uint64(raw) & (num_buckets-1)) + 1``, null -> 0.
+    ``mode="mod"``: ``1 + floormod(raw - 1, num_buckets - 1)`` (the benchmark
+    id rule of src/benchmark.py:1246-1250).  Non-null zeros are counted in
+    ``error_count`` (a device int32 scalar) when ``validate_nonzero``.
+    """
+
+    _require_device(raw, "raw ids")
+    if raw.dtype != torch.int64:
+        raise TypeError("raw ids must be torch.int64")
+    raw = raw.contiguous()
+    out = torch.empty_like(raw)
+    code = _lib.MDL_BUCKET_PRE_HASHED if mode == "pre_hashed" else _lib.MDL_BUCKET_MOD
+    if mode not in ("pre_hashed", "mod"):
+        raise ValueError("mode must be pre_hashed or mod")
+    if valid is not None:
+        valid = valid.to(device=raw.device, dtype=torch.uint8).contiguous()
+    check(
+        lib().mdl_bucketize(
+            raw.data_ptr(),
+            _ptr(valid),
+            raw.numel(),
+            int(num_buckets),
+            code,
+            1 if validate_nonzero else 0,
+            out.data_ptr(),
+            _ptr(error_count),
+            _stream(raw.device),
+        ),
+        "mdl_bucketize",
+    )
+    return out
+
+
+def lengths_to_offsets(lengths: Tensor) -> Tensor:
+    """``[0, cumsum(lengths)]`` as int64 on the device."""
+
+    _require_device(lengths, "lengths")
+    lengths = lengths.to(torch.int64).contiguous()
+    n = lengths.numel()
+    offsets = torch.empty(n + 1, dtype=torch.int64, device=lengths.device)
+    ws = _workspace(lib().mdl_offsets_workspace_bytes(n), lengths.device)
+    check(
+        lib().mdl_lengths_to_offsets(
+            lengths.data_ptr(), n, offsets.data_ptr(), ws.data_ptr(), ws.numel(), _stream(lengths.device)
+        ),
+        "mdl_lengths_to_offsets",
+    )
+    return offsets
+
+
+# ---------------------------------------------------------------- unique --
+
+
+def unique(ids: Tensor, key_bits: int | None = None) -> tuple[Tensor, Tensor, Tensor]:
+    """``torch.unique(ids, sorted=True, return_inverse=True, return_counts=True)``.
+
+    Ids must be non-negative and below ``2**key_bits`` (default: the bit
+    length of ``ids.max()``, which costs one device sync).  Returns
+    ``(unique, inverse, counts)``; syncs once to size ``unique``.
+    """
+
+    _require_device(ids, "ids")
+    ids = ids.to(torch.int64).contiguous()
+    n = ids.numel()
+    device = ids.device
+    if key_bits is None:
+        key_bits = int(ids.max().item()).bit_length() if n else 0
+    uniq = torch.empty(n, dtype=torch.int64, device=device)
+    inverse = torch.empty(n, dtype=torch.int64, device=device)
+    counts = torch.empty(n, dtype=torch.int64, device=device)
+    num = torch.zeros(1, dtype=torch.int64, device=device)
+    ws = _workspace(lib().mdl_unique_workspace_bytes(n), device)
+    check(
+        lib().mdl_unique(
+            ids.data_ptr(), n, int(key_bits), uniq.data_ptr(), inverse.data_ptr(), counts.data_ptr(),
+            num.data_ptr(), ws.data_ptr(), ws.numel(), _stream(device),
+        ),
+        "mdl_unique",
+    )
+    u = int(num.item())
+    return uniq[:u], inverse.view(ids.shape), counts[:u]
+
+
+# --------------------------------------------------------------- adagrad --
+
+
+def rowwise_adagrad_(
+    weight: Tensor,
+    accumulator: Tensor,
+    rows: Tensor,
+    values: Tensor,
+    *,
+    lr: float,
+    eps: float,
+    error_count: Tensor | None = None,
+) -> None:
+    """In-place row-wise Adagrad on unique rows (src/optim.py:68-108)."""
+
+    _require_device(weight, "weight")
+    if weight.ndim != 2:
+        raise ValueError("row-wise Adagrad expects a 2D weight")
+    n = rows.numel()
+    if n == 0:
+        return
+    if accumulator.dtype != torch.float32 or not accumulator.is_contiguous():
+        raise TypeError("row-wise Adagrad accumulator must be a contiguous float32 tensor")
+    if weight.stride(1) != 1:
+        raise ValueError("weight rows must be contiguous")
+    rows = rows.to(torch.int64).contiguous()
+    if weight.dtype == torch.float32 and values.dtype != torch.float32:
+        values = values.float()
+    if values.dtype not in (torch.float32, torch.bfloat16):
+        values = values.float()
+    values = _row_major_aligned(values)
+    check(
+        lib().mdl_rowwise_adagrad(
+            weight.data_ptr(), dtype_code(weight.dtype), weight.size(0), weight.size(1), weight.stride(0),
+            accumulator.data_ptr(), rows.data_ptr(), n, values.data_ptr(), dtype_code(values.dtype),
+            values.stride(0), float(lr), float(eps), _ptr(error_count), _stream(weight.device),
+        ),
+        "mdl_rowwise_adagrad",
+    )
+
+
+# ------------------------------------------------------------- grouping --
+
+
+@dataclass
+class TableSpec:
+    weight: Tensor
+    state: Tensor | None
+    row_base: int
+
+
+@dataclass
+class FeatureSpec:
+    """One lookup request of a grouped call."""
+
+    table: int
+    pooling: int
+    exclude_null: bool
+    padding_idx: int
+    out_dtype: torch.dtype
+
+
+class GroupPlan:
+    """Tables and features of a grouped lookup; static across steps.
+
+    Features that pass the same weight tensor share one table.  Sort keys of
+    table t are ``row_base[t] + id``; the key one past the last row of the last
+    table marks ids that receive no gradient.
+    """
+
+    def __init__(self) -> None:
+        self.tables: list[TableSpec] = []
+        self.features: list[FeatureSpec] = []
+        self._table_of_ptr: dict[int, int] = {}
+        self.total_rows = 0
+
+    def add_table(self, weight: Tensor, state: Tensor | None = None) -> int:
+        key = weight.data_ptr()
+        if key in self._table_of_ptr:
+            t = self._table_of_ptr[key]
+            if state is not None and self.tables[t].state is None:
+                self.tables[t].state = state
+            return t
+        if weight.ndim != 2 or weight.stride(1) != 1 or weight.stride(0) != weight.size(1):
+            raise ValueError("embedding weights must be contiguous [rows, dim] tensors")
+        dtype_code(weight.dtype)
+        _require_device(weight, "embedding weight")
+        t = len(self.tables)
+        self.tables.append(TableSpec(weight=weight, state=state, row_base=self.total_rows))
+        self._table_of_ptr[key] = t
+        self.total_rows += int(weight.size(0))
+        if self.total_rows >= 0xFFFFFFFF:
+            raise ValueError("a grouped lookup supports fewer than 2^32 - 1 rows in total")
+        return t
+
+    def add_feature(
+        self,
+        weight: Tensor,
+        *,
+        pooling: str = "none",
+        null_policy: str = "exclude",
+        padding_idx: int = 0,
+        state: Tensor | None = None,
+        out_dtype: torch.dtype | None = None,
+    ) -> int:
+        if pooling not in POOLING_CODES:
+            raise ValueError(f"unsupported pooling {pooling!r}")
+        if null_policy not in NULL_POLICIES:
+            raise ValueError(f"unsupported categorical bag null policy {null_policy!r}")
+        t = self.add_table(weight, state)
+        self.features.append(
+            FeatureSpec(
+                table=t,
+                pooling=POOLING_CODES[pooling],
+                exclude_null=null_policy == "exclude",
+                padding_idx=int(padding_idx),
+                out_dtype=out_dtype or weight.dtype,
+            )
+        )
+        return len(self.features) - 1
+
+    @property
+    def sentinel(self) -> int:
+        return self.total_rows
+
+    @property
+    def key_bits(self) -> int:
+        return max(1, int(self.sentinel).bit_length())
+
+    @property
+    def max_dim(self) -> int:
+        return max(int(t.weight.size(1)) for t in self.tables)
+
+
+@dataclass
+class ForwardResult:
+    """What a grouped forward leaves for its backward."""
+
+    plan: GroupPlan
+    device: torch.device
+    ids: Tensor
+    offsets: Tensor | None
+    outputs: list[Tensor]
+    feats: np.ndarray
+    keys: Tensor | None
+    payload: Tensor | None
+    bag_count: Tensor | None
+    error_count: Tensor
+    keep: list = field(default_factory=list)
+
+    @property
+    def num_ids(self) -> int:
+        return int(self.ids.numel())
+
+
+class _UploadCache:
+    """Device copies of small host arrays, reused while their bytes repeat."""
+
+    def __init__(self, capacity: int = 8) -> None:
+        self.capacity = capacity
+        self.entries: dict[bytes, Tensor] = {}
+
+    def get(self, host: np.ndarray, device: torch.device) -> Tensor:
+        key = host.tobytes()
+        hit = self.entries.get(key)
+        if hit is not None and hit.device == device:
+            return hit
+        dev = upload(host, device)
+        if len(self.entries) >= self.capacity:
+            self.entries.pop(next(iter(self.entries)))
+        self.entries[key] = dev
+        return dev
+
+
+_CACHE = _UploadCache()
+
+
+def build_features(
+    plan: GroupPlan,
+    id_counts: Sequence[int],
+    bag_counts: Sequence[int],
+    out_ptrs: Sequence[int],
+    out_strides: Sequence[int],
+) -> np.ndarray:
+    """Host image of the feature descriptors (vectorised over features).
+
+    ``bag_counts[f]`` is the number of bags of a pooled feature (ignored for
+    unpooled ones).  When any feature is pooled, every unpooled feature
+    occupies one pseudo-bag in the offsets array (its whole id range), so the
+    offsets of all features come from one scan over the concatenated lengths.
+    """
+
+    specs = plan.features
+    nf = len(specs)
+    tab = [plan.tables[s.table] for s in specs]
+    pool = np.array([s.pooling for s in specs], dtype=np.int32)
+    pooled = pool != MDL_POOL_NONE
+    pooled_any = bool(pooled.any())
+    ids = np.asarray(id_counts, dtype=np.int64)
+    bags = np.where(pooled, np.asarray(bag_counts, dtype=np.int64), 0)
+    rows_out = np.where(pooled, bags, ids)
+    bag_slots = np.where(pooled, bags, 1 if pooled_any else 0)
+    feats = np.zeros(nf, dtype=FEATURE_DTYPE)
+    feats["weight"] = [t.weight.data_ptr() for t in tab]
+    feats["state"] = [t.state.data_ptr() if t.state is not None else 0 for t in tab]
+    feats["out"] = np.asarray(out_ptrs, dtype=np.uint64)
+    feats["num_rows"] = [int(t.weight.size(0)) for t in tab]
+    feats["out_stride"] = np.asarray(out_strides, dtype=np.int64)
+    feats["row_base"] = [t.row_base for t in tab]
+    feats["payload_base"] = np.concatenate(([0], np.cumsum(rows_out)[:-1])) if nf else []
+    feats["ids_begin"] = np.concatenate(([0], np.cumsum(ids)[:-1])) if nf else []
+    feats["num_ids"] = ids
+    feats["bag_base"] = np.concatenate(([0], np.cumsum(bag_slots)[:-1])) if nf else []
+    feats["num_bags"] = bags
+    feats["dim"] = [int(t.weight.size(1)) for t in tab]
+    feats["wdtype"] = [dtype_code(t.weight.dtype) for t in tab]
+    feats["odtype"] = [dtype_code(s.out_dtype) for s in specs]
+    feats["pooling"] = pool
+    feats["flags"] = [MDL_FLAG_EXCLUDE_NULL if s.exclude_null else 0 for s in specs]
+    feats["padding_idx"] = [s.padding_idx for s in specs]
+    feats["table"] = [s.table for s in specs]
+    for s, t in zip(specs, tab):
+        if t.weight.dtype == torch.float32 and s.out_dtype != torch.float32:
+            raise TypeError("float32 tables produce float32 outputs")
+    if int(rows_out.sum()) >= 0xFFFFFFFF:
+        raise ValueError("a grouped lookup supports fewer than 2^32 - 1 output rows")
+    return feats
+
+
+def forward_packed(
+    plan: GroupPlan,
+    all_ids: Tensor,
+    offsets: Tensor | None,
+    id_counts: Sequence[int],
+    bag_counts: Sequence[int],
+    outputs: Sequence[Tensor],
+    *,
+    with_backward: bool,
+    error_count: Tensor | None = None,
+) -> ForwardResult:
+    """Grouped lookup over caller-packed buffers (no per-feature copies).
+
+    ``all_ids``: every feature's ids back to back; ``offsets``: absolute bag
+    bounds from one scan of the concatenated lengths (see build_features);
+    ``outputs[f]``: row-major output rows of feature f (2-D views with unit
+    column stride, e.g. column slices of one ``[B, sum(dim)]`` buffer).
+    """
+
+    device = all_ids.device
+    stream = _stream(device)
+    n = int(all_ids.numel())
+    out_ptrs = [o.data_ptr() for o in outputs]
+    out_strides = [o.stride(0) if o.ndim == 2 else int(o.size(-1)) for o in outputs]
+    feats = build_features(plan, id_counts, bag_counts, out_ptrs, out_strides)
+    pooled_any = bool((feats["pooling"] != MDL_POOL_NONE).any())
+    if pooled_any and offsets is None:
+        raise ValueError("pooled features need offsets")
+    n_chunks = lib().mdl_plan_chunks(feats.ctypes.data, len(feats), FORWARD_TARGET_IDS, None, 0)
+    if n_chunks < 0:
+        check(int(n_chunks), "mdl_plan_chunks")
+    chunks = np.zeros(max(n_chunks, 1), dtype=CHUNK_DTYPE)
+    lib().mdl_plan_chunks(feats.ctypes.data, len(feats), FORWARD_TARGET_IDS, chunks.ctypes.data, n_chunks)
+    feats_dev = _CACHE.get(feats, device)
+    chunks_dev = _CACHE.get(chunks, device)
+    if error_count is None:
+        error_count = torch.zeros(1, dtype=torch.int32, device=device)
+    keys = payload = bag_count = None
+    total_rows_out = int(feats["payload_base"][-1] + (feats["num_bags"][-1] if feats["pooling"][-1] else feats["num_ids"][-1])) if len(feats) else 0
+    if with_backward:
+        keys = torch.empty(max(n, 1), dtype=torch.int32, device=device)
+        payload = torch.empty(max(n, 1), dtype=torch.int32, device=device)
+        if pooled_any:
+            bag_count = torch.empty(max(total_rows_out, 1), dtype=torch.float32, device=device)
+    check(
+        lib().mdl_forward(
+            feats_dev.data_ptr(), len(feats), chunks_dev.data_ptr(), n_chunks, all_ids.data_ptr(),
+            _ptr(offsets), _ptr(keys), _ptr(payload), plan.sentinel, _ptr(bag_count),
+            error_count.data_ptr(), stream,
+        ),
+        "mdl_forward",
+    )
+    return ForwardResult(
+        plan=plan, device=device, ids=all_ids, offsets=offsets, outputs=list(outputs), feats=feats,
+        keys=keys, payload=payload, bag_count=bag_count, error_count=error_count,
+        keep=[feats_dev, chunks_dev],
+    )
+
+
+def grouped_forward(
+    plan: GroupPlan,
+    ids: Sequence[Tensor],
+    lengths: Sequence[Tensor | None],
+    *,
+    with_backward: bool,
+    outputs: Sequence[Tensor] | None = None,
+    error_count: Tensor | None = None,
+) -> ForwardResult:
+    """Look up (and pool) every feature of ``plan`` in one launch.
+
+    ``ids[f]`` are feature f's ids (any shape for unpooled features, a flat
+    CSR value list for pooled ones) and ``lengths[f]`` its bag lengths (None
+    for unpooled features).  Outputs are ``[*ids.shape, dim]`` (unpooled) or
+    ``[len(lengths), dim]`` (pooled) unless the caller passes ``outputs``.
+    """
+
+    specs = plan.features
+    if len(ids) != len(specs) or len(lengths) != len(specs):
+        raise ValueError("one ids tensor and one lengths entry per feature")
+    device = plan.tables[0].weight.device
+    id_counts = []
+    bag_counts = []
+    pooled_any = any(s.pooling != MDL_POOL_NONE for s in specs)
+    length_parts = []
+    for f, spec in enumerate(specs):
+        t = ids[f]
+        if t.dtype != torch.long:
+            raise TypeError("sharded embedding indices must be torch.long")
+        _require_device(t, "ids")
+        id_counts.append(int(t.numel()))
+        if spec.pooling != MDL_POOL_NONE:
+            ln = lengths[f]
+            if ln is None or ln.ndim != 1:
+                raise ValueError("categorical bag lengths must have shape [B]")
+            bag_counts.append(int(ln.numel()))
+            length_parts.append(ln.to(device=device, dtype=torch.int64))
+        else:
+            bag_counts.append(0)
+            if pooled_any:
+                length_parts.append(torch.full((1,), int(t.numel()), dtype=torch.int64, device=device))
+    flat = [t.reshape(-1) for t in ids]
+    all_ids = (flat[0] if len(flat) == 1 else torch.cat(flat)).contiguous()
+    offsets = None
+    if pooled_any:
+        offsets = lengths_to_offsets(torch.cat(length_parts) if len(length_parts) > 1 else length_parts[0])
+    if outputs is None:
+        outputs = []
+        for f, spec in enumerate(specs):
+            dim = int(plan.tables[spec.table].weight.size(1))
+            shape = (*ids[f].shape, dim) if spec.pooling == MDL_POOL_NONE else (bag_counts[f], dim)
+            outputs.append(torch.empty(shape, dtype=spec.out_dtype, device=device))
+    else:
+        for f, spec in enumerate(specs):
+            o = outputs[f]
+            if o.stride(-1) != 1 or o.dtype != spec.out_dtype:
+                raise ValueError("caller outputs must have unit column stride and the feature's dtype")
+    return forward_packed(
+        plan, all_ids, offsets, id_counts, bag_counts, outputs,
+        with_backward=with_backward, error_count=error_count,
+    )
+
+
+def _tables_array(plan: GroupPlan, feats: np.ndarray) -> np.ndarray:
+    tables = np.zeros(len(plan.tables), dtype=TABLE_DTYPE)
+    users: dict[int, list[int]] = {}
+    for f, spec in enumerate(plan.features):
+        users.setdefault(spec.table, []).append(f)
+    for t, table in enumerate(plan.tables):
+        w = table.weight
+        rec = tables[t]
+        rec["weight"] = w.data_ptr()
+        rec["state"] = table.state.data_ptr() if table.state is not None else 0
+        rec["num_rows"] = int(w.size(0))
+        rec["row_base"] = table.row_base
+        rec["dim"] = int(w.size(1))
+        rec["wdtype"] = dtype_code(w.dtype)
+        fs = users.get(t, [])
+        rec["feature"] = fs[0] if len(fs) == 1 else -1
+        gd = {int(feats[f]["odtype"]) for f in fs}
+        if len(gd) > 1:
+            raise TypeError("features that share a table must share an output dtype")
+        rec["gdtype"] = gd.pop() if gd else dtype_code(w.dtype)
+        esize = w.element_size()
+        vec = w.data_ptr() % 16 == 0 and (int(w.size(1)) * esize) % 16 == 0
+        lanes_cover = 64 * (16 // esize if vec else 1)
+        if int(w.size(1)) > lanes_cover:
+            raise NotImplementedError(
+                f"backward supports rows of at most {lanes_cover} elements for this table layout"
+            )
+    return tables
+
+
+def _attach_grads(res: ForwardResult, grads: Sequence[Tensor | None]) -> tuple[np.ndarray, list[Tensor]]:
+    feats = res.feats.copy()
+    keep = []
+    gptr = []
+    gstride = []
+    for f, spec in enumerate(res.plan.features):
+        out = res.outputs[f]
+        g = grads[f]
+        if g is None:
+            g = torch.zeros_like(out)
+        if g.dtype != spec.out_dtype:
+            g = g.to(spec.out_dtype)
+        dim = int(res.plan.tables[spec.table].weight.size(1))
+        g2 = g if g.ndim == 2 else g.reshape(-1, dim)
+        esize = g2.element_size()
+        if (dim * esize) % 16 == 0 and (
+            g2.stride(-1) != 1 or g2.data_ptr() % 16 != 0 or (g2.stride(0) * esize) % 16 != 0
+        ):
+            g2 = g2.contiguous()
+            if g2.data_ptr() % 16 != 0:
+                g2 = g2.clone()
+        if g2.stride(-1) != 1:
+            g2 = g2.contiguous()
+        keep.append(g2)
+        gptr.append(g2.data_ptr())
+        gstride.append(g2.stride(0))
+    feats["grad"] = np.asarray(gptr, dtype=np.uint64)
+    feats["out_stride"] = np.asarray(gstride, dtype=np.int64)
+    return feats, keep
+
+
+def backward_adagrad(res: ForwardResult, grads: Sequence[Tensor | None], *, lr: float, eps: float) -> None:
+    """Fused backward + row-wise Adagrad of every table (consumes the keys)."""
+
+    plan = res.plan
+    if res.keys is None:
+        raise RuntimeError("the forward ran without backward bookkeeping")
+    for t in plan.tables:
+        if t.state is None:
+            raise RuntimeError("every table needs a row-wise Adagrad accumulator")
+    feats, keep = _attach_grads(res, grads)
+    tables = _tables_array(plan, feats)
+    device = res.device
+    feats_dev = _CACHE.get(feats, device)
+    tables_dev = _CACHE.get(tables, device)
+    n = res.num_ids
+    ws = _workspace(lib().mdl_backward_workspace_bytes(n, len(tables), plan.max_dim), device)
+    check(
+        lib().mdl_backward_adagrad(
+            feats_dev.data_ptr(), len(feats), tables_dev.data_ptr(), len(tables), plan.max_dim,
+            res.keys.data_ptr(), res.payload.data_ptr(), n, plan.key_bits, _ptr(res.bag_count),
+            float(lr), float(eps), ws.data_ptr(), ws.numel(), _stream(device),
+        ),
+        "mdl_backward_adagrad",
+    )
+    res.keys = None
+    res.payload = None
+    del keep
+
+
+def backward_coalesce(res: ForwardResult, grads: Sequence[Tensor | None]) -> list[tuple[Tensor, Tensor]]:
+    """Coalesced sparse gradient ``(rows, values)`` of every table.
+
+    Rows are ascending and unique; values have the table's dtype.  Syncs once
+    (to size the per-table outputs).
+    """
+
+    plan = res.plan
+    if res.keys is None:
+        raise RuntimeError("the forward ran without backward bookkeeping")
+    feats, keep = _attach_grads(res, grads)
+    tables = _tables_array(plan, feats)
+    device = res.device
+    feats_dev = upload(feats, device)
+    tables_dev = upload(tables, device)
+    n = res.num_ids
+    T = len(tables)
+    stream = _stream(device)
+    ws = _workspace(lib().mdl_backward_workspace_bytes(n, T, plan.max_dim), device)
+    urange = torch.zeros(2 * T, dtype=torch.int64, device=device)
+    check(
+        lib().mdl_backward_count(
+            tables_dev.data_ptr(), T, plan.max_dim, res.keys.data_ptr(), res.payload.data_ptr(), n,
+            plan.key_bits, urange.data_ptr(), ws.data_ptr(), ws.numel(), stream,
+        ),
+        "mdl_backward_count",
+    )
+    ur = urange.cpu().numpy().reshape(T, 2)
+    result = []
+    rows_addr = np.zeros(T, dtype=np.uint64)
+    vals_addr = np.zeros(T, dtype=np.uint64)
+    for t, table in enumerate(plan.tables):
+        u = int(ur[t, 1] - ur[t, 0])
+        w = table.weight
+        rows = torch.empty(u, dtype=torch.int64, device=device)
+        vals = torch.empty((u, int(w.size(1))), dtype=w.dtype, device=device)
+        rows_addr[t] = rows.data_ptr() if u else 0
+        vals_addr[t] = vals.data_ptr() if u else 0
+        result.append((rows, vals))
+    if n:
+        rows_dev = upload(rows_addr, device)
+        vals_dev = upload(vals_addr, device)
+        check(
+            lib().mdl_backward_coalesce(
+                feats_dev.data_ptr(), len(feats), tables_dev.data_ptr(), T, plan.max_dim,
+                res.keys.data_ptr(), res.payload.data_ptr(), n, plan.key_bits, _ptr(res.bag_count),
+                urange.data_ptr(), rows_dev.data_ptr(), vals_dev.data_ptr(), ws.data_ptr(), ws.numel(),
+                stream,
+            ),
+            "mdl_backward_coalesce",
+        )
+    res.keys = None
+    res.payload = None
+    del keep
+    return result
+
+
+def coalesce_rows(
+    indices: Tensor, values: Tensor, num_rows: int, *, padding_idx: int = -1
+) -> tuple[Tensor, Tensor]:
+    """Sort + unique + segment-sum of an uncoalesced COO gradient.
+
+    ``indices`` [n] row ids, ``values`` [n, dim]; returns ``(rows, summed)``
+    with rows ascending and unique (the work ``Tensor.coalesce()`` does for
+    src/optim.py:323-324).  Syncs once.
+    """
+
+    _require_device(values, "values")
+    device = values.device
+    n = int(indices.numel())
+    dim = int(values.size(1))
+    if n == 0:
+        return indices.new_empty(0), values.new_empty((0, dim))
+    indices = indices.to(torch.int64).contiguous()
+    values = _row_major_aligned(values)
+    plan = GroupPlan()
+    # A stand-in table of the right shape: only its row count, dim and dtype
+    # are read, never its rows.
+    fake_w = torch.empty((0, dim), dtype=values.dtype, device=device)
+    plan.tables.append(TableSpec(weight=fake_w, state=None, row_base=0))
+    plan.total_rows = int(num_rows)
+    plan.features.append(FeatureSpec(table=0, pooling=MDL_POOL_NONE, exclude_null=False,
+                                     padding_idx=padding_idx, out_dtype=values.dtype))
+    keys = torch.empty(n, dtype=torch.int32, device=device)
+    payload = torch.empty(n, dtype=torch.int32, device=device)
+    err = torch.zeros(1, dtype=torch.int32, device=device)
+    stream = _stream(device)
+    check(
+        lib().mdl_sparse_keys(
+            indices.data_ptr(), n, int(num_rows), 0, 0, int(padding_idx), keys.data_ptr(),
+            payload.data_ptr(), plan.sentinel, err.data_ptr(), stream,
+        ),
+        "mdl_sparse_keys",
+    )
+    feats = np.zeros(1, dtype=FEATURE_DTYPE)
+    rec = feats[0]
+    rec["grad"] = values.data_ptr()
+    rec["num_rows"] = int(num_rows)
+    rec["out_stride"] = values.stride(0)
+    rec["num_ids"] = n
+    rec["dim"] = dim
+    rec["wdtype"] = dtype_code(values.dtype)
+    rec["odtype"] = dtype_code(values.dtype)
+    rec["pooling"] = MDL_POOL_NONE
+    rec["padding_idx"] = padding_idx
+    tables = np.zeros(1, dtype=TABLE_DTYPE)
+    tables[0]["num_rows"] = int(num_rows)
+    tables[0]["dim"] = dim
+    tables[0]["wdtype"] = dtype_code(values.dtype)
+    tables[0]["feature"] = 0
+    tables[0]["gdtype"] = dtype_code(values.dtype)
+    res = ForwardResult(
+        plan=plan, device=device, ids=indices, offsets=None, outputs=[values], feats=feats,
+        keys=keys, payload=payload, bag_count=None, error_count=err,
+    )
+    feats_dev = upload(feats, device)
+    tables_dev = upload(tables, device)
+    ws = _workspace(lib().mdl_backward_workspace_bytes(n, 1, dim), device)
+    urange = torch.zeros(2, dtype=torch.int64, device=device)
+    check(
+        lib().mdl_backward_count(
+            tables_dev.data_ptr(), 1, dim, keys.data_ptr(), payload.data_ptr(), n, plan.key_bits,
+            urange.data_ptr(), ws.data_ptr(), ws.numel(), stream,
+        ),
+        "mdl_backward_count",
+    )
+    if int(err.item()):
+        raise IndexError(f"sparse gradient rows outside [0, {num_rows})")
+    u = int((urange[1] - urange[0]).item())
+    rows = torch.empty(u, dtype=torch.int64, device=device)
+    summed = torch.empty((u, dim), dtype=values.dtype, device=device)
+    if u:
+        rows_dev = upload(np.array([rows.data_ptr()], dtype=np.uint64), device)
+        vals_dev = upload(np.array([summed.data_ptr()], dtype=np.uint64), device)
+        check(
+            lib().mdl_backward_coalesce(
+                feats_dev.data_ptr(), 1, tables_dev.data_ptr(), 1, dim, keys.data_ptr(), payload.data_ptr(),
+                n, plan.key_bits, None, urange.data_ptr(), rows_dev.data_ptr(), vals_dev.data_ptr(),
+                ws.data_ptr(), ws.numel(), stream,
+            ),
+            "mdl_backward_coalesce",
+        )
+    del res
+    return rows, summed
+
+
+# ------------------------------------------------------------- sequences --
+
+
+def sequence_forward(
+    weight: Tensor,
+    ids: Tensor,
+    lengths: Tensor,
+    *,
+    out_len: int | None = None,
+    order: str = "oldest_to_newest",
+    padding_idx: int = 0,
+    out_dtype: torch.dtype | None = None,
+    keys: Tensor | None = None,
+    payload: Tensor | None = None,
+    row_base: int = 0,
+    payload_base: int = 0,
+    sentinel: int = 0,
+    error_count: Tensor | None = None,
+) -> tuple[Tensor, Tensor]:
+    """Right-aligned sequence gather: ``([B, L, dim] embeddings, [B, L] mask)``.
+
+    Semantics of F.embedding + ``_right_aligned_sequence`` (+ the reversal
+    of ``_align_sequence_inputs`` for newest_to_oldest), src/model.py:2989-3100.
+    """
+
+    _require_device(ids, "sequence ids")
+    if ids.dtype != torch.long:
+        raise TypeError("sharded embedding indices must be torch.long")
+    if ids.ndim != 2:
+        raise ValueError("sequence ids must be [batch, length]")
+    batch, in_len = int(ids.size(0)), int(ids.size(1))
+    out_len = in_len if out_len is None else int(out_len)
+    device = ids.device
+    out_dtype = out_dtype or weight.dtype
+    dim = int(weight.size(1))
+    out = torch.empty((batch, out_len, dim), dtype=out_dtype, device=device)
+    mask = torch.empty((batch, out_len), dtype=torch.bool, device=device)
+    feat = np.zeros(1, dtype=FEATURE_DTYPE)
+    rec = feat[0]
+    rec["weight"] = weight.data_ptr()
+    rec["num_rows"] = int(weight.size(0))
+    rec["row_base"] = row_base
+    rec["payload_base"] = payload_base
+    rec["dim"] = dim
+    rec["wdtype"] = dtype_code(weight.dtype)
+    rec["odtype"] = dtype_code(out_dtype)
+    rec["padding_idx"] = padding_idx
+    order_code = _lib.MDL_SEQ_OLDEST_TO_NEWEST if order == "oldest_to_newest" else _lib.MDL_SEQ_NEWEST_TO_OLDEST
+    if order not in ("oldest_to_newest", "newest_to_oldest"):
+        raise ValueError("order must be oldest_to_newest or newest_to_oldest")
+    ids = ids.contiguous()
+    lengths = lengths.to(device=device, dtype=torch.int64).contiguous()
+    check(
+        lib().mdl_sequence_forward(
+            feat.ctypes.data, ids.data_ptr(), lengths.data_ptr(), batch, in_len, out_len, order_code,
+            out.data_ptr(), mask.data_ptr(), _ptr(keys), _ptr(payload), int(sentinel), _ptr(error_count),
+            _stream(device),
+        ),
+        "mdl_sequence_forward",
+    )
+    return out, mask

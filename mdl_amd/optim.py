@@ -1,0 +1,168 @@
+"""Drop-in ``ShardedRowWiseAdagrad`` whose update is a gfx950 HIP kernel.
+
+Same constructor, state layout (``step``: 0-d float64 on CPU, ``sum``: one
+fp32 accumulator per row) and ``load_state_dict`` behaviour as
+src/optim.py:212-377, so checkpoints move between the two unchanged.
+Gradients must be sparse COO on a ROCm device; uncoalesced ones are coalesced
+by the library's sort/segment-reduce before the update.
+"""
+
+from __future__ import annotations
+
+import copy
+from collections.abc import Iterable
+from typing import Any, Callable
+
+import torch
+from torch import Tensor, nn
+
+from . import embeddings, ops
+
+
+def fused_rowwise_adagrad_update(
+    parameter: Tensor,
+    accumulator: Tensor,
+    rows: Tensor,
+    values: Tensor,
+    *,
+    lr: float,
+    eps: float,
+) -> None:
+    """Row-wise Adagrad for one table (src/optim.py:68-108).
+
+    ``rows`` must be unique.  ``values`` may be bf16 or fp32; the accumulator
+    stays fp32 and the weight may be bf16 or fp32 (one rounding on store).
+    """
+
+    if rows.numel() == 0:
+        return
+    ops.rowwise_adagrad_(parameter, accumulator, rows, values, lr=lr, eps=eps)
+
+
+class ShardedRowWiseAdagrad(torch.optim.Optimizer):
+    """Row-wise Adagrad: one fp32 accumulator per row (mean of squared grads)."""
+
+    def __init__(
+        self,
+        params: Iterable[nn.Parameter],
+        lr: float,
+        lr_decay: float = 0.0,
+        weight_decay: float = 0.0,
+        initial_accumulator_value: float = 0.0,
+        eps: float = 1.0e-10,
+        *,
+        state_dtype: torch.dtype = torch.float32,
+    ) -> None:
+        if lr <= 0.0:
+            raise ValueError("lr must be positive")
+        if lr_decay < 0.0:
+            raise ValueError("lr_decay must be non-negative")
+        if weight_decay != 0.0:
+            raise ValueError(
+                "ShardedRowWiseAdagrad does not support weight decay for sparse gradients"
+            )
+        if initial_accumulator_value < 0.0:
+            raise ValueError("initial_accumulator_value must be non-negative")
+        if eps <= 0.0:
+            raise ValueError("eps must be positive")
+        defaults = {
+            "lr": lr,
+            "lr_decay": lr_decay,
+            "weight_decay": weight_decay,
+            "initial_accumulator_value": initial_accumulator_value,
+            "eps": eps,
+            "state_dtype": state_dtype,
+        }
+        super().__init__(params, defaults)
+        for group in self.param_groups:
+            for parameter in group["params"]:
+                if parameter.ndim != 2:
+                    raise ValueError("ShardedRowWiseAdagrad expects 2D embedding parameters")
+                state = self.state[parameter]
+                state["step"] = torch.zeros((), dtype=torch.float64)
+                state["sum"] = torch.full(
+                    (parameter.shape[0],),
+                    float(initial_accumulator_value),
+                    dtype=state_dtype,
+                    device=parameter.device,
+                )
+
+    def load_state_dict(self, state_dict: dict[str, Any]) -> None:
+        # The base class casts state tensors to the parameter dtype; restore
+        # the fp32 accumulators and CPU float64 steps from a snapshot.
+        original = copy.deepcopy(state_dict)
+        super().load_state_dict(state_dict)
+        saved_items: list[dict[str, Any]] = []
+        for group in original.get("param_groups", ()):
+            for param_id in group["params"]:
+                saved_items.append(original.get("state", {}).get(param_id, {}))
+        index = 0
+        for group in self.param_groups:
+            state_dtype = group.get("state_dtype", torch.float32)
+            for parameter in group["params"]:
+                saved = saved_items[index] if index < len(saved_items) else {}
+                index += 1
+                state = self.state.get(parameter)
+                if not state:
+                    continue
+                accumulator = saved.get("sum", state.get("sum"))
+                if isinstance(accumulator, Tensor):
+                    state["sum"] = accumulator.to(device=parameter.device, dtype=state_dtype)
+                step = saved.get("step", state.get("step"))
+                if isinstance(step, Tensor):
+                    state["step"] = step.to(device="cpu", dtype=torch.float64)
+
+    def _advance(self, parameter: Tensor, group: dict[str, Any]) -> float:
+        """Bump the CPU step counter; return the decayed learning rate."""
+
+        step_tensor = self.state[parameter]["step"]
+        step = float(step_tensor) + 1.0
+        step_tensor.fill_(step)
+        lr = float(group["lr"])
+        lr_decay = float(group["lr_decay"])
+        return lr if lr_decay == 0.0 else lr / (1.0 + (step - 1.0) * lr_decay)
+
+    @torch.no_grad()
+    def step(self, closure: Callable[[], Tensor] | None = None) -> Tensor | None:
+        loss = None
+        if closure is not None:
+            with torch.enable_grad():
+                loss = closure()
+        if embeddings.deferred_index_checks():
+            embeddings.check_index_errors()
+        for group in self.param_groups:
+            eps = float(group["eps"])
+            for parameter in group["params"]:
+                grad = parameter.grad
+                if grad is None:
+                    continue
+                if not grad.is_sparse or grad.layout != torch.sparse_coo:
+                    raise RuntimeError(
+                        "ShardedRowWiseAdagrad expects one-dimensional row-sparse COO gradients"
+                    )
+                if grad.sparse_dim() != 1 or grad.dense_dim() != 1:
+                    raise RuntimeError(
+                        "ShardedRowWiseAdagrad expects one sparse row dimension and one dense dimension"
+                    )
+                if grad.is_coalesced():
+                    rows = grad.indices()[0]
+                    values = grad.values()
+                else:
+                    rows, values = ops.coalesce_rows(
+                        grad._indices()[0], grad._values(), int(parameter.shape[0])
+                    )
+                    parameter.grad = torch.sparse_coo_tensor(
+                        rows.unsqueeze(0), values, tuple(grad.shape), is_coalesced=True
+                    )
+                clear_lr = self._advance(parameter, group)
+                if rows.numel() == 0:
+                    continue
+                accumulator: Tensor = self.state[parameter]["sum"]
+                if not (parameter.is_cuda and accumulator.is_cuda):
+                    raise RuntimeError(
+                        "ShardedRowWiseAdagrad runs on ROCm devices only (libmdl_hip)"
+                    )
+                fused_rowwise_adagrad_update(
+                    parameter, accumulator, rows, values, lr=clear_lr, eps=eps
+                )
+        return loss

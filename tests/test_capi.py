@@ -1,0 +1,106 @@
+"""C ABI of libmdl_hip.so without a GPU: exports, struct layout, host-only
+entry points and argument validation (no kernel is launched here)."""
+
+import ctypes
+import re
+import subprocess
+
+import numpy as np
+import pytest
+
+from mdl_amd import _lib
+from tests.conftest import ROOT
+
+HEADER = ROOT / "include" / "mdl_hip.h"
+
+
+def _declared_functions():
+    text = HEADER.read_text()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(mdl_[a-z0-9_]+)\s*\(", text)))
+
+
+def test_library_exports_every_declared_function():
+    lib = _lib.lib()
+    names = _declared_functions()
+    assert len(names) >= 15
+    missing = [n for n in names if not hasattr(lib, n)]
+    assert not missing, missing
+    assert set(names) == set(_lib.SIGNATURES), set(names) ^ set(_lib.SIGNATURES)
+
+
+def test_struct_layout_matches_header(tmp_path):
+    probe = tmp_path / "probe.c"
+    fields = {
+        "mdl_feature": _lib.FEATURE_DTYPE,
+        "mdl_chunk": _lib.CHUNK_DTYPE,
+        "mdl_table": _lib.TABLE_DTYPE,
+    }
+    lines = ['#include <stdio.h>', '#include <stddef.h>', f'#include "{HEADER}"', "int main(void){"]
+    for st, dt in fields.items():
+        lines.append(f'printf("{st} size %zu\\n", sizeof({st}));')
+        for name in dt.names:
+            lines.append(f'printf("{st} {name} %zu\\n", offsetof({st}, {name}));')
+    lines.append("return 0;}")
+    probe.write_text("\n".join(lines))
+    exe = tmp_path / "probe"
+    subprocess.run(["gcc", "-std=c11", str(probe), "-o", str(exe)], check=True)
+    out = subprocess.run([str(exe)], check=True, capture_output=True, text=True).stdout.split("\n")
+    got = {}
+    for line in out:
+        if line:
+            st, name, val = line.split()
+            got[(st, name)] = int(val)
+    for st, dt in fields.items():
+        assert got[(st, "size")] == dt.itemsize
+        for name in dt.names:
+            assert got[(st, name)] == dt.fields[name][1], (st, name)
+
+
+def test_plan_chunks_host_helper():
+    lib = _lib.lib()
+    feats = np.zeros(3, dtype=_lib.FEATURE_DTYPE)
+    feats["pooling"] = [_lib.MDL_POOL_MEAN, _lib.MDL_POOL_NONE, _lib.MDL_POOL_SUM]
+    feats["num_bags"] = [8192, 0, 1000]
+    feats["num_ids"] = [8192 * 16, 1500, 1000]
+    n = lib.mdl_plan_chunks(feats.ctypes.data, 3, 512, None, 0)
+    chunks = np.zeros(n, dtype=_lib.CHUNK_DTYPE)
+    assert lib.mdl_plan_chunks(feats.ctypes.data, 3, 512, chunks.ctypes.data, n) == n
+    f0 = chunks[chunks["feature"] == 0]
+    assert (f0["count"] == 32).all() and f0["count"].sum() == 8192  # 32 bags x ~16 ids
+    assert f0["first"].tolist() == list(range(0, 8192, 32))
+    f1 = chunks[chunks["feature"] == 1]
+    assert f1["count"].tolist() == [512, 512, 476] and f1["first"].tolist() == [0, 512, 1024]
+    f2 = chunks[chunks["feature"] == 2]
+    assert f2["count"].max() == 256 and f2["count"].sum() == 1000  # bag cap 256
+    assert lib.mdl_plan_chunks(feats.ctypes.data, 3, 0, None, 0) == _lib.MDL_OK - 1  # MDL_ERR_INVALID
+
+
+def test_invalid_arguments_fail_before_any_launch():
+    lib = _lib.lib()
+    rc = lib.mdl_bucketize(None, None, 4, 6, _lib.MDL_BUCKET_PRE_HASHED, 1, None, None, None)
+    assert rc == -1 and b"power of two" in lib.mdl_last_error()
+    rc = lib.mdl_bucketize(None, None, 4, 1, _lib.MDL_BUCKET_MOD, 0, None, None, None)
+    assert rc == -1 and b"num_buckets > 1" in lib.mdl_last_error()
+    rc = lib.mdl_sort_pairs(None, None, None, None, 10, 40, None, 0, None, None)
+    assert rc == -1 and b"key_bits" in lib.mdl_last_error()
+    rc = lib.mdl_sort_pairs(None, None, None, None, 1 << 33, 8, None, 0, None, None)
+    assert rc == -4
+    rc = lib.mdl_backward_adagrad(None, 0, None, 0, 8, None, None, 10, 8, None, 0.1, 1e-8, None, 0, None)
+    assert rc == -1 and b"table" in lib.mdl_last_error()
+    rc = lib.mdl_rowwise_adagrad(None, _lib.MDL_F32, 10, 4, 4, None, None, 3, None, _lib.MDL_BF16, 4, 0.1,
+                                 1e-8, None, None)
+    assert rc == -1  # null pointers
+    # zero-sized work is a no-op success without touching the device
+    assert lib.mdl_forward(None, 0, None, 0, None, None, None, None, 0, None, None, None) == 0
+    assert lib.mdl_rowwise_adagrad(None, 0, 0, 4, 4, None, None, 0, None, 0, 4, 0.1, 1e-8, None, None) == 0
+
+
+def test_workspace_queries_are_monotone():
+    lib = _lib.lib()
+    a = lib.mdl_backward_workspace_bytes(1000, 4, 64)
+    b = lib.mdl_backward_workspace_bytes(100000, 4, 64)
+    c = lib.mdl_backward_workspace_bytes(100000, 200, 128)
+    assert 0 < a < b < c
+    assert lib.mdl_sort_workspace_bytes(1 << 20) >= 256 * 256 * 4
+    assert lib.mdl_unique_workspace_bytes(1000) > 16 * 1000

@@ -1,0 +1,202 @@
+"""The drop-in modules on the GPU, written like the reference's own tests
+(tests/test_rowwise_adagrad.py, tests/test_sharded_embedding.py:755-802) and
+checked against the CPU oracle."""
+
+import json
+import pathlib
+import sys
+
+import numpy as np
+import pytest
+import torch
+import torch.nn.functional as F
+from torch import nn
+
+from mdl_amd.embeddings import (
+    EmbeddingTableSpec,
+    ShardedEmbedding,
+    grouped_sharded_embedding_lookup,
+    plan_embedding_shards,
+    pooled_embedding_lookup,
+)
+from mdl_amd.optim import ShardedRowWiseAdagrad
+from oracle import oracle as O
+
+pytestmark = pytest.mark.gpu
+GOLD = json.loads((pathlib.Path(__file__).parent / "golden" / "reference_vectors.json").read_text())
+
+
+def announce(*parts):
+    print("CASE", *parts, flush=True)
+    sys.stdout.flush()
+
+
+def _coo(rows, values, size, dtype=torch.float32, device="cuda"):
+    idx = torch.tensor([rows], dtype=torch.int64, device=device)
+    return torch.sparse_coo_tensor(idx, torch.tensor(values, dtype=dtype, device=device), size=size)
+
+
+def _modules(device, specs):
+    plan = plan_embedding_shards(
+        [EmbeddingTableSpec(n, r, d) for n, r, d in specs], world_size=1, strategy="row_wise",
+        table_wise_max_rows=32,
+    )
+    out = []
+    for n, r, d in specs:
+        m = ShardedEmbedding(r, d, table_name=n, shard_spec=plan.tables[n], padding_idx=0, collect_stats=False)
+        out.append(m.to(device))
+    return out
+
+
+def test_single_rank_grouped_lookup_matches_native_embedding(device):
+    announce("grouped_lookup_native")
+    emb_a, emb_b = _modules(device, [("a", 16, 4), ("b", 16, 4)])
+    full_a = torch.randn(16, 4)
+    full_b = torch.randn(16, 4)
+    full_a[0].zero_()
+    full_b[0].zero_()
+    emb_a.load_full_weight_(full_a.to(device))
+    emb_b.load_full_weight_(full_b.to(device))
+    ids_a = torch.tensor([0, 3, 3, 7], dtype=torch.long, device=device)
+    ids_b = torch.tensor([1, 2, 0, 15], dtype=torch.long, device=device)
+    actual = grouped_sharded_embedding_lookup(((emb_a, ids_a), (emb_b, ids_b)))
+    torch.testing.assert_close(actual[0].cpu(), F.embedding(ids_a.cpu(), full_a, padding_idx=0))
+    torch.testing.assert_close(actual[1].cpu(), F.embedding(ids_b.cpu(), full_b, padding_idx=0))
+    loss = actual[0].square().sum() + actual[1].square().sum()
+    loss.backward()
+    ga = emb_a.weight.grad
+    assert ga is not None and ga.is_sparse and ga.is_coalesced()
+    assert ga.indices()[0].tolist() == [3, 7]  # padding row 0 gets no gradient
+    torch.testing.assert_close(ga.values().cpu(), torch.stack([4 * full_a[3], 2 * full_a[7]]))
+    assert emb_b.weight.grad is not None
+
+
+def test_out_of_range_ids_raise_index_error(device):
+    announce("index_error")
+    (emb,) = _modules(device, [("t", 10, 8)])
+    with pytest.raises(IndexError, match=r"embedding 't' received IDs outside \[0, 10\): \[10, -1\]"):
+        emb(torch.tensor([1, 10, -1], device=device))
+    with pytest.raises(TypeError, match="torch.long"):
+        emb(torch.tensor([1, 2], dtype=torch.int32, device=device))
+
+
+def test_adagrad_golden_mean_not_sum(device):
+    announce("adagrad_golden_mean_not_sum")
+    g = GOLD["rowwise_adagrad_mean_not_sum"]
+    p = nn.Parameter(torch.zeros(*g["shape"], device=device))
+    opt = ShardedRowWiseAdagrad([p], lr=g["lr"], initial_accumulator_value=0.0, eps=g["eps"])
+    p.grad = _coo(g["rows"], g["values"], p.shape, device=device).coalesce()
+    opt.step()
+    state = opt.state[p]["sum"].cpu()
+    for r, a in g["expected_acc"].items():
+        assert abs(float(state[int(r)]) - a) < 1e-6
+    for r, w in g["expected_neg_weight"].items():
+        assert torch.allclose(p[int(r)].neg().cpu(), torch.tensor(w), atol=g["atol"])
+
+
+def test_adagrad_golden_duplicates_coalesce_once(device):
+    announce("adagrad_golden_duplicates")
+    g = GOLD["rowwise_adagrad_duplicates_coalesce"]
+    p = nn.Parameter(torch.zeros(*g["shape"], device=device))
+    opt = ShardedRowWiseAdagrad([p], lr=g["lr"], initial_accumulator_value=0.0, eps=g["eps"])
+    p.grad = _coo(g["rows"], g["values"], p.shape, device=device)  # uncoalesced
+    opt.step()
+    state = opt.state[p]["sum"].cpu()
+    assert abs(float(state[3]) - g["expected_acc"]["3"]) < 1e-6
+    assert int((state != 0).sum()) == g["expected_nonzero_acc_rows"]
+
+
+def test_adagrad_golden_empty_gradient_is_noop(device):
+    announce("adagrad_golden_empty")
+    g = GOLD["rowwise_adagrad_empty_noop"]
+    p = nn.Parameter(torch.ones(*g["shape"], device=device))
+    opt = ShardedRowWiseAdagrad([p], lr=g["lr"], initial_accumulator_value=g["acc0"])
+    before_w = p.detach().clone()
+    before_s = opt.state[p]["sum"].clone()
+    p.grad = torch.sparse_coo_tensor(torch.empty((1, 0), dtype=torch.int64, device=device),
+                                     torch.empty((0, 2), device=device), size=p.shape)
+    opt.step()
+    assert torch.equal(p, before_w) and torch.equal(opt.state[p]["sum"], before_s)
+    assert float(opt.state[p]["step"].item()) == g["expected_step"]
+
+
+def test_adagrad_golden_bf16_untouched_rows(device):
+    announce("adagrad_golden_bf16")
+    g = GOLD["rowwise_adagrad_bf16_untouched"]
+    p = nn.Parameter(torch.tensor(g["weight"], dtype=torch.bfloat16, device=device))
+    before = p.detach().clone()
+    opt = ShardedRowWiseAdagrad([p], lr=g["lr"], initial_accumulator_value=0.0, eps=g["eps"])
+    p.grad = _coo(g["rows"], g["values"], p.shape, dtype=torch.bfloat16, device=device).coalesce()
+    opt.step()
+    for r in g["untouched_rows"]:
+        assert torch.equal(p[r], before[r])
+    assert not torch.equal(p[1], before[1])
+    st = opt.state[p]
+    assert st["sum"].dtype == torch.float32 and st["step"].device.type == "cpu"
+    assert abs(float(st["sum"][1]) - g["expected_acc_row1"]) < 1e-6
+
+
+def test_state_dict_round_trip_keeps_fp32_accumulator(device):
+    announce("state_dict_round_trip")
+    p = nn.Parameter(torch.zeros(4, 2, dtype=torch.bfloat16, device=device))
+    opt = ShardedRowWiseAdagrad([p], lr=0.1, initial_accumulator_value=0.1)
+    p.grad = _coo([0, 2], [[1.0, 2.0], [0.5, 0.5]], p.shape, dtype=torch.bfloat16, device=device).coalesce()
+    opt.step()
+    q = nn.Parameter(p.detach().clone())
+    restored = ShardedRowWiseAdagrad([q], lr=0.1, initial_accumulator_value=0.1)
+    restored.load_state_dict(opt.state_dict())
+    st = restored.state[q]
+    assert st["sum"].dtype == torch.float32 and st["step"].device.type == "cpu"
+    assert torch.allclose(st["sum"], opt.state[p]["sum"])
+    q.grad = _coo([1], [[1.0, 0.0]], q.shape, dtype=torch.bfloat16, device=device).coalesce()
+    restored.step()
+    assert st["sum"].dtype == torch.float32
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+def test_training_steps_match_oracle(device, dtype):
+    """Lookups + mean/sum pooling + loss.backward() + optimizer.step(), 3 steps."""
+
+    announce("training_steps", dtype)
+    rng = np.random.default_rng(90)
+    specs = [("bag_a", 2000, 32), ("bag_b", 500, 16), ("single", 3000, 64)]
+    mods = _modules(device, specs)
+    for m in mods:
+        with torch.no_grad():
+            w = torch.from_numpy(rng.standard_normal(tuple(m.weight.shape)).astype(np.float32))
+            w[0] = 0
+            m.weight.data = w.to(dtype).to(device)
+    opt = ShardedRowWiseAdagrad([m.weight for m in mods], lr=0.05, eps=1e-8)
+    W = [m.weight.detach().float().cpu().numpy().copy() for m in mods]
+    A = [np.zeros(m.weight.shape[0], np.float32) for m in mods]
+    B = 128
+    for step in range(3):
+        la = rng.integers(0, 12, size=B)
+        lb = rng.integers(1, 5, size=B)
+        xa = rng.zipf(1.2, size=int(la.sum())) % 2000
+        xb = rng.integers(0, 500, size=int(lb.sum()))
+        xs = rng.integers(0, 3000, size=B)
+        opt.zero_grad(set_to_none=True)
+        pooled = pooled_embedding_lookup([
+            (mods[0], torch.from_numpy(xa).to(device), torch.from_numpy(la).to(device), "mean", "exclude"),
+            (mods[1], torch.from_numpy(xb).to(device), torch.from_numpy(lb).to(device), "sum", "exclude"),
+        ])
+        single = mods[2](torch.from_numpy(xs).to(device))
+        outs = [pooled[0], pooled[1], single]
+        grads = [torch.from_numpy(rng.standard_normal(tuple(o.shape)).astype(np.float32)).to(dtype).to(device)
+                 for o in outs]
+        torch.autograd.backward(outs, grads)
+        opt.step()
+        # oracle
+        ra, va = O.per_id_grads(xa, la, grads[0].float().cpu().numpy(), "mean", "exclude")
+        rb, vb = O.per_id_grads(xb, lb, grads[1].float().cpu().numpy(), "sum", "exclude")
+        rs, vs = O.per_id_grads(xs, None, grads[2].float().cpu().numpy(), "none", "exclude")
+        for t, (r, v) in enumerate(((ra, va), (rb, vb), (rs, vs))):
+            r, v = O.coalesce(r, v)
+            W[t], A[t] = O.rowwise_adagrad(W[t], A[t], r, v, 0.05, 1e-8, is_bf16=dtype == torch.bfloat16)
+    tol = 1e-5 if dtype == torch.float32 else 1e-2
+    for t, m in enumerate(mods):
+        got = m.weight.detach().float().cpu().numpy()
+        assert np.all(np.abs(got - W[t]) <= tol * np.abs(W[t]) + tol * 1e-1), t
+        s = opt.state[m.weight]["sum"].cpu().numpy()
+        assert np.all(np.abs(s - A[t]) <= 1e-5 * np.abs(A[t]) + 1e-6), t

@@ -1,0 +1,371 @@
+"""GPU parity of every libmdl_hip kernel against the CPU oracle.
+
+Integer work (bucketing, offsets, sort, unique, coalesced rows) must match
+bit for bit; floating point within 1e-5 relative for fp32 storage and 1e-2
+relative for bf16 storage (fp32 accumulation), the tolerances the path's
+specification states.  Every case prints its name and shape before it runs.
+"""
+
+import sys
+
+import numpy as np
+import pytest
+import torch
+
+from mdl_amd import _lib, ops
+from oracle import oracle as O
+
+pytestmark = pytest.mark.gpu
+
+INT64_MIN = -(1 << 63)
+INT64_MAX = (1 << 63) - 1
+RTOL = {torch.float32: 1e-5, torch.bfloat16: 1e-2}
+
+
+def announce(*parts):
+    print("CASE", *parts, flush=True)
+    sys.stdout.flush()
+
+
+def assert_close(got, ref, rtol, atol):
+    got = np.asarray(got, dtype=np.float64)
+    ref = np.asarray(ref, dtype=np.float64)
+    assert got.shape == ref.shape, (got.shape, ref.shape)
+    err = np.abs(got - ref)
+    bound = atol + rtol * np.abs(ref)
+    bad = err > bound
+    assert not bad.any(), f"{int(bad.sum())} mismatches, worst {float((err - bound).max())}"
+
+
+def to_np(t):
+    if t.dtype == torch.bfloat16:
+        return t.float().cpu().numpy()
+    return t.cpu().numpy()
+
+
+# ------------------------------------------------------------- bucketing --
+
+
+def test_bucketize_pre_hashed_bit_exact(device):
+    rng = np.random.default_rng(10)
+    for n in (1, 7, 4096, 100_003):
+        for buckets in (1, 8, 1 << 20, 1 << 40):
+            announce("bucketize_pre_hashed", n, buckets)
+            raw = rng.integers(INT64_MIN, INT64_MAX, size=n, dtype=np.int64, endpoint=True)
+            raw[: min(n, 4)] = [INT64_MIN, INT64_MAX, 0, -1][: min(n, 4)]
+            valid = (rng.random(n) > 0.1).astype(np.uint8)
+            ref, zeros = O.bucketize_pre_hashed(raw, buckets, valid)
+            err = torch.zeros(1, dtype=torch.int32, device=device)
+            got = ops.bucketize(torch.from_numpy(raw).to(device), buckets, valid=torch.from_numpy(valid).to(device),
+                                error_count=err)
+            assert np.array_equal(got.cpu().numpy(), ref)
+            assert int(err.item()) == zeros
+
+
+def test_bucketize_mod_bit_exact(device):
+    rng = np.random.default_rng(11)
+    for n in (1, 5000, 65_537):
+        for rows in (2, 3, 1_000_000, 999_999_937):
+            announce("bucketize_mod", n, rows)
+            raw = rng.integers(INT64_MIN, INT64_MAX, size=n, dtype=np.int64, endpoint=True)
+            raw[: min(n, 3)] = [INT64_MIN, INT64_MAX, 0][: min(n, 3)]
+            got = ops.bucketize(torch.from_numpy(raw).to(device), rows, mode="mod", validate_nonzero=False)
+            assert np.array_equal(got.cpu().numpy(), O.bucketize_mod(raw, rows))
+
+
+def test_lengths_to_offsets_bit_exact(device):
+    rng = np.random.default_rng(12)
+    for n in (0, 1, 5, 2048, 2049, 100_003, 1_638_400):
+        announce("lengths_to_offsets", n)
+        lengths = rng.integers(0, 33, size=n).astype(np.int64)
+        got = ops.lengths_to_offsets(torch.from_numpy(lengths).to(device))
+        assert np.array_equal(got.cpu().numpy(), O.offsets_of(lengths))
+
+
+# ----------------------------------------------------------------- sort --
+
+
+@pytest.mark.parametrize("bits", [1, 7, 8, 13, 24, 31, 32])
+def test_radix_sort_is_stable_and_exact(device, bits):
+    rng = np.random.default_rng(13 + bits)
+    lib = _lib.lib()
+    for n in (1, 100, 4096, 4097, 300_001):
+        announce("sort_pairs", n, bits)
+        hi = (1 << bits) - 1
+        keys = rng.integers(0, hi, size=n, dtype=np.uint64, endpoint=True)
+        keys[: n // 3] = keys[: n // 3] % 17  # many duplicates
+        keys = keys.astype(np.uint32)
+        k = torch.from_numpy(keys.view(np.int32)).to(device)
+        v = torch.arange(n, dtype=torch.int32, device=device)
+        k2 = torch.empty_like(k)
+        v2 = torch.empty_like(v)
+        ws = torch.empty(lib.mdl_sort_workspace_bytes(n), dtype=torch.uint8, device=device)
+        in_alt = _lib.ctypes.c_int32(0)
+        rc = lib.mdl_sort_pairs(k.data_ptr(), v.data_ptr(), k2.data_ptr(), v2.data_ptr(), n, bits, ws.data_ptr(),
+                                ws.numel(), _lib.ctypes.addressof(in_alt), torch.cuda.current_stream().cuda_stream)
+        _lib.check(rc, "mdl_sort_pairs")
+        ks, vs = (k2, v2) if in_alt.value else (k, v)
+        order = np.argsort(keys, kind="stable")
+        assert np.array_equal(ks.cpu().numpy().view(np.uint32), keys[order])
+        assert np.array_equal(vs.cpu().numpy(), order.astype(np.int32))
+
+
+def test_unique_matches_torch_unique(device):
+    rng = np.random.default_rng(14)
+    for n in (1, 1000, 250_000):
+        announce("unique", n)
+        ids = (rng.zipf(1.1, size=n) % 1_000_003).astype(np.int64)
+        u, inv, cnt = ops.unique(torch.from_numpy(ids).to(device))
+        ru, rinv, rcnt = O.unique(ids)
+        assert np.array_equal(u.cpu().numpy(), ru)
+        assert np.array_equal(inv.cpu().numpy(), rinv)
+        assert np.array_equal(cnt.cpu().numpy(), rcnt)
+
+
+# -------------------------------------------------------------- forward --
+
+
+def _table(rng, rows, dim, dtype, device):
+    w = torch.from_numpy(rng.standard_normal((rows, dim)).astype(np.float32)).to(dtype)
+    w[0] = 0
+    return w.to(device)
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+@pytest.mark.parametrize("dim", [1, 3, 4, 8, 16, 24, 64, 128, 256, 300])
+def test_gather_is_exact_copy(device, dtype, dim):
+    rng = np.random.default_rng(dim)
+    announce("gather", dtype, dim)
+    w = _table(rng, 1000, dim, dtype, device)
+    ids = torch.from_numpy(rng.integers(0, 1000, size=(37, 5))).to(device)
+    plan = ops.GroupPlan()
+    plan.add_feature(w, pooling="none")
+    res = ops.grouped_forward(plan, [ids], [None], with_backward=False)
+    out = res.outputs[0]
+    assert out.shape == (37, 5, dim)
+    assert torch.equal(out, w[ids])
+    assert int(res.error_count.item()) == 0
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+@pytest.mark.parametrize("mode", ["sum", "mean"])
+@pytest.mark.parametrize("policy", ["exclude", "include_as_padding"])
+@pytest.mark.parametrize("dim", [4, 16, 24, 32, 64, 128, 300])
+def test_pooled_forward_matches_oracle(device, dtype, mode, policy, dim):
+    rng = np.random.default_rng(dim * 7 + len(mode) + len(policy))
+    announce("pooled_forward", dtype, mode, policy, dim)
+    rows = 5000
+    w = _table(rng, rows, dim, dtype, device)
+    B = 700
+    lengths = rng.integers(0, 33, size=B)
+    lengths[::50] = 0
+    lengths[7] = 2000  # one very long bag spans many passes
+    ids = rng.integers(0, rows, size=int(lengths.sum()))
+    ids[::9] = 0
+    plan = ops.GroupPlan()
+    plan.add_feature(w, pooling=mode, null_policy=policy)
+    res = ops.grouped_forward(plan, [torch.from_numpy(ids).to(device)], [torch.from_numpy(lengths).to(device)],
+                              with_backward=False)
+    ref, _ = O.pool(to_np(w), ids, lengths, mode, policy)
+    assert_close(to_np(res.outputs[0]), ref, RTOL[dtype], 1e-6 if dtype == torch.float32 else 1e-2)
+
+
+def test_grouped_mixed_features_one_launch(device):
+    """Pooled and unpooled features of several dims and two aliased tables."""
+
+    rng = np.random.default_rng(21)
+    announce("grouped_mixed")
+    tabs = [_table(rng, r, d, torch.float32, device) for r, d in ((300, 16), (5000, 64), (77, 128), (1000, 32))]
+    B = 257
+    plan = ops.GroupPlan()
+    spec = [(0, "mean", "exclude"), (1, "sum", "include_as_padding"), (2, "none", "exclude"),
+            (1, "mean", "include_as_padding"), (3, "none", "exclude"), (0, "sum", "exclude")]
+    ids, lens, refs = [], [], []
+    for t, mode, pol in spec:
+        plan.add_feature(tabs[t], pooling=mode, null_policy=pol)
+        rows = tabs[t].shape[0]
+        if mode == "none":
+            x = rng.integers(0, rows, size=B)
+            ids.append(torch.from_numpy(x).to(device))
+            lens.append(None)
+            refs.append(O.gather(to_np(tabs[t]), x))
+        else:
+            ln = rng.integers(0, 20, size=B)
+            x = rng.integers(0, rows, size=int(ln.sum()))
+            ids.append(torch.from_numpy(x).to(device))
+            lens.append(torch.from_numpy(ln).to(device))
+            refs.append(O.pool(to_np(tabs[t]), x, ln, mode, pol)[0])
+    assert len(plan.tables) == 4
+    res = ops.grouped_forward(plan, ids, lens, with_backward=False)
+    for out, ref in zip(res.outputs, refs):
+        assert_close(to_np(out), ref, 1e-5, 1e-6)
+
+
+@pytest.mark.parametrize("order", ["oldest_to_newest", "newest_to_oldest"])
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+def test_sequence_forward_matches_oracle(device, order, dtype):
+    rng = np.random.default_rng(22)
+    announce("sequence_forward", order, dtype)
+    w = _table(rng, 3000, 64, dtype, device)
+    B, L = 33, 200
+    lengths = rng.integers(0, L + 1, size=B)
+    lengths[0] = L
+    ids = np.zeros((B, L), dtype=np.int64)
+    for b in range(B):
+        ids[b, : lengths[b]] = rng.integers(1, 3000, size=lengths[b])
+    for out_len in (L, 150, 256):
+        out, mask = ops.sequence_forward(w, torch.from_numpy(ids).to(device), torch.from_numpy(lengths).to(device),
+                                         out_len=out_len, order=order)
+        ref, rmask = O.sequence_gather(to_np(w), ids, lengths, out_len, order)
+        assert np.array_equal(mask.cpu().numpy(), rmask)
+        assert np.array_equal(to_np(out), ref.astype(np.float32))
+
+
+def test_invalid_ids_are_counted_not_read(device):
+    rng = np.random.default_rng(23)
+    announce("invalid_ids")
+    w = _table(rng, 100, 16, torch.float32, device)
+    ids = torch.tensor([1, 2, 100, -1, 5], device=device)
+    plan = ops.GroupPlan()
+    plan.add_feature(w, pooling="none")
+    res = ops.grouped_forward(plan, [ids], [None], with_backward=False)
+    assert int(res.error_count.item()) == 2
+    out = res.outputs[0]
+    assert torch.equal(out[[0, 1, 4]], w[[1, 2, 5]])
+    assert out[2].abs().sum() == 0 and out[3].abs().sum() == 0
+    # lengths that overrun the ids are clamped and counted
+    plan = ops.GroupPlan()
+    plan.add_feature(w, pooling="sum")
+    res = ops.grouped_forward(plan, [torch.tensor([1, 2, 3], device=device)],
+                              [torch.tensor([2, 5], device=device)], with_backward=False)
+    assert int(res.error_count.item()) > 0
+    assert_close(to_np(res.outputs[0][0]), to_np(w[1] + w[2]), 1e-6, 1e-6)
+
+
+# -------------------------------------------------------------- backward --
+
+
+def _random_group(rng, device, dtype=torch.float32, hot=False, B=300):
+    dims = [16, 64, 32, 128, 24]
+    rows = [50, 4000, 100_000, 700, 1000]
+    tabs = [_table(rng, r, d, dtype, device) for r, d in zip(rows, dims)]
+    spec = [(0, "mean", "exclude"), (1, "sum", "include_as_padding"), (2, "none", "exclude"),
+            (1, "mean", "exclude"), (3, "none", "exclude"), (4, "mean", "include_as_padding")]
+    plan = ops.GroupPlan()
+    states = [torch.from_numpy(rng.random(r).astype(np.float32)).to(device) for r in rows]
+    ids, lens, meta = [], [], []
+    for t, mode, pol in spec:
+        plan.add_feature(tabs[t], pooling=mode, null_policy=pol, state=states[t])
+        r = rows[t]
+        if mode == "none":
+            x = rng.integers(0, r, size=B)
+            ln = None
+        else:
+            ln = rng.integers(0, 40, size=B)
+            x = (rng.zipf(1.2, size=int(ln.sum())) % r) if hot else rng.integers(0, r, size=int(ln.sum()))
+        if hot:
+            x[: len(x) // 2] = 3  # one row with thousands of entries spans many chunks
+        x[::11] = 0
+        ids.append(torch.from_numpy(np.asarray(x, dtype=np.int64)).to(device))
+        lens.append(None if ln is None else torch.from_numpy(ln).to(device))
+        meta.append((t, mode, pol, np.asarray(x), ln))
+    return plan, tabs, states, ids, lens, meta, dims
+
+
+@pytest.mark.parametrize("hot", [False, True])
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+def test_backward_coalesce_matches_oracle(device, hot, dtype):
+    rng = np.random.default_rng(30 + hot)
+    announce("backward_coalesce", hot, dtype)
+    plan, tabs, states, ids, lens, meta, dims = _random_group(rng, device, dtype, hot)
+    res = ops.grouped_forward(plan, ids, lens, with_backward=True)
+    grads = [torch.from_numpy(rng.standard_normal(tuple(o.shape)).astype(np.float32)).to(dtype).to(device)
+             for o in res.outputs]
+    out = ops.backward_coalesce(res, grads)
+    for t in range(len(tabs)):
+        rs, vs = [], []
+        for f, (tt, mode, pol, x, ln) in enumerate(meta):
+            if tt != t:
+                continue
+            g = to_np(grads[f]).reshape(-1, dims[t])
+            r, v = O.per_id_grads(x, ln, g, mode, pol)
+            rs.append(r)
+            vs.append(v)
+        rr, vv = O.coalesce(np.concatenate(rs), np.concatenate(vs))
+        rows, vals = out[t]
+        assert np.array_equal(rows.cpu().numpy(), rr), f"table {t} rows"
+        assert_close(to_np(vals), vv, RTOL[dtype], 1e-5 if dtype == torch.float32 else 1e-2)
+
+
+@pytest.mark.parametrize("hot", [False, True])
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+def test_fused_backward_adagrad_matches_oracle(device, hot, dtype):
+    rng = np.random.default_rng(40 + hot)
+    announce("fused_backward_adagrad", hot, dtype)
+    plan, tabs, states, ids, lens, meta, dims = _random_group(rng, device, dtype, hot)
+    w0 = [to_np(t).copy() for t in tabs]
+    a0 = [s.cpu().numpy().copy() for s in states]
+    res = ops.grouped_forward(plan, ids, lens, with_backward=True)
+    grads = [torch.from_numpy(rng.standard_normal(tuple(o.shape)).astype(np.float32)).to(dtype).to(device)
+             for o in res.outputs]
+    lr, eps = 0.01, 1e-8
+    ops.backward_adagrad(res, grads, lr=lr, eps=eps)
+    for t in range(len(tabs)):
+        rs, vs = [], []
+        for f, (tt, mode, pol, x, ln) in enumerate(meta):
+            if tt != t:
+                continue
+            r, v = O.per_id_grads(x, ln, to_np(grads[f]).reshape(-1, dims[t]), mode, pol)
+            rs.append(r)
+            vs.append(v)
+        rr, vv = O.coalesce(np.concatenate(rs), np.concatenate(vs))
+        wexp, aexp = O.rowwise_adagrad(w0[t], a0[t], rr, vv, lr, eps, is_bf16=dtype == torch.bfloat16)
+        assert_close(states[t].cpu().numpy(), aexp, 1e-5, 1e-7)
+        assert_close(to_np(tabs[t]), wexp, RTOL[dtype], 1e-6 if dtype == torch.float32 else 1e-2)
+        untouched = np.setdiff1d(np.arange(w0[t].shape[0]), rr)
+        assert np.array_equal(to_np(tabs[t])[untouched], w0[t][untouched])
+
+
+def test_fused_backward_is_deterministic(device):
+    announce("determinism")
+    results = []
+    for _ in range(2):
+        rng = np.random.default_rng(50)
+        plan, tabs, states, ids, lens, meta, dims = _random_group(rng, device, torch.float32, True)
+        res = ops.grouped_forward(plan, ids, lens, with_backward=True)
+        grads = [torch.from_numpy(rng.standard_normal(tuple(o.shape)).astype(np.float32)).to(device)
+                 for o in res.outputs]
+        ops.backward_adagrad(res, grads, lr=0.01, eps=1e-8)
+        results.append([t.cpu().clone() for t in tabs] + [s.cpu().clone() for s in states])
+    for a, b in zip(*results):
+        assert torch.equal(a, b)
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+@pytest.mark.parametrize("dim", [2, 16, 48, 128, 256])
+def test_rowwise_adagrad_matches_oracle(device, dtype, dim):
+    rng = np.random.default_rng(60 + dim)
+    announce("rowwise_adagrad", dtype, dim)
+    rows = 3000
+    w = _table(rng, rows, dim, dtype, device)
+    acc = torch.from_numpy(rng.random(rows).astype(np.float32)).to(device)
+    touched = rng.choice(rows, size=900, replace=False)
+    vals = rng.standard_normal((900, dim)).astype(np.float32)
+    vt = torch.from_numpy(vals).to(dtype).to(device)
+    wexp, aexp = O.rowwise_adagrad(to_np(w), acc.cpu().numpy(), touched, to_np(vt), 0.05, 1e-8,
+                                   is_bf16=dtype == torch.bfloat16)
+    ops.rowwise_adagrad_(w, acc, torch.from_numpy(touched).to(device), vt, lr=0.05, eps=1e-8)
+    assert_close(acc.cpu().numpy(), aexp, 1e-5, 1e-7)
+    assert_close(to_np(w), wexp, RTOL[dtype], 1e-6 if dtype == torch.float32 else 1e-2)
+
+
+def test_coalesce_rows_matches_torch(device):
+    rng = np.random.default_rng(70)
+    announce("coalesce_rows")
+    n, dim, rows = 50_000, 32, 10_000
+    idx = (rng.zipf(1.1, size=n) % rows).astype(np.int64)
+    vals = rng.standard_normal((n, dim)).astype(np.float32)
+    r, v = ops.coalesce_rows(torch.from_numpy(idx).to(device), torch.from_numpy(vals).to(device), rows)
+    rr, vv = O.coalesce(idx, vals.astype(np.float64))
+    assert np.array_equal(r.cpu().numpy(), rr)
+    assert_close(v.cpu().numpy(), vv, 1e-5, 1e-5)
