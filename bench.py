@@ -1,0 +1,462 @@
+"""Benchmark of the MI355X sparse path: fused forward + backward + row-wise
+Adagrad over one synthetic batch per step.
+
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--config c1]
+
+Prints one JSON line.  ``value`` is looked-up (non-padding) rows per second
+of the whole step, timed between device synchronisations with every input
+already resident in HBM.  ``roofline`` reports the dominant kernel's
+algorithmic bytes per launch over its HIP-event-measured duration against
+MI355X's 8 TB/s; ``cpu_baseline`` times the CPU oracle (a plain-C port of
+the reference path) on a bounded sample of the same workload.
+
+Workloads:
+  c1  RankMixer-scale step (default): 200 features (150 single-valued, 50 bags
+      of 1..32 ids), batch 8192, table rows log-uniform in [1e3, 5e7] scaled to
+      1.5e9 rows in total, dims {16,32,64,128} (tables above 1e7 rows use 16/32
+      so fp32 tables + state fit one GPU), fp32, Zipf(1.1) ids, mean pooling.
+  c3  c1 with bf16 tables (fp32 accumulation and state).
+  c0  32 tables x 1e6 x 64 fp32, batch 4096, Poisson(3) bags clipped to
+      [1,16], Zipf(1.05) raw ids over 2^40 bucketed mod table size, sum pooling.
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import platform
+import sys
+import time
+from dataclasses import dataclass, field
+from pathlib import Path
+
+import numpy as np
+
+ROOT = Path(__file__).resolve().parent
+sys.path.insert(0, str(ROOT))
+
+METRIC = "looked-up rows/s + achieved HBM GB/s (fwd+bwd+Adagrad) at batch 8192, 1 GPU"
+PEAK_HBM_GBPS = 8000.0
+
+
+# ------------------------------------------------------------- workloads --
+
+
+@dataclass
+class Feature:
+    table: int
+    pooling: str  # "none" | "sum" | "mean"
+    bag_len: tuple[int, int] | None  # uniform [lo, hi] bag length; None = single-valued
+    poisson: float | None = None
+
+
+@dataclass
+class Workload:
+    name: str
+    batch: int
+    rows: list[int]
+    dims: list[int]
+    dtype: str  # "fp32" | "bf16"
+    features: list[Feature]
+    zipf: list[float]  # per table; 0 = uniform
+    raw_bits: int | None = None  # raw ids drawn over 2^raw_bits then bucketed mod rows
+    lr: float = 0.01
+    eps: float = 1e-8
+    notes: dict = field(default_factory=dict)
+
+
+def workload_c1(dtype: str = "fp32") -> Workload:
+    rng = np.random.default_rng(2024)
+    n_tables = 200
+    log_rows = rng.uniform(np.log(1e3), np.log(5e7), size=n_tables)
+    rows = np.exp(log_rows)
+    rows = np.maximum((rows * (1.5e9 / rows.sum())).astype(np.int64), 1000)
+    dims = rng.choice([16, 32, 64, 128], size=n_tables)
+    big = rows > 10_000_000
+    dims[big] = rng.choice([16, 32], size=int(big.sum()))
+    esize = 4 if dtype == "fp32" else 2
+    # keep weights + fp32 state under 250 GB: narrow the largest tables first
+    order = np.argsort(-rows)
+    k = 0
+    while int((rows * dims * esize + rows * 4).sum()) > 250e9 and k < n_tables:
+        dims[order[k]] = 16
+        k += 1
+    feats = []
+    perm = rng.permutation(n_tables)
+    bag_tables = set(perm[:50].tolist())
+    for t in range(n_tables):
+        if t in bag_tables:
+            feats.append(Feature(table=t, pooling="mean", bag_len=(1, 32)))
+        else:
+            feats.append(Feature(table=t, pooling="none", bag_len=None))
+    return Workload(
+        name="c1" if dtype == "fp32" else "c3",
+        batch=8192,
+        rows=rows.tolist(),
+        dims=dims.tolist(),
+        dtype=dtype,
+        features=feats,
+        zipf=[1.1] * n_tables,
+        notes={"table_rows_total": int(rows.sum())},
+    )
+
+
+def workload_c0() -> Workload:
+    feats = [Feature(table=t, pooling="sum", bag_len=(1, 16), poisson=3.0) for t in range(32)]
+    return Workload(
+        name="c0", batch=4096, rows=[1_000_000] * 32, dims=[64] * 32, dtype="fp32", features=feats,
+        zipf=[1.05] * 32, raw_bits=40,
+    )
+
+
+WORKLOADS = {"c1": workload_c1, "c3": lambda: workload_c1("bf16"), "c0": workload_c0}
+
+
+def bounded_zipf(rng: np.random.Generator, alpha: float, n: int, hi: int) -> np.ndarray:
+    """Zipf(alpha) on [1, hi] by inverse CDF over a log-spaced grid (alpha > 0)."""
+
+    if alpha > 1.0 and hi > 1 << 40:
+        return rng.zipf(alpha, size=n)
+    grid = np.unique(np.logspace(0, np.log10(hi), 4096).astype(np.int64))
+    grid = grid[grid >= 1]
+    # P(X <= k) ~ H(k, alpha) / H(hi, alpha), H via the integral approximation
+    def H(k):
+        k = k.astype(np.float64)
+        if abs(alpha - 1.0) < 1e-9:
+            return np.log(k) + 0.5772156649 + 1 / (2 * k)
+        return (k ** (1 - alpha) - 1) / (1 - alpha) + 0.5 * (1 + k ** (-alpha))
+    cdf = H(grid) / H(np.array([hi]))[0]
+    u = rng.random(n)
+    idx = np.searchsorted(cdf, u)
+    idx = np.minimum(idx, grid.size - 1)
+    lo = np.where(idx > 0, grid[np.maximum(idx - 1, 0)] + 1, 1)
+    hi_ = grid[idx]
+    return lo + (rng.random(n) * (hi_ - lo + 1)).astype(np.int64)
+
+
+def draw_ids(rng: np.random.Generator, wl: Workload, t: int, n: int) -> np.ndarray:
+    rows = wl.rows[t]
+    a = wl.zipf[t]
+    if a <= 0:
+        return rng.integers(1, rows, size=n)
+    if wl.raw_bits:
+        raw = bounded_zipf(rng, a, n, 1 << wl.raw_bits)
+    else:
+        raw = rng.zipf(a, size=n)
+    # the reference benchmark's id rule: 1 + (z - 1) mod (N - 1), src/benchmark.py:1246-1250
+    return 1 + (raw - 1) % (rows - 1)
+
+
+def draw_batch(rng: np.random.Generator, wl: Workload):
+    """Per-feature ids and bag lengths (None for single-valued features)."""
+
+    ids, lengths = [], []
+    for f in wl.features:
+        if f.bag_len is None:
+            ln = None
+            n = wl.batch
+        else:
+            lo, hi = f.bag_len
+            if f.poisson:
+                ln = np.clip(rng.poisson(f.poisson, size=wl.batch), lo, hi)
+            else:
+                ln = rng.integers(lo, hi + 1, size=wl.batch)
+            n = int(ln.sum())
+        ids.append(draw_ids(rng, wl, f.table, n))
+        lengths.append(ln)
+    return ids, lengths
+
+
+def algorithmic_bytes(wl: Workload, ids, lengths) -> dict:
+    """Per-step algorithmic HBM bytes (SURVEY 8(d) formula) and its parts."""
+
+    esize = 4 if wl.dtype == "fp32" else 2
+    n_t = {}
+    uniq_t = {}
+    bags_t = {}
+    for f, x, ln in zip(wl.features, ids, lengths):
+        n_t.setdefault(f.table, []).append(x)
+        bags_t[f.table] = bags_t.get(f.table, 0) + (len(ln) if ln is not None else wl.batch)
+    total = 0
+    fwd_unique_rows_bytes = 0
+    n_ids = 0
+    for t, xs in n_t.items():
+        x = np.concatenate(xs)
+        x = x[x != 0]
+        u = np.unique(x).size
+        uniq_t[t] = u
+        n = x.size
+        n_ids += n
+        d = wl.dims[t]
+        total += 16 * n + 16 * (bags_t[t] + 1) + 3 * u * d * esize + 8 * u
+        fwd_unique_rows_bytes += u * d * esize
+    sum_d = sum(wl.dims[f.table] for f in wl.features)
+    total += 2 * wl.batch * sum_d * 4
+    return {
+        "B_alg": total,
+        "n_ids": n_ids,
+        "unique_rows": int(sum(uniq_t.values())),
+        "fwd_unique_row_bytes": fwd_unique_rows_bytes,
+        "sum_dim": sum_d,
+    }
+
+
+# ---------------------------------------------------------------- device --
+
+
+class DeviceStep:
+    """Buffers and launches of one fused sparse step on the GPU."""
+
+    def __init__(self, wl: Workload, batches, device):
+        import torch
+
+        from mdl_amd import ops
+
+        self.torch = torch
+        self.ops = ops
+        self.wl = wl
+        self.device = device
+        wdtype = torch.float32 if wl.dtype == "fp32" else torch.bfloat16
+        self.tables = []
+        self.states = []
+        gen = torch.Generator(device=device)
+        gen.manual_seed(1234)
+        for r, d in zip(wl.rows, wl.dims):
+            w = torch.empty((r, d), dtype=wdtype, device=device)
+            w.normal_(0.0, 0.02, generator=gen)
+            w[0].zero_()
+            self.tables.append(w)
+            self.states.append(torch.zeros(r, dtype=torch.float32, device=device))
+        self.plan = ops.GroupPlan()
+        for f in wl.features:
+            self.plan.add_feature(
+                self.tables[f.table], pooling=f.pooling, null_policy="exclude", state=self.states[f.table]
+            )
+        sum_d = sum(wl.dims[f.table] for f in wl.features)
+        self.out = torch.empty((wl.batch, sum_d), dtype=wdtype, device=device)
+        self.grad = torch.empty((wl.batch, sum_d), dtype=wdtype, device=device)
+        self.grad.normal_(0.0, 1.0, generator=gen)
+        col = 0
+        self.out_views = []
+        self.grad_views = []
+        for f in wl.features:
+            d = wl.dims[f.table]
+            self.out_views.append(self.out[:, col: col + d])
+            self.grad_views.append(self.grad[:, col: col + d])
+            col += d
+        # device-resident batches: packed ids + concatenated lengths (an unpooled
+        # feature contributes one pseudo-bag holding all its ids)
+        self.batches = []
+        for ids, lengths in batches:
+            id_counts = [int(x.size) for x in ids]
+            bag_counts = [0 if ln is None else int(ln.size) for ln in lengths]
+            parts = [ln if ln is not None else np.array([x.size]) for x, ln in zip(ids, lengths)]
+            packed = torch.from_numpy(np.concatenate(ids).astype(np.int64)).to(device)
+            lens = torch.from_numpy(np.concatenate(parts).astype(np.int64)).to(device)
+            self.batches.append((packed, lens, id_counts, bag_counts))
+        self.err = torch.zeros(1, dtype=torch.int32, device=device)
+        self.t_fwd = []
+
+    def step(self, i: int, timer=None):
+        ops = self.ops
+        packed, lens, id_counts, bag_counts = self.batches[i % len(self.batches)]
+        offsets = ops.lengths_to_offsets(lens)
+        if timer is not None:
+            timer.mark("fwd_start")
+        res = ops.forward_packed(
+            self.plan, packed, offsets, id_counts, bag_counts, self.out_views, with_backward=True,
+            error_count=self.err,
+        )
+        if timer is not None:
+            timer.mark("fwd_end")
+        ops.backward_adagrad(res, self.grad_views, lr=self.wl.lr, eps=self.wl.eps)
+        return res
+
+
+class EventTimer:
+    """HIP events recorded on the launch stream around one kernel."""
+
+    def __init__(self, torch):
+        self.torch = torch
+        self.pairs = []
+        self._open = None
+
+    def mark(self, name):
+        ev = self.torch.cuda.Event(enable_timing=True)
+        ev.record(self.torch.cuda.current_stream())
+        if name.endswith("_start"):
+            self._open = ev
+        else:
+            self.pairs.append((self._open, ev))
+
+    def mean_ms(self):
+        self.torch.cuda.synchronize()
+        ts = [a.elapsed_time(b) for a, b in self.pairs]
+        return float(np.mean(ts)) if ts else float("nan")
+
+
+# ------------------------------------------------------------ cpu baseline --
+
+
+def cpu_baseline(wl: Workload, seconds: float = 12.0, row_cap: int = 1 << 16, batch: int = 512) -> dict:
+    """Time the CPU oracle (plain-C port of the reference step) on a sample."""
+
+    from oracle import oracle as O
+
+    rng = np.random.default_rng(7)
+    sample = Workload(
+        name=wl.name, batch=batch, rows=[min(r, row_cap) for r in wl.rows], dims=wl.dims, dtype=wl.dtype,
+        features=wl.features, zipf=wl.zipf, raw_bits=wl.raw_bits, lr=wl.lr, eps=wl.eps,
+    )
+    tables = []
+    for r, d in zip(sample.rows, sample.dims):
+        # values do not affect the CPU time; tile one random block to fill fast
+        W = np.resize(rng.standard_normal((min(r, 4096), d), dtype=np.float32) * np.float32(0.02), (r, d))
+        W[0] = 0
+        tables.append({"W": W, "acc": np.zeros(r, np.float32), "is_bf16": wl.dtype == "bf16"})
+    ids, lengths = draw_batch(rng, sample)
+    feats = []
+    offs_parts = []
+    bag_off = 0
+    ids_off = 0
+    col = 0
+    for f, x, ln in zip(sample.features, ids, lengths):
+        pooling = {"none": 0, "sum": 1, "mean": 2}[f.pooling]
+        feats.append({"table": f.table, "pooling": pooling, "exclude": 1, "ids_off": ids_off,
+                      "bag_off": bag_off, "num_bags": 0 if ln is None else len(ln), "out_col": col})
+        if ln is not None:
+            o = O.offsets_of(ln)
+            offs_parts.append(o)
+            bag_off += len(o)
+        ids_off += x.size
+        col += sample.dims[f.table]
+    all_ids = np.concatenate(ids)
+    offs = np.concatenate(offs_parts) if offs_parts else np.zeros(1, np.int64)
+    grad = rng.standard_normal((batch, col))
+    n_active = int(sum(int((x != 0).sum()) for x in ids))
+    steps = 0
+    t0 = time.perf_counter()
+    while True:
+        O.sparse_step(feats, tables, all_ids, offs, col, grad, wl.lr, wl.eps)
+        steps += 1
+        el = time.perf_counter() - t0
+        if el >= seconds:
+            break
+    return {
+        "value": n_active * steps / el,
+        "unit": "rows/s",
+        "cores": 1,
+        "kind": "port",
+        "sample": (f"{wl.name} layout at batch {batch} (of {wl.batch}), tables capped at {row_cap} rows "
+                   f"(same id stream bucketed mod the cap), {steps} steps in {el:.1f} s, "
+                   f"single-threaded C oracle on {platform.processor() or platform.machine()}, "
+                   f"host has {os.cpu_count()} cores"),
+    }
+
+
+# ------------------------------------------------------------------- main --
+
+
+def main() -> int:
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=30)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--config", default="c1", choices=sorted(WORKLOADS))
+    ap.add_argument("--batches", type=int, default=3, help="distinct synthetic batches cycled through")
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--cpu-seconds", type=float, default=12.0)
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU only; --gpus {args.gpus} is not supported in this build "
+              "(the path is single-GPU; multi-GPU sharding is a design note, not a measured run)",
+              file=sys.stderr)
+        return 2
+
+    import torch
+
+    device = torch.device("cuda:0")
+    wl = WORKLOADS[args.config]()
+    print(f"[bench] workload {wl.name}: {len(wl.features)} features, {len(wl.rows)} tables, "
+          f"{sum(wl.rows):.3e} rows, batch {wl.batch}, {wl.dtype}", file=sys.stderr, flush=True)
+    rng = np.random.default_rng(99)
+    batches = [draw_batch(rng, wl) for _ in range(args.batches)]
+    alg = [algorithmic_bytes(wl, ids, lengths) for ids, lengths in batches]
+    print(f"[bench] drew {args.batches} batches; {alg[0]['n_ids']} ids/step, "
+          f"{alg[0]['unique_rows']} distinct rows", file=sys.stderr, flush=True)
+    dev = DeviceStep(wl, batches, device)
+    torch.cuda.synchronize()
+    print("[bench] tables initialised", file=sys.stderr, flush=True)
+    for i in range(args.warmup):
+        dev.step(i)
+    torch.cuda.synchronize()
+    if int(dev.err.item()):
+        raise RuntimeError("synthetic ids out of range")
+    timer = EventTimer(torch)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for i in range(args.steps):
+        dev.step(args.warmup + i, timer)
+    torch.cuda.synchronize()
+    elapsed = time.perf_counter() - t0
+    ms = elapsed * 1e3 / args.steps
+    used = [alg[(args.warmup + i) % len(alg)] for i in range(args.steps)]
+    n_ids = float(np.mean([a["n_ids"] for a in used]))
+    b_alg = float(np.mean([a["B_alg"] for a in used]))
+    rows_per_s = n_ids / (ms * 1e-3)
+    gbps = b_alg / (ms * 1e-3) / 1e9
+    # dominant kernel: the grouped forward (one launch), bracketed by events
+    fwd_ms = timer.mean_ms()
+    nb = sum(len(ln) for ln in batches[0][1] if ln is not None)
+    fwd_bytes = float(np.mean([
+        16 * a["n_ids"] + 8 * (nb + 1) + a["fwd_unique_row_bytes"] + wl.batch * a["sum_dim"] * (4 if wl.dtype == "fp32" else 2)
+        + 4 * nb for a in used
+    ]))
+    fwd_gbps = fwd_bytes / (fwd_ms * 1e-3) / 1e9
+    result = {
+        "metric": METRIC,
+        "value": rows_per_s,
+        "unit": "rows/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": ms,
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f32" if wl.dtype == "fp32" else "bf16-storage/f32-accumulate",
+        "data": "synthetic (seeded Zipf ids, random-init tables)",
+        "config": {
+            "workload": f"{wl.name}: {len(wl.features)} features, batch {wl.batch}, "
+                        f"{sum(wl.rows):.3e} table rows, {wl.dtype} tables, fused fwd+bwd+row-wise Adagrad",
+            "global_batch": wl.batch,
+            "ids_per_step": n_ids,
+            "distinct_rows_per_step": float(np.mean([a["unique_rows"] for a in used])),
+            "parallelism": "single GPU",
+        },
+        "hbm_gbps_achieved": gbps,
+        "roofline_fraction_step": gbps / PEAK_HBM_GBPS,
+        "B_alg_bytes_per_step": b_alg,
+        "roofline": {
+            "kernel": "forward_kernel (grouped lookup + pooling + sort-key emission)",
+            "bound": "hbm",
+            "achieved": fwd_gbps,
+            "peak": PEAK_HBM_GBPS,
+            "unit": "GB/s",
+            "frac": fwd_gbps / PEAK_HBM_GBPS,
+            "traffic": None,
+            "kernel_ms": fwd_ms,
+            "alg_bytes_per_launch": fwd_bytes,
+        },
+        "cpu_baseline": None,
+    }
+    if not args.no_cpu_baseline:
+        print("[bench] timing the CPU oracle sample", file=sys.stderr, flush=True)
+        result["cpu_baseline"] = cpu_baseline(wl, seconds=args.cpu_seconds)
+    print(json.dumps(result), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

@@ -21,9 +21,8 @@ int sort_pairs(uint32_t* keys, uint32_t* vals, uint32_t* keys_alt, uint32_t* val
                int key_bits, void* ws, size_t ws_bytes, int* in_alt, hipStream_t s);
 size_t sort_ws_bytes(int64_t n);
 
-constexpr int kChunk = 1024;
+constexpr int kChunkMax = 1024;
 constexpr int kBwdWaves = 4;
-constexpr int kBwdUnroll = 4;
 constexpr int kPlanThreads = 1024;
 
 enum { kHeadOpen = 1, kTailOpen = 2, kSingle = 4 };
@@ -37,6 +36,7 @@ struct BwdWs {
   int64_t* table_start;   // [T]
   int64_t* table_end;     // [T]
   int64_t* chunk_base;    // [T+1]
+  int64_t* table_cb;      // [T] entries per chunk of table t
   int32_t* chunk_flags;   // [max_chunks]
   int64_t* head_base;     // [max_chunks+1]
   void* scan_ws;
@@ -45,7 +45,11 @@ struct BwdWs {
   float* part_last;       // [max_chunks, max_dim]
 };
 
-static inline int64_t max_chunks_for(int64_t n, int32_t T) { return (n + kChunk - 1) / kChunk + T + 1; }
+// Chunks hold kPassesPerChunk passes of G rows; G >= 1, so a table of m
+// entries has at most ceil(m / kPassesPerChunk) chunks.
+static inline int64_t max_chunks_for(int64_t n, int32_t T) {
+  return (n + kPassesPerChunk - 1) / kPassesPerChunk + T + 1;
+}
 
 static size_t carve(BwdWs* w, void* base, int64_t n, int32_t T, int32_t max_dim) {
   char* p = static_cast<char*>(base);
@@ -64,6 +68,7 @@ static size_t carve(BwdWs* w, void* base, int64_t n, int32_t T, int32_t max_dim)
   w->table_start = (int64_t*)take((size_t)T * 8 + 8);
   w->table_end = (int64_t*)take((size_t)T * 8 + 8);
   w->chunk_base = (int64_t*)take(((size_t)T + 1) * 8);
+  w->table_cb = (int64_t*)take((size_t)T * 8 + 8);
   w->chunk_flags = (int32_t*)take((size_t)mc * 4);
   w->head_base = (int64_t*)take(((size_t)mc + 1) * 8);
   w->scan_bytes = mdl_offsets_workspace_bytes(mc);
@@ -85,10 +90,25 @@ __device__ __forceinline__ int64_t lower_bound_u32(const uint32_t* a, int64_t n,
   return lo;
 }
 
+// Whether a table's rows (and so its gradient and value rows, which the host
+// lays out alike) use 16-byte vectors, and the chunk length that gives one
+// wave kPassesPerChunk passes over it.
+__device__ __forceinline__ bool table_vec(const mdl_table& tb) {
+  const int wsz = tb.wdtype == MDL_BF16 ? 2 : 4;
+  return (tb.weight % 16 == 0) && ((int64_t)tb.dim * wsz) % 16 == 0;
+}
+
+__device__ __forceinline__ int64_t table_chunk_len(const mdl_table& tb) {
+  const int c = table_vec(tb) ? (tb.wdtype == MDL_BF16 ? 8 : 4) : 1;
+  const int64_t g = kWave / lanes_for(tb.dim > 0 ? tb.dim : 1, c);
+  const int64_t cb = (int64_t)kPassesPerChunk * g;
+  return cb < kChunkMax ? cb : kChunkMax;
+}
+
 __global__ __launch_bounds__(kPlanThreads) void bwd_plan_kernel(const mdl_table* __restrict__ tables, int32_t T,
                                                                  const uint32_t* __restrict__ keys, int64_t n,
                                                                  int64_t* table_start, int64_t* table_end,
-                                                                 int64_t* chunk_base) {
+                                                                 int64_t* chunk_base, int64_t* table_cb) {
   __shared__ int64_t smem[kPlanThreads];
   int64_t carry = 0;
   for (int32_t base = 0; base < T; base += kPlanThreads) {
@@ -101,7 +121,9 @@ __global__ __launch_bounds__(kPlanThreads) void bwd_plan_kernel(const mdl_table*
       const int64_t hi = lower_bound_u32(keys, n, hi_key);
       table_start[t] = lo;
       table_end[t] = hi;
-      nch = (hi - lo + kChunk - 1) / kChunk;
+      const int64_t cb = table_chunk_len(tables[t]);
+      table_cb[t] = cb;
+      nch = (hi - lo + cb - 1) / cb;
     }
     smem[threadIdx.x] = nch;
     __syncthreads();
@@ -133,7 +155,7 @@ __device__ __forceinline__ int64_t uni64b(int64_t v) {
 // Locate chunk c: returns false when c is past the last chunk.
 __device__ __forceinline__ bool find_chunk(int64_t c, int32_t T, const int64_t* chunk_base,
                                            const int64_t* table_start, const int64_t* table_end,
-                                           ChunkRange* r) {
+                                           const int64_t* table_cb, ChunkRange* r) {
   const int64_t total = chunk_base[T];
   if (c >= total) return false;
   int32_t lo = 0, hi = T - 1;  // last t with chunk_base[t] <= c
@@ -147,8 +169,9 @@ __device__ __forceinline__ bool find_chunk(int64_t c, int32_t T, const int64_t* 
   r->t = __builtin_amdgcn_readfirstlane(lo);
   r->t_begin = uni64b(table_start[lo]);
   r->t_end = uni64b(table_end[lo]);
-  r->c_begin = r->t_begin + (c - chunk_base[lo]) * kChunk;
-  r->c_end = r->c_begin + kChunk < r->t_end ? r->c_begin + kChunk : r->t_end;
+  const int64_t cb = uni64b(table_cb[lo]);
+  r->c_begin = r->t_begin + (c - chunk_base[lo]) * cb;
+  r->c_end = r->c_begin + cb < r->t_end ? r->c_begin + cb : r->t_end;
   r->c_begin = uni64b(r->c_begin);
   r->c_end = uni64b(r->c_end);
   return true;
@@ -156,13 +179,14 @@ __device__ __forceinline__ bool find_chunk(int64_t c, int32_t T, const int64_t* 
 
 __global__ __launch_bounds__(256) void count_heads_kernel(int32_t T, const int64_t* chunk_base,
                                                           const int64_t* table_start, const int64_t* table_end,
+                                                          const int64_t* table_cb,
                                                           const uint32_t* __restrict__ keys, int64_t max_chunks,
                                                           int64_t* __restrict__ heads) {
   const int w = threadIdx.x / kWave, lane = lane_id();
   const int64_t c = uni64b((int64_t)blockIdx.x * 4 + w);
   if (c >= max_chunks) return;
   ChunkRange r;
-  if (!find_chunk(c, T, chunk_base, table_start, table_end, &r)) {
+  if (!find_chunk(c, T, chunk_base, table_start, table_end, table_cb, &r)) {
     if (lane == 0) heads[c] = 0;
     return;
   }
@@ -214,6 +238,7 @@ struct BwdArgs {
   const int64_t* table_start;
   const int64_t* table_end;
   const int64_t* chunk_base;
+  const int64_t* table_cb;
   int32_t* chunk_flags;
   const int64_t* head_base;
   float* part_first;
@@ -250,6 +275,10 @@ struct Reducer {
   TW* W;
   float* state;
   int64_t row_base;
+  // fields of the table's only feature (single >= 0)
+  const TG* g_base;
+  int64_t g_stride, pbase;
+  bool g_mean;
 
   __device__ Reducer(const BwdArgs& args, int32_t table) : a(args), t(table) {
     const mdl_table& tb = a.tables[t];
@@ -265,27 +294,27 @@ struct Reducer {
     sub = lane % L;
     col = sub * C;
     col_ok = col < dim;
+    g_base = nullptr;
+    g_stride = pbase = 0;
+    g_mean = false;
+    if (single >= 0) {
+      const mdl_feature& f = a.feats[single];
+      g_base = (const TG*)uni64b((int64_t)f.grad);
+      g_stride = uni64b(f.out_stride);
+      pbase = uni64b(f.payload_base);
+      g_mean = __builtin_amdgcn_readfirstlane(f.pooling) == MDL_POOL_MEAN;
+    }
   }
 
-  // Gradient contribution of sorted entry e (zero when !valid).
-  __device__ __forceinline__ void load(bool valid, int64_t e, float (&v)[C]) const {
-#pragma unroll
-    for (int k = 0; k < C; ++k) v[k] = 0.f;
-    if (!valid) return;
-    const uint32_t p = a.vals[e];
-    const int32_t fi = feature_of(a, single, p);
-    const mdl_feature& f = a.feats[fi];
-    const int64_t r = (int64_t)p - f.payload_base;
-    const TG* g = (const TG*)f.grad + r * f.out_stride;
-    if (col_ok) RowIO<TG, C>::load(g + col, v);
-    if (f.pooling == MDL_POOL_MEAN) {
-      const float cnt = a.bag_count[p];
-      if (cnt != 1.f) {
-        const float den = fmaxf(cnt, 1.f);
-#pragma unroll
-        for (int k = 0; k < C; ++k) v[k] = v[k] / den;
-      }
+  // Gradient row of payload p and whether it is divided by its bag count.
+  __device__ __forceinline__ const TG* grad_row(uint32_t p, bool& mean) const {
+    if (single >= 0) {
+      mean = g_mean;
+      return g_base + ((int64_t)p - pbase) * g_stride;
     }
+    const mdl_feature& f = a.feats[feature_of(a, single, p)];
+    mean = f.pooling == MDL_POOL_MEAN;
+    return (const TG*)f.grad + ((int64_t)p - f.payload_base) * f.out_stride;
   }
 
   // Sum of squares of the whole row held by this slot's L lanes.
@@ -298,20 +327,19 @@ struct Reducer {
     return ss;
   }
 
-  // Finish the run of `key` with summed gradient v (ss = its row sum of squares).
-  __device__ __forceinline__ void finish(uint32_t key, const float (&v)[C], float ss, int64_t uidx) const {
+  // Finish the run of `key` with summed gradient v: the Adagrad update from
+  // the preloaded weight row w and accumulator acc0, or the coalesced row.
+  __device__ __forceinline__ void finish(uint32_t key, const float (&v)[C], float ss, float acc0, float (&w)[C],
+                                         int64_t uidx) const {
     const int64_t row = (int64_t)key - row_base;
     if (a.mode == kModeAdagrad) {
-      const float acc = state[row] + ss / (float)dim;
+      const float acc = acc0 + ss / (float)dim;
       if (sub == 0) state[row] = acc;
       const float den = sqrtf(acc) + a.eps;
       if (col_ok) {
-        float w[C];
-        TW* wp = W + row * dim + col;
-        RowIO<TW, C>::load(wp, w);
 #pragma unroll
         for (int k = 0; k < C; ++k) w[k] = w[k] - a.lr * (v[k] / den);
-        RowIO<TW, C>::store(wp, w);
+        RowIO<TW, C>::store(W + row * dim + col, w);
       }
     } else {
       const int64_t local = uidx - a.unique_range[2 * t];
@@ -325,10 +353,14 @@ struct Reducer {
 
 template <typename TW, typename TG, int C>
 __device__ __forceinline__ void reduce_chunk(const BwdArgs& a, int64_t c, const ChunkRange& r) {
+  // Pass groups per iteration: 16 columns of loads in flight per lane.
+  constexpr int U = C >= 8 ? 2 : 4;
   Reducer<TW, TG, C> R(a, r.t);
   if (R.dim > kWave * C) return;  // rejected on the host; never reached
   const int lane = lane_id();
   const uint32_t* keys = a.keys;
+  const bool adagrad = a.mode == kModeAdagrad;
+  const bool coalesce = !adagrad;
   const bool head_open = r.c_begin > r.t_begin && keys[r.c_begin - 1] == keys[r.c_begin];
   const bool tail_open = r.c_end < r.t_end && keys[r.c_end] == keys[r.c_end - 1];
   const uint32_t first_key = keys[r.c_begin];
@@ -336,30 +368,76 @@ __device__ __forceinline__ void reduce_chunk(const BwdArgs& a, int64_t c, const 
   const bool single = head_open && tail_open && first_key == last_key;
   const uint32_t kNone = 0xffffffffu;
   const uint64_t lt_mask = (lane == 0) ? 0ull : (~0ull >> (64 - lane));
-  int64_t heads_before = a.mode == kModeCoalesce ? a.head_base[c] : 0;
+  int64_t heads_before = coalesce ? a.head_base[c] : 0;
 
   float carry[C];
 #pragma unroll
   for (int k = 0; k < C; ++k) carry[k] = 0.f;
   uint32_t carry_key = kNone;
   const int G = R.G, L = R.L, slot = R.slot, sub = R.sub;
+  const int64_t step = (int64_t)G * U;
 
-  for (int64_t base = r.c_begin; base < r.c_end; base += (int64_t)G * kBwdUnroll) {
-    float v[kBwdUnroll][C];
-    uint32_t key[kBwdUnroll];
-    bool fin[kBwdUnroll], head[kBwdUnroll];
+  // keys, next keys, previous keys (coalesced layout only) and payloads of
+  // the next pass group, fetched one group ahead
+  uint32_t nk[U], nn[U], npv[U], np[U];
+  auto fetch = [&](int64_t base) {
 #pragma unroll
-    for (int u = 0; u < kBwdUnroll; ++u) {
+    for (int u = 0; u < U; ++u) {
       const int64_t e = base + (int64_t)u * G + slot;
       const bool valid = e < r.c_end;
-      key[u] = valid ? keys[e] : kNone;
-      const uint32_t next = (valid && e + 1 < r.c_end) ? keys[e + 1] : kNone;
-      fin[u] = valid && ((e + 1 == r.c_end) ? !tail_open : next != key[u]);
-      head[u] = valid && (e == r.t_begin || (e > r.c_begin ? keys[e - 1] != key[u] : !head_open));
-      R.load(valid, e, v[u]);
+      nk[u] = valid ? keys[e] : kNone;
+      nn[u] = (valid && e + 1 < r.c_end) ? keys[e + 1] : kNone;
+      npv[u] = (coalesce && valid && e > r.c_begin) ? keys[e - 1] : kNone;
+      np[u] = valid ? a.vals[e] : 0u;
+    }
+  };
+  fetch(r.c_begin);
+
+  for (int64_t base = r.c_begin; base < r.c_end; base += step) {
+    float v[U][C], w[U][C], acc0[U], cnt[U];
+    uint32_t key[U], pay[U];
+    bool fin[U], head[U], own[U], mean[U];
+    const TG* gp[U];
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const int64_t e = base + (int64_t)u * G + slot;
+      const bool valid = e < r.c_end;
+      key[u] = nk[u];
+      pay[u] = np[u];
+      fin[u] = valid && ((e + 1 == r.c_end) ? !tail_open : nn[u] != key[u]);
+      head[u] = coalesce && valid && (e == r.t_begin || (e > r.c_begin ? npv[u] != key[u] : !head_open));
+      own[u] = fin[u] && !(head_open && key[u] == first_key);  // the run finishes in this chunk
+      mean[u] = false;
+      gp[u] = valid && R.col_ok ? R.grad_row(pay[u], mean[u]) + R.col : zero_row<TG>();
+    }
+    // Every load of the group, back to back: gradient rows, bag counts and,
+    // for runs that finish here, the weight row and its accumulator.
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      RowIO<TG, C>::load(gp[u], v[u]);
+      const float* cp = mean[u] ? a.bag_count + pay[u] : zero_row<float>();
+      cnt[u] = *cp;
+      if (adagrad) {
+        const int64_t row = (int64_t)key[u] - R.row_base;
+        RowIO<TW, C>::load(own[u] && R.col_ok ? R.W + row * R.dim + R.col : zero_row<TW>(), w[u]);
+        acc0[u] = *(own[u] ? R.state + row : zero_row<float>());
+      } else {
+#pragma unroll
+        for (int k = 0; k < C; ++k) w[u][k] = 0.f;
+        acc0[u] = 0.f;
+      }
+    }
+    fetch(base + step);
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      if (mean[u] && cnt[u] != 1.f) {
+        const float den = fmaxf(cnt[u], 1.f);
+#pragma unroll
+        for (int k = 0; k < C; ++k) v[u][k] = v[u][k] / den;
+      }
     }
 #pragma unroll
-    for (int u = 0; u < kBwdUnroll; ++u) {
+    for (int u = 0; u < U; ++u) {
       for (int d = 1; d < G; d <<= 1) {
         const int src = slot >= d ? lane - d * L : lane;
         const uint32_t okey = shfl_u(key[u], src);
@@ -377,21 +455,21 @@ __device__ __forceinline__ void reduce_chunk(const BwdArgs& a, int64_t c, const 
       }
       // Distinct-row index of this entry's run (coalesced layout only).
       int64_t uidx = 0;
-      if (a.mode == kModeCoalesce) {
+      if (coalesce) {
         const uint64_t hm = __ballot(head[u] && sub == 0);
         uidx = heads_before + (int64_t)__popcll(hm & (lt_mask | (1ull << lane))) - 1;
         heads_before += __popcll(hm);
       }
       const float ss = R.row_sumsq(v[u]);
       if (fin[u]) {
-        if (head_open && key[u] == first_key) {
+        if (!own[u]) {
           if (R.col_ok) {
             float* pf = a.part_first + c * a.max_dim + R.col;
 #pragma unroll
             for (int k = 0; k < C; ++k) pf[k] = v[u][k];
           }
         } else {
-          R.finish(key[u], v[u], ss, uidx);
+          R.finish(key[u], v[u], ss, acc0[u], w[u], uidx);
         }
       }
       const int src = (G - 1) * L + sub;
@@ -425,7 +503,23 @@ __device__ __forceinline__ void fixup_chunk(const BwdArgs& a, int64_t c, const C
 #pragma unroll
   for (int k = 0; k < C; ++k) v[k] = 0.f;
   if (R.col_ok) {
-    for (int64_t q = s; q < c; ++q) {
+    // Partials of the chunks the run covers, added in chunk order; loads
+    // are issued eight chunks at a time.
+    int64_t q = s;
+    for (; q + 8 <= c; q += 8) {
+      float t[8][C];
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        const float* pl = a.part_last + (q + j) * a.max_dim + R.col;
+#pragma unroll
+        for (int k = 0; k < C; ++k) t[j][k] = pl[k];
+      }
+#pragma unroll
+      for (int j = 0; j < 8; ++j)
+#pragma unroll
+        for (int k = 0; k < C; ++k) v[k] += t[j][k];
+    }
+    for (; q < c; ++q) {
       const float* pl = a.part_last + q * a.max_dim + R.col;
 #pragma unroll
       for (int k = 0; k < C; ++k) v[k] += pl[k];
@@ -437,17 +531,32 @@ __device__ __forceinline__ void fixup_chunk(const BwdArgs& a, int64_t c, const C
   const float ss = R.row_sumsq(v);
   const uint32_t key = a.keys[r.c_begin];
   const int64_t uidx = a.mode == kModeCoalesce ? a.head_base[c] - 1 : 0;
-  if (R.slot == 0) R.finish(key, v, ss, uidx);
+  float w[C];
+  float acc0 = 0.f;
+#pragma unroll
+  for (int k = 0; k < C; ++k) w[k] = 0.f;
+  if (a.mode == kModeAdagrad && R.slot == 0) {
+    const int64_t row = (int64_t)key - R.row_base;
+    if (R.col_ok) RowIO<TW, C>::load(R.W + row * R.dim + R.col, w);
+    acc0 = R.state[row];
+  }
+  if (R.slot == 0) R.finish(key, v, ss, acc0, w, uidx);
 }
 
 template <bool kFixup>
 __global__ __launch_bounds__(kBwdWaves * kWave) void bwd_reduce_kernel(BwdArgs a) {
   const int w = threadIdx.x / kWave;
-  const int64_t blk = xcd_block(blockIdx.x, gridDim.x);
+  // The grid covers the worst-case chunk count; only the first `real` blocks
+  // have work.  They are spread round-robin over the XCDs by the hardware, and
+  // remapped so that each XCD takes one contiguous range of chunks.
+  const int64_t total = uni64b(a.chunk_base[a.T]);
+  const int64_t real = (total + kBwdWaves - 1) / kBwdWaves;
+  if ((int64_t)blockIdx.x >= real) return;
+  const int64_t blk = xcd_block(blockIdx.x, real);
   const int64_t c = uni64b(blk * kBwdWaves + w);
-  if (c >= a.max_chunks) return;
+  if (c >= total) return;
   ChunkRange r;
-  if (!find_chunk(c, a.T, a.chunk_base, a.table_start, a.table_end, &r)) return;
+  if (!find_chunk(c, a.T, a.chunk_base, a.table_start, a.table_end, a.table_cb, &r)) return;
   const mdl_table& tb = a.tables[r.t];
   const int wdtype = __builtin_amdgcn_readfirstlane(tb.wdtype);
   const int dim = __builtin_amdgcn_readfirstlane(tb.dim);
@@ -488,7 +597,7 @@ static int prepare(const mdl_table* tables, int32_t T, int32_t max_dim, uint32_t
   *sk = in_alt ? w->keys_alt : keys;
   *sv = in_alt ? w->vals_alt : payload;
   hipLaunchKernelGGL(bwd_plan_kernel, dim3(1), dim3(kPlanThreads), 0, s, tables, T, *sk, n, w->table_start,
-                     w->table_end, w->chunk_base);
+                     w->table_end, w->chunk_base, w->table_cb);
   MDL_CHECK_LAUNCH("bwd_plan_kernel");
   return MDL_OK;
 }
@@ -506,6 +615,7 @@ static void fill_args(BwdArgs* a, const mdl_feature* feats, int32_t F, const mdl
   a->table_start = w.table_start;
   a->table_end = w.table_end;
   a->chunk_base = w.chunk_base;
+  a->table_cb = w.table_cb;
   a->chunk_flags = w.chunk_flags;
   a->head_base = w.head_base;
   a->part_first = w.part_first;
@@ -597,7 +707,7 @@ int mdl_backward_count(const mdl_table* tables, int32_t num_tables, int32_t max_
   const int64_t mc = max_chunks_for(n, num_tables);
   int64_t* heads = (int64_t*)((char*)workspace + carve(&w, workspace, n, num_tables, max_dim));
   hipLaunchKernelGGL(count_heads_kernel, dim3((unsigned)((mc + 3) / 4)), dim3(256), 0, s, num_tables,
-                     w.chunk_base, w.table_start, w.table_end, sk, mc, heads);
+                     w.chunk_base, w.table_start, w.table_end, w.table_cb, sk, mc, heads);
   MDL_CHECK_LAUNCH("count_heads_kernel");
   rc = mdl_lengths_to_offsets(heads, mc, w.head_base, w.scan_ws, w.scan_bytes, stream);
   if (rc) return rc;

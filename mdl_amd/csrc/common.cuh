@@ -112,6 +112,21 @@ struct RowIO<bf16_t, 1> {
   }
 };
 
+// A row of zeros in device memory.  Lanes whose row is absent (past the end
+// of a chunk, an invalid id, a column past dim) load from here instead of
+// branching around the load, so every load of a pass issues back to back.
+// (One copy per translation unit; only device code reads it.)
+static __device__ __align__(256) float g_zero_row[512];
+
+template <typename T>
+__device__ __forceinline__ const T* zero_row() {
+  return reinterpret_cast<const T*>(g_zero_row);
+}
+
+// Rows one pass covers and the chunk length that gives a wave about
+// kPassesPerChunk passes.
+constexpr int kPassesPerChunk = 32;
+
 // ------------------------------------------------------------ wave helpers --
 
 __device__ __forceinline__ int lane_id() { return (int)(threadIdx.x & (kWave - 1)); }

@@ -21,7 +21,6 @@ namespace mdl {
 
 constexpr int kFwdWaves = 4;
 constexpr int kMaxBagsPerChunk = 256;
-constexpr int kUnroll = 4;
 
 struct FwdArgs {
   const mdl_feature* feats;
@@ -87,6 +86,7 @@ __device__ __forceinline__ void wave_sync() { __builtin_amdgcn_wave_barrier(); _
 
 template <typename TW, typename TO, int C>
 __device__ __forceinline__ void gather_chunk(const Feat& f, int64_t first, int count, const FwdArgs& a) {
+  constexpr int kUnroll = C >= 8 ? 2 : 4;  // 16 columns of loads in flight per lane
   const int lane = lane_id();
   const int L = lanes_for(f.dim, C);
   const int G = kWave / L;
@@ -94,23 +94,39 @@ __device__ __forceinline__ void gather_chunk(const Feat& f, int64_t first, int c
   const int ncb = (f.dim + L * C - 1) / (L * C);
   const TW* W = static_cast<const TW*>(f.weight);
   TO* out = static_cast<TO*>(f.out);
+  const int64_t* ids = a.ids + f.ids_begin + first;
+  const int step = G * kUnroll;
   int bad = 0;
   for (int cb = 0; cb < ncb; ++cb) {
     const int col = (cb * L + sub) * C;
     const bool col_ok = col < f.dim;
-    for (int base = 0; base < count; base += G * kUnroll) {
-      float v[kUnroll][C];
+    int64_t nid[kUnroll];  // ids of the next pass group, fetched one group ahead
+#pragma unroll
+    for (int u = 0; u < kUnroll; ++u) {
+      const int i = u * G + slot;
+      nid[u] = i < count ? ids[i] : 0;
+    }
+    for (int base = 0; base < count; base += step) {
       int64_t id[kUnroll];
+      float v[kUnroll][C];
+#pragma unroll
+      for (int u = 0; u < kUnroll; ++u) {
+        id[u] = nid[u];
+        const int i = base + u * G + slot;
+        const bool ok = i < count && (uint64_t)id[u] < (uint64_t)f.num_rows && col_ok;
+        RowIO<TW, C>::load(ok ? W + id[u] * f.dim + col : zero_row<TW>(), v[u]);
+      }
+#pragma unroll
+      for (int u = 0; u < kUnroll; ++u) {
+        const int i = base + step + u * G + slot;
+        nid[u] = i < count ? ids[i] : 0;
+      }
 #pragma unroll
       for (int u = 0; u < kUnroll; ++u) {
         const int i = base + u * G + slot;
-        const bool valid = i < count;
-        id[u] = valid ? a.ids[f.ids_begin + first + i] : 0;
+        if (i >= count) continue;
         const bool in_range = (uint64_t)id[u] < (uint64_t)f.num_rows;
-#pragma unroll
-        for (int k = 0; k < C; ++k) v[u][k] = 0.f;
-        if (valid && in_range && col_ok) RowIO<TW, C>::load(W + id[u] * f.dim + col, v[u]);
-        if (cb == 0 && sub == 0 && valid) {
+        if (cb == 0 && sub == 0) {
           bad += !in_range;
           if (a.keys != nullptr) {
             const int64_t e = f.ids_begin + first + i;
@@ -118,11 +134,7 @@ __device__ __forceinline__ void gather_chunk(const Feat& f, int64_t first, int c
             a.payload[e] = (uint32_t)(f.payload_base + first + i);
           }
         }
-      }
-#pragma unroll
-      for (int u = 0; u < kUnroll; ++u) {
-        const int i = base + u * G + slot;
-        if (i < count && col_ok) RowIO<TO, C>::store(out + (first + i) * f.out_stride + col, v[u]);
+        if (col_ok) RowIO<TO, C>::store(out + (first + i) * f.out_stride + col, v[u]);
       }
     }
   }
@@ -133,6 +145,7 @@ __device__ __forceinline__ void gather_chunk(const Feat& f, int64_t first, int c
 
 template <typename TW, typename TO, int C>
 __device__ __forceinline__ void pooled_chunk(const Feat& f, int64_t first_bag, int nb, int64_t* s_off, const FwdArgs& a) {
+  constexpr int kUnroll = C >= 8 ? 2 : 4;  // 16 columns of loads in flight per lane
   const int lane = lane_id();
   // Offsets are clamped into the feature's own id range, so lengths that do
   // not add up to the ids passed can only give wrong sums (and an error
@@ -157,6 +170,7 @@ __device__ __forceinline__ void pooled_chunk(const Feat& f, int64_t first_bag, i
   const TW* W = static_cast<const TW*>(f.weight);
   TO* out = static_cast<TO*>(f.out);
   const int last_lane_base = (G - 1) * L;
+  const int64_t step = (int64_t)G * kUnroll;
   int bad = 0;
 
   for (int cb = 0; cb < ncb; ++cb) {
@@ -168,37 +182,56 @@ __device__ __forceinline__ void pooled_chunk(const Feat& f, int64_t first_bag, i
     float carry_w = 0.f;
     int carry_seg = -2;
     int bag = 0;  // cursor: bag (relative to the chunk) of this slot's current id
-    for (int64_t base = e_begin; base < e_end; base += (int64_t)G * kUnroll) {
+    int64_t nid[kUnroll];
+#pragma unroll
+    for (int u = 0; u < kUnroll; ++u) {
+      const int64_t e = e_begin + (int64_t)u * G + slot;
+      nid[u] = e < e_end ? a.ids[e] : 0;
+    }
+    for (int64_t base = e_begin; base < e_end; base += step) {
       float v[kUnroll][C];
       float wt[kUnroll];
       int seg[kUnroll];
       bool tail[kUnroll];
+      int64_t id[kUnroll];
+      // Bag of every slot (LDS cursor walk), then all row loads of the group
+      // in one branch-free block, then the backward's sort keys.
 #pragma unroll
       for (int u = 0; u < kUnroll; ++u) {
+        id[u] = nid[u];
         const int64_t e = base + (int64_t)u * G + slot;
         const bool valid = e < e_end;
-        const int64_t id = valid ? a.ids[e] : 0;
         if (valid) {
           while (s_off[bag + 1] <= e) ++bag;
         }
-        const bool in_range = (uint64_t)id < (uint64_t)f.num_rows;
-        float w = (exclude && id == 0) ? 0.f : 1.f;
-        if (!in_range) w = 0.f;
+        const bool in_range = (uint64_t)id[u] < (uint64_t)f.num_rows;
+        float w = (exclude && id[u] == 0) ? 0.f : 1.f;
+        if (!in_range || !valid) w = 0.f;
         seg[u] = valid ? bag : -1;
-        wt[u] = valid ? w : 0.f;
+        wt[u] = w;
         tail[u] = valid && (e + 1 == s_off[bag + 1]);
+      }
 #pragma unroll
-        for (int k = 0; k < C; ++k) v[u][k] = 0.f;
-        if (valid && w != 0.f && col_ok) RowIO<TW, C>::load(W + id * f.dim + col, v[u]);
-        if (cb == 0 && sub == 0 && valid) {
-          bad += !in_range;
+      for (int u = 0; u < kUnroll; ++u)
+        RowIO<TW, C>::load(wt[u] != 0.f && col_ok ? W + id[u] * f.dim + col : zero_row<TW>(), v[u]);
+      if (cb == 0 && sub == 0) {
+#pragma unroll
+        for (int u = 0; u < kUnroll; ++u) {
+          const int64_t e = base + (int64_t)u * G + slot;
+          if (e >= e_end) continue;
+          bad += (uint64_t)id[u] >= (uint64_t)f.num_rows;
           if (a.keys != nullptr) {
             // w == 0 covers invalid ids and nulls under "exclude": their
             // gradient is exactly zero, so they take no part in the backward.
-            a.keys[e] = (w != 0.f && id != f.padding_idx) ? (uint32_t)(f.row_base + id) : a.sentinel;
-            a.payload[e] = (uint32_t)(f.payload_base + first_bag + bag);
+            a.keys[e] = (wt[u] != 0.f && id[u] != f.padding_idx) ? (uint32_t)(f.row_base + id[u]) : a.sentinel;
+            a.payload[e] = (uint32_t)(f.payload_base + first_bag + seg[u]);
           }
         }
+      }
+#pragma unroll
+      for (int u = 0; u < kUnroll; ++u) {
+        const int64_t e = base + step + (int64_t)u * G + slot;
+        nid[u] = e < e_end ? a.ids[e] : 0;
       }
 #pragma unroll
       for (int u = 0; u < kUnroll; ++u) {
@@ -321,6 +354,7 @@ __device__ __forceinline__ int64_t seq_len(const SeqArgs& a, int64_t b) {
 template <typename TW, typename TO, int C>
 __device__ __forceinline__ void seq_rows(const SeqArgs& a, int64_t row0, int64_t nrows) {
   const Feat& f = a.f;
+  constexpr int kUnroll = C >= 8 ? 2 : 4;  // 16 columns of loads in flight per lane
   const int lane = lane_id();
   const int L = lanes_for(f.dim, C);
   const int G = kWave / L;
@@ -418,20 +452,31 @@ int64_t mdl_plan_chunks(const mdl_feature* feats, int32_t num_features, int32_t 
   int64_t n = 0;
   for (int32_t fi = 0; fi < num_features; ++fi) {
     const mdl_feature& f = feats[fi];
+    // Rows a wave gathers per pass (same lane layout as the kernel): chunks
+    // hold about kPassesPerChunk passes, so no wave walks a long serial chain
+    // of dependent loads, whatever the row width.
+    const int wsz = f.wdtype == MDL_BF16 ? 2 : 4;
+    const int osz = f.odtype == MDL_BF16 ? 2 : 4;
+    const int c = 16 / wsz;
+    const bool vec = f.weight % 16 == 0 && f.out % 16 == 0 && ((int64_t)f.dim * wsz) % 16 == 0 &&
+                     (f.out_stride * osz) % 16 == 0 && ((int64_t)c * osz) % 16 == 0;
+    const int lanes = lanes_for(f.dim > 0 ? f.dim : 1, vec ? c : 1);
+    const int64_t per_pass = kWave / lanes;
+    int64_t target = (int64_t)kPassesPerChunk * per_pass;
+    if (target > target_ids) target = target_ids;
     if (f.pooling == MDL_POOL_NONE) {
-      const int64_t step = target_ids;
-      for (int64_t s = 0; s < f.num_ids; s += step) {
+      for (int64_t s = 0; s < f.num_ids; s += target) {
         if (chunks && n < capacity) {
           chunks[n].feature = fi;
           chunks[n].first = s;
-          chunks[n].count = (int32_t)(f.num_ids - s < step ? f.num_ids - s : step);
+          chunks[n].count = (int32_t)(f.num_ids - s < target ? f.num_ids - s : target);
         }
         ++n;
       }
     } else {
       const double avg = f.num_bags > 0 ? (double)f.num_ids / (double)f.num_bags : 1.0;
       int64_t nb = 1;
-      while (nb * 2 <= kMaxBagsPerChunk && (double)(nb * 2) * (avg > 1.0 ? avg : 1.0) <= (double)target_ids) nb *= 2;
+      while (nb * 2 <= kMaxBagsPerChunk && (double)(nb * 2) * (avg > 1.0 ? avg : 1.0) <= (double)target) nb *= 2;
       for (int64_t s = 0; s < f.num_bags; s += nb) {
         if (chunks && n < capacity) {
           chunks[n].feature = fi;

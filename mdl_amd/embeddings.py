@@ -18,6 +18,7 @@ from dataclasses import asdict, dataclass
 from hashlib import sha256
 import json
 import threading
+import weakref
 from typing import Any, Iterable, Iterator, Literal
 
 import torch
@@ -327,6 +328,41 @@ def _raise_for_errors(modules: list["ShardedEmbedding"], ids: list[Tensor], err:
     raise IndexError("embedding lookup received out-of-range IDs")
 
 
+# Sparse gradients this module produced already coalesced, by parameter.
+# Autograd's AccumulateGrad re-wraps a sparse gradient around the same index
+# and value storage but drops its coalesced flag; the optimizer compares the
+# storage with this record to restore the flag instead of sorting again.  A
+# gradient accumulated over several backward passes has new storage and is
+# coalesced normally.
+_COALESCED: dict[int, tuple] = {}
+
+
+def _remember_coalesced(parameter: Tensor, rows: Tensor, vals: Tensor) -> None:
+    for key in [k for k, (ref, _, _) in _COALESCED.items() if ref() is None]:
+        del _COALESCED[key]
+    _COALESCED[id(parameter)] = (weakref.ref(parameter), rows, vals)
+
+
+def known_coalesced(parameter: Tensor, grad: Tensor) -> bool:
+    """Whether ``grad`` is the coalesced gradient last emitted for ``parameter``."""
+
+    entry = _COALESCED.get(id(parameter))
+    if entry is None or entry[0]() is not parameter:
+        return False
+    _, rows, vals = entry
+    idx, val = grad._indices(), grad._values()
+    return (
+        idx.data_ptr() == rows.data_ptr()
+        and val.data_ptr() == vals.data_ptr()
+        and idx.size(-1) == rows.numel()
+        and tuple(val.shape) == tuple(vals.shape)
+    )
+
+
+def forget_coalesced(parameter: Tensor) -> None:
+    _COALESCED.pop(id(parameter), None)
+
+
 class _GroupedLookupFn(torch.autograd.Function):
     """Grouped lookup whose weight gradients are coalesced sparse COO tensors."""
 
@@ -344,7 +380,7 @@ class _GroupedLookupFn(torch.autograd.Function):
             _raise_for_errors(ctl["modules"], ids, res.error_count)
         ctx.res = res
         ctx.nf = nf
-        ctx.weight_shapes = [tuple(w.shape) for w in weights]
+        ctx.weights = list(weights)
         return tuple(res.outputs)
 
     @staticmethod
@@ -353,10 +389,12 @@ class _GroupedLookupFn(torch.autograd.Function):
         coalesced = ops.backward_coalesce(res, list(grads))
         ctx.res = None
         out: list[Tensor | None] = [None] * ctx.nf
-        for (rows, vals), shape in zip(coalesced, ctx.weight_shapes):
+        for (rows, vals), weight in zip(coalesced, ctx.weights):
             out.append(
-                torch.sparse_coo_tensor(rows.unsqueeze(0), vals, shape, is_coalesced=True)
+                torch.sparse_coo_tensor(rows.unsqueeze(0), vals, tuple(weight.shape), is_coalesced=True)
             )
+            _remember_coalesced(weight, rows, vals)
+        ctx.weights = None
         return (None, *out)
 
 

@@ -144,6 +144,9 @@ class ShardedRowWiseAdagrad(torch.optim.Optimizer):
                     raise RuntimeError(
                         "ShardedRowWiseAdagrad expects one sparse row dimension and one dense dimension"
                     )
+                if not grad.is_coalesced() and embeddings.known_coalesced(parameter, grad):
+                    grad._coalesced_(True)
+                embeddings.forget_coalesced(parameter)
                 if grad.is_coalesced():
                     rows = grad.indices()[0]
                     values = grad.values()

