@@ -206,15 +206,15 @@ def algorithmic_bytes(wl: Workload, ids, lengths) -> dict:
 
 
 class DeviceStep:
-    """Buffers and launches of one fused sparse step on the GPU."""
+    """Tables, persistent buffers and one SparseStep per synthetic batch."""
 
     def __init__(self, wl: Workload, batches, device):
         import torch
 
         from mdl_amd import ops
+        from mdl_amd.sparse_step import SparseStep
 
         self.torch = torch
-        self.ops = ops
         self.wl = wl
         self.device = device
         wdtype = torch.float32 if wl.dtype == "fp32" else torch.bfloat16
@@ -234,61 +234,60 @@ class DeviceStep:
                 self.tables[f.table], pooling=f.pooling, null_policy="exclude", state=self.states[f.table]
             )
         sum_d = sum(wl.dims[f.table] for f in wl.features)
+        # pooled outputs go straight into the token-slot buffer [B, sum(dim)]
         self.out = torch.empty((wl.batch, sum_d), dtype=wdtype, device=device)
         self.grad = torch.empty((wl.batch, sum_d), dtype=wdtype, device=device)
         self.grad.normal_(0.0, 1.0, generator=gen)
         col = 0
-        self.out_views = []
-        self.grad_views = []
+        out_views, grad_views = [], []
         for f in wl.features:
             d = wl.dims[f.table]
-            self.out_views.append(self.out[:, col: col + d])
-            self.grad_views.append(self.grad[:, col: col + d])
+            out_views.append(self.out[:, col: col + d])
+            grad_views.append(self.grad[:, col: col + d])
             col += d
+        self.err = torch.zeros(1, dtype=torch.int32, device=device)
         # device-resident batches: packed ids + concatenated lengths (an unpooled
         # feature contributes one pseudo-bag holding all its ids)
-        self.batches = []
+        self.steps = []
         for ids, lengths in batches:
             id_counts = [int(x.size) for x in ids]
             bag_counts = [0 if ln is None else int(ln.size) for ln in lengths]
             parts = [ln if ln is not None else np.array([x.size]) for x, ln in zip(ids, lengths)]
             packed = torch.from_numpy(np.concatenate(ids).astype(np.int64)).to(device)
             lens = torch.from_numpy(np.concatenate(parts).astype(np.int64)).to(device)
-            self.batches.append((packed, lens, id_counts, bag_counts))
-        self.err = torch.zeros(1, dtype=torch.int32, device=device)
-        self.t_fwd = []
+            self.steps.append(SparseStep(self.plan, packed, lens, id_counts, bag_counts, out_views, grad_views,
+                                         error_count=self.err))
 
-    def step(self, i: int, timer=None):
-        ops = self.ops
-        packed, lens, id_counts, bag_counts = self.batches[i % len(self.batches)]
-        offsets = ops.lengths_to_offsets(lens)
-        if timer is not None:
-            timer.mark("fwd_start")
-        res = ops.forward_packed(
-            self.plan, packed, offsets, id_counts, bag_counts, self.out_views, with_backward=True,
-            error_count=self.err,
-        )
-        if timer is not None:
-            timer.mark("fwd_end")
-        ops.backward_adagrad(res, self.grad_views, lr=self.wl.lr, eps=self.wl.eps)
-        return res
+    def step(self, i: int, timers=None):
+        st = self.steps[i % len(self.steps)]
+        if timers is None:
+            st.step(self.wl.lr, self.wl.eps)
+            return
+        timers["forward"].start()
+        st.forward()
+        timers["forward"].stop()
+        st.sort()
+        timers["apply"].start()
+        st.apply(self.wl.lr, self.wl.eps)
+        timers["apply"].stop()
 
 
 class EventTimer:
-    """HIP events recorded on the launch stream around one kernel."""
+    """HIP events recorded on the launch stream around one call's kernels."""
 
     def __init__(self, torch):
         self.torch = torch
         self.pairs = []
         self._open = None
 
-    def mark(self, name):
+    def start(self):
+        self._open = self.torch.cuda.Event(enable_timing=True)
+        self._open.record(self.torch.cuda.current_stream())
+
+    def stop(self):
         ev = self.torch.cuda.Event(enable_timing=True)
         ev.record(self.torch.cuda.current_stream())
-        if name.endswith("_start"):
-            self._open = ev
-        else:
-            self.pairs.append((self._open, ev))
+        self.pairs.append((self._open, ev))
 
     def mean_ms(self):
         self.torch.cuda.synchronize()
@@ -393,11 +392,10 @@ def main() -> int:
     torch.cuda.synchronize()
     if int(dev.err.item()):
         raise RuntimeError("synthetic ids out of range")
-    timer = EventTimer(torch)
     torch.cuda.synchronize()
     t0 = time.perf_counter()
     for i in range(args.steps):
-        dev.step(args.warmup + i, timer)
+        dev.step(args.warmup + i)
     torch.cuda.synchronize()
     elapsed = time.perf_counter() - t0
     ms = elapsed * 1e3 / args.steps
@@ -406,14 +404,27 @@ def main() -> int:
     b_alg = float(np.mean([a["B_alg"] for a in used]))
     rows_per_s = n_ids / (ms * 1e-3)
     gbps = b_alg / (ms * 1e-3) / 1e9
-    # dominant kernel: the grouped forward (one launch), bracketed by events
-    fwd_ms = timer.mean_ms()
-    nb = sum(len(ln) for ln in batches[0][1] if ln is not None)
-    fwd_bytes = float(np.mean([
-        16 * a["n_ids"] + 8 * (nb + 1) + a["fwd_unique_row_bytes"] + wl.batch * a["sum_dim"] * (4 if wl.dtype == "fp32" else 2)
-        + 4 * nb for a in used
-    ]))
-    fwd_gbps = fwd_bytes / (fwd_ms * 1e-3) / 1e9
+    # Per-kernel durations: HIP events around each call on the launch stream,
+    # in separate (untimed) steps so the event records do not touch the step time.
+    timers = {"forward": EventTimer(torch), "apply": EventTimer(torch)}
+    for i in range(args.steps):
+        dev.step(args.warmup + args.steps + i, timers)
+    torch.cuda.synchronize()
+    esz = 4 if wl.dtype == "fp32" else 2
+    nb = float(np.mean([sum(len(ln) for ln in b[1] if ln is not None) for b in batches]))
+    kernels = {}
+    fwd_bytes = float(np.mean([16 * a["n_ids"] + 8 * (nb + 1) + a["fwd_unique_row_bytes"]
+                               + wl.batch * a["sum_dim"] * esz + 4 * nb for a in used]))
+    apply_bytes = float(np.mean([8 * a["n_ids"] + wl.batch * a["sum_dim"] * esz + 2 * a["fwd_unique_row_bytes"]
+                                 + 8 * a["unique_rows"] + 4 * nb for a in used]))
+    for name, nbytes, label in (
+        ("forward", fwd_bytes, "forward_kernel (grouped lookup + pooling + sort-key emission)"),
+        ("apply", apply_bytes, "bwd_reduce_kernel + fix-up (segment reduction + row-wise Adagrad)"),
+    ):
+        kms = timers[name].mean_ms()
+        kernels[name] = {"kernel": label, "ms": kms, "alg_bytes_per_launch": nbytes,
+                         "achieved_gbps": nbytes / (kms * 1e-3) / 1e9}
+    dom = max(kernels.values(), key=lambda k: k["ms"])
     result = {
         "metric": METRIC,
         "value": rows_per_s,
@@ -439,16 +450,17 @@ def main() -> int:
         "roofline_fraction_step": gbps / PEAK_HBM_GBPS,
         "B_alg_bytes_per_step": b_alg,
         "roofline": {
-            "kernel": "forward_kernel (grouped lookup + pooling + sort-key emission)",
+            "kernel": dom["kernel"],
             "bound": "hbm",
-            "achieved": fwd_gbps,
+            "achieved": dom["achieved_gbps"],
             "peak": PEAK_HBM_GBPS,
             "unit": "GB/s",
-            "frac": fwd_gbps / PEAK_HBM_GBPS,
+            "frac": dom["achieved_gbps"] / PEAK_HBM_GBPS,
             "traffic": None,
-            "kernel_ms": fwd_ms,
-            "alg_bytes_per_launch": fwd_bytes,
+            "kernel_ms": dom["ms"],
+            "alg_bytes_per_launch": dom["alg_bytes_per_launch"],
         },
+        "kernels": kernels,
         "cpu_baseline": None,
     }
     if not args.no_cpu_baseline:

@@ -271,6 +271,19 @@ int mdl_backward_adagrad(const mdl_feature* feats, int32_t num_features,
                          int32_t key_bits, const float* bag_count, float lr, float eps,
                          void* workspace, size_t workspace_bytes, void* stream);
 
+/* mdl_backward_adagrad in two calls with the same arguments and workspace:
+ * mdl_backward_sort (radix sort + chunk plan), then mdl_backward_apply
+ * (segment reduction + update). */
+int mdl_backward_sort(const mdl_table* tables, int32_t num_tables, int32_t max_dim,
+                      uint32_t* sort_keys, uint32_t* sort_payload, int64_t n,
+                      int32_t key_bits, void* workspace, size_t workspace_bytes,
+                      void* stream);
+int mdl_backward_apply(const mdl_feature* feats, int32_t num_features,
+                       const mdl_table* tables, int32_t num_tables, int32_t max_dim,
+                       uint32_t* sort_keys, uint32_t* sort_payload, int64_t n,
+                       int32_t key_bits, const float* bag_count, float lr, float eps,
+                       void* workspace, size_t workspace_bytes, void* stream);
+
 /*
  * Coalesced sparse gradients, the autograd contract of src/optim.py:317-329 and
  * src/train.py:5730-5742 (rows ascending and unique), in two calls:

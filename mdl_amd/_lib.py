@@ -100,6 +100,11 @@ SIGNATURES: dict[str, tuple] = {
         _I32,
         [_P, _I32, _P, _I32, _I32, _P, _P, _I64, _I32, _P, _F, _F, _P, _SZ, _P],
     ),
+    "mdl_backward_sort": (_I32, [_P, _I32, _I32, _P, _P, _I64, _I32, _P, _SZ, _P]),
+    "mdl_backward_apply": (
+        _I32,
+        [_P, _I32, _P, _I32, _I32, _P, _P, _I64, _I32, _P, _F, _F, _P, _SZ, _P],
+    ),
     "mdl_backward_count": (_I32, [_P, _I32, _I32, _P, _P, _I64, _I32, _P, _P, _SZ, _P]),
     "mdl_backward_coalesce": (
         _I32,

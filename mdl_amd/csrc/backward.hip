@@ -667,25 +667,48 @@ size_t mdl_backward_workspace_bytes(int64_t n, int32_t num_tables, int32_t max_d
   return bytes + 256;
 }
 
-int mdl_backward_adagrad(const mdl_feature* feats, int32_t num_features, const mdl_table* tables,
-                         int32_t num_tables, int32_t max_dim, uint32_t* sort_keys, uint32_t* sort_payload,
-                         int64_t n, int32_t key_bits, const float* bag_count, float lr, float eps,
-                         void* workspace, size_t workspace_bytes, void* stream) {
-  int rc = validate_tables("mdl_backward_adagrad", num_tables, max_dim, n);
+int mdl_backward_sort(const mdl_table* tables, int32_t num_tables, int32_t max_dim, uint32_t* sort_keys,
+                      uint32_t* sort_payload, int64_t n, int32_t key_bits, void* workspace, size_t workspace_bytes,
+                      void* stream) {
+  int rc = validate_tables("mdl_backward_sort", num_tables, max_dim, n);
   if (rc) return rc;
   if (n == 0) return MDL_OK;
-  hipStream_t s = as_stream(stream);
   BwdWs w;
   const uint32_t *sk, *sv;
-  rc = prepare(tables, num_tables, max_dim, sort_keys, sort_payload, n, key_bits, workspace, workspace_bytes, s,
-               &w, &sk, &sv);
+  return prepare(tables, num_tables, max_dim, sort_keys, sort_payload, n, key_bits, workspace, workspace_bytes,
+                 as_stream(stream), &w, &sk, &sv);
+}
+
+int mdl_backward_apply(const mdl_feature* feats, int32_t num_features, const mdl_table* tables,
+                       int32_t num_tables, int32_t max_dim, uint32_t* sort_keys, uint32_t* sort_payload,
+                       int64_t n, int32_t key_bits, const float* bag_count, float lr, float eps,
+                       void* workspace, size_t workspace_bytes, void* stream) {
+  int rc = validate_tables("mdl_backward_apply", num_tables, max_dim, n);
   if (rc) return rc;
+  if (n == 0) return MDL_OK;
+  BwdWs w;
+  const size_t need = carve(&w, workspace, n, num_tables, max_dim);
+  if (workspace_bytes < need) return fail(MDL_ERR_WORKSPACE, "mdl_backward_apply: workspace too small");
+  const int passes = (key_bits + 7) / 8;
+  const uint32_t* sk = (passes & 1) ? w.keys_alt : sort_keys;
+  const uint32_t* sv = (passes & 1) ? w.vals_alt : sort_payload;
   BwdArgs a;
   fill_args(&a, feats, num_features, tables, num_tables, max_dim, sk, sv, bag_count, w, n);
   a.lr = lr;
   a.eps = eps;
   a.mode = kModeAdagrad;
-  return run_reduce(a, s);
+  return run_reduce(a, as_stream(stream));
+}
+
+int mdl_backward_adagrad(const mdl_feature* feats, int32_t num_features, const mdl_table* tables,
+                         int32_t num_tables, int32_t max_dim, uint32_t* sort_keys, uint32_t* sort_payload,
+                         int64_t n, int32_t key_bits, const float* bag_count, float lr, float eps,
+                         void* workspace, size_t workspace_bytes, void* stream) {
+  int rc = mdl_backward_sort(tables, num_tables, max_dim, sort_keys, sort_payload, n, key_bits, workspace,
+                             workspace_bytes, stream);
+  if (rc) return rc;
+  return mdl_backward_apply(feats, num_features, tables, num_tables, max_dim, sort_keys, sort_payload, n,
+                            key_bits, bag_count, lr, eps, workspace, workspace_bytes, stream);
 }
 
 int mdl_backward_count(const mdl_table* tables, int32_t num_tables, int32_t max_dim, uint32_t* sort_keys,

@@ -1,0 +1,147 @@
+"""One fused sparse step over fixed device buffers.
+
+``SparseStep`` binds a feature layout (:class:`mdl_amd.ops.GroupPlan`) to
+persistent buffers -- packed ids, concatenated bag lengths, pooled outputs,
+upstream gradients -- and builds every descriptor, chunk table and workspace
+once.  A step is then launches only, with no host work, allocation or sync:
+
+    lengths -> offsets scan, grouped lookup + pooling (+ sort keys),
+    radix sort, segment reduction + row-wise Adagrad.
+
+This is the path of a training loop whose batch layout is fixed (same
+features, batch size and bag-count per feature), e.g. with the pooled outputs
+written straight into the RankMixer token-slot buffer ``[B, sum(dim)]``.
+"""
+
+from __future__ import annotations
+
+from typing import Sequence
+
+import numpy as np
+import torch
+from torch import Tensor
+
+from . import ops
+from ._lib import CHUNK_DTYPE, MDL_POOL_NONE, check, lib
+
+
+class SparseStep:
+    def __init__(
+        self,
+        plan: ops.GroupPlan,
+        packed_ids: Tensor,
+        lengths: Tensor | None,
+        id_counts: Sequence[int],
+        bag_counts: Sequence[int],
+        outputs: Sequence[Tensor],
+        grads: Sequence[Tensor],
+        *,
+        error_count: Tensor | None = None,
+    ) -> None:
+        for t in plan.tables:
+            if t.state is None:
+                raise RuntimeError("every table needs a row-wise Adagrad accumulator")
+        self.plan = plan
+        self.device = packed_ids.device
+        self.ids = packed_ids.contiguous()
+        self.n = int(self.ids.numel())
+        pooled_any = any(s.pooling != MDL_POOL_NONE for s in plan.features)
+        self.lengths = None
+        self.offsets = None
+        if pooled_any:
+            if lengths is None:
+                raise ValueError("pooled features need bag lengths")
+            self.lengths = lengths.to(torch.int64).contiguous()
+            nl = int(self.lengths.numel())
+            self.offsets = torch.empty(nl + 1, dtype=torch.int64, device=self.device)
+            self.scan_ws = ops._workspace(lib().mdl_offsets_workspace_bytes(nl), self.device)
+        self.error_count = (
+            error_count if error_count is not None else torch.zeros(1, dtype=torch.int32, device=self.device)
+        )
+        out_ptrs = [o.data_ptr() for o in outputs]
+        out_strides = [o.stride(0) if o.ndim == 2 else int(o.size(-1)) for o in outputs]
+        self.feats_fwd = ops.build_features(plan, id_counts, bag_counts, out_ptrs, out_strides)
+        n_chunks = lib().mdl_plan_chunks(self.feats_fwd.ctypes.data, len(self.feats_fwd),
+                                         ops.FORWARD_TARGET_IDS, None, 0)
+        if n_chunks < 0:
+            check(int(n_chunks), "mdl_plan_chunks")
+        chunks = np.zeros(max(n_chunks, 1), dtype=CHUNK_DTYPE)
+        lib().mdl_plan_chunks(self.feats_fwd.ctypes.data, len(self.feats_fwd), ops.FORWARD_TARGET_IDS,
+                              chunks.ctypes.data, n_chunks)
+        self.n_chunks = int(n_chunks)
+        res = ops.ForwardResult(
+            plan=plan, device=self.device, ids=self.ids, offsets=None, outputs=list(outputs),
+            feats=self.feats_fwd, keys=None, payload=None, bag_count=None, error_count=self.error_count,
+        )
+        self.feats_bwd, self._grads = ops._attach_grads(res, grads)
+        self.tables = ops._tables_array(plan, self.feats_bwd)
+        self.feats_fwd_dev = ops.upload(self.feats_fwd, self.device)
+        self.chunks_dev = ops.upload(chunks, self.device)
+        self.feats_bwd_dev = ops.upload(self.feats_bwd, self.device)
+        self.tables_dev = ops.upload(self.tables, self.device)
+        total_rows = int(
+            np.where(self.feats_fwd["pooling"] != MDL_POOL_NONE, self.feats_fwd["num_bags"],
+                     self.feats_fwd["num_ids"]).sum()
+        )
+        self.keys = torch.empty(max(self.n, 1), dtype=torch.int32, device=self.device)
+        self.payload = torch.empty(max(self.n, 1), dtype=torch.int32, device=self.device)
+        self.bag_count = (
+            torch.empty(max(total_rows, 1), dtype=torch.float32, device=self.device) if pooled_any else None
+        )
+        self.ws = ops._workspace(
+            lib().mdl_backward_workspace_bytes(self.n, len(self.tables), plan.max_dim), self.device
+        )
+
+    def _stream(self) -> int:
+        return torch.cuda.current_stream(self.device).cuda_stream
+
+    def forward(self) -> None:
+        """Offsets scan + grouped lookup/pooling (+ backward sort keys)."""
+
+        s = self._stream()
+        if self.offsets is not None:
+            check(
+                lib().mdl_lengths_to_offsets(
+                    self.lengths.data_ptr(), self.lengths.numel(), self.offsets.data_ptr(),
+                    self.scan_ws.data_ptr(), self.scan_ws.numel(), s,
+                ),
+                "mdl_lengths_to_offsets",
+            )
+        check(
+            lib().mdl_forward(
+                self.feats_fwd_dev.data_ptr(), len(self.feats_fwd), self.chunks_dev.data_ptr(), self.n_chunks,
+                self.ids.data_ptr(), ops._ptr(self.offsets), self.keys.data_ptr(), self.payload.data_ptr(),
+                self.plan.sentinel, ops._ptr(self.bag_count), self.error_count.data_ptr(), s,
+            ),
+            "mdl_forward",
+        )
+
+    def sort(self) -> None:
+        """Radix sort of the (row, gradient-row) pairs + chunk plan."""
+
+        check(
+            lib().mdl_backward_sort(
+                self.tables_dev.data_ptr(), len(self.tables), self.plan.max_dim, self.keys.data_ptr(),
+                self.payload.data_ptr(), self.n, self.plan.key_bits, self.ws.data_ptr(), self.ws.numel(),
+                self._stream(),
+            ),
+            "mdl_backward_sort",
+        )
+
+    def apply(self, lr: float, eps: float) -> None:
+        """Segment reduction of duplicate rows + fused row-wise Adagrad."""
+
+        check(
+            lib().mdl_backward_apply(
+                self.feats_bwd_dev.data_ptr(), len(self.feats_bwd), self.tables_dev.data_ptr(), len(self.tables),
+                self.plan.max_dim, self.keys.data_ptr(), self.payload.data_ptr(), self.n, self.plan.key_bits,
+                ops._ptr(self.bag_count), float(lr), float(eps), self.ws.data_ptr(), self.ws.numel(),
+                self._stream(),
+            ),
+            "mdl_backward_apply",
+        )
+
+    def step(self, lr: float, eps: float) -> None:
+        self.forward()
+        self.sort()
+        self.apply(lr, eps)
