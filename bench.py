@@ -61,6 +61,9 @@ class Workload:
     features: list[Feature]
     zipf: list[float]  # per table; 0 = uniform
     raw_bits: int | None = None  # raw ids drawn over 2^raw_bits then bucketed mod rows
+    kind: str = "pooled"  # "pooled" | "sequence"
+    seq_len: tuple[int, int, int] | None = None  # (min len, max len, padded length) for sequences
+    repeat_frac: float = 0.0  # share of sequence positions that repeat an earlier id of the row
     lr: float = 0.01
     eps: float = 1e-8
     notes: dict = field(default_factory=dict)
@@ -110,7 +113,32 @@ def workload_c0() -> Workload:
     )
 
 
-WORKLOADS = {"c1": workload_c1, "c3": lambda: workload_c1("bf16"), "c0": workload_c0}
+def workload_c2() -> Workload:
+    feats = [Feature(table=t, pooling="none", bag_len=None) for t in range(4)]
+    return Workload(
+        name="c2", batch=1024, rows=[200_000_000] * 4, dims=[64] * 4, dtype="fp32", features=feats,
+        zipf=[0.9] * 4, kind="sequence", seq_len=(64, 2000, 2048), repeat_frac=0.1,
+    )
+
+
+def workload_c4() -> Workload:
+    # 1.5e9 rows in total over the 8 large bf16 tables (192 GB), plus 24 small
+    feats = [Feature(table=t, pooling="sum", bag_len=(1, 1)) for t in range(32)]
+    rows = [187_500_000] * 8 + [100_000] * 24
+    dims = [64] * 8 + [32] * 24
+    return Workload(
+        name="c4", batch=16384, rows=rows, dims=dims, dtype="bf16", features=feats,
+        zipf=[0.0] * 8 + [1.2] * 24,
+    )
+
+
+WORKLOADS = {
+    "c1": workload_c1,
+    "c3": lambda: workload_c1("bf16"),
+    "c0": workload_c0,
+    "c2": workload_c2,
+    "c4": workload_c4,
+}
 
 
 def bounded_zipf(rng: np.random.Generator, alpha: float, n: int, hi: int) -> np.ndarray:
@@ -142,6 +170,8 @@ def draw_ids(rng: np.random.Generator, wl: Workload, t: int, n: int) -> np.ndarr
         return rng.integers(1, rows, size=n)
     if wl.raw_bits:
         raw = bounded_zipf(rng, a, n, 1 << wl.raw_bits)
+    elif a <= 1.0:
+        raw = bounded_zipf(rng, a, n, rows - 1)
     else:
         raw = rng.zipf(a, size=n)
     # the reference benchmark's id rule: 1 + (z - 1) mod (N - 1), src/benchmark.py:1246-1250
@@ -149,8 +179,30 @@ def draw_ids(rng: np.random.Generator, wl: Workload, t: int, n: int) -> np.ndarr
 
 
 def draw_batch(rng: np.random.Generator, wl: Workload):
-    """Per-feature ids and bag lengths (None for single-valued features)."""
+    """Per-feature ids and bag lengths (None for single-valued features).
 
+    Sequence workloads return right-padded ``[B, L]`` ids and ``[B]`` lengths."""
+
+    if wl.kind == "sequence":
+        lo, hi, pad = wl.seq_len
+        ids, lengths = [], []
+        for f in wl.features:
+            ln = rng.integers(lo, hi + 1, size=wl.batch)
+            flat = draw_ids(rng, wl, f.table, int(ln.sum()))
+            mat = np.zeros((wl.batch, pad), dtype=np.int64)
+            pos = 0
+            for b in range(wl.batch):
+                row = flat[pos: pos + ln[b]].copy()
+                pos += ln[b]
+                k = int(wl.repeat_frac * ln[b])
+                if k and ln[b] > 1:
+                    dst = rng.integers(1, ln[b], size=k)
+                    src = (rng.random(k) * dst).astype(np.int64)  # an earlier position of the row
+                    row[dst] = row[src]
+                mat[b, : ln[b]] = row
+            ids.append(mat)
+            lengths.append(ln)
+        return ids, lengths
     ids, lengths = [], []
     for f in wl.features:
         if f.bag_len is None:
@@ -172,6 +224,28 @@ def algorithmic_bytes(wl: Workload, ids, lengths) -> dict:
     """Per-step algorithmic HBM bytes (SURVEY 8(d) formula) and its parts."""
 
     esize = 4 if wl.dtype == "fp32" else 2
+    if wl.kind == "sequence":
+        total = 0
+        n_ids = 0
+        uniq = 0
+        fwd_rows = 0
+        _, _, pad = wl.seq_len
+        for f, mat, ln in zip(wl.features, ids, lengths):
+            valid = np.arange(mat.shape[1])[None, :] < ln[:, None]
+            x = mat[valid]
+            x = x[x != 0]
+            u = np.unique(x).size
+            n = x.size
+            d = wl.dims[f.table]
+            n_ids += n
+            uniq += u
+            fwd_rows += u * d * esize
+            # ids + lengths read twice, distinct rows 3x, state, padded output +
+            # mask, gradient rows at the valid positions
+            total += 16 * n + 16 * (wl.batch + 1) + 3 * u * d * esize + 8 * u
+            total += wl.batch * pad * d * 4 + wl.batch * pad + n * d * 4
+        return {"B_alg": total, "n_ids": n_ids, "unique_rows": uniq, "fwd_unique_row_bytes": fwd_rows,
+                "sum_dim": sum(wl.dims[f.table] for f in wl.features)}
     n_t = {}
     uniq_t = {}
     bags_t = {}
@@ -257,6 +331,60 @@ class DeviceStep:
             lens = torch.from_numpy(np.concatenate(parts).astype(np.int64)).to(device)
             self.steps.append(SparseStep(self.plan, packed, lens, id_counts, bag_counts, out_views, grad_views,
                                          error_count=self.err))
+
+    def step(self, i: int, timers=None):
+        st = self.steps[i % len(self.steps)]
+        if timers is None:
+            st.step(self.wl.lr, self.wl.eps)
+            return
+        timers["forward"].start()
+        st.forward()
+        timers["forward"].stop()
+        st.sort()
+        timers["apply"].start()
+        st.apply(self.wl.lr, self.wl.eps)
+        timers["apply"].stop()
+
+
+class SequenceDeviceStep:
+    """Sequence tables, padded windows and one SequenceStep per batch."""
+
+    def __init__(self, wl: Workload, batches, device):
+        import torch
+
+        from mdl_amd import ops
+        from mdl_amd.sparse_step import SequenceStep
+
+        self.torch = torch
+        self.wl = wl
+        wdtype = torch.float32 if wl.dtype == "fp32" else torch.bfloat16
+        gen = torch.Generator(device=device)
+        gen.manual_seed(1234)
+        self.tables, self.states = [], []
+        for r, d in zip(wl.rows, wl.dims):
+            w = torch.empty((r, d), dtype=wdtype, device=device)
+            w.normal_(0.0, 0.02, generator=gen)
+            w[0].zero_()
+            self.tables.append(w)
+            self.states.append(torch.zeros(r, dtype=torch.float32, device=device))
+        self.plan = ops.GroupPlan()
+        for f in wl.features:
+            self.plan.add_feature(self.tables[f.table], pooling="none", state=self.states[f.table])
+        _, _, pad = wl.seq_len
+        self.outs = [torch.empty((wl.batch, pad, wl.dims[f.table]), dtype=wdtype, device=device) for f in wl.features]
+        self.masks = [torch.empty((wl.batch, pad), dtype=torch.bool, device=device) for _ in wl.features]
+        self.grads = []
+        for o in self.outs:
+            g = torch.empty_like(o)
+            g.normal_(0.0, 1.0, generator=gen)
+            self.grads.append(g)
+        self.err = torch.zeros(1, dtype=torch.int32, device=device)
+        self.steps = []
+        for ids, lengths in batches:
+            dids = [torch.from_numpy(m).to(device) for m in ids]
+            dlen = [torch.from_numpy(ln.astype(np.int64)).to(device) for ln in lengths]
+            self.steps.append(SequenceStep(self.plan, dids, dlen, self.outs, self.masks, self.grads,
+                                           error_count=self.err))
 
     def step(self, i: int, timers=None):
         st = self.steps[i % len(self.steps)]
@@ -384,7 +512,7 @@ def main() -> int:
     alg = [algorithmic_bytes(wl, ids, lengths) for ids, lengths in batches]
     print(f"[bench] drew {args.batches} batches; {alg[0]['n_ids']} ids/step, "
           f"{alg[0]['unique_rows']} distinct rows", file=sys.stderr, flush=True)
-    dev = DeviceStep(wl, batches, device)
+    dev = (SequenceDeviceStep if wl.kind == "sequence" else DeviceStep)(wl, batches, device)
     torch.cuda.synchronize()
     print("[bench] tables initialised", file=sys.stderr, flush=True)
     for i in range(args.warmup):
@@ -413,10 +541,21 @@ def main() -> int:
     esz = 4 if wl.dtype == "fp32" else 2
     nb = float(np.mean([sum(len(ln) for ln in b[1] if ln is not None) for b in batches]))
     kernels = {}
-    fwd_bytes = float(np.mean([16 * a["n_ids"] + 8 * (nb + 1) + a["fwd_unique_row_bytes"]
-                               + wl.batch * a["sum_dim"] * esz + 4 * nb for a in used]))
-    apply_bytes = float(np.mean([8 * a["n_ids"] + wl.batch * a["sum_dim"] * esz + 2 * a["fwd_unique_row_bytes"]
-                                 + 8 * a["unique_rows"] + 4 * nb for a in used]))
+    if wl.kind == "sequence":
+        _, _, pad = wl.seq_len
+        nf = len(wl.features)
+        d = wl.dims[0]
+        # ids + lengths read, distinct rows, padded window + mask, sort keys/payloads
+        fwd_bytes = float(np.mean([8 * nf * wl.batch * pad + 8 * nf * wl.batch + a["fwd_unique_row_bytes"]
+                                   + nf * wl.batch * pad * (d * esz + 1) + 8 * nf * wl.batch * pad for a in used]))
+        # sorted keys/payloads, gradient rows at valid positions, rows read+written, state
+        apply_bytes = float(np.mean([8 * nf * wl.batch * pad + a["n_ids"] * d * esz
+                                     + 2 * a["fwd_unique_row_bytes"] + 8 * a["unique_rows"] for a in used]))
+    else:
+        fwd_bytes = float(np.mean([16 * a["n_ids"] + 8 * (nb + 1) + a["fwd_unique_row_bytes"]
+                                   + wl.batch * a["sum_dim"] * esz + 4 * nb for a in used]))
+        apply_bytes = float(np.mean([8 * a["n_ids"] + wl.batch * a["sum_dim"] * esz
+                                     + 2 * a["fwd_unique_row_bytes"] + 8 * a["unique_rows"] + 4 * nb for a in used]))
     for name, nbytes, label in (
         ("forward", fwd_bytes, "forward_kernel (grouped lookup + pooling + sort-key emission)"),
         ("apply", apply_bytes, "bwd_reduce_kernel + fix-up (segment reduction + row-wise Adagrad)"),

@@ -593,6 +593,73 @@ def pooled_embedding_lookup(
     )
 
 
+class _SequenceLookupFn(torch.autograd.Function):
+    """Right-aligned sequence lookup with a coalesced sparse weight gradient."""
+
+    @staticmethod
+    def forward(ctx, ctl: dict, ids: Tensor, lengths: Tensor, weight: Tensor):  # type: ignore[override]
+        module: ShardedEmbedding = ctl["module"]
+        err = ctl.get("error_count")
+        res = ops.sequence_lookup(
+            weight, ids, lengths, out_len=ctl["out_len"], order=ctl["order"], padding_idx=module.padding_idx,
+            with_backward=weight.requires_grad, error_count=err,
+        )
+        if ctl.get("check", True):
+            _raise_for_errors([module], [ids], res.error_count)
+        ctx.res = res
+        ctx.weight = weight
+        mask = res.keep[0]
+        ctx.mark_non_differentiable(mask)
+        return res.outputs[0], mask
+
+    @staticmethod
+    def backward(ctx, grad_out: Tensor, _grad_mask):  # type: ignore[override]
+        (rows, vals), = ops.backward_coalesce(ctx.res, [grad_out])
+        weight = ctx.weight
+        ctx.res = None
+        ctx.weight = None
+        grad = torch.sparse_coo_tensor(rows.unsqueeze(0), vals, tuple(weight.shape), is_coalesced=True)
+        _remember_coalesced(weight, rows, vals)
+        return None, None, None, grad
+
+
+def sequence_embedding_lookup(
+    module: ShardedEmbedding,
+    ids: Tensor,
+    lengths: Tensor,
+    *,
+    target_length: int | None = None,
+    sequence_order: str = "oldest_to_newest",
+) -> tuple[Tensor, Tensor]:
+    """Embed a right-padded ``[B, L]`` id sequence into a right-aligned window.
+
+    Same result as ``module(ids)`` followed by ``_right_aligned_sequence`` (and
+    the reversal of ``_align_sequence_inputs`` for ``newest_to_oldest``),
+    src/model.py:2989-3100: ``([B, T, dim] embeddings, [B, T] bool mask)`` with
+    ``T = target_length or L``; the padded window is written in one launch.
+    """
+
+    module._require_single_rank()
+    if ids.dtype != torch.long:
+        raise TypeError("sharded embedding indices must be torch.long")
+    if ids.ndim != 2 or lengths.ndim != 1 or lengths.numel() != ids.size(0):
+        raise ValueError("sequence ids must be [B, L] with lengths [B]")
+    if sequence_order not in ("oldest_to_newest", "newest_to_oldest"):
+        raise ValueError("sequence_order must be oldest_to_newest or newest_to_oldest")
+    deferred = deferred_index_checks()
+    ctl = {
+        "module": module,
+        "out_len": int(ids.size(1) if target_length is None else target_length),
+        "order": sequence_order,
+        "check": module.validate_indices and not deferred,
+        "error_count": _deferred_counter(module.weight.device) if deferred else None,
+    }
+    out, mask = _SequenceLookupFn.apply(ctl, ids, lengths, module.weight)
+    if module.collect_stats and embedding_stats_host_sync_enabled():
+        module._stats_sink.record_forward(_local_stats(module.table_name, int(ids.numel())))
+    return out, mask
+
+
 def sharded_embedding_modules(module: nn.Module) -> list[ShardedEmbedding]:
     return [item for item in module.modules() if isinstance(item, ShardedEmbedding)]
 

@@ -831,3 +831,71 @@ def sequence_forward(
         "mdl_sequence_forward",
     )
     return out, mask
+
+
+def sequence_feature(
+    weight: Tensor,
+    *,
+    state: Tensor | None = None,
+    padding_idx: int = 0,
+    out_dtype: torch.dtype | None = None,
+    row_base: int = 0,
+    payload_base: int = 0,
+    grad: Tensor | None = None,
+) -> np.ndarray:
+    """Descriptor of one sequence feature: an unpooled feature whose output
+    rows are the ``[B * out_len]`` positions of the padded window."""
+
+    feat = np.zeros(1, dtype=FEATURE_DTYPE)
+    rec = feat[0]
+    rec["weight"] = weight.data_ptr()
+    rec["state"] = state.data_ptr() if state is not None else 0
+    rec["grad"] = grad.data_ptr() if grad is not None else 0
+    rec["num_rows"] = int(weight.size(0))
+    rec["out_stride"] = int(weight.size(1))
+    rec["row_base"] = row_base
+    rec["payload_base"] = payload_base
+    rec["dim"] = int(weight.size(1))
+    rec["wdtype"] = dtype_code(weight.dtype)
+    rec["odtype"] = dtype_code(out_dtype or weight.dtype)
+    rec["pooling"] = MDL_POOL_NONE
+    rec["padding_idx"] = padding_idx
+    return feat
+
+
+def sequence_lookup(
+    weight: Tensor,
+    ids: Tensor,
+    lengths: Tensor,
+    *,
+    out_len: int | None = None,
+    order: str = "oldest_to_newest",
+    padding_idx: int = 0,
+    with_backward: bool = True,
+    error_count: Tensor | None = None,
+) -> ForwardResult:
+    """Right-aligned sequence gather with backward bookkeeping.
+
+    ``outputs[0]`` is ``[B, out_len, dim]`` and ``keep[0]`` the ``[B, out_len]``
+    mask; the result feeds :func:`backward_coalesce` like a grouped lookup.
+    """
+
+    plan = GroupPlan()
+    plan.add_feature(weight, pooling="none", padding_idx=padding_idx)
+    device = ids.device
+    n = int(ids.numel())
+    keys = payload = None
+    if with_backward:
+        keys = torch.empty(max(n, 1), dtype=torch.int32, device=device)
+        payload = torch.empty(max(n, 1), dtype=torch.int32, device=device)
+    if error_count is None:
+        error_count = torch.zeros(1, dtype=torch.int32, device=device)
+    out, mask = sequence_forward(
+        weight, ids, lengths, out_len=out_len, order=order, padding_idx=padding_idx, keys=keys,
+        payload=payload, row_base=0, payload_base=0, sentinel=plan.sentinel, error_count=error_count,
+    )
+    feats = sequence_feature(weight, padding_idx=padding_idx)
+    return ForwardResult(
+        plan=plan, device=device, ids=ids, offsets=None, outputs=[out], feats=feats, keys=keys,
+        payload=payload, bag_count=None, error_count=error_count, keep=[mask],
+    )

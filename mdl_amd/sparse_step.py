@@ -145,3 +145,114 @@ class SparseStep:
         self.forward()
         self.sort()
         self.apply(lr, eps)
+
+
+class SequenceStep:
+    """Fused step over sequence features (long user-behaviour histories).
+
+    Every feature ``f`` has a table, right-padded ids ``[B, L_in]``, lengths
+    ``[B]`` and a padded output window ``[B, L_out, dim]`` (+ mask); the
+    backward reads the window's gradient.  Forward: one gather launch per
+    feature; backward: one sort and one segment-reduce + row-wise Adagrad over
+    all features together.
+    """
+
+    def __init__(
+        self,
+        plan: ops.GroupPlan,
+        ids: Sequence[Tensor],
+        lengths: Sequence[Tensor],
+        outputs: Sequence[Tensor],
+        masks: Sequence[Tensor],
+        grads: Sequence[Tensor],
+        *,
+        order: str = "oldest_to_newest",
+        error_count: Tensor | None = None,
+    ) -> None:
+        for t in plan.tables:
+            if t.state is None:
+                raise RuntimeError("every table needs a row-wise Adagrad accumulator")
+        self.plan = plan
+        self.device = ids[0].device
+        self.ids = [t.contiguous() for t in ids]
+        self.lengths = [t.to(torch.int64).contiguous() for t in lengths]
+        self.outputs = list(outputs)
+        self.masks = list(masks)
+        self.grads = [g.contiguous() for g in grads]
+        self.order = ops._lib.MDL_SEQ_OLDEST_TO_NEWEST if order == "oldest_to_newest" else ops._lib.MDL_SEQ_NEWEST_TO_OLDEST
+        self.error_count = (
+            error_count if error_count is not None else torch.zeros(1, dtype=torch.int32, device=self.device)
+        )
+        self.n = sum(int(t.numel()) for t in self.ids)
+        self.keys = torch.empty(max(self.n, 1), dtype=torch.int32, device=self.device)
+        self.payload = torch.empty(max(self.n, 1), dtype=torch.int32, device=self.device)
+        feats = []
+        self.fwd_feats = []
+        key_off = 0
+        payload_base = 0
+        self.key_offsets = []
+        for f, spec in enumerate(plan.features):
+            table = plan.tables[spec.table]
+            out = self.outputs[f]
+            B, L_out, _ = out.shape
+            rec = ops.sequence_feature(
+                table.weight, state=table.state, padding_idx=spec.padding_idx, out_dtype=spec.out_dtype,
+                row_base=table.row_base, payload_base=payload_base, grad=self.grads[f],
+            )
+            rec["table"] = spec.table
+            feats.append(rec)
+            self.fwd_feats.append(rec.copy())
+            self.key_offsets.append(key_off)
+            key_off += int(self.ids[f].numel())
+            payload_base += int(B) * int(L_out)
+        self.feats_bwd = np.concatenate(feats)
+        self.tables = ops._tables_array(plan, self.feats_bwd)
+        self.feats_bwd_dev = ops.upload(self.feats_bwd, self.device)
+        self.tables_dev = ops.upload(self.tables, self.device)
+        self.ws = ops._workspace(
+            lib().mdl_backward_workspace_bytes(self.n, len(self.tables), plan.max_dim), self.device
+        )
+
+    def _stream(self) -> int:
+        return torch.cuda.current_stream(self.device).cuda_stream
+
+    def forward(self) -> None:
+        s = self._stream()
+        for f, rec in enumerate(self.fwd_feats):
+            ids = self.ids[f]
+            out = self.outputs[f]
+            off = self.key_offsets[f]
+            check(
+                lib().mdl_sequence_forward(
+                    rec.ctypes.data, ids.data_ptr(), self.lengths[f].data_ptr(), ids.size(0), ids.size(1),
+                    out.size(1), self.order, out.data_ptr(), self.masks[f].data_ptr(),
+                    self.keys.data_ptr() + 4 * off, self.payload.data_ptr() + 4 * off, self.plan.sentinel,
+                    self.error_count.data_ptr(), s,
+                ),
+                "mdl_sequence_forward",
+            )
+
+    def sort(self) -> None:
+        check(
+            lib().mdl_backward_sort(
+                self.tables_dev.data_ptr(), len(self.tables), self.plan.max_dim, self.keys.data_ptr(),
+                self.payload.data_ptr(), self.n, self.plan.key_bits, self.ws.data_ptr(), self.ws.numel(),
+                self._stream(),
+            ),
+            "mdl_backward_sort",
+        )
+
+    def apply(self, lr: float, eps: float) -> None:
+        check(
+            lib().mdl_backward_apply(
+                self.feats_bwd_dev.data_ptr(), len(self.feats_bwd), self.tables_dev.data_ptr(), len(self.tables),
+                self.plan.max_dim, self.keys.data_ptr(), self.payload.data_ptr(), self.n, self.plan.key_bits,
+                None, float(lr), float(eps), self.ws.data_ptr(), self.ws.numel(), self._stream(),
+            ),
+            "mdl_backward_apply",
+        )
+
+    def step(self, lr: float, eps: float) -> None:
+        self.forward()
+        self.sort()
+        self.apply(lr, eps)

@@ -206,3 +206,54 @@ def test_training_steps_match_oracle(device, dtype):
         assert np.all(np.abs(got - W[t]) <= tol * np.abs(W[t]) + tol * 1e-1), t
         s = opt.state[m.weight]["sum"].cpu().numpy()
         assert np.all(np.abs(s - A[t]) <= tol * np.abs(A[t]) + 1e-6), t
+
+
+@pytest.mark.parametrize("order", ["oldest_to_newest", "newest_to_oldest"])
+def test_sequence_lookup_forward_backward_step(device, order):
+    """sequence_embedding_lookup == F.embedding + right alignment; its sparse
+    gradient and the optimizer step match the oracle."""
+
+    from mdl_amd.embeddings import sequence_embedding_lookup
+
+    announce("sequence_lookup", order)
+    rng = np.random.default_rng(95)
+    (m,) = _modules(device, [("hist", 5000, 32)])
+    with torch.no_grad():
+        w = torch.from_numpy(rng.standard_normal((5000, 32)).astype(np.float32))
+        w[0] = 0
+        m.weight.data = w.to(device)
+    W0 = m.weight.detach().cpu().numpy().copy()
+    opt = ShardedRowWiseAdagrad([m.weight], lr=0.05, eps=1e-8)
+    B, L = 40, 300
+    lengths = rng.integers(0, L + 1, size=B)
+    ids = np.zeros((B, L), dtype=np.int64)
+    for b in range(B):
+        ids[b, : lengths[b]] = rng.zipf(1.1, size=lengths[b]) % 5000
+    for T in (L, 200):
+        out, mask = sequence_embedding_lookup(m, torch.from_numpy(ids).to(device),
+                                              torch.from_numpy(lengths).to(device), target_length=T,
+                                              sequence_order=order)
+        ref, rmask = O.sequence_gather(m.weight.detach().cpu().numpy(), ids, lengths, T, order)
+        assert np.array_equal(mask.cpu().numpy(), rmask)
+        assert np.array_equal(out.detach().cpu().numpy(), ref.astype(np.float32))
+    g = rng.standard_normal(tuple(out.shape)).astype(np.float32)
+    opt.zero_grad(set_to_none=True)
+    out.backward(torch.from_numpy(g).to(device))
+    opt.step()
+    # oracle: every valid position (b, k) sends grad[b, p(k)] to row ids[b, k]
+    rows, vals = [], []
+    for b in range(B):
+        n = min(int(lengths[b]), T)
+        start = T - n
+        for k in range(n):
+            p = start + k if order == "oldest_to_newest" else start + (n - 1 - k)
+            if ids[b, k] != 0:
+                rows.append(ids[b, k])
+                vals.append(g[b, p])
+    rr, vv = O.coalesce(np.array(rows), np.array(vals, dtype=np.float64))
+    wexp, aexp = O.rowwise_adagrad(W0, np.zeros(5000, np.float32), rr, vv, 0.05, 1e-8)
+    got = m.weight.detach().cpu().numpy()
+    _, vabs = O.coalesce(np.array(rows), np.abs(np.array(vals, dtype=np.float64)))
+    assert np.all(np.abs(got - wexp) <= 1e-5 * np.abs(wexp) + 1e-6)
+    s = opt.state[m.weight]["sum"].cpu().numpy()
+    assert np.all(np.abs(s - aexp) <= 1e-5 * np.abs(aexp) + 1e-6)

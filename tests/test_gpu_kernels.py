@@ -379,3 +379,109 @@ def test_coalesce_rows_matches_torch(device):
     _, vabs = O.coalesce(idx, np.abs(vals.astype(np.float64)))
     assert np.array_equal(r.cpu().numpy(), rr)
     assert_close(v.cpu().numpy(), vv, 1e-5, 1e-6, vabs)
+
+
+def test_sparse_step_slot_buffer_matches_oracle(device):
+    """SparseStep: pooled + unpooled features written into one [B, sum(dim)]
+    slot buffer, gradients read from the same layout, fused update."""
+
+    from mdl_amd.sparse_step import SparseStep
+
+    announce("sparse_step")
+    rng = np.random.default_rng(80)
+    B = 512
+    rows = [3000, 500, 20000, 64]
+    dims = [32, 16, 64, 128]
+    pools = ["mean", "none", "mean", "sum"]
+    W = [rng.standard_normal((r, d)).astype(np.float32) for r, d in zip(rows, dims)]
+    for w in W:
+        w[0] = 0
+    tabs = [torch.from_numpy(w.copy()).to(device) for w in W]
+    accs = [torch.zeros(r, device=device) for r in rows]
+    plan = ops.GroupPlan()
+    for t, p in enumerate(pools):
+        plan.add_feature(tabs[t], pooling=p, null_policy="exclude", state=accs[t])
+    ids, lens = [], []
+    for t, p in enumerate(pools):
+        if p == "none":
+            ids.append(rng.zipf(1.1, size=B) % rows[t])
+            lens.append(None)
+        else:
+            ln = rng.integers(0, 25, size=B)
+            ids.append(rng.zipf(1.1, size=int(ln.sum())) % rows[t])
+            lens.append(ln)
+    S = sum(dims)
+    out = torch.empty((B, S), device=device)
+    grad = torch.from_numpy(rng.standard_normal((B, S)).astype(np.float32)).to(device)
+    cols = np.concatenate([[0], np.cumsum(dims)[:-1]])
+    parts = [ln if ln is not None else np.array([x.size]) for x, ln in zip(ids, lens)]
+    st = SparseStep(plan, torch.from_numpy(np.concatenate(ids)).to(device),
+                    torch.from_numpy(np.concatenate(parts)).to(device), [x.size for x in ids],
+                    [0 if ln is None else ln.size for ln in lens],
+                    [out[:, c: c + d] for c, d in zip(cols, dims)], [grad[:, c: c + d] for c, d in zip(cols, dims)])
+    st.step(0.02, 1e-8)
+    feats = []
+    offs, bag_off, ids_off = [], 0, 0
+    for t, (p, x, ln) in enumerate(zip(pools, ids, lens)):
+        feats.append({"table": t, "pooling": {"none": 0, "sum": 1, "mean": 2}[p], "exclude": 1, "ids_off": ids_off,
+                      "bag_off": bag_off, "num_bags": 0 if ln is None else B, "out_col": int(cols[t])})
+        if ln is not None:
+            o = O.offsets_of(ln)
+            offs.append(o)
+            bag_off += len(o)
+        ids_off += x.size
+    tables = [{"W": w.copy(), "acc": np.zeros(r, np.float32)} for w, r in zip(W, rows)]
+    ref_out = O.sparse_step(feats, tables, np.concatenate(ids), np.concatenate(offs), S,
+                            grad.cpu().numpy().astype(np.float64), 0.02, 1e-8)
+    absw = [{"W": np.abs(w), "acc": np.zeros(r, np.float32)} for w, r in zip(W, rows)]
+    scale = O.sparse_step(feats, absw, np.concatenate(ids), np.concatenate(offs), S,
+                          np.zeros((B, S)), 0.0, 1.0)
+    assert_close(out.cpu().numpy(), ref_out, 1e-5, 1e-6, scale)
+    for t in range(len(rows)):
+        assert_close(tabs[t].cpu().numpy(), tables[t]["W"], 1e-5, 1e-6)
+        assert_close(accs[t].cpu().numpy(), tables[t]["acc"], 1e-5, 1e-7)
+
+
+def test_sequence_step_matches_oracle(device):
+    from mdl_amd.sparse_step import SequenceStep
+
+    announce("sequence_step")
+    rng = np.random.default_rng(81)
+    B, L = 64, 256
+    rows = [4000, 9000]
+    W = [rng.standard_normal((r, 64)).astype(np.float32) for r in rows]
+    tabs = [torch.from_numpy(w.copy()).to(device) for w in W]
+    accs = [torch.zeros(r, device=device) for r in rows]
+    plan = ops.GroupPlan()
+    for t in range(2):
+        plan.add_feature(tabs[t], pooling="none", state=accs[t])
+    ids, lens = [], []
+    for t in range(2):
+        ln = rng.integers(0, L + 1, size=B)
+        m = np.zeros((B, L), dtype=np.int64)
+        for b in range(B):
+            m[b, : ln[b]] = rng.zipf(1.05, size=ln[b]) % rows[t]
+        ids.append(m)
+        lens.append(ln)
+    outs = [torch.empty((B, L, 64), device=device) for _ in range(2)]
+    masks = [torch.empty((B, L), dtype=torch.bool, device=device) for _ in range(2)]
+    grads = [torch.from_numpy(rng.standard_normal((B, L, 64)).astype(np.float32)).to(device) for _ in range(2)]
+    st = SequenceStep(plan, [torch.from_numpy(m).to(device) for m in ids],
+                      [torch.from_numpy(ln).to(device) for ln in lens], outs, masks, grads)
+    st.step(0.03, 1e-8)
+    for t in range(2):
+        ref, rmask = O.sequence_gather(W[t], ids[t], lens[t], L)
+        assert np.array_equal(outs[t].cpu().numpy(), ref.astype(np.float32))
+        assert np.array_equal(masks[t].cpu().numpy(), rmask)
+        g = grads[t].cpu().numpy()
+        r, v = [], []
+        for b in range(B):
+            n = int(lens[t][b])
+            for k in range(n):
+                if ids[t][b, k] != 0:
+                    r.append(ids[t][b, k])
+                    v.append(g[b, L - n + k])
+        rr, vv = O.coalesce(np.array(r), np.array(v, dtype=np.float64))
+        wexp, aexp = O.rowwise_adagrad(W[t], np.zeros(rows[t], np.float32), rr, vv, 0.03, 1e-8)
+        assert_close(tabs[t].cpu().numpy(), wexp, 1e-5, 1e-6)
+        assert_close(accs[t].cpu().numpy(), aexp, 1e-5, 1e-7)
