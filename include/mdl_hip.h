@@ -47,6 +47,17 @@ enum { MDL_FLAG_EXCLUDE_NULL = 1 };
 
 enum { MDL_BUCKET_PRE_HASHED = 0, MDL_BUCKET_MOD = 1 };
 
+/* Row-access classes of a feature or table: weight dtype x output/gradient
+ * dtype x whether every row access is 16-byte aligned.  Kernels are
+ * specialised per class; the calls taking a `classes` mask launch only the
+ * classes whose bit (1 << class) is set, 0 meaning all.  mdl_feature_classes
+ * and mdl_table_classes compute the mask of a host descriptor array with the
+ * kernels' own rule; a mask that misses a present class skips its rows. */
+enum {
+  MDL_CLASS_F32_VEC = 0, MDL_CLASS_F32 = 1, MDL_CLASS_BF16_VEC = 2,
+  MDL_CLASS_BF16 = 3, MDL_CLASS_BF16_F32_VEC = 4, MDL_CLASS_BF16_F32 = 5
+};
+
 /* Sequence output order (src/model.py:3074-3100). */
 enum { MDL_SEQ_OLDEST_TO_NEWEST = 0, MDL_SEQ_NEWEST_TO_OLDEST = 1 };
 
@@ -143,6 +154,10 @@ int mdl_lengths_to_offsets(const int64_t* lengths, int64_t n, int64_t* offsets,
 
 /* -------------------------------------------------------------- planning --- */
 
+/* Host helpers: class masks (see MDL_CLASS_*) of host descriptor arrays. */
+uint32_t mdl_feature_classes(const mdl_feature* feats_host, int32_t num_features);
+uint32_t mdl_table_classes(const mdl_table* tables_host, int32_t num_tables);
+
 /* Host helper: split every feature into forward chunks of about target_ids ids.
  * feats_host: host copy of the descriptors.  Writes at most `capacity`
  * chunks to chunks_host (host, may be NULL) and returns the number needed,
@@ -179,7 +194,8 @@ int mdl_forward(const mdl_feature* feats, int32_t num_features,
                 const mdl_chunk* chunks, int64_t num_chunks,
                 const int64_t* ids, const int64_t* offsets,
                 uint32_t* sort_keys, uint32_t* sort_payload, uint32_t sentinel,
-                float* bag_count, int32_t* error_count, void* stream);
+                float* bag_count, int32_t* error_count, uint32_t classes,
+                void* stream);
 
 /*
  * Sequence gather without pooling, right-aligned into a padded window
@@ -269,7 +285,8 @@ int mdl_backward_adagrad(const mdl_feature* feats, int32_t num_features,
                          const mdl_table* tables, int32_t num_tables, int32_t max_dim,
                          uint32_t* sort_keys, uint32_t* sort_payload, int64_t n,
                          int32_t key_bits, const float* bag_count, float lr, float eps,
-                         void* workspace, size_t workspace_bytes, void* stream);
+                         void* workspace, size_t workspace_bytes, uint32_t classes,
+                         void* stream);
 
 /* mdl_backward_adagrad in two calls with the same arguments and workspace:
  * mdl_backward_sort (radix sort + chunk plan), then mdl_backward_apply
@@ -282,7 +299,8 @@ int mdl_backward_apply(const mdl_feature* feats, int32_t num_features,
                        const mdl_table* tables, int32_t num_tables, int32_t max_dim,
                        uint32_t* sort_keys, uint32_t* sort_payload, int64_t n,
                        int32_t key_bits, const float* bag_count, float lr, float eps,
-                       void* workspace, size_t workspace_bytes, void* stream);
+                       void* workspace, size_t workspace_bytes, uint32_t classes,
+                         void* stream);
 
 /*
  * Coalesced sparse gradients, the autograd contract of src/optim.py:317-329 and
@@ -304,7 +322,7 @@ int mdl_backward_coalesce(const mdl_feature* feats, int32_t num_features,
                           int32_t key_bits, const float* bag_count,
                           const int64_t* unique_range, const uint64_t* rows_addr,
                           const uint64_t* values_addr, void* workspace,
-                          size_t workspace_bytes, void* stream);
+                          size_t workspace_bytes, uint32_t classes, void* stream);
 
 /* ------------------------------------------------------------- update --- */
 

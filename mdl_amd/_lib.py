@@ -85,7 +85,9 @@ SIGNATURES: dict[str, tuple] = {
     "mdl_offsets_workspace_bytes": (_SZ, [_I64]),
     "mdl_lengths_to_offsets": (_I32, [_P, _I64, _P, _P, _SZ, _P]),
     "mdl_plan_chunks": (_I64, [_P, _I32, _I32, _P, _I64]),
-    "mdl_forward": (_I32, [_P, _I32, _P, _I64, _P, _P, _P, _P, _U32, _P, _P, _P]),
+    "mdl_forward": (_I32, [_P, _I32, _P, _I64, _P, _P, _P, _P, _U32, _P, _P, _U32, _P]),
+    "mdl_feature_classes": (_U32, [_P, _I32]),
+    "mdl_table_classes": (_U32, [_P, _I32]),
     "mdl_sequence_forward": (
         _I32,
         [_P, _P, _P, _I64, _I64, _I64, _I32, _P, _P, _P, _P, _U32, _P, _P],
@@ -98,17 +100,17 @@ SIGNATURES: dict[str, tuple] = {
     "mdl_backward_workspace_bytes": (_SZ, [_I64, _I32, _I32]),
     "mdl_backward_adagrad": (
         _I32,
-        [_P, _I32, _P, _I32, _I32, _P, _P, _I64, _I32, _P, _F, _F, _P, _SZ, _P],
+        [_P, _I32, _P, _I32, _I32, _P, _P, _I64, _I32, _P, _F, _F, _P, _SZ, _U32, _P],
     ),
     "mdl_backward_sort": (_I32, [_P, _I32, _I32, _P, _P, _I64, _I32, _P, _SZ, _P]),
     "mdl_backward_apply": (
         _I32,
-        [_P, _I32, _P, _I32, _I32, _P, _P, _I64, _I32, _P, _F, _F, _P, _SZ, _P],
+        [_P, _I32, _P, _I32, _I32, _P, _P, _I64, _I32, _P, _F, _F, _P, _SZ, _U32, _P],
     ),
     "mdl_backward_count": (_I32, [_P, _I32, _I32, _P, _P, _I64, _I32, _P, _P, _SZ, _P]),
     "mdl_backward_coalesce": (
         _I32,
-        [_P, _I32, _P, _I32, _I32, _P, _P, _I64, _I32, _P, _P, _P, _P, _P, _SZ, _P],
+        [_P, _I32, _P, _I32, _I32, _P, _P, _I64, _I32, _P, _P, _P, _P, _P, _SZ, _U32, _P],
     ),
     "mdl_rowwise_adagrad": (
         _I32,

@@ -21,7 +21,7 @@ int sort_pairs(uint32_t* keys, uint32_t* vals, uint32_t* keys_alt, uint32_t* val
                int key_bits, void* ws, size_t ws_bytes, int* in_alt, hipStream_t s);
 size_t sort_ws_bytes(int64_t n);
 
-constexpr int kChunkMax = 1024;
+constexpr int kChunkMax = 512;
 constexpr int kBwdWaves = 4;
 constexpr int kPlanThreads = 1024;
 
@@ -94,8 +94,7 @@ __device__ __forceinline__ int64_t lower_bound_u32(const uint32_t* a, int64_t n,
 // lays out alike) use 16-byte vectors, and the chunk length that gives one
 // wave kPassesPerChunk passes over it.
 __device__ __forceinline__ bool table_vec(const mdl_table& tb) {
-  const int wsz = tb.wdtype == MDL_BF16 ? 2 : 4;
-  return (tb.weight % 16 == 0) && ((int64_t)tb.dim * wsz) % 16 == 0;
+  return table_vec_of(tb.weight, tb.dim, tb.wdtype);
 }
 
 __device__ __forceinline__ int64_t table_chunk_len(const mdl_table& tb) {
@@ -265,7 +264,7 @@ __device__ __forceinline__ int32_t feature_of(const BwdArgs& a, int32_t single, 
   return lo;
 }
 
-template <typename TW, typename TG, int C>
+template <int kMode, typename TW, typename TG, int C>
 struct Reducer {
   const BwdArgs& a;
   int32_t t;
@@ -332,13 +331,13 @@ struct Reducer {
   __device__ __forceinline__ void finish(uint32_t key, const float (&v)[C], float ss, float acc0, float (&w)[C],
                                          int64_t uidx) const {
     const int64_t row = (int64_t)key - row_base;
-    if (a.mode == kModeAdagrad) {
+    if (kMode == kModeAdagrad) {
       const float acc = acc0 + ss / (float)dim;
       if (sub == 0) state[row] = acc;
-      const float den = sqrtf(acc) + a.eps;
+      const float inv = 1.f / (sqrtf(acc) + a.eps);
       if (col_ok) {
 #pragma unroll
-        for (int k = 0; k < C; ++k) w[k] = w[k] - a.lr * (v[k] / den);
+        for (int k = 0; k < C; ++k) w[k] = w[k] - a.lr * (v[k] * inv);
         RowIO<TW, C>::store(W + row * dim + col, w);
       }
     } else {
@@ -351,22 +350,28 @@ struct Reducer {
   }
 };
 
-template <typename TW, typename TG, int C>
-__device__ __forceinline__ void reduce_chunk(const BwdArgs& a, int64_t c, const ChunkRange& r) {
+// Keys and payloads of the chunk a wave reduces, staged in LDS: entry i of
+// the chunk is s_key[i + 1]; s_key[0] and s_key[len + 1] hold the keys just
+// before and after the chunk inside its table (kNone at a table edge).
+struct ChunkStage {
+  uint32_t key[kChunkMax + 2];
+  uint32_t pay[kChunkMax];
+};
+
+template <int kMode, bool kOneFeature, typename TW, typename TG, int C>
+__device__ __forceinline__ void reduce_chunk_body(const BwdArgs& a, int64_t c, const ChunkRange& r,
+                                                  const Reducer<kMode, TW, TG, C>& R, const ChunkStage& st) {
   // Pass groups per iteration: 16 columns of loads in flight per lane.
   constexpr int U = C >= 8 ? 2 : 4;
-  Reducer<TW, TG, C> R(a, r.t);
-  if (R.dim > kWave * C) return;  // rejected on the host; never reached
+  constexpr bool adagrad = kMode == kModeAdagrad;
+  constexpr bool coalesce = !adagrad;
   const int lane = lane_id();
-  const uint32_t* keys = a.keys;
-  const bool adagrad = a.mode == kModeAdagrad;
-  const bool coalesce = !adagrad;
-  const bool head_open = r.c_begin > r.t_begin && keys[r.c_begin - 1] == keys[r.c_begin];
-  const bool tail_open = r.c_end < r.t_end && keys[r.c_end] == keys[r.c_end - 1];
-  const uint32_t first_key = keys[r.c_begin];
-  const uint32_t last_key = keys[r.c_end - 1];
-  const bool single = head_open && tail_open && first_key == last_key;
   const uint32_t kNone = 0xffffffffu;
+  const int len = (int)(r.c_end - r.c_begin);
+  const bool head_open = st.key[0] == st.key[1];
+  const bool tail_open = st.key[len + 1] == st.key[len];
+  const uint32_t first_key = st.key[1];
+  const bool single = head_open && tail_open && first_key == st.key[len];
   const uint64_t lt_mask = (lane == 0) ? 0ull : (~0ull >> (64 - lane));
   int64_t heads_before = coalesce ? a.head_base[c] : 0;
 
@@ -375,48 +380,39 @@ __device__ __forceinline__ void reduce_chunk(const BwdArgs& a, int64_t c, const 
   for (int k = 0; k < C; ++k) carry[k] = 0.f;
   uint32_t carry_key = kNone;
   const int G = R.G, L = R.L, slot = R.slot, sub = R.sub;
-  const int64_t step = (int64_t)G * U;
 
-  // keys, next keys, previous keys (coalesced layout only) and payloads of
-  // the next pass group, fetched one group ahead
-  uint32_t nk[U], nn[U], npv[U], np[U];
-  auto fetch = [&](int64_t base) {
-#pragma unroll
-    for (int u = 0; u < U; ++u) {
-      const int64_t e = base + (int64_t)u * G + slot;
-      const bool valid = e < r.c_end;
-      nk[u] = valid ? keys[e] : kNone;
-      nn[u] = (valid && e + 1 < r.c_end) ? keys[e + 1] : kNone;
-      npv[u] = (coalesce && valid && e > r.c_begin) ? keys[e - 1] : kNone;
-      np[u] = valid ? a.vals[e] : 0u;
-    }
-  };
-  fetch(r.c_begin);
-
-  for (int64_t base = r.c_begin; base < r.c_end; base += step) {
+  for (int base = 0; base < len; base += G * U) {
     float v[U][C], w[U][C], acc0[U], cnt[U];
     uint32_t key[U], pay[U];
     bool fin[U], head[U], own[U], mean[U];
     const TG* gp[U];
 #pragma unroll
     for (int u = 0; u < U; ++u) {
-      const int64_t e = base + (int64_t)u * G + slot;
-      const bool valid = e < r.c_end;
-      key[u] = nk[u];
-      pay[u] = np[u];
-      fin[u] = valid && ((e + 1 == r.c_end) ? !tail_open : nn[u] != key[u]);
-      head[u] = coalesce && valid && (e == r.t_begin || (e > r.c_begin ? npv[u] != key[u] : !head_open));
+      const int i = base + u * G + slot;
+      const bool valid = i < len;
+      const int ii = valid ? i : 0;
+      key[u] = valid ? st.key[ii + 1] : kNone;
+      pay[u] = st.pay[ii];
+      const uint32_t next = st.key[ii + 2];
+      fin[u] = valid && next != key[u];
+      head[u] = coalesce && valid && st.key[ii] != key[u] &&
+                (i > 0 || r.c_begin == r.t_begin || !head_open);
+      if (coalesce && valid && i == 0 && r.c_begin == r.t_begin) head[u] = true;
       own[u] = fin[u] && !(head_open && key[u] == first_key);  // the run finishes in this chunk
-      mean[u] = false;
-      gp[u] = valid && R.col_ok ? R.grad_row(pay[u], mean[u]) + R.col : zero_row<TG>();
+      if (kOneFeature) {
+        mean[u] = R.g_mean;
+        gp[u] = valid && R.col_ok ? R.g_base + ((int64_t)pay[u] - R.pbase) * R.g_stride + R.col : zero_row<TG>();
+      } else {
+        mean[u] = false;
+        gp[u] = valid && R.col_ok ? R.grad_row(pay[u], mean[u]) + R.col : zero_row<TG>();
+      }
     }
-    // Every load of the group, back to back: gradient rows, bag counts and,
-    // for runs that finish here, the weight row and its accumulator.
+    // Every global load of the group, back to back: gradient rows, bag
+    // counts and, for runs that finish here, the weight row and accumulator.
 #pragma unroll
     for (int u = 0; u < U; ++u) {
       RowIO<TG, C>::load(gp[u], v[u]);
-      const float* cp = mean[u] ? a.bag_count + pay[u] : zero_row<float>();
-      cnt[u] = *cp;
+      cnt[u] = *(mean[u] ? a.bag_count + pay[u] : zero_row<float>());
       if (adagrad) {
         const int64_t row = (int64_t)key[u] - R.row_base;
         RowIO<TW, C>::load(own[u] && R.col_ok ? R.W + row * R.dim + R.col : zero_row<TW>(), w[u]);
@@ -427,14 +423,11 @@ __device__ __forceinline__ void reduce_chunk(const BwdArgs& a, int64_t c, const 
         acc0[u] = 0.f;
       }
     }
-    fetch(base + step);
 #pragma unroll
     for (int u = 0; u < U; ++u) {
-      if (mean[u] && cnt[u] != 1.f) {
-        const float den = fmaxf(cnt[u], 1.f);
+      const float inv = mean[u] ? 1.f / fmaxf(cnt[u], 1.f) : 1.f;
 #pragma unroll
-        for (int k = 0; k < C; ++k) v[u][k] = v[u][k] / den;
-      }
+      for (int k = 0; k < C; ++k) v[u][k] *= inv;
     }
 #pragma unroll
     for (int u = 0; u < U; ++u) {
@@ -488,11 +481,32 @@ __device__ __forceinline__ void reduce_chunk(const BwdArgs& a, int64_t c, const 
   if (lane == 0) a.chunk_flags[c] = (head_open ? kHeadOpen : 0) | (tail_open ? kTailOpen : 0) | (single ? kSingle : 0);
 }
 
-template <typename TW, typename TG, int C>
+template <int kMode, typename TW, typename TG, int C>
+__device__ __forceinline__ void reduce_chunk(const BwdArgs& a, int64_t c, const ChunkRange& r, ChunkStage& st) {
+  Reducer<kMode, TW, TG, C> R(a, r.t);
+  if (R.dim > kWave * C) return;  // rejected on the host; never reached
+  const int lane = lane_id();
+  const uint32_t kNone = 0xffffffffu;
+  const int len = (int)(r.c_end - r.c_begin);
+  for (int i = lane; i < len; i += kWave) {
+    st.key[i + 1] = a.keys[r.c_begin + i];
+    st.pay[i] = a.vals[r.c_begin + i];
+  }
+  if (lane == 0) {
+    st.key[0] = r.c_begin > r.t_begin ? a.keys[r.c_begin - 1] : kNone;
+    st.key[len + 1] = r.c_end < r.t_end ? a.keys[r.c_end] : kNone;
+  }
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
+  if (R.single >= 0) reduce_chunk_body<kMode, true, TW, TG, C>(a, c, r, R, st);
+  else reduce_chunk_body<kMode, false, TW, TG, C>(a, c, r, R, st);
+}
+
+template <int kMode, typename TW, typename TG, int C>
 __device__ __forceinline__ void fixup_chunk(const BwdArgs& a, int64_t c, const ChunkRange& r) {
   const int32_t flags = __builtin_amdgcn_readfirstlane(a.chunk_flags[c]);
   if (!(flags & kHeadOpen) || (flags & kSingle)) return;
-  Reducer<TW, TG, C> R(a, r.t);
+  Reducer<kMode, TW, TG, C> R(a, r.t);
   if (R.dim > kWave * C) return;  // rejected on the host; never reached
   // Walk back over chunks that lie wholly inside the run to the chunk holding
   // its first entry (never past the table's first chunk).
@@ -530,12 +544,12 @@ __device__ __forceinline__ void fixup_chunk(const BwdArgs& a, int64_t c, const C
   }
   const float ss = R.row_sumsq(v);
   const uint32_t key = a.keys[r.c_begin];
-  const int64_t uidx = a.mode == kModeCoalesce ? a.head_base[c] - 1 : 0;
+  const int64_t uidx = kMode == kModeCoalesce ? a.head_base[c] - 1 : 0;
   float w[C];
   float acc0 = 0.f;
 #pragma unroll
   for (int k = 0; k < C; ++k) w[k] = 0.f;
-  if (a.mode == kModeAdagrad && R.slot == 0) {
+  if (kMode == kModeAdagrad && R.slot == 0) {
     const int64_t row = (int64_t)key - R.row_base;
     if (R.col_ok) RowIO<TW, C>::load(R.W + row * R.dim + R.col, w);
     acc0 = R.state[row];
@@ -543,7 +557,7 @@ __device__ __forceinline__ void fixup_chunk(const BwdArgs& a, int64_t c, const C
   if (R.slot == 0) R.finish(key, v, ss, acc0, w, uidx);
 }
 
-template <bool kFixup>
+template <bool kFixup, int kMode, typename TW, typename TG, int C>
 __global__ __launch_bounds__(kBwdWaves * kWave) void bwd_reduce_kernel(BwdArgs a) {
   const int w = threadIdx.x / kWave;
   // The grid covers the worst-case chunk count; only the first `real` blocks
@@ -558,22 +572,14 @@ __global__ __launch_bounds__(kBwdWaves * kWave) void bwd_reduce_kernel(BwdArgs a
   ChunkRange r;
   if (!find_chunk(c, a.T, a.chunk_base, a.table_start, a.table_end, a.table_cb, &r)) return;
   const mdl_table& tb = a.tables[r.t];
-  const int wdtype = __builtin_amdgcn_readfirstlane(tb.wdtype);
-  const int dim = __builtin_amdgcn_readfirstlane(tb.dim);
-  const int gdtype = __builtin_amdgcn_readfirstlane(tb.gdtype);
-  const int wsz = wdtype == MDL_BF16 ? 2 : 4;
-  // Vector path when every row of the table (weights, gradients, values) is
-  // 16-byte aligned; the host checks gradients and values.
-  const bool vec = ((uint64_t)tb.weight % 16 == 0) && ((int64_t)dim * wsz) % 16 == 0;
-  if (wdtype == MDL_F32) {
-    if (vec) { if (kFixup) fixup_chunk<float, float, 4>(a, c, r); else reduce_chunk<float, float, 4>(a, c, r); }
-    else { if (kFixup) fixup_chunk<float, float, 1>(a, c, r); else reduce_chunk<float, float, 1>(a, c, r); }
-  } else if (gdtype == MDL_BF16) {
-    if (vec) { if (kFixup) fixup_chunk<bf16_t, bf16_t, 8>(a, c, r); else reduce_chunk<bf16_t, bf16_t, 8>(a, c, r); }
-    else { if (kFixup) fixup_chunk<bf16_t, bf16_t, 1>(a, c, r); else reduce_chunk<bf16_t, bf16_t, 1>(a, c, r); }
+  const int cls = row_class(__builtin_amdgcn_readfirstlane(tb.wdtype), __builtin_amdgcn_readfirstlane(tb.gdtype),
+                            table_vec(tb));
+  if (cls != ClassOf<TW, TG, C>::value) return;  // another class's launch owns it
+  if (kFixup) {
+    fixup_chunk<kMode, TW, TG, C>(a, c, r);
   } else {
-    if (vec) { if (kFixup) fixup_chunk<bf16_t, float, 8>(a, c, r); else reduce_chunk<bf16_t, float, 8>(a, c, r); }
-    else { if (kFixup) fixup_chunk<bf16_t, float, 1>(a, c, r); else reduce_chunk<bf16_t, float, 1>(a, c, r); }
+    __shared__ ChunkStage stage[kBwdWaves];
+    reduce_chunk<kMode, TW, TG, C>(a, c, r, stage[w]);
   }
 }
 
@@ -630,13 +636,37 @@ static void fill_args(BwdArgs* a, const mdl_feature* feats, int32_t F, const mdl
   a->unique_range = nullptr;
 }
 
-static int run_reduce(const BwdArgs& a, hipStream_t s) {
+template <bool kFixup, typename TW, typename TG, int C>
+static int launch_reduce(const BwdArgs& a, uint32_t classes, hipStream_t s) {
+  if (classes != 0 && !(classes & (1u << ClassOf<TW, TG, C>::value))) return MDL_OK;
   const int64_t blocks = (a.max_chunks + kBwdWaves - 1) / kBwdWaves;
-  hipLaunchKernelGGL(bwd_reduce_kernel<false>, dim3((unsigned)blocks), dim3(kBwdWaves * kWave), 0, s, a);
-  MDL_CHECK_LAUNCH("bwd_reduce_kernel");
-  hipLaunchKernelGGL(bwd_reduce_kernel<true>, dim3((unsigned)blocks), dim3(kBwdWaves * kWave), 0, s, a);
-  MDL_CHECK_LAUNCH("bwd_fixup_kernel");
+  if (a.mode == kModeAdagrad)
+    hipLaunchKernelGGL((bwd_reduce_kernel<kFixup, kModeAdagrad, TW, TG, C>), dim3((unsigned)blocks),
+                       dim3(kBwdWaves * kWave), 0, s, a);
+  else
+    hipLaunchKernelGGL((bwd_reduce_kernel<kFixup, kModeCoalesce, TW, TG, C>), dim3((unsigned)blocks),
+                       dim3(kBwdWaves * kWave), 0, s, a);
+  MDL_CHECK_LAUNCH(kFixup ? "bwd_fixup_kernel" : "bwd_reduce_kernel");
   return MDL_OK;
+}
+
+template <bool kFixup>
+static int launch_all(const BwdArgs& a, uint32_t classes, hipStream_t s) {
+  int rc = launch_reduce<kFixup, float, float, 4>(a, classes, s);
+  if (!rc) rc = launch_reduce<kFixup, float, float, 1>(a, classes, s);
+  if (!rc) rc = launch_reduce<kFixup, bf16_t, bf16_t, 8>(a, classes, s);
+  if (!rc) rc = launch_reduce<kFixup, bf16_t, bf16_t, 1>(a, classes, s);
+  if (!rc) rc = launch_reduce<kFixup, bf16_t, float, 8>(a, classes, s);
+  if (!rc) rc = launch_reduce<kFixup, bf16_t, float, 1>(a, classes, s);
+  return rc;
+}
+
+// Every reduce launch (all classes) before any fix-up launch: a fix-up reads
+// partials that the reduce of the same table wrote.
+static int run_reduce(const BwdArgs& a, uint32_t classes, hipStream_t s) {
+  int rc = launch_all<false>(a, classes, s);
+  if (!rc) rc = launch_all<true>(a, classes, s);
+  return rc;
 }
 
 }  // namespace mdl
@@ -656,6 +686,15 @@ int mdl_sparse_keys(const int64_t* ids, int64_t n, int64_t num_rows, int64_t row
                      row_base, payload_base, padding_idx, keys, payload, sentinel, error_count);
   MDL_CHECK_LAUNCH("sparse_keys_kernel");
   return MDL_OK;
+}
+
+uint32_t mdl_table_classes(const mdl_table* tables, int32_t num_tables) {
+  uint32_t m = 0;
+  for (int32_t i = 0; i < num_tables; ++i) {
+    const mdl_table& t = tables[i];
+    m |= 1u << row_class(t.wdtype, t.gdtype, table_vec_of(t.weight, t.dim, t.wdtype));
+  }
+  return m;
 }
 
 size_t mdl_backward_workspace_bytes(int64_t n, int32_t num_tables, int32_t max_dim) {
@@ -682,7 +721,7 @@ int mdl_backward_sort(const mdl_table* tables, int32_t num_tables, int32_t max_d
 int mdl_backward_apply(const mdl_feature* feats, int32_t num_features, const mdl_table* tables,
                        int32_t num_tables, int32_t max_dim, uint32_t* sort_keys, uint32_t* sort_payload,
                        int64_t n, int32_t key_bits, const float* bag_count, float lr, float eps,
-                       void* workspace, size_t workspace_bytes, void* stream) {
+                       void* workspace, size_t workspace_bytes, uint32_t classes, void* stream) {
   int rc = validate_tables("mdl_backward_apply", num_tables, max_dim, n);
   if (rc) return rc;
   if (n == 0) return MDL_OK;
@@ -697,18 +736,18 @@ int mdl_backward_apply(const mdl_feature* feats, int32_t num_features, const mdl
   a.lr = lr;
   a.eps = eps;
   a.mode = kModeAdagrad;
-  return run_reduce(a, as_stream(stream));
+  return run_reduce(a, classes, as_stream(stream));
 }
 
 int mdl_backward_adagrad(const mdl_feature* feats, int32_t num_features, const mdl_table* tables,
                          int32_t num_tables, int32_t max_dim, uint32_t* sort_keys, uint32_t* sort_payload,
                          int64_t n, int32_t key_bits, const float* bag_count, float lr, float eps,
-                         void* workspace, size_t workspace_bytes, void* stream) {
+                         void* workspace, size_t workspace_bytes, uint32_t classes, void* stream) {
   int rc = mdl_backward_sort(tables, num_tables, max_dim, sort_keys, sort_payload, n, key_bits, workspace,
                              workspace_bytes, stream);
   if (rc) return rc;
   return mdl_backward_apply(feats, num_features, tables, num_tables, max_dim, sort_keys, sort_payload, n,
-                            key_bits, bag_count, lr, eps, workspace, workspace_bytes, stream);
+                            key_bits, bag_count, lr, eps, workspace, workspace_bytes, classes, stream);
 }
 
 int mdl_backward_count(const mdl_table* tables, int32_t num_tables, int32_t max_dim, uint32_t* sort_keys,
@@ -744,7 +783,7 @@ int mdl_backward_coalesce(const mdl_feature* feats, int32_t num_features, const 
                           int32_t num_tables, int32_t max_dim, uint32_t* sort_keys, uint32_t* sort_payload,
                           int64_t n, int32_t key_bits, const float* bag_count, const int64_t* unique_range,
                           const uint64_t* rows_addr, const uint64_t* values_addr, void* workspace,
-                          size_t workspace_bytes, void* stream) {
+                          size_t workspace_bytes, uint32_t classes, void* stream) {
   int rc = validate_tables("mdl_backward_coalesce", num_tables, max_dim, n);
   if (rc) return rc;
   if (n == 0) return MDL_OK;
@@ -761,7 +800,7 @@ int mdl_backward_coalesce(const mdl_feature* feats, int32_t num_features, const 
   a.rows_addr = rows_addr;
   a.values_addr = values_addr;
   a.unique_range = unique_range;
-  return run_reduce(a, s);
+  return run_reduce(a, classes, s);
 }
 
 }  // extern "C"

@@ -127,6 +127,45 @@ __device__ __forceinline__ const T* zero_row() {
 // kPassesPerChunk passes.
 constexpr int kPassesPerChunk = 32;
 
+// ------------------------------------------------------- row-access classes --
+//
+// Weight dtype x output/gradient dtype x 16-byte vectors or scalars.  Every
+// kernel that moves rows is instantiated once per class and launched only
+// for the classes present, so one launch never carries the registers of six
+// code paths.
+
+template <typename TW, typename TO, int C>
+struct ClassOf;
+template <> struct ClassOf<float, float, 4> { static constexpr int value = MDL_CLASS_F32_VEC; };
+template <> struct ClassOf<float, float, 1> { static constexpr int value = MDL_CLASS_F32; };
+template <> struct ClassOf<bf16_t, bf16_t, 8> { static constexpr int value = MDL_CLASS_BF16_VEC; };
+template <> struct ClassOf<bf16_t, bf16_t, 1> { static constexpr int value = MDL_CLASS_BF16; };
+template <> struct ClassOf<bf16_t, float, 8> { static constexpr int value = MDL_CLASS_BF16_F32_VEC; };
+template <> struct ClassOf<bf16_t, float, 1> { static constexpr int value = MDL_CLASS_BF16_F32; };
+
+__host__ __device__ __forceinline__ int row_class(int wdtype, int odtype, bool vec) {
+  const int base = wdtype == MDL_F32 ? MDL_CLASS_F32_VEC
+                   : (odtype == MDL_BF16 ? MDL_CLASS_BF16_VEC : MDL_CLASS_BF16_F32_VEC);
+  return base + (vec ? 0 : 1);
+}
+
+// Whether a feature's weight, output and gradient rows allow 16-byte lanes.
+__host__ __device__ __forceinline__ bool feature_vec(uint64_t weight, uint64_t out, int64_t dim,
+                                                     int64_t out_stride, int wdtype, int odtype) {
+  const int wsz = wdtype == MDL_BF16 ? 2 : 4;
+  const int osz = odtype == MDL_BF16 ? 2 : 4;
+  const int c = 16 / wsz;
+  return weight % 16 == 0 && out % 16 == 0 && (dim * wsz) % 16 == 0 && (out_stride * osz) % 16 == 0 &&
+         ((int64_t)c * osz) % 16 == 0;
+}
+
+// Whether a table's rows (and its gradient/value rows, laid out alike by
+// the caller) allow 16-byte lanes.
+__host__ __device__ __forceinline__ bool table_vec_of(uint64_t weight, int64_t dim, int wdtype) {
+  const int wsz = wdtype == MDL_BF16 ? 2 : 4;
+  return weight % 16 == 0 && (dim * wsz) % 16 == 0;
+}
+
 // ------------------------------------------------------------ wave helpers --
 
 __device__ __forceinline__ int lane_id() { return (int)(threadIdx.x & (kWave - 1)); }

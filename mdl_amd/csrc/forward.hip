@@ -70,14 +70,9 @@ __device__ __forceinline__ Feat load_feat(const mdl_feature* p) {
   return f;
 }
 
-// Whether every row access of the feature can use 16-byte vectors.
-__device__ __forceinline__ bool vec_ok(const Feat& f) {
-  const int wsz = f.wdtype == MDL_BF16 ? 2 : 4;
-  const int osz = f.odtype == MDL_BF16 ? 2 : 4;
-  const int c = 16 / wsz;
-  return ((uint64_t)f.weight % 16 == 0) && ((uint64_t)f.out % 16 == 0) &&
-         ((int64_t)f.dim * wsz) % 16 == 0 && (f.out_stride * osz) % 16 == 0 &&
-         ((int64_t)c * osz) % 16 == 0;
+__device__ __forceinline__ int feat_class(const Feat& f) {
+  return row_class(f.wdtype, f.odtype,
+                   feature_vec((uint64_t)f.weight, (uint64_t)f.out, f.dim, f.out_stride, f.wdtype, f.odtype));
 }
 
 __device__ __forceinline__ void wave_sync() { __builtin_amdgcn_wave_barrier(); __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront"); }
@@ -258,9 +253,9 @@ __device__ __forceinline__ void pooled_chunk(const Feat& f, int64_t first_bag, i
           const int64_t b = first_bag + seg[u];
           if (col_ok) {
             float r[C];
-            const float den = fmaxf(wt[u], 1.f);
+            const float inv = mean ? 1.f / fmaxf(wt[u], 1.f) : 1.f;
 #pragma unroll
-            for (int k = 0; k < C; ++k) r[k] = mean ? v[u][k] / den : v[u][k];
+            for (int k = 0; k < C; ++k) r[k] = v[u][k] * inv;
             RowIO<TO, C>::store(out + b * f.out_stride + col, r);
           }
           if (cb == 0 && sub == 0 && a.bag_count != nullptr) a.bag_count[f.payload_base + b] = wt[u];
@@ -299,6 +294,7 @@ __device__ __forceinline__ void run_chunk(const Feat& f, const mdl_chunk& ch, in
     pooled_chunk<TW, TO, C>(f, ch.first, ch.count, s_off, a);
 }
 
+template <typename TW, typename TO, int C>
 __global__ __launch_bounds__(kFwdWaves * kWave) void forward_kernel(FwdArgs a) {
   __shared__ int64_t s_off[kFwdWaves][kMaxBagsPerChunk + 1];
   const int w = threadIdx.x / kWave;
@@ -310,21 +306,20 @@ __global__ __launch_bounds__(kFwdWaves * kWave) void forward_kernel(FwdArgs a) {
   ch.count = uni32(a.chunks[c].count);
   ch.first = uni64(a.chunks[c].first);
   const Feat f = load_feat(a.feats + ch.feature);
+  if (feat_class(f) != ClassOf<TW, TO, C>::value) return;  // another class's launch owns it
   if (f.pooling != MDL_POOL_NONE && (ch.count > kMaxBagsPerChunk || ch.count < 0)) {
     if (lane_id() == 0 && a.error_count) atomicAdd(a.error_count, 1);
     return;
   }
-  const bool v = vec_ok(f);
-  if (f.wdtype == MDL_F32) {
-    if (v) run_chunk<float, float, 4>(f, ch, s_off[w], a);
-    else run_chunk<float, float, 1>(f, ch, s_off[w], a);
-  } else if (f.odtype == MDL_BF16) {
-    if (v) run_chunk<bf16_t, bf16_t, 8>(f, ch, s_off[w], a);
-    else run_chunk<bf16_t, bf16_t, 1>(f, ch, s_off[w], a);
-  } else {
-    if (v) run_chunk<bf16_t, float, 8>(f, ch, s_off[w], a);
-    else run_chunk<bf16_t, float, 1>(f, ch, s_off[w], a);
-  }
+  run_chunk<TW, TO, C>(f, ch, s_off[w], a);
+}
+
+template <typename TW, typename TO, int C>
+static int launch_forward(const FwdArgs& a, uint32_t classes, int64_t blocks, hipStream_t s) {
+  if (classes != 0 && !(classes & (1u << ClassOf<TW, TO, C>::value))) return MDL_OK;
+  hipLaunchKernelGGL((forward_kernel<TW, TO, C>), dim3((unsigned)blocks), dim3(kFwdWaves * kWave), 0, s, a);
+  MDL_CHECK_LAUNCH("forward_kernel");
+  return MDL_OK;
 }
 
 // ------------------------------------------------------------ sequences --
@@ -446,6 +441,16 @@ using namespace mdl;
 
 extern "C" {
 
+uint32_t mdl_feature_classes(const mdl_feature* feats, int32_t num_features) {
+  uint32_t m = 0;
+  for (int32_t i = 0; i < num_features; ++i) {
+    const mdl_feature& f = feats[i];
+    m |= 1u << row_class(f.wdtype, f.odtype,
+                         feature_vec(f.weight, f.out, f.dim, f.out_stride, f.wdtype, f.odtype));
+  }
+  return m;
+}
+
 int64_t mdl_plan_chunks(const mdl_feature* feats, int32_t num_features, int32_t target_ids,
                         mdl_chunk* chunks, int64_t capacity) {
   if (num_features < 0 || target_ids <= 0) return fail(MDL_ERR_INVALID, "mdl_plan_chunks: bad arguments");
@@ -455,11 +460,8 @@ int64_t mdl_plan_chunks(const mdl_feature* feats, int32_t num_features, int32_t 
     // Rows a wave gathers per pass (same lane layout as the kernel): chunks
     // hold about kPassesPerChunk passes, so no wave walks a long serial chain
     // of dependent loads, whatever the row width.
-    const int wsz = f.wdtype == MDL_BF16 ? 2 : 4;
-    const int osz = f.odtype == MDL_BF16 ? 2 : 4;
-    const int c = 16 / wsz;
-    const bool vec = f.weight % 16 == 0 && f.out % 16 == 0 && ((int64_t)f.dim * wsz) % 16 == 0 &&
-                     (f.out_stride * osz) % 16 == 0 && ((int64_t)c * osz) % 16 == 0;
+    const int c = f.wdtype == MDL_BF16 ? 8 : 4;
+    const bool vec = feature_vec(f.weight, f.out, f.dim, f.out_stride, f.wdtype, f.odtype);
     const int lanes = lanes_for(f.dim > 0 ? f.dim : 1, vec ? c : 1);
     const int64_t per_pass = kWave / lanes;
     int64_t target = (int64_t)kPassesPerChunk * per_pass;
@@ -493,7 +495,7 @@ int64_t mdl_plan_chunks(const mdl_feature* feats, int32_t num_features, int32_t 
 int mdl_forward(const mdl_feature* feats, int32_t num_features, const mdl_chunk* chunks,
                 int64_t num_chunks, const int64_t* ids, const int64_t* offsets, uint32_t* sort_keys,
                 uint32_t* sort_payload, uint32_t sentinel, float* bag_count, int32_t* error_count,
-                void* stream) {
+                uint32_t classes, void* stream) {
   if (num_features < 0 || num_chunks < 0) return fail(MDL_ERR_INVALID, "mdl_forward: negative count");
   if (num_chunks == 0) return MDL_OK;
   if (!feats || !chunks || !ids) return fail(MDL_ERR_INVALID, "mdl_forward: null pointer");
@@ -512,10 +514,14 @@ int mdl_forward(const mdl_feature* feats, int32_t num_features, const mdl_chunk*
   a.sentinel = sentinel;
   const int64_t blocks = (num_chunks + kFwdWaves - 1) / kFwdWaves;
   if (blocks > 0x7fffffff) return fail(MDL_ERR_UNSUPPORTED, "mdl_forward: too many chunks");
-  hipLaunchKernelGGL(forward_kernel, dim3((unsigned)blocks), dim3(kFwdWaves * kWave), 0,
-                     as_stream(stream), a);
-  MDL_CHECK_LAUNCH("forward_kernel");
-  return MDL_OK;
+  hipStream_t s = as_stream(stream);
+  int rc = launch_forward<float, float, 4>(a, classes, blocks, s);
+  if (!rc) rc = launch_forward<float, float, 1>(a, classes, blocks, s);
+  if (!rc) rc = launch_forward<bf16_t, bf16_t, 8>(a, classes, blocks, s);
+  if (!rc) rc = launch_forward<bf16_t, bf16_t, 1>(a, classes, blocks, s);
+  if (!rc) rc = launch_forward<bf16_t, float, 8>(a, classes, blocks, s);
+  if (!rc) rc = launch_forward<bf16_t, float, 1>(a, classes, blocks, s);
+  return rc;
 }
 
 int mdl_sequence_forward(const mdl_feature* feature, const int64_t* ids, const int64_t* lengths,

@@ -460,7 +460,7 @@ def forward_packed(
         lib().mdl_forward(
             feats_dev.data_ptr(), len(feats), chunks_dev.data_ptr(), n_chunks, all_ids.data_ptr(),
             _ptr(offsets), _ptr(keys), _ptr(payload), plan.sentinel, _ptr(bag_count),
-            error_count.data_ptr(), stream,
+            error_count.data_ptr(), feature_classes(feats), stream,
         ),
         "mdl_forward",
     )
@@ -532,6 +532,16 @@ def grouped_forward(
         plan, all_ids, offsets, id_counts, bag_counts, outputs,
         with_backward=with_backward, error_count=error_count,
     )
+
+
+def feature_classes(feats: np.ndarray) -> int:
+    """Mask of the row-access classes present (which kernels to launch)."""
+
+    return int(lib().mdl_feature_classes(feats.ctypes.data, len(feats)))
+
+
+def table_classes(tables: np.ndarray) -> int:
+    return int(lib().mdl_table_classes(tables.ctypes.data, len(tables)))
 
 
 def _tables_array(plan: GroupPlan, feats: np.ndarray) -> np.ndarray:
@@ -615,7 +625,7 @@ def backward_adagrad(res: ForwardResult, grads: Sequence[Tensor | None], *, lr: 
         lib().mdl_backward_adagrad(
             feats_dev.data_ptr(), len(feats), tables_dev.data_ptr(), len(tables), plan.max_dim,
             res.keys.data_ptr(), res.payload.data_ptr(), n, plan.key_bits, _ptr(res.bag_count),
-            float(lr), float(eps), ws.data_ptr(), ws.numel(), _stream(device),
+            float(lr), float(eps), ws.data_ptr(), ws.numel(), table_classes(tables), _stream(device),
         ),
         "mdl_backward_adagrad",
     )
@@ -671,7 +681,7 @@ def backward_coalesce(res: ForwardResult, grads: Sequence[Tensor | None]) -> lis
                 feats_dev.data_ptr(), len(feats), tables_dev.data_ptr(), T, plan.max_dim,
                 res.keys.data_ptr(), res.payload.data_ptr(), n, plan.key_bits, _ptr(res.bag_count),
                 urange.data_ptr(), rows_dev.data_ptr(), vals_dev.data_ptr(), ws.data_ptr(), ws.numel(),
-                stream,
+                table_classes(tables), stream,
             ),
             "mdl_backward_coalesce",
         )
@@ -762,7 +772,7 @@ def coalesce_rows(
             lib().mdl_backward_coalesce(
                 feats_dev.data_ptr(), 1, tables_dev.data_ptr(), 1, dim, keys.data_ptr(), payload.data_ptr(),
                 n, plan.key_bits, None, urange.data_ptr(), rows_dev.data_ptr(), vals_dev.data_ptr(),
-                ws.data_ptr(), ws.numel(), stream,
+                ws.data_ptr(), ws.numel(), table_classes(tables), stream,
             ),
             "mdl_backward_coalesce",
         )

@@ -75,6 +75,8 @@ class SparseStep:
         )
         self.feats_bwd, self._grads = ops._attach_grads(res, grads)
         self.tables = ops._tables_array(plan, self.feats_bwd)
+        self.fwd_classes = ops.feature_classes(self.feats_fwd)
+        self.bwd_classes = ops.table_classes(self.tables)
         self.feats_fwd_dev = ops.upload(self.feats_fwd, self.device)
         self.chunks_dev = ops.upload(chunks, self.device)
         self.feats_bwd_dev = ops.upload(self.feats_bwd, self.device)
@@ -111,7 +113,7 @@ class SparseStep:
             lib().mdl_forward(
                 self.feats_fwd_dev.data_ptr(), len(self.feats_fwd), self.chunks_dev.data_ptr(), self.n_chunks,
                 self.ids.data_ptr(), ops._ptr(self.offsets), self.keys.data_ptr(), self.payload.data_ptr(),
-                self.plan.sentinel, ops._ptr(self.bag_count), self.error_count.data_ptr(), s,
+                self.plan.sentinel, ops._ptr(self.bag_count), self.error_count.data_ptr(), self.fwd_classes, s,
             ),
             "mdl_forward",
         )
@@ -136,7 +138,7 @@ class SparseStep:
                 self.feats_bwd_dev.data_ptr(), len(self.feats_bwd), self.tables_dev.data_ptr(), len(self.tables),
                 self.plan.max_dim, self.keys.data_ptr(), self.payload.data_ptr(), self.n, self.plan.key_bits,
                 ops._ptr(self.bag_count), float(lr), float(eps), self.ws.data_ptr(), self.ws.numel(),
-                self._stream(),
+                self.bwd_classes, self._stream(),
             ),
             "mdl_backward_apply",
         )
@@ -207,6 +209,7 @@ class SequenceStep:
             payload_base += int(B) * int(L_out)
         self.feats_bwd = np.concatenate(feats)
         self.tables = ops._tables_array(plan, self.feats_bwd)
+        self.bwd_classes = ops.table_classes(self.tables)
         self.feats_bwd_dev = ops.upload(self.feats_bwd, self.device)
         self.tables_dev = ops.upload(self.tables, self.device)
         self.ws = ops._workspace(
@@ -247,7 +250,8 @@ class SequenceStep:
             lib().mdl_backward_apply(
                 self.feats_bwd_dev.data_ptr(), len(self.feats_bwd), self.tables_dev.data_ptr(), len(self.tables),
                 self.plan.max_dim, self.keys.data_ptr(), self.payload.data_ptr(), self.n, self.plan.key_bits,
-                None, float(lr), float(eps), self.ws.data_ptr(), self.ws.numel(), self._stream(),
+                None, float(lr), float(eps), self.ws.data_ptr(), self.ws.numel(), self.bwd_classes,
+                self._stream(),
             ),
             "mdl_backward_apply",
         )

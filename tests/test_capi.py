@@ -86,13 +86,13 @@ def test_invalid_arguments_fail_before_any_launch():
     assert rc == -1 and b"key_bits" in lib.mdl_last_error()
     rc = lib.mdl_sort_pairs(None, None, None, None, 1 << 33, 8, None, 0, None, None)
     assert rc == -4
-    rc = lib.mdl_backward_adagrad(None, 0, None, 0, 8, None, None, 10, 8, None, 0.1, 1e-8, None, 0, None)
+    rc = lib.mdl_backward_adagrad(None, 0, None, 0, 8, None, None, 10, 8, None, 0.1, 1e-8, None, 0, 0, None)
     assert rc == -1 and b"table" in lib.mdl_last_error()
     rc = lib.mdl_rowwise_adagrad(None, _lib.MDL_F32, 10, 4, 4, None, None, 3, None, _lib.MDL_BF16, 4, 0.1,
                                  1e-8, None, None)
     assert rc == -1  # null pointers
     # zero-sized work is a no-op success without touching the device
-    assert lib.mdl_forward(None, 0, None, 0, None, None, None, None, 0, None, None, None) == 0
+    assert lib.mdl_forward(None, 0, None, 0, None, None, None, None, 0, None, None, 0, None) == 0
     assert lib.mdl_rowwise_adagrad(None, 0, 0, 4, 4, None, None, 0, None, 0, 4, 0.1, 1e-8, None, None) == 0
 
 
@@ -104,3 +104,22 @@ def test_workspace_queries_are_monotone():
     assert 0 < a < b < c
     assert lib.mdl_sort_workspace_bytes(1 << 20) >= 256 * 256 * 4
     assert lib.mdl_unique_workspace_bytes(1000) > 16 * 1000
+
+
+def test_class_masks_follow_dtype_and_alignment():
+    lib = _lib.lib()
+    feats = np.zeros(3, dtype=_lib.FEATURE_DTYPE)
+    feats["wdtype"] = [_lib.MDL_F32, _lib.MDL_BF16, _lib.MDL_BF16]
+    feats["odtype"] = [_lib.MDL_F32, _lib.MDL_BF16, _lib.MDL_F32]
+    feats["dim"] = [64, 64, 12]           # bf16 x 12 = 24 bytes: not 16-byte rows
+    feats["out_stride"] = [64, 64, 12]
+    feats["weight"] = [256, 512, 1024]
+    feats["out"] = [4096, 8192, 8196]
+    m = lib.mdl_feature_classes(feats.ctypes.data, 3)
+    assert m == (1 << 0) | (1 << 2) | (1 << 5)
+    tables = np.zeros(2, dtype=_lib.TABLE_DTYPE)
+    tables["wdtype"] = [_lib.MDL_F32, _lib.MDL_BF16]
+    tables["gdtype"] = [_lib.MDL_F32, _lib.MDL_BF16]
+    tables["dim"] = [3, 32]
+    tables["weight"] = [256, 512]
+    assert lib.mdl_table_classes(tables.ctypes.data, 2) == (1 << 1) | (1 << 2)
