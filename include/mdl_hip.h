@@ -42,8 +42,13 @@ enum { MDL_POOL_NONE = 0, MDL_POOL_SUM = 1, MDL_POOL_MEAN = 2 };
 
 /* Feature flags. EXCLUDE_NULL is the "exclude" null policy: ids equal to 0
  * carry weight 0 in the pooled sum and in the mean's denominator
- * (src/model.py:554-557); without it ("include_as_padding") every id counts. */
-enum { MDL_FLAG_EXCLUDE_NULL = 1 };
+ * (src/model.py:554-557); without it ("include_as_padding") every id counts.
+ * ROWS_BY_POSITION (pooled features only) pools rows that are already
+ * embedded: the row of id slot i is weight row i - ids_begin, whatever the id,
+ * and the ids only decide the null weights; this is _mean_pool_categorical_bag
+ * on its `embedded` input (src/model.py:509-570).  Such features emit no sort
+ * keys (sentinel) since they own no table. */
+enum { MDL_FLAG_EXCLUDE_NULL = 1, MDL_FLAG_ROWS_BY_POSITION = 2 };
 
 enum { MDL_BUCKET_PRE_HASHED = 0, MDL_BUCKET_MOD = 1 };
 
@@ -177,8 +182,9 @@ int64_t mdl_plan_chunks(const mdl_feature* feats_host, int32_t num_features,
  * with w_i = 0 for id 0 under MDL_FLAG_EXCLUDE_NULL and 1 otherwise; sums in
  * fp32, one rounding to odtype.  Empty bags give 0.  Ids outside
  * [0, num_rows) contribute 0 and are counted in *error_count (may be NULL);
- * so are bag offsets outside the feature's id range (clamped into it) and
- * pooled chunks of more than 256 bags (skipped).
+ * so are bag offsets outside the feature's id range (clamped into it),
+ * decreasing bag offsets and pooled chunks of more than 256 bags (skipped).
+ * Under MDL_FLAG_ROWS_BY_POSITION, weight[id_i] reads weight[i - ids_begin].
  *
  * When sort_keys is not NULL the call also writes, for every id position i of
  * every feature, the backward sort key and payload:
@@ -196,6 +202,29 @@ int mdl_forward(const mdl_feature* feats, int32_t num_features,
                 uint32_t* sort_keys, uint32_t* sort_payload, uint32_t sentinel,
                 float* bag_count, int32_t* error_count, uint32_t classes,
                 void* stream);
+
+/*
+ * Backward of bag pooling with respect to the pooled rows (the autograd of
+ * src/model.py:564-570 and :672-676): for every id position i of a pooled
+ * feature, in bag b,
+ *   weight[i - ids_begin] = out[b] * w_i / max(bag_count[payload_base + b], 1)  (MEAN)
+ *   weight[i - ids_begin] = out[b] * w_i                                         (SUM)
+ * computed in fp32 and rounded once.  In this call `out` is read (the
+ * upstream gradient of the pooled rows, odtype, row stride out_stride) and
+ * `weight` is written ([num_ids, dim], wdtype): the per-position gradient of
+ * the rows the forward pooled, i.e. the gradient of the `embedded` input of a
+ * MDL_FLAG_ROWS_BY_POSITION feature, or the uncoalesced COO values of the
+ * sparse embedding backward of a lookup feature.  Null weights w_i follow the
+ * forward (ids, flags and num_rows as the forward had them); bag_count
+ * (required) is what mdl_forward wrote
+ * for these features.  chunks come from mdl_plan_chunks over
+ * these descriptors and classes from mdl_feature_classes of them (0: all).
+ * MDL_POOL_NONE features are skipped.
+ */
+int mdl_pool_backward(const mdl_feature* feats, int32_t num_features,
+                      const mdl_chunk* chunks, int64_t num_chunks,
+                      const int64_t* ids, const int64_t* offsets,
+                      const float* bag_count, uint32_t classes, void* stream);
 
 /*
  * Sequence gather without pooling, right-aligned into a padded window
@@ -248,7 +277,7 @@ int mdl_unique(const int64_t* ids, int64_t n, int32_t key_bits, int64_t* unique_
  * mdl_forward / mdl_sequence_forward (n entries, keys < 2^key_bits; the
  * sentinel must be < 2^key_bits too).  It sorts them in place (keys/payload
  * and the workspace are clobbered), cuts the sorted array into chunks of
- * <= 1024 entries that never straddle two tables and reduces every run of
+ * <= 512 entries that never straddle two tables and reduces every run of
  * equal keys.  The num_tables tables (device array) are ordered by row_base,
  * cover every non-sentinel key, and their gradients are 16-byte aligned with
  * row strides that are multiples of 16 bytes whenever dim*sizeof(weight) is.
@@ -276,17 +305,20 @@ int mdl_sparse_keys(const int64_t* ids, int64_t n, int64_t num_rows, int64_t row
 
 /*
  * Fused backward + row-wise Adagrad: every distinct (table, row) is updated
- * once from its summed gradient g:
+ * once from its summed gradient g (times *grad_scale when grad_scale, a
+ * device float, is not NULL):
  *   acc += sum(g^2)/dim;  w = w - lr * (g / (sqrt(acc) + eps))
  * rounded once to the weight dtype (round-to-nearest-even for bf16).
- * Semantics of src/optim.py:31-62 (Triton kernel) and :299-357 (step).
+ * Semantics of src/optim.py:31-62 (Triton kernel) and :299-357 (step); the
+ * scale is the clip coefficient of src/train.py:5788-5826 applied to the
+ * coalesced gradient before the step.
  */
 int mdl_backward_adagrad(const mdl_feature* feats, int32_t num_features,
                          const mdl_table* tables, int32_t num_tables, int32_t max_dim,
                          uint32_t* sort_keys, uint32_t* sort_payload, int64_t n,
                          int32_t key_bits, const float* bag_count, float lr, float eps,
-                         void* workspace, size_t workspace_bytes, uint32_t classes,
-                         void* stream);
+                         const float* grad_scale, void* workspace, size_t workspace_bytes,
+                         uint32_t classes, void* stream);
 
 /* mdl_backward_adagrad in two calls with the same arguments and workspace:
  * mdl_backward_sort (radix sort + chunk plan), then mdl_backward_apply
@@ -299,8 +331,24 @@ int mdl_backward_apply(const mdl_feature* feats, int32_t num_features,
                        const mdl_table* tables, int32_t num_tables, int32_t max_dim,
                        uint32_t* sort_keys, uint32_t* sort_payload, int64_t n,
                        int32_t key_bits, const float* bag_count, float lr, float eps,
+                       const float* grad_scale, void* workspace, size_t workspace_bytes,
+                       uint32_t classes, void* stream);
+
+/*
+ * Squared 2-norm of the coalesced gradient of every table,
+ *   *sumsq = sum over distinct (table, row) of sum_j g[row, j]^2,
+ * after mdl_backward_sort and with the same arguments and workspace (the
+ * sorted pairs are kept, so mdl_backward_apply can follow).  With
+ * mdl_clip_coef this fuses the sparse clip (src/train.py:5788-5826) into the
+ * backward without materialising the coalesced gradient: sort, sumsq,
+ * clip_coef, apply(grad_scale = coef).  Deterministic (fixed-order sums).
+ */
+int mdl_backward_sumsq(const mdl_feature* feats, int32_t num_features,
+                       const mdl_table* tables, int32_t num_tables, int32_t max_dim,
+                       uint32_t* sort_keys, uint32_t* sort_payload, int64_t n,
+                       int32_t key_bits, const float* bag_count, float* sumsq,
                        void* workspace, size_t workspace_bytes, uint32_t classes,
-                         void* stream);
+                       void* stream);
 
 /*
  * Coalesced sparse gradients, the autograd contract of src/optim.py:317-329 and
@@ -323,6 +371,37 @@ int mdl_backward_coalesce(const mdl_feature* feats, int32_t num_features,
                           const int64_t* unique_range, const uint64_t* rows_addr,
                           const uint64_t* values_addr, void* workspace,
                           size_t workspace_bytes, uint32_t classes, void* stream);
+
+/* ------------------------------------------------------------ clipping --- */
+
+/* A contiguous gradient tensor (dense, or the values of a coalesced COO). */
+typedef struct mdl_span {
+  uint64_t data;          /* device address */
+  int64_t numel;
+  int32_t dtype;          /* MDL_F32 / MDL_BF16 */
+  int32_t reserved;
+} mdl_span;               /* 24 bytes */
+
+/*
+ * Sparse gradient clipping of the trainer (_clip_sparse_grad_norm,
+ * src/train.py:5788-5826, with _gradient_squared_norm :5745-5753 and
+ * _scale_gradients :5756-5772), as three stream-ordered calls that never
+ * synchronise:
+ *   mdl_sumsq      *sumsq = sum over spans of sum_i x_i^2 (fp32 squares and
+ *                  partials, fp64 final sum; deterministic).  spans: device
+ *                  array of num_spans (<= 65535) descriptors.
+ *   mdl_clip_coef  total = sqrt(sumsq[0] + ... + sumsq[count-1]) (fp32, in
+ *                  order), *total_norm = total (may be NULL),
+ *                  *coef = min(max_norm / (total + 1e-6), 1).
+ *   mdl_scale      x *= *coef in place, in each span's dtype (bf16: the
+ *                  coefficient rounded to bf16, one rounding of the product).
+ */
+size_t mdl_sumsq_workspace_bytes(int32_t num_spans);
+int mdl_sumsq(const mdl_span* spans, int32_t num_spans, float* sumsq,
+              void* workspace, size_t workspace_bytes, void* stream);
+int mdl_clip_coef(const float* sumsq, int32_t count, float max_norm,
+                  float* total_norm, float* coef, void* stream);
+int mdl_scale(const mdl_span* spans, int32_t num_spans, const float* coef, void* stream);
 
 /* ------------------------------------------------------------- update --- */
 

@@ -23,6 +23,7 @@ MDL_POOL_NONE = 0
 MDL_POOL_SUM = 1
 MDL_POOL_MEAN = 2
 MDL_FLAG_EXCLUDE_NULL = 1
+MDL_FLAG_ROWS_BY_POSITION = 2
 MDL_BUCKET_PRE_HASHED = 0
 MDL_BUCKET_MOD = 1
 MDL_SEQ_OLDEST_TO_NEWEST = 0
@@ -54,6 +55,7 @@ FEATURE_DTYPE = np.dtype(
     ]
 )
 CHUNK_DTYPE = np.dtype([("feature", "<i4"), ("count", "<i4"), ("first", "<i8")])
+SPAN_DTYPE = np.dtype([("data", "<u8"), ("numel", "<i8"), ("dtype", "<i4"), ("reserved", "<i4")])
 TABLE_DTYPE = np.dtype(
     [
         ("weight", "<u8"),
@@ -68,6 +70,7 @@ TABLE_DTYPE = np.dtype(
 )
 assert FEATURE_DTYPE.itemsize == 128
 assert CHUNK_DTYPE.itemsize == 16
+assert SPAN_DTYPE.itemsize == 24
 assert TABLE_DTYPE.itemsize == 48
 
 _P = ctypes.c_void_p
@@ -86,6 +89,7 @@ SIGNATURES: dict[str, tuple] = {
     "mdl_lengths_to_offsets": (_I32, [_P, _I64, _P, _P, _SZ, _P]),
     "mdl_plan_chunks": (_I64, [_P, _I32, _I32, _P, _I64]),
     "mdl_forward": (_I32, [_P, _I32, _P, _I64, _P, _P, _P, _P, _U32, _P, _P, _U32, _P]),
+    "mdl_pool_backward": (_I32, [_P, _I32, _P, _I64, _P, _P, _P, _U32, _P]),
     "mdl_feature_classes": (_U32, [_P, _I32]),
     "mdl_table_classes": (_U32, [_P, _I32]),
     "mdl_sequence_forward": (
@@ -100,13 +104,21 @@ SIGNATURES: dict[str, tuple] = {
     "mdl_backward_workspace_bytes": (_SZ, [_I64, _I32, _I32]),
     "mdl_backward_adagrad": (
         _I32,
-        [_P, _I32, _P, _I32, _I32, _P, _P, _I64, _I32, _P, _F, _F, _P, _SZ, _U32, _P],
+        [_P, _I32, _P, _I32, _I32, _P, _P, _I64, _I32, _P, _F, _F, _P, _P, _SZ, _U32, _P],
     ),
     "mdl_backward_sort": (_I32, [_P, _I32, _I32, _P, _P, _I64, _I32, _P, _SZ, _P]),
     "mdl_backward_apply": (
         _I32,
-        [_P, _I32, _P, _I32, _I32, _P, _P, _I64, _I32, _P, _F, _F, _P, _SZ, _U32, _P],
+        [_P, _I32, _P, _I32, _I32, _P, _P, _I64, _I32, _P, _F, _F, _P, _P, _SZ, _U32, _P],
     ),
+    "mdl_backward_sumsq": (
+        _I32,
+        [_P, _I32, _P, _I32, _I32, _P, _P, _I64, _I32, _P, _P, _P, _SZ, _U32, _P],
+    ),
+    "mdl_sumsq_workspace_bytes": (_SZ, [_I32]),
+    "mdl_sumsq": (_I32, [_P, _I32, _P, _P, _SZ, _P]),
+    "mdl_clip_coef": (_I32, [_P, _I32, _F, _P, _P, _P]),
+    "mdl_scale": (_I32, [_P, _I32, _P, _P]),
     "mdl_backward_count": (_I32, [_P, _I32, _I32, _P, _P, _I64, _I32, _P, _P, _SZ, _P]),
     "mdl_backward_coalesce": (
         _I32,

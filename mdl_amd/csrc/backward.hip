@@ -20,13 +20,16 @@ namespace mdl {
 int sort_pairs(uint32_t* keys, uint32_t* vals, uint32_t* keys_alt, uint32_t* vals_alt, int64_t n,
                int key_bits, void* ws, size_t ws_bytes, int* in_alt, hipStream_t s);
 size_t sort_ws_bytes(int64_t n);
+int launch_sum_partials(const float* partial, int64_t m, const int64_t* m_dev, float* out, hipStream_t s);
 
 constexpr int kChunkMax = 512;
 constexpr int kBwdWaves = 4;
 constexpr int kPlanThreads = 1024;
 
 enum { kHeadOpen = 1, kTailOpen = 2, kSingle = 4 };
-enum { kModeAdagrad = 0, kModeCoalesce = 1 };
+// Adagrad: update the rows; Coalesce: write the coalesced gradient; Sumsq:
+// only the squared 2-norm of the coalesced gradient (for clipping).
+enum { kModeAdagrad = 0, kModeCoalesce = 1, kModeSumsq = 2 };
 
 struct BwdWs {
   uint32_t* keys_alt;
@@ -43,6 +46,7 @@ struct BwdWs {
   size_t scan_bytes;
   float* part_first;      // [max_chunks, max_dim]
   float* part_last;       // [max_chunks, max_dim]
+  float* chunk_ss;        // [max_chunks] squared norms of the runs finished per chunk
 };
 
 // Chunks hold kPassesPerChunk passes of G rows; G >= 1, so a table of m
@@ -75,6 +79,7 @@ static size_t carve(BwdWs* w, void* base, int64_t n, int32_t T, int32_t max_dim)
   w->scan_ws = take(w->scan_bytes);
   w->part_first = (float*)take((size_t)mc * max_dim * 4);
   w->part_last = (float*)take((size_t)mc * max_dim * 4);
+  w->chunk_ss = (float*)take((size_t)mc * 4);
   return (size_t)(p - start);
 }
 
@@ -242,6 +247,8 @@ struct BwdArgs {
   const int64_t* head_base;
   float* part_first;
   float* part_last;
+  float* chunk_ss;
+  const float* grad_scale;  // Adagrad: gradients are multiplied by *grad_scale (NULL: 1)
   int64_t max_chunks;
   int32_t max_dim;
   float lr, eps;
@@ -278,6 +285,7 @@ struct Reducer {
   const TG* g_base;
   int64_t g_stride, pbase;
   bool g_mean;
+  float scale;
 
   __device__ Reducer(const BwdArgs& args, int32_t table) : a(args), t(table) {
     const mdl_table& tb = a.tables[t];
@@ -296,6 +304,9 @@ struct Reducer {
     g_base = nullptr;
     g_stride = pbase = 0;
     g_mean = false;
+    scale = 1.f;
+    if (kMode == kModeAdagrad && a.grad_scale != nullptr)
+      scale = __builtin_bit_cast(float, __builtin_amdgcn_readfirstlane(__builtin_bit_cast(int, *a.grad_scale)));
     if (single >= 0) {
       const mdl_feature& f = a.feats[single];
       g_base = (const TG*)uni64b((int64_t)f.grad);
@@ -332,15 +343,16 @@ struct Reducer {
                                          int64_t uidx) const {
     const int64_t row = (int64_t)key - row_base;
     if (kMode == kModeAdagrad) {
-      const float acc = acc0 + ss / (float)dim;
+      // scale == 1 leaves every product exact, so unclipped steps are unchanged
+      const float acc = acc0 + (ss * (scale * scale)) / (float)dim;
       if (sub == 0) state[row] = acc;
       const float inv = 1.f / (sqrtf(acc) + a.eps);
       if (col_ok) {
 #pragma unroll
-        for (int k = 0; k < C; ++k) w[k] = w[k] - a.lr * (v[k] * inv);
+        for (int k = 0; k < C; ++k) w[k] = w[k] - a.lr * ((v[k] * scale) * inv);
         RowIO<TW, C>::store(W + row * dim + col, w);
       }
-    } else {
+    } else if (kMode == kModeCoalesce) {
       const int64_t local = uidx - a.unique_range[2 * t];
       int64_t* rows = (int64_t*)a.rows_addr[t];
       TW* vals = (TW*)a.values_addr[t];
@@ -364,7 +376,9 @@ __device__ __forceinline__ void reduce_chunk_body(const BwdArgs& a, int64_t c, c
   // Pass groups per iteration: 16 columns of loads in flight per lane.
   constexpr int U = C >= 8 ? 2 : 4;
   constexpr bool adagrad = kMode == kModeAdagrad;
-  constexpr bool coalesce = !adagrad;
+  constexpr bool coalesce = kMode == kModeCoalesce;
+  constexpr bool sumsq = kMode == kModeSumsq;
+  float ss_acc = 0.f;  // Sumsq: squared norms of the runs this lane's slot finishes
   const int lane = lane_id();
   const uint32_t kNone = 0xffffffffu;
   const int len = (int)(r.c_end - r.c_begin);
@@ -461,6 +475,8 @@ __device__ __forceinline__ void reduce_chunk_body(const BwdArgs& a, int64_t c, c
 #pragma unroll
             for (int k = 0; k < C; ++k) pf[k] = v[u][k];
           }
+        } else if (sumsq) {
+          if (sub == 0) ss_acc += ss;
         } else {
           R.finish(key[u], v[u], ss, acc0[u], w[u], uidx);
         }
@@ -477,6 +493,10 @@ __device__ __forceinline__ void reduce_chunk_body(const BwdArgs& a, int64_t c, c
     float* pl = a.part_last + c * a.max_dim + R.col;
 #pragma unroll
     for (int k = 0; k < C; ++k) pl[k] = carry[k];
+  }
+  if (sumsq) {
+    for (int m = 1; m < kWave; m <<= 1) ss_acc += shfl_f(ss_acc, lane ^ m);
+    if (lane == 0) a.chunk_ss[c] = ss_acc;
   }
   if (lane == 0) a.chunk_flags[c] = (head_open ? kHeadOpen : 0) | (tail_open ? kTailOpen : 0) | (single ? kSingle : 0);
 }
@@ -554,7 +574,12 @@ __device__ __forceinline__ void fixup_chunk(const BwdArgs& a, int64_t c, const C
     if (R.col_ok) RowIO<TW, C>::load(R.W + row * R.dim + R.col, w);
     acc0 = R.state[row];
   }
-  if (R.slot == 0) R.finish(key, v, ss, acc0, w, uidx);
+  if (kMode == kModeSumsq) {
+    // The reduce of chunk c wrote its own runs' share before this launch.
+    if (lane_id() == 0) a.chunk_ss[c] += ss;
+  } else if (R.slot == 0) {
+    R.finish(key, v, ss, acc0, w, uidx);
+  }
 }
 
 template <bool kFixup, int kMode, typename TW, typename TG, int C>
@@ -626,6 +651,8 @@ static void fill_args(BwdArgs* a, const mdl_feature* feats, int32_t F, const mdl
   a->head_base = w.head_base;
   a->part_first = w.part_first;
   a->part_last = w.part_last;
+  a->chunk_ss = w.chunk_ss;
+  a->grad_scale = nullptr;
   a->max_chunks = max_chunks_for(n, T);
   a->max_dim = max_dim;
   a->lr = 0.f;
@@ -643,8 +670,11 @@ static int launch_reduce(const BwdArgs& a, uint32_t classes, hipStream_t s) {
   if (a.mode == kModeAdagrad)
     hipLaunchKernelGGL((bwd_reduce_kernel<kFixup, kModeAdagrad, TW, TG, C>), dim3((unsigned)blocks),
                        dim3(kBwdWaves * kWave), 0, s, a);
-  else
+  else if (a.mode == kModeCoalesce)
     hipLaunchKernelGGL((bwd_reduce_kernel<kFixup, kModeCoalesce, TW, TG, C>), dim3((unsigned)blocks),
+                       dim3(kBwdWaves * kWave), 0, s, a);
+  else
+    hipLaunchKernelGGL((bwd_reduce_kernel<kFixup, kModeSumsq, TW, TG, C>), dim3((unsigned)blocks),
                        dim3(kBwdWaves * kWave), 0, s, a);
   MDL_CHECK_LAUNCH(kFixup ? "bwd_fixup_kernel" : "bwd_reduce_kernel");
   return MDL_OK;
@@ -718,36 +748,71 @@ int mdl_backward_sort(const mdl_table* tables, int32_t num_tables, int32_t max_d
                  as_stream(stream), &w, &sk, &sv);
 }
 
-int mdl_backward_apply(const mdl_feature* feats, int32_t num_features, const mdl_table* tables,
-                       int32_t num_tables, int32_t max_dim, uint32_t* sort_keys, uint32_t* sort_payload,
-                       int64_t n, int32_t key_bits, const float* bag_count, float lr, float eps,
-                       void* workspace, size_t workspace_bytes, uint32_t classes, void* stream) {
-  int rc = validate_tables("mdl_backward_apply", num_tables, max_dim, n);
-  if (rc) return rc;
-  if (n == 0) return MDL_OK;
+// Arguments of the calls that follow mdl_backward_sort: the sorted pairs are
+// where the sort's pass count left them.
+static int sorted_args(const char* who, BwdArgs* a, const mdl_feature* feats, int32_t num_features,
+                       const mdl_table* tables, int32_t num_tables, int32_t max_dim, uint32_t* sort_keys,
+                       uint32_t* sort_payload, int64_t n, int32_t key_bits, const float* bag_count,
+                       void* workspace, size_t workspace_bytes) {
   BwdWs w;
   const size_t need = carve(&w, workspace, n, num_tables, max_dim);
-  if (workspace_bytes < need) return fail(MDL_ERR_WORKSPACE, "mdl_backward_apply: workspace too small");
+  if (workspace_bytes < need) return fail(MDL_ERR_WORKSPACE, std::string(who) + ": workspace too small");
   const int passes = (key_bits + 7) / 8;
   const uint32_t* sk = (passes & 1) ? w.keys_alt : sort_keys;
   const uint32_t* sv = (passes & 1) ? w.vals_alt : sort_payload;
+  fill_args(a, feats, num_features, tables, num_tables, max_dim, sk, sv, bag_count, w, n);
+  return MDL_OK;
+}
+
+int mdl_backward_apply(const mdl_feature* feats, int32_t num_features, const mdl_table* tables,
+                       int32_t num_tables, int32_t max_dim, uint32_t* sort_keys, uint32_t* sort_payload,
+                       int64_t n, int32_t key_bits, const float* bag_count, float lr, float eps,
+                       const float* grad_scale, void* workspace, size_t workspace_bytes, uint32_t classes,
+                       void* stream) {
+  int rc = validate_tables("mdl_backward_apply", num_tables, max_dim, n);
+  if (rc) return rc;
+  if (n == 0) return MDL_OK;
   BwdArgs a;
-  fill_args(&a, feats, num_features, tables, num_tables, max_dim, sk, sv, bag_count, w, n);
+  rc = sorted_args("mdl_backward_apply", &a, feats, num_features, tables, num_tables, max_dim, sort_keys,
+                   sort_payload, n, key_bits, bag_count, workspace, workspace_bytes);
+  if (rc) return rc;
   a.lr = lr;
   a.eps = eps;
+  a.grad_scale = grad_scale;
   a.mode = kModeAdagrad;
   return run_reduce(a, classes, as_stream(stream));
+}
+
+int mdl_backward_sumsq(const mdl_feature* feats, int32_t num_features, const mdl_table* tables,
+                       int32_t num_tables, int32_t max_dim, uint32_t* sort_keys, uint32_t* sort_payload,
+                       int64_t n, int32_t key_bits, const float* bag_count, float* sumsq, void* workspace,
+                       size_t workspace_bytes, uint32_t classes, void* stream) {
+  int rc = validate_tables("mdl_backward_sumsq", num_tables, max_dim, n);
+  if (rc) return rc;
+  if (!sumsq) return fail(MDL_ERR_INVALID, "mdl_backward_sumsq: null output");
+  hipStream_t s = as_stream(stream);
+  if (n == 0) return launch_sum_partials(nullptr, 0, nullptr, sumsq, s);
+  BwdArgs a;
+  rc = sorted_args("mdl_backward_sumsq", &a, feats, num_features, tables, num_tables, max_dim, sort_keys,
+                   sort_payload, n, key_bits, bag_count, workspace, workspace_bytes);
+  if (rc) return rc;
+  a.mode = kModeSumsq;
+  rc = run_reduce(a, classes, s);
+  if (rc) return rc;
+  // chunk_base[T] chunks were reduced; their partials are added in chunk order.
+  return launch_sum_partials(a.chunk_ss, 0, a.chunk_base + num_tables, sumsq, s);
 }
 
 int mdl_backward_adagrad(const mdl_feature* feats, int32_t num_features, const mdl_table* tables,
                          int32_t num_tables, int32_t max_dim, uint32_t* sort_keys, uint32_t* sort_payload,
                          int64_t n, int32_t key_bits, const float* bag_count, float lr, float eps,
-                         void* workspace, size_t workspace_bytes, uint32_t classes, void* stream) {
+                         const float* grad_scale, void* workspace, size_t workspace_bytes, uint32_t classes,
+                         void* stream) {
   int rc = mdl_backward_sort(tables, num_tables, max_dim, sort_keys, sort_payload, n, key_bits, workspace,
                              workspace_bytes, stream);
   if (rc) return rc;
   return mdl_backward_apply(feats, num_features, tables, num_tables, max_dim, sort_keys, sort_payload, n,
-                            key_bits, bag_count, lr, eps, workspace, workspace_bytes, classes, stream);
+                            key_bits, bag_count, lr, eps, grad_scale, workspace, workspace_bytes, classes, stream);
 }
 
 int mdl_backward_count(const mdl_table* tables, int32_t num_tables, int32_t max_dim, uint32_t* sort_keys,
@@ -788,14 +853,10 @@ int mdl_backward_coalesce(const mdl_feature* feats, int32_t num_features, const 
   if (rc) return rc;
   if (n == 0) return MDL_OK;
   hipStream_t s = as_stream(stream);
-  BwdWs w;
-  const size_t need = carve(&w, workspace, n, num_tables, max_dim);
-  if (workspace_bytes < need) return fail(MDL_ERR_WORKSPACE, "mdl_backward_coalesce: workspace too small");
-  const int passes = (key_bits + 7) / 8;
-  const uint32_t* sk = (passes & 1) ? w.keys_alt : sort_keys;
-  const uint32_t* sv = (passes & 1) ? w.vals_alt : sort_payload;
   BwdArgs a;
-  fill_args(&a, feats, num_features, tables, num_tables, max_dim, sk, sv, bag_count, w, n);
+  rc = sorted_args("mdl_backward_coalesce", &a, feats, num_features, tables, num_tables, max_dim, sort_keys,
+                   sort_payload, n, key_bits, bag_count, workspace, workspace_bytes);
+  if (rc) return rc;
   a.mode = kModeCoalesce;
   a.rows_addr = rows_addr;
   a.values_addr = values_addr;

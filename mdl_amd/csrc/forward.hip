@@ -153,14 +153,20 @@ __device__ __forceinline__ void pooled_chunk(const Feat& f, int64_t first_bag, i
     clamped += oc != o;
     s_off[i] = oc;
   }
-  if (clamped && a.error_count) atomicAdd(a.error_count, clamped);
   wave_sync();
+  // Decreasing offsets (negative lengths) are errors too; the walk below
+  // stays inside [s_off[0], s_off[nb]) whatever the offsets hold.
+  for (int i = lane + 1; i <= nb; i += kWave) clamped += s_off[i] < s_off[i - 1];
+  if (clamped && a.error_count) atomicAdd(a.error_count, clamped);
   const int64_t e_begin = s_off[0], e_end = s_off[nb];
   const int L = lanes_for(f.dim, C);
   const int G = kWave / L;
   const int slot = lane / L, sub = lane % L;
   const int ncb = (f.dim + L * C - 1) / (L * C);
   const bool exclude = (f.flags & MDL_FLAG_EXCLUDE_NULL) != 0;
+  // Rows by position: row e - ids_begin of `weight` is the id slot's row
+  // (already-embedded input); the ids only decide the null weights.
+  const bool by_pos = (f.flags & MDL_FLAG_ROWS_BY_POSITION) != 0;
   const bool mean = f.pooling == MDL_POOL_MEAN;
   const TW* W = static_cast<const TW*>(f.weight);
   TO* out = static_cast<TO*>(f.out);
@@ -188,7 +194,7 @@ __device__ __forceinline__ void pooled_chunk(const Feat& f, int64_t first_bag, i
       float wt[kUnroll];
       int seg[kUnroll];
       bool tail[kUnroll];
-      int64_t id[kUnroll];
+      int64_t id[kUnroll], row[kUnroll];
       // Bag of every slot (LDS cursor walk), then all row loads of the group
       // in one branch-free block, then the backward's sort keys.
 #pragma unroll
@@ -199,7 +205,8 @@ __device__ __forceinline__ void pooled_chunk(const Feat& f, int64_t first_bag, i
         if (valid) {
           while (s_off[bag + 1] <= e) ++bag;
         }
-        const bool in_range = (uint64_t)id[u] < (uint64_t)f.num_rows;
+        row[u] = by_pos ? e - f.ids_begin : id[u];
+        const bool in_range = (uint64_t)row[u] < (uint64_t)f.num_rows;
         float w = (exclude && id[u] == 0) ? 0.f : 1.f;
         if (!in_range || !valid) w = 0.f;
         seg[u] = valid ? bag : -1;
@@ -208,17 +215,19 @@ __device__ __forceinline__ void pooled_chunk(const Feat& f, int64_t first_bag, i
       }
 #pragma unroll
       for (int u = 0; u < kUnroll; ++u)
-        RowIO<TW, C>::load(wt[u] != 0.f && col_ok ? W + id[u] * f.dim + col : zero_row<TW>(), v[u]);
+        RowIO<TW, C>::load(wt[u] != 0.f && col_ok ? W + row[u] * f.dim + col : zero_row<TW>(), v[u]);
       if (cb == 0 && sub == 0) {
 #pragma unroll
         for (int u = 0; u < kUnroll; ++u) {
           const int64_t e = base + (int64_t)u * G + slot;
           if (e >= e_end) continue;
-          bad += (uint64_t)id[u] >= (uint64_t)f.num_rows;
+          bad += (uint64_t)row[u] >= (uint64_t)f.num_rows;
           if (a.keys != nullptr) {
             // w == 0 covers invalid ids and nulls under "exclude": their
             // gradient is exactly zero, so they take no part in the backward.
-            a.keys[e] = (wt[u] != 0.f && id[u] != f.padding_idx) ? (uint32_t)(f.row_base + id[u]) : a.sentinel;
+            // Rows by position belong to no table.
+            a.keys[e] = (wt[u] != 0.f && !by_pos && id[u] != f.padding_idx) ? (uint32_t)(f.row_base + id[u])
+                                                                            : a.sentinel;
             a.payload[e] = (uint32_t)(f.payload_base + first_bag + seg[u]);
           }
         }
@@ -319,6 +328,103 @@ static int launch_forward(const FwdArgs& a, uint32_t classes, int64_t blocks, hi
   if (classes != 0 && !(classes & (1u << ClassOf<TW, TO, C>::value))) return MDL_OK;
   hipLaunchKernelGGL((forward_kernel<TW, TO, C>), dim3((unsigned)blocks), dim3(kFwdWaves * kWave), 0, s, a);
   MDL_CHECK_LAUNCH("forward_kernel");
+  return MDL_OK;
+}
+
+// ------------------------------------------------------ pool backward --
+
+// Per-position gradient of one chunk of bags: slot e of bag b receives the
+// bag's upstream gradient row times w_e / max(count_b, 1) (mean) or w_e (sum).
+// The walk over the chunk's positions is the forward's (same LDS bounds and
+// bag cursor); consecutive slots of one bag read the same gradient row, which
+// stays in L2, so HBM sees about one read of each pooled gradient row and one
+// write of each position row.
+template <typename TW, typename TO, int C>
+__device__ __forceinline__ void unpool_chunk(const Feat& f, int64_t first_bag, int nb, int64_t* s_off,
+                                             const FwdArgs& a) {
+  constexpr int kUnroll = C >= 8 ? 2 : 4;
+  const int lane = lane_id();
+  const int64_t lo = f.ids_begin, hi = f.ids_begin + f.num_ids;
+  for (int i = lane; i <= nb; i += kWave) {
+    const int64_t o = a.offsets[f.bag_base + first_bag + i];
+    s_off[i] = o < lo ? lo : (o > hi ? hi : o);
+  }
+  wave_sync();
+  const int64_t e_begin = s_off[0], e_end = s_off[nb];
+  const int L = lanes_for(f.dim, C);
+  const int G = kWave / L;
+  const int slot = lane / L, sub = lane % L;
+  const int ncb = (f.dim + L * C - 1) / (L * C);
+  const bool exclude = (f.flags & MDL_FLAG_EXCLUDE_NULL) != 0;
+  const bool by_pos = (f.flags & MDL_FLAG_ROWS_BY_POSITION) != 0;
+  const bool mean = f.pooling == MDL_POOL_MEAN;
+  const TO* grad = static_cast<const TO*>(f.out);
+  TW* dst = static_cast<TW*>(const_cast<void*>(f.weight));
+  const float* counts = a.bag_count + f.payload_base + first_bag;
+  const int64_t step = (int64_t)G * kUnroll;
+  for (int cb = 0; cb < ncb; ++cb) {
+    const int col = (cb * L + sub) * C;
+    const bool col_ok = col < f.dim;
+    int bag = 0;
+    for (int64_t base = e_begin; base < e_end; base += step) {
+      int64_t id[kUnroll];
+      int bg[kUnroll];
+      bool valid[kUnroll];
+      float cnt[kUnroll], v[kUnroll][C];
+#pragma unroll
+      for (int u = 0; u < kUnroll; ++u) {
+        const int64_t e = base + (int64_t)u * G + slot;
+        valid[u] = e < e_end;
+        id[u] = valid[u] ? a.ids[e] : 0;
+        if (valid[u]) {
+          while (s_off[bag + 1] <= e) ++bag;
+        }
+        bg[u] = bag;
+      }
+#pragma unroll
+      for (int u = 0; u < kUnroll; ++u) {
+        cnt[u] = *(mean && valid[u] ? counts + bg[u] : zero_row<float>());
+        RowIO<TO, C>::load(valid[u] && col_ok ? grad + (first_bag + bg[u]) * f.out_stride + col : zero_row<TO>(),
+                           v[u]);
+      }
+#pragma unroll
+      for (int u = 0; u < kUnroll; ++u) {
+        const int64_t e = base + (int64_t)u * G + slot;
+        const int64_t row = e - f.ids_begin;
+        // Positions the forward gave weight 0: nulls under "exclude" and rows
+        // outside [0, num_rows).
+        const int64_t src = by_pos ? row : id[u];
+        const bool dead = (exclude && id[u] == 0) || (uint64_t)src >= (uint64_t)f.num_rows;
+        const float sc = dead ? 0.f : (mean ? 1.f / fmaxf(cnt[u], 1.f) : 1.f);
+#pragma unroll
+        for (int k = 0; k < C; ++k) v[u][k] *= sc;
+        if (valid[u] && col_ok) RowIO<TW, C>::store(dst + row * f.dim + col, v[u]);
+      }
+    }
+  }
+}
+
+template <typename TW, typename TO, int C>
+__global__ __launch_bounds__(kFwdWaves * kWave) void pool_backward_kernel(FwdArgs a) {
+  __shared__ int64_t s_off[kFwdWaves][kMaxBagsPerChunk + 1];
+  const int w = threadIdx.x / kWave;
+  const int64_t blk = xcd_block(blockIdx.x, gridDim.x);
+  const int64_t c = uni64(blk * kFwdWaves + w);
+  if (c >= a.num_chunks) return;
+  const int32_t fi = uni32(a.chunks[c].feature);
+  const int32_t count = uni32(a.chunks[c].count);
+  const int64_t first = uni64(a.chunks[c].first);
+  const Feat f = load_feat(a.feats + fi);
+  if (feat_class(f) != ClassOf<TW, TO, C>::value) return;  // another class's launch owns it
+  if (f.pooling == MDL_POOL_NONE || count > kMaxBagsPerChunk || count < 0) return;
+  unpool_chunk<TW, TO, C>(f, first, count, s_off[w], a);
+}
+
+template <typename TW, typename TO, int C>
+static int launch_pool_backward(const FwdArgs& a, uint32_t classes, int64_t blocks, hipStream_t s) {
+  if (classes != 0 && !(classes & (1u << ClassOf<TW, TO, C>::value))) return MDL_OK;
+  hipLaunchKernelGGL((pool_backward_kernel<TW, TO, C>), dim3((unsigned)blocks), dim3(kFwdWaves * kWave), 0, s, a);
+  MDL_CHECK_LAUNCH("pool_backward_kernel");
   return MDL_OK;
 }
 
@@ -521,6 +627,36 @@ int mdl_forward(const mdl_feature* feats, int32_t num_features, const mdl_chunk*
   if (!rc) rc = launch_forward<bf16_t, bf16_t, 1>(a, classes, blocks, s);
   if (!rc) rc = launch_forward<bf16_t, float, 8>(a, classes, blocks, s);
   if (!rc) rc = launch_forward<bf16_t, float, 1>(a, classes, blocks, s);
+  return rc;
+}
+
+int mdl_pool_backward(const mdl_feature* feats, int32_t num_features, const mdl_chunk* chunks,
+                      int64_t num_chunks, const int64_t* ids, const int64_t* offsets, const float* bag_count,
+                      uint32_t classes, void* stream) {
+  if (num_features < 0 || num_chunks < 0) return fail(MDL_ERR_INVALID, "mdl_pool_backward: negative count");
+  if (num_chunks == 0) return MDL_OK;
+  if (!feats || !chunks || !ids || !offsets || !bag_count)
+    return fail(MDL_ERR_INVALID, "mdl_pool_backward: null pointer");
+  FwdArgs a;
+  a.feats = feats;
+  a.chunks = chunks;
+  a.num_chunks = num_chunks;
+  a.ids = ids;
+  a.offsets = offsets;
+  a.keys = nullptr;
+  a.payload = nullptr;
+  a.bag_count = const_cast<float*>(bag_count);
+  a.error_count = nullptr;
+  a.sentinel = 0;
+  const int64_t blocks = (num_chunks + kFwdWaves - 1) / kFwdWaves;
+  if (blocks > 0x7fffffff) return fail(MDL_ERR_UNSUPPORTED, "mdl_pool_backward: too many chunks");
+  hipStream_t s = as_stream(stream);
+  int rc = launch_pool_backward<float, float, 4>(a, classes, blocks, s);
+  if (!rc) rc = launch_pool_backward<float, float, 1>(a, classes, blocks, s);
+  if (!rc) rc = launch_pool_backward<bf16_t, bf16_t, 8>(a, classes, blocks, s);
+  if (!rc) rc = launch_pool_backward<bf16_t, bf16_t, 1>(a, classes, blocks, s);
+  if (!rc) rc = launch_pool_backward<bf16_t, float, 8>(a, classes, blocks, s);
+  if (!rc) rc = launch_pool_backward<bf16_t, float, 1>(a, classes, blocks, s);
   return rc;
 }
 

@@ -92,7 +92,10 @@ def check_index_errors() -> None:
         bad = int(counter.item())
         if bad:
             counter.zero_()
-            raise IndexError(f"{bad} embedding lookups received out-of-range IDs on {device}")
+            raise IndexError(
+                f"{bad} embedding lookups or bag poolings received out-of-range IDs "
+                f"or inconsistent bag lengths on {device}"
+            )
 
 
 # ------------------------------------------------------------ plan types --

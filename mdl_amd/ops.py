@@ -23,6 +23,7 @@ from ._lib import (
     MDL_BF16,
     MDL_F32,
     MDL_FLAG_EXCLUDE_NULL,
+    MDL_FLAG_ROWS_BY_POSITION,
     MDL_POOL_MEAN,
     MDL_POOL_NONE,
     MDL_POOL_SUM,
@@ -243,6 +244,7 @@ class FeatureSpec:
     exclude_null: bool
     padding_idx: int
     out_dtype: torch.dtype
+    rows_by_position: bool = False
 
 
 class GroupPlan:
@@ -259,9 +261,9 @@ class GroupPlan:
         self._table_of_ptr: dict[int, int] = {}
         self.total_rows = 0
 
-    def add_table(self, weight: Tensor, state: Tensor | None = None) -> int:
+    def add_table(self, weight: Tensor, state: Tensor | None = None, *, shared: bool = True) -> int:
         key = weight.data_ptr()
-        if key in self._table_of_ptr:
+        if shared and key in self._table_of_ptr:
             t = self._table_of_ptr[key]
             if state is not None and self.tables[t].state is None:
                 self.tables[t].state = state
@@ -272,7 +274,8 @@ class GroupPlan:
         _require_device(weight, "embedding weight")
         t = len(self.tables)
         self.tables.append(TableSpec(weight=weight, state=state, row_base=self.total_rows))
-        self._table_of_ptr[key] = t
+        if shared:
+            self._table_of_ptr[key] = t
         self.total_rows += int(weight.size(0))
         if self.total_rows >= 0xFFFFFFFF:
             raise ValueError("a grouped lookup supports fewer than 2^32 - 1 rows in total")
@@ -287,12 +290,19 @@ class GroupPlan:
         padding_idx: int = 0,
         state: Tensor | None = None,
         out_dtype: torch.dtype | None = None,
+        rows_by_position: bool = False,
     ) -> int:
+        """Add one lookup request; ``rows_by_position`` pools the rows of an
+        already-embedded ``weight`` (row i = id slot i) instead of looking up
+        ids, which then only decide the null weights."""
+
         if pooling not in POOLING_CODES:
             raise ValueError(f"unsupported pooling {pooling!r}")
         if null_policy not in NULL_POLICIES:
             raise ValueError(f"unsupported categorical bag null policy {null_policy!r}")
-        t = self.add_table(weight, state)
+        if rows_by_position and pooling == "none":
+            raise ValueError("rows by position need a pooled feature")
+        t = self.add_table(weight, state, shared=not rows_by_position)
         self.features.append(
             FeatureSpec(
                 table=t,
@@ -300,6 +310,7 @@ class GroupPlan:
                 exclude_null=null_policy == "exclude",
                 padding_idx=int(padding_idx),
                 out_dtype=out_dtype or weight.dtype,
+                rows_by_position=bool(rows_by_position),
             )
         )
         return len(self.features) - 1
@@ -401,7 +412,10 @@ def build_features(
     feats["wdtype"] = [dtype_code(t.weight.dtype) for t in tab]
     feats["odtype"] = [dtype_code(s.out_dtype) for s in specs]
     feats["pooling"] = pool
-    feats["flags"] = [MDL_FLAG_EXCLUDE_NULL if s.exclude_null else 0 for s in specs]
+    feats["flags"] = [
+        (MDL_FLAG_EXCLUDE_NULL if s.exclude_null else 0) | (MDL_FLAG_ROWS_BY_POSITION if s.rows_by_position else 0)
+        for s in specs
+    ]
     feats["padding_idx"] = [s.padding_idx for s in specs]
     feats["table"] = [s.table for s in specs]
     for s, t in zip(specs, tab):
@@ -422,6 +436,7 @@ def forward_packed(
     *,
     with_backward: bool,
     error_count: Tensor | None = None,
+    with_bag_count: bool | None = None,
 ) -> ForwardResult:
     """Grouped lookup over caller-packed buffers (no per-feature copies).
 
@@ -429,11 +444,16 @@ def forward_packed(
     bounds from one scan of the concatenated lengths (see build_features);
     ``outputs[f]``: row-major output rows of feature f (2-D views with unit
     column stride, e.g. column slices of one ``[B, sum(dim)]`` buffer).
+    ``with_backward`` emits the backward's sort keys and bag counts;
+    ``with_bag_count`` (default: ``with_backward``) only the bag counts.
     """
 
     device = all_ids.device
     stream = _stream(device)
     n = int(all_ids.numel())
+    # Bags that are all empty still get zero rows: the kernel needs a real
+    # address even when there are no ids (it reads none of them).
+    ids_arg = all_ids if n else torch.zeros(1, dtype=torch.int64, device=device)
     out_ptrs = [o.data_ptr() for o in outputs]
     out_strides = [o.stride(0) if o.ndim == 2 else int(o.size(-1)) for o in outputs]
     feats = build_features(plan, id_counts, bag_counts, out_ptrs, out_strides)
@@ -451,14 +471,16 @@ def forward_packed(
         error_count = torch.zeros(1, dtype=torch.int32, device=device)
     keys = payload = bag_count = None
     total_rows_out = int(feats["payload_base"][-1] + (feats["num_bags"][-1] if feats["pooling"][-1] else feats["num_ids"][-1])) if len(feats) else 0
+    if with_bag_count is None:
+        with_bag_count = with_backward
     if with_backward:
         keys = torch.empty(max(n, 1), dtype=torch.int32, device=device)
         payload = torch.empty(max(n, 1), dtype=torch.int32, device=device)
-        if pooled_any:
-            bag_count = torch.empty(max(total_rows_out, 1), dtype=torch.float32, device=device)
+    if with_bag_count and pooled_any:
+        bag_count = torch.empty(max(total_rows_out, 1), dtype=torch.float32, device=device)
     check(
         lib().mdl_forward(
-            feats_dev.data_ptr(), len(feats), chunks_dev.data_ptr(), n_chunks, all_ids.data_ptr(),
+            feats_dev.data_ptr(), len(feats), chunks_dev.data_ptr(), n_chunks, ids_arg.data_ptr(),
             _ptr(offsets), _ptr(keys), _ptr(payload), plan.sentinel, _ptr(bag_count),
             error_count.data_ptr(), feature_classes(feats), stream,
         ),
@@ -467,7 +489,7 @@ def forward_packed(
     return ForwardResult(
         plan=plan, device=device, ids=all_ids, offsets=offsets, outputs=list(outputs), feats=feats,
         keys=keys, payload=payload, bag_count=bag_count, error_count=error_count,
-        keep=[feats_dev, chunks_dev],
+        keep=[feats_dev, chunks_dev, ids_arg],
     )
 
 
@@ -479,6 +501,7 @@ def grouped_forward(
     with_backward: bool,
     outputs: Sequence[Tensor] | None = None,
     error_count: Tensor | None = None,
+    with_bag_count: bool | None = None,
 ) -> ForwardResult:
     """Look up (and pool) every feature of ``plan`` in one launch.
 
@@ -530,7 +553,7 @@ def grouped_forward(
                 raise ValueError("caller outputs must have unit column stride and the feature's dtype")
     return forward_packed(
         plan, all_ids, offsets, id_counts, bag_counts, outputs,
-        with_backward=with_backward, error_count=error_count,
+        with_backward=with_backward, error_count=error_count, with_bag_count=with_bag_count,
     )
 
 
@@ -605,8 +628,80 @@ def _attach_grads(res: ForwardResult, grads: Sequence[Tensor | None]) -> tuple[n
     return feats, keep
 
 
-def backward_adagrad(res: ForwardResult, grads: Sequence[Tensor | None], *, lr: float, eps: float) -> None:
-    """Fused backward + row-wise Adagrad of every table (consumes the keys)."""
+def pool_backward(
+    res: ForwardResult, grads: Sequence[Tensor | None], dests: Sequence[Tensor | None]
+) -> None:
+    """Per-position gradient of the pooled features of a forward (one launch).
+
+    ``grads[f]`` is the upstream gradient of feature f's pooled output and
+    ``dests[f]`` a contiguous ``[num_ids_f, dim]`` tensor of the weight dtype
+    that receives ``grad[bag] * w_i / max(count, 1)`` (mean) or
+    ``grad[bag] * w_i`` (sum) for every id position i; None skips feature f.
+    The forward must have kept its bag counts.
+    """
+
+    if res.bag_count is None or res.offsets is None:
+        raise RuntimeError("the forward ran without bag counts")
+    feats = res.feats.copy()
+    keep: list[Tensor] = []
+    sel: list[int] = []
+    for f, spec in enumerate(res.plan.features):
+        d = dests[f]
+        if d is None or spec.pooling == MDL_POOL_NONE:
+            continue
+        weight = res.plan.tables[spec.table].weight
+        n_f = int(feats["num_ids"][f])
+        dim = int(feats["dim"][f])
+        if d.dtype != weight.dtype or not d.is_contiguous() or d.numel() != n_f * dim:
+            raise ValueError("pool_backward destinations are contiguous [num_ids, dim] tensors of the weight dtype")
+        g = grads[f]
+        if g is None:
+            g = torch.zeros_like(res.outputs[f])
+        if g.dtype != spec.out_dtype:
+            g = g.to(spec.out_dtype)
+        if g.ndim != 2 or g.stride(-1) != 1:
+            g = g.reshape(-1, dim).contiguous()
+        keep.append(g)
+        feats["out"][f] = g.data_ptr()
+        feats["out_stride"][f] = g.stride(0)
+        feats["weight"][f] = d.data_ptr()
+        sel.append(f)
+    if not sel:
+        return
+    sub = np.ascontiguousarray(feats[sel])
+    n_chunks = lib().mdl_plan_chunks(sub.ctypes.data, len(sub), FORWARD_TARGET_IDS, None, 0)
+    if n_chunks < 0:
+        check(int(n_chunks), "mdl_plan_chunks")
+    chunks = np.zeros(max(n_chunks, 1), dtype=CHUNK_DTYPE)
+    lib().mdl_plan_chunks(sub.ctypes.data, len(sub), FORWARD_TARGET_IDS, chunks.ctypes.data, n_chunks)
+    device = res.device
+    sub_dev = upload(sub, device)
+    chunks_dev = upload(chunks, device)
+    ids_arg = res.ids if res.ids.numel() else res.keep[-1]
+    check(
+        lib().mdl_pool_backward(
+            sub_dev.data_ptr(), len(sub), chunks_dev.data_ptr(), n_chunks, ids_arg.data_ptr(),
+            res.offsets.data_ptr(), res.bag_count.data_ptr(), feature_classes(sub), _stream(device),
+        ),
+        "mdl_pool_backward",
+    )
+    del keep
+
+
+def backward_adagrad(
+    res: ForwardResult,
+    grads: Sequence[Tensor | None],
+    *,
+    lr: float,
+    eps: float,
+    clip_norm: float | None = None,
+) -> Tensor | None:
+    """Fused backward + row-wise Adagrad of every table (consumes the keys).
+
+    With ``clip_norm`` the coalesced gradient of all tables is first clipped to
+    that global 2-norm (the trainer's sparse clip, src/train.py:5788-5826)
+    without being materialised; returns the pre-clip norm (device fp32 [1]).
+    """
 
     plan = res.plan
     if res.keys is None:
@@ -621,17 +716,91 @@ def backward_adagrad(res: ForwardResult, grads: Sequence[Tensor | None], *, lr: 
     tables_dev = _CACHE.get(tables, device)
     n = res.num_ids
     ws = _workspace(lib().mdl_backward_workspace_bytes(n, len(tables), plan.max_dim), device)
-    check(
-        lib().mdl_backward_adagrad(
-            feats_dev.data_ptr(), len(feats), tables_dev.data_ptr(), len(tables), plan.max_dim,
-            res.keys.data_ptr(), res.payload.data_ptr(), n, plan.key_bits, _ptr(res.bag_count),
-            float(lr), float(eps), ws.data_ptr(), ws.numel(), table_classes(tables), _stream(device),
-        ),
-        "mdl_backward_adagrad",
-    )
+    classes = table_classes(tables)
+    stream = _stream(device)
+    args = (feats_dev.data_ptr(), len(feats), tables_dev.data_ptr(), len(tables), plan.max_dim,
+            res.keys.data_ptr(), res.payload.data_ptr(), n, plan.key_bits, _ptr(res.bag_count))
+    norm = None
+    if clip_norm is None:
+        check(
+            lib().mdl_backward_adagrad(*args, float(lr), float(eps), None, ws.data_ptr(), ws.numel(), classes, stream),
+            "mdl_backward_adagrad",
+        )
+    else:
+        check(
+            lib().mdl_backward_sort(tables_dev.data_ptr(), len(tables), plan.max_dim, res.keys.data_ptr(),
+                                    res.payload.data_ptr(), n, plan.key_bits, ws.data_ptr(), ws.numel(), stream),
+            "mdl_backward_sort",
+        )
+        sumsq = torch.empty(1, dtype=torch.float32, device=device)
+        check(lib().mdl_backward_sumsq(*args, sumsq.data_ptr(), ws.data_ptr(), ws.numel(), classes, stream),
+              "mdl_backward_sumsq")
+        norm, coef = clip_coefficient(sumsq, clip_norm)
+        check(
+            lib().mdl_backward_apply(*args, float(lr), float(eps), coef.data_ptr(), ws.data_ptr(), ws.numel(),
+                                     classes, stream),
+            "mdl_backward_apply",
+        )
     res.keys = None
     res.payload = None
     del keep
+    return norm
+
+
+# ------------------------------------------------------------- clipping --
+
+
+def _spans(tensors: Sequence[Tensor]) -> tuple[np.ndarray, list[Tensor]]:
+    spans = np.zeros(len(tensors), dtype=_lib.SPAN_DTYPE)
+    for i, t in enumerate(tensors):
+        _require_device(t, "gradient")
+        if not t.is_contiguous():
+            raise ValueError("gradients to clip must be contiguous")
+        spans[i]["data"] = t.data_ptr()
+        spans[i]["numel"] = t.numel()
+        spans[i]["dtype"] = dtype_code(t.dtype)
+    return spans, list(tensors)
+
+
+def grad_sumsq(tensors: Sequence[Tensor], device: torch.device) -> Tensor:
+    """Sum of squares of every element of every tensor: fp32 [1] on device."""
+
+    out = torch.empty(1, dtype=torch.float32, device=device)
+    tensors = [t for t in tensors if t.numel()]
+    spans, _ = _spans(tensors)
+    ws = _workspace(lib().mdl_sumsq_workspace_bytes(len(spans)), device)
+    spans_dev = upload(spans, device) if len(spans) else None
+    check(
+        lib().mdl_sumsq(_ptr(spans_dev), len(spans), out.data_ptr(), ws.data_ptr(), ws.numel(), _stream(device)),
+        "mdl_sumsq",
+    )
+    return out
+
+
+def clip_coefficient(sumsq: Tensor, max_norm: float) -> tuple[Tensor, Tensor]:
+    """(total norm, min(max_norm / (norm + 1e-6), 1)) from squared norms."""
+
+    sumsq = sumsq.reshape(-1).to(torch.float32).contiguous()
+    norm = torch.empty(1, dtype=torch.float32, device=sumsq.device)
+    coef = torch.empty(1, dtype=torch.float32, device=sumsq.device)
+    check(
+        lib().mdl_clip_coef(sumsq.data_ptr(), sumsq.numel(), float(max_norm), norm.data_ptr(), coef.data_ptr(),
+                            _stream(sumsq.device)),
+        "mdl_clip_coef",
+    )
+    return norm, coef
+
+
+def scale_(tensors: Sequence[Tensor], coef: Tensor) -> None:
+    """In-place ``t *= coef`` in each tensor's dtype (coef: device fp32 [1])."""
+
+    tensors = [t for t in tensors if t.numel()]
+    if not tensors:
+        return
+    spans, _ = _spans(tensors)
+    device = tensors[0].device
+    spans_dev = upload(spans, device)
+    check(lib().mdl_scale(spans_dev.data_ptr(), len(spans), coef.data_ptr(), _stream(device)), "mdl_scale")
 
 
 def backward_coalesce(res: ForwardResult, grads: Sequence[Tensor | None]) -> list[tuple[Tensor, Tensor]]:

@@ -19,6 +19,27 @@ from torch import Tensor, nn
 from . import embeddings, ops
 
 
+def coalesced_grad(parameter: Tensor) -> Tensor:
+    """The parameter's sparse COO gradient, coalesced on the device.
+
+    A gradient that the grouped lookup emitted already coalesced only gets
+    its flag restored (autograd drops it); any other is coalesced by the HIP
+    sort + segment reduction and stored back as ``parameter.grad``, like
+    ``grad.coalesce()`` in src/optim.py:323-324 and src/train.py:5736-5738.
+    """
+
+    grad = parameter.grad
+    if not grad.is_coalesced() and embeddings.known_coalesced(parameter, grad):
+        grad._coalesced_(True)
+    if grad.is_coalesced():
+        return grad
+    rows, values = ops.coalesce_rows(grad._indices()[0], grad._values(), int(parameter.shape[0]))
+    grad = torch.sparse_coo_tensor(rows.unsqueeze(0), values, tuple(grad.shape), is_coalesced=True)
+    parameter.grad = grad
+    embeddings._remember_coalesced(parameter, rows, values)
+    return grad
+
+
 def fused_rowwise_adagrad_update(
     parameter: Tensor,
     accumulator: Tensor,
@@ -144,19 +165,10 @@ class ShardedRowWiseAdagrad(torch.optim.Optimizer):
                     raise RuntimeError(
                         "ShardedRowWiseAdagrad expects one sparse row dimension and one dense dimension"
                     )
-                if not grad.is_coalesced() and embeddings.known_coalesced(parameter, grad):
-                    grad._coalesced_(True)
+                grad = coalesced_grad(parameter)
                 embeddings.forget_coalesced(parameter)
-                if grad.is_coalesced():
-                    rows = grad.indices()[0]
-                    values = grad.values()
-                else:
-                    rows, values = ops.coalesce_rows(
-                        grad._indices()[0], grad._values(), int(parameter.shape[0])
-                    )
-                    parameter.grad = torch.sparse_coo_tensor(
-                        rows.unsqueeze(0), values, tuple(grad.shape), is_coalesced=True
-                    )
+                rows = grad.indices()[0]
+                values = grad.values()
                 clear_lr = self._advance(parameter, group)
                 if rows.numel() == 0:
                     continue

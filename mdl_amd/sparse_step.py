@@ -93,6 +93,9 @@ class SparseStep:
         self.ws = ops._workspace(
             lib().mdl_backward_workspace_bytes(self.n, len(self.tables), plan.max_dim), self.device
         )
+        self.sumsq = torch.zeros(1, dtype=torch.float32, device=self.device)
+        self.norm = torch.zeros(1, dtype=torch.float32, device=self.device)
+        self.coef = torch.ones(1, dtype=torch.float32, device=self.device)
 
     def _stream(self) -> int:
         return torch.cuda.current_stream(self.device).cuda_stream
@@ -130,23 +133,53 @@ class SparseStep:
             "mdl_backward_sort",
         )
 
-    def apply(self, lr: float, eps: float) -> None:
-        """Segment reduction of duplicate rows + fused row-wise Adagrad."""
+    def _bwd_args(self) -> tuple:
+        return (
+            self.feats_bwd_dev.data_ptr(), len(self.feats_bwd), self.tables_dev.data_ptr(), len(self.tables),
+            self.plan.max_dim, self.keys.data_ptr(), self.payload.data_ptr(), self.n, self.plan.key_bits,
+            ops._ptr(self.bag_count),
+        )
+
+    def apply(self, lr: float, eps: float, grad_scale: Tensor | None = None) -> None:
+        """Segment reduction of duplicate rows + fused row-wise Adagrad
+        (gradients times ``grad_scale``, a device fp32 [1], when given)."""
 
         check(
             lib().mdl_backward_apply(
-                self.feats_bwd_dev.data_ptr(), len(self.feats_bwd), self.tables_dev.data_ptr(), len(self.tables),
-                self.plan.max_dim, self.keys.data_ptr(), self.payload.data_ptr(), self.n, self.plan.key_bits,
-                ops._ptr(self.bag_count), float(lr), float(eps), self.ws.data_ptr(), self.ws.numel(),
-                self.bwd_classes, self._stream(),
+                *self._bwd_args(), float(lr), float(eps), ops._ptr(grad_scale), self.ws.data_ptr(),
+                self.ws.numel(), self.bwd_classes, self._stream(),
             ),
             "mdl_backward_apply",
         )
 
-    def step(self, lr: float, eps: float) -> None:
+    def clip(self, max_norm: float) -> tuple[Tensor, Tensor]:
+        """After sort(): (pre-clip global norm, clip coefficient), on device.
+
+        The norm is that of the coalesced gradient of every table, as the
+        trainer's sparse clip computes it (src/train.py:5788-5826)."""
+
+        check(
+            lib().mdl_backward_sumsq(
+                *self._bwd_args(), self.sumsq.data_ptr(), self.ws.data_ptr(), self.ws.numel(), self.bwd_classes,
+                self._stream(),
+            ),
+            "mdl_backward_sumsq",
+        )
+        check(
+            lib().mdl_clip_coef(self.sumsq.data_ptr(), 1, float(max_norm), self.norm.data_ptr(),
+                                self.coef.data_ptr(), self._stream()),
+            "mdl_clip_coef",
+        )
+        return self.norm, self.coef
+
+    def step(self, lr: float, eps: float, clip_norm: float | None = None) -> None:
         self.forward()
         self.sort()
-        self.apply(lr, eps)
+        if clip_norm is None:
+            self.apply(lr, eps)
+        else:
+            _, coef = self.clip(clip_norm)
+            self.apply(lr, eps, coef)
 
 
 class SequenceStep:
@@ -250,7 +283,7 @@ class SequenceStep:
             lib().mdl_backward_apply(
                 self.feats_bwd_dev.data_ptr(), len(self.feats_bwd), self.tables_dev.data_ptr(), len(self.tables),
                 self.plan.max_dim, self.keys.data_ptr(), self.payload.data_ptr(), self.n, self.plan.key_bits,
-                None, float(lr), float(eps), self.ws.data_ptr(), self.ws.numel(), self.bwd_classes,
+                None, float(lr), float(eps), None, self.ws.data_ptr(), self.ws.numel(), self.bwd_classes,
                 self._stream(),
             ),
             "mdl_backward_apply",

@@ -20,6 +20,11 @@ pinned (see ``tests/test_oracle.py``):
   tests/test_multivalue_features.py:95-120 and by torch's
   ``F.embedding_bag(mode="sum"/"mean")`` and ``_mean_pool``-style index_add_
   formulas on random bags (library routines, CPU).
+* pool_rows / pool_rows_padded / pool_rows_backward -- src/model.py:509-587
+  on already-embedded rows; pinned by the vectors of
+  tests/test_multivalue_features.py:95-121, by torch's ``F.embedding_bag``
+  (weighted sum / mean, library, CPU) and its autograd, and by the adjoint
+  identity <pool(E), G> = <E, pool_backward(G)> of a linear map.
 * sequence_gather -- src/model.py:2989-3100; pinned by a brute-force
   per-position definition and by the reference's padded vectors
   (tests/test_direct_id.py:242-280 layout).
@@ -27,6 +32,9 @@ pinned (see ``tests/test_oracle.py``):
   torch.unique(sorted, return_inverse, return_counts).
 * rowwise_adagrad -- src/optim.py:31-62; pinned by the closed-form cases of
   tests/test_rowwise_adagrad.py:40-128 and tests/test_sharded_embedding.py:647-699.
+* clip_grad_norm -- src/train.py:5745-5826; pinned by
+  torch.nn.utils.clip_grad_norm_ (same max_norm / (norm + 1e-6) clamped
+  coefficient; library, CPU) and by the no-op case norm <= max_norm.
 * sparse_step -- composition of the above; pinned by comparing it with the
   separately pinned pieces on random workloads.
 """
@@ -159,6 +167,60 @@ def pool(weight: np.ndarray, ids: np.ndarray, lengths: np.ndarray, mode: str, nu
     return out, cnt
 
 
+def pool_rows(embedded: np.ndarray, indices: np.ndarray, lengths: np.ndarray, mode: str,
+              null_policy: str):
+    """_mean_pool_categorical_bag on already-embedded rows, flat layout
+    (src/model.py:552-570): w_i = (id_i != 0) under "exclude" else 1,
+    sums[b] = sum_i w_i e_i, counts[b] = sum_i w_i, mean = sums / max(counts, 1).
+    Returns (out fp64 [B, dim], counts fp64 [B])."""
+
+    e = np.asarray(embedded, dtype=np.float64)
+    ids = np.asarray(indices, dtype=np.int64)
+    offs = offsets_of(lengths)
+    B = offs.size - 1
+    seg = np.repeat(np.arange(B), np.diff(offs))
+    w = (ids != 0).astype(np.float64) if null_policy == "exclude" else np.ones(ids.size)
+    sums = np.zeros((B, e.shape[1]))
+    cnt = np.zeros(B)
+    np.add.at(sums, seg, e * w[:, None])
+    np.add.at(cnt, seg, w)
+    if mode == "mean":
+        sums /= np.maximum(cnt, 1.0)[:, None]
+    return sums, cnt
+
+
+def pool_rows_padded(embedded: np.ndarray, indices: np.ndarray, lengths: np.ndarray, null_policy: str):
+    """Padded layout of the same mean pool (src/model.py:572-587), per bag."""
+
+    e = np.asarray(embedded, dtype=np.float64)
+    ids = np.asarray(indices, dtype=np.int64)
+    B, L, D = e.shape
+    out = np.zeros((B, D))
+    for b in range(B):
+        keep = [p for p in range(L) if p < lengths[b] and (null_policy != "exclude" or ids[b, p] != 0)]
+        if keep:
+            out[b] = e[b, keep].sum(0) / len(keep)
+    return out
+
+
+def pool_rows_backward(indices: np.ndarray, lengths: np.ndarray, grad: np.ndarray, mode: str,
+                       null_policy: str) -> np.ndarray:
+    """Gradient of pool_rows with respect to every embedded row (autograd of
+    the index_add_ + division of src/model.py:564-570): grad[b] * w_i /
+    max(counts[b], 1) (mean) or grad[b] * w_i (sum), fp64 [N, dim]."""
+
+    ids = np.asarray(indices, dtype=np.int64)
+    g = np.asarray(grad, dtype=np.float64)
+    offs = offsets_of(lengths)
+    B = offs.size - 1
+    seg = np.repeat(np.arange(B), np.diff(offs))
+    w = (ids != 0).astype(np.float64) if null_policy == "exclude" else np.ones(ids.size)
+    cnt = np.zeros(B)
+    np.add.at(cnt, seg, w)
+    den = np.maximum(cnt, 1.0) if mode == "mean" else np.ones(B)
+    return g[seg] / den[seg][:, None] * w[:, None]
+
+
 def sequence_gather(weight: np.ndarray, ids: np.ndarray, lengths: np.ndarray, out_len: int,
                     order: str = "oldest_to_newest"):
     """Right-aligned padded gather + mask (src/model.py:2989-3100), brute force."""
@@ -233,6 +295,17 @@ def rowwise_adagrad(weight: np.ndarray, acc: np.ndarray, rows: np.ndarray, value
     _lib().oracle_rowwise_adagrad(_p(w), 1 if is_bf16 else 0, w.shape[0], w.shape[1], _p(a), _p(rows),
                                   rows.size, _p(vals), float(lr), float(eps))
     return w, a
+
+
+def clip_grad_norm(values: list, max_norm: float):
+    """_clip_sparse_grad_norm on coalesced values (src/train.py:5745-5826):
+    total = sqrt(sum of squared 2-norms) (fp64 here), coef =
+    min(max_norm / (total + 1e-6), 1); returns (scaled fp64 copies, total, coef)."""
+
+    vals = [np.asarray(v, dtype=np.float64) for v in values]
+    total = float(np.sqrt(sum(float((v * v).sum()) for v in vals)))
+    coef = min(max_norm / (total + 1e-6), 1.0)
+    return [v * coef for v in vals], total, coef
 
 
 def sparse_step(features, tables, ids, offsets_rel, out_stride, grad, lr, eps):

@@ -66,6 +66,13 @@ VECTORS = {
         "expected_exclude": [[5.0], [0.0]],
         "expected_include_as_padding": [[10.0 / 3.0], [0.0]],
     },
+    "mean_pool_padded": {
+        "source": "tests/test_multivalue_features.py:113-121",
+        "indices": [[2, 0, 8], [0, 0, 0]],
+        "lengths": [3, 0],
+        "embedded_is_index_value": True,
+        "expected_exclude": [[5.0], [0.0]],
+    },
     "rowwise_adagrad_mean_not_sum": {
         "source": "tests/test_rowwise_adagrad.py:40-62",
         "shape": [4, 2],

@@ -86,7 +86,7 @@ def test_invalid_arguments_fail_before_any_launch():
     assert rc == -1 and b"key_bits" in lib.mdl_last_error()
     rc = lib.mdl_sort_pairs(None, None, None, None, 1 << 33, 8, None, 0, None, None)
     assert rc == -4
-    rc = lib.mdl_backward_adagrad(None, 0, None, 0, 8, None, None, 10, 8, None, 0.1, 1e-8, None, 0, 0, None)
+    rc = lib.mdl_backward_adagrad(None, 0, None, 0, 8, None, None, 10, 8, None, 0.1, 1e-8, None, None, 0, 0, None)
     assert rc == -1 and b"table" in lib.mdl_last_error()
     rc = lib.mdl_rowwise_adagrad(None, _lib.MDL_F32, 10, 4, 4, None, None, 3, None, _lib.MDL_BF16, 4, 0.1,
                                  1e-8, None, None)

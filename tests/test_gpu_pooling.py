@@ -1,0 +1,176 @@
+"""Bag pooling of already-embedded rows on the GPU: the drop-ins for
+``_mean_pool_categorical_bag`` / ``_batch_mean_pool_flat_bags``
+(src/model.py:509-678), written like tests/test_multivalue_features.py:95-121
+and checked against the CPU oracle."""
+
+import json
+import pathlib
+import sys
+
+import numpy as np
+import pytest
+import torch
+
+from mdl_amd import embeddings as E
+from mdl_amd.pooling import _batch_mean_pool_flat_bags, _mean_pool_categorical_bag, pool_bags
+from oracle import oracle as O
+
+pytestmark = pytest.mark.gpu
+GOLD = json.loads((pathlib.Path(__file__).parent / "golden" / "reference_vectors.json").read_text())
+
+# fp32: sums of a few terms, rounded once; bf16: one rounding of the result.
+TOL = {torch.float32: (1e-5, 1e-6), torch.bfloat16: (1e-2, 1e-2)}
+
+
+def announce(*parts):
+    print("CASE", *parts, flush=True)
+    sys.stdout.flush()
+
+
+def test_pooling_null_policies_have_distinct_denominators(device):
+    announce("pool_golden_flat")
+    g = GOLD["mean_pool_null_policies"]
+    indices = torch.tensor(g["indices"], device=device)
+    lengths = torch.tensor(g["lengths"], device=device)
+    embedded = indices.float().unsqueeze(-1)
+    excluded = _mean_pool_categorical_bag(embedded, indices, lengths, "exclude")
+    preserved = _mean_pool_categorical_bag(embedded, indices, lengths, "include_as_padding")
+    torch.testing.assert_close(excluded.cpu(), torch.tensor(g["expected_exclude"]))
+    torch.testing.assert_close(preserved.cpu(), torch.tensor(g["expected_include_as_padding"]))
+
+
+def test_padded_bag_pooling_path_still_supported(device):
+    announce("pool_golden_padded")
+    g = GOLD["mean_pool_padded"]
+    indices = torch.tensor(g["indices"], device=device)
+    lengths = torch.tensor(g["lengths"], device=device)
+    embedded = indices.float().unsqueeze(-1)
+    excluded = _mean_pool_categorical_bag(embedded, indices, lengths, "exclude")
+    torch.testing.assert_close(excluded.cpu(), torch.tensor(g["expected_exclude"]))
+
+
+def _bag(rng, B, dim, max_len, dtype, device, null_every=4):
+    lengths = rng.integers(0, max_len + 1, size=B)
+    n = int(lengths.sum())
+    ids = rng.integers(1, 1000, size=n)
+    ids[::null_every] = 0
+    emb = torch.from_numpy(rng.standard_normal((n, dim)).astype(np.float32)).to(device=device, dtype=dtype)
+    return emb, torch.from_numpy(ids).to(device), torch.from_numpy(lengths).to(device)
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+@pytest.mark.parametrize("dim", [1, 6, 16, 64, 200])
+@pytest.mark.parametrize("policy", ["exclude", "include_as_padding"])
+def test_flat_mean_pool_forward_backward_match_oracle(device, dtype, dim, policy):
+    announce("pool_flat", dtype, dim, policy)
+    rng = np.random.default_rng(dim * 7 + (policy == "exclude"))
+    emb, ids, lengths = _bag(rng, 300, dim, 33, dtype, device)
+    emb.requires_grad_(True)
+    out = _mean_pool_categorical_bag(emb, ids, lengths, policy)
+    assert out.shape == (300, dim) and out.dtype == dtype
+    e64 = emb.detach().float().cpu().numpy()
+    ref, _ = O.pool_rows(e64, ids.cpu().numpy(), lengths.cpu().numpy(), "mean", policy)
+    rtol, atol = TOL[dtype]
+    np.testing.assert_allclose(out.detach().float().cpu().numpy(), ref, rtol=rtol, atol=atol)
+    g = torch.randn(300, dim, device=device).to(dtype)
+    out.backward(g)
+    back = O.pool_rows_backward(ids.cpu().numpy(), lengths.cpu().numpy(), g.float().cpu().numpy(), "mean", policy)
+    np.testing.assert_allclose(emb.grad.float().cpu().numpy(), back, rtol=rtol, atol=atol)
+
+
+@pytest.mark.parametrize("mode", ["sum", "mean"])
+def test_pool_bags_sum_and_mean_adjoint(device, mode):
+    """The backward is the adjoint of the forward: <pool(E), G> = <E, dE>."""
+
+    announce("pool_adjoint", mode)
+    rng = np.random.default_rng(5)
+    emb, ids, lengths = _bag(rng, 4096, 64, 20, torch.float32, device)
+    emb.requires_grad_(True)
+    (out,) = pool_bags([(emb, ids, lengths, "exclude")], mode=mode)
+    g = torch.randn_like(out)
+    out.backward(g)
+    lhs = float((out.double() * g.double()).sum())
+    rhs = float((emb.detach().double() * emb.grad.double()).sum())
+    assert abs(lhs - rhs) <= 1e-4 * max(1.0, abs(lhs))
+    ref, _ = O.pool_rows(emb.detach().cpu().numpy(), ids.cpu().numpy(), lengths.cpu().numpy(), mode, "exclude")
+    np.testing.assert_allclose(out.detach().cpu().numpy(), ref, rtol=1e-5, atol=1e-5)
+
+
+@pytest.mark.parametrize("policy", ["exclude", "include_as_padding"])
+def test_padded_layout_matches_oracle_with_grad(device, policy):
+    announce("pool_padded", policy)
+    rng = np.random.default_rng(9)
+    B, L, D = 257, 9, 24
+    lengths = torch.from_numpy(rng.integers(0, L + 1, size=B)).to(device)
+    idx = torch.from_numpy(rng.integers(0, 5, size=(B, L))).to(device)
+    emb = torch.randn(B, L, D, device=device, requires_grad=True)
+    out = _mean_pool_categorical_bag(emb, idx, lengths, policy)
+    ref = O.pool_rows_padded(emb.detach().cpu().numpy(), idx.cpu().numpy(), lengths.cpu().numpy(), policy)
+    np.testing.assert_allclose(out.detach().cpu().numpy(), ref, rtol=1e-5, atol=1e-6)
+    g = torch.randn(B, D, device=device)
+    out.backward(g)
+    # the gradient of a padded slot is grad[b] / count_b when it counts, else 0
+    valid = (torch.arange(L, device=device)[None, :] < lengths[:, None]).cpu().numpy()
+    if policy == "exclude":
+        valid &= idx.cpu().numpy() != 0
+    cnt = np.maximum(valid.sum(1), 1)
+    expect = g.cpu().numpy()[:, None, :] * (valid / cnt[:, None])[..., None]
+    np.testing.assert_allclose(emb.grad.cpu().numpy(), expect, rtol=1e-6, atol=1e-7)
+
+
+def test_batch_flat_bags_one_launch_equals_single_bag_calls(device):
+    """Mixed dtypes, dims and policies in one call give the same bits as one
+    call per bag (a bag's summation order depends only on its own layout)."""
+
+    announce("pool_batch")
+    rng = np.random.default_rng(21)
+    bags = []
+    for k, (dim, dtype, policy) in enumerate(
+        [(16, torch.float32, "exclude"), (32, torch.bfloat16, "include_as_padding"), (7, torch.float32,
+         "include_as_padding"), (128, torch.bfloat16, "exclude"), (16, torch.float32, "exclude")]
+    ):
+        emb, ids, lengths = _bag(rng, 512, dim, 12, dtype, device)
+        bags.append((f"f{k}", emb, ids, lengths, policy))
+    # a zero-batch bag and a bag whose ids are all empty bags
+    bags.append(("empty_batch", torch.zeros(0, 8, device=device), torch.zeros(0, dtype=torch.long, device=device),
+                 torch.zeros(0, dtype=torch.long, device=device), "exclude"))
+    bags.append(("all_empty", torch.zeros(0, 8, device=device), torch.zeros(0, dtype=torch.long, device=device),
+                 torch.zeros(5, dtype=torch.long, device=device), "exclude"))
+    out = _batch_mean_pool_flat_bags(bags)
+    assert list(out) == [b[0] for b in bags]
+    for name, emb, ids, lengths, policy in bags:
+        single = _mean_pool_categorical_bag(emb, ids, lengths, policy)
+        assert out[name].shape == single.shape and out[name].dtype == emb.dtype
+        assert torch.equal(out[name], single), name
+    assert out["empty_batch"].shape == (0, 8)
+    assert torch.count_nonzero(out["all_empty"]) == 0 and out["all_empty"].shape == (5, 8)
+
+
+def test_errors_follow_the_reference(device):
+    announce("pool_errors")
+    emb = torch.randn(5, 4, device=device)
+    ids = torch.tensor([1, 2, 0, 3, 4], device=device)
+    with pytest.raises(ValueError, match="shape \\[B\\]"):
+        _mean_pool_categorical_bag(emb, ids, torch.ones(1, 5, dtype=torch.long, device=device), "exclude")
+    with pytest.raises(ValueError, match="null policy"):
+        _mean_pool_categorical_bag(emb, ids, torch.tensor([5], device=device), "drop")
+    with pytest.raises(ValueError, match="misaligned"):
+        _mean_pool_categorical_bag(emb[:4], ids, torch.tensor([5], device=device), "exclude")
+    with pytest.raises(ValueError, match="must be zero"):
+        _mean_pool_categorical_bag(emb, ids, torch.zeros(0, dtype=torch.long, device=device), "exclude")
+    with pytest.raises(ValueError, match="5 != sum\\(lengths\\) 4"):
+        _mean_pool_categorical_bag(emb, ids, torch.tensor([2, 2], device=device), "exclude")
+    with pytest.raises(ValueError, match="5 != sum\\(lengths\\) 7"):
+        _mean_pool_categorical_bag(emb, ids, torch.tensor([3, 4], device=device), "exclude")
+    with pytest.raises(ValueError, match="non-negative"):
+        _mean_pool_categorical_bag(emb, ids, torch.tensor([6, -1], device=device), "exclude")
+    with pytest.raises(ValueError, match="flat \\[N,D\\]"):
+        _mean_pool_categorical_bag(emb, ids.view(5, 1), torch.tensor([5], device=device), "exclude")
+    # deferred mode: no sync, the error surfaces at the next check
+    E.set_deferred_index_checks(True)
+    try:
+        _mean_pool_categorical_bag(emb, ids, torch.tensor([2, 2], device=device), "exclude")
+        with pytest.raises(IndexError):
+            E.check_index_errors()
+    finally:
+        E.set_deferred_index_checks(False)

@@ -112,6 +112,67 @@ def test_pool_matches_torch_embedding_bag(mode):
     np.testing.assert_allclose(got, ref.numpy(), rtol=1e-12, atol=1e-12)
 
 
+def test_pool_rows_golden_flat_and_padded():
+    g = GOLD["mean_pool_null_policies"]
+    idx = np.array(g["indices"])
+    emb = idx.astype(np.float64)[:, None]  # the embedded row of an id holds the id
+    ex, _ = O.pool_rows(emb, idx, np.array(g["lengths"]), "mean", "exclude")
+    inc, _ = O.pool_rows(emb, idx, np.array(g["lengths"]), "mean", "include_as_padding")
+    np.testing.assert_allclose(ex, g["expected_exclude"], rtol=1e-12)
+    np.testing.assert_allclose(inc, g["expected_include_as_padding"], rtol=1e-12)
+    p = GOLD["mean_pool_padded"]
+    pidx = np.array(p["indices"])
+    pad = O.pool_rows_padded(pidx.astype(np.float64)[..., None], pidx, np.array(p["lengths"]), "exclude")
+    np.testing.assert_allclose(pad, p["expected_exclude"], rtol=1e-12)
+
+
+@pytest.mark.parametrize("policy", ["exclude", "include_as_padding"])
+@pytest.mark.parametrize("mode", ["sum", "mean"])
+def test_pool_rows_match_embedding_bag_and_autograd(mode, policy):
+    """Rows pooled by position = F.embedding_bag over arange(N) with the null
+    weights as per-sample weights; the backward = its autograd."""
+
+    rng = np.random.default_rng(11)
+    B, dim = 48, 6
+    lengths = rng.integers(0, 7, size=B)
+    n = int(lengths.sum())
+    ids = rng.integers(0, 5, size=n)  # many nulls
+    emb = torch.from_numpy(rng.standard_normal((n, dim))).requires_grad_(True)
+    offs = O.offsets_of(lengths)
+    w = (ids != 0).astype(np.float64) if policy == "exclude" else np.ones(n)
+    cnt = np.add.reduceat(np.append(w, 0.0), offs[:-1])[:B] * (np.diff(offs) > 0)
+    den = np.maximum(cnt, 1.0) if mode == "mean" else np.ones(B)
+    seg = np.repeat(np.arange(B), np.diff(offs))
+    psw = torch.from_numpy(w / den[seg])
+    ref = F.embedding_bag(torch.arange(n), emb, torch.from_numpy(offs[:-1]), mode="sum", per_sample_weights=psw)
+    got, got_cnt = O.pool_rows(emb.detach().numpy(), ids, lengths, mode, policy)
+    np.testing.assert_allclose(got, ref.detach().numpy(), rtol=1e-12, atol=1e-12)
+    np.testing.assert_allclose(got_cnt, cnt, rtol=0, atol=0)
+    g = rng.standard_normal((B, dim))
+    ref.backward(torch.from_numpy(g))
+    back = O.pool_rows_backward(ids, lengths, g, mode, policy)
+    np.testing.assert_allclose(back, emb.grad.numpy(), rtol=1e-12, atol=1e-12)
+    # adjoint identity of the linear map E -> pool(E)
+    E = rng.standard_normal((n, dim))
+    lhs = float((O.pool_rows(E, ids, lengths, mode, policy)[0] * g).sum())
+    rhs = float((E * back).sum())
+    assert abs(lhs - rhs) <= 1e-10 * max(1.0, abs(lhs))
+
+
+def test_pool_rows_padded_equals_flat():
+    rng = np.random.default_rng(12)
+    B, L, dim = 20, 5, 3
+    lengths = rng.integers(0, L + 1, size=B)
+    idx = rng.integers(0, 4, size=(B, L))
+    emb = rng.standard_normal((B, L, dim))
+    for policy in ("exclude", "include_as_padding"):
+        pad = O.pool_rows_padded(emb, idx, lengths, policy)
+        flat_e = np.concatenate([emb[b, : lengths[b]] for b in range(B)])
+        flat_i = np.concatenate([idx[b, : lengths[b]] for b in range(B)])
+        flat, _ = O.pool_rows(flat_e, flat_i, lengths, "mean", policy)
+        np.testing.assert_allclose(pad, flat, rtol=1e-12, atol=1e-12)
+
+
 @pytest.mark.parametrize("policy", ["exclude", "include_as_padding"])
 @pytest.mark.parametrize("mode", ["sum", "mean", "none"])
 def test_per_id_grads_match_autograd(mode, policy):
@@ -280,3 +341,21 @@ def test_bf16_rounding_matches_torch():
     ours = O.f32_to_bf16_bits(x)
     theirs = torch.from_numpy(x).to(torch.bfloat16).view(torch.int16).numpy().view(np.uint16)
     assert np.array_equal(ours, theirs)
+
+
+@pytest.mark.parametrize("max_norm", [0.5, 1.0, 1e6])
+def test_clip_grad_norm_matches_torch_clip_grad_norm(max_norm):
+    rng = np.random.default_rng(31)
+    vals = [rng.standard_normal((int(rng.integers(1, 40)), 8)) * 0.1 for _ in range(5)]
+    params = [torch.nn.Parameter(torch.zeros(v.shape, dtype=torch.float64)) for v in vals]
+    for p, v in zip(params, vals):
+        p.grad = torch.from_numpy(v.copy())
+    ref_norm = torch.nn.utils.clip_grad_norm_(params, max_norm)
+    got, total, coef = O.clip_grad_norm(vals, max_norm)
+    assert abs(total - float(ref_norm)) <= 1e-12 * max(1.0, total)
+    for g, p in zip(got, params):
+        np.testing.assert_allclose(g, p.grad.numpy(), rtol=1e-12, atol=0)
+    if max_norm >= total:
+        assert coef == 1.0
+        for g, v in zip(got, vals):
+            np.testing.assert_array_equal(g, v)
