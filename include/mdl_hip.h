@@ -54,10 +54,14 @@ enum { MDL_BUCKET_PRE_HASHED = 0, MDL_BUCKET_MOD = 1 };
 
 /* Row-access classes of a feature or table: weight dtype x output/gradient
  * dtype x whether every row access is 16-byte aligned.  Kernels are
- * specialised per class; the calls taking a `classes` mask launch only the
- * classes whose bit (1 << class) is set, 0 meaning all.  mdl_feature_classes
- * and mdl_table_classes compute the mask of a host descriptor array with the
- * kernels' own rule; a mask that misses a present class skips its rows. */
+ * specialised per variant = class x lane width: a lane moves C elements of a
+ * row, C = 1 for the unaligned classes and otherwise one 16-byte vector of the
+ * weight type (4 fp32, 8 bf16) doubled up to 8 while four lanes do not cover
+ * the row and the doubled C divides dim; variant = 3*class + log2(C/4).  The
+ * calls taking a `classes` mask launch only the variants whose bit
+ * (1 << variant) is set, 0 meaning all.  mdl_feature_classes and
+ * mdl_table_classes compute the mask of a host descriptor array with the
+ * kernels' own rule; a mask that misses a present variant skips its rows. */
 enum {
   MDL_CLASS_F32_VEC = 0, MDL_CLASS_F32 = 1, MDL_CLASS_BF16_VEC = 2,
   MDL_CLASS_BF16 = 3, MDL_CLASS_BF16_F32_VEC = 4, MDL_CLASS_BF16_F32 = 5
@@ -159,7 +163,7 @@ int mdl_lengths_to_offsets(const int64_t* lengths, int64_t n, int64_t* offsets,
 
 /* -------------------------------------------------------------- planning --- */
 
-/* Host helpers: class masks (see MDL_CLASS_*) of host descriptor arrays. */
+/* Host helpers: variant masks (see MDL_CLASS_*) of host descriptor arrays. */
 uint32_t mdl_feature_classes(const mdl_feature* feats_host, int32_t num_features);
 uint32_t mdl_table_classes(const mdl_table* tables_host, int32_t num_tables);
 
@@ -281,7 +285,8 @@ int mdl_unique(const int64_t* ids, int64_t n, int32_t key_bits, int64_t* unique_
  * equal keys.  The num_tables tables (device array) are ordered by row_base,
  * cover every non-sentinel key, and their gradients are 16-byte aligned with
  * row strides that are multiples of 16 bytes whenever dim*sizeof(weight) is.
- * dim <= 64*16/sizeof(weight) (256 fp32, 512 bf16) and max_dim >= every dim.
+ * dim <= 64*C (C the table's lane width above; 512 when dim is a multiple
+ * of 8) and max_dim >= every dim.
  * The per-id gradient of a pooled id is grad[row b] / max(bag_count, 1) (mean)
  * or grad[row b] (sum, none); padding ids get none (src/model.py:564-570 and
  * the F.embedding sparse backward).  Duplicate ids are summed in input order

@@ -1,18 +1,26 @@
 // Backward of the grouped lookup: sort, unique and deterministic segment
 // reduction of per-id gradients, fused with the row-wise Adagrad update (or
-// writing a coalesced sparse gradient).
+// writing a coalesced sparse gradient, or only its squared norm).
 //
 // After the stable radix sort every distinct (table, row) is one run of equal
 // keys whose payloads (gradient rows) appear in input order.  The sorted
-// array is cut into chunks of <= kChunk entries that never straddle two
-// tables; one wavefront reduces one chunk with the same slot-parallel
-// segmented scan as the forward pooling.  A run that ends inside the chunk it
-// started in is finished there: its summed gradient goes straight into the
-// Adagrad update (weights and accumulator read and written once) or into the
-// coalesced gradient.  A run that crosses chunk boundaries (hot Zipf rows can
-// have 10^4+ entries) leaves one fp32 partial per chunk it touches; a second
-// kernel adds those partials in chunk order and finishes the run.  No
-// floating-point atomics are used, so results do not depend on scheduling.
+// array is cut into chunks of <= kChunkMax entries that never straddle two
+// tables, numbered so that the chunks of one kernel variant (row-access
+// class x lane width) are contiguous and each table's chunks consecutive.
+//
+// One wavefront reduces one chunk.  Its G = 64/L lane groups ("slots", L
+// lanes per row) each walk a contiguous slice of about kSlotRun entries,
+// accumulating the per-id gradients in registers: the gradient rows of the
+// slice are the only per-entry work, and a run that ends inside the slot that
+// began it is finished right there -- its summed gradient goes straight into
+// the Adagrad update, with the weight row and accumulator loaded alongside
+// the gradient rows (read and written once).  Runs that cross slot bounds are
+// joined once per chunk by a segmented scan over the slots' open partials.
+// A run that crosses chunk bounds (hot Zipf rows can have 10^4+ entries)
+// leaves one fp32 partial per chunk it touches; a second kernel adds those in
+// chunk order and finishes the run.  The summation order depends on the
+// chunk layout only, and no floating-point atomics are used, so results do
+// not depend on scheduling.
 #include "common.cuh"
 
 namespace mdl {
@@ -22,14 +30,22 @@ int sort_pairs(uint32_t* keys, uint32_t* vals, uint32_t* keys_alt, uint32_t* val
 size_t sort_ws_bytes(int64_t n);
 int launch_sum_partials(const float* partial, int64_t m, const int64_t* m_dev, float* out, hipStream_t s);
 
-constexpr int kChunkMax = 512;
+constexpr int kChunkMax = 512;    // entries of one chunk at most
+constexpr int kSlotRun = kPassesPerChunk;  // entries one slot walks in a full chunk
 constexpr int kBwdWaves = 4;
-constexpr int kPlanThreads = 1024;
+constexpr int kBoundThreads = 256;
 
 enum { kHeadOpen = 1, kTailOpen = 2, kSingle = 4 };
 // Adagrad: update the rows; Coalesce: write the coalesced gradient; Sumsq:
 // only the squared 2-norm of the coalesced gradient (for clipping).
 enum { kModeAdagrad = 0, kModeCoalesce = 1, kModeSumsq = 2 };
+
+// One chunk: entries [begin, begin + len) of the sorted array, all of table.
+struct ChunkDesc {
+  int32_t table;
+  int32_t len;
+  int64_t begin;
+};
 
 struct BwdWs {
   uint32_t* keys_alt;
@@ -38,8 +54,9 @@ struct BwdWs {
   size_t sort_bytes;
   int64_t* table_start;   // [T]
   int64_t* table_end;     // [T]
-  int64_t* chunk_base;    // [T+1]
-  int64_t* table_cb;      // [T] entries per chunk of table t
+  int64_t* chunk_base;    // [T]   first chunk of table t
+  int64_t* num_chunks;    // [1]
+  ChunkDesc* desc;        // [max_chunks]
   int32_t* chunk_flags;   // [max_chunks]
   int64_t* head_base;     // [max_chunks+1]
   void* scan_ws;
@@ -49,10 +66,10 @@ struct BwdWs {
   float* chunk_ss;        // [max_chunks] squared norms of the runs finished per chunk
 };
 
-// Chunks hold kPassesPerChunk passes of G rows; G >= 1, so a table of m
-// entries has at most ceil(m / kPassesPerChunk) chunks.
+// A chunk holds at least kSlotRun entries unless it is its table's last, so
+// a table of m entries has at most ceil(m / kSlotRun) chunks.
 static inline int64_t max_chunks_for(int64_t n, int32_t T) {
-  return (n + kPassesPerChunk - 1) / kPassesPerChunk + T + 1;
+  return (n + kSlotRun - 1) / kSlotRun + T + 1;
 }
 
 static size_t carve(BwdWs* w, void* base, int64_t n, int32_t T, int32_t max_dim) {
@@ -71,8 +88,9 @@ static size_t carve(BwdWs* w, void* base, int64_t n, int32_t T, int32_t max_dim)
   w->sort_ws = take(w->sort_bytes);
   w->table_start = (int64_t*)take((size_t)T * 8 + 8);
   w->table_end = (int64_t*)take((size_t)T * 8 + 8);
-  w->chunk_base = (int64_t*)take(((size_t)T + 1) * 8);
-  w->table_cb = (int64_t*)take((size_t)T * 8 + 8);
+  w->chunk_base = (int64_t*)take((size_t)T * 8 + 8);
+  w->num_chunks = (int64_t*)take(8);
+  w->desc = (ChunkDesc*)take((size_t)mc * sizeof(ChunkDesc));
   w->chunk_flags = (int32_t*)take((size_t)mc * 4);
   w->head_base = (int64_t*)take(((size_t)mc + 1) * 8);
   w->scan_bytes = mdl_offsets_workspace_bytes(mc);
@@ -83,129 +101,150 @@ static size_t carve(BwdWs* w, void* base, int64_t n, int32_t T, int32_t max_dim)
   return (size_t)(p - start);
 }
 
-// ------------------------------------------------------------------ plan --
-
-__device__ __forceinline__ int64_t lower_bound_u32(const uint32_t* a, int64_t n, uint64_t x) {
-  int64_t lo = 0, hi = n;
-  while (lo < hi) {
-    const int64_t mid = (lo + hi) >> 1;
-    if ((uint64_t)a[mid] < x) lo = mid + 1;
-    else hi = mid;
-  }
-  return lo;
-}
-
-// Whether a table's rows (and so its gradient and value rows, which the host
-// lays out alike) use 16-byte vectors, and the chunk length that gives one
-// wave kPassesPerChunk passes over it.
-__device__ __forceinline__ bool table_vec(const mdl_table& tb) {
-  return table_vec_of(tb.weight, tb.dim, tb.wdtype);
-}
-
-__device__ __forceinline__ int64_t table_chunk_len(const mdl_table& tb) {
-  const int c = table_vec(tb) ? (tb.wdtype == MDL_BF16 ? 8 : 4) : 1;
-  const int64_t g = kWave / lanes_for(tb.dim > 0 ? tb.dim : 1, c);
-  const int64_t cb = (int64_t)kPassesPerChunk * g;
-  return cb < kChunkMax ? cb : kChunkMax;
-}
-
-__global__ __launch_bounds__(kPlanThreads) void bwd_plan_kernel(const mdl_table* __restrict__ tables, int32_t T,
-                                                                 const uint32_t* __restrict__ keys, int64_t n,
-                                                                 int64_t* table_start, int64_t* table_end,
-                                                                 int64_t* chunk_base, int64_t* table_cb) {
-  __shared__ int64_t smem[kPlanThreads];
-  int64_t carry = 0;
-  for (int32_t base = 0; base < T; base += kPlanThreads) {
-    const int32_t t = base + threadIdx.x;
-    int64_t nch = 0;
-    if (t < T) {
-      const uint64_t lo_key = (uint64_t)tables[t].row_base;
-      const uint64_t hi_key = lo_key + (uint64_t)tables[t].num_rows;
-      const int64_t lo = lower_bound_u32(keys, n, lo_key);
-      const int64_t hi = lower_bound_u32(keys, n, hi_key);
-      table_start[t] = lo;
-      table_end[t] = hi;
-      const int64_t cb = table_chunk_len(tables[t]);
-      table_cb[t] = cb;
-      nch = (hi - lo + cb - 1) / cb;
-    }
-    smem[threadIdx.x] = nch;
-    __syncthreads();
-    for (int d = 1; d < kPlanThreads; d <<= 1) {
-      int64_t o = threadIdx.x >= d ? smem[threadIdx.x - d] : 0;
-      __syncthreads();
-      smem[threadIdx.x] += o;
-      __syncthreads();
-    }
-    if (t < T) chunk_base[t] = carry + smem[threadIdx.x] - nch;
-    carry += smem[kPlanThreads - 1];
-    __syncthreads();
-  }
-  if (threadIdx.x == 0) chunk_base[T] = carry;
-}
-
-// Heads (first entry of a run) per chunk, for the coalesced layout.
-struct ChunkRange {
-  int64_t c_begin, c_end, t_begin, t_end;
-  int32_t t;
-};
-
 __device__ __forceinline__ int64_t uni64b(int64_t v) {
   int lo = __builtin_amdgcn_readfirstlane((int)(v & 0xffffffff));
   int hi = __builtin_amdgcn_readfirstlane((int)(v >> 32));
   return (int64_t)(((uint64_t)(uint32_t)hi << 32) | (uint32_t)lo);
 }
 
-// Locate chunk c: returns false when c is past the last chunk.
-__device__ __forceinline__ bool find_chunk(int64_t c, int32_t T, const int64_t* chunk_base,
-                                           const int64_t* table_start, const int64_t* table_end,
-                                           const int64_t* table_cb, ChunkRange* r) {
-  const int64_t total = chunk_base[T];
-  if (c >= total) return false;
-  int32_t lo = 0, hi = T - 1;  // last t with chunk_base[t] <= c
-  while (lo < hi) {
-    const int32_t mid = (lo + hi + 1) >> 1;
-    if (chunk_base[mid] <= c) lo = mid;
-    else hi = mid - 1;
-  }
-  // Skip empty tables that share the same chunk_base.
-  while (lo + 1 <= T - 1 && chunk_base[lo + 1] <= c) ++lo;
-  r->t = __builtin_amdgcn_readfirstlane(lo);
-  r->t_begin = uni64b(table_start[lo]);
-  r->t_end = uni64b(table_end[lo]);
-  const int64_t cb = uni64b(table_cb[lo]);
-  r->c_begin = r->t_begin + (c - chunk_base[lo]) * cb;
-  r->c_end = r->c_begin + cb < r->t_end ? r->c_begin + cb : r->t_end;
-  r->c_begin = uni64b(r->c_begin);
-  r->c_end = uni64b(r->c_end);
-  return true;
+// ------------------------------------------------------------------ plan --
+
+__device__ __forceinline__ bool table_vec(const mdl_table& tb) {
+  return table_vec_of(tb.weight, tb.dim, tb.wdtype);
 }
 
-__global__ __launch_bounds__(256) void count_heads_kernel(int32_t T, const int64_t* chunk_base,
-                                                          const int64_t* table_start, const int64_t* table_end,
-                                                          const int64_t* table_cb,
+__device__ __forceinline__ int table_variant(const mdl_table& tb) {
+  return variant_of(tb.wdtype, tb.gdtype, table_vec(tb), tb.dim);
+}
+
+// Entries per chunk of a table: kSlotRun per slot, one slot per L lanes.
+__device__ __forceinline__ int64_t table_chunk_len(const mdl_table& tb) {
+  const int c = variant_elems(table_variant(tb));
+  const int64_t g = kWave / lanes_for(tb.dim > 0 ? tb.dim : 1, c);
+  const int64_t cb = (int64_t)kSlotRun * g;
+  return cb < kChunkMax ? cb : kChunkMax;
+}
+
+// Bounds of every table in the sorted keys: block 2t finds the first key >=
+// row_base[t], block 2t+1 the first key >= row_base[t] + num_rows.  A k-ary
+// search: each round the block probes 256 evenly spaced keys of the
+// remaining range, so 2^23 keys take three dependent loads instead of 23.
+__global__ __launch_bounds__(kBoundThreads) void bwd_bounds_kernel(const mdl_table* __restrict__ tables,
+                                                                   const uint32_t* __restrict__ keys, int64_t n,
+                                                                   int64_t* table_start, int64_t* table_end) {
+  const int32_t t = blockIdx.x >> 1;
+  const bool upper = blockIdx.x & 1;
+  const uint64_t key = (uint64_t)tables[t].row_base + (upper ? (uint64_t)tables[t].num_rows : 0ull);
+  int64_t lo = 0, hi = n;  // the answer lies in [lo, hi]
+  const int tid = threadIdx.x;
+  while (hi > lo) {
+    const int64_t span = hi - lo;
+    if (span <= kBoundThreads) {
+      const bool less = tid < span && (uint64_t)keys[lo + tid] < key;
+      lo += __syncthreads_count(less);
+      break;
+    }
+    // probe p_i = lo + span*(i+1)/(K+1), i < K; keys[p_i] < key holds for a prefix of i
+    const int64_t p = lo + span * (tid + 1) / (kBoundThreads + 1);
+    const int cnt = __syncthreads_count((uint64_t)keys[p] < key);
+    const int64_t nlo = cnt > 0 ? lo + span * cnt / (kBoundThreads + 1) + 1 : lo;
+    const int64_t nhi = cnt < kBoundThreads ? lo + span * (cnt + 1) / (kBoundThreads + 1) : hi;
+    lo = nlo;
+    hi = nhi;
+  }
+  if (tid == 0) (upper ? table_end : table_start)[t] = lo;
+}
+
+__device__ __forceinline__ int64_t wave_incl_scan(int64_t x) {
+  const int lane = lane_id();
+#pragma unroll
+  for (int d = 1; d < kWave; d <<= 1) {
+    const int lo = shfl_i((int)(x & 0xffffffff), lane >= d ? lane - d : lane);
+    const int hi = shfl_i((int)(x >> 32), lane >= d ? lane - d : lane);
+    const int64_t o = (int64_t)(((uint64_t)(uint32_t)hi << 32) | (uint32_t)lo);
+    if (lane >= d) x += o;
+  }
+  return x;
+}
+
+// Chunk numbering (one wavefront): table t's chunks are [chunk_base[t],
+// chunk_base[t] + n_t) in table order, so neighbouring chunks (one XCD's
+// range) share a table; *total = the number of chunks.
+__global__ __launch_bounds__(kWave) void bwd_number_kernel(const mdl_table* __restrict__ tables, int32_t T,
+                                                           const int64_t* __restrict__ table_start,
+                                                           const int64_t* __restrict__ table_end,
+                                                           int64_t* __restrict__ chunk_base,
+                                                           int64_t* __restrict__ total) {
+  const int lane = lane_id();
+  int64_t run = 0;
+  for (int32_t g = 0; g < T; g += kWave) {
+    const int32_t t = g + lane;
+    int64_t nch = 0;
+    if (t < T) {
+      const int64_t cb = table_chunk_len(tables[t]);
+      nch = (table_end[t] - table_start[t] + cb - 1) / cb;
+    }
+    const int64_t incl = wave_incl_scan(nch);
+    if (t < T) chunk_base[t] = run + incl - nch;
+    const int tlo = shfl_i((int)(incl & 0xffffffff), kWave - 1);
+    const int thi = shfl_i((int)(incl >> 32), kWave - 1);
+    run += (int64_t)(((uint64_t)(uint32_t)thi << 32) | (uint32_t)tlo);
+  }
+  if (lane == 0) *total = run;
+}
+
+// Descriptors of table t's chunks (block t).
+__global__ __launch_bounds__(256) void bwd_desc_kernel(const mdl_table* __restrict__ tables,
+                                                       const int64_t* __restrict__ table_start,
+                                                       const int64_t* __restrict__ table_end,
+                                                       const int64_t* __restrict__ chunk_base,
+                                                       ChunkDesc* __restrict__ desc) {
+  const int32_t t = blockIdx.x;
+  const int64_t lo = table_start[t], hi = table_end[t];
+  const int64_t cb = table_chunk_len(tables[t]);
+  const int64_t nch = (hi - lo + cb - 1) / cb;
+  const int64_t base = chunk_base[t];
+  for (int64_t j = threadIdx.x; j < nch; j += blockDim.x) {
+    const int64_t b = lo + j * cb;
+    ChunkDesc d;
+    d.table = t;
+    d.len = (int32_t)(hi - b < cb ? hi - b : cb);
+    d.begin = b;
+    desc[base + j] = d;
+  }
+}
+
+// Heads (first entry of a run) per chunk, for the coalesced layout.
+__global__ __launch_bounds__(256) void count_heads_kernel(const int64_t* __restrict__ num_chunks,
+                                                          const ChunkDesc* __restrict__ desc,
+                                                          const int64_t* __restrict__ table_start,
                                                           const uint32_t* __restrict__ keys, int64_t max_chunks,
                                                           int64_t* __restrict__ heads) {
   const int w = threadIdx.x / kWave, lane = lane_id();
   const int64_t c = uni64b((int64_t)blockIdx.x * 4 + w);
   if (c >= max_chunks) return;
-  ChunkRange r;
-  if (!find_chunk(c, T, chunk_base, table_start, table_end, table_cb, &r)) {
+  if (c >= *num_chunks) {
     if (lane == 0) heads[c] = 0;
     return;
   }
+  const ChunkDesc d = desc[c];
+  const int64_t t_begin = table_start[d.table];
   int cnt = 0;
-  for (int64_t e = r.c_begin + lane; e < r.c_end; e += kWave)
-    cnt += (e == r.t_begin || keys[e] != keys[e - 1]) ? 1 : 0;
+  for (int64_t e = d.begin + lane; e < d.begin + d.len; e += kWave)
+    cnt += (e == t_begin || keys[e] != keys[e - 1]) ? 1 : 0;
   for (int m = 1; m < kWave; m <<= 1) cnt += __shfl_xor(cnt, m);
   if (lane == 0) heads[c] = cnt;
 }
 
-__global__ void unique_range_kernel(int32_t T, const int64_t* chunk_base, const int64_t* head_base,
-                                    int64_t* unique_range) {
+__global__ void unique_range_end_kernel(int32_t T, const int64_t* table_start, const int64_t* table_end,
+                                        const int64_t* chunk_base, const int64_t* head_base,
+                                        const mdl_table* __restrict__ tables, int64_t* unique_range) {
   for (int32_t t = blockIdx.x * blockDim.x + threadIdx.x; t < T; t += gridDim.x * blockDim.x) {
+    const int64_t lo = table_start[t], hi = table_end[t];
+    const int64_t cb = table_chunk_len(tables[t]);
+    const int64_t nch = (hi - lo + cb - 1) / cb;
     unique_range[2 * t] = head_base[chunk_base[t]];
-    unique_range[2 * t + 1] = head_base[chunk_base[t + 1]];
+    unique_range[2 * t + 1] = head_base[chunk_base[t] + nch];
   }
 }
 
@@ -242,7 +281,8 @@ struct BwdArgs {
   const int64_t* table_start;
   const int64_t* table_end;
   const int64_t* chunk_base;
-  const int64_t* table_cb;
+  const int64_t* num_chunks;
+  const ChunkDesc* desc;
   int32_t* chunk_flags;
   const int64_t* head_base;
   float* part_first;
@@ -260,8 +300,7 @@ struct BwdArgs {
 
 // Feature that owns gradient payload p: the last feature whose
 // payload_base <= p (descriptors are ordered by payload_base).
-__device__ __forceinline__ int32_t feature_of(const BwdArgs& a, int32_t single, uint32_t p) {
-  if (single >= 0) return single;
+__device__ __forceinline__ int32_t feature_of(const BwdArgs& a, uint32_t p) {
   int32_t lo = 0, hi = a.F - 1;
   while (lo < hi) {
     const int32_t mid = (lo + hi + 1) >> 1;
@@ -281,6 +320,7 @@ struct Reducer {
   TW* W;
   float* state;
   int64_t row_base;
+  float inv_dim;
   // fields of the table's only feature (single >= 0)
   const TG* g_base;
   int64_t g_stride, pbase;
@@ -294,6 +334,7 @@ struct Reducer {
     W = (TW*)uni64b((int64_t)tb.weight);
     state = (float*)uni64b((int64_t)tb.state);
     row_base = uni64b(tb.row_base);
+    inv_dim = 1.f / (float)dim;  // exact for power-of-two dims
     L = lanes_for(dim, C);
     G = kWave / L;
     const int lane = lane_id();
@@ -317,12 +358,13 @@ struct Reducer {
   }
 
   // Gradient row of payload p and whether it is divided by its bag count.
+  template <bool kOne>
   __device__ __forceinline__ const TG* grad_row(uint32_t p, bool& mean) const {
-    if (single >= 0) {
+    if (kOne) {
       mean = g_mean;
       return g_base + ((int64_t)p - pbase) * g_stride;
     }
-    const mdl_feature& f = a.feats[feature_of(a, single, p)];
+    const mdl_feature& f = a.feats[feature_of(a, p)];
     mean = f.pooling == MDL_POOL_MEAN;
     return (const TG*)f.grad + ((int64_t)p - f.payload_base) * f.out_stride;
   }
@@ -338,18 +380,20 @@ struct Reducer {
   }
 
   // Finish the run of `key` with summed gradient v: the Adagrad update from
-  // the preloaded weight row w and accumulator acc0, or the coalesced row.
-  __device__ __forceinline__ void finish(uint32_t key, const float (&v)[C], float ss, float acc0, float (&w)[C],
-                                         int64_t uidx) const {
+  // the weight row w and accumulator acc0, or the coalesced row at uidx, or
+  // (Sumsq) only add its squared norm to ss_acc.
+  __device__ __forceinline__ void finish(uint32_t key, const float (&v)[C], float acc0, float (&w)[C], int64_t uidx,
+                                         float& ss_acc) const {
     const int64_t row = (int64_t)key - row_base;
     if (kMode == kModeAdagrad) {
+      const float ss = row_sumsq(v);
       // scale == 1 leaves every product exact, so unclipped steps are unchanged
-      const float acc = acc0 + (ss * (scale * scale)) / (float)dim;
+      const float acc = acc0 + (ss * (scale * scale)) * inv_dim;
       if (sub == 0) state[row] = acc;
-      const float inv = 1.f / (sqrtf(acc) + a.eps);
+      const float step = a.lr * __builtin_amdgcn_rcpf(sqrtf(acc) + a.eps);
       if (col_ok) {
 #pragma unroll
-        for (int k = 0; k < C; ++k) w[k] = w[k] - a.lr * ((v[k] * scale) * inv);
+        for (int k = 0; k < C; ++k) w[k] = w[k] - step * (v[k] * scale);
         RowIO<TW, C>::store(W + row * dim + col, w);
       }
     } else if (kMode == kModeCoalesce) {
@@ -358,200 +402,251 @@ struct Reducer {
       TW* vals = (TW*)a.values_addr[t];
       if (sub == 0) rows[local] = row;
       if (col_ok) RowIO<TW, C>::store(vals + local * dim + col, v);
+    } else {
+      const float ss = row_sumsq(v);
+      if (sub == 0) ss_acc += ss;
     }
   }
 };
 
 // Keys and payloads of the chunk a wave reduces, staged in LDS: entry i of
-// the chunk is s_key[i + 1]; s_key[0] and s_key[len + 1] hold the keys just
-// before and after the chunk inside its table (kNone at a table edge).
+// the chunk is key[i + 1]; key[0] and key[len + 1] hold the keys just before
+// and after the chunk inside its table (kNone at a table edge).  hc[i] counts
+// the runs that begin in entries [0, i) (coalesced layout only).
 struct ChunkStage {
   uint32_t key[kChunkMax + 2];
   uint32_t pay[kChunkMax];
+  uint16_t hc[kChunkMax + 1];
 };
 
-template <int kMode, bool kOneFeature, typename TW, typename TG, int C>
-__device__ __forceinline__ void reduce_chunk_body(const BwdArgs& a, int64_t c, const ChunkRange& r,
+template <int C>
+__device__ __forceinline__ void zero(float (&v)[C]) {
+#pragma unroll
+  for (int k = 0; k < C; ++k) v[k] = 0.f;
+}
+
+template <int kMode, bool kOne, typename TW, typename TG, int C>
+__device__ __forceinline__ void reduce_chunk_body(const BwdArgs& a, int64_t c, const ChunkDesc& d,
                                                   const Reducer<kMode, TW, TG, C>& R, const ChunkStage& st) {
-  // Pass groups per iteration: 16 columns of loads in flight per lane.
-  constexpr int U = C >= 8 ? 2 : 4;
+  // Entries per slot per iteration: about 32 elements of loads in flight per lane.
+  constexpr int U = unroll_for<C>();
   constexpr bool adagrad = kMode == kModeAdagrad;
   constexpr bool coalesce = kMode == kModeCoalesce;
-  constexpr bool sumsq = kMode == kModeSumsq;
-  float ss_acc = 0.f;  // Sumsq: squared norms of the runs this lane's slot finishes
-  const int lane = lane_id();
   const uint32_t kNone = 0xffffffffu;
-  const int len = (int)(r.c_end - r.c_begin);
+  const int lane = lane_id();
+  const int len = d.len;
+  const int G = R.G, L = R.L, slot = R.slot;
   const bool head_open = st.key[0] == st.key[1];
   const bool tail_open = st.key[len + 1] == st.key[len];
-  const uint32_t first_key = st.key[1];
-  const bool single = head_open && tail_open && first_key == st.key[len];
-  const uint64_t lt_mask = (lane == 0) ? 0ull : (~0ull >> (64 - lane));
-  int64_t heads_before = coalesce ? a.head_base[c] : 0;
+  const int64_t hb = coalesce ? a.head_base[c] : 0;
+  // This slot's slice [s0, s1) of the chunk.
+  // Slices of an odd length start on distinct LDS banks.
+  const int K = ((len + G - 1) / G) | 1;
+  const int s0 = slot * K;
+  const int s1 = s0 + K < len ? s0 + K : len;
+  // The slice continues a run that began before it.
+  const bool cont = s0 < len && st.key[s0] == st.key[s0 + 1];
 
-  float carry[C];
-#pragma unroll
-  for (int k = 0; k < C; ++k) carry[k] = 0.f;
-  uint32_t carry_key = kNone;
-  const int G = R.G, L = R.L, slot = R.slot, sub = R.sub;
+  float acc[C], hp[C];
+  zero(acc);
+  zero(hp);
+  float ss_acc = 0.f;
+  int hend = -1;      // entry where this slot's first run ends, when that run began before the slice
+  bool ended = false;  // a run ended inside the slice
 
-  for (int base = 0; base < len; base += G * U) {
+  for (int j = s0; j < s1; j += U) {
     float v[U][C], w[U][C], acc0[U], cnt[U];
-    uint32_t key[U], pay[U];
-    bool fin[U], head[U], own[U], mean[U];
+    uint32_t key[U];
+    bool fin[U], own[U], mean[U], valid[U];
     const TG* gp[U];
+    bool e = ended;
 #pragma unroll
     for (int u = 0; u < U; ++u) {
-      const int i = base + u * G + slot;
-      const bool valid = i < len;
-      const int ii = valid ? i : 0;
-      key[u] = valid ? st.key[ii + 1] : kNone;
-      pay[u] = st.pay[ii];
-      const uint32_t next = st.key[ii + 2];
-      fin[u] = valid && next != key[u];
-      head[u] = coalesce && valid && st.key[ii] != key[u] &&
-                (i > 0 || r.c_begin == r.t_begin || !head_open);
-      if (coalesce && valid && i == 0 && r.c_begin == r.t_begin) head[u] = true;
-      own[u] = fin[u] && !(head_open && key[u] == first_key);  // the run finishes in this chunk
-      if (kOneFeature) {
-        mean[u] = R.g_mean;
-        gp[u] = valid && R.col_ok ? R.g_base + ((int64_t)pay[u] - R.pbase) * R.g_stride + R.col : zero_row<TG>();
-      } else {
-        mean[u] = false;
-        gp[u] = valid && R.col_ok ? R.grad_row(pay[u], mean[u]) + R.col : zero_row<TG>();
-      }
+      const int i = j + u;
+      valid[u] = i < s1;
+      const int ii = valid[u] ? i : s0;
+      key[u] = st.key[ii + 1];
+      const uint32_t pay = st.pay[ii];
+      fin[u] = valid[u] && st.key[ii + 2] != key[u];
+      own[u] = fin[u] && (!cont || e);  // the run began inside the slice
+      e = e || fin[u];
+      mean[u] = false;
+      gp[u] = valid[u] && R.col_ok ? R.template grad_row<kOne>(pay, mean[u]) + R.col : zero_row<TG>();
+      cnt[u] = 0.f;
+      if (mean[u]) cnt[u] = a.bag_count[pay];
     }
-    // Every global load of the group, back to back: gradient rows, bag
-    // counts and, for runs that finish here, the weight row and accumulator.
+    // Every global load of the group, back to back: gradient rows and, for
+    // runs that finish here, the weight row and accumulator.
 #pragma unroll
     for (int u = 0; u < U; ++u) {
       RowIO<TG, C>::load(gp[u], v[u]);
-      cnt[u] = *(mean[u] ? a.bag_count + pay[u] : zero_row<float>());
       if (adagrad) {
         const int64_t row = (int64_t)key[u] - R.row_base;
         RowIO<TW, C>::load(own[u] && R.col_ok ? R.W + row * R.dim + R.col : zero_row<TW>(), w[u]);
         acc0[u] = *(own[u] ? R.state + row : zero_row<float>());
       } else {
-#pragma unroll
-        for (int k = 0; k < C; ++k) w[u][k] = 0.f;
+        zero(w[u]);
         acc0[u] = 0.f;
       }
     }
 #pragma unroll
     for (int u = 0; u < U; ++u) {
-      const float inv = mean[u] ? 1.f / fmaxf(cnt[u], 1.f) : 1.f;
+      if (!valid[u]) continue;
+      const float inv = mean[u] ? __builtin_amdgcn_rcpf(fmaxf(cnt[u], 1.f)) : 1.f;
 #pragma unroll
-      for (int k = 0; k < C; ++k) v[u][k] *= inv;
-    }
-#pragma unroll
-    for (int u = 0; u < U; ++u) {
-      for (int d = 1; d < G; d <<= 1) {
-        const int src = slot >= d ? lane - d * L : lane;
-        const uint32_t okey = shfl_u(key[u], src);
-        float ov[C];
-#pragma unroll
-        for (int k = 0; k < C; ++k) ov[k] = shfl_f(v[u][k], src);
-        if (slot >= d && okey == key[u]) {
-#pragma unroll
-          for (int k = 0; k < C; ++k) v[u][k] += ov[k];
-        }
-      }
-      if (key[u] == carry_key && key[u] != kNone) {
-#pragma unroll
-        for (int k = 0; k < C; ++k) v[u][k] += carry[k];
-      }
-      // Distinct-row index of this entry's run (coalesced layout only).
-      int64_t uidx = 0;
-      if (coalesce) {
-        const uint64_t hm = __ballot(head[u] && sub == 0);
-        uidx = heads_before + (int64_t)__popcll(hm & (lt_mask | (1ull << lane))) - 1;
-        heads_before += __popcll(hm);
-      }
-      const float ss = R.row_sumsq(v[u]);
+      for (int k = 0; k < C; ++k) acc[k] = fmaf(v[u][k], inv, acc[k]);
       if (fin[u]) {
-        if (!own[u]) {
-          if (R.col_ok) {
-            float* pf = a.part_first + c * a.max_dim + R.col;
-#pragma unroll
-            for (int k = 0; k < C; ++k) pf[k] = v[u][k];
-          }
-        } else if (sumsq) {
-          if (sub == 0) ss_acc += ss;
+        if (own[u]) {
+          R.finish(key[u], acc, acc0[u], w[u], coalesce ? hb + (int64_t)st.hc[j + u + 1] - 1 : 0, ss_acc);
         } else {
-          R.finish(key[u], v[u], ss, acc0[u], w[u], uidx);
-        }
-      }
-      const int src = (G - 1) * L + sub;
-      const uint32_t lkey = shfl_u(key[u], src);
-      const int lfin = shfl_i((int)fin[u], src);
 #pragma unroll
-      for (int k = 0; k < C; ++k) carry[k] = shfl_f(v[u][k], src);
-      carry_key = (lkey != kNone && !lfin) ? lkey : kNone;
+          for (int k = 0; k < C; ++k) hp[k] = acc[k];
+          hend = j + u;
+        }
+        zero(acc);
+      }
+    }
+    ended = e;
+  }
+
+  // Join the runs that cross slot bounds.  Slot s exports o = the partial of
+  // the run open at its end; a slice inside one run (cont, no end) passes the
+  // previous slot's export through: o[s] = acc[s] + pass[s] * o[s-1].  The
+  // inclusive scan also tells whether that run began before the chunk.
+  float o[C];
+#pragma unroll
+  for (int k = 0; k < C; ++k) o[k] = acc[k];
+  bool pass = s0 < len && cont && !ended;
+  for (int dd = 1; dd < G; dd <<= 1) {
+    const int src = slot >= dd ? lane - dd * L : lane;
+    const int opass = shfl_i((int)pass, src);
+    float ov[C];
+#pragma unroll
+    for (int k = 0; k < C; ++k) ov[k] = shfl_f(o[k], src);
+    if (slot >= dd) {
+      if (pass) {
+#pragma unroll
+        for (int k = 0; k < C; ++k) o[k] += ov[k];
+      }
+      pass = pass && opass;
     }
   }
-  if (tail_open && slot == 0 && R.col_ok) {
+  // The previous slot's export (the part of this slot's first run before it).
+  float in[C];
+  const int prev = slot > 0 ? lane - L : lane;
+#pragma unroll
+  for (int k = 0; k < C; ++k) in[k] = shfl_f(o[k], prev);
+  // (Every lane takes part in the permute: a source lane outside EXEC reads as 0.)
+  const int prev_pass = shfl_i((int)pass, prev);
+  const bool in_from_head = slot > 0 ? prev_pass != 0 : head_open;
+  if (slot == 0) zero(in);
+
+  if (hend >= 0) {
+    // The first run of a continuing slice ends inside it.
+    float tot[C];
+#pragma unroll
+    for (int k = 0; k < C; ++k) tot[k] = in[k] + hp[k];
+    if (in_from_head) {
+      // it began in an earlier chunk: the fix-up kernel finishes it
+      if (R.col_ok) {
+        float* pf = a.part_first + c * a.max_dim + R.col;
+#pragma unroll
+        for (int k = 0; k < C; ++k) pf[k] = tot[k];
+      }
+    } else {
+      const uint32_t key = st.key[hend + 1];
+      const int64_t row = (int64_t)key - R.row_base;
+      float w[C];
+      float acc0 = 0.f;
+      zero(w);
+      if (adagrad) {
+        if (R.col_ok) RowIO<TW, C>::load(R.W + row * R.dim + R.col, w);
+        acc0 = R.state[row];
+      }
+      R.finish(key, tot, acc0, w, coalesce ? hb + (int64_t)st.hc[hend + 1] - 1 : 0, ss_acc);
+    }
+  }
+  // The run open at the chunk's end continues in the next chunk.
+  const int last = (len - 1) / K;
+  if (tail_open && slot == last && R.col_ok) {
     float* pl = a.part_last + c * a.max_dim + R.col;
 #pragma unroll
-    for (int k = 0; k < C; ++k) pl[k] = carry[k];
+    for (int k = 0; k < C; ++k) pl[k] = o[k];
   }
-  if (sumsq) {
+  if (kMode == kModeSumsq) {
     for (int m = 1; m < kWave; m <<= 1) ss_acc += shfl_f(ss_acc, lane ^ m);
     if (lane == 0) a.chunk_ss[c] = ss_acc;
   }
+  const bool single = head_open && tail_open && st.key[1] == st.key[len];
+  (void)kNone;
   if (lane == 0) a.chunk_flags[c] = (head_open ? kHeadOpen : 0) | (tail_open ? kTailOpen : 0) | (single ? kSingle : 0);
 }
 
 template <int kMode, typename TW, typename TG, int C>
-__device__ __forceinline__ void reduce_chunk(const BwdArgs& a, int64_t c, const ChunkRange& r, ChunkStage& st) {
-  Reducer<kMode, TW, TG, C> R(a, r.t);
+__device__ __forceinline__ void reduce_chunk(const BwdArgs& a, int64_t c, const ChunkDesc& d, ChunkStage& st) {
+  Reducer<kMode, TW, TG, C> R(a, d.table);
   if (R.dim > kWave * C) return;  // rejected on the host; never reached
   const int lane = lane_id();
   const uint32_t kNone = 0xffffffffu;
-  const int len = (int)(r.c_end - r.c_begin);
+  const int len = d.len;
+  const int64_t t_begin = uni64b(a.table_start[d.table]);
+  const int64_t t_end = uni64b(a.table_end[d.table]);
   for (int i = lane; i < len; i += kWave) {
-    st.key[i + 1] = a.keys[r.c_begin + i];
-    st.pay[i] = a.vals[r.c_begin + i];
+    st.key[i + 1] = a.keys[d.begin + i];
+    st.pay[i] = a.vals[d.begin + i];
   }
   if (lane == 0) {
-    st.key[0] = r.c_begin > r.t_begin ? a.keys[r.c_begin - 1] : kNone;
-    st.key[len + 1] = r.c_end < r.t_end ? a.keys[r.c_end] : kNone;
+    st.key[0] = d.begin > t_begin ? a.keys[d.begin - 1] : kNone;
+    st.key[len + 1] = d.begin + len < t_end ? a.keys[d.begin + len] : kNone;
   }
   __builtin_amdgcn_wave_barrier();
   __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
-  if (R.single >= 0) reduce_chunk_body<kMode, true, TW, TG, C>(a, c, r, R, st);
-  else reduce_chunk_body<kMode, false, TW, TG, C>(a, c, r, R, st);
+  if (kMode == kModeCoalesce) {
+    // hc[i]: runs beginning in entries [0, i)
+    const uint64_t lt = lane == 0 ? 0ull : (~0ull >> (kWave - lane));
+    int run = 0;
+    if (lane == 0) st.hc[0] = 0;
+    for (int b = 0; b < len; b += kWave) {
+      const int i = b + lane;
+      const bool head = i < len && st.key[i] != st.key[i + 1];
+      const uint64_t m = __ballot(head);
+      if (i < len) st.hc[i + 1] = (uint16_t)(run + __popcll(m & (lt | (1ull << lane))));
+      run += __popcll(m);
+    }
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
+  }
+  if (R.single >= 0) reduce_chunk_body<kMode, true, TW, TG, C>(a, c, d, R, st);
+  else reduce_chunk_body<kMode, false, TW, TG, C>(a, c, d, R, st);
 }
 
 template <int kMode, typename TW, typename TG, int C>
-__device__ __forceinline__ void fixup_chunk(const BwdArgs& a, int64_t c, const ChunkRange& r) {
-  const int32_t flags = __builtin_amdgcn_readfirstlane(a.chunk_flags[c]);
-  if (!(flags & kHeadOpen) || (flags & kSingle)) return;
-  Reducer<kMode, TW, TG, C> R(a, r.t);
+__device__ __forceinline__ void fixup_chunk(const BwdArgs& a, int64_t c, const ChunkDesc& d, int32_t flags) {
+  Reducer<kMode, TW, TG, C> R(a, d.table);
   if (R.dim > kWave * C) return;  // rejected on the host; never reached
   // Walk back over chunks that lie wholly inside the run to the chunk holding
   // its first entry (never past the table's first chunk).
-  const int64_t first_chunk = a.chunk_base[r.t];
+  const int64_t first_chunk = uni64b(a.chunk_base[d.table]);
   int64_t s = c - 1;
   while (s > first_chunk && (__builtin_amdgcn_readfirstlane(a.chunk_flags[s]) & kSingle)) --s;
   float v[C];
-#pragma unroll
-  for (int k = 0; k < C; ++k) v[k] = 0.f;
+  zero(v);
   if (R.col_ok) {
     // Partials of the chunks the run covers, added in chunk order; loads
     // are issued eight chunks at a time.
     int64_t q = s;
     for (; q + 8 <= c; q += 8) {
-      float t[8][C];
+      float tt[8][C];
 #pragma unroll
       for (int j = 0; j < 8; ++j) {
         const float* pl = a.part_last + (q + j) * a.max_dim + R.col;
 #pragma unroll
-        for (int k = 0; k < C; ++k) t[j][k] = pl[k];
+        for (int k = 0; k < C; ++k) tt[j][k] = pl[k];
       }
 #pragma unroll
       for (int j = 0; j < 8; ++j)
 #pragma unroll
-        for (int k = 0; k < C; ++k) v[k] += t[j][k];
+        for (int k = 0; k < C; ++k) v[k] += tt[j][k];
     }
     for (; q < c; ++q) {
       const float* pl = a.part_last + q * a.max_dim + R.col;
@@ -562,49 +657,55 @@ __device__ __forceinline__ void fixup_chunk(const BwdArgs& a, int64_t c, const C
 #pragma unroll
     for (int k = 0; k < C; ++k) v[k] += pf[k];
   }
-  const float ss = R.row_sumsq(v);
-  const uint32_t key = a.keys[r.c_begin];
+  const uint32_t key = a.keys[d.begin];
   const int64_t uidx = kMode == kModeCoalesce ? a.head_base[c] - 1 : 0;
   float w[C];
   float acc0 = 0.f;
-#pragma unroll
-  for (int k = 0; k < C; ++k) w[k] = 0.f;
+  zero(w);
   if (kMode == kModeAdagrad && R.slot == 0) {
     const int64_t row = (int64_t)key - R.row_base;
     if (R.col_ok) RowIO<TW, C>::load(R.W + row * R.dim + R.col, w);
     acc0 = R.state[row];
   }
+  float ss = 0.f;
+  if (R.slot == 0) R.finish(key, v, acc0, w, uidx, ss);
   if (kMode == kModeSumsq) {
     // The reduce of chunk c wrote its own runs' share before this launch.
     if (lane_id() == 0) a.chunk_ss[c] += ss;
-  } else if (R.slot == 0) {
-    R.finish(key, v, ss, acc0, w, uidx);
   }
+  (void)flags;
 }
 
-template <bool kFixup, int kMode, typename TW, typename TG, int C>
+template <bool kFixup, int kMode, typename TW, typename TG, bool kVec>
 __global__ __launch_bounds__(kBwdWaves * kWave) void bwd_reduce_kernel(BwdArgs a) {
   const int w = threadIdx.x / kWave;
-  // The grid covers the worst-case chunk count; only the first `real` blocks
-  // have work.  They are spread round-robin over the XCDs by the hardware, and
-  // remapped so that each XCD takes one contiguous range of chunks.
-  const int64_t total = uni64b(a.chunk_base[a.T]);
+  // One wave per chunk.  The grid covers the worst-case chunk count; only the
+  // first `real` blocks have work (the rest return at once).  The hardware
+  // deals blocks round-robin to the XCDs; they are remapped so that each XCD
+  // takes one contiguous range of chunks, whose rows and gradient slices then
+  // share that XCD's L2.
+  const int64_t total = uni64b(*a.num_chunks);
   const int64_t real = (total + kBwdWaves - 1) / kBwdWaves;
   if ((int64_t)blockIdx.x >= real) return;
   const int64_t blk = xcd_block(blockIdx.x, real);
   const int64_t c = uni64b(blk * kBwdWaves + w);
   if (c >= total) return;
-  ChunkRange r;
-  if (!find_chunk(c, a.T, a.chunk_base, a.table_start, a.table_end, a.table_cb, &r)) return;
-  const mdl_table& tb = a.tables[r.t];
-  const int cls = row_class(__builtin_amdgcn_readfirstlane(tb.wdtype), __builtin_amdgcn_readfirstlane(tb.gdtype),
-                            table_vec(tb));
-  if (cls != ClassOf<TW, TG, C>::value) return;  // another class's launch owns it
+  int32_t flags = 0;
   if (kFixup) {
-    fixup_chunk<kMode, TW, TG, C>(a, c, r);
+    flags = __builtin_amdgcn_readfirstlane(a.chunk_flags[c]);
+    if (!(flags & kHeadOpen) || (flags & kSingle)) return;
+  }
+  ChunkDesc d;
+  d.table = __builtin_amdgcn_readfirstlane(a.desc[c].table);
+  d.len = __builtin_amdgcn_readfirstlane(a.desc[c].len);
+  d.begin = uni64b(a.desc[c].begin);
+  const int v = table_variant(a.tables[d.table]);
+  if (v / kWidths != ClassOf<TW, TG, kVec>::value) return;  // another class's launch owns it
+  if (kFixup) {
+    with_width<TW, kVec>(v % kWidths, [&]<int C>() { fixup_chunk<kMode, TW, TG, C>(a, c, d, flags); });
   } else {
     __shared__ ChunkStage stage[kBwdWaves];
-    reduce_chunk<kMode, TW, TG, C>(a, c, r, stage[w]);
+    with_width<TW, kVec>(v % kWidths, [&]<int C>() { reduce_chunk<kMode, TW, TG, C>(a, c, d, stage[w]); });
   }
 }
 
@@ -614,6 +715,19 @@ static int validate_tables(const char* who, int32_t T, int32_t max_dim, int64_t 
   if (T <= 0) return fail(MDL_ERR_INVALID, std::string(who) + ": need at least one table");
   if (max_dim <= 0) return fail(MDL_ERR_INVALID, std::string(who) + ": max_dim must be positive");
   if (n < 0 || n > 0xffffffffll) return fail(MDL_ERR_UNSUPPORTED, std::string(who) + ": n outside [0, 2^32)");
+  return MDL_OK;
+}
+
+static int plan(const mdl_table* tables, int32_t T, const uint32_t* sk, int64_t n, const BwdWs& w, hipStream_t s) {
+  hipLaunchKernelGGL(bwd_bounds_kernel, dim3((unsigned)(2 * T)), dim3(kBoundThreads), 0, s, tables, sk, n,
+                     w.table_start, w.table_end);
+  MDL_CHECK_LAUNCH("bwd_bounds_kernel");
+  hipLaunchKernelGGL(bwd_number_kernel, dim3(1), dim3(kWave), 0, s, tables, T, w.table_start, w.table_end,
+                     w.chunk_base, w.num_chunks);
+  MDL_CHECK_LAUNCH("bwd_number_kernel");
+  hipLaunchKernelGGL(bwd_desc_kernel, dim3((unsigned)T), dim3(256), 0, s, tables, w.table_start, w.table_end,
+                     w.chunk_base, w.desc);
+  MDL_CHECK_LAUNCH("bwd_desc_kernel");
   return MDL_OK;
 }
 
@@ -627,10 +741,7 @@ static int prepare(const mdl_table* tables, int32_t T, int32_t max_dim, uint32_t
   if (rc) return rc;
   *sk = in_alt ? w->keys_alt : keys;
   *sv = in_alt ? w->vals_alt : payload;
-  hipLaunchKernelGGL(bwd_plan_kernel, dim3(1), dim3(kPlanThreads), 0, s, tables, T, *sk, n, w->table_start,
-                     w->table_end, w->chunk_base, w->table_cb);
-  MDL_CHECK_LAUNCH("bwd_plan_kernel");
-  return MDL_OK;
+  return plan(tables, T, *sk, n, *w, s);
 }
 
 static void fill_args(BwdArgs* a, const mdl_feature* feats, int32_t F, const mdl_table* tables, int32_t T,
@@ -646,7 +757,8 @@ static void fill_args(BwdArgs* a, const mdl_feature* feats, int32_t F, const mdl
   a->table_start = w.table_start;
   a->table_end = w.table_end;
   a->chunk_base = w.chunk_base;
-  a->table_cb = w.table_cb;
+  a->num_chunks = w.num_chunks;
+  a->desc = w.desc;
   a->chunk_flags = w.chunk_flags;
   a->head_base = w.head_base;
   a->part_first = w.part_first;
@@ -663,39 +775,35 @@ static void fill_args(BwdArgs* a, const mdl_feature* feats, int32_t F, const mdl
   a->unique_range = nullptr;
 }
 
-template <bool kFixup, typename TW, typename TG, int C>
-static int launch_reduce(const BwdArgs& a, uint32_t classes, hipStream_t s) {
-  if (classes != 0 && !(classes & (1u << ClassOf<TW, TG, C>::value))) return MDL_OK;
-  const int64_t blocks = (a.max_chunks + kBwdWaves - 1) / kBwdWaves;
-  if (a.mode == kModeAdagrad)
-    hipLaunchKernelGGL((bwd_reduce_kernel<kFixup, kModeAdagrad, TW, TG, C>), dim3((unsigned)blocks),
-                       dim3(kBwdWaves * kWave), 0, s, a);
-  else if (a.mode == kModeCoalesce)
-    hipLaunchKernelGGL((bwd_reduce_kernel<kFixup, kModeCoalesce, TW, TG, C>), dim3((unsigned)blocks),
-                       dim3(kBwdWaves * kWave), 0, s, a);
-  else
-    hipLaunchKernelGGL((bwd_reduce_kernel<kFixup, kModeSumsq, TW, TG, C>), dim3((unsigned)blocks),
-                       dim3(kBwdWaves * kWave), 0, s, a);
-  MDL_CHECK_LAUNCH(kFixup ? "bwd_fixup_kernel" : "bwd_reduce_kernel");
-  return MDL_OK;
-}
-
 template <bool kFixup>
-static int launch_all(const BwdArgs& a, uint32_t classes, hipStream_t s) {
-  int rc = launch_reduce<kFixup, float, float, 4>(a, classes, s);
-  if (!rc) rc = launch_reduce<kFixup, float, float, 1>(a, classes, s);
-  if (!rc) rc = launch_reduce<kFixup, bf16_t, bf16_t, 8>(a, classes, s);
-  if (!rc) rc = launch_reduce<kFixup, bf16_t, bf16_t, 1>(a, classes, s);
-  if (!rc) rc = launch_reduce<kFixup, bf16_t, float, 8>(a, classes, s);
-  if (!rc) rc = launch_reduce<kFixup, bf16_t, float, 1>(a, classes, s);
-  return rc;
-}
+struct LaunchReduce {
+  const BwdArgs& a;
+  hipStream_t s;
+  int64_t grid_blocks;
+  template <typename TW, typename TG, bool kVec>
+  int operator()() const {
+    const int64_t blocks = grid_blocks;
+    if (a.mode == kModeAdagrad)
+      hipLaunchKernelGGL((bwd_reduce_kernel<kFixup, kModeAdagrad, TW, TG, kVec>), dim3((unsigned)blocks),
+                         dim3(kBwdWaves * kWave), 0, s, a);
+    else if (a.mode == kModeCoalesce)
+      hipLaunchKernelGGL((bwd_reduce_kernel<kFixup, kModeCoalesce, TW, TG, kVec>), dim3((unsigned)blocks),
+                         dim3(kBwdWaves * kWave), 0, s, a);
+    else
+      hipLaunchKernelGGL((bwd_reduce_kernel<kFixup, kModeSumsq, TW, TG, kVec>), dim3((unsigned)blocks),
+                         dim3(kBwdWaves * kWave), 0, s, a);
+    MDL_CHECK_LAUNCH(kFixup ? "bwd_fixup_kernel" : "bwd_reduce_kernel");
+    return MDL_OK;
+  }
+};
 
 // Every reduce launch (all classes) before any fix-up launch: a fix-up reads
 // partials that the reduce of the same table wrote.
-static int run_reduce(const BwdArgs& a, uint32_t classes, hipStream_t s) {
-  int rc = launch_all<false>(a, classes, s);
-  if (!rc) rc = launch_all<true>(a, classes, s);
+static int run_reduce(const BwdArgs& a, uint32_t variants, hipStream_t s) {
+  const int64_t blocks = (a.max_chunks + kBwdWaves - 1) / kBwdWaves;
+  if (blocks > 0x7fffffffll) return fail(MDL_ERR_UNSUPPORTED, "backward: too many chunks");
+  int rc = for_each_class(variants, LaunchReduce<false>{a, s, blocks});
+  if (!rc) rc = for_each_class(variants, LaunchReduce<true>{a, s, blocks});
   return rc;
 }
 
@@ -722,7 +830,7 @@ uint32_t mdl_table_classes(const mdl_table* tables, int32_t num_tables) {
   uint32_t m = 0;
   for (int32_t i = 0; i < num_tables; ++i) {
     const mdl_table& t = tables[i];
-    m |= 1u << row_class(t.wdtype, t.gdtype, table_vec_of(t.weight, t.dim, t.wdtype));
+    m |= 1u << variant_of(t.wdtype, t.gdtype, table_vec_of(t.weight, t.dim, t.wdtype), t.dim);
   }
   return m;
 }
@@ -799,8 +907,8 @@ int mdl_backward_sumsq(const mdl_feature* feats, int32_t num_features, const mdl
   a.mode = kModeSumsq;
   rc = run_reduce(a, classes, s);
   if (rc) return rc;
-  // chunk_base[T] chunks were reduced; their partials are added in chunk order.
-  return launch_sum_partials(a.chunk_ss, 0, a.chunk_base + num_tables, sumsq, s);
+  // *num_chunks chunks were reduced; their partials are added in chunk order.
+  return launch_sum_partials(a.chunk_ss, 0, a.num_chunks, sumsq, s);
 }
 
 int mdl_backward_adagrad(const mdl_feature* feats, int32_t num_features, const mdl_table* tables,
@@ -833,14 +941,14 @@ int mdl_backward_count(const mdl_table* tables, int32_t num_tables, int32_t max_
   if (rc) return rc;
   const int64_t mc = max_chunks_for(n, num_tables);
   int64_t* heads = (int64_t*)((char*)workspace + carve(&w, workspace, n, num_tables, max_dim));
-  hipLaunchKernelGGL(count_heads_kernel, dim3((unsigned)((mc + 3) / 4)), dim3(256), 0, s, num_tables,
-                     w.chunk_base, w.table_start, w.table_end, w.table_cb, sk, mc, heads);
+  hipLaunchKernelGGL(count_heads_kernel, dim3((unsigned)((mc + 3) / 4)), dim3(256), 0, s, w.num_chunks, w.desc,
+                     w.table_start, sk, mc, heads);
   MDL_CHECK_LAUNCH("count_heads_kernel");
   rc = mdl_lengths_to_offsets(heads, mc, w.head_base, w.scan_ws, w.scan_bytes, stream);
   if (rc) return rc;
-  hipLaunchKernelGGL(unique_range_kernel, dim3((unsigned)((num_tables + 255) / 256)), dim3(256), 0, s,
-                     num_tables, w.chunk_base, w.head_base, unique_range);
-  MDL_CHECK_LAUNCH("unique_range_kernel");
+  hipLaunchKernelGGL(unique_range_end_kernel, dim3((unsigned)((num_tables + 255) / 256)), dim3(256), 0, s,
+                     num_tables, w.table_start, w.table_end, w.chunk_base, w.head_base, tables, unique_range);
+  MDL_CHECK_LAUNCH("unique_range_end_kernel");
   return MDL_OK;
 }
 

@@ -45,70 +45,71 @@ __device__ __forceinline__ float bf16_to_f32(bf16_t h) {
 // ------------------------------------------------------------ vector I/O --
 //
 // A lane moves C consecutive elements of one row.  For C > 1 the address is
-// 16-byte aligned for the weight type (C = 16 / sizeof(T)); C == 1 is the
-// scalar path for rows whose byte size or base is not 16-byte aligned.
+// 16-byte aligned and C is a multiple of one 16-byte vector of the type
+// (4 fp32 or 8 bf16), so a lane issues C/4 (fp32) or C/8 (bf16) 16-byte
+// accesses; C == 1 is the scalar path for rows whose byte size or base is not
+// 16-byte aligned.
 
 template <typename T, int C>
 struct RowIO;
 
-template <>
-struct RowIO<float, 4> {
-  static __device__ __forceinline__ void load(const float* p, float (&v)[4]) {
-    float4 x = *reinterpret_cast<const float4*>(p);
-    v[0] = x.x; v[1] = x.y; v[2] = x.z; v[3] = x.w;
-  }
-  static __device__ __forceinline__ void store(float* p, const float (&v)[4]) {
-    *reinterpret_cast<float4*>(p) = make_float4(v[0], v[1], v[2], v[3]);
-  }
-};
-
-template <>
-struct RowIO<float, 8> {
-  static __device__ __forceinline__ void load(const float* p, float (&v)[8]) {
-    float4 x = *reinterpret_cast<const float4*>(p);
-    float4 y = *reinterpret_cast<const float4*>(p + 4);
-    v[0] = x.x; v[1] = x.y; v[2] = x.z; v[3] = x.w;
-    v[4] = y.x; v[5] = y.y; v[6] = y.z; v[7] = y.w;
-  }
-  static __device__ __forceinline__ void store(float* p, const float (&v)[8]) {
-    *reinterpret_cast<float4*>(p) = make_float4(v[0], v[1], v[2], v[3]);
-    *reinterpret_cast<float4*>(p + 4) = make_float4(v[4], v[5], v[6], v[7]);
-  }
-};
-
-template <>
-struct RowIO<bf16_t, 8> {
-  static __device__ __forceinline__ void load(const bf16_t* p, float (&v)[8]) {
-    uint4 x = *reinterpret_cast<const uint4*>(p);
-    uint32_t w[4] = {x.x, x.y, x.z, x.w};
+template <int C>
+struct RowIO<float, C> {
+  static_assert(C == 1 || C % 4 == 0, "fp32 rows move 1 or 4k elements per lane");
+  static __device__ __forceinline__ void load(const float* p, float (&v)[C]) {
+    if constexpr (C == 1) {
+      v[0] = *p;
+    } else {
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      v[2 * i] = __uint_as_float(w[i] << 16);
-      v[2 * i + 1] = __uint_as_float(w[i] & 0xffff0000u);
+      for (int q = 0; q < C / 4; ++q) {
+        const float4 x = reinterpret_cast<const float4*>(p)[q];
+        v[4 * q] = x.x; v[4 * q + 1] = x.y; v[4 * q + 2] = x.z; v[4 * q + 3] = x.w;
+      }
     }
   }
-  static __device__ __forceinline__ void store(bf16_t* p, const float (&v)[8]) {
-    uint32_t w[4];
+  static __device__ __forceinline__ void store(float* p, const float (&v)[C]) {
+    if constexpr (C == 1) {
+      *p = v[0];
+    } else {
 #pragma unroll
-    for (int i = 0; i < 4; ++i)
-      w[i] = (uint32_t)f32_to_bf16(v[2 * i]) | ((uint32_t)f32_to_bf16(v[2 * i + 1]) << 16);
-    *reinterpret_cast<uint4*>(p) = make_uint4(w[0], w[1], w[2], w[3]);
+      for (int q = 0; q < C / 4; ++q)
+        reinterpret_cast<float4*>(p)[q] = make_float4(v[4 * q], v[4 * q + 1], v[4 * q + 2], v[4 * q + 3]);
+    }
   }
 };
 
-template <>
-struct RowIO<float, 1> {
-  static __device__ __forceinline__ void load(const float* p, float (&v)[1]) { v[0] = *p; }
-  static __device__ __forceinline__ void store(float* p, const float (&v)[1]) { *p = v[0]; }
-};
-
-template <>
-struct RowIO<bf16_t, 1> {
-  static __device__ __forceinline__ void load(const bf16_t* p, float (&v)[1]) {
-    v[0] = bf16_to_f32(*p);
+template <int C>
+struct RowIO<bf16_t, C> {
+  static_assert(C == 1 || C % 8 == 0, "bf16 rows move 1 or 8k elements per lane");
+  static __device__ __forceinline__ void load(const bf16_t* p, float (&v)[C]) {
+    if constexpr (C == 1) {
+      v[0] = bf16_to_f32(*p);
+    } else {
+#pragma unroll
+      for (int q = 0; q < C / 8; ++q) {
+        const uint4 x = reinterpret_cast<const uint4*>(p)[q];
+        const uint32_t w[4] = {x.x, x.y, x.z, x.w};
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          v[8 * q + 2 * i] = __uint_as_float(w[i] << 16);
+          v[8 * q + 2 * i + 1] = __uint_as_float(w[i] & 0xffff0000u);
+        }
+      }
+    }
   }
-  static __device__ __forceinline__ void store(bf16_t* p, const float (&v)[1]) {
-    *p = f32_to_bf16(v[0]);
+  static __device__ __forceinline__ void store(bf16_t* p, const float (&v)[C]) {
+    if constexpr (C == 1) {
+      *p = f32_to_bf16(v[0]);
+    } else {
+#pragma unroll
+      for (int q = 0; q < C / 8; ++q) {
+        uint32_t w[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+          w[i] = (uint32_t)f32_to_bf16(v[8 * q + 2 * i]) | ((uint32_t)f32_to_bf16(v[8 * q + 2 * i + 1]) << 16);
+        reinterpret_cast<uint4*>(p)[q] = make_uint4(w[0], w[1], w[2], w[3]);
+      }
+    }
   }
 };
 
@@ -123,30 +124,118 @@ __device__ __forceinline__ const T* zero_row() {
   return reinterpret_cast<const T*>(g_zero_row);
 }
 
-// Rows one pass covers and the chunk length that gives a wave about
-// kPassesPerChunk passes.
-constexpr int kPassesPerChunk = 32;
+// Compile-time tuning knobs (defaults are the ones measured best on MI355X):
+// rows a lane group walks per chunk, and the row elements a lane keeps in
+// flight per iteration.
+#ifndef MDL_PASSES
+#define MDL_PASSES 32
+#endif
+#ifndef MDL_ELEMS_IN_FLIGHT
+#define MDL_ELEMS_IN_FLIGHT 16
+#endif
+constexpr int kPassesPerChunk = MDL_PASSES;
 
-// ------------------------------------------------------- row-access classes --
+// Rows per lane group per iteration for lanes of C elements.
+template <int C>
+__host__ __device__ constexpr int unroll_for() {
+  return C == 1 ? 8 : (MDL_ELEMS_IN_FLIGHT / C > 1 ? MDL_ELEMS_IN_FLIGHT / C : 1);
+}
+
+// ------------------------------------------------------- kernel variants --
 //
-// Weight dtype x output/gradient dtype x 16-byte vectors or scalars.  Every
-// kernel that moves rows is instantiated once per class and launched only
-// for the classes present, so one launch never carries the registers of six
-// code paths.
+// A row-access class is weight dtype x output/gradient dtype x 16-byte
+// vectors or scalars.  A variant is a class x lane width: vector classes move
+// C = 4 << w elements per lane (fp32 4/8/16, bf16 8/16), picked so that about
+// four lanes cover a row; scalar classes move one.  A wide row then costs a
+// few lanes, and the per-row bookkeeping (ids, keys, addresses, run and bag
+// bounds) is paid once per 64-256 bytes instead of once per 16.  Every kernel
+// that moves rows is instantiated once per variant and launched only for the
+// variants present (bit `variant` of a uint32 mask).
 
-template <typename TW, typename TO, int C>
-struct ClassOf;
-template <> struct ClassOf<float, float, 4> { static constexpr int value = MDL_CLASS_F32_VEC; };
-template <> struct ClassOf<float, float, 1> { static constexpr int value = MDL_CLASS_F32; };
-template <> struct ClassOf<bf16_t, bf16_t, 8> { static constexpr int value = MDL_CLASS_BF16_VEC; };
-template <> struct ClassOf<bf16_t, bf16_t, 1> { static constexpr int value = MDL_CLASS_BF16; };
-template <> struct ClassOf<bf16_t, float, 8> { static constexpr int value = MDL_CLASS_BF16_F32_VEC; };
-template <> struct ClassOf<bf16_t, float, 1> { static constexpr int value = MDL_CLASS_BF16_F32; };
+constexpr int kWidths = 3;
+#ifndef MDL_MAX_WIDTH
+#define MDL_MAX_WIDTH 8
+#endif
+constexpr int kVariants = 6 * kWidths;
 
 __host__ __device__ __forceinline__ int row_class(int wdtype, int odtype, bool vec) {
   const int base = wdtype == MDL_F32 ? MDL_CLASS_F32_VEC
                    : (odtype == MDL_BF16 ? MDL_CLASS_BF16_VEC : MDL_CLASS_BF16_F32_VEC);
   return base + (vec ? 0 : 1);
+}
+
+// Width index of a row of `dim` elements: C = 4 << w starts at one 16-byte
+// vector of the weight type and doubles, up to 16 elements, while four lanes
+// do not cover the row and the doubled C still divides dim (a lane's C
+// elements are always wholly inside the row).
+__host__ __device__ __forceinline__ int width_index(int64_t dim, int wdtype, bool vec) {
+  if (!vec) return 0;
+  int w = wdtype == MDL_BF16 ? 1 : 0;
+  while (w < kWidths - 1 && (8 << w) <= MDL_MAX_WIDTH && (int64_t)(4 << w) * 4 < dim && dim % (8 << w) == 0) ++w;
+  return w;
+}
+
+__host__ __device__ __forceinline__ int variant_of(int wdtype, int odtype, bool vec, int64_t dim) {
+  return row_class(wdtype, odtype, vec) * kWidths + width_index(dim, wdtype, vec);
+}
+
+// Elements per lane of a variant.
+__host__ __device__ __forceinline__ int variant_elems(int v) {
+  const int cls = v / kWidths;
+  return (cls & 1) ? 1 : (4 << (v % kWidths));
+}
+
+template <typename TW, typename TO, int C>
+struct VariantOf {
+  static constexpr bool kF32 = sizeof(TW) == 4;
+  static constexpr bool kOutBf16 = sizeof(TO) == 2;
+  static constexpr int cls = kF32 ? (C == 1 ? MDL_CLASS_F32 : MDL_CLASS_F32_VEC)
+                             : kOutBf16 ? (C == 1 ? MDL_CLASS_BF16 : MDL_CLASS_BF16_VEC)
+                                        : (C == 1 ? MDL_CLASS_BF16_F32 : MDL_CLASS_BF16_F32_VEC);
+  static constexpr int w = C == 1 ? 0 : (C == 4 ? 0 : (C == 8 ? 1 : 2));
+  static constexpr int value = cls * kWidths + w;
+};
+
+// Kernels are launched once per row-access class present and pick the lane
+// width of each chunk inside (one launch instead of one per width: separate
+// launches would each pay a ramp-up and a tail).  for_each_class calls
+// f.template operator()<TW, TO, kVec>() for every class with a variant bit set
+// in mask (0 = all), stopping at the first non-zero return.
+template <typename F>
+__host__ int for_each_class(uint32_t mask, F&& f) {
+  auto on = [&](int cls) { return mask == 0 || ((mask >> (cls * kWidths)) & ((1u << kWidths) - 1u)) != 0; };
+  int rc = 0;
+  if (!rc && on(MDL_CLASS_F32_VEC)) rc = f.template operator()<float, float, true>();
+  if (!rc && on(MDL_CLASS_F32)) rc = f.template operator()<float, float, false>();
+  if (!rc && on(MDL_CLASS_BF16_VEC)) rc = f.template operator()<bf16_t, bf16_t, true>();
+  if (!rc && on(MDL_CLASS_BF16)) rc = f.template operator()<bf16_t, bf16_t, false>();
+  if (!rc && on(MDL_CLASS_BF16_F32_VEC)) rc = f.template operator()<bf16_t, float, true>();
+  if (!rc && on(MDL_CLASS_BF16_F32)) rc = f.template operator()<bf16_t, float, false>();
+  return rc;
+}
+
+template <typename TW, typename TO, bool kVec>
+struct ClassOf {
+  static constexpr int value = VariantOf<TW, TO, kVec ? (sizeof(TW) == 4 ? 4 : 8) : 1>::cls;
+};
+
+// Calls body.template operator()<C>() with the lane width of width index w
+// for a class (scalar classes: C = 1).
+template <typename TW, bool kVec, typename B>
+__device__ __forceinline__ void with_width(int w, B&& body) {
+  if constexpr (!kVec) {
+    body.template operator()<1>();
+  } else {
+    if constexpr (sizeof(TW) == 4 && MDL_MAX_WIDTH >= 4) {
+      if (w == 0) { body.template operator()<4>(); return; }
+    }
+    if constexpr (MDL_MAX_WIDTH >= 8) {
+      if (w == 1) { body.template operator()<8>(); return; }
+    }
+    if constexpr (MDL_MAX_WIDTH >= 16) {
+      if (w == 2) { body.template operator()<16>(); return; }
+    }
+  }
 }
 
 // Whether a feature's weight, output and gradient rows allow 16-byte lanes.

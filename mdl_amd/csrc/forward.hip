@@ -2,17 +2,16 @@
 //
 // One wavefront owns one chunk (a run of whole bags of one feature, or a run
 // of ids of an unpooled feature).  A row of `dim` elements is spread over L
-// lanes (L = next_pow2(dim / C), C elements = 16 bytes per lane), so a wave
-// gathers G = 64 / L rows per pass; four passes are issued before any is
-// reduced to keep 4*G row loads in flight per wave.
+// lanes of C elements each (C = 4..16 fp32 or 8..16 bf16, 16-byte accesses;
+// the kernel variant), so a wave holds G = 64 / L rows at a time.
 //
-// Pooling walks the chunk's ids as one flat stream (bags are consecutive
-// segments of it).  Each pass forms an inclusive segmented scan over the G
-// slots (bag index is the segment key) with cross-lane permutes, adds the
-// carry of a bag that began in an earlier pass, and the slot holding a bag's
-// last id writes that bag's pooled row.  Every id costs the same regardless
-// of how the bag lengths are distributed, so ragged bags (lengths 1..32 in
-// the RankMixer workload) keep all lanes busy, and the summation order is
+// Pooling: the chunk's ids form one flat stream in which bags are consecutive
+// segments.  The G lane groups ("slots") each walk a contiguous slice of that
+// stream, adding rows into registers; a bag that ends inside the slot that
+// began it is divided (mean) and written right there, so every id costs a
+// row load and C adds whatever the bag lengths (ragged bags of 1..32 ids keep
+// all lanes busy).  Bags that cross slot bounds are joined once per chunk by
+// a segmented scan over the slots' open partial sums.  The summation order is
 // fixed by the chunk layout alone (deterministic).  Bag bounds are staged in
 // LDS once per chunk.
 #include "common.cuh"
@@ -70,18 +69,25 @@ __device__ __forceinline__ Feat load_feat(const mdl_feature* p) {
   return f;
 }
 
-__device__ __forceinline__ int feat_class(const Feat& f) {
-  return row_class(f.wdtype, f.odtype,
-                   feature_vec((uint64_t)f.weight, (uint64_t)f.out, f.dim, f.out_stride, f.wdtype, f.odtype));
+__device__ __forceinline__ int feat_variant(const Feat& f) {
+  return variant_of(f.wdtype, f.odtype,
+                    feature_vec((uint64_t)f.weight, (uint64_t)f.out, f.dim, f.out_stride, f.wdtype, f.odtype),
+                    f.dim);
 }
 
 __device__ __forceinline__ void wave_sync() { __builtin_amdgcn_wave_barrier(); __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront"); }
+
+template <int C>
+__device__ __forceinline__ void zero_c(float (&v)[C]) {
+#pragma unroll
+  for (int k = 0; k < C; ++k) v[k] = 0.f;
+}
 
 // ------------------------------------------------------------ unpooled --
 
 template <typename TW, typename TO, int C>
 __device__ __forceinline__ void gather_chunk(const Feat& f, int64_t first, int count, const FwdArgs& a) {
-  constexpr int kUnroll = C >= 8 ? 2 : 4;  // 16 columns of loads in flight per lane
+  constexpr int kUnroll = unroll_for<C>();
   const int lane = lane_id();
   const int L = lanes_for(f.dim, C);
   const int G = kWave / L;
@@ -91,7 +97,6 @@ __device__ __forceinline__ void gather_chunk(const Feat& f, int64_t first, int c
   TO* out = static_cast<TO*>(f.out);
   const int64_t* ids = a.ids + f.ids_begin + first;
   const int step = G * kUnroll;
-  int bad = 0;
   for (int cb = 0; cb < ncb; ++cb) {
     const int col = (cb * L + sub) * C;
     const bool col_ok = col < f.dim;
@@ -119,18 +124,20 @@ __device__ __forceinline__ void gather_chunk(const Feat& f, int64_t first, int c
 #pragma unroll
       for (int u = 0; u < kUnroll; ++u) {
         const int i = base + u * G + slot;
-        if (i >= count) continue;
-        const bool in_range = (uint64_t)id[u] < (uint64_t)f.num_rows;
-        if (cb == 0 && sub == 0) {
-          bad += !in_range;
-          if (a.keys != nullptr) {
-            const int64_t e = f.ids_begin + first + i;
-            a.keys[e] = (in_range && id[u] != f.padding_idx) ? (uint32_t)(f.row_base + id[u]) : a.sentinel;
-            a.payload[e] = (uint32_t)(f.payload_base + first + i);
-          }
-        }
-        if (col_ok) RowIO<TO, C>::store(out + (first + i) * f.out_stride + col, v[u]);
+        if (i < count && col_ok) RowIO<TO, C>::store(out + (first + i) * f.out_stride + col, v[u]);
       }
+    }
+  }
+  // Sort keys and payloads (and the invalid-id count), one id per lane.
+  int bad = 0;
+  for (int i = lane; i < count; i += kWave) {
+    const int64_t id = ids[i];
+    const bool in_range = (uint64_t)id < (uint64_t)f.num_rows;
+    bad += !in_range;
+    if (a.keys != nullptr) {
+      const int64_t e = f.ids_begin + first + i;
+      a.keys[e] = (in_range && id != f.padding_idx) ? (uint32_t)(f.row_base + id) : a.sentinel;
+      a.payload[e] = (uint32_t)(f.payload_base + first + i);
     }
   }
   if (bad && a.error_count) atomicAdd(a.error_count, bad);
@@ -138,27 +145,57 @@ __device__ __forceinline__ void gather_chunk(const Feat& f, int64_t first, int c
 
 // -------------------------------------------------------------- pooled --
 
-template <typename TW, typename TO, int C>
-__device__ __forceinline__ void pooled_chunk(const Feat& f, int64_t first_bag, int nb, int64_t* s_off, const FwdArgs& a) {
-  constexpr int kUnroll = C >= 8 ? 2 : 4;  // 16 columns of loads in flight per lane
+// Stage the chunk's bag bounds [0, nb] in LDS, clamped into the feature's own
+// id range, so lengths that do not add up to the ids passed can only give
+// wrong sums (and an error count), never an out-of-bounds read.  Decreasing
+// offsets (negative lengths) are made non-decreasing.
+__device__ __forceinline__ int stage_offsets(const Feat& f, int64_t first_bag, int nb, int64_t* s_off,
+                                             const FwdArgs& a) {
   const int lane = lane_id();
-  // Offsets are clamped into the feature's own id range, so lengths that do
-  // not add up to the ids passed can only give wrong sums (and an error
-  // count), never an out-of-bounds read.
   const int64_t lo = f.ids_begin, hi = f.ids_begin + f.num_ids;
   int clamped = 0;
   for (int i = lane; i <= nb; i += kWave) {
-    int64_t o = a.offsets[f.bag_base + first_bag + i];
+    const int64_t o = a.offsets[f.bag_base + first_bag + i];
     const int64_t oc = o < lo ? lo : (o > hi ? hi : o);
     clamped += oc != o;
     s_off[i] = oc;
   }
   wave_sync();
-  // Decreasing offsets (negative lengths) are errors too; the walk below
-  // stays inside [s_off[0], s_off[nb]) whatever the offsets hold.
-  for (int i = lane + 1; i <= nb; i += kWave) clamped += s_off[i] < s_off[i - 1];
-  if (clamped && a.error_count) atomicAdd(a.error_count, clamped);
+  int dec = 0;
+  for (int i = lane + 1; i <= nb; i += kWave) dec += s_off[i] < s_off[i - 1];
+  if (__ballot(dec != 0) != 0) {
+    // Error path: a running maximum makes every bag's bounds ordered.
+    if (lane == 0) {
+      int64_t m = s_off[0];
+      for (int i = 1; i <= nb; ++i) {
+        if (s_off[i] < m) s_off[i] = m;
+        m = s_off[i];
+      }
+    }
+    wave_sync();
+  }
+  return clamped + dec;
+}
+
+// Last bag b in [0, nb) with s_off[b] <= e (the bag holding entry e, skipping
+// empty bags), by binary search over the staged bounds.
+__device__ __forceinline__ int bag_of(const int64_t* s_off, int nb, int64_t e) {
+  int lo = 0, hi = nb - 1;
+  while (lo < hi) {
+    const int mid = (lo + hi + 1) >> 1;
+    if (s_off[mid] <= e) lo = mid;
+    else hi = mid - 1;
+  }
+  return lo;
+}
+
+template <typename TW, typename TO, int C>
+__device__ __forceinline__ void pooled_chunk(const Feat& f, int64_t first_bag, int nb, int64_t* s_off,
+                                             const FwdArgs& a) {
+  constexpr int U = unroll_for<C>();  // ids per slot per iteration
+  const int lane = lane_id();
   const int64_t e_begin = s_off[0], e_end = s_off[nb];
+  const int64_t len = e_end - e_begin;
   const int L = lanes_for(f.dim, C);
   const int G = kWave / L;
   const int slot = lane / L, sub = lane % L;
@@ -170,140 +207,168 @@ __device__ __forceinline__ void pooled_chunk(const Feat& f, int64_t first_bag, i
   const bool mean = f.pooling == MDL_POOL_MEAN;
   const TW* W = static_cast<const TW*>(f.weight);
   TO* out = static_cast<TO*>(f.out);
-  const int last_lane_base = (G - 1) * L;
-  const int64_t step = (int64_t)G * kUnroll;
-  int bad = 0;
+  // This slot's slice [s0, s1) of the chunk's ids.
+  const int64_t K = (len + G - 1) / G;
+  const int64_t s0 = e_begin + slot * K;
+  const int64_t s1 = s0 + K < e_end ? s0 + K : e_end;
+  const bool any = s0 < s1;
+  const int b0 = any ? bag_of(s_off, nb, s0) : 0;
+  const bool cont = any && s_off[b0] < s0;  // the slice starts inside a bag
 
   for (int cb = 0; cb < ncb; ++cb) {
     const int col = (cb * L + sub) * C;
     const bool col_ok = col < f.dim;
-    float carry[C];
+    const bool emit = cb == 0 && sub == 0;
+    float acc[C], hp[C];
+    zero_c(acc);
+    zero_c(hp);
+    float wsum = 0.f, hw = 0.f;
+    int hbag = -1;  // first bag of a slice that starts inside it, when it ends in the slice
+    bool ended = false;
+    int b = b0;
+    int64_t bend = any ? s_off[b0 + 1] : 0;
+    int64_t nid[U];  // ids of the next iteration, fetched one iteration ahead
 #pragma unroll
-    for (int k = 0; k < C; ++k) carry[k] = 0.f;
-    float carry_w = 0.f;
-    int carry_seg = -2;
-    int bag = 0;  // cursor: bag (relative to the chunk) of this slot's current id
-    int64_t nid[kUnroll];
+    for (int u = 0; u < U; ++u) nid[u] = s0 + u < s1 ? a.ids[s0 + u] : 0;
+    for (int64_t j = s0; j < s1; j += U) {
+      float v[U][C], wt[U];
+      int64_t id[U];
 #pragma unroll
-    for (int u = 0; u < kUnroll; ++u) {
-      const int64_t e = e_begin + (int64_t)u * G + slot;
-      nid[u] = e < e_end ? a.ids[e] : 0;
-    }
-    for (int64_t base = e_begin; base < e_end; base += step) {
-      float v[kUnroll][C];
-      float wt[kUnroll];
-      int seg[kUnroll];
-      bool tail[kUnroll];
-      int64_t id[kUnroll], row[kUnroll];
-      // Bag of every slot (LDS cursor walk), then all row loads of the group
-      // in one branch-free block, then the backward's sort keys.
+      for (int u = 0; u < U; ++u) id[u] = nid[u];
 #pragma unroll
-      for (int u = 0; u < kUnroll; ++u) {
-        id[u] = nid[u];
-        const int64_t e = base + (int64_t)u * G + slot;
-        const bool valid = e < e_end;
-        if (valid) {
-          while (s_off[bag + 1] <= e) ++bag;
-        }
-        row[u] = by_pos ? e - f.ids_begin : id[u];
-        const bool in_range = (uint64_t)row[u] < (uint64_t)f.num_rows;
+      for (int u = 0; u < U; ++u) {
+        const int64_t e = j + u;
+        const int64_t row = by_pos ? e - f.ids_begin : id[u];
+        const bool in_range = (uint64_t)row < (uint64_t)f.num_rows;
         float w = (exclude && id[u] == 0) ? 0.f : 1.f;
-        if (!in_range || !valid) w = 0.f;
-        seg[u] = valid ? bag : -1;
+        if (!in_range || e >= s1) w = 0.f;
         wt[u] = w;
-        tail[u] = valid && (e + 1 == s_off[bag + 1]);
+        RowIO<TW, C>::load(w != 0.f && col_ok ? W + row * f.dim + col : zero_row<TW>(), v[u]);
       }
 #pragma unroll
-      for (int u = 0; u < kUnroll; ++u)
-        RowIO<TW, C>::load(wt[u] != 0.f && col_ok ? W + row[u] * f.dim + col : zero_row<TW>(), v[u]);
-      if (cb == 0 && sub == 0) {
+      for (int u = 0; u < U; ++u) nid[u] = j + U + u < s1 ? a.ids[j + U + u] : 0;
 #pragma unroll
-        for (int u = 0; u < kUnroll; ++u) {
-          const int64_t e = base + (int64_t)u * G + slot;
-          if (e >= e_end) continue;
-          bad += (uint64_t)row[u] >= (uint64_t)f.num_rows;
-          if (a.keys != nullptr) {
-            // w == 0 covers invalid ids and nulls under "exclude": their
-            // gradient is exactly zero, so they take no part in the backward.
-            // Rows by position belong to no table.
-            a.keys[e] = (wt[u] != 0.f && !by_pos && id[u] != f.padding_idx) ? (uint32_t)(f.row_base + id[u])
-                                                                            : a.sentinel;
-            a.payload[e] = (uint32_t)(f.payload_base + first_bag + seg[u]);
+      for (int u = 0; u < U; ++u) {
+        const int64_t e = j + u;
+        if (e >= s1) continue;
+#pragma unroll
+        for (int k = 0; k < C; ++k) acc[k] += v[u][k];
+        wsum += wt[u];
+        if (e + 1 == bend) {
+          if (s_off[b] >= s0) {
+            if (col_ok) {
+              const float inv = mean ? __builtin_amdgcn_rcpf(fmaxf(wsum, 1.f)) : 1.f;
+              float r[C];
+#pragma unroll
+              for (int k = 0; k < C; ++k) r[k] = acc[k] * inv;
+              RowIO<TO, C>::store(out + (first_bag + b) * f.out_stride + col, r);
+            }
+            if (emit && a.bag_count != nullptr) a.bag_count[f.payload_base + first_bag + b] = wsum;
+          } else {
+#pragma unroll
+            for (int k = 0; k < C; ++k) hp[k] = acc[k];
+            hw = wsum;
+            hbag = b;
           }
+          ended = true;
+          zero_c(acc);
+          wsum = 0.f;
+          // next non-empty bag
+          ++b;
+          while (b < nb - 1 && s_off[b + 1] <= e + 1) ++b;
+          bend = s_off[b + 1 <= nb ? b + 1 : nb];
         }
       }
+    }
+    // Join bags that cross slot bounds: slot s exports the partial of the bag
+    // open at its end; a slice inside one bag passes the previous export on.
+    float o[C];
 #pragma unroll
-      for (int u = 0; u < kUnroll; ++u) {
-        const int64_t e = base + step + (int64_t)u * G + slot;
-        nid[u] = e < e_end ? a.ids[e] : 0;
+    for (int k = 0; k < C; ++k) o[k] = acc[k];
+    float ow = wsum;
+    bool pass = cont && !ended;
+    for (int d = 1; d < G; d <<= 1) {
+      const int src = slot >= d ? lane - d * L : lane;
+      const int opass = shfl_i((int)pass, src);
+      const float oww = shfl_f(ow, src);
+      float ov[C];
+#pragma unroll
+      for (int k = 0; k < C; ++k) ov[k] = shfl_f(o[k], src);
+      if (slot >= d) {
+        if (pass) {
+#pragma unroll
+          for (int k = 0; k < C; ++k) o[k] += ov[k];
+          ow += oww;
+        }
+        pass = pass && opass;
       }
+    }
+    const int prev = slot > 0 ? lane - L : lane;
+    float in[C];
 #pragma unroll
-      for (int u = 0; u < kUnroll; ++u) {
-        // Inclusive segmented scan over the G slots of this pass.
-        for (int d = 1; d < G; d <<= 1) {
-          const int src = slot >= d ? lane - d * L : lane;
-          const int oseg = shfl_i(seg[u], src);
-          const float ow = shfl_f(wt[u], src);
-          float ov[C];
+    for (int k = 0; k < C; ++k) in[k] = shfl_f(o[k], prev);
+    const float inw = shfl_f(ow, prev);
+    if (hbag >= 0) {
+      const float tw = inw + hw;
+      if (col_ok) {
+        const float inv = mean ? __builtin_amdgcn_rcpf(fmaxf(tw, 1.f)) : 1.f;
+        float r[C];
 #pragma unroll
-          for (int k = 0; k < C; ++k) ov[k] = shfl_f(v[u][k], src);
-          if (slot >= d && oseg == seg[u]) {
-            wt[u] += ow;
-#pragma unroll
-            for (int k = 0; k < C; ++k) v[u][k] += ov[k];
-          }
-        }
-        if (seg[u] == carry_seg) {
-          wt[u] += carry_w;
-#pragma unroll
-          for (int k = 0; k < C; ++k) v[u][k] += carry[k];
-        }
-        if (tail[u]) {
-          const int64_t b = first_bag + seg[u];
-          if (col_ok) {
-            float r[C];
-            const float inv = mean ? 1.f / fmaxf(wt[u], 1.f) : 1.f;
-#pragma unroll
-            for (int k = 0; k < C; ++k) r[k] = v[u][k] * inv;
-            RowIO<TO, C>::store(out + b * f.out_stride + col, r);
-          }
-          if (cb == 0 && sub == 0 && a.bag_count != nullptr) a.bag_count[f.payload_base + b] = wt[u];
-        }
-        const int src = last_lane_base + sub;
-        const int lseg = shfl_i(seg[u], src);
-        const int ltail = shfl_i((int)tail[u], src);
-        carry_w = shfl_f(wt[u], src);
-#pragma unroll
-        for (int k = 0; k < C; ++k) carry[k] = shfl_f(v[u][k], src);
-        carry_seg = (lseg >= 0 && !ltail) ? lseg : -2;
+        for (int k = 0; k < C; ++k) r[k] = (in[k] + hp[k]) * inv;
+        RowIO<TO, C>::store(out + (first_bag + hbag) * f.out_stride + col, r);
       }
+      if (emit && a.bag_count != nullptr) a.bag_count[f.payload_base + first_bag + hbag] = tw;
     }
   }
   // Empty bags pool to zero.
-  for (int b = slot; b < nb; b += G) {
-    if (s_off[b] == s_off[b + 1]) {
+  for (int bb = slot; bb < nb; bb += G) {
+    if (s_off[bb] == s_off[bb + 1]) {
       float z[C];
-#pragma unroll
-      for (int k = 0; k < C; ++k) z[k] = 0.f;
+      zero_c(z);
       for (int cb = 0; cb < ncb; ++cb) {
         const int col = (cb * L + sub) * C;
-        if (col < f.dim) RowIO<TO, C>::store(out + (first_bag + b) * f.out_stride + col, z);
+        if (col < f.dim) RowIO<TO, C>::store(out + (first_bag + bb) * f.out_stride + col, z);
       }
-      if (sub == 0 && a.bag_count != nullptr) a.bag_count[f.payload_base + first_bag + b] = 0.f;
+      if (sub == 0 && a.bag_count != nullptr) a.bag_count[f.payload_base + first_bag + bb] = 0.f;
     }
   }
-  if (bad && a.error_count) atomicAdd(a.error_count, bad);
 }
 
-template <typename TW, typename TO, int C>
-__device__ __forceinline__ void run_chunk(const Feat& f, const mdl_chunk& ch, int64_t* s_off, const FwdArgs& a) {
-  if (f.pooling == MDL_POOL_NONE)
-    gather_chunk<TW, TO, C>(f, ch.first, ch.count, a);
-  else
-    pooled_chunk<TW, TO, C>(f, ch.first, ch.count, s_off, a);
+// Sort keys and payloads of a pooled chunk (and its invalid-id count), one
+// id per lane so the stores coalesce; an id's bag comes from a binary search
+// of the staged bounds, resumed from the lane's previous id.
+__device__ __forceinline__ int pooled_keys(const Feat& f, int64_t first_bag, int nb, const int64_t* s_off,
+                                           const FwdArgs& a) {
+  const int lane = lane_id();
+  const int64_t e_begin = s_off[0], e_end = s_off[nb];
+  const bool exclude = (f.flags & MDL_FLAG_EXCLUDE_NULL) != 0;
+  const bool by_pos = (f.flags & MDL_FLAG_ROWS_BY_POSITION) != 0;
+  int bad = 0;
+  int b = 0;
+  for (int64_t e = e_begin + lane; e < e_end; e += kWave) {
+    int hi = nb - 1;  // last bag with s_off[bag] <= e, searched in [b, nb)
+    while (b < hi) {
+      const int mid = (b + hi + 1) >> 1;
+      if (s_off[mid] <= e) b = mid;
+      else hi = mid - 1;
+    }
+    const int64_t id = a.ids[e];
+    const int64_t row = by_pos ? e - f.ids_begin : id;
+    const bool in_range = (uint64_t)row < (uint64_t)f.num_rows;
+    bad += !in_range;
+    if (a.keys != nullptr) {
+      // Invalid ids and nulls under "exclude" pool with weight 0: their
+      // gradient is exactly zero, so they take no part in the backward.
+      // Rows by position belong to no table.
+      const bool live = in_range && !(exclude && id == 0) && !by_pos && id != f.padding_idx;
+      a.keys[e] = live ? (uint32_t)(f.row_base + id) : a.sentinel;
+      a.payload[e] = (uint32_t)(f.payload_base + first_bag + b);
+    }
+  }
+  return bad;
 }
 
-template <typename TW, typename TO, int C>
+template <typename TW, typename TO, bool kVec>
 __global__ __launch_bounds__(kFwdWaves * kWave) void forward_kernel(FwdArgs a) {
   __shared__ int64_t s_off[kFwdWaves][kMaxBagsPerChunk + 1];
   const int w = threadIdx.x / kWave;
@@ -315,41 +380,37 @@ __global__ __launch_bounds__(kFwdWaves * kWave) void forward_kernel(FwdArgs a) {
   ch.count = uni32(a.chunks[c].count);
   ch.first = uni64(a.chunks[c].first);
   const Feat f = load_feat(a.feats + ch.feature);
-  if (feat_class(f) != ClassOf<TW, TO, C>::value) return;  // another class's launch owns it
-  if (f.pooling != MDL_POOL_NONE && (ch.count > kMaxBagsPerChunk || ch.count < 0)) {
-    if (lane_id() == 0 && a.error_count) atomicAdd(a.error_count, 1);
+  const int v = feat_variant(f);
+  if (v / kWidths != ClassOf<TW, TO, kVec>::value) return;  // another class's launch owns it
+  if (f.pooling == MDL_POOL_NONE) {
+    with_width<TW, kVec>(v % kWidths, [&]<int C>() { gather_chunk<TW, TO, C>(f, ch.first, ch.count, a); });
     return;
   }
-  run_chunk<TW, TO, C>(f, ch, s_off[w], a);
-}
-
-template <typename TW, typename TO, int C>
-static int launch_forward(const FwdArgs& a, uint32_t classes, int64_t blocks, hipStream_t s) {
-  if (classes != 0 && !(classes & (1u << ClassOf<TW, TO, C>::value))) return MDL_OK;
-  hipLaunchKernelGGL((forward_kernel<TW, TO, C>), dim3((unsigned)blocks), dim3(kFwdWaves * kWave), 0, s, a);
-  MDL_CHECK_LAUNCH("forward_kernel");
-  return MDL_OK;
+  if (ch.count > kMaxBagsPerChunk || ch.count <= 0) {
+    if (lane_id() == 0 && a.error_count && ch.count != 0) atomicAdd(a.error_count, 1);
+    return;
+  }
+  int bad = stage_offsets(f, ch.first, ch.count, s_off[w], a);
+  bad += pooled_keys(f, ch.first, ch.count, s_off[w], a);
+  with_width<TW, kVec>(v % kWidths, [&]<int C>() { pooled_chunk<TW, TO, C>(f, ch.first, ch.count, s_off[w], a); });
+  for (int m = 1; m < kWave; m <<= 1) bad += __shfl_xor(bad, m);
+  if (lane_id() == 0 && bad && a.error_count) atomicAdd(a.error_count, bad);
 }
 
 // ------------------------------------------------------ pool backward --
 
 // Per-position gradient of one chunk of bags: slot e of bag b receives the
 // bag's upstream gradient row times w_e / max(count_b, 1) (mean) or w_e (sum).
-// The walk over the chunk's positions is the forward's (same LDS bounds and
-// bag cursor); consecutive slots of one bag read the same gradient row, which
-// stays in L2, so HBM sees about one read of each pooled gradient row and one
-// write of each position row.
+// The walk over the chunk's positions visits consecutive slots of one bag
+// together, so they read the same gradient row, which stays in L2: HBM sees
+// about one read of each pooled gradient row and one write of each position
+// row.
 template <typename TW, typename TO, int C>
 __device__ __forceinline__ void unpool_chunk(const Feat& f, int64_t first_bag, int nb, int64_t* s_off,
                                              const FwdArgs& a) {
-  constexpr int kUnroll = C >= 8 ? 2 : 4;
+  constexpr int kUnroll = unroll_for<C>();
   const int lane = lane_id();
-  const int64_t lo = f.ids_begin, hi = f.ids_begin + f.num_ids;
-  for (int i = lane; i <= nb; i += kWave) {
-    const int64_t o = a.offsets[f.bag_base + first_bag + i];
-    s_off[i] = o < lo ? lo : (o > hi ? hi : o);
-  }
-  wave_sync();
+  stage_offsets(f, first_bag, nb, s_off, a);
   const int64_t e_begin = s_off[0], e_end = s_off[nb];
   const int L = lanes_for(f.dim, C);
   const int G = kWave / L;
@@ -395,7 +456,7 @@ __device__ __forceinline__ void unpool_chunk(const Feat& f, int64_t first_bag, i
         // outside [0, num_rows).
         const int64_t src = by_pos ? row : id[u];
         const bool dead = (exclude && id[u] == 0) || (uint64_t)src >= (uint64_t)f.num_rows;
-        const float sc = dead ? 0.f : (mean ? 1.f / fmaxf(cnt[u], 1.f) : 1.f);
+        const float sc = dead ? 0.f : (mean ? __builtin_amdgcn_rcpf(fmaxf(cnt[u], 1.f)) : 1.f);
 #pragma unroll
         for (int k = 0; k < C; ++k) v[u][k] *= sc;
         if (valid[u] && col_ok) RowIO<TW, C>::store(dst + row * f.dim + col, v[u]);
@@ -404,7 +465,7 @@ __device__ __forceinline__ void unpool_chunk(const Feat& f, int64_t first_bag, i
   }
 }
 
-template <typename TW, typename TO, int C>
+template <typename TW, typename TO, bool kVec>
 __global__ __launch_bounds__(kFwdWaves * kWave) void pool_backward_kernel(FwdArgs a) {
   __shared__ int64_t s_off[kFwdWaves][kMaxBagsPerChunk + 1];
   const int w = threadIdx.x / kWave;
@@ -415,18 +476,30 @@ __global__ __launch_bounds__(kFwdWaves * kWave) void pool_backward_kernel(FwdArg
   const int32_t count = uni32(a.chunks[c].count);
   const int64_t first = uni64(a.chunks[c].first);
   const Feat f = load_feat(a.feats + fi);
-  if (feat_class(f) != ClassOf<TW, TO, C>::value) return;  // another class's launch owns it
-  if (f.pooling == MDL_POOL_NONE || count > kMaxBagsPerChunk || count < 0) return;
-  unpool_chunk<TW, TO, C>(f, first, count, s_off[w], a);
+  const int v = feat_variant(f);
+  if (v / kWidths != ClassOf<TW, TO, kVec>::value) return;  // another class's launch owns it
+  if (f.pooling == MDL_POOL_NONE || count > kMaxBagsPerChunk || count <= 0) return;
+  with_width<TW, kVec>(v % kWidths, [&]<int C>() { unpool_chunk<TW, TO, C>(f, first, count, s_off[w], a); });
 }
 
-template <typename TW, typename TO, int C>
-static int launch_pool_backward(const FwdArgs& a, uint32_t classes, int64_t blocks, hipStream_t s) {
-  if (classes != 0 && !(classes & (1u << ClassOf<TW, TO, C>::value))) return MDL_OK;
-  hipLaunchKernelGGL((pool_backward_kernel<TW, TO, C>), dim3((unsigned)blocks), dim3(kFwdWaves * kWave), 0, s, a);
-  MDL_CHECK_LAUNCH("pool_backward_kernel");
-  return MDL_OK;
-}
+struct LaunchForward {
+  const FwdArgs& a;
+  int64_t blocks;
+  hipStream_t s;
+  bool backward;
+  template <typename TW, typename TO, bool kVec>
+  int operator()() const {
+    if (backward) {
+      hipLaunchKernelGGL((pool_backward_kernel<TW, TO, kVec>), dim3((unsigned)blocks), dim3(kFwdWaves * kWave), 0, s,
+                         a);
+      MDL_CHECK_LAUNCH("pool_backward_kernel");
+    } else {
+      hipLaunchKernelGGL((forward_kernel<TW, TO, kVec>), dim3((unsigned)blocks), dim3(kFwdWaves * kWave), 0, s, a);
+      MDL_CHECK_LAUNCH("forward_kernel");
+    }
+    return MDL_OK;
+  }
+};
 
 // ------------------------------------------------------------ sequences --
 
@@ -551,8 +624,8 @@ uint32_t mdl_feature_classes(const mdl_feature* feats, int32_t num_features) {
   uint32_t m = 0;
   for (int32_t i = 0; i < num_features; ++i) {
     const mdl_feature& f = feats[i];
-    m |= 1u << row_class(f.wdtype, f.odtype,
-                         feature_vec(f.weight, f.out, f.dim, f.out_stride, f.wdtype, f.odtype));
+    m |= 1u << variant_of(f.wdtype, f.odtype, feature_vec(f.weight, f.out, f.dim, f.out_stride, f.wdtype, f.odtype),
+                          f.dim);
   }
   return m;
 }
@@ -563,12 +636,12 @@ int64_t mdl_plan_chunks(const mdl_feature* feats, int32_t num_features, int32_t 
   int64_t n = 0;
   for (int32_t fi = 0; fi < num_features; ++fi) {
     const mdl_feature& f = feats[fi];
-    // Rows a wave gathers per pass (same lane layout as the kernel): chunks
-    // hold about kPassesPerChunk passes, so no wave walks a long serial chain
-    // of dependent loads, whatever the row width.
-    const int c = f.wdtype == MDL_BF16 ? 8 : 4;
+    // Rows a wave holds at once (same lane layout as the kernel): chunks hold
+    // about kPassesPerChunk of them per slot, so no slot walks a long serial
+    // chain of dependent loads, whatever the row width.
     const bool vec = feature_vec(f.weight, f.out, f.dim, f.out_stride, f.wdtype, f.odtype);
-    const int lanes = lanes_for(f.dim > 0 ? f.dim : 1, vec ? c : 1);
+    const int c = variant_elems(variant_of(f.wdtype, f.odtype, vec, f.dim));
+    const int lanes = lanes_for(f.dim > 0 ? f.dim : 1, c);
     const int64_t per_pass = kWave / lanes;
     int64_t target = (int64_t)kPassesPerChunk * per_pass;
     if (target > target_ids) target = target_ids;
@@ -620,14 +693,7 @@ int mdl_forward(const mdl_feature* feats, int32_t num_features, const mdl_chunk*
   a.sentinel = sentinel;
   const int64_t blocks = (num_chunks + kFwdWaves - 1) / kFwdWaves;
   if (blocks > 0x7fffffff) return fail(MDL_ERR_UNSUPPORTED, "mdl_forward: too many chunks");
-  hipStream_t s = as_stream(stream);
-  int rc = launch_forward<float, float, 4>(a, classes, blocks, s);
-  if (!rc) rc = launch_forward<float, float, 1>(a, classes, blocks, s);
-  if (!rc) rc = launch_forward<bf16_t, bf16_t, 8>(a, classes, blocks, s);
-  if (!rc) rc = launch_forward<bf16_t, bf16_t, 1>(a, classes, blocks, s);
-  if (!rc) rc = launch_forward<bf16_t, float, 8>(a, classes, blocks, s);
-  if (!rc) rc = launch_forward<bf16_t, float, 1>(a, classes, blocks, s);
-  return rc;
+  return for_each_class(classes, LaunchForward{a, blocks, as_stream(stream), false});
 }
 
 int mdl_pool_backward(const mdl_feature* feats, int32_t num_features, const mdl_chunk* chunks,
@@ -650,14 +716,7 @@ int mdl_pool_backward(const mdl_feature* feats, int32_t num_features, const mdl_
   a.sentinel = 0;
   const int64_t blocks = (num_chunks + kFwdWaves - 1) / kFwdWaves;
   if (blocks > 0x7fffffff) return fail(MDL_ERR_UNSUPPORTED, "mdl_pool_backward: too many chunks");
-  hipStream_t s = as_stream(stream);
-  int rc = launch_pool_backward<float, float, 4>(a, classes, blocks, s);
-  if (!rc) rc = launch_pool_backward<float, float, 1>(a, classes, blocks, s);
-  if (!rc) rc = launch_pool_backward<bf16_t, bf16_t, 8>(a, classes, blocks, s);
-  if (!rc) rc = launch_pool_backward<bf16_t, bf16_t, 1>(a, classes, blocks, s);
-  if (!rc) rc = launch_pool_backward<bf16_t, float, 8>(a, classes, blocks, s);
-  if (!rc) rc = launch_pool_backward<bf16_t, float, 1>(a, classes, blocks, s);
-  return rc;
+  return for_each_class(classes, LaunchForward{a, blocks, as_stream(stream), true});
 }
 
 int mdl_sequence_forward(const mdl_feature* feature, const int64_t* ids, const int64_t* lengths,

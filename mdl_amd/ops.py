@@ -567,6 +567,20 @@ def table_classes(tables: np.ndarray) -> int:
     return int(lib().mdl_table_classes(tables.ctypes.data, len(tables)))
 
 
+def lane_elems(dim: int, esize: int, vec: bool) -> int:
+    """Elements one lane moves per row in the kernels (their width rule):
+    one 16-byte vector of the weight type, doubled up to 8 elements while
+    four lanes do not cover the row and the doubled width divides ``dim``;
+    1 for rows that are not 16-byte aligned."""
+
+    if not vec:
+        return 1
+    w = 1 if esize == 2 else 0
+    while (8 << w) <= 8 and (4 << w) * 4 < dim and dim % (8 << w) == 0:
+        w += 1
+    return 4 << w
+
+
 def _tables_array(plan: GroupPlan, feats: np.ndarray) -> np.ndarray:
     tables = np.zeros(len(plan.tables), dtype=TABLE_DTYPE)
     users: dict[int, list[int]] = {}
@@ -589,7 +603,7 @@ def _tables_array(plan: GroupPlan, feats: np.ndarray) -> np.ndarray:
         rec["gdtype"] = gd.pop() if gd else dtype_code(w.dtype)
         esize = w.element_size()
         vec = w.data_ptr() % 16 == 0 and (int(w.size(1)) * esize) % 16 == 0
-        lanes_cover = 64 * (16 // esize if vec else 1)
+        lanes_cover = 64 * lane_elems(int(w.size(1)), esize, vec)
         if int(w.size(1)) > lanes_cover:
             raise NotImplementedError(
                 f"backward supports rows of at most {lanes_cover} elements for this table layout"

@@ -8,7 +8,7 @@ import subprocess
 import numpy as np
 import pytest
 
-from mdl_amd import _lib
+from mdl_amd import _lib, ops
 from tests.conftest import ROOT
 
 HEADER = ROOT / "include" / "mdl_hip.h"
@@ -116,10 +116,42 @@ def test_class_masks_follow_dtype_and_alignment():
     feats["weight"] = [256, 512, 1024]
     feats["out"] = [4096, 8192, 8196]
     m = lib.mdl_feature_classes(feats.ctypes.data, 3)
-    assert m == (1 << 0) | (1 << 2) | (1 << 5)
+    # variant = 3 * class + log2(C / 4): fp32 x 64 moves 8 per lane (class 0),
+    # bf16 x 64 8 per lane (class 2), unaligned bf16 -> fp32 rows 1 (class 5)
+    assert m == (1 << (3 * 0 + 1)) | (1 << (3 * 2 + 1)) | (1 << (3 * 5))
     tables = np.zeros(2, dtype=_lib.TABLE_DTYPE)
     tables["wdtype"] = [_lib.MDL_F32, _lib.MDL_BF16]
     tables["gdtype"] = [_lib.MDL_F32, _lib.MDL_BF16]
     tables["dim"] = [3, 32]
     tables["weight"] = [256, 512]
-    assert lib.mdl_table_classes(tables.ctypes.data, 2) == (1 << 1) | (1 << 2)
+    # fp32 x 3 is unaligned (class 1); bf16 x 32: four lanes of 8 cover it (class 2, C = 8)
+    assert lib.mdl_table_classes(tables.ctypes.data, 2) == (1 << (3 * 1)) | (1 << (3 * 2 + 1))
+
+
+@pytest.mark.parametrize("dim,esize,vec,expect", [
+    (16, 4, True, 4), (32, 4, True, 8), (64, 4, True, 8), (128, 4, True, 8), (24, 4, True, 8),
+    (40, 4, True, 8), (300, 4, True, 4), (8, 2, True, 8), (64, 2, True, 8), (24, 2, True, 8), (3, 4, False, 1),
+])
+def test_lane_width_rule(dim, esize, vec, expect):
+    # C divides dim, so a lane's elements lie wholly inside the row
+    c = ops.lane_elems(dim, esize, vec)
+    assert c == expect and dim % c == 0
+
+
+def test_lane_width_rule_matches_the_library():
+    """The host rule (used to reject rows too wide for the backward) and the
+    library's variant of a table agree for every dim and dtype."""
+    lib = _lib.lib()
+    tables = np.zeros(1, dtype=_lib.TABLE_DTYPE)
+    for wd, esize in ((_lib.MDL_F32, 4), (_lib.MDL_BF16, 2)):
+        for dim in range(1, 300):
+            tables["wdtype"] = wd
+            tables["gdtype"] = wd
+            tables["dim"] = dim
+            tables["weight"] = 4096
+            m = lib.mdl_table_classes(tables.ctypes.data, 1)
+            vec = (dim * esize) % 16 == 0
+            c = ops.lane_elems(dim, esize, vec)
+            cls = (0 if wd == _lib.MDL_F32 else 2) + (0 if vec else 1)
+            w = 0 if c == 1 else {4: 0, 8: 1, 16: 2}[c]
+            assert m == 1 << (3 * cls + w), (wd, dim)
