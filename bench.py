@@ -282,7 +282,7 @@ def algorithmic_bytes(wl: Workload, ids, lengths) -> dict:
 class DeviceStep:
     """Tables, persistent buffers and one SparseStep per synthetic batch."""
 
-    def __init__(self, wl: Workload, batches, device):
+    def __init__(self, wl: Workload, batches, device, layout: str = "slot"):
         import torch
 
         from mdl_amd import ops
@@ -308,17 +308,30 @@ class DeviceStep:
                 self.tables[f.table], pooling=f.pooling, null_policy="exclude", state=self.states[f.table]
             )
         sum_d = sum(wl.dims[f.table] for f in wl.features)
-        # pooled outputs go straight into the token-slot buffer [B, sum(dim)]
-        self.out = torch.empty((wl.batch, sum_d), dtype=wdtype, device=device)
-        self.grad = torch.empty((wl.batch, sum_d), dtype=wdtype, device=device)
-        self.grad.normal_(0.0, 1.0, generator=gen)
-        col = 0
         out_views, grad_views = [], []
-        for f in wl.features:
-            d = wl.dims[f.table]
-            out_views.append(self.out[:, col: col + d])
-            grad_views.append(self.grad[:, col: col + d])
-            col += d
+        if layout == "slot":
+            # pooled outputs go straight into the token-slot buffer [B, sum(dim)]
+            self.out = torch.empty((wl.batch, sum_d), dtype=wdtype, device=device)
+            self.grad = torch.empty((wl.batch, sum_d), dtype=wdtype, device=device)
+            self.grad.normal_(0.0, 1.0, generator=gen)
+            col = 0
+            for f in wl.features:
+                d = wl.dims[f.table]
+                out_views.append(self.out[:, col: col + d])
+                grad_views.append(self.grad[:, col: col + d])
+                col += d
+        else:
+            # one [B, dim] output per feature, as the grouped lookup returns them
+            # (src/embeddings.py:1646-1751, pooled per feature src/model.py:590-678)
+            self.out = torch.empty(wl.batch * sum_d, dtype=wdtype, device=device)
+            self.grad = torch.empty(wl.batch * sum_d, dtype=wdtype, device=device)
+            self.grad.normal_(0.0, 1.0, generator=gen)
+            off = 0
+            for f in wl.features:
+                d = wl.dims[f.table]
+                out_views.append(self.out[off: off + wl.batch * d].view(wl.batch, d))
+                grad_views.append(self.grad[off: off + wl.batch * d].view(wl.batch, d))
+                off += wl.batch * d
         self.err = torch.zeros(1, dtype=torch.int32, device=device)
         # device-resident batches: packed ids + concatenated lengths (an unpooled
         # feature contributes one pseudo-bag holding all its ids)
@@ -482,6 +495,111 @@ def cpu_baseline(wl: Workload, seconds: float = 12.0, row_cap: int = 1 << 16, ba
     }
 
 
+# ------------------------------------------------------------ rocprof data --
+#
+# HBM traffic of the dominant kernel comes from two rocprofv3 counter runs of
+# this script (FETCH_SIZE, then WRITE_SIZE, KiB per dispatch), each scaled by
+# what the same counter reads for a plain 1 GiB device copy measured in the
+# same runs (--calibrate-copy):
+#   rocprofv3 --pmc FETCH_SIZE -d D1 -o run -- python bench.py --calibrate-copy ...
+# (the calibration kernel is torch.neg over 1 GiB: 1 GiB read, 1 GiB written)
+#   rocprofv3 --pmc WRITE_SIZE -d D2 -o run -- python bench.py --calibrate-copy ...
+#   python bench.py --summarize-pmc D1 D2 --pmc-out profiles/<config>_traffic.json
+# The bench line then reports that file's figure as roofline.traffic.
+
+KERNEL_GROUPS = {
+    "forward": ("forward_kernel",),
+    "apply": ("bwd_reduce_kernel<false", "bwd_reduce_kernel<true"),
+    "sort": ("radix_upsweep", "radix_scan", "radix_downsweep"),
+}
+COPY_BYTES = 1 << 30
+
+
+def _rocpd_rows(dirs, query):
+    import glob
+    import sqlite3
+
+    for d in dirs:
+        for f in sorted(glob.glob(os.path.join(d, "**", "*.db"), recursive=True)):
+            con = sqlite3.connect(f)
+            try:
+                yield from con.execute(query)
+            finally:
+                con.close()
+
+
+def summarize_pmc(dirs, out_path, config):
+    """Per-dispatch FETCH_SIZE / WRITE_SIZE of the kernel groups and the copy
+    calibration, from rocprofv3 --pmc databases; writes a JSON summary."""
+
+    per = {}
+    for name, ctr, val in _rocpd_rows(dirs, "select kernel_name, counter_name, value from counters_collection"):
+        per.setdefault(ctr, {}).setdefault(name, []).append(float(val))
+    for ctr in ("FETCH_SIZE", "WRITE_SIZE"):
+        if ctr not in per:
+            raise SystemExit(f"no {ctr} samples under {dirs}")
+    copy = [n for n in per["FETCH_SIZE"] if "neg_kernel" in n]
+    if not copy:
+        raise SystemExit("no copy-kernel calibration samples (run with --calibrate-copy)")
+    cname = max(copy, key=lambda n: np.mean(per["FETCH_SIZE"][n]))
+    f_kib = float(np.mean(per["FETCH_SIZE"][cname]))
+    w_kib = float(np.mean(per["WRITE_SIZE"].get(cname, [float("nan")])))
+    scale = {"FETCH_SIZE": COPY_BYTES / (f_kib * 1024), "WRITE_SIZE": COPY_BYTES / (w_kib * 1024)}
+    groups = {}
+    for g, pats in KERNEL_GROUPS.items():
+        tot = {"FETCH_SIZE": 0.0, "WRITE_SIZE": 0.0}
+        kernels = {}
+        for ctr in tot:
+            for n, vals in per[ctr].items():
+                if any(p in n for p in pats):
+                    # dispatches per step: the group's kernels repeat the same
+                    # number of times, so the mean per dispatch x (launches per
+                    # step) is the traffic of one step's launch of the group
+                    k = kernels.setdefault(n.split("(")[0].replace("void ", ""), {})
+                    k[ctr + "_KiB"] = float(np.mean(vals))
+                    k["dispatches"] = len(vals)
+        steps = max((k["dispatches"] for k in kernels.values()), default=0)
+        for k in kernels.values():
+            for ctr in tot:
+                tot[ctr] += k.get(ctr + "_KiB", 0.0) * k["dispatches"] / max(steps, 1)
+        groups[g] = {
+            "kernels": kernels,
+            "fetch_KiB_per_launch": tot["FETCH_SIZE"],
+            "write_KiB_per_launch": tot["WRITE_SIZE"],
+            "hbm_bytes_per_launch": tot["FETCH_SIZE"] * 1024 * scale["FETCH_SIZE"]
+            + tot["WRITE_SIZE"] * 1024 * scale["WRITE_SIZE"],
+        }
+    res = {"config": config, "copy_kernel": cname, "copy_bytes": COPY_BYTES, "copy_FETCH_KiB": f_kib,
+           "copy_WRITE_KiB": w_kib, "scale": scale, "groups": groups}
+    Path(out_path).write_text(json.dumps(res, indent=1) + "\n")
+    print(json.dumps(res, indent=1))
+
+
+def summarize_trace(dirs, out_path, title, command):
+    """Markdown table of per-kernel durations from rocprofv3 --kernel-trace."""
+
+    agg = {}
+    for name, dur in _rocpd_rows(dirs, "select name, duration from kernels"):
+        agg.setdefault(name.replace("void ", "").split("(")[0], []).append(float(dur))
+    total = sum(sum(v) for v in agg.values())
+    lines = [f"# {title}", "", "```", command, "```", "", "| kernel | calls | avg us | total ms | share |",
+             "|---|---:|---:|---:|---:|"]
+    for k, v in sorted(agg.items(), key=lambda kv: -sum(kv[1])):
+        lines.append(f"| `{k}` | {len(v)} | {np.mean(v) / 1e3:.1f} | {sum(v) / 1e6:.2f} | {100 * sum(v) / total:.1f}% |")
+    Path(out_path).write_text("\n".join(lines) + "\n")
+    print("\n".join(lines))
+
+
+def load_traffic(config: str):
+    p = ROOT / "profiles" / f"{config}_traffic.json"
+    if not p.exists():
+        return None
+    try:
+        return json.loads(p.read_text())
+    except (OSError, ValueError):
+        return None
+
+
 # ------------------------------------------------------------------- main --
 
 
@@ -494,7 +612,27 @@ def main() -> int:
     ap.add_argument("--batches", type=int, default=3, help="distinct synthetic batches cycled through")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
+    ap.add_argument("--calibrate-copy", action="store_true",
+                    help="also run three plain 1 GiB device copies (counter calibration for rocprofv3 --pmc runs)")
+    ap.add_argument("--summarize-pmc", nargs="+", metavar="DIR",
+                    help="summarise rocprofv3 --pmc databases into --pmc-out and exit (no GPU)")
+    ap.add_argument("--pmc-out", default=None)
+    ap.add_argument("--summarize-trace", nargs="+", metavar="DIR",
+                    help="summarise rocprofv3 --kernel-trace databases into --trace-out and exit (no GPU)")
+    ap.add_argument("--trace-out", default=None)
+    ap.add_argument("--trace-command", default="")
+    ap.add_argument("--layout", choices=["slot", "feature"], default="slot",
+                    help="pooled outputs and their gradients: one [B, sum(dim)] token-slot buffer, or one [B, dim] "
+                         "tensor per feature")
     args = ap.parse_args()
+    if args.summarize_pmc:
+        summarize_pmc(args.summarize_pmc, args.pmc_out or str(ROOT / "profiles" / f"{args.config}_traffic.json"),
+                      args.config)
+        return 0
+    if args.summarize_trace:
+        summarize_trace(args.summarize_trace, args.trace_out or "/dev/stdout",
+                        f"{args.config}: rocprofv3 kernel trace", args.trace_command)
+        return 0
     if args.gpus != 1:
         print(f"bench.py measures one GPU only; --gpus {args.gpus} is not supported in this build "
               "(the path is single-GPU; multi-GPU sharding is a design note, not a measured run)",
@@ -512,9 +650,20 @@ def main() -> int:
     alg = [algorithmic_bytes(wl, ids, lengths) for ids, lengths in batches]
     print(f"[bench] drew {args.batches} batches; {alg[0]['n_ids']} ids/step, "
           f"{alg[0]['unique_rows']} distinct rows", file=sys.stderr, flush=True)
-    dev = (SequenceDeviceStep if wl.kind == "sequence" else DeviceStep)(wl, batches, device)
+    if wl.kind == "sequence":
+        dev = SequenceDeviceStep(wl, batches, device)
+    else:
+        dev = DeviceStep(wl, batches, device, layout=args.layout)
     torch.cuda.synchronize()
     print("[bench] tables initialised", file=sys.stderr, flush=True)
+    if args.calibrate_copy:
+        # a plain streaming kernel of known traffic: read 1 GiB, write 1 GiB
+        src = torch.ones(COPY_BYTES // 4, dtype=torch.float32, device=device)
+        dst = torch.empty_like(src)
+        for _ in range(3):
+            torch.neg(src, out=dst)
+        torch.cuda.synchronize()
+        del src, dst
     for i in range(args.warmup):
         dev.step(i)
     torch.cuda.synchronize()
@@ -563,7 +712,13 @@ def main() -> int:
         kms = timers[name].mean_ms()
         kernels[name] = {"kernel": label, "ms": kms, "alg_bytes_per_launch": nbytes,
                          "achieved_gbps": nbytes / (kms * 1e-3) / 1e9}
-    dom = max(kernels.values(), key=lambda k: k["ms"])
+    dom_name = max(kernels, key=lambda k: kernels[k]["ms"])
+    dom = kernels[dom_name]
+    traffic = None
+    tr = load_traffic(wl.name)
+    if tr is not None and dom_name in tr.get("groups", {}):
+        traffic = tr["groups"][dom_name]["hbm_bytes_per_launch"]
+        dom["traffic_source"] = f"profiles/{wl.name}_traffic.json (rocprofv3 FETCH_SIZE/WRITE_SIZE, copy-calibrated)"
     result = {
         "metric": METRIC,
         "value": rows_per_s,
@@ -595,7 +750,7 @@ def main() -> int:
             "peak": PEAK_HBM_GBPS,
             "unit": "GB/s",
             "frac": dom["achieved_gbps"] / PEAK_HBM_GBPS,
-            "traffic": None,
+            "traffic": traffic,
             "kernel_ms": dom["ms"],
             "alg_bytes_per_launch": dom["alg_bytes_per_launch"],
         },

@@ -677,7 +677,7 @@ __device__ __forceinline__ void fixup_chunk(const BwdArgs& a, int64_t c, const C
 }
 
 template <bool kFixup, int kMode, typename TW, typename TG, bool kVec>
-__global__ __launch_bounds__(kBwdWaves * kWave) void bwd_reduce_kernel(BwdArgs a) {
+__global__ MDL_OCCUPANCY __launch_bounds__(kBwdWaves * kWave) void bwd_reduce_kernel(BwdArgs a) {
   const int w = threadIdx.x / kWave;
   // One wave per chunk.  The grid covers the worst-case chunk count; only the
   // first `real` blocks have work (the rest return at once).  The hardware

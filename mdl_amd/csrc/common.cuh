@@ -135,6 +135,14 @@ __device__ __forceinline__ const T* zero_row() {
 #endif
 constexpr int kPassesPerChunk = MDL_PASSES;
 
+// Waves per SIMD the gather/reduce kernels are compiled for: their per-wave
+// work is a chain of dependent memory round trips, so throughput follows the
+// number of resident waves more than the registers each one keeps.
+#ifndef MDL_WAVES_PER_EU
+#define MDL_WAVES_PER_EU 5
+#endif
+#define MDL_OCCUPANCY __attribute__((amdgpu_waves_per_eu(MDL_WAVES_PER_EU)))
+
 // Rows per lane group per iteration for lanes of C elements.
 template <int C>
 __host__ __device__ constexpr int unroll_for() {

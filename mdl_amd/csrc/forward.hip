@@ -100,44 +100,69 @@ __device__ __forceinline__ void gather_chunk(const Feat& f, int64_t first, int c
   for (int cb = 0; cb < ncb; ++cb) {
     const int col = (cb * L + sub) * C;
     const bool col_ok = col < f.dim;
-    int64_t nid[kUnroll];  // ids of the next pass group, fetched one group ahead
-#pragma unroll
-    for (int u = 0; u < kUnroll; ++u) {
-      const int i = u * G + slot;
-      nid[u] = i < count ? ids[i] : 0;
-    }
-    for (int base = 0; base < count; base += step) {
-      int64_t id[kUnroll];
-      float v[kUnroll][C];
+    // Two pass groups in flight: the rows of group k+1 are requested before
+    // group k is stored, so no row load waits behind a store.
+    int64_t nid[kUnroll];  // ids of the next group to load
+    auto fetch_ids = [&](int base) {
 #pragma unroll
       for (int u = 0; u < kUnroll; ++u) {
-        id[u] = nid[u];
         const int i = base + u * G + slot;
-        const bool ok = i < count && (uint64_t)id[u] < (uint64_t)f.num_rows && col_ok;
-        RowIO<TW, C>::load(ok ? W + id[u] * f.dim + col : zero_row<TW>(), v[u]);
-      }
-#pragma unroll
-      for (int u = 0; u < kUnroll; ++u) {
-        const int i = base + step + u * G + slot;
         nid[u] = i < count ? ids[i] : 0;
       }
+    };
+    auto load_rows = [&](int base, float (&v)[kUnroll][C]) {
+#pragma unroll
+      for (int u = 0; u < kUnroll; ++u) {
+        const int i = base + u * G + slot;
+        const bool ok = i < count && (uint64_t)nid[u] < (uint64_t)f.num_rows && col_ok;
+        RowIO<TW, C>::load(ok ? W + nid[u] * f.dim + col : zero_row<TW>(), v[u]);
+      }
+    };
+    auto store_rows = [&](int base, const float (&v)[kUnroll][C]) {
 #pragma unroll
       for (int u = 0; u < kUnroll; ++u) {
         const int i = base + u * G + slot;
         if (i < count && col_ok) RowIO<TO, C>::store(out + (first + i) * f.out_stride + col, v[u]);
       }
+    };
+    float va[kUnroll][C], vb[kUnroll][C];
+    fetch_ids(0);
+    load_rows(0, va);
+    fetch_ids(step);
+    for (int base = 0; base < count; base += 2 * step) {
+      const bool more = base + step < count;
+      if (more) {
+        load_rows(base + step, vb);
+        fetch_ids(base + 2 * step);
+      }
+      store_rows(base, va);
+      if (!more) break;
+      if (base + 2 * step < count) {
+        load_rows(base + 2 * step, va);
+        fetch_ids(base + 3 * step);
+      }
+      store_rows(base + step, vb);
     }
   }
-  // Sort keys and payloads (and the invalid-id count), one id per lane.
+  // Sort keys and payloads (and the invalid-id count), one id per lane, the
+  // loads of a batch issued before its stores.
+  constexpr int kBatch = 4;
   int bad = 0;
-  for (int i = lane; i < count; i += kWave) {
-    const int64_t id = ids[i];
-    const bool in_range = (uint64_t)id < (uint64_t)f.num_rows;
-    bad += !in_range;
-    if (a.keys != nullptr) {
-      const int64_t e = f.ids_begin + first + i;
-      a.keys[e] = (in_range && id != f.padding_idx) ? (uint32_t)(f.row_base + id) : a.sentinel;
-      a.payload[e] = (uint32_t)(f.payload_base + first + i);
+  for (int i0 = lane; i0 < count; i0 += kWave * kBatch) {
+    int64_t id[kBatch];
+#pragma unroll
+    for (int q = 0; q < kBatch; ++q) id[q] = i0 + q * kWave < count ? ids[i0 + q * kWave] : 0;
+#pragma unroll
+    for (int q = 0; q < kBatch; ++q) {
+      const int i = i0 + q * kWave;
+      if (i >= count) break;
+      const bool in_range = (uint64_t)id[q] < (uint64_t)f.num_rows;
+      bad += !in_range;
+      if (a.keys != nullptr) {
+        const int64_t e = f.ids_begin + first + i;
+        a.keys[e] = (in_range && id[q] != f.padding_idx) ? (uint32_t)(f.row_base + id[q]) : a.sentinel;
+        a.payload[e] = (uint32_t)(f.payload_base + first + i);
+      }
     }
   }
   if (bad && a.error_count) atomicAdd(a.error_count, bad);
@@ -189,9 +214,40 @@ __device__ __forceinline__ int bag_of(const int64_t* s_off, int nb, int64_t e) {
   return lo;
 }
 
+// Pooled rows of a chunk are staged in LDS (fp32) while the ids are walked and
+// written out after the walk: a store inside the walk would make the next
+// row loads wait for it (one in-order counter for loads and stores).
+constexpr int kOutStage = 1024;  // staged floats per wave
+
+template <int C>
+__device__ __forceinline__ void lds_put(float* p, const float (&v)[C]) {
+  if constexpr (C % 4 == 0) {
+#pragma unroll
+    for (int q = 0; q < C / 4; ++q)
+      reinterpret_cast<float4*>(p)[q] = make_float4(v[4 * q], v[4 * q + 1], v[4 * q + 2], v[4 * q + 3]);
+  } else {
+#pragma unroll
+    for (int k = 0; k < C; ++k) p[k] = v[k];
+  }
+}
+
+template <int C>
+__device__ __forceinline__ void lds_get(const float* p, float (&v)[C]) {
+  if constexpr (C % 4 == 0) {
+#pragma unroll
+    for (int q = 0; q < C / 4; ++q) {
+      const float4 x = reinterpret_cast<const float4*>(p)[q];
+      v[4 * q] = x.x; v[4 * q + 1] = x.y; v[4 * q + 2] = x.z; v[4 * q + 3] = x.w;
+    }
+  } else {
+#pragma unroll
+    for (int k = 0; k < C; ++k) v[k] = p[k];
+  }
+}
+
 template <typename TW, typename TO, int C>
-__device__ __forceinline__ void pooled_chunk(const Feat& f, int64_t first_bag, int nb, int64_t* s_off,
-                                             const FwdArgs& a) {
+__device__ __forceinline__ void pooled_chunk(const Feat& f, int64_t first_bag, int nb, const int64_t* s_off,
+                                             float* s_out, float* s_cnt, const FwdArgs& a) {
   constexpr int U = unroll_for<C>();  // ids per slot per iteration
   const int lane = lane_id();
   const int64_t e_begin = s_off[0], e_end = s_off[nb];
@@ -205,6 +261,7 @@ __device__ __forceinline__ void pooled_chunk(const Feat& f, int64_t first_bag, i
   // (already-embedded input); the ids only decide the null weights.
   const bool by_pos = (f.flags & MDL_FLAG_ROWS_BY_POSITION) != 0;
   const bool mean = f.pooling == MDL_POOL_MEAN;
+  const bool staged = (int64_t)nb * f.dim <= kOutStage;
   const TW* W = static_cast<const TW*>(f.weight);
   TO* out = static_cast<TO*>(f.out);
   // This slot's slice [s0, s1) of the chunk's ids.
@@ -214,6 +271,21 @@ __device__ __forceinline__ void pooled_chunk(const Feat& f, int64_t first_bag, i
   const bool any = s0 < s1;
   const int b0 = any ? bag_of(s_off, nb, s0) : 0;
   const bool cont = any && s_off[b0] < s0;  // the slice starts inside a bag
+
+  // Pooled row of bag b from its sum and weight: staged, or stored at once.
+  auto emit_row = [&](int bag, const float (&sum)[C], float wsum, int col, bool col_ok, bool emit_cnt) {
+    const float inv = mean ? __builtin_amdgcn_rcpf(fmaxf(wsum, 1.f)) : 1.f;
+    float r[C];
+#pragma unroll
+    for (int k = 0; k < C; ++k) r[k] = sum[k] * inv;
+    if (staged) {
+      if (col_ok) lds_put<C>(s_out + (int64_t)bag * f.dim + col, r);
+      if (emit_cnt) s_cnt[bag] = wsum;
+    } else {
+      if (col_ok) RowIO<TO, C>::store(out + (first_bag + bag) * f.out_stride + col, r);
+      if (emit_cnt && a.bag_count != nullptr) a.bag_count[f.payload_base + first_bag + bag] = wsum;
+    }
+  };
 
   for (int cb = 0; cb < ncb; ++cb) {
     const int col = (cb * L + sub) * C;
@@ -256,14 +328,7 @@ __device__ __forceinline__ void pooled_chunk(const Feat& f, int64_t first_bag, i
         wsum += wt[u];
         if (e + 1 == bend) {
           if (s_off[b] >= s0) {
-            if (col_ok) {
-              const float inv = mean ? __builtin_amdgcn_rcpf(fmaxf(wsum, 1.f)) : 1.f;
-              float r[C];
-#pragma unroll
-              for (int k = 0; k < C; ++k) r[k] = acc[k] * inv;
-              RowIO<TO, C>::store(out + (first_bag + b) * f.out_stride + col, r);
-            }
-            if (emit && a.bag_count != nullptr) a.bag_count[f.payload_base + first_bag + b] = wsum;
+            emit_row(b, acc, wsum, col, col_ok, emit);
           } else {
 #pragma unroll
             for (int k = 0; k < C; ++k) hp[k] = acc[k];
@@ -309,16 +374,30 @@ __device__ __forceinline__ void pooled_chunk(const Feat& f, int64_t first_bag, i
     for (int k = 0; k < C; ++k) in[k] = shfl_f(o[k], prev);
     const float inw = shfl_f(ow, prev);
     if (hbag >= 0) {
-      const float tw = inw + hw;
-      if (col_ok) {
-        const float inv = mean ? __builtin_amdgcn_rcpf(fmaxf(tw, 1.f)) : 1.f;
-        float r[C];
+      float t[C];
 #pragma unroll
-        for (int k = 0; k < C; ++k) r[k] = (in[k] + hp[k]) * inv;
-        RowIO<TO, C>::store(out + (first_bag + hbag) * f.out_stride + col, r);
-      }
-      if (emit && a.bag_count != nullptr) a.bag_count[f.payload_base + first_bag + hbag] = tw;
+      for (int k = 0; k < C; ++k) t[k] = in[k] + hp[k];
+      emit_row(hbag, t, inw + hw, col, col_ok, emit);
     }
+  }
+  if (staged) {
+    // Flush the staged rows (empty bags pool to zero) and the bag weights.
+    wave_sync();
+    for (int bb = slot; bb < nb; bb += G) {
+      const bool empty = s_off[bb] == s_off[bb + 1];
+      for (int cb = 0; cb < ncb; ++cb) {
+        const int col = (cb * L + sub) * C;
+        if (col >= f.dim) continue;
+        float r[C];
+        if (empty) zero_c(r);
+        else lds_get<C>(s_out + (int64_t)bb * f.dim + col, r);
+        RowIO<TO, C>::store(out + (first_bag + bb) * f.out_stride + col, r);
+      }
+    }
+    if (a.bag_count != nullptr)
+      for (int i = lane; i < nb; i += kWave)
+        a.bag_count[f.payload_base + first_bag + i] = s_off[i] == s_off[i + 1] ? 0.f : s_cnt[i];
+    return;
   }
   // Empty bags pool to zero.
   for (int bb = slot; bb < nb; bb += G) {
@@ -339,38 +418,51 @@ __device__ __forceinline__ void pooled_chunk(const Feat& f, int64_t first_bag, i
 // of the staged bounds, resumed from the lane's previous id.
 __device__ __forceinline__ int pooled_keys(const Feat& f, int64_t first_bag, int nb, const int64_t* s_off,
                                            const FwdArgs& a) {
+  constexpr int kBatch = 4;  // ids per lane whose loads are issued before any store
   const int lane = lane_id();
   const int64_t e_begin = s_off[0], e_end = s_off[nb];
   const bool exclude = (f.flags & MDL_FLAG_EXCLUDE_NULL) != 0;
   const bool by_pos = (f.flags & MDL_FLAG_ROWS_BY_POSITION) != 0;
   int bad = 0;
   int b = 0;
-  for (int64_t e = e_begin + lane; e < e_end; e += kWave) {
-    int hi = nb - 1;  // last bag with s_off[bag] <= e, searched in [b, nb)
-    while (b < hi) {
-      const int mid = (b + hi + 1) >> 1;
-      if (s_off[mid] <= e) b = mid;
-      else hi = mid - 1;
+  for (int64_t base = e_begin + lane; base < e_end; base += kWave * kBatch) {
+    int64_t id[kBatch];
+#pragma unroll
+    for (int q = 0; q < kBatch; ++q) {
+      const int64_t e = base + q * kWave;
+      id[q] = e < e_end ? a.ids[e] : 0;
     }
-    const int64_t id = a.ids[e];
-    const int64_t row = by_pos ? e - f.ids_begin : id;
-    const bool in_range = (uint64_t)row < (uint64_t)f.num_rows;
-    bad += !in_range;
-    if (a.keys != nullptr) {
-      // Invalid ids and nulls under "exclude" pool with weight 0: their
-      // gradient is exactly zero, so they take no part in the backward.
-      // Rows by position belong to no table.
-      const bool live = in_range && !(exclude && id == 0) && !by_pos && id != f.padding_idx;
-      a.keys[e] = live ? (uint32_t)(f.row_base + id) : a.sentinel;
-      a.payload[e] = (uint32_t)(f.payload_base + first_bag + b);
+#pragma unroll
+    for (int q = 0; q < kBatch; ++q) {
+      const int64_t e = base + q * kWave;
+      if (e >= e_end) break;
+      int hi = nb - 1;  // last bag with s_off[bag] <= e, searched in [b, nb)
+      while (b < hi) {
+        const int mid = (b + hi + 1) >> 1;
+        if (s_off[mid] <= e) b = mid;
+        else hi = mid - 1;
+      }
+      const int64_t row = by_pos ? e - f.ids_begin : id[q];
+      const bool in_range = (uint64_t)row < (uint64_t)f.num_rows;
+      bad += !in_range;
+      if (a.keys != nullptr) {
+        // Invalid ids and nulls under "exclude" pool with weight 0: their
+        // gradient is exactly zero, so they take no part in the backward.
+        // Rows by position belong to no table.
+        const bool live = in_range && !(exclude && id[q] == 0) && !by_pos && id[q] != f.padding_idx;
+        a.keys[e] = live ? (uint32_t)(f.row_base + id[q]) : a.sentinel;
+        a.payload[e] = (uint32_t)(f.payload_base + first_bag + b);
+      }
     }
   }
   return bad;
 }
 
 template <typename TW, typename TO, bool kVec>
-__global__ __launch_bounds__(kFwdWaves * kWave) void forward_kernel(FwdArgs a) {
+__global__ MDL_OCCUPANCY __launch_bounds__(kFwdWaves * kWave) void forward_kernel(FwdArgs a) {
   __shared__ int64_t s_off[kFwdWaves][kMaxBagsPerChunk + 1];
+  __shared__ __align__(16) float s_out[kFwdWaves][kOutStage];
+  __shared__ float s_cnt[kFwdWaves][kMaxBagsPerChunk];
   const int w = threadIdx.x / kWave;
   const int64_t blk = xcd_block(blockIdx.x, gridDim.x);
   const int64_t c = uni64(blk * kFwdWaves + w);
@@ -391,8 +483,11 @@ __global__ __launch_bounds__(kFwdWaves * kWave) void forward_kernel(FwdArgs a) {
     return;
   }
   int bad = stage_offsets(f, ch.first, ch.count, s_off[w], a);
+  with_width<TW, kVec>(v % kWidths, [&]<int C>() {
+    pooled_chunk<TW, TO, C>(f, ch.first, ch.count, s_off[w], s_out[w], s_cnt[w], a);
+  });
+  // After the walk, so that its stores never hold up the walk's loads.
   bad += pooled_keys(f, ch.first, ch.count, s_off[w], a);
-  with_width<TW, kVec>(v % kWidths, [&]<int C>() { pooled_chunk<TW, TO, C>(f, ch.first, ch.count, s_off[w], a); });
   for (int m = 1; m < kWave; m <<= 1) bad += __shfl_xor(bad, m);
   if (lane_id() == 0 && bad && a.error_count) atomicAdd(a.error_count, bad);
 }
