@@ -20,21 +20,27 @@ constexpr int kSortThreads = 256;
 constexpr int kSortWaves = kSortThreads / kWave;
 constexpr int kSortItems = 16;
 constexpr int kSortTile = kSortThreads * kSortItems;
-constexpr int kRadix = 256;
+constexpr int kDigitBits = 8;
+constexpr int kRadix = 1 << kDigitBits;
 
-__device__ uint32_t block_exclusive_scan_u32(uint32_t v, uint32_t* smem) {
-  const int tid = threadIdx.x;
-  smem[tid] = v;
-  __syncthreads();
-  for (int d = 1; d < kSortThreads; d <<= 1) {
-    uint32_t o = tid >= d ? smem[tid - d] : 0u;
-    __syncthreads();
-    smem[tid] += o;
-    __syncthreads();
+// Exclusive scan of one value per thread over a block of kSortThreads:
+// shuffles inside each wave, one barrier for the wave totals.  smem holds at
+// least kSortWaves words.
+__device__ __forceinline__ uint32_t block_exclusive_scan_u32(uint32_t v, uint32_t* smem) {
+  const int tid = threadIdx.x, lane = lane_id(), w = tid / kWave;
+  uint32_t x = v;
+#pragma unroll
+  for (int d = 1; d < kWave; d <<= 1) {
+    const uint32_t o = shfl_u(x, lane >= d ? lane - d : lane);
+    if (lane >= d) x += o;
   }
-  uint32_t incl = smem[tid];
+  if (lane == kWave - 1) smem[w] = x;
   __syncthreads();
-  return incl - v;
+  uint32_t before = 0;
+#pragma unroll
+  for (int q = 0; q < kSortWaves; ++q) before += q < w ? smem[q] : 0u;
+  __syncthreads();
+  return before + x - v;
 }
 
 __global__ __launch_bounds__(kSortThreads) void radix_upsweep(const uint32_t* __restrict__ keys, int64_t n,
@@ -44,17 +50,43 @@ __global__ __launch_bounds__(kSortThreads) void radix_upsweep(const uint32_t* __
   const int tid = threadIdx.x, w = tid / kWave;
   for (int i = tid; i < kSortWaves * kRadix; i += kSortThreads) (&hist[0][0])[i] = 0u;
   __syncthreads();
-  const int64_t base = (int64_t)blockIdx.x * kSortTile;
+  // Consecutive tiles run on one XCD, so the partial lines each tile writes
+  // (its counts column here, its digit runs in the downsweep) meet their
+  // neighbours in that XCD's L2 before they are written back.
+  const int tile = (int)xcd_block(blockIdx.x, ntiles);
+  const int64_t base = (int64_t)tile * kSortTile;
+  uint32_t k[kSortItems];
 #pragma unroll
   for (int i = 0; i < kSortItems; ++i) {
     const int64_t idx = base + (int64_t)i * kSortThreads + tid;
-    if (idx < n) atomicAdd(&hist[w][(keys[idx] >> shift) & mask], 1u);
+    k[i] = idx < n ? keys[idx] : 0u;
+  }
+  // A run of neighbouring lanes with one digit adds its length once, from
+  // its first lane.  Hot ids (Zipf) sit next to each other once the keys are
+  // ordered by their low digits, and the high digits change rarely between
+  // neighbours; one LDS atomic per lane would serialise those lanes on one
+  // address.
+  const int lane = lane_id();
+#pragma unroll
+  for (int i = 0; i < kSortItems; ++i) {
+    const int64_t idx = base + (int64_t)i * kSortThreads + tid;
+    const bool valid = idx < n;
+    const uint32_t d = (k[i] >> shift) & mask;
+    const uint32_t dprev = shfl_u(d, lane > 0 ? lane - 1 : 0);
+    const bool head = valid && (lane == 0 || d != dprev);
+    const uint64_t heads = __ballot(head);
+    const uint32_t nvalid = (uint32_t)__popcll(__ballot(valid));
+    if (head) {
+      const uint64_t after = heads & ~((2ull << lane) - 1ull);
+      const uint32_t end = after ? (uint32_t)__builtin_ctzll(after) : nvalid;
+      atomicAdd(&hist[w][d], end - (uint32_t)lane);
+    }
   }
   __syncthreads();
   uint32_t s = 0;
 #pragma unroll
   for (int q = 0; q < kSortWaves; ++q) s += hist[q][tid];
-  counts[(int64_t)tid * ntiles + blockIdx.x] = s;
+  counts[(int64_t)tid * ntiles + tile] = s;
 }
 
 // Exclusive scan of counts[d][0..ntiles) for digit d = blockIdx.x.
@@ -90,7 +122,7 @@ __global__ __launch_bounds__(kSortThreads) void radix_scan(uint32_t* __restrict_
   if (threadIdx.x == 0) digit_total[blockIdx.x] = carry;
 }
 
-__global__ __launch_bounds__(kSortThreads) void radix_downsweep(
+__global__ __launch_bounds__(kSortThreads) __attribute__((amdgpu_waves_per_eu(4))) void radix_downsweep(
     const uint32_t* __restrict__ keys_in, const uint32_t* __restrict__ vals_in,
     uint32_t* __restrict__ keys_out, uint32_t* __restrict__ vals_out, int64_t n, int shift, int bits,
     const uint32_t* __restrict__ counts, const uint32_t* __restrict__ digit_total, int ntiles) {
@@ -104,9 +136,14 @@ __global__ __launch_bounds__(kSortThreads) void radix_downsweep(
   const int tid = threadIdx.x, w = tid / kWave, lane = tid % kWave;
   const uint32_t mask = (bits >= 32) ? 0xffffffffu : ((1u << bits) - 1u);
   for (int i = tid; i < kSortWaves * kRadix; i += kSortThreads) (&s_wh[0][0])[i] = 0u;
+  // This tile's offset inside each digit and the digit totals, requested now
+  // and used after the ranking (thread d owns digit d; kSortThreads == kRadix).
+  const int tile = (int)xcd_block(blockIdx.x, ntiles);
+  const uint32_t my_count_off = counts[(int64_t)tid * ntiles + tile];
+  const uint32_t my_total = digit_total[tid];
   __syncthreads();
 
-  const int64_t tile_base = (int64_t)blockIdx.x * kSortTile;
+  const int64_t tile_base = (int64_t)tile * kSortTile;
   const int64_t wave_base = tile_base + (int64_t)w * (kWave * kSortItems);
   const uint64_t lt_mask = (lane == 0) ? 0ull : (~0ull >> (64 - lane));
   uint32_t k[kSortItems], v[kSortItems], rank[kSortItems];
@@ -123,7 +160,10 @@ __global__ __launch_bounds__(kSortThreads) void radix_downsweep(
     const bool valid = idx < n;
     const uint32_t d = (k[i] >> shift) & mask;
     uint64_t m = __ballot(valid);
-    for (int b = 0; b < bits; ++b) {
+    // Always eight ballots, unrolled: a narrower last digit has zero high
+    // bits in every lane, whose ballots leave m unchanged.
+#pragma unroll
+    for (int b = 0; b < kDigitBits; ++b) {
       const bool bit = (d >> b) & 1u;
       const uint64_t bb = __ballot(bit);
       m &= bit ? bb : ~bb;
@@ -147,9 +187,9 @@ __global__ __launch_bounds__(kSortThreads) void radix_downsweep(
       run += c;
     }
     const uint32_t tile_prefix = block_exclusive_scan_u32(run, s_scan);
-    const uint32_t global_prefix = block_exclusive_scan_u32(digit_total[d], s_scan);
+    const uint32_t global_prefix = block_exclusive_scan_u32(my_total, s_scan);
     s_tile[d] = tile_prefix;
-    s_gbase[d] = global_prefix + counts[(int64_t)d * ntiles + blockIdx.x] - tile_prefix;
+    s_gbase[d] = global_prefix + my_count_off - tile_prefix;
   }
   __syncthreads();
 #pragma unroll
