@@ -202,16 +202,107 @@ __device__ __forceinline__ int stage_offsets(const Feat& f, int64_t first_bag, i
   return clamped + dec;
 }
 
-// Last bag b in [0, nb) with s_off[b] <= e (the bag holding entry e, skipping
+// Last bag b in [0, nb) with off[b] <= e (the bag holding entry e, skipping
 // empty bags), by binary search over the staged bounds.
-__device__ __forceinline__ int bag_of(const int64_t* s_off, int nb, int64_t e) {
+template <typename T>
+__device__ __forceinline__ int bag_of(const T* off, int nb, T e) {
   int lo = 0, hi = nb - 1;
   while (lo < hi) {
     const int mid = (lo + hi + 1) >> 1;
-    if (s_off[mid] <= e) lo = mid;
+    if (off[mid] <= e) lo = mid;
     else hi = mid - 1;
   }
   return lo;
+}
+
+// Per-wave LDS of a pooled chunk.  Bag bounds are relative to the chunk's
+// first id.  row[i] is the table row of the chunk's id i (kNoRow: the id
+// pools with weight 0) for the first kIdStage ids, so ids are read from HBM
+// once, in one coalesced sweep, and the walk's only global loads are the
+// table rows; ids past the stage (a chunk of very long bags) are read where
+// they are used.
+constexpr int kIdStage = 480;
+constexpr uint32_t kNoRow = 0xffffffffu;
+struct PoolStage {
+  int32_t off[kMaxBagsPerChunk + 1];
+  float cnt[kMaxBagsPerChunk];
+  uint32_t row[kIdStage];
+};
+
+// Wave-uniform extent of a staged chunk.
+struct PoolChunk {
+  int64_t e0;  // first id of the chunk in the packed id array
+  int len;     // ids in the chunk
+  int lim;     // ids whose rows are staged
+};
+
+// Stage the chunk's bag bounds, clamped into the feature's own id range, so
+// lengths that do not add up to the ids passed can only give wrong sums (and
+// an error count), never an out-of-bounds read; decreasing offsets (negative
+// lengths) are made non-decreasing.  Then stage the rows of its ids, counting
+// ids outside [0, num_rows) into bad.
+__device__ __forceinline__ PoolChunk stage_pooled(const Feat& f, int64_t first_bag, int nb, PoolStage& st,
+                                                  const FwdArgs& a, int& bad) {
+  const int lane = lane_id();
+  const int64_t lo = f.ids_begin, hi = f.ids_begin + f.num_ids;
+  const int64_t* offs = a.offsets + f.bag_base + first_bag;
+  const int64_t o0 = offs[0];
+  PoolChunk pc;
+  pc.e0 = o0 < lo ? lo : (o0 > hi ? hi : o0);
+  int err = 0;
+  for (int i = lane; i <= nb; i += kWave) {
+    const int64_t o = offs[i];
+    const int64_t oc = o < lo ? lo : (o > hi ? hi : o);
+    err += oc != o;
+    int64_t r = oc - pc.e0;
+    if (r > 0x7fffffffll) {  // 2^31 ids in one chunk: cut short, counted
+      r = 0x7fffffffll;
+      ++err;
+    }
+    st.off[i] = (int32_t)(r < -0x7fffffffll ? -0x7fffffffll : r);
+  }
+  wave_sync();
+  int dec = 0;
+  for (int i = lane + 1; i <= nb; i += kWave) dec += st.off[i] < st.off[i - 1];
+  if (__ballot(dec != 0) != 0) {
+    // Error path: a running maximum makes every bag's bounds ordered.
+    if (lane == 0) {
+      int32_t m = st.off[0];
+      for (int i = 1; i <= nb; ++i) {
+        if (st.off[i] < m) st.off[i] = m;
+        m = st.off[i];
+      }
+    }
+    wave_sync();
+  }
+  err += dec;
+  pc.len = uni32(st.off[nb]);
+  // Rows are staged as 32-bit values; a table of 2^32 - 1 rows or more
+  // reads every id where it is used.
+  pc.lim = f.num_rows < (int64_t)kNoRow ? (pc.len < kIdStage ? pc.len : kIdStage) : 0;
+  const bool exclude = (f.flags & MDL_FLAG_EXCLUDE_NULL) != 0;
+  const bool by_pos = (f.flags & MDL_FLAG_ROWS_BY_POSITION) != 0;
+  constexpr int kBatch = 4;  // ids per lane whose loads are issued together
+  for (int i0 = lane; i0 < pc.lim; i0 += kWave * kBatch) {
+    int64_t id[kBatch];
+#pragma unroll
+    for (int q = 0; q < kBatch; ++q) id[q] = i0 + q * kWave < pc.lim ? a.ids[pc.e0 + i0 + q * kWave] : 0;
+#pragma unroll
+    for (int q = 0; q < kBatch; ++q) {
+      const int i = i0 + q * kWave;
+      if (i < pc.lim) {
+        // Rows by position: row e - ids_begin of `weight` is the id slot's
+        // row (already-embedded input); the ids only decide the null weights.
+        const int64_t row = by_pos ? pc.e0 + i - f.ids_begin : id[q];
+        const bool in_range = (uint64_t)row < (uint64_t)f.num_rows;
+        err += !in_range;
+        st.row[i] = in_range && !(exclude && id[q] == 0) ? (uint32_t)row : kNoRow;
+      }
+    }
+  }
+  wave_sync();
+  bad += err;
+  return pc;
 }
 
 // Pooled rows of a chunk are staged in LDS (fp32) while the ids are walked and
@@ -246,31 +337,40 @@ __device__ __forceinline__ void lds_get(const float* p, float (&v)[C]) {
 }
 
 template <typename TW, typename TO, int C>
-__device__ __forceinline__ void pooled_chunk(const Feat& f, int64_t first_bag, int nb, const int64_t* s_off,
-                                             float* s_out, float* s_cnt, const FwdArgs& a) {
+__device__ __forceinline__ void pooled_chunk(const Feat& f, int64_t first_bag, int nb, const PoolStage& st,
+                                             const PoolChunk& pc, float* s_out, const FwdArgs& a) {
   constexpr int U = unroll_for<C>();  // ids per slot per iteration
   const int lane = lane_id();
-  const int64_t e_begin = s_off[0], e_end = s_off[nb];
-  const int64_t len = e_end - e_begin;
+  const int len = pc.len;
   const int L = lanes_for(f.dim, C);
   const int G = kWave / L;
   const int slot = lane / L, sub = lane % L;
   const int ncb = (f.dim + L * C - 1) / (L * C);
   const bool exclude = (f.flags & MDL_FLAG_EXCLUDE_NULL) != 0;
-  // Rows by position: row e - ids_begin of `weight` is the id slot's row
-  // (already-embedded input); the ids only decide the null weights.
   const bool by_pos = (f.flags & MDL_FLAG_ROWS_BY_POSITION) != 0;
   const bool mean = f.pooling == MDL_POOL_MEAN;
   const bool staged = (int64_t)nb * f.dim <= kOutStage;
   const TW* W = static_cast<const TW*>(f.weight);
   TO* out = static_cast<TO*>(f.out);
   // This slot's slice [s0, s1) of the chunk's ids.
-  const int64_t K = (len + G - 1) / G;
-  const int64_t s0 = e_begin + slot * K;
-  const int64_t s1 = s0 + K < e_end ? s0 + K : e_end;
+  const int K = (len + G - 1) / G;
+  const int s0 = slot * K;
+  const int s1 = s0 + K < len ? s0 + K : len;
   const bool any = s0 < s1;
-  const int b0 = any ? bag_of(s_off, nb, s0) : 0;
-  const bool cont = any && s_off[b0] < s0;  // the slice starts inside a bag
+  const int b0 = any ? bag_of(st.off, nb, s0) : 0;
+  const bool cont = any && st.off[b0] < s0;  // the slice starts inside a bag
+
+  // Row of the chunk's id i, or -1 for weight 0.
+  auto row_at = [&](int i) -> int64_t {
+    if (i < pc.lim) {
+      const uint32_t r = st.row[i];
+      return r == kNoRow ? -1 : (int64_t)r;
+    }
+    const int64_t e = pc.e0 + i;
+    const int64_t id = a.ids[e];
+    const int64_t row = by_pos ? e - f.ids_begin : id;
+    return (uint64_t)row < (uint64_t)f.num_rows && !(exclude && id == 0) ? row : -1;
+  };
 
   // Pooled row of bag b from its sum and weight: staged, or stored at once.
   auto emit_row = [&](int bag, const float (&sum)[C], float wsum, int col, bool col_ok, bool emit_cnt) {
@@ -279,8 +379,8 @@ __device__ __forceinline__ void pooled_chunk(const Feat& f, int64_t first_bag, i
 #pragma unroll
     for (int k = 0; k < C; ++k) r[k] = sum[k] * inv;
     if (staged) {
-      if (col_ok) lds_put<C>(s_out + (int64_t)bag * f.dim + col, r);
-      if (emit_cnt) s_cnt[bag] = wsum;
+      if (col_ok) lds_put<C>(s_out + bag * f.dim + col, r);
+      if (emit_cnt) const_cast<PoolStage&>(st).cnt[bag] = wsum;
     } else {
       if (col_ok) RowIO<TO, C>::store(out + (first_bag + bag) * f.out_stride + col, r);
       if (emit_cnt && a.bag_count != nullptr) a.bag_count[f.payload_base + first_bag + bag] = wsum;
@@ -298,36 +398,32 @@ __device__ __forceinline__ void pooled_chunk(const Feat& f, int64_t first_bag, i
     int hbag = -1;  // first bag of a slice that starts inside it, when it ends in the slice
     bool ended = false;
     int b = b0;
-    int64_t bend = any ? s_off[b0 + 1] : 0;
-    int64_t nid[U];  // ids of the next iteration, fetched one iteration ahead
+    int bend = any ? st.off[b0 + 1] : 0;
+    int64_t nrow[U];  // rows of the next iteration
 #pragma unroll
-    for (int u = 0; u < U; ++u) nid[u] = s0 + u < s1 ? a.ids[s0 + u] : 0;
-    for (int64_t j = s0; j < s1; j += U) {
+    for (int u = 0; u < U; ++u) nrow[u] = s0 + u < s1 ? row_at(s0 + u) : -1;
+    for (int j = s0; j < s1; j += U) {
       float v[U][C], wt[U];
-      int64_t id[U];
+      int64_t row[U];
 #pragma unroll
-      for (int u = 0; u < U; ++u) id[u] = nid[u];
+      for (int u = 0; u < U; ++u) row[u] = nrow[u];
 #pragma unroll
       for (int u = 0; u < U; ++u) {
-        const int64_t e = j + u;
-        const int64_t row = by_pos ? e - f.ids_begin : id[u];
-        const bool in_range = (uint64_t)row < (uint64_t)f.num_rows;
-        float w = (exclude && id[u] == 0) ? 0.f : 1.f;
-        if (!in_range || e >= s1) w = 0.f;
-        wt[u] = w;
-        RowIO<TW, C>::load(w != 0.f && col_ok ? W + row * f.dim + col : zero_row<TW>(), v[u]);
+        const bool live = row[u] >= 0 && j + u < s1;
+        wt[u] = live ? 1.f : 0.f;
+        RowIO<TW, C>::load(live && col_ok ? W + row[u] * f.dim + col : zero_row<TW>(), v[u]);
       }
 #pragma unroll
-      for (int u = 0; u < U; ++u) nid[u] = j + U + u < s1 ? a.ids[j + U + u] : 0;
+      for (int u = 0; u < U; ++u) nrow[u] = j + U + u < s1 ? row_at(j + U + u) : -1;
 #pragma unroll
       for (int u = 0; u < U; ++u) {
-        const int64_t e = j + u;
+        const int e = j + u;
         if (e >= s1) continue;
 #pragma unroll
         for (int k = 0; k < C; ++k) acc[k] += v[u][k];
         wsum += wt[u];
         if (e + 1 == bend) {
-          if (s_off[b] >= s0) {
+          if (st.off[b] >= s0) {
             emit_row(b, acc, wsum, col, col_ok, emit);
           } else {
 #pragma unroll
@@ -340,8 +436,8 @@ __device__ __forceinline__ void pooled_chunk(const Feat& f, int64_t first_bag, i
           wsum = 0.f;
           // next non-empty bag
           ++b;
-          while (b < nb - 1 && s_off[b + 1] <= e + 1) ++b;
-          bend = s_off[b + 1 <= nb ? b + 1 : nb];
+          while (b < nb - 1 && st.off[b + 1] <= e + 1) ++b;
+          bend = st.off[b + 1 <= nb ? b + 1 : nb];
         }
       }
     }
@@ -384,24 +480,24 @@ __device__ __forceinline__ void pooled_chunk(const Feat& f, int64_t first_bag, i
     // Flush the staged rows (empty bags pool to zero) and the bag weights.
     wave_sync();
     for (int bb = slot; bb < nb; bb += G) {
-      const bool empty = s_off[bb] == s_off[bb + 1];
+      const bool empty = st.off[bb] == st.off[bb + 1];
       for (int cb = 0; cb < ncb; ++cb) {
         const int col = (cb * L + sub) * C;
         if (col >= f.dim) continue;
         float r[C];
         if (empty) zero_c(r);
-        else lds_get<C>(s_out + (int64_t)bb * f.dim + col, r);
+        else lds_get<C>(s_out + bb * f.dim + col, r);
         RowIO<TO, C>::store(out + (first_bag + bb) * f.out_stride + col, r);
       }
     }
     if (a.bag_count != nullptr)
       for (int i = lane; i < nb; i += kWave)
-        a.bag_count[f.payload_base + first_bag + i] = s_off[i] == s_off[i + 1] ? 0.f : s_cnt[i];
+        a.bag_count[f.payload_base + first_bag + i] = st.off[i] == st.off[i + 1] ? 0.f : st.cnt[i];
     return;
   }
   // Empty bags pool to zero.
   for (int bb = slot; bb < nb; bb += G) {
-    if (s_off[bb] == s_off[bb + 1]) {
+    if (st.off[bb] == st.off[bb + 1]) {
       float z[C];
       zero_c(z);
       for (int cb = 0; cb < ncb; ++cb) {
@@ -413,44 +509,55 @@ __device__ __forceinline__ void pooled_chunk(const Feat& f, int64_t first_bag, i
   }
 }
 
-// Sort keys and payloads of a pooled chunk (and its invalid-id count), one
-// id per lane so the stores coalesce; an id's bag comes from a binary search
-// of the staged bounds, resumed from the lane's previous id.
-__device__ __forceinline__ int pooled_keys(const Feat& f, int64_t first_bag, int nb, const int64_t* s_off,
-                                           const FwdArgs& a) {
+// Sort keys and payloads of a pooled chunk, one id per lane so the stores
+// coalesce; an id's bag comes from a binary search of the staged bounds,
+// resumed from the lane's previous id.  Returns the invalid ids among those
+// not staged (the staged ones were counted when staged).
+__device__ __forceinline__ int pooled_keys(const Feat& f, int64_t first_bag, int nb, const PoolStage& st,
+                                           const PoolChunk& pc, const FwdArgs& a) {
   constexpr int kBatch = 4;  // ids per lane whose loads are issued before any store
   const int lane = lane_id();
-  const int64_t e_begin = s_off[0], e_end = s_off[nb];
   const bool exclude = (f.flags & MDL_FLAG_EXCLUDE_NULL) != 0;
   const bool by_pos = (f.flags & MDL_FLAG_ROWS_BY_POSITION) != 0;
   int bad = 0;
   int b = 0;
-  for (int64_t base = e_begin + lane; base < e_end; base += kWave * kBatch) {
+  for (int base = lane; base < pc.len; base += kWave * kBatch) {
     int64_t id[kBatch];
 #pragma unroll
     for (int q = 0; q < kBatch; ++q) {
-      const int64_t e = base + q * kWave;
-      id[q] = e < e_end ? a.ids[e] : 0;
+      const int i = base + q * kWave;
+      id[q] = i < pc.len && i >= pc.lim ? a.ids[pc.e0 + i] : 0;
     }
 #pragma unroll
     for (int q = 0; q < kBatch; ++q) {
-      const int64_t e = base + q * kWave;
-      if (e >= e_end) break;
-      int hi = nb - 1;  // last bag with s_off[bag] <= e, searched in [b, nb)
+      const int i = base + q * kWave;
+      if (i >= pc.len) break;
+      int hi = nb - 1;  // last bag with off[bag] <= i, searched in [b, nb)
       while (b < hi) {
         const int mid = (b + hi + 1) >> 1;
-        if (s_off[mid] <= e) b = mid;
+        if (st.off[mid] <= i) b = mid;
         else hi = mid - 1;
       }
-      const int64_t row = by_pos ? e - f.ids_begin : id[q];
-      const bool in_range = (uint64_t)row < (uint64_t)f.num_rows;
-      bad += !in_range;
+      // Invalid ids and nulls under "exclude" pool with weight 0: their
+      // gradient is exactly zero, so they take no part in the backward.
+      // Rows by position belong to no table.
+      int64_t row;
+      bool live;
+      if (i < pc.lim) {
+        const uint32_t r = st.row[i];
+        row = (int64_t)r;
+        live = r != kNoRow;
+      } else {
+        const int64_t e = pc.e0 + i;
+        row = by_pos ? e - f.ids_begin : id[q];
+        const bool in_range = (uint64_t)row < (uint64_t)f.num_rows;
+        bad += !in_range;
+        live = in_range && !(exclude && id[q] == 0);
+      }
       if (a.keys != nullptr) {
-        // Invalid ids and nulls under "exclude" pool with weight 0: their
-        // gradient is exactly zero, so they take no part in the backward.
-        // Rows by position belong to no table.
-        const bool live = in_range && !(exclude && id[q] == 0) && !by_pos && id[q] != f.padding_idx;
-        a.keys[e] = live ? (uint32_t)(f.row_base + id[q]) : a.sentinel;
+        const int64_t e = pc.e0 + i;
+        live = live && !by_pos && row != (int64_t)f.padding_idx;
+        a.keys[e] = live ? (uint32_t)(f.row_base + row) : a.sentinel;
         a.payload[e] = (uint32_t)(f.payload_base + first_bag + b);
       }
     }
@@ -460,9 +567,8 @@ __device__ __forceinline__ int pooled_keys(const Feat& f, int64_t first_bag, int
 
 template <typename TW, typename TO, bool kVec>
 __global__ MDL_OCCUPANCY __launch_bounds__(kFwdWaves * kWave) void forward_kernel(FwdArgs a) {
-  __shared__ int64_t s_off[kFwdWaves][kMaxBagsPerChunk + 1];
+  __shared__ PoolStage s_st[kFwdWaves];
   __shared__ __align__(16) float s_out[kFwdWaves][kOutStage];
-  __shared__ float s_cnt[kFwdWaves][kMaxBagsPerChunk];
   const int w = threadIdx.x / kWave;
   const int64_t blk = xcd_block(blockIdx.x, gridDim.x);
   const int64_t c = uni64(blk * kFwdWaves + w);
@@ -482,12 +588,13 @@ __global__ MDL_OCCUPANCY __launch_bounds__(kFwdWaves * kWave) void forward_kerne
     if (lane_id() == 0 && a.error_count && ch.count != 0) atomicAdd(a.error_count, 1);
     return;
   }
-  int bad = stage_offsets(f, ch.first, ch.count, s_off[w], a);
+  int bad = 0;
+  const PoolChunk pc = stage_pooled(f, ch.first, ch.count, s_st[w], a, bad);
   with_width<TW, kVec>(v % kWidths, [&]<int C>() {
-    pooled_chunk<TW, TO, C>(f, ch.first, ch.count, s_off[w], s_out[w], s_cnt[w], a);
+    pooled_chunk<TW, TO, C>(f, ch.first, ch.count, s_st[w], pc, s_out[w], a);
   });
   // After the walk, so that its stores never hold up the walk's loads.
-  bad += pooled_keys(f, ch.first, ch.count, s_off[w], a);
+  bad += pooled_keys(f, ch.first, ch.count, s_st[w], pc, a);
   for (int m = 1; m < kWave; m <<= 1) bad += __shfl_xor(bad, m);
   if (lane_id() == 0 && bad && a.error_count) atomicAdd(a.error_count, bad);
 }
