@@ -125,15 +125,19 @@ __device__ __forceinline__ const T* zero_row() {
 }
 
 // Compile-time tuning knobs (defaults are the ones measured best on MI355X):
-// rows a lane group walks per chunk, and the row elements a lane keeps in
-// flight per iteration.
+// rows a lane group walks per backward chunk and per forward chunk, and the
+// row elements a lane keeps in flight per iteration.
 #ifndef MDL_PASSES
 #define MDL_PASSES 32
+#endif
+#ifndef MDL_FWD_PASSES
+#define MDL_FWD_PASSES 48
 #endif
 #ifndef MDL_ELEMS_IN_FLIGHT
 #define MDL_ELEMS_IN_FLIGHT 16
 #endif
 constexpr int kPassesPerChunk = MDL_PASSES;
+constexpr int kFwdPassesPerChunk = MDL_FWD_PASSES;
 
 // Waves per SIMD the gather/reduce kernels are compiled for: their per-wave
 // work is a chain of dependent memory round trips, so throughput follows the

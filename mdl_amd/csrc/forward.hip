@@ -839,13 +839,13 @@ int64_t mdl_plan_chunks(const mdl_feature* feats, int32_t num_features, int32_t 
   for (int32_t fi = 0; fi < num_features; ++fi) {
     const mdl_feature& f = feats[fi];
     // Rows a wave holds at once (same lane layout as the kernel): chunks hold
-    // about kPassesPerChunk of them per slot, so no slot walks a long serial
+    // about kFwdPassesPerChunk of them per slot, so no slot walks a long serial
     // chain of dependent loads, whatever the row width.
     const bool vec = feature_vec(f.weight, f.out, f.dim, f.out_stride, f.wdtype, f.odtype);
     const int c = variant_elems(variant_of(f.wdtype, f.odtype, vec, f.dim));
     const int lanes = lanes_for(f.dim > 0 ? f.dim : 1, c);
     const int64_t per_pass = kWave / lanes;
-    int64_t target = (int64_t)kPassesPerChunk * per_pass;
+    int64_t target = (int64_t)kFwdPassesPerChunk * per_pass;
     if (target > target_ids) target = target_ids;
     if (f.pooling == MDL_POOL_NONE) {
       for (int64_t s = 0; s < f.num_ids; s += target) {

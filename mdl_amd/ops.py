@@ -34,7 +34,10 @@ from ._lib import (
 
 POOLING_CODES = {"none": MDL_POOL_NONE, "sum": MDL_POOL_SUM, "mean": MDL_POOL_MEAN}
 NULL_POLICIES = ("exclude", "include_as_padding")
-FORWARD_TARGET_IDS = 512
+# Ids per forward chunk at most: the forward stages up to 480 rows of a
+# pooled chunk in LDS, and chunks of about that size balance each wave's
+# fixed cost against the length of its walk.
+FORWARD_TARGET_IDS = 480
 
 
 def _require_device(t: Tensor, what: str) -> None:
