@@ -128,7 +128,7 @@ __device__ __forceinline__ const T* zero_row() {
 // rows a lane group walks per backward chunk and per forward chunk, and the
 // row elements a lane keeps in flight per iteration.
 #ifndef MDL_PASSES
-#define MDL_PASSES 32
+#define MDL_PASSES 48
 #endif
 #ifndef MDL_FWD_PASSES
 #define MDL_FWD_PASSES 48
