@@ -726,95 +726,146 @@ __device__ __forceinline__ int64_t seq_len(const SeqArgs& a, int64_t b) {
   return n > a.in_len ? a.in_len : n;
 }
 
-// One slot per output row (b, p) of [batch, out_len].
+// One wave per chunk of kSeqRows output positions [p0, p0 + np) of one row
+// b of [batch, out_len]: the chunk's first nz positions are padding (zeros),
+// the rest hold the ids of one contiguous (oldest_to_newest) or reversed
+// (newest_to_oldest) run of input positions, so the row's length is one
+// scalar load and the ids load coalesced.  The gather keeps two pass groups
+// of rows in flight, as the unpooled lookup does; padding rows and the mask
+// are stored after it, so no row load waits behind those stores.
+// Positions per wave: short chunks (about one pass group pair) spread the
+// ragged rows evenly over the waves; measured best at 16..48.
+#ifndef MDL_SEQ_ROWS
+#define MDL_SEQ_ROWS 32
+#endif
+constexpr int kSeqRows = MDL_SEQ_ROWS;
+
 template <typename TW, typename TO, int C>
-__device__ __forceinline__ void seq_rows(const SeqArgs& a, int64_t row0, int64_t nrows) {
+__device__ __forceinline__ void seq_chunk(const SeqArgs& a, int64_t b, int64_t p0, int np) {
+  constexpr int kUnroll = unroll_for<C>();
   const Feat& f = a.f;
-  constexpr int kUnroll = C >= 8 ? 2 : 4;  // 16 columns of loads in flight per lane
   const int lane = lane_id();
   const int L = lanes_for(f.dim, C);
   const int G = kWave / L;
   const int slot = lane / L, sub = lane % L;
   const int ncb = (f.dim + L * C - 1) / (L * C);
   const TW* W = static_cast<const TW*>(f.weight);
-  TO* out = static_cast<TO*>(a.out);
+  TO* out = static_cast<TO*>(a.out) + (b * a.out_len + p0) * f.out_stride;
+  const int64_t len = uni64(seq_len(a, b));
+  const int64_t start = a.out_len - len;
+  const int nz = start <= p0 ? 0 : (start - p0 < np ? (int)(start - p0) : np);
+  const int count = np - nz;
+  const int64_t k0 = p0 + nz - start;  // run position of the chunk's first id
+  const bool forward = a.order == MDL_SEQ_OLDEST_TO_NEWEST;
+  const int64_t* ids = a.ids + b * a.in_len;
+  const int step = G * kUnroll;
   int bad = 0;
   for (int cb = 0; cb < ncb; ++cb) {
     const int col = (cb * L + sub) * C;
     const bool col_ok = col < f.dim;
-    for (int64_t base = 0; base < nrows; base += (int64_t)G * kUnroll) {
-      float v[kUnroll][C];
+    const bool first = cb == 0 && sub == 0;
+    int64_t nid[kUnroll];  // ids of the next group to load
+    auto fetch_ids = [&](int base) {
 #pragma unroll
       for (int u = 0; u < kUnroll; ++u) {
-        const int64_t r = row0 + base + u * G + slot;
-        const bool in_chunk = base + u * G + slot < nrows;
-        int64_t b = in_chunk ? r / a.out_len : 0;
-        int64_t p = in_chunk ? r - b * a.out_len : 0;
-        const int64_t len = in_chunk ? seq_len(a, b) : 0;
-        const int64_t start = a.out_len - len;
-        const bool valid = in_chunk && p >= start;
-        const int64_t k = a.order == MDL_SEQ_OLDEST_TO_NEWEST ? p - start : len - 1 - (p - start);
-        const int64_t id = valid ? a.ids[b * a.in_len + k] : 0;
-        const bool in_range = (uint64_t)id < (uint64_t)f.num_rows;
-#pragma unroll
-        for (int q = 0; q < C; ++q) v[u][q] = 0.f;
-        if (valid && in_range && col_ok) RowIO<TW, C>::load(W + id * f.dim + col, v[u]);
-        if (cb == 0 && sub == 0 && in_chunk) {
-          bad += valid && !in_range;
-          if (a.mask) a.mask[r] = valid ? 1 : 0;
-        }
+        const int i = base + u * G + slot;
+        nid[u] = i < count ? ids[forward ? k0 + i : len - 1 - (k0 + i)] : 0;
       }
+    };
+    auto load_rows = [&](int base, float (&v)[kUnroll][C]) {
 #pragma unroll
       for (int u = 0; u < kUnroll; ++u) {
-        const int64_t i = base + u * G + slot;
-        if (i < nrows && col_ok) RowIO<TO, C>::store(out + (row0 + i) * f.out_stride + col, v[u]);
+        const int i = base + u * G + slot;
+        const bool in_range = (uint64_t)nid[u] < (uint64_t)f.num_rows;
+        if (first && i < count) bad += !in_range;
+        RowIO<TW, C>::load(i < count && in_range && col_ok ? W + nid[u] * f.dim + col : zero_row<TW>(), v[u]);
       }
+    };
+    auto store_rows = [&](int base, const float (&v)[kUnroll][C]) {
+#pragma unroll
+      for (int u = 0; u < kUnroll; ++u) {
+        const int i = base + u * G + slot;
+        if (i < count && col_ok) RowIO<TO, C>::store(out + (int64_t)(nz + i) * f.out_stride + col, v[u]);
+      }
+    };
+    float va[kUnroll][C], vb[kUnroll][C];
+    fetch_ids(0);
+    load_rows(0, va);
+    fetch_ids(step);
+    for (int base = 0; base < count; base += 2 * step) {
+      const bool more = base + step < count;
+      if (more) {
+        load_rows(base + step, vb);
+        fetch_ids(base + 2 * step);
+      }
+      store_rows(base, va);
+      if (!more) break;
+      if (base + 2 * step < count) {
+        load_rows(base + 2 * step, va);
+        fetch_ids(base + 3 * step);
+      }
+      store_rows(base + step, vb);
     }
+    float z[C];
+#pragma unroll
+    for (int k = 0; k < C; ++k) z[k] = 0.f;
+    if (col_ok)
+      for (int i = slot; i < nz; i += G) RowIO<TO, C>::store(out + (int64_t)i * f.out_stride + col, z);
   }
-  if (bad && a.error_count) atomicAdd(a.error_count, bad);
+  if (a.mask)
+    for (int i = lane; i < np; i += kWave) a.mask[b * a.out_len + p0 + i] = i >= nz ? 1 : 0;
+  for (int m = 1; m < kWave; m <<= 1) bad += __shfl_xor(bad, m);
+  if (lane == 0 && bad && a.error_count) atomicAdd(a.error_count, bad);
 }
 
-constexpr int kSeqRowsPerWave = 256;
-
-__global__ __launch_bounds__(kFwdWaves * kWave) void sequence_kernel(SeqArgs a) {
+template <typename TW, typename TO, bool kVec>
+__global__ MDL_OCCUPANCY __launch_bounds__(kFwdWaves * kWave) void sequence_kernel(SeqArgs a, int width) {
   const int w = threadIdx.x / kWave;
   const int64_t blk = xcd_block(blockIdx.x, gridDim.x);
-  const int64_t total = a.batch * a.out_len;
-  const int64_t row0 = uni64((blk * kFwdWaves + w) * kSeqRowsPerWave);
-  if (row0 >= total) return;
-  const int64_t nrows = total - row0 < kSeqRowsPerWave ? total - row0 : kSeqRowsPerWave;
-  Feat f = a.f;
-  const bool v = ((uint64_t)f.weight % 16 == 0) && ((uint64_t)a.out % 16 == 0) &&
-                 ((int64_t)f.dim * (f.wdtype == MDL_BF16 ? 2 : 4)) % 16 == 0 &&
-                 (f.wdtype == MDL_F32 || f.odtype == MDL_BF16 || f.dim % 8 == 0);
-  if (f.wdtype == MDL_F32) {
-    if (v) seq_rows<float, float, 4>(a, row0, nrows);
-    else seq_rows<float, float, 1>(a, row0, nrows);
-  } else if (f.odtype == MDL_BF16) {
-    if (v) seq_rows<bf16_t, bf16_t, 8>(a, row0, nrows);
-    else seq_rows<bf16_t, bf16_t, 1>(a, row0, nrows);
-  } else {
-    if (v) seq_rows<bf16_t, float, 8>(a, row0, nrows);
-    else seq_rows<bf16_t, float, 1>(a, row0, nrows);
-  }
+  const int64_t wid = uni64(blk * kFwdWaves + w);
+  const int64_t per_row = (a.out_len + kSeqRows - 1) / kSeqRows;
+  if (wid >= a.batch * per_row) return;
+  const int64_t b = wid / per_row;
+  const int64_t p0 = (wid - b * per_row) * kSeqRows;
+  const int np = a.out_len - p0 < kSeqRows ? (int)(a.out_len - p0) : kSeqRows;
+  with_width<TW, kVec>(width, [&]<int C>() { seq_chunk<TW, TO, C>(a, b, p0, np); });
 }
 
-// Sort keys/payloads of the input positions (b, k) of a sequence feature.
-__global__ void sequence_keys_kernel(SeqArgs a) {
-  const int64_t n = a.batch * a.in_len;
-  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n;
-       i += (int64_t)gridDim.x * blockDim.x) {
-    const int64_t b = i / a.in_len;
-    const int64_t k = i - b * a.in_len;
-    const int64_t len = seq_len(a, b);
+// Sort keys/payloads of the input positions (b, k) of a sequence feature; one
+// block per kSeqKeys positions of one row, so the row's length is one load.
+constexpr int kSeqKeys = 1024;
+
+__global__ __launch_bounds__(256) void sequence_keys_kernel(SeqArgs a) {
+  const int64_t per_row = (a.in_len + kSeqKeys - 1) / kSeqKeys;
+  const int64_t b = (int64_t)blockIdx.x / per_row;
+  const int64_t kb = ((int64_t)blockIdx.x - b * per_row) * kSeqKeys;
+  const int64_t len = seq_len(a, b);
+  const int64_t start = a.out_len - len;
+  for (int j = threadIdx.x; j < kSeqKeys; j += 256) {
+    const int64_t k = kb + j;
+    if (k >= a.in_len) break;
+    const int64_t i = b * a.in_len + k;
     const int64_t id = a.ids[i];
     const bool valid = k < len && (uint64_t)id < (uint64_t)a.f.num_rows && id != a.f.padding_idx;
-    const int64_t start = a.out_len - len;
     const int64_t p = a.order == MDL_SEQ_OLDEST_TO_NEWEST ? start + k : start + (len - 1 - k);
     a.keys[i] = valid ? (uint32_t)(a.f.row_base + id) : a.sentinel;
     a.payload[i] = valid ? (uint32_t)(a.f.payload_base + b * a.out_len + p) : 0u;
   }
 }
+
+struct LaunchSequence {
+  const SeqArgs& a;
+  int64_t blocks;
+  int width;
+  hipStream_t s;
+  template <typename TW, typename TO, bool kVec>
+  int operator()() const {
+    hipLaunchKernelGGL((sequence_kernel<TW, TO, kVec>), dim3((unsigned)blocks), dim3(kFwdWaves * kWave), 0, s, a,
+                       width);
+    MDL_CHECK_LAUNCH("sequence_kernel");
+    return MDL_OK;
+  }
+};
 
 }  // namespace mdl
 
@@ -963,16 +1014,18 @@ int mdl_sequence_forward(const mdl_feature* feature, const int64_t* ids, const i
   a.sentinel = sentinel;
   a.error_count = error_count;
   hipStream_t s = as_stream(stream);
-  const int64_t total = batch * out_len;
-  if (total > 0) {
-    const int64_t waves = (total + kSeqRowsPerWave - 1) / kSeqRowsPerWave;
+  if (batch > 0 && out_len > 0) {
+    const int64_t waves = batch * ((out_len + kSeqRows - 1) / kSeqRows);
     const int64_t blocks = (waves + kFwdWaves - 1) / kFwdWaves;
-    hipLaunchKernelGGL(sequence_kernel, dim3((unsigned)blocks), dim3(kFwdWaves * kWave), 0, s, a);
-    MDL_CHECK_LAUNCH("sequence_kernel");
+    if (blocks > 0x7fffffff) return fail(MDL_ERR_UNSUPPORTED, "mdl_sequence_forward: too many rows");
+    const bool vec = feature_vec(d.weight, (uint64_t)out, d.dim, d.dim, d.wdtype, d.odtype);
+    const int v = variant_of(d.wdtype, d.odtype, vec, d.dim);
+    const int rc = for_each_class(1u << v, LaunchSequence{a, blocks, v % kWidths, s});
+    if (rc != MDL_OK) return rc;
   }
-  if (sort_keys != nullptr && batch * in_len > 0) {
-    int64_t blocks = (batch * in_len + 255) / 256;
-    if (blocks > 65536) blocks = 65536;
+  if (sort_keys != nullptr && batch > 0 && in_len > 0) {
+    const int64_t blocks = batch * ((in_len + kSeqKeys - 1) / kSeqKeys);
+    if (blocks > 0x7fffffff) return fail(MDL_ERR_UNSUPPORTED, "mdl_sequence_forward: too many positions");
     hipLaunchKernelGGL(sequence_keys_kernel, dim3((unsigned)blocks), dim3(256), 0, s, a);
     MDL_CHECK_LAUNCH("sequence_keys_kernel");
   }

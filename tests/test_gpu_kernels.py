@@ -229,6 +229,43 @@ def test_sequence_forward_matches_oracle(device, order, dtype):
         assert np.array_equal(to_np(out), ref.astype(np.float32))
 
 
+@pytest.mark.parametrize("dim,dtype,out_dtype", [
+    (3, torch.float32, torch.float32),      # scalar lanes (12-byte rows)
+    (24, torch.float32, torch.float32),     # 8 per lane, last lane of 4 outside the row
+    (128, torch.float32, torch.float32),
+    (12, torch.bfloat16, torch.bfloat16),   # 24-byte rows: scalar lanes
+    (40, torch.bfloat16, torch.float32),
+])
+@pytest.mark.parametrize("order", ["oldest_to_newest", "newest_to_oldest"])
+def test_sequence_forward_widths_and_invalid_ids(device, dim, dtype, out_dtype, order):
+    """Every lane-width variant of the window gather, windows shorter than
+    the input rows, empty rows, and ids outside the table: those read as
+    zero rows (still valid positions) and are counted once each."""
+    rng = np.random.default_rng(31)
+    announce("sequence_widths", dim, dtype, out_dtype, order)
+    rows = 500
+    w = _table(rng, rows, dim, dtype, device)
+    B, L, out_len = 7, 90, 64
+    lengths = rng.integers(0, L + 1, size=B)
+    lengths[0], lengths[1], lengths[2] = L, 0, 10
+    ids = np.zeros((B, L), dtype=np.int64)
+    for b in range(B):
+        ids[b, : lengths[b]] = rng.integers(1, rows, size=lengths[b])
+    ids[0, 5], ids[0, 6], ids[2, 0] = rows, -3, 10**9
+    ids[3, L - 1] = 10**9 if lengths[3] < L else ids[3, L - 1]  # past the row's length: not looked up
+    # a row longer than the window contributes its first out_len ids (either
+    # order), so all three planted ids are looked up
+    err = torch.zeros(1, dtype=torch.int32, device=device)
+    out, mask = ops.sequence_forward(w, torch.from_numpy(ids).to(device), torch.from_numpy(lengths).to(device),
+                                     out_len=out_len, order=order, out_dtype=out_dtype, error_count=err)
+    safe = np.where((ids >= 0) & (ids < rows), ids, 0)  # row 0 is zero
+    ref, rmask = O.sequence_gather(to_np(w), safe, lengths, out_len, order)
+    assert out.dtype == out_dtype
+    assert np.array_equal(mask.cpu().numpy(), rmask)
+    assert np.array_equal(to_np(out), ref.astype(np.float32))
+    assert int(err.item()) == 3
+
+
 def test_invalid_ids_are_counted_not_read(device):
     rng = np.random.default_rng(23)
     announce("invalid_ids")
