@@ -705,8 +705,10 @@ def main() -> int:
                                    + wl.batch * a["sum_dim"] * esz + 4 * nb for a in used]))
         apply_bytes = float(np.mean([8 * a["n_ids"] + wl.batch * a["sum_dim"] * esz
                                      + 2 * a["fwd_unique_row_bytes"] + 8 * a["unique_rows"] + 4 * nb for a in used]))
+    fwd_label = ("sequence_kernel + sequence_keys_kernel per feature (window gather, mask, sort keys)"
+                 if wl.kind == "sequence" else "forward_kernel (grouped lookup + pooling + sort-key emission)")
     for name, nbytes, label in (
-        ("forward", fwd_bytes, "forward_kernel (grouped lookup + pooling + sort-key emission)"),
+        ("forward", fwd_bytes, fwd_label),
         ("apply", apply_bytes, "bwd_reduce_kernel + fix-up (segment reduction + row-wise Adagrad)"),
     ):
         kms = timers[name].mean_ms()
