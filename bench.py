@@ -508,7 +508,7 @@ def cpu_baseline(wl: Workload, seconds: float = 12.0, row_cap: int = 1 << 16, ba
 # The bench line then reports that file's figure as roofline.traffic.
 
 KERNEL_GROUPS = {
-    "forward": ("forward_kernel",),
+    "forward": ("forward_kernel", "sequence_kernel", "sequence_keys_kernel"),
     "apply": ("bwd_reduce_kernel<false", "bwd_reduce_kernel<true"),
     "sort": ("radix_upsweep", "radix_scan", "radix_downsweep"),
 }
@@ -528,9 +528,10 @@ def _rocpd_rows(dirs, query):
                 con.close()
 
 
-def summarize_pmc(dirs, out_path, config):
-    """Per-dispatch FETCH_SIZE / WRITE_SIZE of the kernel groups and the copy
-    calibration, from rocprofv3 --pmc databases; writes a JSON summary."""
+def summarize_pmc(dirs, out_path, config, steps_run):
+    """FETCH_SIZE / WRITE_SIZE per step of the kernel groups and the copy
+    calibration, from rocprofv3 --pmc databases of a bench run that made
+    ``steps_run`` step() calls; writes a JSON summary."""
 
     per = {}
     for name, ctr, val in _rocpd_rows(dirs, "select kernel_name, counter_name, value from counters_collection"):
@@ -552,24 +553,24 @@ def summarize_pmc(dirs, out_path, config):
         for ctr in tot:
             for n, vals in per[ctr].items():
                 if any(p in n for p in pats):
-                    # dispatches per step: the group's kernels repeat the same
-                    # number of times, so the mean per dispatch x (launches per
-                    # step) is the traffic of one step's launch of the group
                     k = kernels.setdefault(n.split("(")[0].replace("void ", ""), {})
                     k[ctr + "_KiB"] = float(np.mean(vals))
                     k["dispatches"] = len(vals)
-        steps = max((k["dispatches"] for k in kernels.values()), default=0)
         for k in kernels.values():
+            k["dispatches_per_step"] = k["dispatches"] / steps_run
             for ctr in tot:
-                tot[ctr] += k.get(ctr + "_KiB", 0.0) * k["dispatches"] / max(steps, 1)
+                tot[ctr] += k.get(ctr + "_KiB", 0.0) * k["dispatches_per_step"]
+        # one step's launches of the group: the unit bench.py times per kernel
+        # group (all features' forward launches, all sort passes)
         groups[g] = {
             "kernels": kernels,
-            "fetch_KiB_per_launch": tot["FETCH_SIZE"],
-            "write_KiB_per_launch": tot["WRITE_SIZE"],
-            "hbm_bytes_per_launch": tot["FETCH_SIZE"] * 1024 * scale["FETCH_SIZE"]
+            "fetch_KiB_per_step": tot["FETCH_SIZE"],
+            "write_KiB_per_step": tot["WRITE_SIZE"],
+            "hbm_bytes_per_step": tot["FETCH_SIZE"] * 1024 * scale["FETCH_SIZE"]
             + tot["WRITE_SIZE"] * 1024 * scale["WRITE_SIZE"],
         }
-    res = {"config": config, "copy_kernel": cname, "copy_bytes": COPY_BYTES, "copy_FETCH_KiB": f_kib,
+    res = {"config": config, "steps_run": steps_run, "copy_kernel": cname, "copy_bytes": COPY_BYTES,
+           "copy_FETCH_KiB": f_kib,
            "copy_WRITE_KiB": w_kib, "scale": scale, "groups": groups}
     Path(out_path).write_text(json.dumps(res, indent=1) + "\n")
     print(json.dumps(res, indent=1))
@@ -581,11 +582,20 @@ def summarize_trace(dirs, out_path, title, command):
     agg = {}
     for name, dur in _rocpd_rows(dirs, "select name, duration from kernels"):
         agg.setdefault(name.replace("void ", "").split("(")[0], []).append(float(dur))
-    total = sum(sum(v) for v in agg.values())
-    lines = [f"# {title}", "", "```", command, "```", "", "| kernel | calls | avg us | total ms | share |",
-             "|---|---:|---:|---:|---:|"]
-    for k, v in sorted(agg.items(), key=lambda kv: -sum(kv[1])):
+    # The library's kernels are the steps; torch's (random table init, fills)
+    # run while the bench sets up, outside the timed steps.
+    ours = {k: v for k, v in agg.items() if k.startswith("mdl::")}
+    setup = {k: v for k, v in agg.items() if not k.startswith("mdl::")}
+    total = sum(sum(v) for v in ours.values())
+    lines = [f"# {title}", "", "```", command, "```", "",
+             "Library kernels (share of their summed time):", "",
+             "| kernel | calls | avg us | total ms | share |", "|---|---:|---:|---:|---:|"]
+    for k, v in sorted(ours.items(), key=lambda kv: -sum(kv[1])):
         lines.append(f"| `{k}` | {len(v)} | {np.mean(v) / 1e3:.1f} | {sum(v) / 1e6:.2f} | {100 * sum(v) / total:.1f}% |")
+    lines += ["", "Set-up kernels (torch: table init, fills; not in the timed steps):", "",
+              "| kernel | calls | avg us | total ms |", "|---|---:|---:|---:|"]
+    for k, v in sorted(setup.items(), key=lambda kv: -sum(kv[1])):
+        lines.append(f"| `{k[:80]}` | {len(v)} | {np.mean(v) / 1e3:.1f} | {sum(v) / 1e6:.2f} |")
     Path(out_path).write_text("\n".join(lines) + "\n")
     print("\n".join(lines))
 
@@ -615,7 +625,8 @@ def main() -> int:
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="also run three plain 1 GiB device copies (counter calibration for rocprofv3 --pmc runs)")
     ap.add_argument("--summarize-pmc", nargs="+", metavar="DIR",
-                    help="summarise rocprofv3 --pmc databases into --pmc-out and exit (no GPU)")
+                    help="summarise rocprofv3 --pmc databases into --pmc-out and exit (no GPU); give the "
+                         "--steps/--warmup of the profiled run")
     ap.add_argument("--pmc-out", default=None)
     ap.add_argument("--summarize-trace", nargs="+", metavar="DIR",
                     help="summarise rocprofv3 --kernel-trace databases into --trace-out and exit (no GPU)")
@@ -626,8 +637,10 @@ def main() -> int:
                          "tensor per feature")
     args = ap.parse_args()
     if args.summarize_pmc:
+        # the profiled run made warmup + steps timed + steps per-kernel-timed step() calls;
+        # pass the same --steps/--warmup here
         summarize_pmc(args.summarize_pmc, args.pmc_out or str(ROOT / "profiles" / f"{args.config}_traffic.json"),
-                      args.config)
+                      args.config, args.warmup + 2 * args.steps)
         return 0
     if args.summarize_trace:
         summarize_trace(args.summarize_trace, args.trace_out or "/dev/stdout",
@@ -718,8 +731,8 @@ def main() -> int:
     dom = kernels[dom_name]
     traffic = None
     tr = load_traffic(wl.name)
-    if tr is not None and dom_name in tr.get("groups", {}):
-        traffic = tr["groups"][dom_name]["hbm_bytes_per_launch"]
+    if tr is not None and "hbm_bytes_per_step" in tr.get("groups", {}).get(dom_name, {}):
+        traffic = tr["groups"][dom_name]["hbm_bytes_per_step"]
         dom["traffic_source"] = f"profiles/{wl.name}_traffic.json (rocprofv3 FETCH_SIZE/WRITE_SIZE, copy-calibrated)"
     result = {
         "metric": METRIC,
