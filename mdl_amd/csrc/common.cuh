@@ -150,7 +150,7 @@ constexpr int kFwdPassesPerChunk = MDL_FWD_PASSES;
 // Rows per lane group per iteration for lanes of C elements.
 template <int C>
 __host__ __device__ constexpr int unroll_for() {
-  return C == 1 ? 8 : (MDL_ELEMS_IN_FLIGHT / C > 1 ? MDL_ELEMS_IN_FLIGHT / C : 1);
+  return C == 1 ? 4 : (MDL_ELEMS_IN_FLIGHT / C > 1 ? MDL_ELEMS_IN_FLIGHT / C : 1);
 }
 
 // ------------------------------------------------------- kernel variants --

@@ -339,7 +339,9 @@ __device__ __forceinline__ void lds_get(const float* p, float (&v)[C]) {
 template <typename TW, typename TO, int C>
 __device__ __forceinline__ void pooled_chunk(const Feat& f, int64_t first_bag, int nb, const PoolStage& st,
                                              const PoolChunk& pc, float* s_out, const FwdArgs& a) {
-  constexpr int U = unroll_for<C>();  // ids per slot per iteration
+  // Ids per slot per iteration: 24 row elements per lane in flight (the
+  // walk's registers allow it at five waves per SIMD; 16 measured 3% slower).
+  constexpr int U = C == 1 ? 4 : (24 / C > 1 ? 24 / C : 1);
   const int lane = lane_id();
   const int len = pc.len;
   const int L = lanes_for(f.dim, C);
