@@ -287,6 +287,34 @@ def test_invalid_ids_are_counted_not_read(device):
     assert_close(to_np(res.outputs[0][0]), to_np(w[1] + w[2]), 1e-6, 1e-6)
 
 
+def test_pooled_bad_lengths_and_ids_stay_in_bounds(device):
+    """A negative length (decreasing offsets) and an id outside the table in
+    a bag: both are counted, nothing is read out of bounds, the other bags
+    pool as usual, and a bad id weighs 0 in a mean."""
+    rng = np.random.default_rng(24)
+    announce("pooled_bad_lengths")
+    w = _table(rng, 100, 16, torch.float32, device)
+    plan = ops.GroupPlan()
+    plan.add_feature(w, pooling="sum")
+    ids = torch.tensor([1, 2, 3, 4, 5, 6], device=device)
+    res = ops.grouped_forward(plan, [ids], [torch.tensor([2, -1, 3, 2], device=device)], with_backward=False)
+    assert int(res.error_count.item()) >= 1
+    out = to_np(res.outputs[0])
+    assert np.isfinite(out).all()
+    assert_close(out[0], to_np(w[1] + w[2]), 1e-6, 1e-6)
+    # offsets 0, 2, 1, 4, 6 are made non-decreasing (0, 2, 2, 4, 6): bag 1 is empty
+    assert np.abs(out[1]).sum() == 0
+    assert_close(out[3], to_np(w[5] + w[6]), 1e-6, 1e-6)
+    plan = ops.GroupPlan()
+    plan.add_feature(w, pooling="mean", null_policy="exclude")
+    res = ops.grouped_forward(plan, [torch.tensor([1, 200, 3, 0, 7], device=device)],
+                              [torch.tensor([3, 2], device=device)], with_backward=False)
+    assert int(res.error_count.item()) == 1
+    out = to_np(res.outputs[0])
+    assert_close(out[0], to_np((w[1] + w[3]) / 2), 1e-6, 1e-6)  # the bad id weighs 0
+    assert_close(out[1], to_np(w[7]), 1e-6, 1e-6)  # the null (0) is excluded from the mean
+
+
 # -------------------------------------------------------------- backward --
 
 
