@@ -389,19 +389,19 @@ struct Reducer {
       const float ss = row_sumsq(v);
       // scale == 1 leaves every product exact, so unclipped steps are unchanged
       const float acc = acc0 + (ss * (scale * scale)) * inv_dim;
-      if (sub == 0) state[row] = acc;
+      if (sub == 0) st_policy<kUpdatePolicy>(state + row, acc);
       const float step = a.lr * __builtin_amdgcn_rcpf(sqrtf(acc) + a.eps);
       if (col_ok) {
 #pragma unroll
         for (int k = 0; k < C; ++k) w[k] = w[k] - step * (v[k] * scale);
-        RowIO<TW, C>::store(W + row * dim + col, w);
+        RowIO<TW, C>::template store<kUpdatePolicy>(W + row * dim + col, w);
       }
     } else if (kMode == kModeCoalesce) {
       const int64_t local = uidx - a.unique_range[2 * t];
       int64_t* rows = (int64_t*)a.rows_addr[t];
       TW* vals = (TW*)a.values_addr[t];
-      if (sub == 0) rows[local] = row;
-      if (col_ok) RowIO<TW, C>::store(vals + local * dim + col, v);
+      if (sub == 0) st_policy(rows + local, row);
+      if (col_ok) RowIO<TW, C>::template store<kUpdatePolicy>(vals + local * dim + col, v);
     } else {
       const float ss = row_sumsq(v);
       if (sub == 0) ss_acc += ss;
@@ -482,8 +482,9 @@ __device__ __forceinline__ void reduce_chunk_body(const BwdArgs& a, int64_t c, c
       RowIO<TG, C>::load(gp[u], v[u]);
       if (adagrad) {
         const int64_t row = (int64_t)key[u] - R.row_base;
-        RowIO<TW, C>::load(own[u] && R.col_ok ? R.W + row * R.dim + R.col : zero_row<TW>(), w[u]);
-        acc0[u] = *(own[u] ? R.state + row : zero_row<float>());
+        RowIO<TW, C>::template load<kUpdatePolicy>(own[u] && R.col_ok ? R.W + row * R.dim + R.col : zero_row<TW>(),
+                                                   w[u]);
+        acc0[u] = ld_policy<kUpdatePolicy>(own[u] ? R.state + row : zero_row<float>());
       } else {
         zero(w[u]);
         acc0[u] = 0.f;
@@ -560,8 +561,8 @@ __device__ __forceinline__ void reduce_chunk_body(const BwdArgs& a, int64_t c, c
       float acc0 = 0.f;
       zero(w);
       if (adagrad) {
-        if (R.col_ok) RowIO<TW, C>::load(R.W + row * R.dim + R.col, w);
-        acc0 = R.state[row];
+        if (R.col_ok) RowIO<TW, C>::template load<kUpdatePolicy>(R.W + row * R.dim + R.col, w);
+        acc0 = ld_policy<kUpdatePolicy>(R.state + row);
       }
       R.finish(key, tot, acc0, w, coalesce ? hb + (int64_t)st.hc[hend + 1] - 1 : 0, ss_acc);
     }
@@ -664,8 +665,8 @@ __device__ __forceinline__ void fixup_chunk(const BwdArgs& a, int64_t c, const C
   zero(w);
   if (kMode == kModeAdagrad && R.slot == 0) {
     const int64_t row = (int64_t)key - R.row_base;
-    if (R.col_ok) RowIO<TW, C>::load(R.W + row * R.dim + R.col, w);
-    acc0 = R.state[row];
+    if (R.col_ok) RowIO<TW, C>::template load<kUpdatePolicy>(R.W + row * R.dim + R.col, w);
+    acc0 = ld_policy<kUpdatePolicy>(R.state + row);
   }
   float ss = 0.f;
   if (R.slot == 0) R.finish(key, v, acc0, w, uidx, ss);

@@ -122,7 +122,7 @@ __device__ __forceinline__ void gather_chunk(const Feat& f, int64_t first, int c
 #pragma unroll
       for (int u = 0; u < kUnroll; ++u) {
         const int i = base + u * G + slot;
-        if (i < count && col_ok) RowIO<TO, C>::store(out + (first + i) * f.out_stride + col, v[u]);
+        if (i < count && col_ok) RowIO<TO, C>::template store<kOutPolicy>(out + (first + i) * f.out_stride + col, v[u]);
       }
     };
     float va[kUnroll][C], vb[kUnroll][C];
@@ -160,8 +160,9 @@ __device__ __forceinline__ void gather_chunk(const Feat& f, int64_t first, int c
       bad += !in_range;
       if (a.keys != nullptr) {
         const int64_t e = f.ids_begin + first + i;
-        a.keys[e] = (in_range && id[q] != f.padding_idx) ? (uint32_t)(f.row_base + id[q]) : a.sentinel;
-        a.payload[e] = (uint32_t)(f.payload_base + first + i);
+        st_policy<kOutPolicy>(a.keys + e,
+                              (in_range && id[q] != f.padding_idx) ? (uint32_t)(f.row_base + id[q]) : a.sentinel);
+        st_policy<kOutPolicy>(a.payload + e, (uint32_t)(f.payload_base + first + i));
       }
     }
   }
@@ -384,8 +385,8 @@ __device__ __forceinline__ void pooled_chunk(const Feat& f, int64_t first_bag, i
       if (col_ok) lds_put<C>(s_out + bag * f.dim + col, r);
       if (emit_cnt) const_cast<PoolStage&>(st).cnt[bag] = wsum;
     } else {
-      if (col_ok) RowIO<TO, C>::store(out + (first_bag + bag) * f.out_stride + col, r);
-      if (emit_cnt && a.bag_count != nullptr) a.bag_count[f.payload_base + first_bag + bag] = wsum;
+      if (col_ok) RowIO<TO, C>::template store<kOutPolicy>(out + (first_bag + bag) * f.out_stride + col, r);
+      if (emit_cnt && a.bag_count != nullptr) st_policy(a.bag_count + f.payload_base + first_bag + bag, wsum);
     }
   };
 
@@ -489,12 +490,12 @@ __device__ __forceinline__ void pooled_chunk(const Feat& f, int64_t first_bag, i
         float r[C];
         if (empty) zero_c(r);
         else lds_get<C>(s_out + bb * f.dim + col, r);
-        RowIO<TO, C>::store(out + (first_bag + bb) * f.out_stride + col, r);
+        RowIO<TO, C>::template store<kOutPolicy>(out + (first_bag + bb) * f.out_stride + col, r);
       }
     }
     if (a.bag_count != nullptr)
       for (int i = lane; i < nb; i += kWave)
-        a.bag_count[f.payload_base + first_bag + i] = st.off[i] == st.off[i + 1] ? 0.f : st.cnt[i];
+        st_policy(a.bag_count + f.payload_base + first_bag + i, st.off[i] == st.off[i + 1] ? 0.f : st.cnt[i]);
     return;
   }
   // Empty bags pool to zero.
@@ -504,9 +505,9 @@ __device__ __forceinline__ void pooled_chunk(const Feat& f, int64_t first_bag, i
       zero_c(z);
       for (int cb = 0; cb < ncb; ++cb) {
         const int col = (cb * L + sub) * C;
-        if (col < f.dim) RowIO<TO, C>::store(out + (first_bag + bb) * f.out_stride + col, z);
+        if (col < f.dim) RowIO<TO, C>::template store<kOutPolicy>(out + (first_bag + bb) * f.out_stride + col, z);
       }
-      if (sub == 0 && a.bag_count != nullptr) a.bag_count[f.payload_base + first_bag + bb] = 0.f;
+      if (sub == 0 && a.bag_count != nullptr) st_policy(a.bag_count + f.payload_base + first_bag + bb, 0.f);
     }
   }
 }
@@ -559,8 +560,8 @@ __device__ __forceinline__ int pooled_keys(const Feat& f, int64_t first_bag, int
       if (a.keys != nullptr) {
         const int64_t e = pc.e0 + i;
         live = live && !by_pos && row != (int64_t)f.padding_idx;
-        a.keys[e] = live ? (uint32_t)(f.row_base + row) : a.sentinel;
-        a.payload[e] = (uint32_t)(f.payload_base + first_bag + b);
+        st_policy<kOutPolicy>(a.keys + e, live ? (uint32_t)(f.row_base + row) : a.sentinel);
+        st_policy<kOutPolicy>(a.payload + e, (uint32_t)(f.payload_base + first_bag + b));
       }
     }
   }
@@ -787,7 +788,7 @@ __device__ __forceinline__ void seq_chunk(const SeqArgs& a, int64_t b, int64_t p
 #pragma unroll
       for (int u = 0; u < kUnroll; ++u) {
         const int i = base + u * G + slot;
-        if (i < count && col_ok) RowIO<TO, C>::store(out + (int64_t)(nz + i) * f.out_stride + col, v[u]);
+        if (i < count && col_ok) RowIO<TO, C>::template store<kOutPolicy>(out + (int64_t)(nz + i) * f.out_stride + col, v[u]);
       }
     };
     float va[kUnroll][C], vb[kUnroll][C];
@@ -812,7 +813,7 @@ __device__ __forceinline__ void seq_chunk(const SeqArgs& a, int64_t b, int64_t p
 #pragma unroll
     for (int k = 0; k < C; ++k) z[k] = 0.f;
     if (col_ok)
-      for (int i = slot; i < nz; i += G) RowIO<TO, C>::store(out + (int64_t)i * f.out_stride + col, z);
+      for (int i = slot; i < nz; i += G) RowIO<TO, C>::template store<kOutPolicy>(out + (int64_t)i * f.out_stride + col, z);
   }
   if (a.mask)
     for (int i = lane; i < np; i += kWave) a.mask[b * a.out_len + p0 + i] = i >= nz ? 1 : 0;
