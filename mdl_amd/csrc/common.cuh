@@ -234,9 +234,9 @@ __host__ __device__ __forceinline__ int row_class(int wdtype, int odtype, bool v
 }
 
 // Width index of a row of `dim` elements: C = 4 << w starts at one 16-byte
-// vector of the weight type and doubles, up to 16 elements, while four lanes
-// do not cover the row and the doubled C still divides dim (a lane's C
-// elements are always wholly inside the row).
+// vector of the weight type and doubles, up to MDL_MAX_WIDTH (8) elements,
+// while four lanes do not cover the row and the doubled C still divides dim
+// (a lane's C elements are always wholly inside the row).
 __host__ __device__ __forceinline__ int width_index(int64_t dim, int wdtype, bool vec) {
   if (!vec) return 0;
   int w = wdtype == MDL_BF16 ? 1 : 0;

@@ -2,8 +2,9 @@
 //
 // One wavefront owns one chunk (a run of whole bags of one feature, or a run
 // of ids of an unpooled feature).  A row of `dim` elements is spread over L
-// lanes of C elements each (C = 4..16 fp32 or 8..16 bf16, 16-byte accesses;
-// the kernel variant), so a wave holds G = 64 / L rows at a time.
+// lanes of C elements each (C = 4 or 8 fp32, 8 bf16, in 16-byte accesses;
+// 1 for rows that are not 16-byte aligned), so a wave holds G = 64 / L rows
+// at a time.
 //
 // Pooling: the chunk's ids form one flat stream in which bags are consecutive
 // segments.  The G lane groups ("slots") each walk a contiguous slice of that
@@ -12,8 +13,8 @@
 // row load and C adds whatever the bag lengths (ragged bags of 1..32 ids keep
 // all lanes busy).  Bags that cross slot bounds are joined once per chunk by
 // a segmented scan over the slots' open partial sums.  The summation order is
-// fixed by the chunk layout alone (deterministic).  Bag bounds are staged in
-// LDS once per chunk.
+// fixed by the chunk layout alone (deterministic).  Bag bounds and the
+// table row of every id are staged in LDS once per chunk.
 #include "common.cuh"
 
 namespace mdl {
