@@ -224,6 +224,7 @@ __device__ __forceinline__ int bag_of(const T* off, int nb, T e) {
 // table rows; ids past the stage (a chunk of very long bags) are read where
 // they are used.
 constexpr int kIdStage = 480;
+constexpr int64_t kMaxChunkIds = 1ll << 30;
 constexpr uint32_t kNoRow = 0xffffffffu;
 struct PoolStage {
   int32_t off[kMaxBagsPerChunk + 1];
@@ -257,11 +258,13 @@ __device__ __forceinline__ PoolChunk stage_pooled(const Feat& f, int64_t first_b
     const int64_t oc = o < lo ? lo : (o > hi ? hi : o);
     err += oc != o;
     int64_t r = oc - pc.e0;
-    if (r > 0x7fffffffll) {  // 2^31 ids in one chunk: cut short, counted
-      r = 0x7fffffffll;
+    // 2^30 ids in one chunk: cut short and counted (keeps the walk's int
+    // arithmetic on positions far from overflow)
+    if (r > kMaxChunkIds) {
+      r = kMaxChunkIds;
       ++err;
     }
-    st.off[i] = (int32_t)(r < -0x7fffffffll ? -0x7fffffffll : r);
+    st.off[i] = (int32_t)(r < -kMaxChunkIds ? -kMaxChunkIds : r);
   }
   wave_sync();
   int dec = 0;
