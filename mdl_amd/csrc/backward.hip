@@ -155,55 +155,40 @@ __global__ __launch_bounds__(kBoundThreads) void bwd_bounds_kernel(const mdl_tab
   if (tid == 0) (upper ? table_end : table_start)[t] = lo;
 }
 
-__device__ __forceinline__ int64_t wave_incl_scan(int64_t x) {
-  const int lane = lane_id();
-#pragma unroll
-  for (int d = 1; d < kWave; d <<= 1) {
-    const int lo = shfl_i((int)(x & 0xffffffff), lane >= d ? lane - d : lane);
-    const int hi = shfl_i((int)(x >> 32), lane >= d ? lane - d : lane);
-    const int64_t o = (int64_t)(((uint64_t)(uint32_t)hi << 32) | (uint32_t)lo);
-    if (lane >= d) x += o;
-  }
-  return x;
-}
-
-// Chunk numbering (one wavefront): table t's chunks are [chunk_base[t],
-// chunk_base[t] + n_t) in table order, so neighbouring chunks (one XCD's
-// range) share a table; *total = the number of chunks.
-__global__ __launch_bounds__(kWave) void bwd_number_kernel(const mdl_table* __restrict__ tables, int32_t T,
-                                                           const int64_t* __restrict__ table_start,
-                                                           const int64_t* __restrict__ table_end,
-                                                           int64_t* __restrict__ chunk_base,
-                                                           int64_t* __restrict__ total) {
-  const int lane = lane_id();
-  int64_t run = 0;
-  for (int32_t g = 0; g < T; g += kWave) {
-    const int32_t t = g + lane;
-    int64_t nch = 0;
-    if (t < T) {
-      const int64_t cb = table_chunk_len(tables[t]);
-      nch = (table_end[t] - table_start[t] + cb - 1) / cb;
-    }
-    const int64_t incl = wave_incl_scan(nch);
-    if (t < T) chunk_base[t] = run + incl - nch;
-    const int tlo = shfl_i((int)(incl & 0xffffffff), kWave - 1);
-    const int thi = shfl_i((int)(incl >> 32), kWave - 1);
-    run += (int64_t)(((uint64_t)(uint32_t)thi << 32) | (uint32_t)tlo);
-  }
-  if (lane == 0) *total = run;
-}
-
-// Descriptors of table t's chunks (block t).
-__global__ __launch_bounds__(256) void bwd_desc_kernel(const mdl_table* __restrict__ tables,
+// Chunk numbering and descriptors, block t for table t: table t's chunks are
+// [chunk_base[t], chunk_base[t] + n_t) in table order -- the block adds up
+// the chunk counts of the tables before it -- so neighbouring chunks (one
+// XCD's range) share a table; the last block writes the total.
+__global__ __launch_bounds__(256) void bwd_desc_kernel(const mdl_table* __restrict__ tables, int32_t T,
                                                        const int64_t* __restrict__ table_start,
                                                        const int64_t* __restrict__ table_end,
-                                                       const int64_t* __restrict__ chunk_base,
+                                                       int64_t* __restrict__ chunk_base,
+                                                       int64_t* __restrict__ total,
                                                        ChunkDesc* __restrict__ desc) {
+  __shared__ int64_t s_part[256 / kWave];
   const int32_t t = blockIdx.x;
+  const int lane = lane_id(), w = threadIdx.x / kWave;
+  int64_t before = 0;
+  for (int32_t q = threadIdx.x; q < t; q += blockDim.x) {
+    const int64_t cq = table_chunk_len(tables[q]);
+    before += (table_end[q] - table_start[q] + cq - 1) / cq;
+  }
+  for (int m = 1; m < kWave; m <<= 1) {
+    const int lo = shfl_i((int)(before & 0xffffffff), lane ^ m);
+    const int hi = shfl_i((int)(before >> 32), lane ^ m);
+    before += (int64_t)(((uint64_t)(uint32_t)hi << 32) | (uint32_t)lo);
+  }
+  if (lane == 0) s_part[w] = before;
+  __syncthreads();
+  int64_t base = 0;
+  for (int q = 0; q < 256 / kWave; ++q) base += s_part[q];
   const int64_t lo = table_start[t], hi = table_end[t];
   const int64_t cb = table_chunk_len(tables[t]);
   const int64_t nch = (hi - lo + cb - 1) / cb;
-  const int64_t base = chunk_base[t];
+  if (threadIdx.x == 0) {
+    chunk_base[t] = base;
+    if (t == T - 1) *total = base + nch;
+  }
   for (int64_t j = threadIdx.x; j < nch; j += blockDim.x) {
     const int64_t b = lo + j * cb;
     ChunkDesc d;
@@ -723,11 +708,8 @@ static int plan(const mdl_table* tables, int32_t T, const uint32_t* sk, int64_t 
   hipLaunchKernelGGL(bwd_bounds_kernel, dim3((unsigned)(2 * T)), dim3(kBoundThreads), 0, s, tables, sk, n,
                      w.table_start, w.table_end);
   MDL_CHECK_LAUNCH("bwd_bounds_kernel");
-  hipLaunchKernelGGL(bwd_number_kernel, dim3(1), dim3(kWave), 0, s, tables, T, w.table_start, w.table_end,
-                     w.chunk_base, w.num_chunks);
-  MDL_CHECK_LAUNCH("bwd_number_kernel");
-  hipLaunchKernelGGL(bwd_desc_kernel, dim3((unsigned)T), dim3(256), 0, s, tables, w.table_start, w.table_end,
-                     w.chunk_base, w.desc);
+  hipLaunchKernelGGL(bwd_desc_kernel, dim3((unsigned)T), dim3(256), 0, s, tables, T, w.table_start, w.table_end,
+                     w.chunk_base, w.num_chunks, w.desc);
   MDL_CHECK_LAUNCH("bwd_desc_kernel");
   return MDL_OK;
 }
