@@ -105,10 +105,21 @@ __global__ void scan_sums_single(int64_t* __restrict__ sums, int64_t m) {
   }
 }
 
-// offsets[i+1] = sum(in[0..i]); offsets[0] = 0.
+// offsets[i+1] = sum(in[0..i]); offsets[0] = 0.  The tile's prefix is
+// sums[b] after scan_sums_single, or, with prefix_self (few tiles), the sum
+// of the raw tile sums before it, added up here: one launch fewer.
 __global__ void scan_tiles_final(const int64_t* __restrict__ in, int64_t n,
-                                 const int64_t* __restrict__ sums, int64_t* __restrict__ offsets) {
+                                 const int64_t* __restrict__ sums, int64_t* __restrict__ offsets,
+                                 int prefix_self) {
   __shared__ int64_t smem[kScanThreads];
+  int64_t tile_prefix;
+  if (prefix_self) {
+    int64_t p = 0;
+    for (int64_t j = threadIdx.x; j < (int64_t)blockIdx.x; j += kScanThreads) p += sums[j];
+    block_exclusive_scan<int64_t>(p, smem, &tile_prefix);
+  } else {
+    tile_prefix = sums[blockIdx.x];
+  }
   const int64_t base = (int64_t)blockIdx.x * kScanTile + (int64_t)threadIdx.x * kScanItems;
   int64_t v[kScanItems];
   int64_t s = 0;
@@ -118,7 +129,7 @@ __global__ void scan_tiles_final(const int64_t* __restrict__ in, int64_t n,
     v[k] = i < n ? in[i] : 0;
     s += v[k];
   }
-  int64_t ex = block_exclusive_scan<int64_t>(s, smem, nullptr) + sums[blockIdx.x];
+  int64_t ex = block_exclusive_scan<int64_t>(s, smem, nullptr) + tile_prefix;
   if (blockIdx.x == 0 && threadIdx.x == 0) offsets[0] = 0;
 #pragma unroll
   for (int k = 0; k < kScanItems; ++k) {
@@ -127,6 +138,11 @@ __global__ void scan_tiles_final(const int64_t* __restrict__ in, int64_t n,
     if (i < n) offsets[i + 1] = ex;
   }
 }
+
+static __global__ void zero_offset_kernel(int64_t* p) { *p = 0; }
+
+// Tiles whose prefix the final kernel adds up itself.
+constexpr int64_t kScanSelfPrefixTiles = 1024;
 
 }  // namespace mdl
 
@@ -170,7 +186,10 @@ int mdl_lengths_to_offsets(const int64_t* lengths, int64_t n, int64_t* offsets, 
   if (n < 0) return fail(MDL_ERR_INVALID, "mdl_lengths_to_offsets: negative n");
   hipStream_t s = as_stream(stream);
   if (n == 0) {
-    return check_hip(hipMemsetAsync(offsets, 0, sizeof(int64_t), s), "hipMemsetAsync");
+    // a kernel, not a memset: callers may capture this call in a graph
+    hipLaunchKernelGGL(zero_offset_kernel, dim3(1), dim3(1), 0, s, offsets);
+    MDL_CHECK_LAUNCH("zero_offset_kernel");
+    return MDL_OK;
   }
   if (workspace_bytes < mdl_offsets_workspace_bytes(n))
     return fail(MDL_ERR_WORKSPACE, "mdl_lengths_to_offsets: workspace too small");
@@ -178,10 +197,13 @@ int mdl_lengths_to_offsets(const int64_t* lengths, int64_t n, int64_t* offsets, 
   int64_t* sums = static_cast<int64_t*>(workspace);
   hipLaunchKernelGGL(scan_tile_sums, dim3((unsigned)tiles), dim3(kScanThreads), 0, s, lengths, n, sums);
   MDL_CHECK_LAUNCH("scan_tile_sums");
-  hipLaunchKernelGGL(scan_sums_single, dim3(1), dim3(kScanThreads), 0, s, sums, tiles);
-  MDL_CHECK_LAUNCH("scan_sums_single");
+  const int self = tiles <= kScanSelfPrefixTiles ? 1 : 0;
+  if (!self) {
+    hipLaunchKernelGGL(scan_sums_single, dim3(1), dim3(kScanThreads), 0, s, sums, tiles);
+    MDL_CHECK_LAUNCH("scan_sums_single");
+  }
   hipLaunchKernelGGL(scan_tiles_final, dim3((unsigned)tiles), dim3(kScanThreads), 0, s, lengths, n,
-                     sums, offsets);
+                     sums, offsets, self);
   MDL_CHECK_LAUNCH("scan_tiles_final");
   return MDL_OK;
 }

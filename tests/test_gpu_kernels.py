@@ -82,7 +82,9 @@ def test_bucketize_mod_bit_exact(device):
 
 def test_lengths_to_offsets_bit_exact(device):
     rng = np.random.default_rng(12)
-    for n in (0, 1, 5, 2048, 2049, 100_003, 1_638_400):
+    # up to 1024 tiles of 2048 the final kernel adds up its prefix itself;
+    # 2.5 M lengths (1221 tiles) take the three-launch scan
+    for n in (0, 1, 5, 2048, 2049, 100_003, 1_638_400, 2_500_000):
         announce("lengths_to_offsets", n)
         lengths = rng.integers(0, 33, size=n).astype(np.int64)
         got = ops.lengths_to_offsets(torch.from_numpy(lengths).to(device))
