@@ -161,13 +161,18 @@ __global__ __launch_bounds__(kSortThreads) __attribute__((amdgpu_waves_per_eu(4)
     const uint32_t d = (k[i] >> shift) & mask;
     uint64_t m = __ballot(valid);
     // Always eight ballots, unrolled: a narrower last digit has zero high
-    // bits in every lane, whose ballots leave m unchanged.
+    // bits in every lane, whose ballots leave m unchanged.  The lanes that
+    // agree with this lane on bit b are ~(ballot ^ t) with t all ones when the
+    // lane's bit is set: one three-input logic op per half.
+    uint32_t mlo = (uint32_t)m, mhi = (uint32_t)(m >> 32);
 #pragma unroll
     for (int b = 0; b < kDigitBits; ++b) {
-      const bool bit = (d >> b) & 1u;
-      const uint64_t bb = __ballot(bit);
-      m &= bit ? bb : ~bb;
+      const uint32_t t = (uint32_t)((int32_t)(d << (31 - b)) >> 31);
+      const uint64_t bb = __ballot(t != 0u);
+      mlo &= ~((uint32_t)bb ^ t);
+      mhi &= ~((uint32_t)(bb >> 32) ^ t);
     }
+    m = ((uint64_t)mhi << 32) | mlo;
     const uint32_t r = (uint32_t)__popcll(m & lt_mask);
     const uint32_t cnt = (uint32_t)__popcll(m);
     const uint32_t old = s_wh[w][d];
