@@ -162,17 +162,23 @@ __global__ __launch_bounds__(kSortThreads) __attribute__((amdgpu_waves_per_eu(4)
     uint64_t m = __ballot(valid);
     // Always eight ballots, unrolled: a narrower last digit has zero high
     // bits in every lane, whose ballots leave m unchanged.  The lanes that
-    // agree with this lane on bit b are ~(ballot ^ t) with t all ones when the
-    // lane's bit is set: one three-input logic op per half.
-    uint32_t mlo = (uint32_t)m, mhi = (uint32_t)(m >> 32);
+    // differ from this lane in bit b are ballot ^ t, t all ones when the
+    // lane's bit is set; x gathers them with one three-input logic op per
+    // half (bitop3 table 0xF6: x | (ballot ^ t)).
+    uint32_t t[kDigitBits];
+    uint64_t bb[kDigitBits];
 #pragma unroll
     for (int b = 0; b < kDigitBits; ++b) {
-      const uint32_t t = (uint32_t)((int32_t)(d << (31 - b)) >> 31);
-      const uint64_t bb = __ballot(t != 0u);
-      mlo &= ~((uint32_t)bb ^ t);
-      mhi &= ~((uint32_t)(bb >> 32) ^ t);
+      t[b] = (uint32_t)((int32_t)(d << (31 - b)) >> 31);
+      bb[b] = __ballot(t[b] != 0u);
     }
-    m = ((uint64_t)mhi << 32) | mlo;
+    uint32_t xlo = 0u, xhi = 0u;
+#pragma unroll
+    for (int b = 0; b < kDigitBits; ++b) {
+      xlo = __builtin_amdgcn_bitop3_b32(xlo, (uint32_t)bb[b], t[b], 0xF6);
+      xhi = __builtin_amdgcn_bitop3_b32(xhi, (uint32_t)(bb[b] >> 32), t[b], 0xF6);
+    }
+    m &= ~(((uint64_t)xhi << 32) | xlo);
     const uint32_t r = (uint32_t)__popcll(m & lt_mask);
     const uint32_t cnt = (uint32_t)__popcll(m);
     const uint32_t old = s_wh[w][d];
