@@ -147,12 +147,14 @@ __global__ __launch_bounds__(kSortThreads) __attribute__((amdgpu_waves_per_eu(4)
   const int64_t wave_base = tile_base + (int64_t)w * (kWave * kSortItems);
   const uint64_t lt_mask = (lane == 0) ? 0ull : (~0ull >> (64 - lane));
   uint32_t k[kSortItems], v[kSortItems], rank[kSortItems];
+  // Entries past n (the last tile only) load entry n - 1 instead of
+  // branching around the load; the ranking and scatter skip them.
 #pragma unroll
   for (int i = 0; i < kSortItems; ++i) {
     const int64_t idx = wave_base + (int64_t)i * kWave + lane;
-    const bool valid = idx < n;
-    k[i] = valid ? keys_in[idx] : 0u;
-    v[i] = valid ? vals_in[idx] : 0u;
+    const int64_t ic = idx < n ? idx : n - 1;
+    k[i] = keys_in[ic];
+    v[i] = vals_in[ic];
   }
 #pragma unroll
   for (int i = 0; i < kSortItems; ++i) {
