@@ -59,7 +59,7 @@ __global__ __launch_bounds__(kSortThreads) void radix_upsweep(const uint32_t* __
 #pragma unroll
   for (int i = 0; i < kSortItems; ++i) {
     const int64_t idx = base + (int64_t)i * kSortThreads + tid;
-    k[i] = idx < n ? keys[idx] : 0u;
+    k[i] = keys[idx < n ? idx : n - 1];  // past n: a valid address, not counted
   }
   // A run of neighbouring lanes with one digit adds its length once, from
   // its first lane.  Hot ids (Zipf) sit next to each other once the keys are
