@@ -457,8 +457,13 @@ __device__ __forceinline__ void reduce_chunk_body(const BwdArgs& a, int64_t c, c
       e = e || fin[u];
       mean[u] = false;
       gp[u] = valid[u] && R.col_ok ? R.template grad_row<kOne>(pay, mean[u]) + R.col : zero_row<TG>();
-      cnt[u] = 0.f;
-      if (mean[u]) cnt[u] = a.bag_count[pay];
+      // The bag count loads without a branch (lanes that need none read the
+      // zero row); a table read by one feature decides for the whole wave.
+      if (kOne) {
+        cnt[u] = R.g_mean ? ld_policy(mean[u] ? a.bag_count + pay : zero_row<float>()) : 0.f;
+      } else {
+        cnt[u] = ld_policy(mean[u] ? a.bag_count + pay : zero_row<float>());
+      }
     }
     // Every global load of the group, back to back: gradient rows and, for
     // runs that finish here, the weight row and accumulator.
@@ -477,7 +482,7 @@ __device__ __forceinline__ void reduce_chunk_body(const BwdArgs& a, int64_t c, c
     }
 #pragma unroll
     for (int u = 0; u < U; ++u) {
-      if (!valid[u]) continue;
+      // (an entry past the slice adds its zero row and finishes nothing)
       const float inv = mean[u] ? __builtin_amdgcn_rcpf(fmaxf(cnt[u], 1.f)) : 1.f;
 #pragma unroll
       for (int k = 0; k < C; ++k) acc[k] = fmaf(v[u][k], inv, acc[k]);
