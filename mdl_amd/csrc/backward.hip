@@ -18,7 +18,7 @@
 // joined once per chunk by a segmented scan over the slots' open partials.
 // A run that crosses chunk bounds (hot Zipf rows can have 10^4+ entries)
 // leaves one fp32 partial per chunk it touches; a second kernel adds those in
-// chunk order and finishes the run.  The summation order depends on the
+// an order fixed by the chunk count and finishes the run.  The summation order depends on the
 // chunk layout only, and no floating-point atomics are used, so results do
 // not depend on scheduling.
 #include "common.cuh"
@@ -28,6 +28,7 @@ namespace mdl {
 int sort_pairs(uint32_t* keys, uint32_t* vals, uint32_t* keys_alt, uint32_t* vals_alt, int64_t n,
                int key_bits, void* ws, size_t ws_bytes, int* in_alt, hipStream_t s);
 size_t sort_ws_bytes(int64_t n);
+int sort_pass_count(int key_bits);
 int launch_sum_partials(const float* partial, int64_t m, const int64_t* m_dev, float* out, hipStream_t s);
 
 constexpr int kChunkMax = 512;    // entries of one chunk at most
@@ -158,20 +159,25 @@ __global__ __launch_bounds__(kBoundThreads) void bwd_bounds_kernel(const mdl_tab
 // Chunk numbering and descriptors, block t for table t: table t's chunks are
 // [chunk_base[t], chunk_base[t] + n_t) in table order -- the block adds up
 // the chunk counts of the tables before it -- so neighbouring chunks (one
-// XCD's range) share a table; the last block writes the total.
+// XCD's range) share a table; the last block writes the total.  Bounds found
+// in keys that are not sorted by table could end before they start or
+// overlap: each range is read as [start, max(start, end)) and the chunks
+// stop at max_chunks, so every descriptor stays inside the sorted array and
+// the workspace.
 __global__ __launch_bounds__(256) void bwd_desc_kernel(const mdl_table* __restrict__ tables, int32_t T,
                                                        const int64_t* __restrict__ table_start,
                                                        const int64_t* __restrict__ table_end,
                                                        int64_t* __restrict__ chunk_base,
                                                        int64_t* __restrict__ total,
-                                                       ChunkDesc* __restrict__ desc) {
+                                                       ChunkDesc* __restrict__ desc, int64_t max_chunks) {
   __shared__ int64_t s_part[256 / kWave];
   const int32_t t = blockIdx.x;
   const int lane = lane_id(), w = threadIdx.x / kWave;
   int64_t before = 0;
   for (int32_t q = threadIdx.x; q < t; q += blockDim.x) {
     const int64_t cq = table_chunk_len(tables[q]);
-    before += (table_end[q] - table_start[q] + cq - 1) / cq;
+    const int64_t sq = table_start[q], eq = table_end[q];
+    before += ((eq > sq ? eq : sq) - sq + cq - 1) / cq;
   }
   for (int m = 1; m < kWave; m <<= 1) {
     const int lo = shfl_i((int)(before & 0xffffffff), lane ^ m);
@@ -182,12 +188,15 @@ __global__ __launch_bounds__(256) void bwd_desc_kernel(const mdl_table* __restri
   __syncthreads();
   int64_t base = 0;
   for (int q = 0; q < 256 / kWave; ++q) base += s_part[q];
-  const int64_t lo = table_start[t], hi = table_end[t];
+  const int64_t lo = table_start[t], hi_raw = table_end[t];
+  const int64_t hi = hi_raw > lo ? hi_raw : lo;
   const int64_t cb = table_chunk_len(tables[t]);
-  const int64_t nch = (hi - lo + cb - 1) / cb;
+  const int64_t room = max_chunks - base;
+  const int64_t nch_all = (hi - lo + cb - 1) / cb;
+  const int64_t nch = nch_all < room ? nch_all : (room > 0 ? room : 0);
   if (threadIdx.x == 0) {
-    chunk_base[t] = base;
-    if (t == T - 1) *total = base + nch;
+    chunk_base[t] = base < max_chunks ? base : max_chunks;
+    if (t == T - 1) *total = base + nch < max_chunks ? base + nch : max_chunks;
   }
   for (int64_t j = threadIdx.x; j < nch; j += blockDim.x) {
     const int64_t b = lo + j * cb;
@@ -304,7 +313,7 @@ struct Reducer {
   int32_t single;
   TW* W;
   float* state;
-  int64_t row_base;
+  int64_t row_base, num_rows;
   float inv_dim;
   // fields of the table's only feature (single >= 0)
   const TG* g_base;
@@ -319,6 +328,7 @@ struct Reducer {
     W = (TW*)uni64b((int64_t)tb.weight);
     state = (float*)uni64b((int64_t)tb.state);
     row_base = uni64b(tb.row_base);
+    num_rows = uni64b(tb.num_rows);
     inv_dim = 1.f / (float)dim;  // exact for power-of-two dims
     L = lanes_for(dim, C);
     G = kWave / L;
@@ -340,6 +350,13 @@ struct Reducer {
       pbase = uni64b(f.payload_base);
       g_mean = __builtin_amdgcn_readfirstlane(f.pooling) == MDL_POOL_MEAN;
     }
+  }
+
+  // Whether a sorted key names a row of this table.  Keys that do not (a
+  // caller's key width that does not match its keys leaves them unsorted)
+  // touch no weight row or accumulator.
+  __device__ __forceinline__ bool row_ok(uint32_t key) const {
+    return (uint64_t)((int64_t)key - row_base) < (uint64_t)num_rows;
   }
 
   // Gradient row of payload p and whether it is divided by its bag count.
@@ -371,6 +388,7 @@ struct Reducer {
                                          float& ss_acc) const {
     const int64_t row = (int64_t)key - row_base;
     if (kMode == kModeAdagrad) {
+      if (!row_ok(key)) return;
       const float ss = row_sumsq(v);
       // scale == 1 leaves every product exact, so unclipped steps are unchanged
       const float acc = acc0 + (ss * (scale * scale)) * inv_dim;
@@ -472,9 +490,9 @@ __device__ __forceinline__ void reduce_chunk_body(const BwdArgs& a, int64_t c, c
       RowIO<TG, C>::load(gp[u], v[u]);
       if (adagrad) {
         const int64_t row = (int64_t)key[u] - R.row_base;
-        RowIO<TW, C>::template load<kUpdatePolicy>(own[u] && R.col_ok ? R.W + row * R.dim + R.col : zero_row<TW>(),
-                                                   w[u]);
-        acc0[u] = ld_policy<kUpdatePolicy>(own[u] ? R.state + row : zero_row<float>());
+        const bool ld = own[u] && R.row_ok(key[u]);
+        RowIO<TW, C>::template load<kUpdatePolicy>(ld && R.col_ok ? R.W + row * R.dim + R.col : zero_row<TW>(), w[u]);
+        acc0[u] = ld_policy<kUpdatePolicy>(ld ? R.state + row : zero_row<float>());
       } else {
         zero(w[u]);
         acc0[u] = 0.f;
@@ -550,7 +568,7 @@ __device__ __forceinline__ void reduce_chunk_body(const BwdArgs& a, int64_t c, c
       float w[C];
       float acc0 = 0.f;
       zero(w);
-      if (adagrad) {
+      if (adagrad && R.row_ok(key)) {
         if (R.col_ok) RowIO<TW, C>::template load<kUpdatePolicy>(R.W + row * R.dim + R.col, w);
         acc0 = ld_policy<kUpdatePolicy>(R.state + row);
       }
@@ -617,43 +635,65 @@ __device__ __forceinline__ void fixup_chunk(const BwdArgs& a, int64_t c, const C
   if (R.dim > kWave * C) return;  // rejected on the host; never reached
   // Walk back over chunks that lie wholly inside the run to the chunk holding
   // its first entry (never past the table's first chunk).
+  // The wave reads 64 chunks' flags per step (a Zipf head row spans many
+  // chunks; one dependent load per chunk made this walk the fix-up's cost).
   const int64_t first_chunk = uni64b(a.chunk_base[d.table]);
   int64_t s = c - 1;
-  while (s > first_chunk && (__builtin_amdgcn_readfirstlane(a.chunk_flags[s]) & kSingle)) --s;
+  for (;;) {
+    const int64_t q = s - lane_id();
+    const bool inside = q > first_chunk;
+    const int32_t fq = a.chunk_flags[inside ? q : first_chunk];
+    const uint64_t stop = __ballot(!inside || !(fq & kSingle));
+    if (stop) {
+      s -= __builtin_ctzll(stop);
+      break;
+    }
+    s -= kWave;
+  }
   float v[C];
   zero(v);
-  if (R.col_ok) {
-    // Partials of the chunks the run covers, added in chunk order; loads
-    // are issued eight chunks at a time.
-    int64_t q = s;
-    for (; q + 8 <= c; q += 8) {
-      float tt[8][C];
+  // Partials of the chunks the run covers: slot g adds chunks s + g,
+  // s + g + G, ... (eight loads in flight per lane), then the G slot sums
+  // meet in a butterfly.  Each pairwise add is commutative, so every lane
+  // ends with the same bits and the order is fixed from run to run.
+  {
+    const int G = R.G;
+    int64_t q = s + R.slot;
+    if (R.col_ok) {
+      for (; q + 7 * G < c; q += 8 * G) {
+        float tt[8][C];
 #pragma unroll
-      for (int j = 0; j < 8; ++j) {
-        const float* pl = a.part_last + (q + j) * a.max_dim + R.col;
+        for (int j = 0; j < 8; ++j) {
+          const float* pl = a.part_last + (q + j * G) * a.max_dim + R.col;
 #pragma unroll
-        for (int k = 0; k < C; ++k) tt[j][k] = pl[k];
+          for (int k = 0; k < C; ++k) tt[j][k] = pl[k];
+        }
+#pragma unroll
+        for (int j = 0; j < 8; ++j)
+#pragma unroll
+          for (int k = 0; k < C; ++k) v[k] += tt[j][k];
       }
+      for (; q < c; q += G) {
+        const float* pl = a.part_last + q * a.max_dim + R.col;
 #pragma unroll
-      for (int j = 0; j < 8; ++j)
-#pragma unroll
-        for (int k = 0; k < C; ++k) v[k] += tt[j][k];
+        for (int k = 0; k < C; ++k) v[k] += pl[k];
+      }
     }
-    for (; q < c; ++q) {
-      const float* pl = a.part_last + q * a.max_dim + R.col;
+    for (int m = R.L; m < kWave; m <<= 1)
 #pragma unroll
-      for (int k = 0; k < C; ++k) v[k] += pl[k];
+      for (int k = 0; k < C; ++k) v[k] += shfl_f(v[k], lane_id() ^ m);
+    if (R.col_ok) {
+      const float* pf = a.part_first + c * a.max_dim + R.col;
+#pragma unroll
+      for (int k = 0; k < C; ++k) v[k] += pf[k];
     }
-    const float* pf = a.part_first + c * a.max_dim + R.col;
-#pragma unroll
-    for (int k = 0; k < C; ++k) v[k] += pf[k];
   }
   const uint32_t key = a.keys[d.begin];
   const int64_t uidx = kMode == kModeCoalesce ? a.head_base[c] - 1 : 0;
   float w[C];
   float acc0 = 0.f;
   zero(w);
-  if (kMode == kModeAdagrad && R.slot == 0) {
+  if (kMode == kModeAdagrad && R.slot == 0 && R.row_ok(key)) {
     const int64_t row = (int64_t)key - R.row_base;
     if (R.col_ok) RowIO<TW, C>::template load<kUpdatePolicy>(R.W + row * R.dim + R.col, w);
     acc0 = ld_policy<kUpdatePolicy>(R.state + row);
@@ -714,7 +754,7 @@ static int plan(const mdl_table* tables, int32_t T, const uint32_t* sk, int64_t 
                      w.table_start, w.table_end);
   MDL_CHECK_LAUNCH("bwd_bounds_kernel");
   hipLaunchKernelGGL(bwd_desc_kernel, dim3((unsigned)T), dim3(256), 0, s, tables, T, w.table_start, w.table_end,
-                     w.chunk_base, w.num_chunks, w.desc);
+                     w.chunk_base, w.num_chunks, w.desc, max_chunks_for(n, T));
   MDL_CHECK_LAUNCH("bwd_desc_kernel");
   return MDL_OK;
 }
@@ -853,7 +893,7 @@ static int sorted_args(const char* who, BwdArgs* a, const mdl_feature* feats, in
   BwdWs w;
   const size_t need = carve(&w, workspace, n, num_tables, max_dim);
   if (workspace_bytes < need) return fail(MDL_ERR_WORKSPACE, std::string(who) + ": workspace too small");
-  const int passes = (key_bits + 7) / 8;
+  const int passes = sort_pass_count(key_bits);
   const uint32_t* sk = (passes & 1) ? w.keys_alt : sort_keys;
   const uint32_t* sv = (passes & 1) ? w.vals_alt : sort_payload;
   fill_args(a, feats, num_features, tables, num_tables, max_dim, sk, sv, bag_count, w, n);

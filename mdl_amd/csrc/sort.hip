@@ -227,6 +227,10 @@ __global__ __launch_bounds__(kSortThreads) __attribute__((amdgpu_waves_per_eu(4)
   }
 }
 
+// Passes sort_pairs makes for keys of key_bits bits: the sorted pairs end in
+// the alternate buffers when it is odd.
+int sort_pass_count(int key_bits) { return key_bits > 0 ? (key_bits + kDigitBits - 1) / kDigitBits : 0; }
+
 size_t sort_ws_bytes(int64_t n) {
   const int64_t ntiles = (n + kSortTile - 1) / kSortTile;
   return (size_t)(kRadix * (ntiles > 0 ? ntiles : 1) + kRadix) * sizeof(uint32_t) + 256;
@@ -247,8 +251,8 @@ int sort_pairs(uint32_t* keys, uint32_t* vals, uint32_t* keys_alt, uint32_t* val
   uint32_t* ko = keys_alt;
   uint32_t* vo = vals_alt;
   int passes = 0;
-  for (int shift = 0; shift < key_bits; shift += 8) {
-    const int bits = key_bits - shift < 8 ? key_bits - shift : 8;
+  for (int shift = 0; shift < key_bits; shift += kDigitBits) {
+    const int bits = key_bits - shift < kDigitBits ? key_bits - shift : kDigitBits;
     const uint32_t mask = (1u << bits) - 1u;
     hipLaunchKernelGGL(radix_upsweep, dim3(ntiles), dim3(kSortThreads), 0, s, ki, n, shift, mask, counts,
                        ntiles);
@@ -263,7 +267,7 @@ int sort_pairs(uint32_t* keys, uint32_t* vals, uint32_t* keys_alt, uint32_t* val
     t = vi; vi = vo; vo = t;
     ++passes;
   }
-  *in_alt = passes & 1;
+  *in_alt = passes & 1;  // passes == sort_pass_count(key_bits)
   return MDL_OK;
 }
 

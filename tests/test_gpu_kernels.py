@@ -94,11 +94,14 @@ def test_lengths_to_offsets_bit_exact(device):
 # ----------------------------------------------------------------- sort --
 
 
-@pytest.mark.parametrize("bits", [1, 7, 8, 13, 24, 31, 32])
+@pytest.mark.parametrize("bits", [1, 7, 8, 13, 24, 25, 27, 30, 31, 32])
 def test_radix_sort_is_stable_and_exact(device, bits):
+    """Every key width takes 8-bit passes over 4096-entry tiles; the sizes
+    straddle whole tiles and partial last tiles."""
+
     rng = np.random.default_rng(13 + bits)
     lib = _lib.lib()
-    for n in (1, 100, 4096, 4097, 300_001):
+    for n in (1, 100, 4096, 4097, 8193, 16384, 16385, 300_001, 2_000_003 if bits in (24, 31) else 20_000):
         announce("sort_pairs", n, bits)
         hi = (1 << bits) - 1
         keys = rng.integers(0, hi, size=n, dtype=np.uint64, endpoint=True)
@@ -415,6 +418,132 @@ def test_fused_backward_is_deterministic(device):
         results.append([t.cpu().clone() for t in tabs] + [s.cpu().clone() for s in states])
     for a, b in zip(*results):
         assert torch.equal(a, b)
+
+
+@pytest.mark.parametrize("big_rows,dtype,dim", [((1 << 25) + 3, torch.float32, 8),
+                                                ((1 << 30) + 5, torch.bfloat16, 2)])
+def test_clipped_step_with_wide_keys(device, big_rows, dtype, dim):
+    """The clipped step sorts (mdl_backward_sort), then reduces the sorted
+    pairs twice (mdl_backward_sumsq, mdl_backward_apply), which must find them
+    where the sort's pass count left them; 26- and 31-bit keys (four passes)
+    and the hot last row of a table of 2^30 rows."""
+
+    rng = np.random.default_rng(71)
+    announce("clipped_wide_keys", big_rows, dtype, dim)
+    big = torch.zeros((big_rows, dim), dtype=dtype, device=device)
+    big_state = torch.zeros(big_rows, dtype=torch.float32, device=device)
+    small = _table(rng, 3000, 16, dtype, device)
+    small_state = torch.from_numpy(rng.random(3000).astype(np.float32)).to(device)
+    tabs, states, dims = [big, small], [big_state, small_state], [dim, 16]
+    plan = ops.GroupPlan()
+    ids, lens, meta = [], [], []
+    for t, pool in ((0, "mean"), (1, "sum"), (0, "none")):
+        plan.add_feature(tabs[t], pooling=pool, null_policy="exclude", state=states[t])
+        rows = tabs[t].shape[0]
+        ln = None if pool == "none" else rng.integers(0, 24, size=1500)
+        n = 1500 if ln is None else int(ln.sum())
+        x = rng.integers(0, rows, size=n)
+        x[rng.random(n) < 0.3] = rows - 1  # the table's last row: the widest keys
+        x[::13] = 0
+        ids.append(torch.from_numpy(x.astype(np.int64)).to(device))
+        lens.append(None if ln is None else torch.from_numpy(ln).to(device))
+        meta.append((t, pool, x, ln))
+    assert plan.key_bits == int(big_rows + 3000).bit_length() and plan.key_bits > 24
+    touched = np.unique(np.concatenate([m[2] for m in meta if m[0] == 0]))
+    tidx = torch.from_numpy(touched).to(device)
+    big[tidx] = torch.from_numpy(rng.standard_normal((touched.size, dim)).astype(np.float32)).to(dtype).to(device)
+    big_state[tidx] = torch.from_numpy(rng.random(touched.size).astype(np.float32)).to(device)
+    w0 = [to_np(big[tidx]).copy(), to_np(small).copy()]
+    a0 = [big_state[tidx].cpu().numpy().copy(), small_state.cpu().numpy().copy()]
+    res = ops.grouped_forward(plan, ids, lens, with_backward=True)
+    grads = [torch.from_numpy(rng.standard_normal(tuple(o.shape)).astype(np.float32)).to(dtype).to(device)
+             for o in res.outputs]
+    rows_vals = []
+    for t in range(2):
+        rs, vs = [], []
+        for f, (tt, pool, x, ln) in enumerate(meta):
+            if tt == t:
+                r, v = O.per_id_grads(x, ln, to_np(grads[f]).reshape(-1, dims[t]), pool, "exclude")
+                rs.append(r)
+                vs.append(v)
+        rows_vals.append(O.coalesce(np.concatenate(rs), np.concatenate(vs)))
+    scaled, total, _ = O.clip_grad_norm([v for _, v in rows_vals], 1.0)
+    lr, eps = 0.01, 1e-8
+    norm = ops.backward_adagrad(res, grads, lr=lr, eps=eps, clip_norm=1.0)
+    assert abs(float(norm.item()) - total) <= 1e-4 * total
+    tol = (1e-5, 1e-6) if dtype == torch.float32 else (1e-2, 1e-2)
+    # table 0: compare its touched rows (the oracle runs on them compacted)
+    rr = rows_vals[0][0]
+    pos = np.searchsorted(touched, rr)
+    wexp, aexp = O.rowwise_adagrad(w0[0][pos], a0[0][pos], np.arange(rr.size), scaled[0], lr, eps,
+                                   is_bf16=dtype == torch.bfloat16)
+    rr_dev = torch.from_numpy(rr).to(device)
+    assert_close(to_np(big[rr_dev]), wexp, *tol)
+    assert_close(big_state[rr_dev].cpu().numpy(), aexp, 1e-5, 1e-7)
+    untouched = np.setdiff1d(touched, rr)
+    assert np.array_equal(to_np(big[torch.from_numpy(untouched).to(device)]), w0[0][np.searchsorted(touched, untouched)])
+    wexp, aexp = O.rowwise_adagrad(w0[1], a0[1], rows_vals[1][0], scaled[1], lr, eps, is_bf16=dtype == torch.bfloat16)
+    assert_close(to_np(small), wexp, *tol)
+    assert_close(small_state.cpu().numpy(), aexp, 1e-5, 1e-7)
+
+
+@pytest.mark.parametrize("mode", ["coalesce", "adagrad", "clipped"])
+def test_hot_row_spanning_hundreds_of_chunks(device, mode):
+    """A Zipf head row whose run covers several hundred chunks (the fix-up
+    searches back over such chunks 64 at a time); a second hot row follows it
+    in the same table, and a dim-16 table has a run of ~150 chunks."""
+
+    rng = np.random.default_rng(60)
+    announce("hot_row_chunks", mode)
+    dims, rows = [128, 16], [5000, 3000]
+    tabs = [_table(rng, r, d, torch.float32, device) for r, d in zip(rows, dims)]
+    states = [torch.from_numpy(rng.random(r).astype(np.float32)).to(device) for r in rows]
+    plan = ops.GroupPlan()
+    ids, lens, meta = [], [], []
+    for t, pool in ((0, "mean"), (1, "sum"), (0, "sum")):
+        plan.add_feature(tabs[t], pooling=pool, null_policy="exclude", state=states[t])
+        ln = rng.integers(20, 80, size=2048)
+        x = rng.integers(0, rows[t], size=int(ln.sum()))
+        x[rng.random(x.size) < 0.8] = 7
+        x[rng.random(x.size) < 0.1] = 9
+        ids.append(torch.from_numpy(x.astype(np.int64)).to(device))
+        lens.append(torch.from_numpy(ln).to(device))
+        meta.append((t, pool, x, ln))
+    w0 = [to_np(t).copy() for t in tabs]
+    a0 = [s.cpu().numpy().copy() for s in states]
+    res = ops.grouped_forward(plan, ids, lens, with_backward=True)
+    grads = [torch.from_numpy(rng.standard_normal(tuple(o.shape)).astype(np.float32)).to(device)
+             for o in res.outputs]
+    expect = []
+    for t in range(len(tabs)):
+        rs, vs = [], []
+        for f, (tt, pool, x, ln) in enumerate(meta):
+            if tt == t:
+                r, v = O.per_id_grads(x, ln, to_np(grads[f]).reshape(-1, dims[t]), pool, "exclude")
+                rs.append(r)
+                vs.append(v)
+        expect.append((O.coalesce(np.concatenate(rs), np.concatenate(vs)),
+                       O.coalesce(np.concatenate(rs), np.abs(np.concatenate(vs)))[1]))
+    assert np.count_nonzero(expect[0][0][0] == 7) == 1
+    if mode == "coalesce":
+        out = ops.backward_coalesce(res, grads)
+        for t, ((rr, vv), vabs) in enumerate(expect):
+            got_rows, got_vals = out[t]
+            assert np.array_equal(got_rows.cpu().numpy(), rr), f"table {t} rows"
+            assert_close(to_np(got_vals), vv, 1e-5, 1e-5, vabs)
+        return
+    lr, eps = 0.01, 1e-8
+    vals = [vv for (_, vv), _ in expect]
+    if mode == "clipped":
+        vals, total, _ = O.clip_grad_norm(vals, 1.0)
+        norm = ops.backward_adagrad(res, grads, lr=lr, eps=eps, clip_norm=1.0)
+        assert abs(float(norm.item()) - total) <= 1e-5 * total
+    else:
+        ops.backward_adagrad(res, grads, lr=lr, eps=eps)
+    for t, ((rr, _), _) in enumerate(expect):
+        wexp, aexp = O.rowwise_adagrad(w0[t], a0[t], rr, vals[t], lr, eps)
+        assert_close(states[t].cpu().numpy(), aexp, 1e-5, 1e-7)
+        assert_close(to_np(tabs[t]), wexp, 1e-5, 1e-6)
 
 
 @pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
