@@ -50,6 +50,17 @@ __device__ __forceinline__ float bf16_to_f32(bf16_t h) {
 // accesses; C == 1 is the scalar path for rows whose byte size or base is not
 // 16-byte aligned.
 
+// A row of zeros in device memory.  Lanes whose row is absent (past the end
+// of a chunk, an invalid id, a column past dim) load from here instead of
+// branching around the load, so every load of a pass issues back to back.
+// (One copy per translation unit; only device code reads it.)
+static __device__ __align__(256) float g_zero_row[512];
+
+template <typename T>
+__device__ __forceinline__ const T* zero_row() {
+  return reinterpret_cast<const T*>(g_zero_row);
+}
+
 template <typename T, int C>
 struct RowIO;
 
@@ -62,15 +73,31 @@ enum CachePolicy { kKeep = 0, kStream = 1 };
 // Which accesses stream (compile-time switches): the lookup's outputs and
 // sort keys (on: c1 forward 0.290 -> 0.282 ms, reduce 0.510 -> 0.498 ms), and
 // the update's weight rows and accumulators (off: streaming them slowed the
-// reduce from 0.51 to 0.54 ms).
+// reduce from 0.51 to 0.54 ms; streaming only their loads, 0.536 ms; only
+// their stores, no change).
 #ifndef MDL_STREAM_UPDATE
 #define MDL_STREAM_UPDATE 0
 #endif
 #ifndef MDL_STREAM_OUT
 #define MDL_STREAM_OUT 1
 #endif
+#ifndef MDL_STREAM_UPDATE_LOAD
+#define MDL_STREAM_UPDATE_LOAD MDL_STREAM_UPDATE
+#endif
 constexpr int kUpdatePolicy = MDL_STREAM_UPDATE ? kStream : kKeep;
+constexpr int kUpdateLoadPolicy = MDL_STREAM_UPDATE_LOAD ? kStream : kKeep;
 constexpr int kOutPolicy = MDL_STREAM_OUT ? kStream : kKeep;
+
+// fp32 rows copied eight elements per lane as two 16-byte pieces, lane sub
+// holding pieces sub and sub + L of its slot's row: each load or store
+// instruction then covers 16·L contiguous bytes of the row.  Eight
+// consecutive elements per lane would make each instruction cover every
+// other 16 bytes, and non-temporal stores leave L2 before the two halves of
+// a 64-byte segment meet (c1 forward 0.291 -> 0.276 ms, c2 sequence gather
+// 0.154 -> 0.139 ms per feature).
+#ifndef MDL_SPLIT_ROWS
+#define MDL_SPLIT_ROWS 1
+#endif
 
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
@@ -131,6 +158,26 @@ struct RowIO<float, C> {
       }
     }
   }
+  // The lane's 4-element pieces q at p + q * stride (stride >= 4), piece q
+  // taken only when q < pieces (the rest read as zero / are not written).
+  template <int kPolicy = kKeep>
+  static __device__ __forceinline__ void load_pieces(const float* p, int stride, int pieces, float (&v)[C]) {
+    static_assert(C % 4 == 0, "pieces of four");
+#pragma unroll
+    for (int q = 0; q < C / 4; ++q) {
+      const f32x4 x = ld_policy<kPolicy>(reinterpret_cast<const f32x4*>(q < pieces ? p + q * stride : zero_row<float>()));
+      v[4 * q] = x.x; v[4 * q + 1] = x.y; v[4 * q + 2] = x.z; v[4 * q + 3] = x.w;
+    }
+  }
+  template <int kPolicy = kKeep>
+  static __device__ __forceinline__ void store_pieces(float* p, int stride, int pieces, const float (&v)[C]) {
+    static_assert(C % 4 == 0, "pieces of four");
+#pragma unroll
+    for (int q = 0; q < C / 4; ++q) {
+      const f32x4 x = {v[4 * q], v[4 * q + 1], v[4 * q + 2], v[4 * q + 3]};
+      if (q < pieces) st_policy<kPolicy>(reinterpret_cast<f32x4*>(p + q * stride), x);
+    }
+  }
 };
 
 template <int C>
@@ -169,17 +216,6 @@ struct RowIO<bf16_t, C> {
     }
   }
 };
-
-// A row of zeros in device memory.  Lanes whose row is absent (past the end
-// of a chunk, an invalid id, a column past dim) load from here instead of
-// branching around the load, so every load of a pass issues back to back.
-// (One copy per translation unit; only device code reads it.)
-static __device__ __align__(256) float g_zero_row[512];
-
-template <typename T>
-__device__ __forceinline__ const T* zero_row() {
-  return reinterpret_cast<const T*>(g_zero_row);
-}
 
 // Compile-time tuning knobs (defaults are the ones measured best on MI355X):
 // rows a lane group walks per backward chunk and per forward chunk, and the

@@ -98,9 +98,12 @@ __device__ __forceinline__ void gather_chunk(const Feat& f, int64_t first, int c
   TO* out = static_cast<TO*>(f.out);
   const int64_t* ids = a.ids + f.ids_begin + first;
   const int step = G * kUnroll;
+  constexpr bool kSplit = MDL_SPLIT_ROWS && std::is_same_v<TW, float> && std::is_same_v<TO, float> && C == 8;
   for (int cb = 0; cb < ncb; ++cb) {
-    const int col = (cb * L + sub) * C;
+    const int col = kSplit ? cb * L * C + sub * 4 : (cb * L + sub) * C;
     const bool col_ok = col < f.dim;
+    // split rows: piece 1 sits 4L elements after piece 0 (dims are multiples of 8 here)
+    const int pieces = kSplit ? (col + 4 * L < f.dim ? 2 : 1) : 0;
     // Two pass groups in flight: the rows of group k+1 are requested before
     // group k is stored, so no row load waits behind a store.
     int64_t nid[kUnroll];  // ids of the next group to load
@@ -116,14 +119,22 @@ __device__ __forceinline__ void gather_chunk(const Feat& f, int64_t first, int c
       for (int u = 0; u < kUnroll; ++u) {
         const int i = base + u * G + slot;
         const bool ok = i < count && (uint64_t)nid[u] < (uint64_t)f.num_rows && col_ok;
-        RowIO<TW, C>::load(ok ? W + nid[u] * f.dim + col : zero_row<TW>(), v[u]);
+        if constexpr (kSplit)
+          RowIO<float, C>::load_pieces(ok ? W + nid[u] * f.dim + col : zero_row<float>(), 4 * L, ok ? pieces : 0, v[u]);
+        else
+          RowIO<TW, C>::load(ok ? W + nid[u] * f.dim + col : zero_row<TW>(), v[u]);
       }
     };
     auto store_rows = [&](int base, const float (&v)[kUnroll][C]) {
 #pragma unroll
       for (int u = 0; u < kUnroll; ++u) {
         const int i = base + u * G + slot;
-        if (i < count && col_ok) RowIO<TO, C>::template store<kOutPolicy>(out + (first + i) * f.out_stride + col, v[u]);
+        if (i < count && col_ok) {
+          if constexpr (kSplit)
+            RowIO<float, C>::template store_pieces<kOutPolicy>(out + (first + i) * f.out_stride + col, 4 * L, pieces, v[u]);
+          else
+            RowIO<TO, C>::template store<kOutPolicy>(out + (first + i) * f.out_stride + col, v[u]);
+        }
       }
     };
     float va[kUnroll][C], vb[kUnroll][C];
@@ -341,6 +352,25 @@ __device__ __forceinline__ void lds_get(const float* p, float (&v)[C]) {
   }
 }
 
+// Split fp32 rows (see MDL_SPLIT_ROWS): the lane's two 16-byte pieces sit
+// at col and col + stride.
+template <int C>
+__device__ __forceinline__ void lds_put_pieces(float* p, int stride, int pieces, const float (&v)[C]) {
+#pragma unroll
+  for (int q = 0; q < C / 4; ++q)
+    if (q < pieces)
+      *reinterpret_cast<float4*>(p + q * stride) = make_float4(v[4 * q], v[4 * q + 1], v[4 * q + 2], v[4 * q + 3]);
+}
+
+template <int C>
+__device__ __forceinline__ void lds_get_pieces(const float* p, int stride, int pieces, float (&v)[C]) {
+#pragma unroll
+  for (int q = 0; q < C / 4; ++q) {
+    const float4 x = q < pieces ? *reinterpret_cast<const float4*>(p + q * stride) : make_float4(0.f, 0.f, 0.f, 0.f);
+    v[4 * q] = x.x; v[4 * q + 1] = x.y; v[4 * q + 2] = x.z; v[4 * q + 3] = x.w;
+  }
+}
+
 template <typename TW, typename TO, int C>
 __device__ __forceinline__ void pooled_chunk(const Feat& f, int64_t first_bag, int nb, const PoolStage& st,
                                              const PoolChunk& pc, float* s_out, const FwdArgs& a) {
@@ -359,6 +389,11 @@ __device__ __forceinline__ void pooled_chunk(const Feat& f, int64_t first_bag, i
   const bool staged = (int64_t)nb * f.dim <= kOutStage;
   const TW* W = static_cast<const TW*>(f.weight);
   TO* out = static_cast<TO*>(f.out);
+  constexpr bool kSplit = MDL_SPLIT_ROWS && std::is_same_v<TW, float> && std::is_same_v<TO, float> && C == 8;
+  // First column of the lane's elements in column block cb, and (split rows)
+  // how many of its two pieces lie inside the row (dims are multiples of 8).
+  auto col_of = [&](int cb) { return kSplit ? cb * L * C + sub * 4 : (cb * L + sub) * C; };
+  auto pieces_of = [&](int col) { return col + 4 * L < f.dim ? 2 : 1; };
   // This slot's slice [s0, s1) of the chunk's ids.
   const int K = (len + G - 1) / G;
   const int s0 = slot * K;
@@ -386,17 +421,27 @@ __device__ __forceinline__ void pooled_chunk(const Feat& f, int64_t first_bag, i
 #pragma unroll
     for (int k = 0; k < C; ++k) r[k] = sum[k] * inv;
     if (staged) {
-      if (col_ok) lds_put<C>(s_out + bag * f.dim + col, r);
+      if (col_ok) {
+        if constexpr (kSplit) lds_put_pieces<C>(s_out + bag * f.dim + col, 4 * L, pieces_of(col), r);
+        else lds_put<C>(s_out + bag * f.dim + col, r);
+      }
       if (emit_cnt) const_cast<PoolStage&>(st).cnt[bag] = wsum;
     } else {
-      if (col_ok) RowIO<TO, C>::template store<kOutPolicy>(out + (first_bag + bag) * f.out_stride + col, r);
+      if (col_ok) {
+        if constexpr (kSplit)
+          RowIO<float, C>::template store_pieces<kOutPolicy>(out + (first_bag + bag) * f.out_stride + col, 4 * L,
+                                                             pieces_of(col), r);
+        else
+          RowIO<TO, C>::template store<kOutPolicy>(out + (first_bag + bag) * f.out_stride + col, r);
+      }
       if (emit_cnt && a.bag_count != nullptr) st_policy(a.bag_count + f.payload_base + first_bag + bag, wsum);
     }
   };
 
   for (int cb = 0; cb < ncb; ++cb) {
-    const int col = (cb * L + sub) * C;
+    const int col = col_of(cb);
     const bool col_ok = col < f.dim;
+    const int pcs = pieces_of(col);
     const bool emit = cb == 0 && sub == 0;
     float acc[C], hp[C];
     zero_c(acc);
@@ -418,7 +463,11 @@ __device__ __forceinline__ void pooled_chunk(const Feat& f, int64_t first_bag, i
       for (int u = 0; u < U; ++u) {
         const bool live = row[u] >= 0 && j + u < s1;
         wt[u] = live ? 1.f : 0.f;
-        RowIO<TW, C>::load(live && col_ok ? W + row[u] * f.dim + col : zero_row<TW>(), v[u]);
+        if constexpr (kSplit)
+          RowIO<float, C>::load_pieces(live && col_ok ? W + row[u] * f.dim + col : zero_row<float>(), 4 * L,
+                                       live && col_ok ? pcs : 0, v[u]);
+        else
+          RowIO<TW, C>::load(live && col_ok ? W + row[u] * f.dim + col : zero_row<TW>(), v[u]);
       }
 #pragma unroll
       for (int u = 0; u < U; ++u) nrow[u] = j + U + u < s1 ? row_at(j + U + u) : -1;
@@ -489,12 +538,19 @@ __device__ __forceinline__ void pooled_chunk(const Feat& f, int64_t first_bag, i
     for (int bb = slot; bb < nb; bb += G) {
       const bool empty = st.off[bb] == st.off[bb + 1];
       for (int cb = 0; cb < ncb; ++cb) {
-        const int col = (cb * L + sub) * C;
+        const int col = col_of(cb);
         if (col >= f.dim) continue;
         float r[C];
-        if (empty) zero_c(r);
-        else lds_get<C>(s_out + bb * f.dim + col, r);
-        RowIO<TO, C>::template store<kOutPolicy>(out + (first_bag + bb) * f.out_stride + col, r);
+        if constexpr (kSplit) {
+          const int pcs = pieces_of(col);
+          if (empty) zero_c(r);
+          else lds_get_pieces<C>(s_out + bb * f.dim + col, 4 * L, pcs, r);
+          RowIO<float, C>::template store_pieces<kOutPolicy>(out + (first_bag + bb) * f.out_stride + col, 4 * L, pcs, r);
+        } else {
+          if (empty) zero_c(r);
+          else lds_get<C>(s_out + bb * f.dim + col, r);
+          RowIO<TO, C>::template store<kOutPolicy>(out + (first_bag + bb) * f.out_stride + col, r);
+        }
       }
     }
     if (a.bag_count != nullptr)
@@ -508,8 +564,13 @@ __device__ __forceinline__ void pooled_chunk(const Feat& f, int64_t first_bag, i
       float z[C];
       zero_c(z);
       for (int cb = 0; cb < ncb; ++cb) {
-        const int col = (cb * L + sub) * C;
-        if (col < f.dim) RowIO<TO, C>::template store<kOutPolicy>(out + (first_bag + bb) * f.out_stride + col, z);
+        const int col = col_of(cb);
+        if (col >= f.dim) continue;
+        if constexpr (kSplit)
+          RowIO<float, C>::template store_pieces<kOutPolicy>(out + (first_bag + bb) * f.out_stride + col, 4 * L,
+                                                             pieces_of(col), z);
+        else
+          RowIO<TO, C>::template store<kOutPolicy>(out + (first_bag + bb) * f.out_stride + col, z);
       }
       if (sub == 0 && a.bag_count != nullptr) st_policy(a.bag_count + f.payload_base + first_bag + bb, 0.f);
     }
@@ -767,9 +828,11 @@ __device__ __forceinline__ void seq_chunk(const SeqArgs& a, int64_t b, int64_t p
   const int64_t* ids = a.ids + b * a.in_len;
   const int step = G * kUnroll;
   int bad = 0;
+  constexpr bool kSplit = MDL_SPLIT_ROWS && std::is_same_v<TW, float> && std::is_same_v<TO, float> && C == 8;
   for (int cb = 0; cb < ncb; ++cb) {
-    const int col = (cb * L + sub) * C;
+    const int col = kSplit ? cb * L * C + sub * 4 : (cb * L + sub) * C;
     const bool col_ok = col < f.dim;
+    const int pieces = col + 4 * L < f.dim ? 2 : 1;  // split rows only
     const bool first = cb == 0 && sub == 0;
     int64_t nid[kUnroll];  // ids of the next group to load
     auto fetch_ids = [&](int base) {
@@ -785,14 +848,24 @@ __device__ __forceinline__ void seq_chunk(const SeqArgs& a, int64_t b, int64_t p
         const int i = base + u * G + slot;
         const bool in_range = (uint64_t)nid[u] < (uint64_t)f.num_rows;
         if (first && i < count) bad += !in_range;
-        RowIO<TW, C>::load(i < count && in_range && col_ok ? W + nid[u] * f.dim + col : zero_row<TW>(), v[u]);
+        const bool ok = i < count && in_range && col_ok;
+        if constexpr (kSplit)
+          RowIO<float, C>::load_pieces(ok ? W + nid[u] * f.dim + col : zero_row<float>(), 4 * L, ok ? pieces : 0, v[u]);
+        else
+          RowIO<TW, C>::load(ok ? W + nid[u] * f.dim + col : zero_row<TW>(), v[u]);
       }
     };
     auto store_rows = [&](int base, const float (&v)[kUnroll][C]) {
 #pragma unroll
       for (int u = 0; u < kUnroll; ++u) {
         const int i = base + u * G + slot;
-        if (i < count && col_ok) RowIO<TO, C>::template store<kOutPolicy>(out + (int64_t)(nz + i) * f.out_stride + col, v[u]);
+        if (i < count && col_ok) {
+          if constexpr (kSplit)
+            RowIO<float, C>::template store_pieces<kOutPolicy>(out + (int64_t)(nz + i) * f.out_stride + col, 4 * L,
+                                                               pieces, v[u]);
+          else
+            RowIO<TO, C>::template store<kOutPolicy>(out + (int64_t)(nz + i) * f.out_stride + col, v[u]);
+        }
       }
     };
     float va[kUnroll][C], vb[kUnroll][C];
@@ -817,7 +890,12 @@ __device__ __forceinline__ void seq_chunk(const SeqArgs& a, int64_t b, int64_t p
 #pragma unroll
     for (int k = 0; k < C; ++k) z[k] = 0.f;
     if (col_ok)
-      for (int i = slot; i < nz; i += G) RowIO<TO, C>::template store<kOutPolicy>(out + (int64_t)i * f.out_stride + col, z);
+      for (int i = slot; i < nz; i += G) {
+        if constexpr (kSplit)
+          RowIO<float, C>::template store_pieces<kOutPolicy>(out + (int64_t)i * f.out_stride + col, 4 * L, pieces, z);
+        else
+          RowIO<TO, C>::template store<kOutPolicy>(out + (int64_t)i * f.out_stride + col, z);
+      }
   }
   if (a.mask)
     for (int i = lane; i < np; i += kWave) a.mask[b * a.out_len + p0 + i] = i >= nz ? 1 : 0;
