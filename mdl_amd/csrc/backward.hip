@@ -491,8 +491,8 @@ __device__ __forceinline__ void reduce_chunk_body(const BwdArgs& a, int64_t c, c
       if (adagrad) {
         const int64_t row = (int64_t)key[u] - R.row_base;
         const bool ld = own[u] && R.row_ok(key[u]);
-        RowIO<TW, C>::template load<kUpdateLoadPolicy>(ld && R.col_ok ? R.W + row * R.dim + R.col : zero_row<TW>(), w[u]);
-        acc0[u] = ld_policy<kUpdateLoadPolicy>(ld ? R.state + row : zero_row<float>());
+        RowIO<TW, C>::template load<kUpdatePolicy>(ld && R.col_ok ? R.W + row * R.dim + R.col : zero_row<TW>(), w[u]);
+        acc0[u] = ld_policy<kUpdatePolicy>(ld ? R.state + row : zero_row<float>());
       } else {
         zero(w[u]);
         acc0[u] = 0.f;
@@ -569,8 +569,8 @@ __device__ __forceinline__ void reduce_chunk_body(const BwdArgs& a, int64_t c, c
       float acc0 = 0.f;
       zero(w);
       if (adagrad && R.row_ok(key)) {
-        if (R.col_ok) RowIO<TW, C>::template load<kUpdateLoadPolicy>(R.W + row * R.dim + R.col, w);
-        acc0 = ld_policy<kUpdateLoadPolicy>(R.state + row);
+        if (R.col_ok) RowIO<TW, C>::template load<kUpdatePolicy>(R.W + row * R.dim + R.col, w);
+        acc0 = ld_policy<kUpdatePolicy>(R.state + row);
       }
       R.finish(key, tot, acc0, w, coalesce ? hb + (int64_t)st.hc[hend + 1] - 1 : 0, ss_acc);
     }
@@ -695,8 +695,8 @@ __device__ __forceinline__ void fixup_chunk(const BwdArgs& a, int64_t c, const C
   zero(w);
   if (kMode == kModeAdagrad && R.slot == 0 && R.row_ok(key)) {
     const int64_t row = (int64_t)key - R.row_base;
-    if (R.col_ok) RowIO<TW, C>::template load<kUpdateLoadPolicy>(R.W + row * R.dim + R.col, w);
-    acc0 = ld_policy<kUpdateLoadPolicy>(R.state + row);
+    if (R.col_ok) RowIO<TW, C>::template load<kUpdatePolicy>(R.W + row * R.dim + R.col, w);
+    acc0 = ld_policy<kUpdatePolicy>(R.state + row);
   }
   float ss = 0.f;
   if (R.slot == 0) R.finish(key, v, acc0, w, uidx, ss);

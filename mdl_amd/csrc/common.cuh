@@ -73,19 +73,15 @@ enum CachePolicy { kKeep = 0, kStream = 1 };
 // Which accesses stream (compile-time switches): the lookup's outputs and
 // sort keys (on: c1 forward 0.290 -> 0.282 ms, reduce 0.510 -> 0.498 ms), and
 // the update's weight rows and accumulators (off: streaming them slowed the
-// reduce from 0.51 to 0.54 ms; streaming only their loads, 0.536 ms; only
-// their stores, no change).
+// reduce from 0.51 to 0.54 ms; streaming only their loads 0.536 ms, only the
+// weight rows' loads 0.535 ms, only the stores no change).
 #ifndef MDL_STREAM_UPDATE
 #define MDL_STREAM_UPDATE 0
 #endif
 #ifndef MDL_STREAM_OUT
 #define MDL_STREAM_OUT 1
 #endif
-#ifndef MDL_STREAM_UPDATE_LOAD
-#define MDL_STREAM_UPDATE_LOAD MDL_STREAM_UPDATE
-#endif
 constexpr int kUpdatePolicy = MDL_STREAM_UPDATE ? kStream : kKeep;
-constexpr int kUpdateLoadPolicy = MDL_STREAM_UPDATE_LOAD ? kStream : kKeep;
 constexpr int kOutPolicy = MDL_STREAM_OUT ? kStream : kKeep;
 
 // fp32 rows copied eight elements per lane as two 16-byte pieces, lane sub
