@@ -327,7 +327,11 @@ int mdl_backward_adagrad(const mdl_feature* feats, int32_t num_features,
 
 /* mdl_backward_adagrad in two calls with the same arguments and workspace:
  * mdl_backward_sort (radix sort + chunk plan), then mdl_backward_apply
- * (segment reduction + update). */
+ * (segment reduction + update).  key_bits must be the sort's: the later
+ * calls find the sorted pairs where its pass count left them.  (Keys wider
+ * than key_bits are left unsorted; a reduce then touches no weight row or
+ * accumulator for a key outside its chunk's table, and the result is wrong
+ * but every access stays in bounds.) */
 int mdl_backward_sort(const mdl_table* tables, int32_t num_tables, int32_t max_dim,
                       uint32_t* sort_keys, uint32_t* sort_payload, int64_t n,
                       int32_t key_bits, void* workspace, size_t workspace_bytes,
