@@ -436,6 +436,60 @@ class EventTimer:
         return float(np.mean(ts)) if ts else float("nan")
 
 
+def aux_measurements(torch, dev, wl, n_ids: float, steps: int, device) -> dict:
+    """The rows beside the headline step, each timed on its own after it:
+
+    * the clipped step (SparseStep.step with clip_norm: sort, squared norm of
+      the coalesced gradient, clip coefficient, apply scaled by it --
+      src/train.py:5788-5826), wall clock over ``steps`` steps like the
+      headline;
+    * device bucketing (mdl_bucketize, src/features.py:360-376 and
+      src/benchmark.py:1246-1250) of one step's worth of raw int64 ids, HIP
+      events around 20 back-to-back launches queued behind a spin kernel, so
+      the host's launch time does not show; 16 algorithmic bytes per id
+      (read 8, write 8).
+    """
+
+    from mdl_amd import ops
+
+    out = {}
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for i in range(steps):
+        dev.steps[i % len(dev.steps)].step(wl.lr, wl.eps, clip_norm=1.0)
+    torch.cuda.synchronize()
+    out["clipped_step"] = {
+        "ms_per_step": (time.perf_counter() - t0) * 1e3 / steps,
+        "clip_norm": 1.0,
+        "what": "fused fwd + sort + squared norm + clip coefficient + row-wise Adagrad scaled by it",
+    }
+    n = int(n_ids)
+    gen = torch.Generator(device=device)
+    gen.manual_seed(7)
+    raw = torch.randint(-(1 << 62), 1 << 62, (n,), dtype=torch.int64, device=device, generator=gen)
+    reps = 20
+    for mode, buckets in (("pre_hashed", 1 << 20), ("mod", 1_000_003)):
+        for _ in range(3):
+            ops.bucketize(raw, buckets, mode=mode, validate_nonzero=False)
+        torch.cuda.synchronize()
+        e0 = torch.cuda.Event(enable_timing=True)
+        e1 = torch.cuda.Event(enable_timing=True)
+        torch.cuda._sleep(20_000_000)  # holds the stream while the launches queue up
+        e0.record()
+        for _ in range(reps):
+            ops.bucketize(raw, buckets, mode=mode, validate_nonzero=False)
+        e1.record()
+        torch.cuda.synchronize()
+        ms = e0.elapsed_time(e1) / reps
+        nbytes = 16.0 * n
+        out[f"bucketize_{mode}"] = {
+            "n": n, "buckets": buckets, "ms": ms, "alg_bytes": nbytes,
+            "achieved_gbps": nbytes / (ms * 1e-3) / 1e9, "frac": nbytes / (ms * 1e-3) / 1e9 / PEAK_HBM_GBPS,
+        }
+    del raw
+    return out
+
+
 # ------------------------------------------------------------ cpu baseline --
 
 
@@ -621,6 +675,8 @@ def main() -> int:
     ap.add_argument("--config", default="c1", choices=sorted(WORKLOADS))
     ap.add_argument("--batches", type=int, default=3, help="distinct synthetic batches cycled through")
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--no-aux", action="store_true",
+                    help="skip the clipped-step and bucketing measurements (off with --calibrate-copy)")
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="also run three plain 1 GiB device copies (counter calibration for rocprofv3 --pmc runs)")
@@ -770,8 +826,12 @@ def main() -> int:
             "alg_bytes_per_launch": dom["alg_bytes_per_launch"],
         },
         "kernels": kernels,
+        "aux": None,
         "cpu_baseline": None,
     }
+    if wl.kind != "sequence" and not args.no_aux and not args.calibrate_copy:
+        # after every timed number above, so the extra steps change none of them
+        result["aux"] = aux_measurements(torch, dev, wl, n_ids, args.steps, device)
     if not args.no_cpu_baseline:
         print("[bench] timing the CPU oracle sample", file=sys.stderr, flush=True)
         result["cpu_baseline"] = cpu_baseline(wl, seconds=args.cpu_seconds)

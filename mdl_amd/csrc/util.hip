@@ -21,10 +21,11 @@ int check_hip(hipError_t err, const char* what) {
 
 // ------------------------------------------------------------ bucketing --
 
+// mod_magic = ceil(2^64 / m) for the mod rule's m = num_buckets - 1 >= 2.
 __global__ void bucketize_kernel(const int64_t* __restrict__ raw, const uint8_t* __restrict__ valid,
                                  int64_t n, int64_t num_buckets, int32_t mode,
                                  int32_t validate_nonzero, int64_t* __restrict__ out,
-                                 int32_t* __restrict__ error_count) {
+                                 int32_t* __restrict__ error_count, uint64_t mod_magic) {
   int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
   const int64_t stride = (int64_t)gridDim.x * blockDim.x;
   int bad = 0;
@@ -39,13 +40,21 @@ __global__ void bucketize_kernel(const int64_t* __restrict__ raw, const uint8_t*
         r = (int64_t)(((uint64_t)v & (uint64_t)(num_buckets - 1)) + 1u);
         bad += (validate_nonzero && v == 0);
       } else {
-        // 1 + floormod(v - 1, m) without forming v - 1 (INT64_MIN safe).
-        const int64_t m = num_buckets - 1;
-        int64_t q = v % m;
-        if (q < 0) q += m;
-        q -= 1;
-        if (q < 0) q += m;
-        r = 1 + q;
+        // 1 + floormod(v - 1, m) without forming v - 1 or dividing: the sign
+        // goes first (x = v or ~v = -v - 1, both below 2^63, INT64_MIN
+        // included), and mulhi(x, ceil(2^64 / m)) is floor(x / m) or one
+        // more, which one add of m corrects.
+        const uint64_t m = (uint64_t)(num_buckets - 1);
+        uint64_t fm1 = 0;  // floormod(v - 1, m)
+        if (m > 1) {
+          const bool neg = v < 0;
+          const uint64_t x = neg ? ~(uint64_t)v : (uint64_t)v;
+          uint64_t rem = x - __umul64hi(x, mod_magic) * m;
+          if ((int64_t)rem < 0) rem += m;
+          const uint64_t fm = neg ? m - 1 - rem : rem;  // floormod(v, m)
+          fm1 = fm == 0 ? m - 1 : fm - 1;
+        }
+        r = (int64_t)(1 + fm1);
       }
     }
     out[i] = r;
@@ -170,8 +179,10 @@ int mdl_bucketize(const int64_t* raw, const uint8_t* valid, int64_t n, int64_t n
   if (raw == nullptr || out == nullptr) return fail(MDL_ERR_INVALID, "mdl_bucketize: null pointer");
   int64_t blocks = (n + 255) / 256;
   if (blocks > 65536) blocks = 65536;
+  const uint64_t m = (uint64_t)(num_buckets - 1);
+  const uint64_t mod_magic = mode == MDL_BUCKET_MOD && m > 1 ? UINT64_MAX / m + 1 : 0;  // ceil(2^64 / m)
   hipLaunchKernelGGL(bucketize_kernel, dim3((unsigned)blocks), dim3(256), 0, as_stream(stream), raw,
-                     valid, n, num_buckets, mode, validate_nonzero, out, error_count);
+                     valid, n, num_buckets, mode, validate_nonzero, out, error_count, mod_magic);
   MDL_CHECK_LAUNCH("bucketize_kernel");
   return MDL_OK;
 }

@@ -72,7 +72,8 @@ def test_bucketize_pre_hashed_bit_exact(device):
 def test_bucketize_mod_bit_exact(device):
     rng = np.random.default_rng(11)
     for n in (1, 5000, 65_537):
-        for rows in (2, 3, 1_000_000, 999_999_937):
+        # divisors m = rows - 1 from 1 to 2^62 (the multiply-high reduction)
+        for rows in (2, 3, 6, 1_000_000, 999_999_937, (1 << 31) + 12, (1 << 40) + 2, (1 << 62) + 1):
             announce("bucketize_mod", n, rows)
             raw = rng.integers(INT64_MIN, INT64_MAX, size=n, dtype=np.int64, endpoint=True)
             raw[: min(n, 3)] = [INT64_MIN, INT64_MAX, 0][: min(n, 3)]
