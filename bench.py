@@ -763,11 +763,12 @@ def main() -> int:
         _, _, pad = wl.seq_len
         nf = len(wl.features)
         d = wl.dims[0]
-        # ids + lengths read, distinct rows, padded window + mask, sort keys/payloads
-        fwd_bytes = float(np.mean([8 * nf * wl.batch * pad + 8 * nf * wl.batch + a["fwd_unique_row_bytes"]
-                                   + nf * wl.batch * pad * (d * esz + 1) + 8 * nf * wl.batch * pad for a in used]))
+        # ids of the valid positions + lengths read, distinct rows, padded
+        # window + mask, sort keys/payloads (packed: one per looked-up id)
+        fwd_bytes = float(np.mean([8 * a["n_ids"] + 8 * nf * wl.batch + a["fwd_unique_row_bytes"]
+                                   + nf * wl.batch * pad * (d * esz + 1) + 8 * a["n_ids"] for a in used]))
         # sorted keys/payloads, gradient rows at valid positions, rows read+written, state
-        apply_bytes = float(np.mean([8 * nf * wl.batch * pad + a["n_ids"] * d * esz
+        apply_bytes = float(np.mean([8 * a["n_ids"] + a["n_ids"] * d * esz
                                      + 2 * a["fwd_unique_row_bytes"] + 8 * a["unique_rows"] for a in used]))
     else:
         fwd_bytes = float(np.mean([16 * a["n_ids"] + 8 * (nb + 1) + a["fwd_unique_row_bytes"]

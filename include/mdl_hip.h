@@ -241,13 +241,21 @@ int mdl_pool_backward(const mdl_feature* feats, int32_t num_features,
  * feature->out is ignored (out is passed here); feature->payload_base and
  * row_base are used when sort_keys is not NULL: for input position (b, k),
  * sort_keys[k + b*in_len] = row_base + id (sentinel when k >= len_b or padding),
- * payload = payload_base + b*out_len + p(k).
+ * payload = payload_base + b*out_len + p(k).  With key_offsets (device int64
+ * [batch + 1], nondecreasing; NULL for the dense layout above) the keys are
+ * packed: position k < cap_b = key_offsets[b+1] - key_offsets[b] (at most
+ * in_len) of row b goes to key_offsets[b] + k and nothing is written past
+ * the cap, so a backward over the key_offsets[batch] packed entries sorts no
+ * padding.  With cap_b = min(len_b, in_len, out_len) every valid position is
+ * kept; a row longer than its cap loses the rest, a shorter one pads its
+ * cap with sentinels.
  */
 int mdl_sequence_forward(const mdl_feature* feature_host, const int64_t* ids,
                          const int64_t* lengths, int64_t batch, int64_t in_len,
                          int64_t out_len, int32_t order, void* out, uint8_t* mask,
                          uint32_t* sort_keys, uint32_t* sort_payload,
-                         uint32_t sentinel, int32_t* error_count, void* stream);
+                         const int64_t* key_offsets, uint32_t sentinel,
+                         int32_t* error_count, void* stream);
 
 /* ---------------------------------------------------------------- sort --- */
 

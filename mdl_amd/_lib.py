@@ -94,7 +94,7 @@ SIGNATURES: dict[str, tuple] = {
     "mdl_table_classes": (_U32, [_P, _I32]),
     "mdl_sequence_forward": (
         _I32,
-        [_P, _P, _P, _I64, _I64, _I64, _I32, _P, _P, _P, _P, _U32, _P, _P],
+        [_P, _P, _P, _I64, _I64, _I64, _I32, _P, _P, _P, _P, _P, _U32, _P, _P],
     ),
     "mdl_sort_workspace_bytes": (_SZ, [_I64]),
     "mdl_sort_pairs": (_I32, [_P, _P, _P, _P, _I64, _I32, _P, _SZ, _P, _P]),

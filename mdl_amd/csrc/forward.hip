@@ -783,6 +783,7 @@ struct SeqArgs {
   uint8_t* mask;
   uint32_t* keys;
   uint32_t* payload;
+  const int64_t* key_offsets;  // packed keys: row b's at [key_offsets[b], key_offsets[b + 1])
   uint32_t sentinel;
   int32_t* error_count;
 };
@@ -918,6 +919,10 @@ __global__ MDL_OCCUPANCY __launch_bounds__(kFwdWaves * kWave) void sequence_kern
 
 // Sort keys/payloads of the input positions (b, k) of a sequence feature; one
 // block per kSeqKeys positions of one row, so the row's length is one load.
+// Dense: position k of row b at b * in_len + k.  Packed (key_offsets): the
+// row's first cap = key_offsets[b + 1] - key_offsets[b] positions (at most
+// in_len) at key_offsets[b] + k, so the sort sees no padding; a row longer
+// than its cap loses the rest, a shorter one fills it with sentinels.
 constexpr int kSeqKeys = 1024;
 
 __global__ __launch_bounds__(256) void sequence_keys_kernel(SeqArgs a) {
@@ -926,15 +931,21 @@ __global__ __launch_bounds__(256) void sequence_keys_kernel(SeqArgs a) {
   const int64_t kb = ((int64_t)blockIdx.x - b * per_row) * kSeqKeys;
   const int64_t len = seq_len(a, b);
   const int64_t start = a.out_len - len;
+  const bool packed = a.key_offsets != nullptr;
+  int64_t base = b * a.in_len, cap = a.in_len;
+  if (packed) {
+    base = a.key_offsets[b];
+    cap = a.key_offsets[b + 1] - base;
+    cap = cap < 0 ? 0 : (cap > a.in_len ? a.in_len : cap);
+  }
   for (int j = threadIdx.x; j < kSeqKeys; j += 256) {
     const int64_t k = kb + j;
-    if (k >= a.in_len) break;
-    const int64_t i = b * a.in_len + k;
-    const int64_t id = a.ids[i];
+    if (k >= cap) break;
+    const int64_t id = a.ids[b * a.in_len + k];
     const bool valid = k < len && (uint64_t)id < (uint64_t)a.f.num_rows && id != a.f.padding_idx;
     const int64_t p = a.order == MDL_SEQ_OLDEST_TO_NEWEST ? start + k : start + (len - 1 - k);
-    a.keys[i] = valid ? (uint32_t)(a.f.row_base + id) : a.sentinel;
-    a.payload[i] = valid ? (uint32_t)(a.f.payload_base + b * a.out_len + p) : 0u;
+    a.keys[base + k] = valid ? (uint32_t)(a.f.row_base + id) : a.sentinel;
+    a.payload[base + k] = valid ? (uint32_t)(a.f.payload_base + b * a.out_len + p) : 0u;
   }
 }
 
@@ -1059,8 +1070,9 @@ int mdl_pool_backward(const mdl_feature* feats, int32_t num_features, const mdl_
 
 int mdl_sequence_forward(const mdl_feature* feature, const int64_t* ids, const int64_t* lengths,
                          int64_t batch, int64_t in_len, int64_t out_len, int32_t order, void* out,
-                         uint8_t* mask, uint32_t* sort_keys, uint32_t* sort_payload, uint32_t sentinel,
-                         int32_t* error_count, void* stream) {
+                         uint8_t* mask, uint32_t* sort_keys, uint32_t* sort_payload,
+                         const int64_t* key_offsets, uint32_t sentinel, int32_t* error_count,
+                         void* stream) {
   if (!feature || batch < 0 || in_len < 0 || out_len < 0)
     return fail(MDL_ERR_INVALID, "mdl_sequence_forward: bad arguments");
   if (order != MDL_SEQ_OLDEST_TO_NEWEST && order != MDL_SEQ_NEWEST_TO_OLDEST)
@@ -1096,6 +1108,7 @@ int mdl_sequence_forward(const mdl_feature* feature, const int64_t* ids, const i
   a.mask = mask;
   a.keys = sort_keys;
   a.payload = sort_payload;
+  a.key_offsets = key_offsets;
   a.sentinel = sentinel;
   a.error_count = error_count;
   hipStream_t s = as_stream(stream);

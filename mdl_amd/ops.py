@@ -1021,7 +1021,7 @@ def sequence_forward(
     check(
         lib().mdl_sequence_forward(
             feat.ctypes.data, ids.data_ptr(), lengths.data_ptr(), batch, in_len, out_len, order_code,
-            out.data_ptr(), mask.data_ptr(), _ptr(keys), _ptr(payload), int(sentinel), _ptr(error_count),
+            out.data_ptr(), mask.data_ptr(), _ptr(keys), _ptr(payload), None, int(sentinel), _ptr(error_count),
             _stream(device),
         ),
         "mdl_sequence_forward",

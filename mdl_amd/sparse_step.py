@@ -218,14 +218,28 @@ class SequenceStep:
         self.error_count = (
             error_count if error_count is not None else torch.zeros(1, dtype=torch.int32, device=self.device)
         )
-        self.n = sum(int(t.numel()) for t in self.ids)
-        self.keys = torch.empty(max(self.n, 1), dtype=torch.int32, device=self.device)
-        self.payload = torch.empty(max(self.n, 1), dtype=torch.int32, device=self.device)
+        # Sort keys are packed: row b of feature f keeps min(len, L_in, L_out)
+        # entries (the positions that reach the window), so the backward
+        # sorts no padding.  The lengths are read once here, like the id
+        # counts of SparseStep: a step object serves one batch layout.
         feats = []
         self.fwd_feats = []
         key_off = 0
         payload_base = 0
         self.key_offsets = []
+        self.row_offsets = []
+        for f, spec in enumerate(plan.features):
+            out = self.outputs[f]
+            L_in = int(self.ids[f].size(1))
+            kept = np.clip(self.lengths[f].cpu().numpy(), 0, min(L_in, int(out.size(1))))
+            offs = np.zeros(kept.size + 1, dtype=np.int64)
+            np.cumsum(kept, out=offs[1:])
+            self.row_offsets.append(ops.upload(offs, self.device))
+            self.key_offsets.append(key_off)
+            key_off += int(offs[-1])
+        self.n = key_off
+        self.keys = torch.empty(max(self.n, 1), dtype=torch.int32, device=self.device)
+        self.payload = torch.empty(max(self.n, 1), dtype=torch.int32, device=self.device)
         for f, spec in enumerate(plan.features):
             table = plan.tables[spec.table]
             out = self.outputs[f]
@@ -237,8 +251,6 @@ class SequenceStep:
             rec["table"] = spec.table
             feats.append(rec)
             self.fwd_feats.append(rec.copy())
-            self.key_offsets.append(key_off)
-            key_off += int(self.ids[f].numel())
             payload_base += int(B) * int(L_out)
         self.feats_bwd = np.concatenate(feats)
         self.tables = ops._tables_array(plan, self.feats_bwd)
@@ -262,8 +274,8 @@ class SequenceStep:
                 lib().mdl_sequence_forward(
                     rec.ctypes.data, ids.data_ptr(), self.lengths[f].data_ptr(), ids.size(0), ids.size(1),
                     out.size(1), self.order, out.data_ptr(), self.masks[f].data_ptr(),
-                    self.keys.data_ptr() + 4 * off, self.payload.data_ptr() + 4 * off, self.plan.sentinel,
-                    self.error_count.data_ptr(), s,
+                    self.keys.data_ptr() + 4 * off, self.payload.data_ptr() + 4 * off,
+                    self.row_offsets[f].data_ptr(), self.plan.sentinel, self.error_count.data_ptr(), s,
                 ),
                 "mdl_sequence_forward",
             )

@@ -639,10 +639,14 @@ def test_sparse_step_slot_buffer_matches_oracle(device):
         assert_close(accs[t].cpu().numpy(), tables[t]["acc"], 1e-5, 1e-7)
 
 
-def test_sequence_step_matches_oracle(device):
+@pytest.mark.parametrize("L_out", [256, 128])
+def test_sequence_step_matches_oracle(device, L_out):
+    """SequenceStep sorts packed keys (only the min(len, L_in, L_out)
+    positions of each row that reach the window); a window shorter than the
+    input clamps the lengths."""
     from mdl_amd.sparse_step import SequenceStep
 
-    announce("sequence_step")
+    announce("sequence_step", L_out)
     rng = np.random.default_rng(81)
     B, L = 64, 256
     rows = [4000, 9000]
@@ -660,24 +664,25 @@ def test_sequence_step_matches_oracle(device):
             m[b, : ln[b]] = rng.zipf(1.05, size=ln[b]) % rows[t]
         ids.append(m)
         lens.append(ln)
-    outs = [torch.empty((B, L, 64), device=device) for _ in range(2)]
-    masks = [torch.empty((B, L), dtype=torch.bool, device=device) for _ in range(2)]
-    grads = [torch.from_numpy(rng.standard_normal((B, L, 64)).astype(np.float32)).to(device) for _ in range(2)]
+    outs = [torch.empty((B, L_out, 64), device=device) for _ in range(2)]
+    masks = [torch.empty((B, L_out), dtype=torch.bool, device=device) for _ in range(2)]
+    grads = [torch.from_numpy(rng.standard_normal((B, L_out, 64)).astype(np.float32)).to(device) for _ in range(2)]
     st = SequenceStep(plan, [torch.from_numpy(m).to(device) for m in ids],
                       [torch.from_numpy(ln).to(device) for ln in lens], outs, masks, grads)
+    assert st.n == sum(int(np.minimum(ln, L_out).sum()) for ln in lens)
     st.step(0.03, 1e-8)
     for t in range(2):
-        ref, rmask = O.sequence_gather(W[t], ids[t], lens[t], L)
+        ref, rmask = O.sequence_gather(W[t], ids[t], lens[t], L_out)
         assert np.array_equal(outs[t].cpu().numpy(), ref.astype(np.float32))
         assert np.array_equal(masks[t].cpu().numpy(), rmask)
         g = grads[t].cpu().numpy()
         r, v = [], []
         for b in range(B):
-            n = int(lens[t][b])
+            n = int(min(lens[t][b], L_out))
             for k in range(n):
                 if ids[t][b, k] != 0:
                     r.append(ids[t][b, k])
-                    v.append(g[b, L - n + k])
+                    v.append(g[b, L_out - n + k])
         rr, vv = O.coalesce(np.array(r), np.array(v, dtype=np.float64))
         wexp, aexp = O.rowwise_adagrad(W[t], np.zeros(rows[t], np.float32), rr, vv, 0.03, 1e-8)
         assert_close(tabs[t].cpu().numpy(), wexp, 1e-5, 1e-6)
