@@ -345,10 +345,18 @@ class DeviceStep:
             self.steps.append(SparseStep(self.plan, packed, lens, id_counts, bag_counts, out_views, grad_views,
                                          error_count=self.err))
 
+    def capture(self):
+        for st in self.steps:
+            st.capture(self.wl.lr, self.wl.eps)
+        self.graphs = True
+
     def step(self, i: int, timers=None):
         st = self.steps[i % len(self.steps)]
         if timers is None:
-            st.step(self.wl.lr, self.wl.eps)
+            if getattr(self, "graphs", False):
+                st.replay()
+            else:
+                st.step(self.wl.lr, self.wl.eps)
             return
         timers["forward"].start()
         st.forward()
@@ -399,10 +407,18 @@ class SequenceDeviceStep:
             self.steps.append(SequenceStep(self.plan, dids, dlen, self.outs, self.masks, self.grads,
                                            error_count=self.err))
 
+    def capture(self):
+        for st in self.steps:
+            st.capture(self.wl.lr, self.wl.eps)
+        self.graphs = True
+
     def step(self, i: int, timers=None):
         st = self.steps[i % len(self.steps)]
         if timers is None:
-            st.step(self.wl.lr, self.wl.eps)
+            if getattr(self, "graphs", False):
+                st.replay()
+            else:
+                st.step(self.wl.lr, self.wl.eps)
             return
         timers["forward"].start()
         st.forward()
@@ -675,6 +691,9 @@ def main() -> int:
     ap.add_argument("--config", default="c1", choices=sorted(WORKLOADS))
     ap.add_argument("--batches", type=int, default=3, help="distinct synthetic batches cycled through")
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--graph", action="store_true",
+                    help="replay one HIP graph per batch instead of launching each step's kernels from the host "
+                         "(measured: no faster at c0, c1 or c4 -- the host keeps ahead of the GPU)")
     ap.add_argument("--no-aux", action="store_true",
                     help="skip the clipped-step and bucketing measurements (off with --calibrate-copy)")
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
@@ -736,6 +755,14 @@ def main() -> int:
     for i in range(args.warmup):
         dev.step(i)
     torch.cuda.synchronize()
+    if args.graph:
+        # each batch's step as one HIP graph (recorded after the eager warmup
+        # steps loaded the kernels); the timed steps replay them
+        dev.capture()
+        torch.cuda.synchronize()
+        for i in range(len(dev.steps)):
+            dev.step(args.warmup + i)
+        torch.cuda.synchronize()
     if int(dev.err.item()):
         raise RuntimeError("synthetic ids out of range")
     torch.cuda.synchronize()
@@ -811,6 +838,7 @@ def main() -> int:
             "ids_per_step": n_ids,
             "distinct_rows_per_step": float(np.mean([a["unique_rows"] for a in used])),
             "parallelism": "single GPU",
+            "launch": "one HIP graph per batch (captured step)" if args.graph else "eager",
         },
         "hbm_gbps_achieved": gbps,
         "roofline_fraction_step": gbps / PEAK_HBM_GBPS,

@@ -25,6 +25,18 @@ from . import ops
 from ._lib import CHUNK_DTYPE, MDL_POOL_NONE, check, lib
 
 
+def _capture(device: torch.device, fn) -> "torch.cuda.CUDAGraph":
+    """fn's launches recorded on a side stream of default priority."""
+
+    graph = torch.cuda.CUDAGraph()
+    side = torch.cuda.Stream(device=device)
+    side.wait_stream(torch.cuda.current_stream(device))
+    with torch.cuda.graph(graph, stream=side):
+        fn()
+    torch.cuda.current_stream(device).wait_stream(side)
+    return graph
+
+
 class SparseStep:
     def __init__(
         self,
@@ -181,6 +193,18 @@ class SparseStep:
             _, coef = self.clip(clip_norm)
             self.apply(lr, eps, coef)
 
+    def capture(self, lr: float, eps: float, clip_norm: float | None = None) -> None:
+        """Record step(lr, eps, clip_norm) as one HIP graph; replay() then
+        issues every launch of the step at once (the host no longer paces
+        short steps).  Nothing runs while recording; the step's buffers are
+        its own, so a new batch of the same layout is copied into them before
+        a replay.  Call it after one eager step, which loads the kernels."""
+
+        self._graph = _capture(self.device, lambda: self.step(lr, eps, clip_norm))
+
+    def replay(self) -> None:
+        self._graph.replay()
+
 
 class SequenceStep:
     """Fused step over sequence features (long user-behaviour histories).
@@ -300,6 +324,14 @@ class SequenceStep:
             ),
             "mdl_backward_apply",
         )
+
+    def capture(self, lr: float, eps: float) -> None:
+        """One HIP graph of step(lr, eps); see SparseStep.capture."""
+
+        self._graph = _capture(self.device, lambda: self.step(lr, eps))
+
+    def replay(self) -> None:
+        self._graph.replay()
 
     def step(self, lr: float, eps: float) -> None:
         self.forward()

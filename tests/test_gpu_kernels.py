@@ -687,3 +687,55 @@ def test_sequence_step_matches_oracle(device, L_out):
         wexp, aexp = O.rowwise_adagrad(W[t], np.zeros(rows[t], np.float32), rr, vv, 0.03, 1e-8)
         assert_close(tabs[t].cpu().numpy(), wexp, 1e-5, 1e-6)
         assert_close(accs[t].cpu().numpy(), aexp, 1e-5, 1e-7)
+
+
+# ---------------------------------------------------------------- graphs --
+
+
+def _slot_step(device, seed):
+    """A fixed-layout SparseStep (two tables, a mean-pooled bag feature and a
+    single-valued one, outputs in one [B, sum(dim)] slot buffer)."""
+    from mdl_amd.sparse_step import SparseStep
+
+    rng = np.random.default_rng(seed)
+    B = 512
+    rows, dims = [3000, 20000], [32, 16]
+    tabs = [_table(rng, r, d, torch.float32, device) for r, d in zip(rows, dims)]
+    states = [torch.zeros(r, device=device) for r in rows]
+    plan = ops.GroupPlan()
+    plan.add_feature(tabs[0], pooling="mean", null_policy="exclude", state=states[0])
+    plan.add_feature(tabs[1], pooling="none", state=states[1])
+    ln = rng.integers(0, 20, size=B)
+    bag = rng.zipf(1.2, size=int(ln.sum())) % rows[0]
+    single = rng.zipf(1.2, size=B) % rows[1]
+    packed = torch.from_numpy(np.concatenate([bag, single]).astype(np.int64)).to(device)
+    lens = torch.from_numpy(np.concatenate([ln, [B]]).astype(np.int64)).to(device)
+    out = torch.empty((B, sum(dims)), device=device)
+    grad = torch.from_numpy(rng.standard_normal((B, sum(dims))).astype(np.float32)).to(device)
+    views = [slice(0, dims[0]), slice(dims[0], sum(dims))]
+    st = SparseStep(plan, packed, lens, [bag.size, B], [B, 0], [out[:, v] for v in views],
+                    [grad[:, v] for v in views])
+    return st, tabs, states, out
+
+
+@pytest.mark.parametrize("clip", [None, 0.5])
+def test_sparse_step_graph_replays_match_eager(device, clip):
+    """Every replay of a captured step equals an eager step bit for bit, with
+    eager work and synchronisations between the replays (the step records no
+    memset: its counters and flags are written by kernels)."""
+    announce("graph_replay", clip)
+    eager, tabs_e, states_e, out_e = _slot_step(device, 92)
+    graph, tabs_g, states_g, out_g = _slot_step(device, 92)
+    lr, eps = 0.05, 1e-8
+    eager.step(lr, eps, clip)
+    graph.step(lr, eps, clip)  # loads the kernels before the recording
+    graph.capture(lr, eps, clip)
+    for r in range(4):
+        eager.step(lr, eps, clip)
+        graph.replay()
+        torch.cuda.synchronize()
+        _ = float((tabs_g[0].double() * 2).sum())  # eager work between replays
+        assert torch.equal(out_g, out_e), f"replay {r}: outputs"
+        for t in range(2):
+            assert torch.equal(tabs_g[t], tabs_e[t]), f"replay {r}: table {t}"
+            assert torch.equal(states_g[t], states_e[t]), f"replay {r}: state {t}"
