@@ -18,8 +18,15 @@ namespace mdl {
 
 constexpr int kSortThreads = 256;
 constexpr int kSortWaves = kSortThreads / kWave;
-constexpr int kSortItems = 16;
-constexpr int kSortTile = kSortThreads * kSortItems;
+// Keys per thread: 16 (4096-entry tiles) when that still gives a few blocks
+// per CU, else 8 or 4, so a small sort (c0, c4: ~0.5 M keys) still spreads
+// over every CU.
+constexpr int kMinTiles = 512;
+static inline int sort_items(int64_t n) {
+  for (int items = 16; items > 4; items >>= 1)
+    if ((n + kSortThreads * items - 1) / (kSortThreads * items) >= kMinTiles) return items;
+  return 4;
+}
 constexpr int kDigitBits = 8;
 constexpr int kRadix = 1 << kDigitBits;
 
@@ -43,6 +50,7 @@ __device__ __forceinline__ uint32_t block_exclusive_scan_u32(uint32_t v, uint32_
   return before + x - v;
 }
 
+template <int kSortItems>
 __global__ __launch_bounds__(kSortThreads) void radix_upsweep(const uint32_t* __restrict__ keys, int64_t n,
                                                               int shift, uint32_t mask,
                                                               uint32_t* __restrict__ counts, int ntiles) {
@@ -54,6 +62,7 @@ __global__ __launch_bounds__(kSortThreads) void radix_upsweep(const uint32_t* __
   // (its counts column here, its digit runs in the downsweep) meet their
   // neighbours in that XCD's L2 before they are written back.
   const int tile = (int)xcd_block(blockIdx.x, ntiles);
+  constexpr int kSortTile = kSortThreads * kSortItems;
   const int64_t base = (int64_t)tile * kSortTile;
   uint32_t k[kSortItems];
 #pragma unroll
@@ -122,10 +131,12 @@ __global__ __launch_bounds__(kSortThreads) void radix_scan(uint32_t* __restrict_
   if (threadIdx.x == 0) digit_total[blockIdx.x] = carry;
 }
 
+template <int kSortItems>
 __global__ __launch_bounds__(kSortThreads) __attribute__((amdgpu_waves_per_eu(4))) void radix_downsweep(
     const uint32_t* __restrict__ keys_in, const uint32_t* __restrict__ vals_in,
     uint32_t* __restrict__ keys_out, uint32_t* __restrict__ vals_out, int64_t n, int shift, int bits,
     const uint32_t* __restrict__ counts, const uint32_t* __restrict__ digit_total, int ntiles) {
+  constexpr int kSortTile = kSortThreads * kSortItems;
   __shared__ uint32_t s_keys[kSortTile];
   __shared__ uint32_t s_vals[kSortTile];
   __shared__ uint32_t s_wh[kSortWaves][kRadix];
@@ -232,8 +243,20 @@ __global__ __launch_bounds__(kSortThreads) __attribute__((amdgpu_waves_per_eu(4)
 int sort_pass_count(int key_bits) { return key_bits > 0 ? (key_bits + kDigitBits - 1) / kDigitBits : 0; }
 
 size_t sort_ws_bytes(int64_t n) {
-  const int64_t ntiles = (n + kSortTile - 1) / kSortTile;
+  const int64_t tile = (int64_t)kSortThreads * sort_items(n);
+  const int64_t ntiles = (n + tile - 1) / tile;
   return (size_t)(kRadix * (ntiles > 0 ? ntiles : 1) + kRadix) * sizeof(uint32_t) + 256;
+}
+
+template <int kSortItems>
+static void radix_pass(const uint32_t* ki, const uint32_t* vi, uint32_t* ko, uint32_t* vo, int64_t n, int shift,
+                       int bits, uint32_t* counts, uint32_t* digit_total, int ntiles, hipStream_t s) {
+  const uint32_t mask = (1u << bits) - 1u;
+  hipLaunchKernelGGL(radix_upsweep<kSortItems>, dim3(ntiles), dim3(kSortThreads), 0, s, ki, n, shift, mask,
+                     counts, ntiles);
+  hipLaunchKernelGGL(radix_scan, dim3(kRadix), dim3(kSortThreads), 0, s, counts, ntiles, digit_total);
+  hipLaunchKernelGGL(radix_downsweep<kSortItems>, dim3(ntiles), dim3(kSortThreads), 0, s, ki, vi, ko, vo, n,
+                     shift, bits, counts, digit_total, ntiles);
 }
 
 int sort_pairs(uint32_t* keys, uint32_t* vals, uint32_t* keys_alt, uint32_t* vals_alt, int64_t n,
@@ -243,7 +266,8 @@ int sort_pairs(uint32_t* keys, uint32_t* vals, uint32_t* keys_alt, uint32_t* val
   if (n > 0xffffffffll) return fail(MDL_ERR_UNSUPPORTED, "radix sort: more than 2^32-1 keys");
   if (key_bits > 32) return fail(MDL_ERR_INVALID, "radix sort: key_bits > 32");
   if (ws_bytes < sort_ws_bytes(n)) return fail(MDL_ERR_WORKSPACE, "radix sort: workspace too small");
-  const int ntiles = (int)((n + kSortTile - 1) / kSortTile);
+  const int items = sort_items(n);
+  const int ntiles = (int)((n + (int64_t)kSortThreads * items - 1) / ((int64_t)kSortThreads * items));
   uint32_t* counts = static_cast<uint32_t*>(ws);
   uint32_t* digit_total = counts + (size_t)kRadix * ntiles;
   uint32_t* ki = keys;
@@ -253,15 +277,10 @@ int sort_pairs(uint32_t* keys, uint32_t* vals, uint32_t* keys_alt, uint32_t* val
   int passes = 0;
   for (int shift = 0; shift < key_bits; shift += kDigitBits) {
     const int bits = key_bits - shift < kDigitBits ? key_bits - shift : kDigitBits;
-    const uint32_t mask = (1u << bits) - 1u;
-    hipLaunchKernelGGL(radix_upsweep, dim3(ntiles), dim3(kSortThreads), 0, s, ki, n, shift, mask, counts,
-                       ntiles);
-    MDL_CHECK_LAUNCH("radix_upsweep");
-    hipLaunchKernelGGL(radix_scan, dim3(kRadix), dim3(kSortThreads), 0, s, counts, ntiles, digit_total);
-    MDL_CHECK_LAUNCH("radix_scan");
-    hipLaunchKernelGGL(radix_downsweep, dim3(ntiles), dim3(kSortThreads), 0, s, ki, vi, ko, vo, n, shift,
-                       bits, counts, digit_total, ntiles);
-    MDL_CHECK_LAUNCH("radix_downsweep");
+    if (items == 16) radix_pass<16>(ki, vi, ko, vo, n, shift, bits, counts, digit_total, ntiles, s);
+    else if (items == 8) radix_pass<8>(ki, vi, ko, vo, n, shift, bits, counts, digit_total, ntiles, s);
+    else radix_pass<4>(ki, vi, ko, vo, n, shift, bits, counts, digit_total, ntiles, s);
+    MDL_CHECK_LAUNCH("radix pass");
     uint32_t* t;
     t = ki; ki = ko; ko = t;
     t = vi; vi = vo; vo = t;

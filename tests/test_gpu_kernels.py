@@ -97,12 +97,14 @@ def test_lengths_to_offsets_bit_exact(device):
 
 @pytest.mark.parametrize("bits", [1, 7, 8, 13, 24, 25, 27, 30, 31, 32])
 def test_radix_sort_is_stable_and_exact(device, bits):
-    """Every key width takes 8-bit passes over 4096-entry tiles; the sizes
-    straddle whole tiles and partial last tiles."""
+    """Every key width takes 8-bit passes; tiles hold 256 threads x 4, 8 or 16
+    keys (16 from about 2.1 M keys, so at least 512 tiles), and the sizes
+    straddle whole tiles and partial last tiles of each."""
 
     rng = np.random.default_rng(13 + bits)
     lib = _lib.lib()
-    for n in (1, 100, 4096, 4097, 8193, 16384, 16385, 300_001, 2_000_003 if bits in (24, 31) else 20_000):
+    big = (2_000_003, 4_500_001) if bits in (24, 31) else (20_000,)
+    for n in (1, 100, 1024, 1025, 4096, 4097, 8193, 16384, 16385, 300_001) + big:
         announce("sort_pairs", n, bits)
         hi = (1 << bits) - 1
         keys = rng.integers(0, hi, size=n, dtype=np.uint64, endpoint=True)
