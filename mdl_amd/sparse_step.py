@@ -73,13 +73,13 @@ class SparseStep:
         out_ptrs = [o.data_ptr() for o in outputs]
         out_strides = [o.stride(0) if o.ndim == 2 else int(o.size(-1)) for o in outputs]
         self.feats_fwd = ops.build_features(plan, id_counts, bag_counts, out_ptrs, out_strides)
-        n_chunks = lib().mdl_plan_chunks(self.feats_fwd.ctypes.data, len(self.feats_fwd),
-                                         ops.FORWARD_TARGET_IDS, None, 0)
+        target = ops.forward_target_ids(self.feats_fwd)
+        n_chunks = lib().mdl_plan_chunks(self.feats_fwd.ctypes.data, len(self.feats_fwd), target, None, 0)
         if n_chunks < 0:
             check(int(n_chunks), "mdl_plan_chunks")
         chunks = np.zeros(max(n_chunks, 1), dtype=CHUNK_DTYPE)
-        lib().mdl_plan_chunks(self.feats_fwd.ctypes.data, len(self.feats_fwd), ops.FORWARD_TARGET_IDS,
-                              chunks.ctypes.data, n_chunks)
+        lib().mdl_plan_chunks(self.feats_fwd.ctypes.data, len(self.feats_fwd), target, chunks.ctypes.data,
+                              n_chunks)
         self.n_chunks = int(n_chunks)
         res = ops.ForwardResult(
             plan=plan, device=self.device, ids=self.ids, offsets=None, outputs=list(outputs),
