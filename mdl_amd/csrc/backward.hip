@@ -9,7 +9,7 @@
 // class x lane width) are contiguous and each table's chunks consecutive.
 //
 // One wavefront reduces one chunk.  Its G = 64/L lane groups ("slots", L
-// lanes per row) each walk a contiguous slice of about kSlotRun entries,
+// lanes per row) each walk a contiguous slice of about kSlotRun (48) entries (fewer in a small call),
 // accumulating the per-id gradients in registers: the gradient rows of the
 // slice are the only per-entry work, and a run that ends inside the slot that
 // began it is finished right there -- its summed gradient goes straight into
@@ -67,10 +67,19 @@ struct BwdWs {
   float* chunk_ss;        // [max_chunks] squared norms of the runs finished per chunk
 };
 
-// A chunk holds at least kSlotRun entries unless it is its table's last, so
-// a table of m entries has at most ceil(m / kSlotRun) chunks.
+// Entries one slot walks in a full chunk: kSlotRun for a big call; a small
+// one takes shorter slices (down to 16) so that its chunks -- one wave each
+// -- still give every SIMD a few (about 4096 chunks of 8 slots).
+static inline int slot_run_for(int64_t n) {
+  const int64_t r = n / 32768;
+  return (int)(r < 16 ? 16 : (r > kSlotRun ? kSlotRun : r));
+}
+
+// A chunk holds at least slot_run entries unless it is its table's last, so
+// a table of m entries has at most ceil(m / slot_run) chunks.
 static inline int64_t max_chunks_for(int64_t n, int32_t T) {
-  return (n + kSlotRun - 1) / kSlotRun + T + 1;
+  const int64_t r = slot_run_for(n);
+  return (n + r - 1) / r + T + 1;
 }
 
 static size_t carve(BwdWs* w, void* base, int64_t n, int32_t T, int32_t max_dim) {
@@ -118,11 +127,11 @@ __device__ __forceinline__ int table_variant(const mdl_table& tb) {
   return variant_of(tb.wdtype, tb.gdtype, table_vec(tb), tb.dim);
 }
 
-// Entries per chunk of a table: kSlotRun per slot, one slot per L lanes.
-__device__ __forceinline__ int64_t table_chunk_len(const mdl_table& tb) {
+// Entries per chunk of a table: slot_run per slot, one slot per L lanes.
+__device__ __forceinline__ int64_t table_chunk_len(const mdl_table& tb, int slot_run) {
   const int c = variant_elems(table_variant(tb));
   const int64_t g = kWave / lanes_for(tb.dim > 0 ? tb.dim : 1, c);
-  const int64_t cb = (int64_t)kSlotRun * g;
+  const int64_t cb = (int64_t)slot_run * g;
   return cb < kChunkMax ? cb : kChunkMax;
 }
 
@@ -169,13 +178,14 @@ __global__ __launch_bounds__(256) void bwd_desc_kernel(const mdl_table* __restri
                                                        const int64_t* __restrict__ table_end,
                                                        int64_t* __restrict__ chunk_base,
                                                        int64_t* __restrict__ total,
-                                                       ChunkDesc* __restrict__ desc, int64_t max_chunks) {
+                                                       ChunkDesc* __restrict__ desc, int64_t max_chunks,
+                                                       int slot_run) {
   __shared__ int64_t s_part[256 / kWave];
   const int32_t t = blockIdx.x;
   const int lane = lane_id(), w = threadIdx.x / kWave;
   int64_t before = 0;
   for (int32_t q = threadIdx.x; q < t; q += blockDim.x) {
-    const int64_t cq = table_chunk_len(tables[q]);
+    const int64_t cq = table_chunk_len(tables[q], slot_run);
     const int64_t sq = table_start[q], eq = table_end[q];
     before += ((eq > sq ? eq : sq) - sq + cq - 1) / cq;
   }
@@ -190,7 +200,7 @@ __global__ __launch_bounds__(256) void bwd_desc_kernel(const mdl_table* __restri
   for (int q = 0; q < 256 / kWave; ++q) base += s_part[q];
   const int64_t lo = table_start[t], hi_raw = table_end[t];
   const int64_t hi = hi_raw > lo ? hi_raw : lo;
-  const int64_t cb = table_chunk_len(tables[t]);
+  const int64_t cb = table_chunk_len(tables[t], slot_run);
   const int64_t room = max_chunks - base;
   const int64_t nch_all = (hi - lo + cb - 1) / cb;
   const int64_t nch = nch_all < room ? nch_all : (room > 0 ? room : 0);
@@ -232,10 +242,11 @@ __global__ __launch_bounds__(256) void count_heads_kernel(const int64_t* __restr
 
 __global__ void unique_range_end_kernel(int32_t T, const int64_t* table_start, const int64_t* table_end,
                                         const int64_t* chunk_base, const int64_t* head_base,
-                                        const mdl_table* __restrict__ tables, int64_t* unique_range) {
+                                        const mdl_table* __restrict__ tables, int64_t* unique_range,
+                                        int slot_run) {
   for (int32_t t = blockIdx.x * blockDim.x + threadIdx.x; t < T; t += gridDim.x * blockDim.x) {
     const int64_t lo = table_start[t], hi = table_end[t];
-    const int64_t cb = table_chunk_len(tables[t]);
+    const int64_t cb = table_chunk_len(tables[t], slot_run);
     const int64_t nch = (hi - lo + cb - 1) / cb;
     unique_range[2 * t] = head_base[chunk_base[t]];
     unique_range[2 * t + 1] = head_base[chunk_base[t] + nch];
@@ -754,7 +765,7 @@ static int plan(const mdl_table* tables, int32_t T, const uint32_t* sk, int64_t 
                      w.table_start, w.table_end);
   MDL_CHECK_LAUNCH("bwd_bounds_kernel");
   hipLaunchKernelGGL(bwd_desc_kernel, dim3((unsigned)T), dim3(256), 0, s, tables, T, w.table_start, w.table_end,
-                     w.chunk_base, w.num_chunks, w.desc, max_chunks_for(n, T));
+                     w.chunk_base, w.num_chunks, w.desc, max_chunks_for(n, T), slot_run_for(n));
   MDL_CHECK_LAUNCH("bwd_desc_kernel");
   return MDL_OK;
 }
@@ -975,7 +986,8 @@ int mdl_backward_count(const mdl_table* tables, int32_t num_tables, int32_t max_
   rc = mdl_lengths_to_offsets(heads, mc, w.head_base, w.scan_ws, w.scan_bytes, stream);
   if (rc) return rc;
   hipLaunchKernelGGL(unique_range_end_kernel, dim3((unsigned)((num_tables + 255) / 256)), dim3(256), 0, s,
-                     num_tables, w.table_start, w.table_end, w.chunk_base, w.head_base, tables, unique_range);
+                     num_tables, w.table_start, w.table_end, w.chunk_base, w.head_base, tables, unique_range,
+                     slot_run_for(n));
   MDL_CHECK_LAUNCH("unique_range_end_kernel");
   return MDL_OK;
 }

@@ -408,6 +408,40 @@ def test_fused_backward_adagrad_matches_oracle(device, hot, dtype):
         assert np.array_equal(to_np(tabs[t])[untouched], w0[t][untouched])
 
 
+def test_fused_backward_large_call_matches_oracle(device):
+    """A call of 1.9 M ids: slots walk 48 entries per chunk (smaller calls,
+    as in the other tests, take shorter slices)."""
+
+    rng = np.random.default_rng(45)
+    announce("fused_backward_large")
+    rows, dims = [200_000, 50_000], [16, 64]
+    tabs = [_table(rng, r, d, torch.float32, device) for r, d in zip(rows, dims)]
+    states = [torch.from_numpy(rng.random(r).astype(np.float32)).to(device) for r in rows]
+    plan = ops.GroupPlan()
+    ids, lens, meta = [], [], []
+    for t, mode, B in ((0, "mean", 60_000), (1, "sum", 35_000)):
+        plan.add_feature(tabs[t], pooling=mode, null_policy="exclude", state=states[t])
+        ln = rng.integers(0, 41, size=B)
+        x = rng.zipf(1.1, size=int(ln.sum())) % rows[t]
+        ids.append(torch.from_numpy(x.astype(np.int64)).to(device))
+        lens.append(torch.from_numpy(ln).to(device))
+        meta.append((t, mode, x, ln))
+    assert sum(m[2].size for m in meta) > 48 * 32768
+    w0 = [to_np(t).copy() for t in tabs]
+    a0 = [s.cpu().numpy().copy() for s in states]
+    res = ops.grouped_forward(plan, ids, lens, with_backward=True)
+    grads = [torch.from_numpy(rng.standard_normal(tuple(o.shape)).astype(np.float32)).to(device)
+             for o in res.outputs]
+    lr, eps = 0.01, 1e-8
+    ops.backward_adagrad(res, grads, lr=lr, eps=eps)
+    for f, (t, mode, x, ln) in enumerate(meta):
+        r, v = O.per_id_grads(x, ln, to_np(grads[f]).reshape(-1, dims[t]), mode, "exclude")
+        rr, vv = O.coalesce(r, v)
+        wexp, aexp = O.rowwise_adagrad(w0[t], a0[t], rr, vv, lr, eps)
+        assert_close(states[t].cpu().numpy(), aexp, 1e-5, 1e-7)
+        assert_close(to_np(tabs[t]), wexp, 1e-5, 1e-6)
+
+
 def test_fused_backward_is_deterministic(device):
     announce("determinism")
     results = []
