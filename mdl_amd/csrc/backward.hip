@@ -76,10 +76,14 @@ static inline int slot_run_for(int64_t n) {
 }
 
 // A chunk holds at least slot_run entries unless it is its table's last, so
-// a table of m entries has at most ceil(m / slot_run) chunks.
+// a call of n entries has at most ceil(n / slot_run) + T chunks.  That count
+// wobbles between 32 K and 34 K chunks while slot_run grows with n; the bound
+// below covers it and never decreases with n, so a workspace sized for the
+// largest call serves every smaller one.
 static inline int64_t max_chunks_for(int64_t n, int32_t T) {
-  const int64_t r = slot_run_for(n);
-  return (n + r - 1) / r + T + 1;
+  const int64_t small = 16ll * 32768;
+  const int64_t c = n <= small ? (n + 15) / 16 : ((n + 47) / 48 > 34816 ? (n + 47) / 48 : 34816);
+  return c + T + 1;
 }
 
 static size_t carve(BwdWs* w, void* base, int64_t n, int32_t T, int32_t max_dim) {

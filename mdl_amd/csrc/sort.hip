@@ -247,8 +247,11 @@ __global__ __launch_bounds__(kSortThreads) __attribute__((amdgpu_waves_per_eu(4)
 // the alternate buffers when it is odd.
 int sort_pass_count(int key_bits) { return key_bits > 0 ? (key_bits + kDigitBits - 1) / kDigitBits : 0; }
 
+// Sized for the smallest tiles (4 keys per thread), so the size never
+// decreases with n and a workspace for the largest call serves every smaller
+// one.
 size_t sort_ws_bytes(int64_t n) {
-  const int64_t tile = (int64_t)kSortThreads * sort_items(n);
+  const int64_t tile = (int64_t)kSortThreads * 4;
   const int64_t ntiles = (n + tile - 1) / tile;
   return (size_t)(kRadix * (ntiles > 0 ? ntiles : 1) + kRadix) * sizeof(uint32_t) + 256;
 }

@@ -97,7 +97,21 @@ def test_invalid_arguments_fail_before_any_launch():
 
 
 def test_workspace_queries_are_monotone():
+    """A workspace sized for the largest call serves every smaller one, also
+    across the sizes where the sort tiles and the backward chunks change
+    (about 0.5 M to 2.2 M entries)."""
+
     lib = _lib.lib()
+    prev = (0, 0, 0)
+    for n in range(0, 3_000_000, 4099):
+        cur = (lib.mdl_backward_workspace_bytes(n, 8, 64), lib.mdl_sort_workspace_bytes(n),
+               lib.mdl_unique_workspace_bytes(n))
+        assert all(c >= p for c, p in zip(cur, prev)), n
+        prev = cur
+    for n in (524_287, 557_055, 1_048_575, 1_572_863, 2_097_151):  # where tiles and chunks change
+        for f in (lambda m: lib.mdl_backward_workspace_bytes(m, 8, 64), lib.mdl_sort_workspace_bytes,
+                  lib.mdl_unique_workspace_bytes):
+            assert f(n) <= f(n + 1) <= f(n + 4096), n
     a = lib.mdl_backward_workspace_bytes(1000, 4, 64)
     b = lib.mdl_backward_workspace_bytes(100000, 4, 64)
     c = lib.mdl_backward_workspace_bytes(100000, 200, 128)
