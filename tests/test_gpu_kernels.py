@@ -677,19 +677,22 @@ def test_sparse_step_slot_buffer_matches_oracle(device):
         assert_close(accs[t].cpu().numpy(), tables[t]["acc"], 1e-5, 1e-7)
 
 
-@pytest.mark.parametrize("L_out", [256, 128])
-def test_sequence_step_matches_oracle(device, L_out):
+@pytest.mark.parametrize("L_out,order,dtype", [(256, "oldest_to_newest", torch.float32),
+                                               (128, "oldest_to_newest", torch.float32),
+                                               (256, "newest_to_oldest", torch.float32),
+                                               (128, "newest_to_oldest", torch.bfloat16)])
+def test_sequence_step_matches_oracle(device, L_out, order, dtype):
     """SequenceStep sorts packed keys (only the min(len, L_in, L_out)
     positions of each row that reach the window); a window shorter than the
-    input clamps the lengths."""
+    input clamps the lengths, and newest-first rows reverse the positions."""
     from mdl_amd.sparse_step import SequenceStep
 
-    announce("sequence_step", L_out)
+    announce("sequence_step", L_out, order, dtype)
     rng = np.random.default_rng(81)
     B, L = 64, 256
     rows = [4000, 9000]
-    W = [rng.standard_normal((r, 64)).astype(np.float32) for r in rows]
-    tabs = [torch.from_numpy(w.copy()).to(device) for w in W]
+    tabs = [_table(rng, r, 64, dtype, device) for r in rows]
+    W = [to_np(t).copy() for t in tabs]
     accs = [torch.zeros(r, device=device) for r in rows]
     plan = ops.GroupPlan()
     for t in range(2):
@@ -702,28 +705,31 @@ def test_sequence_step_matches_oracle(device, L_out):
             m[b, : ln[b]] = rng.zipf(1.05, size=ln[b]) % rows[t]
         ids.append(m)
         lens.append(ln)
-    outs = [torch.empty((B, L_out, 64), device=device) for _ in range(2)]
+    outs = [torch.empty((B, L_out, 64), dtype=dtype, device=device) for _ in range(2)]
     masks = [torch.empty((B, L_out), dtype=torch.bool, device=device) for _ in range(2)]
-    grads = [torch.from_numpy(rng.standard_normal((B, L_out, 64)).astype(np.float32)).to(device) for _ in range(2)]
+    grads = [torch.from_numpy(rng.standard_normal((B, L_out, 64)).astype(np.float32)).to(dtype).to(device)
+             for _ in range(2)]
     st = SequenceStep(plan, [torch.from_numpy(m).to(device) for m in ids],
-                      [torch.from_numpy(ln).to(device) for ln in lens], outs, masks, grads)
+                      [torch.from_numpy(ln).to(device) for ln in lens], outs, masks, grads, order=order)
     assert st.n == sum(int(np.minimum(ln, L_out).sum()) for ln in lens)
     st.step(0.03, 1e-8)
+    bf16 = dtype == torch.bfloat16
     for t in range(2):
-        ref, rmask = O.sequence_gather(W[t], ids[t], lens[t], L_out)
-        assert np.array_equal(outs[t].cpu().numpy(), ref.astype(np.float32))
+        ref, rmask = O.sequence_gather(W[t], ids[t], lens[t], L_out, order)
+        assert np.array_equal(to_np(outs[t]), ref.astype(np.float32))
         assert np.array_equal(masks[t].cpu().numpy(), rmask)
-        g = grads[t].cpu().numpy()
+        g = to_np(grads[t])
         r, v = [], []
         for b in range(B):
             n = int(min(lens[t][b], L_out))
             for k in range(n):
                 if ids[t][b, k] != 0:
+                    p = L_out - n + k if order == "oldest_to_newest" else L_out - 1 - k
                     r.append(ids[t][b, k])
-                    v.append(g[b, L_out - n + k])
+                    v.append(g[b, p])
         rr, vv = O.coalesce(np.array(r), np.array(v, dtype=np.float64))
-        wexp, aexp = O.rowwise_adagrad(W[t], np.zeros(rows[t], np.float32), rr, vv, 0.03, 1e-8)
-        assert_close(tabs[t].cpu().numpy(), wexp, 1e-5, 1e-6)
+        wexp, aexp = O.rowwise_adagrad(W[t], np.zeros(rows[t], np.float32), rr, vv, 0.03, 1e-8, is_bf16=bf16)
+        assert_close(to_np(tabs[t]), wexp, RTOL[dtype], 1e-2 if bf16 else 1e-6)
         assert_close(accs[t].cpu().numpy(), aexp, 1e-5, 1e-7)
 
 
