@@ -468,6 +468,7 @@ def aux_measurements(torch, dev, wl, n_ids: float, steps: int, device) -> dict:
       the coalesced gradient, clip coefficient, apply scaled by it --
       src/train.py:5788-5826), wall clock over ``steps`` steps like the
       headline;
+    * the stand-alone row-wise Adagrad update on 1 M unique rows;
     * device bucketing (mdl_bucketize, src/features.py:360-376 and
       src/benchmark.py:1246-1250) of one step's worth of raw int64 ids, HIP
       events around 20 back-to-back launches queued behind a spin kernel, so
@@ -512,6 +513,34 @@ def aux_measurements(torch, dev, wl, n_ids: float, steps: int, device) -> dict:
             "achieved_gbps": nbytes / (ms * 1e-3) / 1e9, "frac": nbytes / (ms * 1e-3) / 1e9 / PEAK_HBM_GBPS,
         }
     del raw
+    # the stand-alone row-wise Adagrad (fused_rowwise_adagrad_update,
+    # src/optim.py:68-108) on 1 M unique rows of the largest table: a weight
+    # row read and written, its gradient row read, 8-byte row index and 4-byte
+    # accumulator read and written per row
+    t = max(range(len(dev.tables)), key=lambda i: dev.tables[i].shape[0])
+    w, acc = dev.tables[t], dev.states[t]
+    u = min(1 << 20, int(w.shape[0]))
+    rows = torch.randperm(int(w.shape[0]), device=device, generator=gen)[:u].sort().values
+    vals = torch.randn((u, int(w.shape[1])), device=device, generator=gen)
+    for _ in range(3):
+        ops.rowwise_adagrad_(w, acc, rows, vals, lr=wl.lr, eps=wl.eps)
+    torch.cuda.synchronize()
+    e0 = torch.cuda.Event(enable_timing=True)
+    e1 = torch.cuda.Event(enable_timing=True)
+    torch.cuda._sleep(20_000_000)
+    e0.record()
+    for _ in range(reps):
+        ops.rowwise_adagrad_(w, acc, rows, vals, lr=wl.lr, eps=wl.eps)
+    e1.record()
+    torch.cuda.synchronize()
+    ms = e0.elapsed_time(e1) / reps
+    esz = w.element_size()
+    nbytes = float(u) * (int(w.shape[1]) * (2 * esz + 4) + 16)
+    out["rowwise_adagrad"] = {
+        "rows": u, "dim": int(w.shape[1]), "table_rows": int(w.shape[0]), "ms": ms, "alg_bytes": nbytes,
+        "achieved_gbps": nbytes / (ms * 1e-3) / 1e9, "frac": nbytes / (ms * 1e-3) / 1e9 / PEAK_HBM_GBPS,
+    }
+    del rows, vals
     return out
 
 
