@@ -461,7 +461,7 @@ class EventTimer:
         return float(np.median(ts)) if ts else float("nan")
 
 
-def aux_measurements(torch, dev, wl, n_ids: float, steps: int, device) -> dict:
+def aux_measurements(torch, dev, wl, n_ids: float, steps: int, device, batches=None) -> dict:
     """The rows beside the headline step, each timed on its own after it:
 
     * the clipped step (SparseStep.step with clip_norm: sort, squared norm of
@@ -469,6 +469,7 @@ def aux_measurements(torch, dev, wl, n_ids: float, steps: int, device) -> dict:
       src/train.py:5788-5826), wall clock over ``steps`` steps like the
       headline;
     * the stand-alone row-wise Adagrad update on 1 M unique rows;
+    * the autograd path's coalesce of one batch's gradients;
     * device bucketing (mdl_bucketize, src/features.py:360-376 and
       src/benchmark.py:1246-1250) of one step's worth of raw int64 ids, HIP
       events around 20 back-to-back launches queued behind a spin kernel, so
@@ -541,6 +542,32 @@ def aux_measurements(torch, dev, wl, n_ids: float, steps: int, device) -> dict:
         "achieved_gbps": nbytes / (ms * 1e-3) / 1e9, "frac": nbytes / (ms * 1e-3) / 1e9 / PEAK_HBM_GBPS,
     }
     del rows, vals
+    # the autograd path's coalesce (sparse gradient rows + values per table,
+    # src/optim.py:321-324 / src/train.py:5730-5742) of one c1 batch: sort,
+    # unique and segment-sum, each after a fresh lookup (the coalesce consumes
+    # the lookup's sort keys); HIP events around the coalesce only
+    if batches is not None:
+        ids, lengths = batches[0]
+        ids_t = [torch.from_numpy(np.asarray(x, dtype=np.int64)).to(device) for x in ids]
+        lens_t = [None if ln is None else torch.from_numpy(np.asarray(ln, dtype=np.int64)).to(device)
+                  for ln in lengths]
+        times = []
+        for _ in range(5):
+            res = ops.grouped_forward(dev.plan, ids_t, lens_t, with_backward=True)
+            grads = [torch.randn(o.shape, dtype=o.dtype, device=device, generator=gen) for o in res.outputs]
+            torch.cuda.synchronize()
+            e0 = torch.cuda.Event(enable_timing=True)
+            e1 = torch.cuda.Event(enable_timing=True)
+            torch.cuda._sleep(20_000_000)
+            e0.record()
+            coalesced = ops.backward_coalesce(res, grads)
+            e1.record()
+            torch.cuda.synchronize()
+            times.append(e0.elapsed_time(e1))
+            del res, grads, coalesced
+        out["coalesce"] = {"ids": int(sum(x.size for x in ids)), "ms": float(np.median(times)),
+                           "what": "sort + unique + per-table segment sums written as (rows, values), "
+                                   "including its host read of the unique counts (to size the outputs)"}
     return out
 
 
@@ -898,7 +925,7 @@ def main() -> int:
     }
     if wl.kind != "sequence" and not args.no_aux and not args.calibrate_copy:
         # after every timed number above, so the extra steps change none of them
-        result["aux"] = aux_measurements(torch, dev, wl, n_ids, args.steps, device)
+        result["aux"] = aux_measurements(torch, dev, wl, n_ids, args.steps, device, batches)
     if not args.no_cpu_baseline:
         print("[bench] timing the CPU oracle sample", file=sys.stderr, flush=True)
         result["cpu_baseline"] = cpu_baseline(wl, seconds=args.cpu_seconds)
