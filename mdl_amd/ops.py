@@ -860,38 +860,41 @@ def backward_coalesce(res: ForwardResult, grads: Sequence[Tensor | None]) -> lis
         "mdl_backward_count",
     )
     ur = urange.cpu().numpy().reshape(T, 2)
-    # Two allocations for all tables (one per table cost more host time than
-    # the coalesce itself at 200 tables): the rows split per table, the values
+    # Two allocations for all tables, the rows split per table and the values
     # as per-table views of one byte buffer, each starting on a 256-byte
-    # boundary (the kernel stores 16-byte vectors).
-    us = [int(ur[t, 1] - ur[t, 0]) for t in range(T)]
-    rows_list = torch.empty(sum(us), dtype=torch.int64, device=device).split(us)
-    nbytes = [us[t] * int(table.weight.size(1)) * table.weight.element_size() for t, table in enumerate(plan.tables)]
+    # boundary (the kernel stores 16-byte vectors).  The kernel's output
+    # addresses come from the two bases, so it is launched before the 200-odd
+    # per-table views are built on the host (that loop overlaps the GPU).
+    us = (ur[:, 1] - ur[:, 0]).astype(np.int64)
+    esz = np.array([t.weight.element_size() for t in plan.tables], dtype=np.int64)
+    dims = np.array([int(t.weight.size(1)) for t in plan.tables], dtype=np.int64)
+    nbytes = us * dims * esz
     offs = np.zeros(T + 1, dtype=np.int64)
-    np.cumsum([(b + 255) // 256 * 256 for b in nbytes], out=offs[1:])
+    np.cumsum((nbytes + 255) // 256 * 256, out=offs[1:])
+    rows_off = np.zeros(T + 1, dtype=np.int64)
+    np.cumsum(us, out=rows_off[1:])
+    rows_all = torch.empty(int(rows_off[-1]), dtype=torch.int64, device=device)
     vbuf = torch.empty(int(offs[-1]), dtype=torch.uint8, device=device)
-    result = []
-    rows_addr = np.zeros(T, dtype=np.uint64)
-    vals_addr = np.zeros(T, dtype=np.uint64)
-    for t, table in enumerate(plan.tables):
-        w = table.weight
-        rows = rows_list[t]
-        vals = vbuf[int(offs[t]): int(offs[t]) + nbytes[t]].view(w.dtype).view(us[t], int(w.size(1)))
-        rows_addr[t] = rows.data_ptr() if us[t] else 0
-        vals_addr[t] = vals.data_ptr() if us[t] else 0
-        result.append((rows, vals))
+    addr = np.zeros(2 * T, dtype=np.uint64)
+    addr[:T] = np.where(us > 0, rows_all.data_ptr() + 8 * rows_off[:T], 0).astype(np.uint64)
+    addr[T:] = np.where(us > 0, vbuf.data_ptr() + offs[:T], 0).astype(np.uint64)
     if n:
-        rows_dev = upload(rows_addr, device)
-        vals_dev = upload(vals_addr, device)
+        addr_dev = upload(addr, device)
         check(
             lib().mdl_backward_coalesce(
                 feats_dev.data_ptr(), len(feats), tables_dev.data_ptr(), T, plan.max_dim,
                 res.keys.data_ptr(), res.payload.data_ptr(), n, plan.key_bits, _ptr(res.bag_count),
-                urange.data_ptr(), rows_dev.data_ptr(), vals_dev.data_ptr(), ws.data_ptr(), ws.numel(),
+                urange.data_ptr(), addr_dev.data_ptr(), addr_dev.data_ptr() + 8 * T, ws.data_ptr(), ws.numel(),
                 table_classes(tables), stream,
             ),
             "mdl_backward_coalesce",
         )
+    rows_list = rows_all.split(us.tolist())
+    result = []
+    for t, table in enumerate(plan.tables):
+        w = table.weight
+        vals = vbuf[int(offs[t]): int(offs[t]) + int(nbytes[t])].view(w.dtype).view(int(us[t]), int(dims[t]))
+        result.append((rows_list[t], vals))
     res.keys = None
     res.payload = None
     del keep
