@@ -240,6 +240,53 @@ def sequence_gather(weight: np.ndarray, ids: np.ndarray, lengths: np.ndarray, ou
     return out, mask
 
 
+def sequence_positions(ids: np.ndarray, lengths: np.ndarray, out_len: int, order: str = "oldest_to_newest"):
+    """Window layout of the right-aligned gather (src/model.py:2989-3100),
+    vectorised: ``(mask [B, out_len], src [B, out_len])`` where ``src[b, p]``
+    is the input position k whose id lands on window position p (valid where
+    mask is set: p >= out_len - n_b with n_b = min(max(len_b, 0), out_len,
+    in_len); k = p - start oldest first, n_b - 1 - (p - start) newest first).
+    Pinned against the per-position loop of ``sequence_gather``."""
+
+    ids = np.asarray(ids, dtype=np.int64)
+    B, in_len = ids.shape
+    n = np.minimum(np.minimum(np.maximum(np.asarray(lengths, dtype=np.int64), 0), out_len), in_len)
+    start = out_len - n
+    p = np.arange(out_len, dtype=np.int64)[None, :]
+    mask = p >= start[:, None]
+    rel = p - start[:, None]
+    src = rel if order == "oldest_to_newest" else n[:, None] - 1 - rel
+    src = np.where(mask, src, 0)
+    return mask, src
+
+
+def sequence_window(weight: np.ndarray, ids: np.ndarray, lengths: np.ndarray, out_len: int,
+                    order: str = "oldest_to_newest"):
+    """``sequence_gather`` without the per-position loop, in the weight's own
+    dtype (a gather copies rows exactly): ``(out [B, out_len, dim], mask)``."""
+
+    w = np.asarray(weight)
+    ids = np.asarray(ids, dtype=np.int64)
+    mask, src = sequence_positions(ids, lengths, out_len, order)
+    rows = np.take_along_axis(ids, src, axis=1)
+    out = w[np.where(mask, rows, 0)]
+    out[~mask] = 0
+    return out, mask
+
+
+def sequence_grads(ids: np.ndarray, lengths: np.ndarray, grad: np.ndarray, out_len: int,
+                   order: str = "oldest_to_newest", padding_idx: int = 0):
+    """(rows, values) of every valid window position whose id is not
+    padding: the sparse embedding backward of the window gather (values are
+    the window gradient at that position, fp64)."""
+
+    ids = np.asarray(ids, dtype=np.int64)
+    mask, src = sequence_positions(ids, lengths, out_len, order)
+    rows = np.take_along_axis(ids, src, axis=1)
+    keep = mask & (rows != padding_idx)
+    return rows[keep], np.asarray(grad)[keep].astype(np.float64)
+
+
 # ---------------------------------------------------------------- backward --
 
 

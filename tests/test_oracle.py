@@ -301,6 +301,49 @@ def test_sequence_gather_closed_forms():
     assert out[0, :, 0].tolist() == [0.0, 4.0, 3.0]
 
 
+@pytest.mark.parametrize("order", ["oldest_to_newest", "newest_to_oldest"])
+def test_sequence_window_equals_per_position_gather(order):
+    """The vectorised window (used at full config sizes) against the
+    per-position definition, with lengths past both the input and the
+    window, zero and negative lengths."""
+
+    rng = np.random.default_rng(21)
+    W = rng.standard_normal((50, 3)).astype(np.float32)
+    B, L_in = 9, 7
+    ids = rng.integers(0, 50, size=(B, L_in))
+    lengths = np.array([0, 1, 3, 7, 9, -2, 5, 6, 2])
+    for out_len in (1, 4, 7, 10):
+        ref, rmask = O.sequence_gather(W, ids, lengths, out_len, order)
+        out, mask = O.sequence_window(W, ids, lengths, out_len, order)
+        assert out.dtype == np.float32
+        assert np.array_equal(mask, rmask)
+        assert np.array_equal(out.astype(np.float64), ref)
+
+
+@pytest.mark.parametrize("order", ["oldest_to_newest", "newest_to_oldest"])
+def test_sequence_grads_match_embedding_autograd(order):
+    """Window gradients scattered to rows equal the autograd of
+    F.embedding(padding_idx=0) followed by the right-aligned window gather
+    (library routine, CPU)."""
+
+    rng = np.random.default_rng(22)
+    rows, dim, B, L_in, out_len = 30, 4, 6, 8, 6
+    ids = rng.integers(0, rows, size=(B, L_in))
+    ids[:, 1] = 0  # padding inside sequences
+    lengths = np.array([0, 2, 8, 5, 11, 1])
+    grad = rng.standard_normal((B, out_len, dim))
+    r, v = O.sequence_grads(ids, lengths, grad, out_len, order)
+    dense = np.zeros((rows, dim))
+    np.add.at(dense, r, v)
+    W = torch.zeros((rows, dim), dtype=torch.float64, requires_grad=True)
+    emb = torch.nn.functional.embedding(torch.from_numpy(ids), W, padding_idx=0)
+    mask, src = O.sequence_positions(ids, lengths, out_len, order)
+    idx = torch.from_numpy(src)[:, :, None].expand(B, out_len, dim)
+    win = torch.gather(emb, 1, idx) * torch.from_numpy(mask)[:, :, None]
+    (win * torch.from_numpy(grad)).sum().backward()
+    np.testing.assert_allclose(dense, W.grad.numpy(), rtol=1e-12, atol=1e-12)
+
+
 def test_sparse_step_equals_composition():
     rng = np.random.default_rng(7)
     B = 16
