@@ -280,7 +280,9 @@ def algorithmic_bytes(wl: Workload, ids, lengths) -> dict:
 
 
 class DeviceStep:
-    """Tables, persistent buffers and one SparseStep per synthetic batch."""
+    """Tables, persistent buffers, every synthetic batch resident in HBM and
+    one SparseStep for all of them: each step binds its batch (packed ids and
+    bag lengths) and the step places the features on the device."""
 
     def __init__(self, wl: Workload, batches, device, layout: str = "slot"):
         import torch
@@ -335,28 +337,39 @@ class DeviceStep:
         self.err = torch.zeros(1, dtype=torch.int32, device=device)
         # device-resident batches: packed ids + concatenated lengths (an unpooled
         # feature contributes one pseudo-bag holding all its ids)
-        self.steps = []
+        self.batches = []
         for ids, lengths in batches:
-            id_counts = [int(x.size) for x in ids]
-            bag_counts = [0 if ln is None else int(ln.size) for ln in lengths]
             parts = [ln if ln is not None else np.array([x.size]) for x, ln in zip(ids, lengths)]
             packed = torch.from_numpy(np.concatenate(ids).astype(np.int64)).to(device)
             lens = torch.from_numpy(np.concatenate(parts).astype(np.int64)).to(device)
-            self.steps.append(SparseStep(self.plan, packed, lens, id_counts, bag_counts, out_views, grad_views,
-                                         error_count=self.err))
+            self.batches.append((packed, lens))
+        ids0, lengths0 = batches[0]
+        capacity = max(int(b[0].numel()) for b in self.batches)
+        self.st = SparseStep(self.plan, self.batches[0][0], self.batches[0][1], [int(x.size) for x in ids0],
+                             [0 if ln is None else int(ln.size) for ln in lengths0], out_views, grad_views,
+                             error_count=self.err, capacity=capacity)
+        self.steps = [self.st]
+
+    def bind(self, i: int):
+        packed, lens = self.batches[i % len(self.batches)]
+        self.st.bind(packed, lens)
+        return self.st
 
     def capture(self):
-        for st in self.steps:
-            st.capture(self.wl.lr, self.wl.eps)
-        self.graphs = True
+        # A graph reads the buffers it was recorded with: one graph per batch.
+        self.graphs = []
+        for i in range(len(self.batches)):
+            self.bind(i)
+            self.st.capture(self.wl.lr, self.wl.eps)
+            self.graphs.append(self.st._graph)
 
     def step(self, i: int, timers=None):
-        st = self.steps[i % len(self.steps)]
+        if timers is None and getattr(self, "graphs", None):
+            self.graphs[i % len(self.graphs)].replay()
+            return
+        st = self.bind(i)
         if timers is None:
-            if getattr(self, "graphs", False):
-                st.replay()
-            else:
-                st.step(self.wl.lr, self.wl.eps)
+            st.step(self.wl.lr, self.wl.eps)
             return
         timers["forward"].start()
         st.forward()
@@ -400,25 +413,34 @@ class SequenceDeviceStep:
             g.normal_(0.0, 1.0, generator=gen)
             self.grads.append(g)
         self.err = torch.zeros(1, dtype=torch.int32, device=device)
-        self.steps = []
+        self.batches = []
         for ids, lengths in batches:
             dids = [torch.from_numpy(m).to(device) for m in ids]
             dlen = [torch.from_numpy(ln.astype(np.int64)).to(device) for ln in lengths]
-            self.steps.append(SequenceStep(self.plan, dids, dlen, self.outs, self.masks, self.grads,
-                                           error_count=self.err))
+            self.batches.append((dids, dlen))
+        self.st = SequenceStep(self.plan, self.batches[0][0], self.batches[0][1], self.outs, self.masks, self.grads,
+                               error_count=self.err)
+        self.steps = [self.st]
+
+    def bind(self, i: int):
+        dids, dlen = self.batches[i % len(self.batches)]
+        self.st.bind(dids, dlen)
+        return self.st
 
     def capture(self):
-        for st in self.steps:
-            st.capture(self.wl.lr, self.wl.eps)
-        self.graphs = True
+        self.graphs = []
+        for i in range(len(self.batches)):
+            self.bind(i)
+            self.st.capture(self.wl.lr, self.wl.eps)
+            self.graphs.append(self.st._graph)
 
     def step(self, i: int, timers=None):
-        st = self.steps[i % len(self.steps)]
+        if timers is None and getattr(self, "graphs", None):
+            self.graphs[i % len(self.graphs)].replay()
+            return
+        st = self.bind(i)
         if timers is None:
-            if getattr(self, "graphs", False):
-                st.replay()
-            else:
-                st.step(self.wl.lr, self.wl.eps)
+            st.step(self.wl.lr, self.wl.eps)
             return
         timers["forward"].start()
         st.forward()
@@ -483,7 +505,7 @@ def aux_measurements(torch, dev, wl, n_ids: float, steps: int, device, batches=N
     torch.cuda.synchronize()
     t0 = time.perf_counter()
     for i in range(steps):
-        dev.steps[i % len(dev.steps)].step(wl.lr, wl.eps, clip_norm=1.0)
+        dev.bind(i).step(wl.lr, wl.eps, clip_norm=1.0)
     torch.cuda.synchronize()
     out["clipped_step"] = {
         "ms_per_step": (time.perf_counter() - t0) * 1e3 / steps,
@@ -574,59 +596,115 @@ def aux_measurements(torch, dev, wl, n_ids: float, steps: int, device, batches=N
 # ------------------------------------------------------------ cpu baseline --
 
 
-def cpu_baseline(wl: Workload, seconds: float = 12.0, row_cap: int = 1 << 16, batch: int = 512) -> dict:
-    """Time the CPU oracle (plain-C port of the reference step) on a sample."""
+CPU_ROW_CAP = {"c1": 1 << 20, "c3": 1 << 20, "c2": 1 << 22, "c4": 1 << 22}
 
-    from oracle import oracle as O
+
+def _host_info() -> dict:
+    info = {"os_cpu_count": os.cpu_count(), "cpu_model": platform.processor() or platform.machine(), "ram_gb": None}
+    try:
+        for line in Path("/proc/cpuinfo").read_text().splitlines():
+            if line.startswith("model name"):
+                info["cpu_model"] = line.split(":", 1)[1].strip()
+                break
+        for line in Path("/proc/meminfo").read_text().splitlines():
+            if line.startswith("MemTotal"):
+                info["ram_gb"] = round(int(line.split()[1]) / 1e6, 1)
+                break
+    except OSError:
+        pass
+    return info
+
+
+def cpu_baseline(wl: Workload, batch, steps: int = 5, warmup: int = 2, row_cap: int | None = None) -> dict:
+    """Time the reference path's PyTorch CPU restatement (oracle/torch_path.py:
+    F.embedding(sparse=True) -> index_add_ pooling -> autograd -> coalesce()
+    -> the CPU row-wise Adagrad branch) on this run's first batch, with every
+    CPU thread the process may use; the median of ``steps`` steps after
+    ``warmup``.  Tables above ``row_cap`` rows are capped (the same ids
+    bucketed mod the cap, the reference benchmark's rule) when the host could
+    not hold them; values do not change the CPU time, so tables are filled by
+    tiling one random block."""
+
+    import torch
+
+    from oracle import torch_path as TP
+
+    threads = len(os.sched_getaffinity(0)) if hasattr(os, "sched_getaffinity") else (os.cpu_count() or 1)
+    torch.set_num_threads(threads)
+    dtype = torch.float32 if wl.dtype == "fp32" else torch.bfloat16
+    cap = row_cap if row_cap is not None else CPU_ROW_CAP.get(wl.name)
+    rows = [min(r, cap) if cap else r for r in wl.rows]
+    capped = any(r != q for r, q in zip(rows, wl.rows))
+    t0 = time.perf_counter()
+    gen = torch.Generator().manual_seed(5)
+    tables, accs = [], []
+    for r, d in zip(rows, wl.dims):
+        block = (torch.randn((min(r, 4096), d), generator=gen) * 0.02).to(dtype)
+        w = torch.empty((r, d), dtype=dtype)
+        for i in range(0, r, block.size(0)):
+            w[i: i + block.size(0)] = block[: r - i]
+        w[0].zero_()
+        tables.append(w)
+        accs.append(torch.zeros(r, dtype=torch.float32))
+    setup_s = time.perf_counter() - t0
+
+    def cap_ids(x, t):
+        x = np.asarray(x, dtype=np.int64)
+        if rows[t] == wl.rows[t]:
+            return torch.from_numpy(x)
+        return torch.from_numpy(np.where(x > 0, 1 + (x - 1) % (rows[t] - 1), 0))
 
     rng = np.random.default_rng(7)
-    sample = Workload(
-        name=wl.name, batch=batch, rows=[min(r, row_cap) for r in wl.rows], dims=wl.dims, dtype=wl.dtype,
-        features=wl.features, zipf=wl.zipf, raw_bits=wl.raw_bits, lr=wl.lr, eps=wl.eps,
-    )
-    tables = []
-    for r, d in zip(sample.rows, sample.dims):
-        # values do not affect the CPU time; tile one random block to fill fast
-        W = np.resize(rng.standard_normal((min(r, 4096), d), dtype=np.float32) * np.float32(0.02), (r, d))
-        W[0] = 0
-        tables.append({"W": W, "acc": np.zeros(r, np.float32), "is_bf16": wl.dtype == "bf16"})
-    ids, lengths = draw_batch(rng, sample)
-    feats = []
-    offs_parts = []
-    bag_off = 0
-    ids_off = 0
-    col = 0
-    for f, x, ln in zip(sample.features, ids, lengths):
-        pooling = {"none": 0, "sum": 1, "mean": 2}[f.pooling]
-        feats.append({"table": f.table, "pooling": pooling, "exclude": 1, "ids_off": ids_off,
-                      "bag_off": bag_off, "num_bags": 0 if ln is None else len(ln), "out_col": col})
-        if ln is not None:
-            o = O.offsets_of(ln)
-            offs_parts.append(o)
-            bag_off += len(o)
-        ids_off += x.size
-        col += sample.dims[f.table]
-    all_ids = np.concatenate(ids)
-    offs = np.concatenate(offs_parts) if offs_parts else np.zeros(1, np.int64)
-    grad = rng.standard_normal((batch, col))
-    n_active = int(sum(int((x != 0).sum()) for x in ids))
-    steps = 0
-    t0 = time.perf_counter()
-    while True:
-        O.sparse_step(feats, tables, all_ids, offs, col, grad, wl.lr, wl.eps)
-        steps += 1
-        el = time.perf_counter() - t0
-        if el >= seconds:
-            break
+    if wl.kind == "sequence":
+        _, _, pad = wl.seq_len
+        feats = [TP.Feature(f.table, "none") for f in wl.features]
+        ids_t, lens_t, grads = [], [], []
+        n_active = 0
+        for f, (m, ln) in zip(wl.features, zip(*batch)):
+            # the window layout of src/model.py:2989-3020 is a gather of the
+            # looked-up rows; time the lookup of every padded position and
+            # the gradient of the valid ones (the padding rows get none)
+            ids_t.append(cap_ids(m, f.table))
+            lens_t.append(None)
+            valid = np.arange(m.shape[1])[None, :] < np.asarray(ln)[:, None]
+            g = np.zeros(m.shape + (wl.dims[f.table],), dtype=np.float32)
+            g[valid] = rng.standard_normal((int(valid.sum()), wl.dims[f.table])).astype(np.float32)
+            grads.append(torch.from_numpy(g).to(dtype))
+            n_active += int((m[valid] != 0).sum())
+    else:
+        ids, lengths = batch
+        feats = [TP.Feature(f.table, f.pooling) for f in wl.features]
+        ids_t = [cap_ids(x, f.table) for f, x in zip(wl.features, ids)]
+        lens_t = [None if ln is None else torch.from_numpy(np.asarray(ln, dtype=np.int64)) for ln in lengths]
+        grads = [torch.from_numpy(rng.standard_normal((wl.batch, wl.dims[f.table])).astype(np.float32)).to(dtype)
+                 for f in wl.features]
+        n_active = int(sum(int((np.asarray(x) != 0).sum()) for x in ids))
+    step = TP.TorchStep(tables, accs, feats)
+    times = []
+    for i in range(warmup + steps):
+        t1 = time.perf_counter()
+        step.step(ids_t, lens_t, grads, wl.lr, wl.eps)
+        if i >= warmup:
+            times.append(time.perf_counter() - t1)
+    ms = float(np.median(times)) * 1e3
+    info = _host_info()
+    total_rows = sum(rows)
     return {
-        "value": n_active * steps / el,
+        "value": n_active / (ms * 1e-3),
         "unit": "rows/s",
-        "cores": 1,
+        "cores": threads,
         "kind": "port",
-        "sample": (f"{wl.name} layout at batch {batch} (of {wl.batch}), tables capped at {row_cap} rows "
-                   f"(same id stream bucketed mod the cap), {steps} steps in {el:.1f} s, "
-                   f"single-threaded C oracle on {platform.processor() or platform.machine()}, "
-                   f"host has {os.cpu_count()} cores"),
+        "ms_per_step": ms,
+        "sample": (f"{wl.name} at full batch {wl.batch} ({n_active} looked-up ids), the bench's first batch; "
+                   + (f"tables capped at {cap} rows ({total_rows:.3e} rows in all, ids bucketed mod the cap) "
+                      "so they fit host RAM; " if capped else "full-size tables; ")
+                   + f"PyTorch {torch.__version__} CPU restatement of the reference path (oracle/torch_path.py), "
+                   f"median of {steps} steps after {warmup} warmup, torch.set_num_threads({threads}); "
+                   f"host: {info['cpu_model']}, os.cpu_count()={info['os_cpu_count']}, "
+                   f"{threads} CPUs usable by the process, {info['ram_gb']} GB RAM; table set-up {setup_s:.1f} s"),
+        "threads": threads,
+        "row_cap": cap if capped else None,
+        "host": info,
     }
 
 
@@ -761,7 +839,7 @@ def main() -> int:
                          "(measured: no faster at c0, c1 or c4 -- the host keeps ahead of the GPU)")
     ap.add_argument("--no-aux", action="store_true",
                     help="skip the clipped-step and bucketing measurements (off with --calibrate-copy)")
-    ap.add_argument("--cpu-seconds", type=float, default=12.0)
+    ap.add_argument("--cpu-steps", type=int, default=5, help="timed steps of the CPU baseline (after 2 warmup)")
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="also run three plain 1 GiB device copies (counter calibration for rocprofv3 --pmc runs)")
     ap.add_argument("--summarize-pmc", nargs="+", metavar="DIR",
@@ -825,7 +903,7 @@ def main() -> int:
         # steps loaded the kernels); the timed steps replay them
         dev.capture()
         torch.cuda.synchronize()
-        for i in range(len(dev.steps)):
+        for i in range(len(dev.batches)):
             dev.step(args.warmup + i)
         torch.cuda.synchronize()
     if int(dev.err.item()):
@@ -928,7 +1006,7 @@ def main() -> int:
         result["aux"] = aux_measurements(torch, dev, wl, n_ids, args.steps, device, batches)
     if not args.no_cpu_baseline:
         print("[bench] timing the CPU oracle sample", file=sys.stderr, flush=True)
-        result["cpu_baseline"] = cpu_baseline(wl, seconds=args.cpu_seconds)
+        result["cpu_baseline"] = cpu_baseline(wl, batches[0], steps=args.cpu_steps)
     print(json.dumps(result), flush=True)
     return 0
 

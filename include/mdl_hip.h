@@ -48,7 +48,15 @@ enum { MDL_POOL_NONE = 0, MDL_POOL_SUM = 1, MDL_POOL_MEAN = 2 };
  * and the ids only decide the null weights; this is _mean_pool_categorical_bag
  * on its `embedded` input (src/model.py:509-570).  Such features emit no sort
  * keys (sentinel) since they own no table. */
-enum { MDL_FLAG_EXCLUDE_NULL = 1, MDL_FLAG_ROWS_BY_POSITION = 2 };
+enum { MDL_FLAG_EXCLUDE_NULL = 1, MDL_FLAG_ROWS_BY_POSITION = 2, MDL_FLAG_IDS_FROM_OFFSETS = 4 };
+/* IDS_FROM_OFFSETS: the feature's ids are [offsets[bag_base], offsets[bag_base
+ * + nb]) of this call (nb = num_bags; 1 for an unpooled feature, whose ids
+ * then occupy one pseudo-bag of the offsets array), and [ids_begin, ids_begin
+ * + num_ids) is only a bound that range is clamped into.  A batch whose bag
+ * lengths change then reuses the same descriptors and chunk plan: one scan
+ * of its lengths places every feature on the device (the training step
+ * encoder of src/model.py:3782-3890 serves any batch).  Forward chunks of an
+ * unpooled feature past its range this call do nothing. */
 
 enum { MDL_BUCKET_PRE_HASHED = 0, MDL_BUCKET_MOD = 1 };
 
@@ -61,7 +69,15 @@ enum { MDL_BUCKET_PRE_HASHED = 0, MDL_BUCKET_MOD = 1 };
  * calls taking a `classes` mask launch only the variants whose bit
  * (1 << variant) is set, 0 meaning all.  mdl_feature_classes and
  * mdl_table_classes compute the mask of a host descriptor array with the
- * kernels' own rule; a mask that misses a present variant skips its rows. */
+ * kernels' own rule; a mask that misses a present variant skips its rows.
+ * mdl_table_classes also sets MDL_CLASSES_UNSUPPORTED when a table's rows
+ * are wider than the backward reduce covers (dim > 64 * C for the table's
+ * lane width C: fp32 rows beyond 256 elements unless dim is a multiple of 8,
+ * any row beyond 512, rows that are not 16-byte aligned beyond 64); every
+ * backward call that reduces rows returns MDL_ERR_UNSUPPORTED for a mask with
+ * that bit (a mask of 0 skips the check: the caller vouches for the widths,
+ * and rows of a too-wide table are then left untouched). */
+#define MDL_CLASSES_UNSUPPORTED 0x80000000u
 enum {
   MDL_CLASS_F32_VEC = 0, MDL_CLASS_F32 = 1, MDL_CLASS_BF16_VEC = 2,
   MDL_CLASS_BF16 = 3, MDL_CLASS_BF16_F32_VEC = 4, MDL_CLASS_BF16_F32 = 5
@@ -75,7 +91,8 @@ enum { MDL_SEQ_OLDEST_TO_NEWEST = 0, MDL_SEQ_NEWEST_TO_OLDEST = 1 };
  * lives in device memory.  Features that alias one table (shared embeddings)
  * carry the same weight/state/row_base/table.
  *
- * Ids of feature f are ids[ids_begin, ids_begin + num_ids).  A pooled feature
+ * Ids of feature f are ids[ids_begin, ids_begin + num_ids) (see
+ * MDL_FLAG_IDS_FROM_OFFSETS for ranges set by the offsets).  A pooled feature
  * has num_bags bags whose bounds are offsets[bag_base .. bag_base+num_bags]
  * (absolute indices into ids, non-decreasing).  A MDL_POOL_NONE feature has
  * one output row per id and ignores bag_base/num_bags.
@@ -198,11 +215,14 @@ int64_t mdl_plan_chunks(const mdl_feature* feats_host, int32_t num_features,
  *   sort_payload[i] = payload_base + output row of the id.
  * and, when bag_count is not NULL, bag_count[payload_base + b] = sum_i w_i for
  * every pooled bag.  sort_keys/sort_payload have one entry per position of
- * the concatenated ids array.
+ * the concatenated ids array.  num_ids is the number of entries of ids: every
+ * feature's id range is clamped into [0, num_ids), so a descriptor or bag
+ * lengths that point past the array read nothing outside it (the clamp is
+ * counted as an error).
  */
 int mdl_forward(const mdl_feature* feats, int32_t num_features,
                 const mdl_chunk* chunks, int64_t num_chunks,
-                const int64_t* ids, const int64_t* offsets,
+                const int64_t* ids, int64_t num_ids, const int64_t* offsets,
                 uint32_t* sort_keys, uint32_t* sort_payload, uint32_t sentinel,
                 float* bag_count, int32_t* error_count, uint32_t classes,
                 void* stream);
@@ -227,7 +247,7 @@ int mdl_forward(const mdl_feature* feats, int32_t num_features,
  */
 int mdl_pool_backward(const mdl_feature* feats, int32_t num_features,
                       const mdl_chunk* chunks, int64_t num_chunks,
-                      const int64_t* ids, const int64_t* offsets,
+                      const int64_t* ids, int64_t num_ids, const int64_t* offsets,
                       const float* bag_count, uint32_t classes, void* stream);
 
 /*
@@ -287,7 +307,14 @@ int mdl_unique(const int64_t* ids, int64_t n, int32_t key_bits, int64_t* unique_
 /*
  * The backward of a grouped call consumes the sort keys/payloads written by
  * mdl_forward / mdl_sequence_forward (n entries, keys < 2^key_bits; the
- * sentinel must be < 2^key_bits too).  It sorts them in place (keys/payload
+ * sentinel must be < 2^key_bits too).  The calls that sort (sort, adagrad,
+ * count) take `count`: NULL, or a device int64 holding how many of the n
+ * entries are present this call (clamped to [0, n]) -- e.g. the last offset
+ * of the forward's offsets scan -- so a batch whose size is only known on the
+ * device is sorted and reduced without a host round trip; n is then the
+ * capacity that sizes the launches and the workspace.  The calls that follow
+ * a sort (apply, sumsq, coalesce) take the same n and read the rest of the
+ * plan from the workspace.  It sorts them in place (keys/payload
  * and the workspace are clobbered), cuts the sorted array into chunks of
  * <= 512 entries that never straddle two tables and reduces every run of
  * equal keys.  The num_tables tables (device array) are ordered by row_base,
@@ -329,7 +356,7 @@ int mdl_sparse_keys(const int64_t* ids, int64_t n, int64_t num_rows, int64_t row
 int mdl_backward_adagrad(const mdl_feature* feats, int32_t num_features,
                          const mdl_table* tables, int32_t num_tables, int32_t max_dim,
                          uint32_t* sort_keys, uint32_t* sort_payload, int64_t n,
-                         int32_t key_bits, const float* bag_count, float lr, float eps,
+                         const int64_t* count, int32_t key_bits, const float* bag_count, float lr, float eps,
                          const float* grad_scale, void* workspace, size_t workspace_bytes,
                          uint32_t classes, void* stream);
 
@@ -342,7 +369,7 @@ int mdl_backward_adagrad(const mdl_feature* feats, int32_t num_features,
  * but every access stays in bounds.) */
 int mdl_backward_sort(const mdl_table* tables, int32_t num_tables, int32_t max_dim,
                       uint32_t* sort_keys, uint32_t* sort_payload, int64_t n,
-                      int32_t key_bits, void* workspace, size_t workspace_bytes,
+                      const int64_t* count, int32_t key_bits, void* workspace, size_t workspace_bytes,
                       void* stream);
 int mdl_backward_apply(const mdl_feature* feats, int32_t num_features,
                        const mdl_table* tables, int32_t num_tables, int32_t max_dim,
@@ -379,7 +406,7 @@ int mdl_backward_sumsq(const mdl_feature* feats, int32_t num_features,
  */
 int mdl_backward_count(const mdl_table* tables, int32_t num_tables, int32_t max_dim,
                        uint32_t* sort_keys, uint32_t* sort_payload, int64_t n,
-                       int32_t key_bits, int64_t* unique_range,
+                       const int64_t* count, int32_t key_bits, int64_t* unique_range,
                        void* workspace, size_t workspace_bytes, void* stream);
 int mdl_backward_coalesce(const mdl_feature* feats, int32_t num_features,
                           const mdl_table* tables, int32_t num_tables, int32_t max_dim,

@@ -24,6 +24,9 @@ MDL_POOL_SUM = 1
 MDL_POOL_MEAN = 2
 MDL_FLAG_EXCLUDE_NULL = 1
 MDL_FLAG_ROWS_BY_POSITION = 2
+MDL_FLAG_IDS_FROM_OFFSETS = 4
+MDL_CLASSES_UNSUPPORTED = 0x80000000
+ABI_VERSION = 4
 MDL_BUCKET_PRE_HASHED = 0
 MDL_BUCKET_MOD = 1
 MDL_SEQ_OLDEST_TO_NEWEST = 0
@@ -88,8 +91,8 @@ SIGNATURES: dict[str, tuple] = {
     "mdl_offsets_workspace_bytes": (_SZ, [_I64]),
     "mdl_lengths_to_offsets": (_I32, [_P, _I64, _P, _P, _SZ, _P]),
     "mdl_plan_chunks": (_I64, [_P, _I32, _I32, _P, _I64]),
-    "mdl_forward": (_I32, [_P, _I32, _P, _I64, _P, _P, _P, _P, _U32, _P, _P, _U32, _P]),
-    "mdl_pool_backward": (_I32, [_P, _I32, _P, _I64, _P, _P, _P, _U32, _P]),
+    "mdl_forward": (_I32, [_P, _I32, _P, _I64, _P, _I64, _P, _P, _P, _U32, _P, _P, _U32, _P]),
+    "mdl_pool_backward": (_I32, [_P, _I32, _P, _I64, _P, _I64, _P, _P, _U32, _P]),
     "mdl_feature_classes": (_U32, [_P, _I32]),
     "mdl_table_classes": (_U32, [_P, _I32]),
     "mdl_sequence_forward": (
@@ -104,9 +107,9 @@ SIGNATURES: dict[str, tuple] = {
     "mdl_backward_workspace_bytes": (_SZ, [_I64, _I32, _I32]),
     "mdl_backward_adagrad": (
         _I32,
-        [_P, _I32, _P, _I32, _I32, _P, _P, _I64, _I32, _P, _F, _F, _P, _P, _SZ, _U32, _P],
+        [_P, _I32, _P, _I32, _I32, _P, _P, _I64, _P, _I32, _P, _F, _F, _P, _P, _SZ, _U32, _P],
     ),
-    "mdl_backward_sort": (_I32, [_P, _I32, _I32, _P, _P, _I64, _I32, _P, _SZ, _P]),
+    "mdl_backward_sort": (_I32, [_P, _I32, _I32, _P, _P, _I64, _P, _I32, _P, _SZ, _P]),
     "mdl_backward_apply": (
         _I32,
         [_P, _I32, _P, _I32, _I32, _P, _P, _I64, _I32, _P, _F, _F, _P, _P, _SZ, _U32, _P],
@@ -119,7 +122,7 @@ SIGNATURES: dict[str, tuple] = {
     "mdl_sumsq": (_I32, [_P, _I32, _P, _P, _SZ, _P]),
     "mdl_clip_coef": (_I32, [_P, _I32, _F, _P, _P, _P]),
     "mdl_scale": (_I32, [_P, _I32, _P, _P]),
-    "mdl_backward_count": (_I32, [_P, _I32, _I32, _P, _P, _I64, _I32, _P, _P, _SZ, _P]),
+    "mdl_backward_count": (_I32, [_P, _I32, _I32, _P, _P, _I64, _P, _I32, _P, _P, _SZ, _P]),
     "mdl_backward_coalesce": (
         _I32,
         [_P, _I32, _P, _I32, _I32, _P, _P, _I64, _I32, _P, _P, _P, _P, _P, _SZ, _U32, _P],
@@ -154,6 +157,12 @@ def lib() -> ctypes.CDLL:
         fn = getattr(handle, name)
         fn.restype = restype
         fn.argtypes = argtypes
+    found = int(handle.mdl_abi_version())
+    if found != ABI_VERSION:
+        raise RuntimeError(
+            f"{path} implements C ABI version {found}, this package binds version {ABI_VERSION}; "
+            "rebuild it with `python -m mdl_amd.build`"
+        )
     _LIB = handle
     return handle
 

@@ -2,7 +2,9 @@
 //
 // L lanes own one row (16 bytes each), so a wavefront updates 64/L rows per
 // pass with one read and one write of every touched weight row, its gradient
-// row and its fp32 accumulator.  The row's sum of squares is combined across
+// row and its fp32 accumulator; a row wider than 64 lanes cover is walked in
+// column blocks by one wave (any dim, like the reference kernel's
+// BLOCK = next_pow2(dim)).  The row's sum of squares is combined across
 // its L lanes with cross-lane permutes; the arithmetic follows the reference
 // update kernel (mean of squares, sqrt, eps added after the root, division
 // before the learning-rate product, one rounding to the weight dtype).
@@ -77,11 +79,63 @@ __device__ __forceinline__ void adagrad_rows(const AdaArgs& a, int64_t wave, int
   if (bad && a.error_count) atomicAdd(a.error_count, bad);
 }
 
+// Rows wider than one wavefront covers (dim > 64 * C): the wave owns one row
+// at a time and walks it in column blocks of 64 * C elements, twice -- the
+// first walk adds up the row's sum of squares, the second (after the
+// accumulator update, which needs the whole row's mean square) reads the
+// gradient again with the weight and writes the updated weight.  The second
+// read of the gradient row mostly hits the cache.
+template <typename TW, typename TV, int C>
+__device__ __forceinline__ void adagrad_wide_rows(const AdaArgs& a, int64_t wave, int64_t nwaves) {
+  const int lane = lane_id();
+  const int span = kWave * C;
+  const int ncb = (a.dim + span - 1) / span;
+  TW* W = static_cast<TW*>(a.weight);
+  const TV* V = static_cast<const TV*>(a.values);
+  int bad = 0;
+  for (int64_t i = wave; i < a.n; i += nwaves) {
+    const int64_t row = a.rows[i];
+    if ((uint64_t)row >= (uint64_t)a.num_rows) {
+      if (lane == 0) ++bad;
+      continue;
+    }
+    const TV* vrow = V + i * a.vstride;
+    TW* wrow = W + row * a.wstride;
+    float ss = 0.f;
+    for (int cb = 0; cb < ncb; ++cb) {
+      const int col = cb * span + lane * C;
+      if (col < a.dim) {
+        float g[C];
+        RowIO<TV, C>::load(vrow + col, g);
+#pragma unroll
+        for (int k = 0; k < C; ++k) ss += g[k] * g[k];
+      }
+    }
+    for (int m = 1; m < kWave; m <<= 1) ss += shfl_f(ss, lane ^ m);
+    const float acc = a.acc[row] + ss / (float)a.dim;
+    if (lane == 0) a.acc[row] = acc;
+    const float den = sqrtf(acc) + a.eps;
+    for (int cb = 0; cb < ncb; ++cb) {
+      const int col = cb * span + lane * C;
+      if (col < a.dim) {
+        float g[C], w[C];
+        RowIO<TV, C>::load(vrow + col, g);
+        RowIO<TW, C>::load(wrow + col, w);
+#pragma unroll
+        for (int k = 0; k < C; ++k) w[k] = w[k] - a.lr * (g[k] / den);
+        RowIO<TW, C>::store(wrow + col, w);
+      }
+    }
+  }
+  if (bad && a.error_count) atomicAdd(a.error_count, bad);
+}
+
 template <typename TW, typename TV, int C>
 __global__ __launch_bounds__(kAdaWaves * kWave) void adagrad_kernel(AdaArgs a) {
   const int64_t nwaves = (int64_t)gridDim.x * kAdaWaves;
   const int64_t wave = (int64_t)blockIdx.x * kAdaWaves + threadIdx.x / kWave;
-  adagrad_rows<TW, TV, C>(a, wave, nwaves);
+  if (a.dim > kWave * C) adagrad_wide_rows<TW, TV, C>(a, wave, nwaves);
+  else adagrad_rows<TW, TV, C>(a, wave, nwaves);
 }
 
 }  // namespace mdl
@@ -118,10 +172,9 @@ int mdl_rowwise_adagrad(void* weight, int32_t wdtype, int64_t num_rows, int32_t 
                    (weight_stride * wsz) % 16 == 0 && (values_stride * vsz) % 16 == 0 &&
                    ((int64_t)dim * wsz) % 16 == 0 && ((int64_t)c * vsz) % 16 == 0;
   const int cc = vec ? c : 1;
-  if (dim > kWave * cc)
-    return fail(MDL_ERR_UNSUPPORTED, "mdl_rowwise_adagrad: row wider than one wavefront covers");
+  // Rows wider than 64 * cc take one wave each (column-block walk).
   const int L = lanes_for(dim, cc);
-  const int64_t rows_per_block = (int64_t)(kWave / L) * kAdaUnroll * kAdaWaves;
+  const int64_t rows_per_block = dim > kWave * cc ? kAdaWaves : (int64_t)(kWave / L) * kAdaUnroll * kAdaWaves;
   int64_t blocks = (num_touched + rows_per_block - 1) / rows_per_block;
   if (blocks > 16384) blocks = 16384;
   hipStream_t s = as_stream(stream);

@@ -26,7 +26,7 @@
 namespace mdl {
 
 int sort_pairs(uint32_t* keys, uint32_t* vals, uint32_t* keys_alt, uint32_t* vals_alt, int64_t n,
-               int key_bits, void* ws, size_t ws_bytes, int* in_alt, hipStream_t s);
+               const int64_t* n_dev, int key_bits, void* ws, size_t ws_bytes, int* in_alt, hipStream_t s);
 size_t sort_ws_bytes(int64_t n);
 int sort_pass_count(int key_bits);
 int launch_sum_partials(const float* partial, int64_t m, const int64_t* m_dev, float* out, hipStream_t s);
@@ -144,8 +144,15 @@ __device__ __forceinline__ int64_t table_chunk_len(const mdl_table& tb, int slot
 // search: each round the block probes 256 evenly spaced keys of the
 // remaining range, so 2^23 keys take three dependent loads instead of 23.
 __global__ __launch_bounds__(kBoundThreads) void bwd_bounds_kernel(const mdl_table* __restrict__ tables,
-                                                                   const uint32_t* __restrict__ keys, int64_t n,
+                                                                   const uint32_t* __restrict__ keys, int64_t n_cap,
+                                                                   const int64_t* __restrict__ n_dev,
                                                                    int64_t* table_start, int64_t* table_end) {
+  // Sorted entries present: n_cap, or the caller's device count (clamped).
+  int64_t n = n_cap;
+  if (n_dev != nullptr) {
+    const int64_t c = *n_dev;
+    n = c < 0 ? 0 : (c > n_cap ? n_cap : c);
+  }
   const int32_t t = blockIdx.x >> 1;
   const bool upper = blockIdx.x & 1;
   const uint64_t key = (uint64_t)tables[t].row_base + (upper ? (uint64_t)tables[t].num_rows : 0ull);
@@ -329,7 +336,7 @@ struct Reducer {
   TW* W;
   float* state;
   int64_t row_base, num_rows;
-  float inv_dim;
+  float fdim;
   // fields of the table's only feature (single >= 0)
   const TG* g_base;
   int64_t g_stride, pbase;
@@ -344,7 +351,7 @@ struct Reducer {
     state = (float*)uni64b((int64_t)tb.state);
     row_base = uni64b(tb.row_base);
     num_rows = uni64b(tb.num_rows);
-    inv_dim = 1.f / (float)dim;  // exact for power-of-two dims
+    fdim = (float)dim;
     L = lanes_for(dim, C);
     G = kWave / L;
     const int lane = lane_id();
@@ -405,13 +412,16 @@ struct Reducer {
     if (kMode == kModeAdagrad) {
       if (!row_ok(key)) return;
       const float ss = row_sumsq(v);
-      // scale == 1 leaves every product exact, so unclipped steps are unchanged
-      const float acc = acc0 + (ss * (scale * scale)) * inv_dim;
+      // The reference update's arithmetic: mean of squares by a true
+      // division, eps after the root, the gradient divided by that before the
+      // learning-rate product (src/optim.py:53-62).  scale == 1 leaves every
+      // product exact, so unclipped steps see the gradient unchanged.
+      const float acc = acc0 + (ss * (scale * scale)) / fdim;
       if (sub == 0) st_policy<kUpdatePolicy>(state + row, acc);
-      const float step = a.lr * __builtin_amdgcn_rcpf(sqrtf(acc) + a.eps);
+      const float den = sqrtf(acc) + a.eps;
       if (col_ok) {
 #pragma unroll
-        for (int k = 0; k < C; ++k) w[k] = w[k] - step * (v[k] * scale);
+        for (int k = 0; k < C; ++k) w[k] = w[k] - a.lr * ((v[k] * scale) / den);
         RowIO<TW, C>::template store<kUpdatePolicy>(W + row * dim + col, w);
       }
     } else if (kMode == kModeCoalesce) {
@@ -609,7 +619,7 @@ __device__ __forceinline__ void reduce_chunk_body(const BwdArgs& a, int64_t c, c
 template <int kMode, typename TW, typename TG, int C>
 __device__ __forceinline__ void reduce_chunk(const BwdArgs& a, int64_t c, const ChunkDesc& d, ChunkStage& st) {
   Reducer<kMode, TW, TG, C> R(a, d.table);
-  if (R.dim > kWave * C) return;  // rejected on the host; never reached
+  if (R.dim > kWave * C) return;  // flagged by mdl_table_classes; the call is refused
   const int lane = lane_id();
   const uint32_t kNone = 0xffffffffu;
   const int len = d.len;
@@ -647,7 +657,7 @@ __device__ __forceinline__ void reduce_chunk(const BwdArgs& a, int64_t c, const 
 template <int kMode, typename TW, typename TG, int C>
 __device__ __forceinline__ void fixup_chunk(const BwdArgs& a, int64_t c, const ChunkDesc& d, int32_t flags) {
   Reducer<kMode, TW, TG, C> R(a, d.table);
-  if (R.dim > kWave * C) return;  // rejected on the host; never reached
+  if (R.dim > kWave * C) return;  // flagged by mdl_table_classes; the call is refused
   // Walk back over chunks that lie wholly inside the run to the chunk holding
   // its first entry (never past the table's first chunk).
   // The wave reads 64 chunks' flags per step (a Zipf head row spans many
@@ -760,12 +770,22 @@ __global__ MDL_OCCUPANCY __launch_bounds__(kBwdWaves * kWave) void bwd_reduce_ke
 static int validate_tables(const char* who, int32_t T, int32_t max_dim, int64_t n) {
   if (T <= 0) return fail(MDL_ERR_INVALID, std::string(who) + ": need at least one table");
   if (max_dim <= 0) return fail(MDL_ERR_INVALID, std::string(who) + ": max_dim must be positive");
+  if (max_dim > kWave * MDL_MAX_WIDTH)
+    return fail(MDL_ERR_UNSUPPORTED, std::string(who) + ": rows wider than 512 elements");
   if (n < 0 || n > 0xffffffffll) return fail(MDL_ERR_UNSUPPORTED, std::string(who) + ": n outside [0, 2^32)");
   return MDL_OK;
 }
 
-static int plan(const mdl_table* tables, int32_t T, const uint32_t* sk, int64_t n, const BwdWs& w, hipStream_t s) {
-  hipLaunchKernelGGL(bwd_bounds_kernel, dim3((unsigned)(2 * T)), dim3(kBoundThreads), 0, s, tables, sk, n,
+static int validate_classes(const char* who, uint32_t classes) {
+  if (classes & MDL_CLASSES_UNSUPPORTED)
+    return fail(MDL_ERR_UNSUPPORTED,
+                std::string(who) + ": a table's rows are wider than its lanes cover (dim > 64 x lane width)");
+  return MDL_OK;
+}
+
+static int plan(const mdl_table* tables, int32_t T, const uint32_t* sk, int64_t n, const int64_t* n_dev,
+                const BwdWs& w, hipStream_t s) {
+  hipLaunchKernelGGL(bwd_bounds_kernel, dim3((unsigned)(2 * T)), dim3(kBoundThreads), 0, s, tables, sk, n, n_dev,
                      w.table_start, w.table_end);
   MDL_CHECK_LAUNCH("bwd_bounds_kernel");
   hipLaunchKernelGGL(bwd_desc_kernel, dim3((unsigned)T), dim3(256), 0, s, tables, T, w.table_start, w.table_end,
@@ -775,16 +795,17 @@ static int plan(const mdl_table* tables, int32_t T, const uint32_t* sk, int64_t 
 }
 
 static int prepare(const mdl_table* tables, int32_t T, int32_t max_dim, uint32_t* keys, uint32_t* payload,
-                   int64_t n, int32_t key_bits, void* ws, size_t ws_bytes, hipStream_t s, BwdWs* w,
-                   const uint32_t** sk, const uint32_t** sv) {
+                   int64_t n, const int64_t* n_dev, int32_t key_bits, void* ws, size_t ws_bytes, hipStream_t s,
+                   BwdWs* w, const uint32_t** sk, const uint32_t** sv) {
   const size_t need = carve(w, ws, n, T, max_dim);
   if (ws_bytes < need) return fail(MDL_ERR_WORKSPACE, "backward: workspace too small");
   int in_alt = 0;
-  int rc = sort_pairs(keys, payload, w->keys_alt, w->vals_alt, n, key_bits, w->sort_ws, w->sort_bytes, &in_alt, s);
+  int rc = sort_pairs(keys, payload, w->keys_alt, w->vals_alt, n, n_dev, key_bits, w->sort_ws, w->sort_bytes,
+                      &in_alt, s);
   if (rc) return rc;
   *sk = in_alt ? w->keys_alt : keys;
   *sv = in_alt ? w->vals_alt : payload;
-  return plan(tables, T, *sk, n, *w, s);
+  return plan(tables, T, *sk, n, n_dev, *w, s);
 }
 
 static void fill_args(BwdArgs* a, const mdl_feature* feats, int32_t F, const mdl_table* tables, int32_t T,
@@ -843,6 +864,9 @@ struct LaunchReduce {
 // Every reduce launch (all classes) before any fix-up launch: a fix-up reads
 // partials that the reduce of the same table wrote.
 static int run_reduce(const BwdArgs& a, uint32_t variants, hipStream_t s) {
+  if (variants & MDL_CLASSES_UNSUPPORTED)
+    return fail(MDL_ERR_UNSUPPORTED,
+                "backward: a table's rows are wider than its lanes cover (dim > 64 x lane width)");
   const int64_t blocks = (a.max_chunks + kBwdWaves - 1) / kBwdWaves;
   if (blocks > 0x7fffffffll) return fail(MDL_ERR_UNSUPPORTED, "backward: too many chunks");
   int rc = for_each_class(variants, LaunchReduce<false>{a, s, blocks});
@@ -873,7 +897,9 @@ uint32_t mdl_table_classes(const mdl_table* tables, int32_t num_tables) {
   uint32_t m = 0;
   for (int32_t i = 0; i < num_tables; ++i) {
     const mdl_table& t = tables[i];
-    m |= 1u << variant_of(t.wdtype, t.gdtype, table_vec_of(t.weight, t.dim, t.wdtype), t.dim);
+    const int v = variant_of(t.wdtype, t.gdtype, table_vec_of(t.weight, t.dim, t.wdtype), t.dim);
+    m |= 1u << v;
+    if (t.dim > kWave * variant_elems(v)) m |= MDL_CLASSES_UNSUPPORTED;
   }
   return m;
 }
@@ -888,15 +914,15 @@ size_t mdl_backward_workspace_bytes(int64_t n, int32_t num_tables, int32_t max_d
 }
 
 int mdl_backward_sort(const mdl_table* tables, int32_t num_tables, int32_t max_dim, uint32_t* sort_keys,
-                      uint32_t* sort_payload, int64_t n, int32_t key_bits, void* workspace, size_t workspace_bytes,
-                      void* stream) {
+                      uint32_t* sort_payload, int64_t n, const int64_t* count, int32_t key_bits, void* workspace,
+                      size_t workspace_bytes, void* stream) {
   int rc = validate_tables("mdl_backward_sort", num_tables, max_dim, n);
   if (rc) return rc;
   if (n == 0) return MDL_OK;
   BwdWs w;
   const uint32_t *sk, *sv;
-  return prepare(tables, num_tables, max_dim, sort_keys, sort_payload, n, key_bits, workspace, workspace_bytes,
-                 as_stream(stream), &w, &sk, &sv);
+  return prepare(tables, num_tables, max_dim, sort_keys, sort_payload, n, count, key_bits, workspace,
+                 workspace_bytes, as_stream(stream), &w, &sk, &sv);
 }
 
 // Arguments of the calls that follow mdl_backward_sort: the sorted pairs are
@@ -921,6 +947,7 @@ int mdl_backward_apply(const mdl_feature* feats, int32_t num_features, const mdl
                        const float* grad_scale, void* workspace, size_t workspace_bytes, uint32_t classes,
                        void* stream) {
   int rc = validate_tables("mdl_backward_apply", num_tables, max_dim, n);
+  if (!rc) rc = validate_classes("mdl_backward_apply", classes);
   if (rc) return rc;
   if (n == 0) return MDL_OK;
   BwdArgs a;
@@ -939,6 +966,7 @@ int mdl_backward_sumsq(const mdl_feature* feats, int32_t num_features, const mdl
                        int64_t n, int32_t key_bits, const float* bag_count, float* sumsq, void* workspace,
                        size_t workspace_bytes, uint32_t classes, void* stream) {
   int rc = validate_tables("mdl_backward_sumsq", num_tables, max_dim, n);
+  if (!rc) rc = validate_classes("mdl_backward_sumsq", classes);
   if (rc) return rc;
   if (!sumsq) return fail(MDL_ERR_INVALID, "mdl_backward_sumsq: null output");
   hipStream_t s = as_stream(stream);
@@ -956,10 +984,12 @@ int mdl_backward_sumsq(const mdl_feature* feats, int32_t num_features, const mdl
 
 int mdl_backward_adagrad(const mdl_feature* feats, int32_t num_features, const mdl_table* tables,
                          int32_t num_tables, int32_t max_dim, uint32_t* sort_keys, uint32_t* sort_payload,
-                         int64_t n, int32_t key_bits, const float* bag_count, float lr, float eps,
-                         const float* grad_scale, void* workspace, size_t workspace_bytes, uint32_t classes,
-                         void* stream) {
-  int rc = mdl_backward_sort(tables, num_tables, max_dim, sort_keys, sort_payload, n, key_bits, workspace,
+                         int64_t n, const int64_t* count, int32_t key_bits, const float* bag_count, float lr,
+                         float eps, const float* grad_scale, void* workspace, size_t workspace_bytes,
+                         uint32_t classes, void* stream) {
+  int rc = validate_classes("mdl_backward_adagrad", classes);
+  if (rc) return rc;
+  rc = mdl_backward_sort(tables, num_tables, max_dim, sort_keys, sort_payload, n, count, key_bits, workspace,
                              workspace_bytes, stream);
   if (rc) return rc;
   return mdl_backward_apply(feats, num_features, tables, num_tables, max_dim, sort_keys, sort_payload, n,
@@ -967,8 +997,8 @@ int mdl_backward_adagrad(const mdl_feature* feats, int32_t num_features, const m
 }
 
 int mdl_backward_count(const mdl_table* tables, int32_t num_tables, int32_t max_dim, uint32_t* sort_keys,
-                       uint32_t* sort_payload, int64_t n, int32_t key_bits, int64_t* unique_range,
-                       void* workspace, size_t workspace_bytes, void* stream) {
+                       uint32_t* sort_payload, int64_t n, const int64_t* count, int32_t key_bits,
+                       int64_t* unique_range, void* workspace, size_t workspace_bytes, void* stream) {
   int rc = validate_tables("mdl_backward_count", num_tables, max_dim, n);
   if (rc) return rc;
   hipStream_t s = as_stream(stream);
@@ -979,8 +1009,8 @@ int mdl_backward_count(const mdl_table* tables, int32_t num_tables, int32_t max_
     MDL_CHECK_LAUNCH("unique_range_zero");
     return MDL_OK;
   }
-  rc = prepare(tables, num_tables, max_dim, sort_keys, sort_payload, n, key_bits, workspace, workspace_bytes, s,
-               &w, &sk, &sv);
+  rc = prepare(tables, num_tables, max_dim, sort_keys, sort_payload, n, count, key_bits, workspace, workspace_bytes,
+               s, &w, &sk, &sv);
   if (rc) return rc;
   const int64_t mc = max_chunks_for(n, num_tables);
   int64_t* heads = (int64_t*)((char*)workspace + carve(&w, workspace, n, num_tables, max_dim));
@@ -1002,6 +1032,7 @@ int mdl_backward_coalesce(const mdl_feature* feats, int32_t num_features, const 
                           const uint64_t* rows_addr, const uint64_t* values_addr, void* workspace,
                           size_t workspace_bytes, uint32_t classes, void* stream) {
   int rc = validate_tables("mdl_backward_coalesce", num_tables, max_dim, n);
+  if (!rc) rc = validate_classes("mdl_backward_coalesce", classes);
   if (rc) return rc;
   if (n == 0) return MDL_OK;
   hipStream_t s = as_stream(stream);

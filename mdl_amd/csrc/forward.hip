@@ -27,6 +27,7 @@ struct FwdArgs {
   const mdl_chunk* chunks;
   int64_t num_chunks;
   const int64_t* ids;
+  int64_t num_ids;  // entries of ids: every feature's id range is clamped into [0, num_ids)
   const int64_t* offsets;
   uint32_t* keys;
   uint32_t* payload;
@@ -39,7 +40,7 @@ struct FwdArgs {
 struct Feat {
   const void* weight;
   void* out;
-  int64_t num_rows, out_stride, row_base, payload_base, ids_begin, num_ids, bag_base;
+  int64_t num_rows, out_stride, row_base, payload_base, ids_begin, num_ids, bag_base, num_bags;
   int dim, wdtype, odtype, pooling, flags, padding_idx;
 };
 
@@ -61,6 +62,7 @@ __device__ __forceinline__ Feat load_feat(const mdl_feature* p) {
   f.ids_begin = uni64(p->ids_begin);
   f.num_ids = uni64(p->num_ids);
   f.bag_base = uni64(p->bag_base);
+  f.num_bags = uni64(p->num_bags);
   f.dim = uni32(p->dim);
   f.wdtype = uni32(p->wdtype);
   f.odtype = uni32(p->odtype);
@@ -68,6 +70,30 @@ __device__ __forceinline__ Feat load_feat(const mdl_feature* p) {
   f.flags = uni32(p->flags);
   f.padding_idx = uni32(p->padding_idx);
   return f;
+}
+
+// The feature's id range for this call.  With MDL_FLAG_IDS_FROM_OFFSETS it
+// is [offsets[bag_base], offsets[bag_base + nb]) (nb = num_bags, or 1 for an
+// unpooled feature's pseudo-bag), so a batch whose bag lengths change needs no
+// new descriptors: the offsets scan of its lengths places every feature.  The
+// descriptor's [ids_begin, ids_begin + num_ids) is then only a bound.  Either
+// way the range is clamped into the call's [0, num_ids), so lengths that do
+// not add up give an error count and wrong sums, never an access outside ids.
+__device__ __forceinline__ void bind_range(Feat& f, const FwdArgs& a) {
+  int64_t lo = f.ids_begin, hi = f.ids_begin + f.num_ids;
+  if ((f.flags & MDL_FLAG_IDS_FROM_OFFSETS) && a.offsets != nullptr) {
+    const int64_t nb = f.pooling == MDL_POOL_NONE ? 1 : f.num_bags;
+    int64_t olo = uni64(a.offsets[f.bag_base]);
+    int64_t ohi = uni64(a.offsets[f.bag_base + nb]);
+    olo = olo < lo ? lo : (olo > hi ? hi : olo);
+    ohi = ohi < olo ? olo : (ohi > hi ? hi : ohi);
+    lo = olo;
+    hi = ohi;
+  }
+  lo = lo < 0 ? 0 : (lo > a.num_ids ? a.num_ids : lo);
+  hi = hi < lo ? lo : (hi > a.num_ids ? a.num_ids : hi);
+  f.ids_begin = lo;
+  f.num_ids = hi - lo;
 }
 
 __device__ __forceinline__ int feat_variant(const Feat& f) {
@@ -645,11 +671,16 @@ __global__ MDL_OCCUPANCY __launch_bounds__(kFwdWaves * kWave) void forward_kerne
   ch.feature = uni32(a.chunks[c].feature);
   ch.count = uni32(a.chunks[c].count);
   ch.first = uni64(a.chunks[c].first);
-  const Feat f = load_feat(a.feats + ch.feature);
+  Feat f = load_feat(a.feats + ch.feature);
   const int v = feat_variant(f);
   if (v / kWidths != ClassOf<TW, TO, kVec>::value) return;  // another class's launch owns it
+  bind_range(f, a);
   if (f.pooling == MDL_POOL_NONE) {
-    with_width<TW, kVec>(v % kWidths, [&]<int C>() { gather_chunk<TW, TO, C>(f, ch.first, ch.count, a); });
+    // The chunk may reach past a range that is shorter this call.
+    const int64_t left = f.num_ids - ch.first;
+    const int count = left < (int64_t)ch.count ? (left > 0 ? (int)left : 0) : ch.count;
+    if (count > 0)
+      with_width<TW, kVec>(v % kWidths, [&]<int C>() { gather_chunk<TW, TO, C>(f, ch.first, count, a); });
     return;
   }
   if (ch.count > kMaxBagsPerChunk || ch.count <= 0) {
@@ -745,10 +776,11 @@ __global__ __launch_bounds__(kFwdWaves * kWave) void pool_backward_kernel(FwdArg
   const int32_t fi = uni32(a.chunks[c].feature);
   const int32_t count = uni32(a.chunks[c].count);
   const int64_t first = uni64(a.chunks[c].first);
-  const Feat f = load_feat(a.feats + fi);
+  Feat f = load_feat(a.feats + fi);
   const int v = feat_variant(f);
   if (v / kWidths != ClassOf<TW, TO, kVec>::value) return;  // another class's launch owns it
   if (f.pooling == MDL_POOL_NONE || count > kMaxBagsPerChunk || count <= 0) return;
+  bind_range(f, a);
   with_width<TW, kVec>(v % kWidths, [&]<int C>() { unpool_chunk<TW, TO, C>(f, first, count, s_off[w], a); });
 }
 
@@ -1021,10 +1053,11 @@ int64_t mdl_plan_chunks(const mdl_feature* feats, int32_t num_features, int32_t 
 }
 
 int mdl_forward(const mdl_feature* feats, int32_t num_features, const mdl_chunk* chunks,
-                int64_t num_chunks, const int64_t* ids, const int64_t* offsets, uint32_t* sort_keys,
-                uint32_t* sort_payload, uint32_t sentinel, float* bag_count, int32_t* error_count,
-                uint32_t classes, void* stream) {
-  if (num_features < 0 || num_chunks < 0) return fail(MDL_ERR_INVALID, "mdl_forward: negative count");
+                int64_t num_chunks, const int64_t* ids, int64_t num_ids, const int64_t* offsets,
+                uint32_t* sort_keys, uint32_t* sort_payload, uint32_t sentinel, float* bag_count,
+                int32_t* error_count, uint32_t classes, void* stream) {
+  if (num_features < 0 || num_chunks < 0 || num_ids < 0)
+    return fail(MDL_ERR_INVALID, "mdl_forward: negative count");
   if (num_chunks == 0) return MDL_OK;
   if (!feats || !chunks || !ids) return fail(MDL_ERR_INVALID, "mdl_forward: null pointer");
   if ((sort_keys == nullptr) != (sort_payload == nullptr))
@@ -1034,6 +1067,7 @@ int mdl_forward(const mdl_feature* feats, int32_t num_features, const mdl_chunk*
   a.chunks = chunks;
   a.num_chunks = num_chunks;
   a.ids = ids;
+  a.num_ids = num_ids;
   a.offsets = offsets;
   a.keys = sort_keys;
   a.payload = sort_payload;
@@ -1046,9 +1080,10 @@ int mdl_forward(const mdl_feature* feats, int32_t num_features, const mdl_chunk*
 }
 
 int mdl_pool_backward(const mdl_feature* feats, int32_t num_features, const mdl_chunk* chunks,
-                      int64_t num_chunks, const int64_t* ids, const int64_t* offsets, const float* bag_count,
-                      uint32_t classes, void* stream) {
-  if (num_features < 0 || num_chunks < 0) return fail(MDL_ERR_INVALID, "mdl_pool_backward: negative count");
+                      int64_t num_chunks, const int64_t* ids, int64_t num_ids, const int64_t* offsets,
+                      const float* bag_count, uint32_t classes, void* stream) {
+  if (num_features < 0 || num_chunks < 0 || num_ids < 0)
+    return fail(MDL_ERR_INVALID, "mdl_pool_backward: negative count");
   if (num_chunks == 0) return MDL_OK;
   if (!feats || !chunks || !ids || !offsets || !bag_count)
     return fail(MDL_ERR_INVALID, "mdl_pool_backward: null pointer");
@@ -1057,6 +1092,7 @@ int mdl_pool_backward(const mdl_feature* feats, int32_t num_features, const mdl_
   a.chunks = chunks;
   a.num_chunks = num_chunks;
   a.ids = ids;
+  a.num_ids = num_ids;
   a.offsets = offsets;
   a.keys = nullptr;
   a.payload = nullptr;

@@ -35,6 +35,22 @@ static inline int sort_items(int64_t n) {
 constexpr int kDigitBits = 8;
 constexpr int kRadix = 1 << kDigitBits;
 
+// Entries a pass sorts: n_cap, or the count in device memory (clamped to
+// [0, n_cap]) when the caller passes one.  Every launch of a sort is sized
+// for n_cap; the blocks past the live tile count return at once, so a sort
+// whose size is only known on the device needs no host round trip.
+__device__ __forceinline__ int64_t live_count(int64_t n_cap, const int64_t* n_dev) {
+  if (n_dev == nullptr) return n_cap;
+  const int64_t n = *n_dev;
+  return n < 0 ? 0 : (n > n_cap ? n_cap : n);
+}
+
+template <int kSortItems>
+__device__ __forceinline__ int live_tiles(int64_t n) {
+  constexpr int64_t kTile = (int64_t)kSortThreads * kSortItems;
+  return (int)((n + kTile - 1) / kTile);
+}
+
 // Exclusive scan of one value per thread over a block of kSortThreads:
 // shuffles inside each wave, one barrier for the wave totals.  smem holds at
 // least kSortWaves words.
@@ -56,10 +72,13 @@ __device__ __forceinline__ uint32_t block_exclusive_scan_u32(uint32_t v, uint32_
 }
 
 template <int kSortItems>
-__global__ __launch_bounds__(kSortThreads) void radix_upsweep(const uint32_t* __restrict__ keys, int64_t n,
-                                                              int shift, uint32_t mask,
-                                                              uint32_t* __restrict__ counts, int ntiles) {
+__global__ __launch_bounds__(kSortThreads) void radix_upsweep(const uint32_t* __restrict__ keys, int64_t n_cap,
+                                                              const int64_t* __restrict__ n_dev, int shift,
+                                                              uint32_t mask, uint32_t* __restrict__ counts) {
   __shared__ uint32_t hist[kSortWaves][kRadix];
+  const int64_t n = live_count(n_cap, n_dev);
+  const int ntiles = live_tiles<kSortItems>(n);
+  if ((int)blockIdx.x >= ntiles) return;
   const int tid = threadIdx.x, w = tid / kWave;
   for (int i = tid; i < kSortWaves * kRadix; i += kSortThreads) (&hist[0][0])[i] = 0u;
   __syncthreads();
@@ -104,9 +123,12 @@ __global__ __launch_bounds__(kSortThreads) void radix_upsweep(const uint32_t* __
 }
 
 // Exclusive scan of counts[d][0..ntiles) for digit d = blockIdx.x.
-__global__ __launch_bounds__(kSortThreads) void radix_scan(uint32_t* __restrict__ counts, int ntiles,
+template <int kSortItems>
+__global__ __launch_bounds__(kSortThreads) void radix_scan(uint32_t* __restrict__ counts, int64_t n_cap,
+                                                           const int64_t* __restrict__ n_dev,
                                                            uint32_t* __restrict__ digit_total) {
   __shared__ uint32_t smem[kSortThreads];
+  const int ntiles = live_tiles<kSortItems>(live_count(n_cap, n_dev));
   uint32_t* row = counts + (int64_t)blockIdx.x * ntiles;
   uint32_t carry = 0;
   constexpr int kPer = 4;
@@ -139,9 +161,13 @@ __global__ __launch_bounds__(kSortThreads) void radix_scan(uint32_t* __restrict_
 template <int kSortItems>
 __global__ __launch_bounds__(kSortThreads) __attribute__((amdgpu_waves_per_eu(4))) void radix_downsweep(
     const uint32_t* __restrict__ keys_in, const uint32_t* __restrict__ vals_in,
-    uint32_t* __restrict__ keys_out, uint32_t* __restrict__ vals_out, int64_t n, int shift, int bits,
-    const uint32_t* __restrict__ counts, const uint32_t* __restrict__ digit_total, int ntiles) {
+    uint32_t* __restrict__ keys_out, uint32_t* __restrict__ vals_out, int64_t n_cap,
+    const int64_t* __restrict__ n_dev, int shift, int bits, const uint32_t* __restrict__ counts,
+    const uint32_t* __restrict__ digit_total) {
   constexpr int kSortTile = kSortThreads * kSortItems;
+  const int64_t n = live_count(n_cap, n_dev);
+  const int ntiles = live_tiles<kSortItems>(n);
+  if ((int)blockIdx.x >= ntiles) return;
   __shared__ uint32_t s_keys[kSortTile];
   __shared__ uint32_t s_vals[kSortTile];
   __shared__ uint32_t s_wh[kSortWaves][kRadix];
@@ -257,18 +283,23 @@ size_t sort_ws_bytes(int64_t n) {
 }
 
 template <int kSortItems>
-static void radix_pass(const uint32_t* ki, const uint32_t* vi, uint32_t* ko, uint32_t* vo, int64_t n, int shift,
-                       int bits, uint32_t* counts, uint32_t* digit_total, int ntiles, hipStream_t s) {
+static void radix_pass(const uint32_t* ki, const uint32_t* vi, uint32_t* ko, uint32_t* vo, int64_t n,
+                       const int64_t* n_dev, int shift, int bits, uint32_t* counts, uint32_t* digit_total,
+                       int ntiles, hipStream_t s) {
   const uint32_t mask = (1u << bits) - 1u;
-  hipLaunchKernelGGL(radix_upsweep<kSortItems>, dim3(ntiles), dim3(kSortThreads), 0, s, ki, n, shift, mask,
-                     counts, ntiles);
-  hipLaunchKernelGGL(radix_scan, dim3(kRadix), dim3(kSortThreads), 0, s, counts, ntiles, digit_total);
+  hipLaunchKernelGGL(radix_upsweep<kSortItems>, dim3(ntiles), dim3(kSortThreads), 0, s, ki, n, n_dev, shift, mask,
+                     counts);
+  hipLaunchKernelGGL(radix_scan<kSortItems>, dim3(kRadix), dim3(kSortThreads), 0, s, counts, n, n_dev,
+                     digit_total);
   hipLaunchKernelGGL(radix_downsweep<kSortItems>, dim3(ntiles), dim3(kSortThreads), 0, s, ki, vi, ko, vo, n,
-                     shift, bits, counts, digit_total, ntiles);
+                     n_dev, shift, bits, counts, digit_total);
 }
 
+// n is the capacity (launch sizes, workspace); n_dev, when not null, holds
+// the entries actually present (clamped to [0, n]).  The tile size follows
+// n, so a count read on the device sorts with the tiles of its capacity.
 int sort_pairs(uint32_t* keys, uint32_t* vals, uint32_t* keys_alt, uint32_t* vals_alt, int64_t n,
-               int key_bits, void* ws, size_t ws_bytes, int* in_alt, hipStream_t s) {
+               const int64_t* n_dev, int key_bits, void* ws, size_t ws_bytes, int* in_alt, hipStream_t s) {
   *in_alt = 0;
   if (n <= 0 || key_bits <= 0) return MDL_OK;
   if (n > 0xffffffffll) return fail(MDL_ERR_UNSUPPORTED, "radix sort: more than 2^32-1 keys");
@@ -285,9 +316,9 @@ int sort_pairs(uint32_t* keys, uint32_t* vals, uint32_t* keys_alt, uint32_t* val
   int passes = 0;
   for (int shift = 0; shift < key_bits; shift += kDigitBits) {
     const int bits = key_bits - shift < kDigitBits ? key_bits - shift : kDigitBits;
-    if (items == 16) radix_pass<16>(ki, vi, ko, vo, n, shift, bits, counts, digit_total, ntiles, s);
-    else if (items == 8) radix_pass<8>(ki, vi, ko, vo, n, shift, bits, counts, digit_total, ntiles, s);
-    else radix_pass<4>(ki, vi, ko, vo, n, shift, bits, counts, digit_total, ntiles, s);
+    if (items == 16) radix_pass<16>(ki, vi, ko, vo, n, n_dev, shift, bits, counts, digit_total, ntiles, s);
+    else if (items == 8) radix_pass<8>(ki, vi, ko, vo, n, n_dev, shift, bits, counts, digit_total, ntiles, s);
+    else radix_pass<4>(ki, vi, ko, vo, n, n_dev, shift, bits, counts, digit_total, ntiles, s);
     MDL_CHECK_LAUNCH("radix pass");
     uint32_t* t;
     t = ki; ki = ko; ko = t;
@@ -360,8 +391,8 @@ int mdl_sort_pairs(uint32_t* keys, uint32_t* payload, uint32_t* keys_alt, uint32
                    int32_t key_bits, void* workspace, size_t workspace_bytes, int32_t* result_in_alt,
                    void* stream) {
   int in_alt = 0;
-  int rc = sort_pairs(keys, payload, keys_alt, payload_alt, n, key_bits, workspace, workspace_bytes, &in_alt,
-                      as_stream(stream));
+  int rc = sort_pairs(keys, payload, keys_alt, payload_alt, n, nullptr, key_bits, workspace, workspace_bytes,
+                      &in_alt, as_stream(stream));
   if (result_in_alt) *result_in_alt = in_alt;
   return rc;
 }
@@ -401,7 +432,7 @@ int mdl_unique(const int64_t* ids, int64_t n, int32_t key_bits, int64_t* unique_
   hipLaunchKernelGGL(unique_init, dim3(grid_for(n)), dim3(256), 0, s, ids, n, k0, v0);
   MDL_CHECK_LAUNCH("unique_init");
   int in_alt = 0;
-  int rc = sort_pairs(k0, v0, k1, v1, n, key_bits, sort_ws, sort_ws_bytes(n), &in_alt, s);
+  int rc = sort_pairs(k0, v0, k1, v1, n, nullptr, key_bits, sort_ws, sort_ws_bytes(n), &in_alt, s);
   if (rc) return rc;
   uint32_t* ks = in_alt ? k1 : k0;
   uint32_t* vs = in_alt ? v1 : v0;

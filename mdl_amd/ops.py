@@ -494,7 +494,7 @@ def forward_packed(
         bag_count = torch.empty(max(total_rows_out, 1), dtype=torch.float32, device=device)
     check(
         lib().mdl_forward(
-            feats_dev.data_ptr(), len(feats), chunks_dev.data_ptr(), n_chunks, ids_arg.data_ptr(),
+            feats_dev.data_ptr(), len(feats), chunks_dev.data_ptr(), n_chunks, ids_arg.data_ptr(), n,
             _ptr(offsets), _ptr(keys), _ptr(payload), plan.sentinel, _ptr(bag_count),
             error_count.data_ptr(), feature_classes(feats), stream,
         ),
@@ -709,7 +709,7 @@ def pool_backward(
     ids_arg = res.ids if res.ids.numel() else res.keep[-1]
     check(
         lib().mdl_pool_backward(
-            sub_dev.data_ptr(), len(sub), chunks_dev.data_ptr(), n_chunks, ids_arg.data_ptr(),
+            sub_dev.data_ptr(), len(sub), chunks_dev.data_ptr(), n_chunks, ids_arg.data_ptr(), res.ids.numel(),
             res.offsets.data_ptr(), res.bag_count.data_ptr(), feature_classes(sub), _stream(device),
         ),
         "mdl_pool_backward",
@@ -752,13 +752,15 @@ def backward_adagrad(
     norm = None
     if clip_norm is None:
         check(
-            lib().mdl_backward_adagrad(*args, float(lr), float(eps), None, ws.data_ptr(), ws.numel(), classes, stream),
+            lib().mdl_backward_adagrad(*args[:8], None, *args[8:], float(lr), float(eps), None, ws.data_ptr(),
+                                       ws.numel(), classes, stream),
             "mdl_backward_adagrad",
         )
     else:
         check(
             lib().mdl_backward_sort(tables_dev.data_ptr(), len(tables), plan.max_dim, res.keys.data_ptr(),
-                                    res.payload.data_ptr(), n, plan.key_bits, ws.data_ptr(), ws.numel(), stream),
+                                    res.payload.data_ptr(), n, None, plan.key_bits, ws.data_ptr(), ws.numel(),
+                                    stream),
             "mdl_backward_sort",
         )
         sumsq = torch.empty(1, dtype=torch.float32, device=device)
@@ -854,7 +856,7 @@ def backward_coalesce(res: ForwardResult, grads: Sequence[Tensor | None]) -> lis
     urange = torch.zeros(2 * T, dtype=torch.int64, device=device)
     check(
         lib().mdl_backward_count(
-            tables_dev.data_ptr(), T, plan.max_dim, res.keys.data_ptr(), res.payload.data_ptr(), n,
+            tables_dev.data_ptr(), T, plan.max_dim, res.keys.data_ptr(), res.payload.data_ptr(), n, None,
             plan.key_bits, urange.data_ptr(), ws.data_ptr(), ws.numel(), stream,
         ),
         "mdl_backward_count",
@@ -955,6 +957,11 @@ def coalesce_rows(
     tables[0]["wdtype"] = dtype_code(values.dtype)
     tables[0]["feature"] = 0
     tables[0]["gdtype"] = dtype_code(values.dtype)
+    if table_classes(tables) & _lib.MDL_CLASSES_UNSUPPORTED:
+        raise NotImplementedError(
+            f"coalescing rows of {dim} {values.dtype} elements is not supported: the reduce covers at most 64 "
+            "lanes of one 16-byte vector (one element when rows are not 16-byte aligned)"
+        )
     res = ForwardResult(
         plan=plan, device=device, ids=indices, offsets=None, outputs=[values], feats=feats,
         keys=keys, payload=payload, bag_count=None, error_count=err,
@@ -965,7 +972,7 @@ def coalesce_rows(
     urange = torch.zeros(2, dtype=torch.int64, device=device)
     check(
         lib().mdl_backward_count(
-            tables_dev.data_ptr(), 1, dim, keys.data_ptr(), payload.data_ptr(), n, plan.key_bits,
+            tables_dev.data_ptr(), 1, dim, keys.data_ptr(), payload.data_ptr(), n, None, plan.key_bits,
             urange.data_ptr(), ws.data_ptr(), ws.numel(), stream,
         ),
         "mdl_backward_count",

@@ -1,16 +1,21 @@
-"""One fused sparse step over fixed device buffers.
+"""One fused sparse step per batch over a fixed feature layout.
 
-``SparseStep`` binds a feature layout (:class:`mdl_amd.ops.GroupPlan`) to
-persistent buffers -- packed ids, concatenated bag lengths, pooled outputs,
-upstream gradients -- and builds every descriptor, chunk table and workspace
-once.  A step is then launches only, with no host work, allocation or sync:
+``SparseStep`` binds a feature layout (:class:`mdl_amd.ops.GroupPlan`) to its
+outputs, upstream gradients and scratch, and builds every descriptor, chunk
+table and workspace once.  A step is then launches only -- no host work,
+allocation or synchronisation:
 
     lengths -> offsets scan, grouped lookup + pooling (+ sort keys),
     radix sort, segment reduction + row-wise Adagrad.
 
-This is the path of a training loop whose batch layout is fixed (same
-features, batch size and bag-count per feature), e.g. with the pooled outputs
-written straight into the RankMixer token-slot buffer ``[B, sum(dim)]``.
+Any batch of the layout (same features and batch size; bag lengths free)
+runs on the same object: :meth:`SparseStep.bind` points the step at the
+batch's packed ids and bag lengths, the offsets scan places every feature's
+ids on the device, and the sort and reduce take the batch's id count from
+the scan's last offset.  This is what the reference encoder does for every
+training batch (src/model.py:3782-3890), with the pooled outputs written
+straight into caller-given views such as the RankMixer token-slot buffer
+``[B, sum(dim)]``.
 """
 
 from __future__ import annotations
@@ -22,7 +27,11 @@ import torch
 from torch import Tensor
 
 from . import ops
-from ._lib import CHUNK_DTYPE, MDL_POOL_NONE, check, lib
+from ._lib import CHUNK_DTYPE, MDL_FLAG_IDS_FROM_OFFSETS, MDL_POOL_NONE, check, lib
+
+# Descriptor bound of a feature whose ids the offsets place: the call's id
+# count clamps the range anyway.
+_NO_BOUND = 1 << 62
 
 
 def _capture(device: torch.device, fn) -> "torch.cuda.CUDAGraph":
@@ -37,7 +46,26 @@ def _capture(device: torch.device, fn) -> "torch.cuda.CUDAGraph":
     return graph
 
 
+def _as_ids(t: Tensor) -> Tensor:
+    if t.dtype != torch.int64:
+        raise TypeError("sharded embedding indices must be torch.long")
+    return t.contiguous()
+
+
 class SparseStep:
+    """Fused lookup/pooling + backward + row-wise Adagrad for one layout.
+
+    ``packed_ids``: every feature's ids back to back (device int64);
+    ``lengths``: every pooled feature's bag lengths back to back, with one
+    pseudo-length (its id count) per unpooled feature, in feature order --
+    None when no feature is pooled; ``id_counts`` / ``bag_counts``: per
+    feature, for this first batch (they size the chunks; bag counts are the
+    batch size of each pooled feature and stay fixed, and so does the id count
+    of an unpooled feature, one per output row).  ``capacity`` bounds the ids
+    of any batch bound later (default: this batch's).  Outputs and gradients
+    are 2-D row views (e.g. column slices of one ``[B, sum(dim)]`` buffer).
+    """
+
     def __init__(
         self,
         plan: ops.GroupPlan,
@@ -49,15 +77,17 @@ class SparseStep:
         grads: Sequence[Tensor],
         *,
         error_count: Tensor | None = None,
+        capacity: int | None = None,
     ) -> None:
         for t in plan.tables:
             if t.state is None:
                 raise RuntimeError("every table needs a row-wise Adagrad accumulator")
         self.plan = plan
         self.device = packed_ids.device
-        self.ids = packed_ids.contiguous()
-        self.n = int(self.ids.numel())
+        self.ids = _as_ids(packed_ids)
+        self.capacity = max(int(self.ids.numel()) if capacity is None else int(capacity), int(self.ids.numel()))
         pooled_any = any(s.pooling != MDL_POOL_NONE for s in plan.features)
+        self.dynamic = pooled_any
         self.lengths = None
         self.offsets = None
         if pooled_any:
@@ -72,15 +102,20 @@ class SparseStep:
         )
         out_ptrs = [o.data_ptr() for o in outputs]
         out_strides = [o.stride(0) if o.ndim == 2 else int(o.size(-1)) for o in outputs]
-        self.feats_fwd = ops.build_features(plan, id_counts, bag_counts, out_ptrs, out_strides)
-        target = ops.forward_target_ids(self.feats_fwd)
-        n_chunks = lib().mdl_plan_chunks(self.feats_fwd.ctypes.data, len(self.feats_fwd), target, None, 0)
+        feats = ops.build_features(plan, id_counts, bag_counts, out_ptrs, out_strides)
+        target = ops.forward_target_ids(feats)
+        n_chunks = lib().mdl_plan_chunks(feats.ctypes.data, len(feats), target, None, 0)
         if n_chunks < 0:
             check(int(n_chunks), "mdl_plan_chunks")
         chunks = np.zeros(max(n_chunks, 1), dtype=CHUNK_DTYPE)
-        lib().mdl_plan_chunks(self.feats_fwd.ctypes.data, len(self.feats_fwd), target, chunks.ctypes.data,
-                              n_chunks)
+        lib().mdl_plan_chunks(feats.ctypes.data, len(feats), target, chunks.ctypes.data, n_chunks)
         self.n_chunks = int(n_chunks)
+        if self.dynamic:
+            # The offsets of each call place every feature's ids.
+            feats["flags"] |= MDL_FLAG_IDS_FROM_OFFSETS
+            feats["ids_begin"] = 0
+            feats["num_ids"] = _NO_BOUND
+        self.feats_fwd = feats
         res = ops.ForwardResult(
             plan=plan, device=self.device, ids=self.ids, offsets=None, outputs=list(outputs),
             feats=self.feats_fwd, keys=None, payload=None, bag_count=None, error_count=self.error_count,
@@ -94,23 +129,61 @@ class SparseStep:
         self.feats_bwd_dev = ops.upload(self.feats_bwd, self.device)
         self.tables_dev = ops.upload(self.tables, self.device)
         total_rows = int(
-            np.where(self.feats_fwd["pooling"] != MDL_POOL_NONE, self.feats_fwd["num_bags"],
-                     self.feats_fwd["num_ids"]).sum()
+            np.where(feats["pooling"] != MDL_POOL_NONE, feats["num_bags"], np.asarray(id_counts)).sum()
         )
-        self.keys = torch.empty(max(self.n, 1), dtype=torch.int32, device=self.device)
-        self.payload = torch.empty(max(self.n, 1), dtype=torch.int32, device=self.device)
+        cap = max(self.capacity, 1)
+        self.keys = torch.empty(cap, dtype=torch.int32, device=self.device)
+        self.payload = torch.empty(cap, dtype=torch.int32, device=self.device)
         self.bag_count = (
             torch.empty(max(total_rows, 1), dtype=torch.float32, device=self.device) if pooled_any else None
         )
         self.ws = ops._workspace(
-            lib().mdl_backward_workspace_bytes(self.n, len(self.tables), plan.max_dim), self.device
+            lib().mdl_backward_workspace_bytes(self.capacity, len(self.tables), plan.max_dim), self.device
         )
         self.sumsq = torch.zeros(1, dtype=torch.float32, device=self.device)
         self.norm = torch.zeros(1, dtype=torch.float32, device=self.device)
         self.coef = torch.ones(1, dtype=torch.float32, device=self.device)
 
+    # ----------------------------------------------------------- batches --
+
+    def bind(self, packed_ids: Tensor, lengths: Tensor | None = None) -> None:
+        """Point the next steps at another batch of this layout (no copy, no
+        sync).  A captured graph keeps the buffers it was recorded with: to
+        replay it on a new batch, copy the batch into ``self.ids`` /
+        ``self.lengths`` instead."""
+
+        ids = _as_ids(packed_ids)
+        if ids.device != self.device:
+            raise ValueError("ids must live on the step's device")
+        if int(ids.numel()) > self.capacity:
+            raise ValueError(f"batch of {ids.numel()} ids exceeds the step's capacity of {self.capacity}")
+        if not self.dynamic:
+            if int(ids.numel()) != int(self.ids.numel()):
+                raise ValueError("a layout without pooled features keeps its id count")
+        elif lengths is not None:
+            ln = lengths if lengths.dtype == torch.int64 else lengths.to(torch.int64)
+            ln = ln.contiguous()
+            if ln.shape != self.lengths.shape or ln.device != self.device:
+                raise ValueError("bag lengths must keep the layout's shape and device")
+            self.lengths = ln
+        self.ids = ids
+
+    @property
+    def count(self) -> Tensor | None:
+        """Device int64 [1]: ids of the bound batch (the scan's last offset)."""
+
+        return None if self.offsets is None else self.offsets[-1:]
+
     def _stream(self) -> int:
         return torch.cuda.current_stream(self.device).cuda_stream
+
+    def _count_ptr(self):
+        return None if self.offsets is None else self.offsets.data_ptr() + 8 * (self.offsets.numel() - 1)
+
+    def _n(self) -> int:
+        return self.capacity if self.dynamic else int(self.ids.numel())
+
+    # ------------------------------------------------------------- steps --
 
     def forward(self) -> None:
         """Offsets scan + grouped lookup/pooling (+ backward sort keys)."""
@@ -124,11 +197,13 @@ class SparseStep:
                 ),
                 "mdl_lengths_to_offsets",
             )
+        ids = self.ids if self.ids.numel() else self.keys  # any valid address; nothing is read
         check(
             lib().mdl_forward(
                 self.feats_fwd_dev.data_ptr(), len(self.feats_fwd), self.chunks_dev.data_ptr(), self.n_chunks,
-                self.ids.data_ptr(), ops._ptr(self.offsets), self.keys.data_ptr(), self.payload.data_ptr(),
-                self.plan.sentinel, ops._ptr(self.bag_count), self.error_count.data_ptr(), self.fwd_classes, s,
+                ids.data_ptr(), int(self.ids.numel()), ops._ptr(self.offsets), self.keys.data_ptr(),
+                self.payload.data_ptr(), self.plan.sentinel, ops._ptr(self.bag_count), self.error_count.data_ptr(),
+                self.fwd_classes, s,
             ),
             "mdl_forward",
         )
@@ -139,8 +214,8 @@ class SparseStep:
         check(
             lib().mdl_backward_sort(
                 self.tables_dev.data_ptr(), len(self.tables), self.plan.max_dim, self.keys.data_ptr(),
-                self.payload.data_ptr(), self.n, self.plan.key_bits, self.ws.data_ptr(), self.ws.numel(),
-                self._stream(),
+                self.payload.data_ptr(), self._n(), self._count_ptr(), self.plan.key_bits, self.ws.data_ptr(),
+                self.ws.numel(), self._stream(),
             ),
             "mdl_backward_sort",
         )
@@ -148,7 +223,7 @@ class SparseStep:
     def _bwd_args(self) -> tuple:
         return (
             self.feats_bwd_dev.data_ptr(), len(self.feats_bwd), self.tables_dev.data_ptr(), len(self.tables),
-            self.plan.max_dim, self.keys.data_ptr(), self.payload.data_ptr(), self.n, self.plan.key_bits,
+            self.plan.max_dim, self.keys.data_ptr(), self.payload.data_ptr(), self._n(), self.plan.key_bits,
             ops._ptr(self.bag_count),
         )
 
@@ -196,9 +271,10 @@ class SparseStep:
     def capture(self, lr: float, eps: float, clip_norm: float | None = None) -> None:
         """Record step(lr, eps, clip_norm) as one HIP graph; replay() then
         issues every launch of the step at once (the host no longer paces
-        short steps).  Nothing runs while recording; the step's buffers are
-        its own, so a new batch of the same layout is copied into them before
-        a replay.  Call it after one eager step, which loads the kernels."""
+        short steps).  Nothing runs while recording; the graph reads the
+        buffers bound at capture time, so a new batch is copied into them
+        before a replay (its lengths may differ).  Call it after one eager
+        step, which loads the kernels."""
 
         self._graph = _capture(self.device, lambda: self.step(lr, eps, clip_norm))
 
@@ -214,6 +290,11 @@ class SequenceStep:
     backward reads the window's gradient.  Forward: one gather launch per
     feature; backward: one sort and one segment-reduce + row-wise Adagrad over
     all features together.
+
+    Sort keys are packed: row b of feature f keeps min(len, L_in, L_out)
+    entries (the positions that reach the window), placed each step by one
+    scan of those clamped lengths on the device, so the backward sorts no
+    padding and any lengths of a later batch are honoured.
     """
 
     def __init__(
@@ -233,37 +314,32 @@ class SequenceStep:
                 raise RuntimeError("every table needs a row-wise Adagrad accumulator")
         self.plan = plan
         self.device = ids[0].device
-        self.ids = [t.contiguous() for t in ids]
+        self.ids = [_as_ids(t) for t in ids]
         self.lengths = [t.to(torch.int64).contiguous() for t in lengths]
         self.outputs = list(outputs)
         self.masks = list(masks)
         self.grads = [g.contiguous() for g in grads]
+        if order not in ("oldest_to_newest", "newest_to_oldest"):
+            raise ValueError("order must be oldest_to_newest or newest_to_oldest")
         self.order = ops._lib.MDL_SEQ_OLDEST_TO_NEWEST if order == "oldest_to_newest" else ops._lib.MDL_SEQ_NEWEST_TO_OLDEST
         self.error_count = (
             error_count if error_count is not None else torch.zeros(1, dtype=torch.int32, device=self.device)
         )
-        # Sort keys are packed: row b of feature f keeps min(len, L_in, L_out)
-        # entries (the positions that reach the window), so the backward
-        # sorts no padding.  The lengths are read once here, like the id
-        # counts of SparseStep: a step object serves one batch layout.
+        self.batch = [int(t.size(0)) for t in self.ids]
+        self.caps = [min(int(i.size(1)), int(o.size(1))) for i, o in zip(self.ids, self.outputs)]
+        self.row_base = np.concatenate([[0], np.cumsum(self.batch)]).astype(np.int64)
+        total_rows = int(self.row_base[-1])
+        # Entries a step can hold: every row at its cap.
+        self.capacity = int(sum(b * c for b, c in zip(self.batch, self.caps)))
+        self.key_len = torch.empty(max(total_rows, 1), dtype=torch.int64, device=self.device)
+        self.offsets = torch.empty(total_rows + 1, dtype=torch.int64, device=self.device)
+        self.scan_ws = ops._workspace(lib().mdl_offsets_workspace_bytes(total_rows), self.device)
+        cap = max(self.capacity, 1)
+        self.keys = torch.empty(cap, dtype=torch.int32, device=self.device)
+        self.payload = torch.empty(cap, dtype=torch.int32, device=self.device)
         feats = []
         self.fwd_feats = []
-        key_off = 0
         payload_base = 0
-        self.key_offsets = []
-        self.row_offsets = []
-        for f, spec in enumerate(plan.features):
-            out = self.outputs[f]
-            L_in = int(self.ids[f].size(1))
-            kept = np.clip(self.lengths[f].cpu().numpy(), 0, min(L_in, int(out.size(1))))
-            offs = np.zeros(kept.size + 1, dtype=np.int64)
-            np.cumsum(kept, out=offs[1:])
-            self.row_offsets.append(ops.upload(offs, self.device))
-            self.key_offsets.append(key_off)
-            key_off += int(offs[-1])
-        self.n = key_off
-        self.keys = torch.empty(max(self.n, 1), dtype=torch.int32, device=self.device)
-        self.payload = torch.empty(max(self.n, 1), dtype=torch.int32, device=self.device)
         for f, spec in enumerate(plan.features):
             table = plan.tables[spec.table]
             out = self.outputs[f]
@@ -282,24 +358,54 @@ class SequenceStep:
         self.feats_bwd_dev = ops.upload(self.feats_bwd, self.device)
         self.tables_dev = ops.upload(self.tables, self.device)
         self.ws = ops._workspace(
-            lib().mdl_backward_workspace_bytes(self.n, len(self.tables), plan.max_dim), self.device
+            lib().mdl_backward_workspace_bytes(self.capacity, len(self.tables), plan.max_dim), self.device
         )
+
+    def bind(self, ids: Sequence[Tensor] | None = None, lengths: Sequence[Tensor] | None = None) -> None:
+        """Point the next steps at another batch (same shapes; any lengths)."""
+
+        if ids is not None:
+            new = [_as_ids(t) for t in ids]
+            if [tuple(t.shape) for t in new] != [tuple(t.shape) for t in self.ids]:
+                raise ValueError("sequence ids must keep their [B, L_in] shapes")
+            self.ids = new
+        if lengths is not None:
+            new = [t.to(torch.int64).contiguous() for t in lengths]
+            if [tuple(t.shape) for t in new] != [tuple(t.shape) for t in self.lengths]:
+                raise ValueError("sequence lengths must keep their [B] shapes")
+            self.lengths = new
+
+    @property
+    def count(self) -> Tensor:
+        """Device int64 [1]: packed sort entries of the bound batch."""
+
+        return self.offsets[-1:]
 
     def _stream(self) -> int:
         return torch.cuda.current_stream(self.device).cuda_stream
 
     def forward(self) -> None:
         s = self._stream()
+        # Entries each row keeps (its positions that reach the window), then
+        # one scan over every feature's rows places them.
+        for f, ln in enumerate(self.lengths):
+            b0, b1 = int(self.row_base[f]), int(self.row_base[f + 1])
+            torch.clamp(ln, 0, self.caps[f], out=self.key_len[b0:b1])
+        nrows = int(self.row_base[-1])
+        check(
+            lib().mdl_lengths_to_offsets(self.key_len.data_ptr(), nrows, self.offsets.data_ptr(),
+                                         self.scan_ws.data_ptr(), self.scan_ws.numel(), s),
+            "mdl_lengths_to_offsets",
+        )
         for f, rec in enumerate(self.fwd_feats):
             ids = self.ids[f]
             out = self.outputs[f]
-            off = self.key_offsets[f]
             check(
                 lib().mdl_sequence_forward(
                     rec.ctypes.data, ids.data_ptr(), self.lengths[f].data_ptr(), ids.size(0), ids.size(1),
-                    out.size(1), self.order, out.data_ptr(), self.masks[f].data_ptr(),
-                    self.keys.data_ptr() + 4 * off, self.payload.data_ptr() + 4 * off,
-                    self.row_offsets[f].data_ptr(), self.plan.sentinel, self.error_count.data_ptr(), s,
+                    out.size(1), self.order, out.data_ptr(), self.masks[f].data_ptr(), self.keys.data_ptr(),
+                    self.payload.data_ptr(), self.offsets.data_ptr() + 8 * int(self.row_base[f]), self.plan.sentinel,
+                    self.error_count.data_ptr(), s,
                 ),
                 "mdl_sequence_forward",
             )
@@ -308,8 +414,8 @@ class SequenceStep:
         check(
             lib().mdl_backward_sort(
                 self.tables_dev.data_ptr(), len(self.tables), self.plan.max_dim, self.keys.data_ptr(),
-                self.payload.data_ptr(), self.n, self.plan.key_bits, self.ws.data_ptr(), self.ws.numel(),
-                self._stream(),
+                self.payload.data_ptr(), self.capacity, self.offsets.data_ptr() + 8 * int(self.row_base[-1]),
+                self.plan.key_bits, self.ws.data_ptr(), self.ws.numel(), self._stream(),
             ),
             "mdl_backward_sort",
         )
@@ -318,7 +424,7 @@ class SequenceStep:
         check(
             lib().mdl_backward_apply(
                 self.feats_bwd_dev.data_ptr(), len(self.feats_bwd), self.tables_dev.data_ptr(), len(self.tables),
-                self.plan.max_dim, self.keys.data_ptr(), self.payload.data_ptr(), self.n, self.plan.key_bits,
+                self.plan.max_dim, self.keys.data_ptr(), self.payload.data_ptr(), self.capacity, self.plan.key_bits,
                 None, float(lr), float(eps), None, self.ws.data_ptr(), self.ws.numel(), self.bwd_classes,
                 self._stream(),
             ),

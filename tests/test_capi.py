@@ -86,13 +86,18 @@ def test_invalid_arguments_fail_before_any_launch():
     assert rc == -1 and b"key_bits" in lib.mdl_last_error()
     rc = lib.mdl_sort_pairs(None, None, None, None, 1 << 33, 8, None, 0, None, None)
     assert rc == -4
-    rc = lib.mdl_backward_adagrad(None, 0, None, 0, 8, None, None, 10, 8, None, 0.1, 1e-8, None, None, 0, 0, None)
+    rc = lib.mdl_backward_adagrad(None, 0, None, 0, 8, None, None, 10, None, 8, None, 0.1, 1e-8, None, None, 0, 0,
+                                  None)
     assert rc == -1 and b"table" in lib.mdl_last_error()
+    rc = lib.mdl_backward_apply(None, 0, None, 1, 600, None, None, 10, 8, None, 0.1, 1e-8, None, None, 0, 0, None)
+    assert rc == -4 and b"512" in lib.mdl_last_error()
+    rc = lib.mdl_forward(None, 0, None, 1, None, -1, None, None, None, 0, None, None, 0, None)
+    assert rc == -1
     rc = lib.mdl_rowwise_adagrad(None, _lib.MDL_F32, 10, 4, 4, None, None, 3, None, _lib.MDL_BF16, 4, 0.1,
                                  1e-8, None, None)
     assert rc == -1  # null pointers
     # zero-sized work is a no-op success without touching the device
-    assert lib.mdl_forward(None, 0, None, 0, None, None, None, None, 0, None, None, 0, None) == 0
+    assert lib.mdl_forward(None, 0, None, 0, None, 0, None, None, None, 0, None, None, 0, None) == 0
     assert lib.mdl_rowwise_adagrad(None, 0, 0, 4, 4, None, None, 0, None, 0, 4, 0.1, 1e-8, None, None) == 0
 
 
@@ -168,4 +173,35 @@ def test_lane_width_rule_matches_the_library():
             c = ops.lane_elems(dim, esize, vec)
             cls = (0 if wd == _lib.MDL_F32 else 2) + (0 if vec else 1)
             w = 0 if c == 1 else {4: 0, 8: 1, 16: 2}[c]
-            assert m == 1 << (3 * cls + w), (wd, dim)
+            wide = _lib.MDL_CLASSES_UNSUPPORTED if dim > 64 * c else 0
+            assert m == (1 << (3 * cls + w)) | wide, (wd, dim)
+
+
+@pytest.mark.parametrize("dim,dtype", [(66, "f32"), (100, "bf16"), (300, "f32"), (600, "f32")])
+def test_too_wide_rows_are_refused_not_skipped(dim, dtype):
+    """Rows the backward reduce cannot cover are reported by the class mask,
+    and every reducing call refuses that mask before it launches anything."""
+
+    lib = _lib.lib()
+    tables = np.zeros(1, dtype=_lib.TABLE_DTYPE)
+    code = _lib.MDL_F32 if dtype == "f32" else _lib.MDL_BF16
+    tables["wdtype"] = code
+    tables["gdtype"] = code
+    tables["dim"] = dim
+    tables["weight"] = 4096
+    m = lib.mdl_table_classes(tables.ctypes.data, 1)
+    assert m & _lib.MDL_CLASSES_UNSUPPORTED
+    for call in (
+        lambda: lib.mdl_backward_apply(None, 1, None, 1, 512, None, None, 10, 8, None, 0.1, 1e-8, None, None, 0,
+                                       m, None),
+        lambda: lib.mdl_backward_sumsq(None, 1, None, 1, 512, None, None, 10, 8, None, None, None, 0, m, None),
+        lambda: lib.mdl_backward_coalesce(None, 1, None, 1, 512, None, None, 10, 8, None, None, None, None, None, 0,
+                                          m, None),
+        lambda: lib.mdl_backward_adagrad(None, 1, None, 1, 512, None, None, 10, None, 8, None, 0.1, 1e-8, None, None,
+                                         0, m, None),
+    ):
+        assert call() == -4 and b"wider" in lib.mdl_last_error()
+
+
+def test_abi_version_matches_binding():
+    assert _lib.lib().mdl_abi_version() == _lib.ABI_VERSION

@@ -586,8 +586,11 @@ def test_hot_row_spanning_hundreds_of_chunks(device, mode):
 
 
 @pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
-@pytest.mark.parametrize("dim", [2, 16, 48, 128, 256])
+@pytest.mark.parametrize("dim", [2, 16, 24, 48, 66, 100, 128, 256, 300, 384, 520])
 def test_rowwise_adagrad_matches_oracle(device, dtype, dim):
+    """Any dim, like the reference kernel (BLOCK = next_pow2(dim)): rows
+    wider than 64 lanes cover (fp32 300/384/520, unaligned 66/100) take the
+    column-block walk."""
     rng = np.random.default_rng(60 + dim)
     announce("rowwise_adagrad", dtype, dim)
     rows = 3000
@@ -614,6 +617,105 @@ def test_coalesce_rows_matches_torch(device):
     _, vabs = O.coalesce(idx, np.abs(vals.astype(np.float64)))
     assert np.array_equal(r.cpu().numpy(), rr)
     assert_close(v.cpu().numpy(), vv, 1e-5, 1e-6, vabs)
+
+
+@pytest.mark.parametrize("dim,dtype", [(66, torch.float32), (100, torch.bfloat16), (600, torch.float32)])
+def test_coalesce_rows_refuses_rows_too_wide(device, dim, dtype):
+    """The backward reduce covers 64 lanes of a row; wider rows raise
+    instead of returning unwritten memory as a gradient."""
+    announce("coalesce_rows_too_wide", dim, dtype)
+    idx = torch.tensor([3, 1, 3], dtype=torch.int64, device=device)
+    vals = torch.ones((3, dim), dtype=dtype, device=device)
+    with pytest.raises(NotImplementedError):
+        ops.coalesce_rows(idx, vals, 10)
+
+
+def _oracle_step_pooled(W, rows, dims, pools, ids, lens, grad, lr, eps, accs=None):
+    """Oracle of one SparseStep over full tables (copies updated in place)."""
+    B = grad.shape[0]
+    cols = np.concatenate([[0], np.cumsum(dims)[:-1]])
+    feats, offs, bag_off, ids_off = [], [], 0, 0
+    for t, (p, x, ln) in enumerate(zip(pools, ids, lens)):
+        feats.append({"table": t, "pooling": {"none": 0, "sum": 1, "mean": 2}[p], "exclude": 1, "ids_off": ids_off,
+                      "bag_off": bag_off, "num_bags": 0 if ln is None else B, "out_col": int(cols[t])})
+        if ln is not None:
+            o = O.offsets_of(ln)
+            offs.append(o)
+            bag_off += len(o)
+        ids_off += x.size
+    tables = [{"W": w, "acc": a} for w, a in zip(W, accs)]
+    out = O.sparse_step(feats, tables, np.concatenate(ids), np.concatenate(offs), sum(dims), grad, lr, eps)
+    absw = [{"W": np.abs(w), "acc": np.zeros(r, np.float32)} for w, r in zip(W, rows)]
+    scale = O.sparse_step(feats, absw, np.concatenate(ids), np.concatenate(offs), sum(dims), np.zeros_like(grad),
+                          0.0, 1.0)
+    return out, scale
+
+
+def test_sparse_step_serves_batches_of_any_bag_lengths(device):
+    """One SparseStep, bound to four batches whose bag lengths (and so id
+    counts) differ, including one with fewer ids and one with more than the
+    batch it was built from: each step matches the oracle continuing from
+    the previous step's tables."""
+
+    from mdl_amd.sparse_step import SparseStep
+
+    rng = np.random.default_rng(84)
+    B = 384
+    rows = [2500, 700, 9000, 300]
+    dims = [32, 16, 64, 24]
+    pools = ["mean", "none", "sum", "mean"]
+    W = [rng.standard_normal((r, d)).astype(np.float32) for r, d in zip(rows, dims)]
+    for w in W:
+        w[0] = 0
+    tabs = [torch.from_numpy(w.copy()).to(device) for w in W]
+    accs = [torch.zeros(r, device=device) for r in rows]
+    ref_acc = [np.zeros(r, np.float32) for r in rows]
+    plan = ops.GroupPlan()
+    for t, p in enumerate(pools):
+        plan.add_feature(tabs[t], pooling=p, null_policy="exclude", state=accs[t])
+    S = sum(dims)
+    cols = np.concatenate([[0], np.cumsum(dims)[:-1]])
+    out = torch.empty((B, S), device=device)
+    grad = torch.empty((B, S), device=device)
+    views = [slice(int(c), int(c) + d) for c, d in zip(cols, dims)]
+
+    def batch(max_len):
+        ids, lens = [], []
+        for t, p in enumerate(pools):
+            if p == "none":
+                ids.append((rng.zipf(1.2, size=B) % rows[t]).astype(np.int64))
+                lens.append(None)
+            else:
+                ln = rng.integers(0, max_len + 1, size=B)
+                ids.append((rng.zipf(1.2, size=int(ln.sum())) % rows[t]).astype(np.int64))
+                lens.append(ln)
+        parts = [ln if ln is not None else np.array([x.size]) for x, ln in zip(ids, lens)]
+        return ids, lens, torch.from_numpy(np.concatenate(ids)).to(device), \
+            torch.from_numpy(np.concatenate(parts).astype(np.int64)).to(device)
+
+    batches = [batch(m) for m in (12, 3, 30, 12)]
+    cap = max(int(b[2].numel()) for b in batches)
+    ids0, lens0, p0, l0 = batches[0]
+    st = SparseStep(plan, p0, l0, [x.size for x in ids0], [0 if ln is None else B for ln in lens0],
+                    [out[:, v] for v in views], [grad[:, v] for v in views], capacity=cap)
+    for k, (ids, lens, packed, lengths) in enumerate(batches):
+        announce("sparse_step_rebind", k, int(packed.numel()))
+        g = rng.standard_normal((B, S)).astype(np.float32)
+        grad.copy_(torch.from_numpy(g))
+        st.bind(packed, lengths)
+        st.step(0.02, 1e-8)
+        ref_out, scale = _oracle_step_pooled(W, rows, dims, pools, ids, lens, g.astype(np.float64), 0.02, 1e-8,
+                                             ref_acc)
+        assert_close(out.cpu().numpy(), ref_out, 1e-5, 1e-6, scale)
+        for t in range(len(rows)):
+            assert_close(accs[t].cpu().numpy(), ref_acc[t], 1e-5, 1e-6)
+            assert_close(tabs[t].cpu().numpy(), W[t], 1e-5, 1e-5)
+            # continue from the device's tables so tolerances do not compound
+            W[t][:] = tabs[t].cpu().numpy()
+            ref_acc[t][:] = accs[t].cpu().numpy()
+    assert int(st.error_count.item()) == 0
+    with pytest.raises(ValueError):
+        st.bind(torch.zeros(cap + 1, dtype=torch.int64, device=device), batches[0][3])
 
 
 def test_sparse_step_slot_buffer_matches_oracle(device):
@@ -711,8 +813,8 @@ def test_sequence_step_matches_oracle(device, L_out, order, dtype):
              for _ in range(2)]
     st = SequenceStep(plan, [torch.from_numpy(m).to(device) for m in ids],
                       [torch.from_numpy(ln).to(device) for ln in lens], outs, masks, grads, order=order)
-    assert st.n == sum(int(np.minimum(ln, L_out).sum()) for ln in lens)
     st.step(0.03, 1e-8)
+    assert int(st.count.item()) == sum(int(np.minimum(ln, L_out).sum()) for ln in lens)
     bf16 = dtype == torch.bfloat16
     for t in range(2):
         ref, rmask = O.sequence_gather(W[t], ids[t], lens[t], L_out, order)
@@ -760,6 +862,54 @@ def _slot_step(device, seed):
     st = SparseStep(plan, packed, lens, [bag.size, B], [B, 0], [out[:, v] for v in views],
                     [grad[:, v] for v in views])
     return st, tabs, states, out
+
+
+def test_sequence_step_rebound_to_longer_rows_matches_oracle(device):
+    """A SequenceStep built on short rows, then bound to rows up to the
+    window: every position of the longer rows gets its gradient (the packed
+    keys are placed each step from the bound lengths)."""
+    from mdl_amd.sparse_step import SequenceStep
+
+    rng = np.random.default_rng(85)
+    B, L, rows = 48, 160, 6000
+    tab = _table(rng, rows, 32, torch.float32, device)
+    acc = torch.zeros(rows, device=device)
+    plan = ops.GroupPlan()
+    plan.add_feature(tab, pooling="none", state=acc)
+    out = torch.empty((B, L, 32), device=device)
+    mask = torch.empty((B, L), dtype=torch.bool, device=device)
+    grad = torch.empty((B, L, 32), device=device)
+
+    def seq(max_len):
+        ln = rng.integers(0, max_len + 1, size=B)
+        m = np.zeros((B, L), dtype=np.int64)
+        for b in range(B):
+            k = min(int(ln[b]), L)  # lengths past the input are clamped to it
+            m[b, :k] = rng.zipf(1.1, size=k) % rows
+        return m, ln
+
+    first = seq(10)
+    st = SequenceStep(plan, [torch.from_numpy(first[0]).to(device)], [torch.from_numpy(first[1]).to(device)], [out],
+                      [mask], [grad])
+    W = to_np(tab).copy()
+    A = np.zeros(rows, np.float32)
+    for k, (m, ln) in enumerate([first, seq(L), seq(L + 40), seq(60)]):
+        announce("sequence_rebind", k, int(np.minimum(ln, L).sum()))
+        g = rng.standard_normal((B, L, 32)).astype(np.float32)
+        grad.copy_(torch.from_numpy(g))
+        st.bind([torch.from_numpy(m).to(device)], [torch.from_numpy(ln).to(device)])
+        st.step(0.03, 1e-8)
+        assert int(st.count.item()) == int(np.minimum(ln, L).sum())
+        ref, rmask = O.sequence_window(W, m, ln, L)
+        assert np.array_equal(mask.cpu().numpy(), rmask)
+        assert np.array_equal(out.cpu().numpy(), ref)
+        r, v = O.sequence_grads(m, ln, g, L)
+        rr, vv = O.coalesce(r, v)
+        wexp, aexp = O.rowwise_adagrad(W, A, rr, vv, 0.03, 1e-8)
+        assert_close(acc.cpu().numpy(), aexp, 1e-5, 1e-7)
+        assert_close(to_np(tab), wexp, 1e-5, 1e-6)
+        W = to_np(tab).copy()
+        A = acc.cpu().numpy().copy()
 
 
 @pytest.mark.parametrize("clip", [None, 0.5])

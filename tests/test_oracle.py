@@ -402,3 +402,50 @@ def test_clip_grad_norm_matches_torch_clip_grad_norm(max_norm):
         assert coef == 1.0
         for g, v in zip(got, vals):
             np.testing.assert_array_equal(g, v)
+
+
+def test_torch_cpu_path_equals_c_oracle():
+    """The PyTorch CPU restatement of the reference step (the bench's CPU
+    baseline) and the C oracle agree on pooled outputs and updated tables."""
+
+    from oracle import torch_path as TP
+
+    rng = np.random.default_rng(31)
+    B = 40
+    rows = [60, 25, 90]
+    dims = [4, 8, 16]
+    pools = ["mean", "none", "sum"]
+    W = [rng.standard_normal((r, d)).astype(np.float32) for r, d in zip(rows, dims)]
+    for w in W:
+        w[0] = 0
+    ids, lens = [], []
+    for t, p in enumerate(pools):
+        if p == "none":
+            ids.append(rng.integers(0, rows[t], size=B))
+            lens.append(None)
+        else:
+            ln = rng.integers(0, 6, size=B)
+            ids.append(rng.integers(0, rows[t], size=int(ln.sum())))
+            lens.append(ln)
+    grad = rng.standard_normal((B, sum(dims)))
+    cols = np.concatenate([[0], np.cumsum(dims)[:-1]])
+    step = TP.TorchStep([torch.from_numpy(w.copy()) for w in W], [torch.full((r,), 0.5) for r in rows],
+                        [TP.Feature(t, p) for t, p in enumerate(pools)])
+    outs = step.step([torch.from_numpy(x) for x in ids], [None if ln is None else torch.from_numpy(ln) for ln in lens],
+                     [torch.from_numpy(grad[:, c: c + d]).float() for c, d in zip(cols, dims)], 0.05, 1e-8)
+    feats, offs, bag_off, ids_off = [], [], 0, 0
+    for t, (p, x, ln) in enumerate(zip(pools, ids, lens)):
+        feats.append({"table": t, "pooling": {"none": 0, "sum": 1, "mean": 2}[p], "exclude": 1, "ids_off": ids_off,
+                      "bag_off": bag_off, "num_bags": 0 if ln is None else B, "out_col": int(cols[t])})
+        if ln is not None:
+            o = O.offsets_of(ln)
+            offs.append(o)
+            bag_off += len(o)
+        ids_off += x.size
+    tables = [{"W": w.copy(), "acc": np.full(r, 0.5, np.float32)} for w, r in zip(W, rows)]
+    grad32 = grad.astype(np.float32).astype(np.float64)
+    ref = O.sparse_step(feats, tables, np.concatenate(ids), np.concatenate(offs), sum(dims), grad32, 0.05, 1e-8)
+    for t in range(3):
+        np.testing.assert_allclose(outs[t].numpy(), ref[:, cols[t]: cols[t] + dims[t]], rtol=1e-5, atol=1e-6)
+        np.testing.assert_allclose(step.params[t].detach().numpy(), tables[t]["W"], rtol=1e-5, atol=1e-6)
+        np.testing.assert_allclose(step.accs[t].numpy(), tables[t]["acc"], rtol=1e-5, atol=1e-6)
