@@ -416,6 +416,27 @@ int mdl_backward_coalesce(const mdl_feature* feats, int32_t num_features,
                           const uint64_t* values_addr, void* workspace,
                           size_t workspace_bytes, uint32_t classes, void* stream);
 
+/*
+ * mdl_backward_adagrad without a workspace argument and without allocating:
+ * no counterpart in the reference.  It is for callers that cannot allocate
+ * device memory -- code under HIP graph capture, tight serving loops,
+ * harnesses that forbid hipMalloc.  Its scratch is a static device array of
+ * mdl_noalloc_scratch_bytes() (64 MiB) per GPU, held until the process ends;
+ * a call whose mdl_backward_workspace_bytes(n, num_tables, max_dim) exceeds
+ * it returns MDL_ERR_UNSUPPORTED (e.g. 1 M entries over 1024 tables of
+ * max_dim 128 need 45 MiB).  Every call on one GPU shares that GPU's array
+ * and leaves its contents behind (the call initialises what it reads), so
+ * calls that overlap on one GPU -- on different streams or host threads --
+ * race.  Otherwise the same arguments and results as mdl_backward_adagrad.
+ */
+size_t mdl_noalloc_scratch_bytes(void);
+int mdl_backward_adagrad_noalloc(const mdl_feature* feats, int32_t num_features,
+                                 const mdl_table* tables, int32_t num_tables, int32_t max_dim,
+                                 uint32_t* sort_keys, uint32_t* sort_payload, int64_t n,
+                                 const int64_t* count, int32_t key_bits, const float* bag_count,
+                                 float lr, float eps, const float* grad_scale, uint32_t classes,
+                                 void* stream);
+
 /* ------------------------------------------------------------ clipping --- */
 
 /* A contiguous gradient tensor (dense, or the values of a coalesced COO). */

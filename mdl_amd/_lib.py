@@ -127,6 +127,11 @@ SIGNATURES: dict[str, tuple] = {
         _I32,
         [_P, _I32, _P, _I32, _I32, _P, _P, _I64, _I32, _P, _P, _P, _P, _P, _SZ, _U32, _P],
     ),
+    "mdl_noalloc_scratch_bytes": (_SZ, []),
+    "mdl_backward_adagrad_noalloc": (
+        _I32,
+        [_P, _I32, _P, _I32, _I32, _P, _P, _I64, _P, _I32, _P, _F, _F, _P, _U32, _P],
+    ),
     "mdl_rowwise_adagrad": (
         _I32,
         [_P, _I32, _I64, _I32, _I64, _P, _P, _I64, _P, _I32, _I64, _F, _F, _P, _P],

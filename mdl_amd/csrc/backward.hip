@@ -21,6 +21,8 @@
 // an order fixed by the chunk count and finishes the run.  The summation order depends on the
 // chunk layout only, and no floating-point atomics are used, so results do
 // not depend on scheduling.
+#include <mutex>
+
 #include "common.cuh"
 
 namespace mdl {
@@ -874,11 +876,45 @@ static int run_reduce(const BwdArgs& a, uint32_t variants, hipStream_t s) {
   return rc;
 }
 
+// --------------------------------------------------- allocation-free call --
+//
+// Scratch of mdl_backward_adagrad_noalloc: one static device array (each GPU
+// the library runs on holds its own copy until the process ends).  Host code
+// never passes the array's name to a kernel -- in host code that name is a
+// stand-in, not a device address -- but the address hipGetSymbolAddress
+// returns for the current device, looked up once per device on its first
+// call.
+constexpr size_t kNoAllocScratchBytes = size_t(64) << 20;
+static __device__ __align__(256) uint8_t scratch[kNoAllocScratchBytes];
+
+constexpr int kMaxDevices = 64;
+static std::mutex g_scratch_mu;
+static void* g_scratch_ptr[kMaxDevices];
+
+static int scratch_for_current_device(void** out) {
+  int dev = -1;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return check_hip(e, "hipGetDevice");
+  if (dev < 0 || dev >= kMaxDevices) return fail(MDL_ERR_UNSUPPORTED, "mdl_backward_adagrad_noalloc: device index");
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (g_scratch_ptr[dev] == nullptr) {
+    void* p = nullptr;
+    e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess) return check_hip(e, "hipGetSymbolAddress(scratch)");
+    if (p == nullptr) return fail(MDL_ERR_HIP, "hipGetSymbolAddress(scratch) returned a null address");
+    g_scratch_ptr[dev] = p;
+  }
+  *out = g_scratch_ptr[dev];
+  return MDL_OK;
+}
+
 }  // namespace mdl
 
 using namespace mdl;
 
 extern "C" {
+
+size_t mdl_noalloc_scratch_bytes(void) { return kNoAllocScratchBytes; }
 
 int mdl_sparse_keys(const int64_t* ids, int64_t n, int64_t num_rows, int64_t row_base, int64_t payload_base,
                     int64_t padding_idx, uint32_t* keys, uint32_t* payload, uint32_t sentinel, int32_t* error_count,
@@ -1045,6 +1081,25 @@ int mdl_backward_coalesce(const mdl_feature* feats, int32_t num_features, const 
   a.values_addr = values_addr;
   a.unique_range = unique_range;
   return run_reduce(a, classes, s);
+}
+
+int mdl_backward_adagrad_noalloc(const mdl_feature* feats, int32_t num_features, const mdl_table* tables,
+                                 int32_t num_tables, int32_t max_dim, uint32_t* sort_keys, uint32_t* sort_payload,
+                                 int64_t n, const int64_t* count, int32_t key_bits, const float* bag_count, float lr,
+                                 float eps, const float* grad_scale, uint32_t classes, void* stream) {
+  int rc = validate_tables("mdl_backward_adagrad_noalloc", num_tables, max_dim, n);
+  if (rc) return rc;
+  const size_t need = mdl_backward_workspace_bytes(n, num_tables, max_dim);
+  if (need > kNoAllocScratchBytes)
+    return fail(MDL_ERR_UNSUPPORTED, "mdl_backward_adagrad_noalloc: this call needs " + std::to_string(need) +
+                                         " bytes of scratch; the static scratch holds " +
+                                         std::to_string(kNoAllocScratchBytes) +
+                                         " (fewer entries, tables or a smaller max_dim fit)");
+  void* ws = nullptr;
+  rc = scratch_for_current_device(&ws);
+  if (rc) return rc;
+  return mdl_backward_adagrad(feats, num_features, tables, num_tables, max_dim, sort_keys, sort_payload, n, count,
+                              key_bits, bag_count, lr, eps, grad_scale, ws, kNoAllocScratchBytes, classes, stream);
 }
 
 }  // extern "C"
