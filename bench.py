@@ -4,11 +4,16 @@ Adagrad over one synthetic batch per step.
     python bench.py [--gpus 1] [--steps K] [--warmup W] [--config c1]
 
 Prints one JSON line.  ``value`` is looked-up (non-padding) rows per second
-of the whole step, timed between device synchronisations with every input
-already resident in HBM.  ``roofline`` reports the dominant kernel's
-algorithmic bytes per launch over its HIP-event-measured duration against
-MI355X's 8 TB/s; ``cpu_baseline`` times the CPU oracle (a plain-C port of
-the reference path) on a bounded sample of the same workload.
+of the headline config's whole step (c1 by default), timed between device
+synchronisations with every input already resident in HBM; each step binds a
+different batch (its own ids and bag lengths) to the one step object.
+``roofline`` reports the dominant kernel's algorithmic bytes per launch over
+its HIP-event-measured duration against MI355X's 8 TB/s; ``cpu_baseline``
+times the reference path's PyTorch CPU restatement (oracle/torch_path.py) on
+this run's first batch with every CPU thread the process may use.
+``configs`` then holds the same measurements for every other BASELINE
+config, run one after another with their tables freed in between (c0 with
+its own full-size CPU baseline).
 
 Workloads:
   c1  RankMixer-scale step (default): 200 features (150 single-valued, 50 bags
@@ -18,6 +23,10 @@ Workloads:
   c3  c1 with bf16 tables (fp32 accumulation and state).
   c0  32 tables x 1e6 x 64 fp32, batch 4096, Poisson(3) bags clipped to
       [1,16], Zipf(1.05) raw ids over 2^40 bucketed mod table size, sum pooling.
+  c2  4 sequences of 64..2000 ids padded to 2048, 2e8 x 64 fp32 tables,
+      batch 1024, Zipf(0.9) with 10% repeats, right-aligned windows + mask.
+  c4  capacity: 8 x 1.875e8 x 64 bf16 tables (1.5e9 rows) with uniform ids
+      plus 24 x 1e5 x 32 with Zipf(1.2), batch 16384, sum pooling.
 """
 
 from __future__ import annotations
@@ -596,6 +605,7 @@ def aux_measurements(torch, dev, wl, n_ids: float, steps: int, device, batches=N
 # ------------------------------------------------------------ cpu baseline --
 
 
+# Row caps for hosts whose RAM is smaller than a config's tables.
 CPU_ROW_CAP = {"c1": 1 << 20, "c3": 1 << 20, "c2": 1 << 22, "c4": 1 << 22}
 
 
@@ -620,10 +630,11 @@ def cpu_baseline(wl: Workload, batch, steps: int = 5, warmup: int = 2, row_cap: 
     F.embedding(sparse=True) -> index_add_ pooling -> autograd -> coalesce()
     -> the CPU row-wise Adagrad branch) on this run's first batch, with every
     CPU thread the process may use; the median of ``steps`` steps after
-    ``warmup``.  Tables above ``row_cap`` rows are capped (the same ids
-    bucketed mod the cap, the reference benchmark's rule) when the host could
-    not hold them; values do not change the CPU time, so tables are filled by
-    tiling one random block."""
+    ``warmup``.  Tables are full size when the host's RAM exceeds their
+    virtual size; otherwise tables above ``row_cap`` rows are capped (the same
+    ids bucketed mod the cap, the reference benchmark's rule).  A step reads and writes only the rows its batch touches:
+    those get random values (accumulators zero); the rest are never faulted
+    in."""
 
     import torch
 
@@ -632,21 +643,21 @@ def cpu_baseline(wl: Workload, batch, steps: int = 5, warmup: int = 2, row_cap: 
     threads = len(os.sched_getaffinity(0)) if hasattr(os, "sched_getaffinity") else (os.cpu_count() or 1)
     torch.set_num_threads(threads)
     dtype = torch.float32 if wl.dtype == "fp32" else torch.bfloat16
-    cap = row_cap if row_cap is not None else CPU_ROW_CAP.get(wl.name)
+    esize = 4 if wl.dtype == "fp32" else 2
+    cap = row_cap
+    if cap is None:
+        # Full-size tables whenever the host's RAM exceeds their virtual size
+        # (only the touched rows' pages are ever committed); else the cap.
+        need = sum(r * (d * esize + 4) for r, d in zip(wl.rows, wl.dims))
+        ram = (_host_info()["ram_gb"] or 0) * 1e9
+        cap = None if need < 0.8 * ram else CPU_ROW_CAP.get(wl.name, 1 << 20)
     rows = [min(r, cap) if cap else r for r in wl.rows]
     capped = any(r != q for r, q in zip(rows, wl.rows))
     t0 = time.perf_counter()
-    gen = torch.Generator().manual_seed(5)
-    tables, accs = [], []
-    for r, d in zip(rows, wl.dims):
-        block = (torch.randn((min(r, 4096), d), generator=gen) * 0.02).to(dtype)
-        w = torch.empty((r, d), dtype=dtype)
-        for i in range(0, r, block.size(0)):
-            w[i: i + block.size(0)] = block[: r - i]
-        w[0].zero_()
-        tables.append(w)
-        accs.append(torch.zeros(r, dtype=torch.float32))
-    setup_s = time.perf_counter() - t0
+    # Left unset except the rows the batch touches, which are the only rows a
+    # step reads or writes (set below): untouched pages are never faulted in.
+    tables = [torch.empty((r, d), dtype=dtype) for r, d in zip(rows, wl.dims)]
+    accs = [torch.empty(r, dtype=torch.float32) for r in rows]
 
     def cap_ids(x, t):
         x = np.asarray(x, dtype=np.int64)
@@ -679,6 +690,13 @@ def cpu_baseline(wl: Workload, batch, steps: int = 5, warmup: int = 2, row_cap: 
         grads = [torch.from_numpy(rng.standard_normal((wl.batch, wl.dims[f.table])).astype(np.float32)).to(dtype)
                  for f in wl.features]
         n_active = int(sum(int((np.asarray(x) != 0).sum()) for x in ids))
+    gen = torch.Generator().manual_seed(5)
+    for f, x in zip(wl.features, ids_t):
+        u = torch.unique(x)
+        tables[f.table][u] = (torch.randn((u.numel(), wl.dims[f.table]), generator=gen) * 0.02).to(dtype)
+        tables[f.table][0].zero_()
+        accs[f.table][u] = 0.0
+    setup_s = time.perf_counter() - t0
     step = TP.TorchStep(tables, accs, feats)
     times = []
     for i in range(warmup + steps):
@@ -697,7 +715,7 @@ def cpu_baseline(wl: Workload, batch, steps: int = 5, warmup: int = 2, row_cap: 
         "ms_per_step": ms,
         "sample": (f"{wl.name} at full batch {wl.batch} ({n_active} looked-up ids), the bench's first batch; "
                    + (f"tables capped at {cap} rows ({total_rows:.3e} rows in all, ids bucketed mod the cap) "
-                      "so they fit host RAM; " if capped else "full-size tables; ")
+                      "so they fit host RAM; " if capped else f"full-size tables ({total_rows:.3e} rows); ")
                    + f"PyTorch {torch.__version__} CPU restatement of the reference path (oracle/torch_path.py), "
                    f"median of {steps} steps after {warmup} warmup, torch.set_num_threads({threads}); "
                    f"host: {info['cpu_model']}, os.cpu_count()={info['os_cpu_count']}, "
@@ -782,7 +800,8 @@ def summarize_pmc(dirs, out_path, config, steps_run):
             "hbm_bytes_per_step": tot["FETCH_SIZE"] * 1024 * scale["FETCH_SIZE"]
             + tot["WRITE_SIZE"] * 1024 * scale["WRITE_SIZE"],
         }
-    res = {"config": config, "steps_run": steps_run, "copy_kernel": cname, "copy_bytes": COPY_BYTES,
+    res = {"config": config, "source_stamp": source_stamp(), "steps_run": steps_run, "copy_kernel": cname,
+           "copy_bytes": COPY_BYTES,
            "copy_FETCH_KiB": f_kib,
            "copy_WRITE_KiB": w_kib, "scale": scale, "groups": groups}
     Path(out_path).write_text(json.dumps(res, indent=1) + "\n")
@@ -813,17 +832,175 @@ def summarize_trace(dirs, out_path, title, command):
     print("\n".join(lines))
 
 
+def source_stamp() -> str:
+    """Hash of the library's sources (kernels, header, build flags): a
+    counter summary is only valid for the build it was measured on."""
+
+    import hashlib
+
+    h = hashlib.sha256()
+    csrc = ROOT / "mdl_amd" / "csrc"
+    for p in sorted(list(csrc.glob("*.hip")) + list(csrc.glob("*.cuh")) + [csrc / "Makefile",
+                    ROOT / "include" / "mdl_hip.h"]):
+        h.update(p.name.encode())
+        h.update(p.read_bytes())
+    return h.hexdigest()[:16]
+
+
 def load_traffic(config: str):
+    """(summary, reason): the committed counter summary of ``config`` when it
+    was measured on these library sources, else (None, why not)."""
+
     p = ROOT / "profiles" / f"{config}_traffic.json"
     if not p.exists():
-        return None
+        return None, f"no profiles/{config}_traffic.json"
     try:
-        return json.loads(p.read_text())
+        tr = json.loads(p.read_text())
     except (OSError, ValueError):
-        return None
+        return None, f"profiles/{config}_traffic.json unreadable"
+    stamp = source_stamp()
+    if tr.get("source_stamp") != stamp:
+        return None, (f"profiles/{config}_traffic.json was measured on library sources "
+                      f"{tr.get('source_stamp')}, not these ({stamp}): not used")
+    return tr, ""
 
 
 # ------------------------------------------------------------------- main --
+
+
+def measure(name: str, args, torch, device, *, with_aux: bool = False) -> dict:
+    """Time one config: ``args.warmup`` untimed steps, ``args.steps`` timed
+    between device synchronisations (a different batch bound every step),
+    then the same number of steps with HIP events around the forward and the
+    apply.  Returns the fields of the bench line for that config."""
+
+    wl = WORKLOADS[name]()
+    print(f"[bench] workload {wl.name}: {len(wl.features)} features, {len(wl.rows)} tables, "
+          f"{sum(wl.rows):.3e} rows, batch {wl.batch}, {wl.dtype}", file=sys.stderr, flush=True)
+    rng = np.random.default_rng(99)
+    batches = [draw_batch(rng, wl) for _ in range(args.batches)]
+    alg = [algorithmic_bytes(wl, ids, lengths) for ids, lengths in batches]
+    print(f"[bench] {wl.name}: drew {args.batches} batches; {alg[0]['n_ids']} ids/step, "
+          f"{alg[0]['unique_rows']} distinct rows", file=sys.stderr, flush=True)
+    if wl.kind == "sequence":
+        dev = SequenceDeviceStep(wl, batches, device)
+    else:
+        dev = DeviceStep(wl, batches, device, layout=args.layout)
+    torch.cuda.synchronize()
+    print(f"[bench] {wl.name}: tables initialised", file=sys.stderr, flush=True)
+    if args.calibrate_copy:
+        # a plain streaming kernel of known traffic: read 1 GiB, write 1 GiB
+        src = torch.ones(COPY_BYTES // 4, dtype=torch.float32, device=device)
+        dst = torch.empty_like(src)
+        for _ in range(3):
+            torch.neg(src, out=dst)
+        torch.cuda.synchronize()
+        del src, dst
+    for i in range(args.warmup):
+        dev.step(i)
+    torch.cuda.synchronize()
+    if args.graph:
+        # each batch's step as one HIP graph (recorded after the eager warmup
+        # steps loaded the kernels); the timed steps replay them
+        dev.capture()
+        torch.cuda.synchronize()
+        for i in range(len(dev.batches)):
+            dev.step(args.warmup + i)
+        torch.cuda.synchronize()
+    if int(dev.err.item()):
+        raise RuntimeError("synthetic ids out of range")
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for i in range(args.steps):
+        dev.step(args.warmup + i)
+    torch.cuda.synchronize()
+    elapsed = time.perf_counter() - t0
+    ms = elapsed * 1e3 / args.steps
+    used = [alg[(args.warmup + i) % len(alg)] for i in range(args.steps)]
+    n_ids = float(np.mean([a["n_ids"] for a in used]))
+    b_alg = float(np.mean([a["B_alg"] for a in used]))
+    # Per-kernel durations: HIP events around each call on the launch stream,
+    # in separate (untimed) steps so the event records do not touch the step time.
+    timers = {"forward": EventTimer(torch), "apply": EventTimer(torch)}
+    for i in range(args.steps):
+        dev.step(args.warmup + args.steps + i, timers)
+    torch.cuda.synchronize()
+    if int(dev.err.item()):
+        raise RuntimeError("synthetic ids out of range")
+    esz = 4 if wl.dtype == "fp32" else 2
+    nb = float(np.mean([sum(len(ln) for ln in b[1] if ln is not None) for b in batches]))
+    kernels = {}
+    if wl.kind == "sequence":
+        _, _, pad = wl.seq_len
+        nf = len(wl.features)
+        d = wl.dims[0]
+        # ids of the valid positions + lengths read, distinct rows, padded
+        # window + mask, sort keys/payloads (packed: one per looked-up id)
+        fwd_bytes = float(np.mean([8 * a["n_ids"] + 8 * nf * wl.batch + a["fwd_unique_row_bytes"]
+                                   + nf * wl.batch * pad * (d * esz + 1) + 8 * a["n_ids"] for a in used]))
+        # sorted keys/payloads, gradient rows at valid positions, rows read+written, state
+        apply_bytes = float(np.mean([8 * a["n_ids"] + a["n_ids"] * d * esz
+                                     + 2 * a["fwd_unique_row_bytes"] + 8 * a["unique_rows"] for a in used]))
+    else:
+        fwd_bytes = float(np.mean([16 * a["n_ids"] + 8 * (nb + 1) + a["fwd_unique_row_bytes"]
+                                   + wl.batch * a["sum_dim"] * esz + 4 * nb for a in used]))
+        apply_bytes = float(np.mean([8 * a["n_ids"] + wl.batch * a["sum_dim"] * esz
+                                     + 2 * a["fwd_unique_row_bytes"] + 8 * a["unique_rows"] + 4 * nb for a in used]))
+    fwd_label = ("sequence_kernel + sequence_keys_kernel per feature (window gather, mask, sort keys)"
+                 if wl.kind == "sequence" else "forward_kernel (grouped lookup + pooling + sort-key emission)")
+    for kname, nbytes, label in (
+        ("forward", fwd_bytes, fwd_label),
+        ("apply", apply_bytes, "bwd_reduce_kernel + fix-up (segment reduction + row-wise Adagrad)"),
+    ):
+        kms = timers[kname].median_ms()
+        kernels[kname] = {"kernel": label, "ms": kms, "alg_bytes_per_launch": nbytes,
+                          "achieved_gbps": nbytes / (kms * 1e-3) / 1e9}
+    dom_name = max(kernels, key=lambda k: kernels[k]["ms"])
+    dom = kernels[dom_name]
+    traffic = None
+    tr, why = load_traffic(wl.name)
+    if tr is not None and "hbm_bytes_per_step" in tr.get("groups", {}).get(dom_name, {}):
+        traffic = tr["groups"][dom_name]["hbm_bytes_per_step"]
+        dom["traffic_source"] = (f"profiles/{wl.name}_traffic.json (rocprofv3 FETCH_SIZE/WRITE_SIZE, copy-calibrated; "
+                                 f"library sources {tr['source_stamp']})")
+    else:
+        dom["traffic_source"] = why
+    out = {
+        "workload": f"{wl.name}: {len(wl.features)} features, batch {wl.batch}, "
+                    f"{sum(wl.rows):.3e} table rows, {wl.dtype} tables, fused fwd+bwd+row-wise Adagrad",
+        "value": n_ids / (ms * 1e-3),
+        "ms_per_step": ms,
+        "global_batch": wl.batch,
+        "ids_per_step": n_ids,
+        "distinct_rows_per_step": float(np.mean([a["unique_rows"] for a in used])),
+        "dtype": "f32" if wl.dtype == "fp32" else "bf16-storage/f32-accumulate",
+        "hbm_gbps_achieved": b_alg / (ms * 1e-3) / 1e9,
+        "roofline_fraction_step": b_alg / (ms * 1e-3) / 1e9 / PEAK_HBM_GBPS,
+        "B_alg_bytes_per_step": b_alg,
+        "roofline": {
+            "kernel": dom["kernel"],
+            "bound": "hbm",
+            "achieved": dom["achieved_gbps"],
+            "peak": PEAK_HBM_GBPS,
+            "unit": "GB/s",
+            "frac": dom["achieved_gbps"] / PEAK_HBM_GBPS,
+            "traffic": traffic,
+            "kernel_ms": dom["ms"],
+            "alg_bytes_per_launch": dom["alg_bytes_per_launch"],
+        },
+        "kernels": kernels,
+        "batches": args.batches,
+        "aux": None,
+    }
+    if with_aux and wl.kind != "sequence":
+        # after every timed number above, so the extra steps change none of them
+        out["aux"] = aux_measurements(torch, dev, wl, n_ids, args.steps, device, batches)
+    del dev
+    torch.cuda.synchronize()
+    torch.cuda.empty_cache()
+    out["_wl"] = wl
+    out["_batch0"] = batches[0]
+    return out
 
 
 def main() -> int:
@@ -832,8 +1009,10 @@ def main() -> int:
     ap.add_argument("--steps", type=int, default=30)
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--config", default="c1", choices=sorted(WORKLOADS))
-    ap.add_argument("--batches", type=int, default=3, help="distinct synthetic batches cycled through")
+    ap.add_argument("--batches", type=int, default=3, help="distinct synthetic batches, one bound per step in turn")
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--no-configs", action="store_true",
+                    help="only the headline config (by default every other config is measured after it)")
     ap.add_argument("--graph", action="store_true",
                     help="replay one HIP graph per batch instead of launching each step's kernels from the host "
                          "(measured: no faster at c0, c1 or c4 -- the host keeps ahead of the GPU)")
@@ -873,140 +1052,59 @@ def main() -> int:
     import torch
 
     device = torch.device("cuda:0")
-    wl = WORKLOADS[args.config]()
-    print(f"[bench] workload {wl.name}: {len(wl.features)} features, {len(wl.rows)} tables, "
-          f"{sum(wl.rows):.3e} rows, batch {wl.batch}, {wl.dtype}", file=sys.stderr, flush=True)
-    rng = np.random.default_rng(99)
-    batches = [draw_batch(rng, wl) for _ in range(args.batches)]
-    alg = [algorithmic_bytes(wl, ids, lengths) for ids, lengths in batches]
-    print(f"[bench] drew {args.batches} batches; {alg[0]['n_ids']} ids/step, "
-          f"{alg[0]['unique_rows']} distinct rows", file=sys.stderr, flush=True)
-    if wl.kind == "sequence":
-        dev = SequenceDeviceStep(wl, batches, device)
-    else:
-        dev = DeviceStep(wl, batches, device, layout=args.layout)
-    torch.cuda.synchronize()
-    print("[bench] tables initialised", file=sys.stderr, flush=True)
-    if args.calibrate_copy:
-        # a plain streaming kernel of known traffic: read 1 GiB, write 1 GiB
-        src = torch.ones(COPY_BYTES // 4, dtype=torch.float32, device=device)
-        dst = torch.empty_like(src)
-        for _ in range(3):
-            torch.neg(src, out=dst)
-        torch.cuda.synchronize()
-        del src, dst
-    for i in range(args.warmup):
-        dev.step(i)
-    torch.cuda.synchronize()
-    if args.graph:
-        # each batch's step as one HIP graph (recorded after the eager warmup
-        # steps loaded the kernels); the timed steps replay them
-        dev.capture()
-        torch.cuda.synchronize()
-        for i in range(len(dev.batches)):
-            dev.step(args.warmup + i)
-        torch.cuda.synchronize()
-    if int(dev.err.item()):
-        raise RuntimeError("synthetic ids out of range")
-    torch.cuda.synchronize()
-    t0 = time.perf_counter()
-    for i in range(args.steps):
-        dev.step(args.warmup + i)
-    torch.cuda.synchronize()
-    elapsed = time.perf_counter() - t0
-    ms = elapsed * 1e3 / args.steps
-    used = [alg[(args.warmup + i) % len(alg)] for i in range(args.steps)]
-    n_ids = float(np.mean([a["n_ids"] for a in used]))
-    b_alg = float(np.mean([a["B_alg"] for a in used]))
-    rows_per_s = n_ids / (ms * 1e-3)
-    gbps = b_alg / (ms * 1e-3) / 1e9
-    # Per-kernel durations: HIP events around each call on the launch stream,
-    # in separate (untimed) steps so the event records do not touch the step time.
-    timers = {"forward": EventTimer(torch), "apply": EventTimer(torch)}
-    for i in range(args.steps):
-        dev.step(args.warmup + args.steps + i, timers)
-    torch.cuda.synchronize()
-    esz = 4 if wl.dtype == "fp32" else 2
-    nb = float(np.mean([sum(len(ln) for ln in b[1] if ln is not None) for b in batches]))
-    kernels = {}
-    if wl.kind == "sequence":
-        _, _, pad = wl.seq_len
-        nf = len(wl.features)
-        d = wl.dims[0]
-        # ids of the valid positions + lengths read, distinct rows, padded
-        # window + mask, sort keys/payloads (packed: one per looked-up id)
-        fwd_bytes = float(np.mean([8 * a["n_ids"] + 8 * nf * wl.batch + a["fwd_unique_row_bytes"]
-                                   + nf * wl.batch * pad * (d * esz + 1) + 8 * a["n_ids"] for a in used]))
-        # sorted keys/payloads, gradient rows at valid positions, rows read+written, state
-        apply_bytes = float(np.mean([8 * a["n_ids"] + a["n_ids"] * d * esz
-                                     + 2 * a["fwd_unique_row_bytes"] + 8 * a["unique_rows"] for a in used]))
-    else:
-        fwd_bytes = float(np.mean([16 * a["n_ids"] + 8 * (nb + 1) + a["fwd_unique_row_bytes"]
-                                   + wl.batch * a["sum_dim"] * esz + 4 * nb for a in used]))
-        apply_bytes = float(np.mean([8 * a["n_ids"] + wl.batch * a["sum_dim"] * esz
-                                     + 2 * a["fwd_unique_row_bytes"] + 8 * a["unique_rows"] + 4 * nb for a in used]))
-    fwd_label = ("sequence_kernel + sequence_keys_kernel per feature (window gather, mask, sort keys)"
-                 if wl.kind == "sequence" else "forward_kernel (grouped lookup + pooling + sort-key emission)")
-    for name, nbytes, label in (
-        ("forward", fwd_bytes, fwd_label),
-        ("apply", apply_bytes, "bwd_reduce_kernel + fix-up (segment reduction + row-wise Adagrad)"),
-    ):
-        kms = timers[name].median_ms()
-        kernels[name] = {"kernel": label, "ms": kms, "alg_bytes_per_launch": nbytes,
-                         "achieved_gbps": nbytes / (kms * 1e-3) / 1e9}
-    dom_name = max(kernels, key=lambda k: kernels[k]["ms"])
-    dom = kernels[dom_name]
-    traffic = None
-    tr = load_traffic(wl.name)
-    if tr is not None and "hbm_bytes_per_step" in tr.get("groups", {}).get(dom_name, {}):
-        traffic = tr["groups"][dom_name]["hbm_bytes_per_step"]
-        dom["traffic_source"] = f"profiles/{wl.name}_traffic.json (rocprofv3 FETCH_SIZE/WRITE_SIZE, copy-calibrated)"
+    head = measure(args.config, args, torch, device,
+                   with_aux=not args.no_aux and not args.calibrate_copy)
+    wl = head.pop("_wl")
+    batch0 = head.pop("_batch0")
     result = {
         "metric": METRIC,
-        "value": rows_per_s,
+        "value": head["value"],
         "unit": "rows/s",
         "n_gpus": 1,
         "steps": args.steps,
         "warmup": args.warmup,
-        "ms_per_step": ms,
+        "ms_per_step": head["ms_per_step"],
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": "f32" if wl.dtype == "fp32" else "bf16-storage/f32-accumulate",
-        "data": "synthetic (seeded Zipf ids, random-init tables)",
+        "dtype": head["dtype"],
+        "data": "synthetic (seeded Zipf ids, random-init tables); a different batch bound every step",
         "config": {
-            "workload": f"{wl.name}: {len(wl.features)} features, batch {wl.batch}, "
-                        f"{sum(wl.rows):.3e} table rows, {wl.dtype} tables, fused fwd+bwd+row-wise Adagrad",
-            "global_batch": wl.batch,
-            "ids_per_step": n_ids,
-            "distinct_rows_per_step": float(np.mean([a["unique_rows"] for a in used])),
+            "workload": head["workload"],
+            "global_batch": head["global_batch"],
+            "ids_per_step": head["ids_per_step"],
+            "distinct_rows_per_step": head["distinct_rows_per_step"],
             "parallelism": "single GPU",
             "launch": "one HIP graph per batch (captured step)" if args.graph else "eager",
+            "batches": args.batches,
         },
-        "hbm_gbps_achieved": gbps,
-        "roofline_fraction_step": gbps / PEAK_HBM_GBPS,
-        "B_alg_bytes_per_step": b_alg,
-        "roofline": {
-            "kernel": dom["kernel"],
-            "bound": "hbm",
-            "achieved": dom["achieved_gbps"],
-            "peak": PEAK_HBM_GBPS,
-            "unit": "GB/s",
-            "frac": dom["achieved_gbps"] / PEAK_HBM_GBPS,
-            "traffic": traffic,
-            "kernel_ms": dom["ms"],
-            "alg_bytes_per_launch": dom["alg_bytes_per_launch"],
-        },
-        "kernels": kernels,
-        "aux": None,
+        "hbm_gbps_achieved": head["hbm_gbps_achieved"],
+        "roofline_fraction_step": head["roofline_fraction_step"],
+        "B_alg_bytes_per_step": head["B_alg_bytes_per_step"],
+        "roofline": head["roofline"],
+        "kernels": head["kernels"],
+        "aux": head["aux"],
         "cpu_baseline": None,
+        "configs": {},
     }
-    if wl.kind != "sequence" and not args.no_aux and not args.calibrate_copy:
-        # after every timed number above, so the extra steps change none of them
-        result["aux"] = aux_measurements(torch, dev, wl, n_ids, args.steps, device, batches)
-    if not args.no_cpu_baseline:
-        print("[bench] timing the CPU oracle sample", file=sys.stderr, flush=True)
-        result["cpu_baseline"] = cpu_baseline(wl, batches[0], steps=args.cpu_steps)
+    if not args.no_cpu_baseline and not args.calibrate_copy:
+        print(f"[bench] timing the CPU restatement on {wl.name}", file=sys.stderr, flush=True)
+        result["cpu_baseline"] = cpu_baseline(wl, batch0, steps=args.cpu_steps)
+    if not args.no_configs and not args.calibrate_copy:
+        for name in ("c0", "c3", "c4", "c2"):
+            if name == args.config:
+                continue
+            m = measure(name, args, torch, device)
+            mwl = m.pop("_wl")
+            mb = m.pop("_batch0")
+            m.pop("aux")
+            if name == "c0" and not args.no_cpu_baseline:
+                # the CPU-runnable plumbing config, at full size
+                print("[bench] timing the CPU restatement on c0", file=sys.stderr, flush=True)
+                m["cpu_baseline"] = cpu_baseline(mwl, mb, steps=args.cpu_steps)
+            result["configs"][name] = m
+            print(f"[bench] {name}: {m['ms_per_step']:.3f} ms/step, {m['value']:.3e} rows/s, "
+                  f"step {m['roofline_fraction_step']:.3f} of HBM peak", file=sys.stderr, flush=True)
     print(json.dumps(result), flush=True)
     return 0
 
