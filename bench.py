@@ -347,7 +347,9 @@ class DeviceStep:
         # device-resident batches: packed ids + concatenated lengths (an unpooled
         # feature contributes one pseudo-bag holding all its ids)
         self.batches = []
+        self.batch_counts = []
         for ids, lengths in batches:
+            self.batch_counts.append([(int(x.size), 0 if ln is None else int(ln.size)) for x, ln in zip(ids, lengths)])
             parts = [ln if ln is not None else np.array([x.size]) for x, ln in zip(ids, lengths)]
             packed = torch.from_numpy(np.concatenate(ids).astype(np.int64)).to(device)
             lens = torch.from_numpy(np.concatenate(parts).astype(np.int64)).to(device)
@@ -500,7 +502,8 @@ def aux_measurements(torch, dev, wl, n_ids: float, steps: int, device, batches=N
       src/train.py:5788-5826), wall clock over ``steps`` steps like the
       headline;
     * the stand-alone row-wise Adagrad update on 1 M unique rows;
-    * the autograd path's coalesce of one batch's gradients;
+    * the drop-in autograd training loop (ShardedEmbedding modules,
+      loss.backward(), ShardedRowWiseAdagrad.step()) on the same batches;
     * device bucketing (mdl_bucketize, src/features.py:360-376 and
       src/benchmark.py:1246-1250) of one step's worth of raw int64 ids, HIP
       events around 20 back-to-back launches queued behind a spin kernel, so
@@ -573,32 +576,90 @@ def aux_measurements(torch, dev, wl, n_ids: float, steps: int, device, batches=N
         "achieved_gbps": nbytes / (ms * 1e-3) / 1e9, "frac": nbytes / (ms * 1e-3) / 1e9 / PEAK_HBM_GBPS,
     }
     del rows, vals
-    # the autograd path's coalesce (sparse gradient rows + values per table,
-    # src/optim.py:321-324 / src/train.py:5730-5742) of one c1 batch: sort,
-    # unique and segment-sum, each after a fresh lookup (the coalesce consumes
-    # the lookup's sort keys); HIP events around the coalesce only
+    # the drop-in autograd path at the same layout: ShardedEmbedding modules
+    # over the bench's tables, pooled_embedding_lookup for the bags and
+    # grouped_sharded_embedding_lookup for the single-valued features,
+    # loss.backward(), ShardedRowWiseAdagrad.step() -- the loop a user of the
+    # reference's modules runs (src/model.py:3782-3890, src/train.py:7060-7188),
+    # timed under the sync debug mode that raises on any host synchronisation
     if batches is not None:
-        ids, lengths = batches[0]
-        ids_t = [torch.from_numpy(np.asarray(x, dtype=np.int64)).to(device) for x in ids]
-        lens_t = [None if ln is None else torch.from_numpy(np.asarray(ln, dtype=np.int64)).to(device)
-                  for ln in lengths]
-        times = []
-        for _ in range(5):
-            res = ops.grouped_forward(dev.plan, ids_t, lens_t, with_backward=True)
-            grads = [torch.randn(o.shape, dtype=o.dtype, device=device, generator=gen) for o in res.outputs]
-            torch.cuda.synchronize()
-            e0 = torch.cuda.Event(enable_timing=True)
-            e1 = torch.cuda.Event(enable_timing=True)
-            torch.cuda._sleep(20_000_000)
-            e0.record()
-            coalesced = ops.backward_coalesce(res, grads)
-            e1.record()
-            torch.cuda.synchronize()
-            times.append(e0.elapsed_time(e1))
-            del res, grads, coalesced
-        out["coalesce"] = {"ids": int(sum(x.size for x in ids)), "ms": float(np.median(times)),
-                           "what": "sort + unique + per-table segment sums written as (rows, values), "
-                                   "including its host read of the unique counts (to size the outputs)"}
+        out["dropin_step"] = dropin_loop(torch, dev, wl, device, steps=min(steps, 10))
+    return out
+
+
+def dropin_loop(torch, dev, wl, device, steps: int = 10) -> dict:
+    from torch import nn
+
+    from mdl_amd.embeddings import (EmbeddingShardSpec, ShardedEmbedding, grouped_sharded_embedding_lookup,
+                                    pooled_embedding_lookup)
+    from mdl_amd.optim import ShardedRowWiseAdagrad
+
+    mods = []
+    for t, w in enumerate(dev.tables):
+        # built small, then given the resident table (no second copy)
+        spec = EmbeddingShardSpec(table_name=f"table_{t}", strategy="row_wise", world_size=1)
+        m = ShardedEmbedding(2, int(w.size(1)), table_name=f"table_{t}", shard_spec=spec, collect_stats=False,
+                             dtype=w.dtype).to(device)
+        m.weight = nn.Parameter(w)
+        m.num_embeddings = int(w.size(0))
+        mods.append(m)
+    opt = ShardedRowWiseAdagrad([m.weight for m in mods], lr=wl.lr, eps=wl.eps)
+    for m, acc in zip(mods, dev.states):
+        opt.state[m.weight]["sum"] = acc
+    cols = np.concatenate([[0], np.cumsum([wl.dims[f.table] for f in wl.features])[:-1]])
+    grads = [dev.grad[:, int(c): int(c) + wl.dims[f.table]].contiguous() for f, c in zip(wl.features, cols)]
+    feats = []
+    for packed, lens in dev.batches:
+        req_pool, req_single, g_pool, g_single = [], [], [], []
+        ofs = 0
+        lofs = 0
+        host_counts = dev.batch_counts[len(feats)]
+        for f, feat in enumerate(wl.features):
+            n, nb = host_counts[f]
+            x = packed[ofs: ofs + n]
+            ofs += n
+            if feat.pooling == "none":
+                req_single.append((mods[feat.table], x))
+                g_single.append(grads[f])
+                lofs += 1
+            else:
+                req_pool.append((mods[feat.table], x, lens[lofs: lofs + nb], feat.pooling, "exclude"))
+                g_pool.append(grads[f])
+                lofs += nb
+        feats.append((req_pool, req_single, g_pool + g_single))
+
+    def one(i):
+        req_pool, req_single, gs = feats[i % len(feats)]
+        opt.zero_grad(set_to_none=True)
+        outs = pooled_embedding_lookup(req_pool) + grouped_sharded_embedding_lookup(req_single)
+        torch.autograd.backward(outs, gs)
+        opt.step()
+
+    for i in range(2):
+        one(i)
+    torch.cuda.synchronize()
+    clean = True
+    torch.cuda.set_sync_debug_mode("error")
+    try:
+        t0 = time.perf_counter()
+        for i in range(steps):
+            one(i)
+        torch.cuda.set_sync_debug_mode("default")
+        torch.cuda.synchronize()
+        ms = (time.perf_counter() - t0) * 1e3 / steps
+    except RuntimeError:
+        clean = False
+        torch.cuda.set_sync_debug_mode("default")
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        for i in range(steps):
+            one(i)
+        torch.cuda.synchronize()
+        ms = (time.perf_counter() - t0) * 1e3 / steps
+    return {"ms_per_step": ms, "steps": steps, "no_host_sync": clean,
+            "what": "ShardedEmbedding modules (pooled_embedding_lookup + grouped_sharded_embedding_lookup), "
+                    "loss.backward() -> capacity-sized coalesced sparse grads, ShardedRowWiseAdagrad.step() "
+                    "(one grouped launch); timed steps under torch.cuda.set_sync_debug_mode('error')"}
     return out
 
 

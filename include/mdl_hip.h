@@ -437,6 +437,22 @@ int mdl_backward_adagrad_noalloc(const mdl_feature* feats, int32_t num_features,
                                  float lr, float eps, const float* grad_scale, uint32_t classes,
                                  void* stream);
 
+/*
+ * Capacity-sized coalesced gradients without a host read: after
+ * mdl_backward_coalesce wrote table t's U_t unique rows and values at
+ * rows_addr[t] / values_addr[t] (buffers of capacity[t] >= U_t entries,
+ * capacity a device int64 [num_tables]), fill entries [U_t, capacity[t])
+ * with the table's last unique row (row 0 when U_t = 0) and zero values
+ * (dim elements of the table's dtype, rows contiguous).  The buffers are then
+ * an uncoalesced COO gradient with the coalesced gradient's sum and a size
+ * the host knows without waiting for the device (a table's id count bounds
+ * U_t).  unit_first (device int64 [num_tables + 1]) is the prefix of
+ * ceil(capacity[t] / 64) and units its last entry.
+ */
+int mdl_backward_pad(const mdl_table* tables, int32_t num_tables, const int64_t* unique_range,
+                     const uint64_t* rows_addr, const uint64_t* values_addr, const int64_t* capacity,
+                     const int64_t* unit_first, int64_t units, void* stream);
+
 /* ------------------------------------------------------------ clipping --- */
 
 /* A contiguous gradient tensor (dense, or the values of a coalesced COO). */
@@ -483,6 +499,46 @@ int mdl_rowwise_adagrad(void* weight, int32_t wdtype, int64_t num_rows, int32_t 
                         int64_t num_touched, const void* values, int32_t vdtype,
                         int64_t values_stride, float lr, float eps,
                         int32_t* error_count, void* stream);
+
+/*
+ * One table of a grouped row-wise Adagrad step.  rows[0 .. n) are the unique
+ * touched rows (int64) and values[i] their gradient rows (vdtype, stride
+ * values_stride elements), n = *count (device int64; count = 0 means n =
+ * capacity).  unit_first is the prefix, over the tables before this one, of
+ * ceil(capacity / MDL_UPDATE_UNIT) -- the host fills it.
+ */
+typedef struct mdl_update {
+  uint64_t weight;        /* [num_rows, dim], row stride weight_stride elements */
+  uint64_t state;         /* fp32 accumulator [num_rows] */
+  uint64_t rows;
+  uint64_t values;
+  uint64_t count;         /* device int64 address, or 0 */
+  int64_t num_rows;
+  int64_t capacity;
+  int64_t weight_stride;
+  int64_t values_stride;
+  int64_t unit_first;
+  int32_t dim;
+  int32_t wdtype;
+  int32_t vdtype;
+  float lr;               /* this table's learning rate (per-parameter decay) */
+} mdl_update;             /* 96 bytes */
+
+#define MDL_UPDATE_UNIT 256
+
+/*
+ * Row-wise Adagrad of every table of an optimizer step in one launch: for
+ * each table and each i < n, the update of mdl_rowwise_adagrad with the
+ * table's lr (ShardedRowWiseAdagrad.step, src/optim.py:299-377, which makes
+ * one fused_rowwise_adagrad_update launch per parameter, :68-108).  updates
+ * is the device array, updates_host a host copy (validated, and used to pick
+ * the kernels); n comes from device memory, so a gradient whose row count is
+ * only known on the device (capacity-sized, see mdl_backward_pad) needs no
+ * host read.  Rows outside [0, num_rows) are skipped and counted.
+ */
+uint32_t mdl_update_classes(const mdl_update* updates_host, int32_t num_updates);
+int mdl_grouped_rowwise_adagrad(const mdl_update* updates, const mdl_update* updates_host,
+                                int32_t num_updates, float eps, int32_t* error_count, void* stream);
 
 #ifdef __cplusplus
 }

@@ -71,6 +71,26 @@ TABLE_DTYPE = np.dtype(
         ("gdtype", "<i4"),
     ]
 )
+UPDATE_DTYPE = np.dtype(
+    [
+        ("weight", "<u8"),
+        ("state", "<u8"),
+        ("rows", "<u8"),
+        ("values", "<u8"),
+        ("count", "<u8"),
+        ("num_rows", "<i8"),
+        ("capacity", "<i8"),
+        ("weight_stride", "<i8"),
+        ("values_stride", "<i8"),
+        ("unit_first", "<i8"),
+        ("dim", "<i4"),
+        ("wdtype", "<i4"),
+        ("vdtype", "<i4"),
+        ("lr", "<f4"),
+    ]
+)
+MDL_UPDATE_UNIT = 256
+assert UPDATE_DTYPE.itemsize == 96
 assert FEATURE_DTYPE.itemsize == 128
 assert CHUNK_DTYPE.itemsize == 16
 assert SPAN_DTYPE.itemsize == 24
@@ -132,6 +152,9 @@ SIGNATURES: dict[str, tuple] = {
         _I32,
         [_P, _I32, _P, _I32, _I32, _P, _P, _I64, _P, _I32, _P, _F, _F, _P, _U32, _P],
     ),
+    "mdl_backward_pad": (_I32, [_P, _I32, _P, _P, _P, _P, _P, _I64, _P]),
+    "mdl_update_classes": (_U32, [_P, _I32]),
+    "mdl_grouped_rowwise_adagrad": (_I32, [_P, _P, _I32, _F, _P, _P]),
     "mdl_rowwise_adagrad": (
         _I32,
         [_P, _I32, _I64, _I32, _I64, _P, _P, _I64, _P, _I32, _I64, _F, _F, _P, _P],

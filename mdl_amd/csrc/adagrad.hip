@@ -138,6 +138,84 @@ __global__ __launch_bounds__(kAdaWaves * kWave) void adagrad_kernel(AdaArgs a) {
   else adagrad_rows<TW, TV, C>(a, wave, nwaves);
 }
 
+// ------------------------------------------------------------ grouped --
+//
+// Every table of an optimizer step in one launch (src/optim.py:299-377 makes
+// one update launch per parameter).  The work is cut into units of
+// MDL_UPDATE_UNIT entries of one table, one wave each; a table's first unit is
+// in its descriptor, and a wave finds its table by binary search over them.
+// Entries at or past a table's device-side count (rows present this step)
+// are skipped, so a capacity-sized gradient needs no host round trip.
+
+struct GroupedArgs {
+  const mdl_update* ups;
+  int32_t num;
+  int64_t units;
+  float eps;
+  int32_t* error_count;
+};
+
+__host__ __device__ __forceinline__ bool update_vec(const mdl_update& u) {
+  const int wsz = u.wdtype == MDL_BF16 ? 2 : 4;
+  const int vsz = u.vdtype == MDL_BF16 ? 2 : 4;
+  const int c = 16 / wsz;
+  return u.weight % 16 == 0 && u.values % 16 == 0 && (u.weight_stride * wsz) % 16 == 0 &&
+         (u.values_stride * vsz) % 16 == 0 && ((int64_t)u.dim * wsz) % 16 == 0 && ((int64_t)c * vsz) % 16 == 0;
+}
+
+__host__ __device__ __forceinline__ int update_class(int wdtype, int vdtype, bool vec) {
+  const int base = wdtype == MDL_F32 ? MDL_CLASS_F32_VEC
+                   : (vdtype == MDL_BF16 ? MDL_CLASS_BF16_VEC : MDL_CLASS_BF16_F32_VEC);
+  return base + (vec ? 0 : 1);
+}
+
+template <typename TW, typename TV, bool kVec>
+__global__ __launch_bounds__(kAdaWaves * kWave) void grouped_adagrad_kernel(GroupedArgs g) {
+  constexpr int C = kVec ? 16 / (int)sizeof(TW) : 1;
+  const int64_t unit = (int64_t)blockIdx.x * kAdaWaves + threadIdx.x / kWave;
+  if (unit >= g.units) return;
+  int lo = 0, hi = g.num - 1;  // last table whose first unit <= unit
+  while (lo < hi) {
+    const int mid = (lo + hi + 1) >> 1;
+    if (g.ups[mid].unit_first <= unit) lo = mid;
+    else hi = mid - 1;
+  }
+  const mdl_update& u = g.ups[lo];
+  if (update_class(u.wdtype, u.vdtype, update_vec(u)) != ClassOf<TW, TV, kVec>::value) return;
+  int64_t present = u.count != 0 ? *reinterpret_cast<const int64_t*>(u.count) : u.capacity;
+  present = present < 0 ? 0 : (present > u.capacity ? u.capacity : present);
+  const int64_t start = (unit - u.unit_first) * MDL_UPDATE_UNIT;
+  if (start >= present) return;
+  AdaArgs a;
+  a.weight = reinterpret_cast<void*>(u.weight);
+  a.num_rows = u.num_rows;
+  a.wstride = u.weight_stride;
+  a.acc = reinterpret_cast<float*>(u.state);
+  a.rows = reinterpret_cast<const int64_t*>(u.rows) + start;
+  a.n = present - start < MDL_UPDATE_UNIT ? present - start : MDL_UPDATE_UNIT;
+  a.values = reinterpret_cast<const TV*>(u.values) + start * u.values_stride;
+  a.vstride = u.values_stride;
+  a.dim = u.dim;
+  a.lr = u.lr;
+  a.eps = g.eps;
+  a.error_count = g.error_count;
+  if (a.dim > kWave * C) adagrad_wide_rows<TW, TV, C>(a, 0, 1);
+  else adagrad_rows<TW, TV, C>(a, 0, 1);
+}
+
+struct LaunchGrouped {
+  const GroupedArgs& g;
+  int64_t blocks;
+  hipStream_t s;
+  template <typename TW, typename TV, bool kVec>
+  int operator()() const {
+    hipLaunchKernelGGL((grouped_adagrad_kernel<TW, TV, kVec>), dim3((unsigned)blocks), dim3(kAdaWaves * kWave), 0,
+                       s, g);
+    MDL_CHECK_LAUNCH("grouped_adagrad_kernel");
+    return MDL_OK;
+  }
+};
+
 }  // namespace mdl
 
 using namespace mdl;
@@ -191,6 +269,44 @@ int mdl_rowwise_adagrad(void* weight, int32_t wdtype, int64_t num_rows, int32_t 
   }
   MDL_CHECK_LAUNCH("adagrad_kernel");
   return MDL_OK;
+}
+
+uint32_t mdl_update_classes(const mdl_update* updates_host, int32_t num_updates) {
+  uint32_t m = 0;
+  for (int32_t i = 0; i < num_updates; ++i) {
+    const mdl_update& u = updates_host[i];
+    m |= 1u << (update_class(u.wdtype, u.vdtype, update_vec(u)) * kWidths);
+  }
+  return m;
+}
+
+int mdl_grouped_rowwise_adagrad(const mdl_update* updates, const mdl_update* updates_host, int32_t num_updates,
+                                float eps, int32_t* error_count, void* stream) {
+  if (num_updates < 0) return fail(MDL_ERR_INVALID, "mdl_grouped_rowwise_adagrad: negative count");
+  if (num_updates == 0) return MDL_OK;
+  if (!updates || !updates_host) return fail(MDL_ERR_INVALID, "mdl_grouped_rowwise_adagrad: null pointer");
+  int64_t units = 0;
+  for (int32_t i = 0; i < num_updates; ++i) {
+    const mdl_update& u = updates_host[i];
+    if (u.capacity < 0 || u.dim <= 0 || u.num_rows < 0)
+      return fail(MDL_ERR_INVALID, "mdl_grouped_rowwise_adagrad: bad sizes");
+    if (u.wdtype == MDL_F32 && u.vdtype != MDL_F32)
+      return fail(MDL_ERR_UNSUPPORTED, "mdl_grouped_rowwise_adagrad: fp32 weights need fp32 values");
+    if (u.unit_first != units)
+      return fail(MDL_ERR_INVALID, "mdl_grouped_rowwise_adagrad: unit_first must be the prefix of "
+                                   "ceil(capacity / MDL_UPDATE_UNIT)");
+    units += (u.capacity + MDL_UPDATE_UNIT - 1) / MDL_UPDATE_UNIT;
+  }
+  if (units == 0) return MDL_OK;
+  GroupedArgs g;
+  g.ups = updates;
+  g.num = num_updates;
+  g.units = units;
+  g.eps = eps;
+  g.error_count = error_count;
+  const int64_t blocks = (units + kAdaWaves - 1) / kAdaWaves;
+  if (blocks > 0x7fffffffll) return fail(MDL_ERR_UNSUPPORTED, "mdl_grouped_rowwise_adagrad: too many rows");
+  return for_each_class(mdl_update_classes(updates_host, num_updates), LaunchGrouped{g, blocks, as_stream(stream)});
 }
 
 }  // extern "C"

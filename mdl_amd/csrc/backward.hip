@@ -342,7 +342,7 @@ struct Reducer {
   // fields of the table's only feature (single >= 0)
   const TG* g_base;
   int64_t g_stride, pbase;
-  bool g_mean;
+  bool g_mean, g_pool_none;
   float scale;
 
   __device__ Reducer(const BwdArgs& args, int32_t table) : a(args), t(table) {
@@ -364,6 +364,7 @@ struct Reducer {
     g_base = nullptr;
     g_stride = pbase = 0;
     g_mean = false;
+    g_pool_none = false;
     scale = 1.f;
     if (kMode == kModeAdagrad && a.grad_scale != nullptr)
       scale = __builtin_bit_cast(float, __builtin_amdgcn_readfirstlane(__builtin_bit_cast(int, *a.grad_scale)));
@@ -373,6 +374,7 @@ struct Reducer {
       g_stride = uni64b(f.out_stride);
       pbase = uni64b(f.payload_base);
       g_mean = __builtin_amdgcn_readfirstlane(f.pooling) == MDL_POOL_MEAN;
+      g_pool_none = __builtin_amdgcn_readfirstlane(f.pooling) == MDL_POOL_NONE;
     }
   }
 
@@ -469,6 +471,10 @@ __device__ __forceinline__ void reduce_chunk_body(const BwdArgs& a, int64_t c, c
   const bool head_open = st.key[0] == st.key[1];
   const bool tail_open = st.key[len + 1] == st.key[len];
   const int64_t hb = coalesce ? a.head_base[c] : 0;
+  // Gradient rows read once (a table read by one unpooled feature: each
+  // output row has one id) can stream past L2, leaving it to rows that are
+  // read again (the bag rows of pooled features, read once per id).
+  const bool stream_grad = MDL_STREAM_GRAD == 2 || (MDL_STREAM_GRAD == 1 && kOne && R.g_pool_none);
   // This slot's slice [s0, s1) of the chunk.
   // Slices of an odd length start on distinct LDS banks.
   const int K = ((len + G - 1) / G) | 1;
@@ -514,7 +520,8 @@ __device__ __forceinline__ void reduce_chunk_body(const BwdArgs& a, int64_t c, c
     // runs that finish here, the weight row and accumulator.
 #pragma unroll
     for (int u = 0; u < U; ++u) {
-      RowIO<TG, C>::load(gp[u], v[u]);
+      if (stream_grad) RowIO<TG, C>::template load<kStream>(gp[u], v[u]);
+      else RowIO<TG, C>::load(gp[u], v[u]);
       if (adagrad) {
         const int64_t row = (int64_t)key[u] - R.row_base;
         const bool ld = own[u] && R.row_ok(key[u]);
@@ -876,6 +883,54 @@ static int run_reduce(const BwdArgs& a, uint32_t variants, hipStream_t s) {
   return rc;
 }
 
+// ------------------------------------------------------ capacity padding --
+//
+// Coalesced gradients sized to a capacity known on the host (a table's id
+// count bounds its distinct rows): entries [U_t, cap_t) of table t repeat
+// its last row (row 0 when it has none) with zero values, so the whole
+// buffer is a valid uncoalesced COO gradient whose sum is the coalesced one.
+// Work: units of kPadRows entries over the capacity prefix, one wave each.
+constexpr int64_t kPadRows = 64;
+
+__global__ __launch_bounds__(256) void pad_kernel(const mdl_table* __restrict__ tables, int32_t T,
+                                                  const int64_t* __restrict__ unique_range,
+                                                  const uint64_t* __restrict__ rows_addr,
+                                                  const uint64_t* __restrict__ values_addr,
+                                                  const int64_t* __restrict__ capacity,
+                                                  const int64_t* __restrict__ unit_first, int64_t units) {
+  const int64_t unit = (int64_t)blockIdx.x * 4 + threadIdx.x / kWave;
+  if (unit >= units) return;
+  int lo = 0, hi = T - 1;
+  while (lo < hi) {
+    const int mid = (lo + hi + 1) >> 1;
+    if (unit_first[mid] <= unit) lo = mid;
+    else hi = mid - 1;
+  }
+  const int t = lo;
+  const int64_t u = unique_range[2 * t + 1] - unique_range[2 * t];
+  const int64_t r0 = (unit - unit_first[t]) * kPadRows;
+  const int64_t cap = capacity[t];
+  const int64_t r1 = r0 + kPadRows < cap ? r0 + kPadRows : cap;
+  const int64_t b = r0 > u ? r0 : u;
+  if (b >= r1 || rows_addr[t] == 0) return;
+  int64_t* rows = reinterpret_cast<int64_t*>(rows_addr[t]);
+  const int lane = lane_id();
+  const int64_t fill = u > 0 ? rows[u - 1] : 0;
+  for (int64_t i = b + lane; i < r1; i += kWave) rows[i] = fill;
+  const mdl_table& tb = tables[t];
+  const int64_t esz = tb.wdtype == MDL_BF16 ? 2 : 4;
+  const int64_t bytes = (r1 - b) * (int64_t)tb.dim * esz;
+  char* v = reinterpret_cast<char*>(values_addr[t]) + b * (int64_t)tb.dim * esz;
+  // 4-byte stores: rows of any dim (a bf16 row of odd dim ends on 2 bytes).
+  if (bytes % 4 == 0 && reinterpret_cast<uint64_t>(v) % 4 == 0) {
+    uint32_t* w = reinterpret_cast<uint32_t*>(v);
+    for (int64_t i = lane; i < bytes / 4; i += kWave) w[i] = 0u;
+  } else {
+    uint16_t* w = reinterpret_cast<uint16_t*>(v);
+    for (int64_t i = lane; i < bytes / 2; i += kWave) w[i] = 0;
+  }
+}
+
 // --------------------------------------------------- allocation-free call --
 //
 // Scratch of mdl_backward_adagrad_noalloc: one static device array (each GPU
@@ -1100,6 +1155,21 @@ int mdl_backward_adagrad_noalloc(const mdl_feature* feats, int32_t num_features,
   if (rc) return rc;
   return mdl_backward_adagrad(feats, num_features, tables, num_tables, max_dim, sort_keys, sort_payload, n, count,
                               key_bits, bag_count, lr, eps, grad_scale, ws, kNoAllocScratchBytes, classes, stream);
+}
+
+int mdl_backward_pad(const mdl_table* tables, int32_t num_tables, const int64_t* unique_range,
+                     const uint64_t* rows_addr, const uint64_t* values_addr, const int64_t* capacity,
+                     const int64_t* unit_first, int64_t units, void* stream) {
+  if (num_tables <= 0 || units < 0) return fail(MDL_ERR_INVALID, "mdl_backward_pad: bad sizes");
+  if (units == 0) return MDL_OK;
+  if (!tables || !unique_range || !rows_addr || !values_addr || !capacity || !unit_first)
+    return fail(MDL_ERR_INVALID, "mdl_backward_pad: null pointer");
+  const int64_t blocks = (units + 3) / 4;
+  if (blocks > 0x7fffffffll) return fail(MDL_ERR_UNSUPPORTED, "mdl_backward_pad: too many rows");
+  hipLaunchKernelGGL(pad_kernel, dim3((unsigned)blocks), dim3(256), 0, as_stream(stream), tables, num_tables,
+                     unique_range, rows_addr, values_addr, capacity, unit_first, units);
+  MDL_CHECK_LAUNCH("pad_kernel");
+  return MDL_OK;
 }
 
 }  // extern "C"

@@ -82,6 +82,11 @@ enum CachePolicy { kKeep = 0, kStream = 1 };
 #define MDL_STREAM_OUT 1
 #endif
 constexpr int kUpdatePolicy = MDL_STREAM_UPDATE ? kStream : kKeep;
+// Gradient rows in the backward reduce: 0 keep, 1 stream the rows of tables
+// read by one unpooled feature (read once), 2 stream all.
+#ifndef MDL_STREAM_GRAD
+#define MDL_STREAM_GRAD 0
+#endif
 constexpr int kOutPolicy = MDL_STREAM_OUT ? kStream : kKeep;
 
 // fp32 rows copied eight elements per lane as two 16-byte pieces, lane sub

@@ -18,14 +18,13 @@ from dataclasses import asdict, dataclass
 from hashlib import sha256
 import json
 import threading
-import weakref
 from typing import Any, Iterable, Iterator, Literal
 
 import torch
 import torch.distributed as torch_dist
 from torch import Tensor, nn
 
-from . import ops
+from . import library, ops  # noqa: F401  (library registers the mdl_hip ops)
 
 _STATS_HOST_SYNC = threading.local()
 _DEFERRED = threading.local()
@@ -55,23 +54,39 @@ def embedding_stats_host_sync(enabled: bool) -> Iterator[None]:
         _STATS_HOST_SYNC.enabled = previous
 
 
-# ---------------------------------------------------- deferred id checks --
+# ------------------------------------------------------------- id checks --
+#
+# Ids outside [0, num_embeddings) are looked up as zero rows and counted on
+# the device.  How the count is checked on a ROCm device:
+#   "async" (default): torch._assert_async on the count -- no host sync, a
+#       device-side assert on failure, as the reference does on GPU
+#       (src/embeddings.py:140-147);
+#   "sync": one host read per lookup and the reference's IndexError naming
+#       the table and the first ids (the reference's CPU behaviour);
+#   "deferred": the count is added to a per-device counter and the next
+#       optimizer step (or check_index_errors()) raises IndexError.
+# CPU tensors always raise IndexError at once, like the reference's CPU path.
+_CHECK_MODES = ("async", "sync", "deferred")
+
+
+def set_index_check_mode(mode: str) -> None:
+    if mode not in _CHECK_MODES:
+        raise ValueError(f"index check mode must be one of {_CHECK_MODES}")
+    _DEFERRED.mode = mode
+
+
+def index_check_mode() -> str:
+    return getattr(_DEFERRED, "mode", "async")
 
 
 def set_deferred_index_checks(enabled: bool) -> None:
-    """Count out-of-range ids on the device instead of syncing per lookup.
+    """Deferred mode on (True) or back to the default asynchronous assert."""
 
-    The reference raises at once on CPU and reports through a device assert
-    on GPU (src/embeddings.py:140-147, :456-467).  Deferred mode keeps lookups
-    sync-free; :func:`check_index_errors` (called by the optimizer step)
-    raises ``IndexError`` for anything counted since the last check.
-    """
-
-    _DEFERRED.enabled = bool(enabled)
+    set_index_check_mode("deferred" if enabled else "async")
 
 
 def deferred_index_checks() -> bool:
-    return bool(getattr(_DEFERRED, "enabled", False))
+    return index_check_mode() == "deferred"
 
 
 _DEFERRED_COUNTERS: dict[torch.device, Tensor] = {}
@@ -317,7 +332,7 @@ def _distributed_rank_world(process_group: Any) -> tuple[int, int]:
 def _raise_for_errors(modules: list["ShardedEmbedding"], ids: list[Tensor], err: Tensor) -> None:
     """Reference error behaviour: IndexError naming the table and examples."""
 
-    if not int(err.item()):
+    if not int(err.reshape(-1)[0].item()):
         return
     for module, t in zip(modules, ids):
         flat = t.reshape(-1)
@@ -331,74 +346,24 @@ def _raise_for_errors(modules: list["ShardedEmbedding"], ids: list[Tensor], err:
     raise IndexError("embedding lookup received out-of-range IDs")
 
 
-# Sparse gradients this module produced already coalesced, by parameter.
-# Autograd's AccumulateGrad re-wraps a sparse gradient around the same index
-# and value storage but drops its coalesced flag; the optimizer compares the
-# storage with this record to restore the flag instead of sorting again.  A
-# gradient accumulated over several backward passes has new storage and is
-# coalesced normally.
-_COALESCED: dict[int, tuple] = {}
+def _check_ids(modules: list["ShardedEmbedding"], ids: list[Tensor], err: Tensor) -> None:
+    if not any(m.validate_indices for m in modules):
+        return
+    checked = [m for m in modules if m.validate_indices]
+    if err.device.type != "cuda":
+        _raise_for_errors(modules, ids, err)
+        return
+    mode = index_check_mode()
+    if mode == "sync":
+        _raise_for_errors(modules, ids, err)
+    elif mode == "deferred":
+        _deferred_counter(err.device).add_(err.reshape(-1)[:1])
+    else:
+        names = ", ".join(repr(m.table_name) for m in checked[:4])
+        torch._assert_async(err.reshape(-1)[0] == 0, f"embedding {names} received an out-of-range ID")
 
 
-def _remember_coalesced(parameter: Tensor, rows: Tensor, vals: Tensor) -> None:
-    for key in [k for k, (ref, _, _) in _COALESCED.items() if ref() is None]:
-        del _COALESCED[key]
-    _COALESCED[id(parameter)] = (weakref.ref(parameter), rows, vals)
-
-
-def known_coalesced(parameter: Tensor, grad: Tensor) -> bool:
-    """Whether ``grad`` is the coalesced gradient last emitted for ``parameter``."""
-
-    entry = _COALESCED.get(id(parameter))
-    if entry is None or entry[0]() is not parameter:
-        return False
-    _, rows, vals = entry
-    idx, val = grad._indices(), grad._values()
-    return (
-        idx.data_ptr() == rows.data_ptr()
-        and val.data_ptr() == vals.data_ptr()
-        and idx.size(-1) == rows.numel()
-        and tuple(val.shape) == tuple(vals.shape)
-    )
-
-
-def forget_coalesced(parameter: Tensor) -> None:
-    _COALESCED.pop(id(parameter), None)
-
-
-class _GroupedLookupFn(torch.autograd.Function):
-    """Grouped lookup whose weight gradients are coalesced sparse COO tensors."""
-
-    @staticmethod
-    def forward(ctx, ctl: dict, *tensors: Tensor):  # type: ignore[override]
-        plan: ops.GroupPlan = ctl["plan"]
-        nf = len(plan.features)
-        ids = list(tensors[:nf])
-        lengths = ctl["lengths"]
-        weights = tensors[nf:]
-        need_grad = any(w.requires_grad for w in weights)
-        err = ctl.get("error_count")
-        res = ops.grouped_forward(plan, ids, lengths, with_backward=need_grad, error_count=err)
-        if ctl.get("check", True):
-            _raise_for_errors(ctl["modules"], ids, res.error_count)
-        ctx.res = res
-        ctx.nf = nf
-        ctx.weights = list(weights)
-        return tuple(res.outputs)
-
-    @staticmethod
-    def backward(ctx, *grads: Tensor):  # type: ignore[override]
-        res: ops.ForwardResult = ctx.res
-        coalesced = ops.backward_coalesce(res, list(grads))
-        ctx.res = None
-        out: list[Tensor | None] = [None] * ctx.nf
-        for (rows, vals), weight in zip(coalesced, ctx.weights):
-            out.append(
-                torch.sparse_coo_tensor(rows.unsqueeze(0), vals, tuple(weight.shape), is_coalesced=True)
-            )
-            _remember_coalesced(weight, rows, vals)
-        ctx.weights = None
-        return (None, *out)
+_POOLING_CODES = {"none": 0, "sum": 1, "mean": 2}
 
 
 def _grouped_lookup(
@@ -408,26 +373,28 @@ def _grouped_lookup(
     poolings: list[str],
     null_policies: list[str],
 ) -> list[Tensor]:
-    plan = ops.GroupPlan()
+    """One ``mdl_hip::grouped_lookup`` call for every request; requests on
+    the same module share its table (one coalesced gradient per table)."""
+
     weights: list[Tensor] = []
-    seen: set[int] = set()
-    for module, pooling, policy in zip(modules, poolings, null_policies):
-        plan.add_feature(
-            module.weight, pooling=pooling, null_policy=policy, padding_idx=module.padding_idx
-        )
-        if id(module.weight) not in seen:
-            seen.add(id(module.weight))
+    index: dict[int, int] = {}
+    table = []
+    for module in modules:
+        key = id(module.weight)
+        if key not in index:
+            index[key] = len(weights)
             weights.append(module.weight)
-    deferred = deferred_index_checks()
-    validate = any(m.validate_indices for m in modules)
-    ctl = {
-        "plan": plan,
-        "lengths": lengths,
-        "modules": modules,
-        "check": validate and not deferred,
-        "error_count": _deferred_counter(weights[0].device) if deferred else None,
-    }
-    return list(_GroupedLookupFn.apply(ctl, *ids, *weights))
+        table.append(index[key])
+    for policy in null_policies:
+        if policy not in ("exclude", "include_as_padding"):
+            raise ValueError(f"unsupported categorical bag null policy {policy!r}")
+    need_backward = torch.is_grad_enabled() and any(w.requires_grad for w in weights)
+    outputs, _, _, _, _, err = torch.ops.mdl_hip.grouped_lookup(
+        weights, list(ids), list(lengths), table, [_POOLING_CODES[p] for p in poolings],
+        [1 if p == "exclude" else 0 for p in null_policies], [int(m.padding_idx) for m in modules], need_backward,
+    )
+    _check_ids(modules, list(ids), err)
+    return list(outputs)
 
 
 # ----------------------------------------------------------------- module --
@@ -596,36 +563,6 @@ def pooled_embedding_lookup(
     )
 
 
-class _SequenceLookupFn(torch.autograd.Function):
-    """Right-aligned sequence lookup with a coalesced sparse weight gradient."""
-
-    @staticmethod
-    def forward(ctx, ctl: dict, ids: Tensor, lengths: Tensor, weight: Tensor):  # type: ignore[override]
-        module: ShardedEmbedding = ctl["module"]
-        err = ctl.get("error_count")
-        res = ops.sequence_lookup(
-            weight, ids, lengths, out_len=ctl["out_len"], order=ctl["order"], padding_idx=module.padding_idx,
-            with_backward=weight.requires_grad, error_count=err,
-        )
-        if ctl.get("check", True):
-            _raise_for_errors([module], [ids], res.error_count)
-        ctx.res = res
-        ctx.weight = weight
-        mask = res.keep[0]
-        ctx.mark_non_differentiable(mask)
-        return res.outputs[0], mask
-
-    @staticmethod
-    def backward(ctx, grad_out: Tensor, _grad_mask):  # type: ignore[override]
-        (rows, vals), = ops.backward_coalesce(ctx.res, [grad_out])
-        weight = ctx.weight
-        ctx.res = None
-        ctx.weight = None
-        grad = torch.sparse_coo_tensor(rows.unsqueeze(0), vals, tuple(weight.shape), is_coalesced=True)
-        _remember_coalesced(weight, rows, vals)
-        return None, None, None, grad
-
-
 def sequence_embedding_lookup(
     module: ShardedEmbedding,
     ids: Tensor,
@@ -649,15 +586,14 @@ def sequence_embedding_lookup(
         raise ValueError("sequence ids must be [B, L] with lengths [B]")
     if sequence_order not in ("oldest_to_newest", "newest_to_oldest"):
         raise ValueError("sequence_order must be oldest_to_newest or newest_to_oldest")
-    deferred = deferred_index_checks()
-    ctl = {
-        "module": module,
-        "out_len": int(ids.size(1) if target_length is None else target_length),
-        "order": sequence_order,
-        "check": module.validate_indices and not deferred,
-        "error_count": _deferred_counter(module.weight.device) if deferred else None,
-    }
-    out, mask = _SequenceLookupFn.apply(ctl, ids, lengths, module.weight)
+    w = module.weight
+    need_backward = torch.is_grad_enabled() and w.requires_grad
+    out, mask, _, _, err = torch.ops.mdl_hip.sequence_lookup(
+        w, ids, lengths.to(device=ids.device, dtype=torch.int64), int(ids.size(1) if target_length is None
+                                                                      else target_length),
+        sequence_order == "newest_to_oldest", int(module.padding_idx), need_backward,
+    )
+    _check_ids([module], [ids], err)
     if module.collect_stats and embedding_stats_host_sync_enabled():
         module._stats_sink.record_forward(_local_stats(module.table_name, int(ids.numel())))
     return out, mask

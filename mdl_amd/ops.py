@@ -356,10 +356,11 @@ class ForwardResult:
     bag_count: Tensor | None
     error_count: Tensor
     keep: list = field(default_factory=list)
+    count: int | None = None  # ids of the call when ``ids`` is not the concatenated array
 
     @property
     def num_ids(self) -> int:
-        return int(self.ids.numel())
+        return int(self.ids.numel()) if self.count is None else int(self.count)
 
 
 class _UploadCache:
@@ -901,6 +902,161 @@ def backward_coalesce(res: ForwardResult, grads: Sequence[Tensor | None]) -> lis
     res.payload = None
     del keep
     return result
+
+
+def table_capacities(res: ForwardResult) -> np.ndarray:
+    """Ids looked up on each table by this forward (host-known from the
+    shapes): a bound on its distinct rows."""
+
+    cap = np.zeros(len(res.plan.tables), dtype=np.int64)
+    np.add.at(cap, np.asarray(res.feats["table"], dtype=np.int64), np.asarray(res.feats["num_ids"], dtype=np.int64))
+    return cap
+
+
+def backward_coalesce_padded(
+    res: ForwardResult, grads: Sequence[Tensor | None]
+) -> tuple[list[Tensor], list[Tensor], Tensor]:
+    """Coalesced sparse gradient of every table without a host read.
+
+    Table t gets ``rows`` int64 ``[cap_t]`` and ``values`` ``[cap_t, dim]``
+    (its dtype), ``cap_t`` its id count: the first ``counts[t]`` entries are
+    the coalesced gradient (rows ascending, unique), the rest repeat the last
+    row with zero values, so the pair is a valid uncoalesced COO gradient with
+    the same sum.  ``counts`` is a device int64 ``[T]``.  Only launches.
+    """
+
+    plan = res.plan
+    if res.keys is None:
+        raise RuntimeError("the forward ran without backward bookkeeping")
+    feats, keep = _attach_grads(res, grads)
+    tables = _tables_array(plan, feats)
+    device = res.device
+    n = res.num_ids
+    T = len(tables)
+    stream = _stream(device)
+    cap = table_capacities(res)
+    esz = np.array([t.weight.element_size() for t in plan.tables], dtype=np.int64)
+    dims = np.array([int(t.weight.size(1)) for t in plan.tables], dtype=np.int64)
+    nbytes = cap * dims * esz
+    offs = np.zeros(T + 1, dtype=np.int64)
+    np.cumsum((nbytes + 255) // 256 * 256, out=offs[1:])
+    rows_off = np.zeros(T + 1, dtype=np.int64)
+    np.cumsum(cap, out=rows_off[1:])
+    rows_all = torch.empty(max(int(rows_off[-1]), 1), dtype=torch.int64, device=device)
+    vbuf = torch.empty(max(int(offs[-1]), 1), dtype=torch.uint8, device=device)
+    urange = torch.zeros(2 * T, dtype=torch.int64, device=device)
+    if n:
+        pad_units = (cap + 63) // 64
+        unit_first = np.zeros(T + 1, dtype=np.int64)
+        np.cumsum(pad_units, out=unit_first[1:])
+        # one upload: row and value addresses, capacities, pad-unit prefix
+        host = np.concatenate([
+            np.where(cap > 0, rows_all.data_ptr() + 8 * rows_off[:T], 0).astype(np.uint64).view(np.int64),
+            np.where(cap > 0, vbuf.data_ptr() + offs[:T], 0).astype(np.uint64).view(np.int64),
+            cap, unit_first,
+        ])
+        meta = upload(host, device)
+        base = meta.data_ptr()
+        feats_dev = _CACHE.get(feats, device)
+        tables_dev = _CACHE.get(tables, device)
+        ws = _workspace(lib().mdl_backward_workspace_bytes(n, T, plan.max_dim), device)
+        check(
+            lib().mdl_backward_count(
+                tables_dev.data_ptr(), T, plan.max_dim, res.keys.data_ptr(), res.payload.data_ptr(), n, None,
+                plan.key_bits, urange.data_ptr(), ws.data_ptr(), ws.numel(), stream,
+            ),
+            "mdl_backward_count",
+        )
+        check(
+            lib().mdl_backward_coalesce(
+                feats_dev.data_ptr(), len(feats), tables_dev.data_ptr(), T, plan.max_dim, res.keys.data_ptr(),
+                res.payload.data_ptr(), n, plan.key_bits, _ptr(res.bag_count), urange.data_ptr(), base,
+                base + 8 * T, ws.data_ptr(), ws.numel(), table_classes(tables), stream,
+            ),
+            "mdl_backward_coalesce",
+        )
+        check(
+            lib().mdl_backward_pad(
+                tables_dev.data_ptr(), T, urange.data_ptr(), base, base + 8 * T, base + 16 * T, base + 24 * T,
+                int(unit_first[-1]), stream,
+            ),
+            "mdl_backward_pad",
+        )
+        keep.append(meta)
+    rows_list = list(rows_all[: int(rows_off[-1])].split(cap.tolist()))
+    vals_list = []
+    for t, table in enumerate(plan.tables):
+        w = table.weight
+        vals_list.append(vbuf[int(offs[t]): int(offs[t]) + int(nbytes[t])].view(w.dtype).view(int(cap[t]), int(dims[t])))
+    counts = urange[1::2] - urange[0::2]
+    res.keys = None
+    res.payload = None
+    del keep
+    return rows_list, vals_list, counts
+
+
+def grouped_rowwise_adagrad_(
+    weights: Sequence[Tensor],
+    accumulators: Sequence[Tensor],
+    rows: Sequence[Tensor],
+    values: Sequence[Tensor],
+    counts: Sequence[Tensor | None],
+    lrs: Sequence[float],
+    *,
+    eps: float,
+    error_count: Tensor | None = None,
+) -> None:
+    """Row-wise Adagrad of many tables in one launch (src/optim.py:299-377).
+
+    Table i updates rows[i][:n] with values[i][:n], n read on the device from
+    ``counts[i]`` (an int64 element; None: all rows).  Rows must be unique.
+    """
+
+    if not weights:
+        return
+    device = weights[0].device
+    ups = np.zeros(len(weights), dtype=_lib.UPDATE_DTYPE)
+    keep = []
+    unit = 0
+    for i, (w, a, r, v, c, lr) in enumerate(zip(weights, accumulators, rows, values, counts, lrs)):
+        _require_device(w, "weight")
+        if w.ndim != 2 or w.stride(1) != 1:
+            raise ValueError("row-wise Adagrad expects 2D weights with contiguous rows")
+        if a.dtype != torch.float32 or not a.is_contiguous():
+            raise TypeError("row-wise Adagrad accumulator must be a contiguous float32 tensor")
+        r = r.to(torch.int64).contiguous()
+        if w.dtype == torch.float32 and v.dtype != torch.float32:
+            v = v.float()
+        if v.dtype not in (torch.float32, torch.bfloat16):
+            v = v.float()
+        v = _row_major_aligned(v)
+        keep += [r, v]
+        cap = int(r.numel())
+        u = ups[i]
+        u["weight"] = w.data_ptr()
+        u["state"] = a.data_ptr()
+        u["rows"] = r.data_ptr()
+        u["values"] = v.data_ptr()
+        u["count"] = 0 if c is None else c.data_ptr()
+        u["num_rows"] = int(w.size(0))
+        u["capacity"] = cap
+        u["weight_stride"] = w.stride(0)
+        u["values_stride"] = v.stride(0) if v.ndim == 2 and v.size(0) else int(w.size(1))
+        u["unit_first"] = unit
+        u["dim"] = int(w.size(1))
+        u["wdtype"] = dtype_code(w.dtype)
+        u["vdtype"] = dtype_code(v.dtype)
+        u["lr"] = float(lr)
+        unit += (cap + _lib.MDL_UPDATE_UNIT - 1) // _lib.MDL_UPDATE_UNIT
+    if unit == 0:
+        return
+    ups_dev = upload(ups, device)
+    check(
+        lib().mdl_grouped_rowwise_adagrad(ups_dev.data_ptr(), ups.ctypes.data, len(ups), float(eps),
+                                          _ptr(error_count), _stream(device)),
+        "mdl_grouped_rowwise_adagrad",
+    )
+    del keep
 
 
 def coalesce_rows(

@@ -3,8 +3,12 @@
 Same constructor, state layout (``step``: 0-d float64 on CPU, ``sum``: one
 fp32 accumulator per row) and ``load_state_dict`` behaviour as
 src/optim.py:212-377, so checkpoints move between the two unchanged.
-Gradients must be sparse COO on a ROCm device; uncoalesced ones are coalesced
-by the library's sort/segment-reduce before the update.
+Gradients must be sparse COO.  ``step`` updates every parameter of a device
+with one ``mdl_hip::grouped_rowwise_adagrad_`` launch: a gradient emitted by
+the grouped lookup is capacity-sized with its row count on the device, so
+the step needs no host read; any other gradient is coalesced by the
+library's sort/segment-reduce first.  Parameters on the CPU take the
+reference's CPU branch (src/optim.py:359-376) through the same ops.
 """
 
 from __future__ import annotations
@@ -16,28 +20,37 @@ from typing import Any, Callable
 import torch
 from torch import Tensor, nn
 
-from . import embeddings, ops
+from . import embeddings, library
+
+
+def update_rows(parameter: Tensor) -> tuple[Tensor, Tensor, Tensor | None]:
+    """``(rows, values, count)`` of the parameter's sparse gradient, rows
+    unique and ascending: a gradient the lookup emitted (``count``: its row
+    count on the device), or the gradient coalesced by ``mdl_hip::sparse_coalesce``
+    (one host read to size it, like ``grad.coalesce()`` in src/optim.py:323-324),
+    stored back as ``parameter.grad`` (``count`` None: all rows)."""
+
+    grad = parameter.grad
+    known = library.capacity_grad(parameter, grad)
+    if known is not None:
+        return known
+    if grad.is_coalesced():
+        return grad._indices()[0], grad._values(), None
+    rows, values = torch.ops.mdl_hip.sparse_coalesce(grad._indices()[0], grad._values(), int(parameter.shape[0]))
+    parameter.grad = torch.sparse_coo_tensor(rows.unsqueeze(0), values, tuple(grad.shape), is_coalesced=True)
+    return rows, values, None
 
 
 def coalesced_grad(parameter: Tensor) -> Tensor:
-    """The parameter's sparse COO gradient, coalesced on the device.
+    """The parameter's sparse gradient with every row's summed value once.
 
-    A gradient that the grouped lookup emitted already coalesced only gets
-    its flag restored (autograd drops it); any other is coalesced by the HIP
-    sort + segment reduction and stored back as ``parameter.grad``, like
-    ``grad.coalesce()`` in src/optim.py:323-324 and src/train.py:5736-5738.
-    """
+    A capacity-sized gradient of the lookup is returned as it is: its entries
+    past the row count repeat a row with zero values, which changes no norm
+    and no scaling (src/train.py:5730-5826 read only the values).  Any other
+    uncoalesced gradient is coalesced on the device and stored back."""
 
-    grad = parameter.grad
-    if not grad.is_coalesced() and embeddings.known_coalesced(parameter, grad):
-        grad._coalesced_(True)
-    if grad.is_coalesced():
-        return grad
-    rows, values = ops.coalesce_rows(grad._indices()[0], grad._values(), int(parameter.shape[0]))
-    grad = torch.sparse_coo_tensor(rows.unsqueeze(0), values, tuple(grad.shape), is_coalesced=True)
-    parameter.grad = grad
-    embeddings._remember_coalesced(parameter, rows, values)
-    return grad
+    update_rows(parameter)
+    return parameter.grad
 
 
 def fused_rowwise_adagrad_update(
@@ -57,7 +70,7 @@ def fused_rowwise_adagrad_update(
 
     if rows.numel() == 0:
         return
-    ops.rowwise_adagrad_(parameter, accumulator, rows, values, lr=lr, eps=eps)
+    torch.ops.mdl_hip.rowwise_adagrad_(parameter, accumulator, rows, values, float(lr), float(eps))
 
 
 class ShardedRowWiseAdagrad(torch.optim.Optimizer):
@@ -151,6 +164,8 @@ class ShardedRowWiseAdagrad(torch.optim.Optimizer):
                 loss = closure()
         if embeddings.deferred_index_checks():
             embeddings.check_index_errors()
+        # every parameter of one device (and eps) in one launch
+        batches: dict[tuple, list] = {}
         for group in self.param_groups:
             eps = float(group["eps"])
             for parameter in group["params"]:
@@ -165,19 +180,17 @@ class ShardedRowWiseAdagrad(torch.optim.Optimizer):
                     raise RuntimeError(
                         "ShardedRowWiseAdagrad expects one sparse row dimension and one dense dimension"
                     )
-                grad = coalesced_grad(parameter)
-                embeddings.forget_coalesced(parameter)
-                rows = grad.indices()[0]
-                values = grad.values()
+                rows, values, count = update_rows(parameter)
                 clear_lr = self._advance(parameter, group)
-                if rows.numel() == 0:
-                    continue
                 accumulator: Tensor = self.state[parameter]["sum"]
-                if not (parameter.is_cuda and accumulator.is_cuda):
-                    raise RuntimeError(
-                        "ShardedRowWiseAdagrad runs on ROCm devices only (libmdl_hip)"
-                    )
-                fused_rowwise_adagrad_update(
-                    parameter, accumulator, rows, values, lr=clear_lr, eps=eps
+                batches.setdefault((parameter.device, eps), []).append(
+                    (parameter, accumulator, rows, values, count, clear_lr)
                 )
+        for (_, eps), items in batches.items():
+            torch.ops.mdl_hip.grouped_rowwise_adagrad_(
+                [i[0] for i in items], [i[1] for i in items], [i[2] for i in items], [i[3] for i in items],
+                [i[4] for i in items], [i[5] for i in items], eps,
+            )
+            for item in items:
+                library.forget_capacity_grad(item[0])
         return loss

@@ -35,6 +35,7 @@ def test_struct_layout_matches_header(tmp_path):
         "mdl_feature": _lib.FEATURE_DTYPE,
         "mdl_chunk": _lib.CHUNK_DTYPE,
         "mdl_table": _lib.TABLE_DTYPE,
+        "mdl_update": _lib.UPDATE_DTYPE,
     }
     lines = ['#include <stdio.h>', '#include <stddef.h>', f'#include "{HEADER}"', "int main(void){"]
     for st, dt in fields.items():

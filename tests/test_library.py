@@ -1,0 +1,228 @@
+"""The mdl_hip torch.library ops on the CPU (no GPU needed).
+
+Every op passes ``torch.library.opcheck`` (schema, autograd registration,
+fake tensors, AOT dispatch); the drop-in modules train on CPU parameters
+through the same ops, checked against the C oracle and the reference tests'
+golden vectors (tests/test_rowwise_adagrad.py); the CPU bucketing matches
+the oracle bit for bit.
+"""
+
+import json
+import pathlib
+
+import numpy as np
+import pytest
+import torch
+from torch import nn
+from torch.library import opcheck
+
+import mdl_amd.library  # noqa: F401  (registers the ops)
+from mdl_amd.embeddings import (
+    EmbeddingTableSpec,
+    ShardedEmbedding,
+    grouped_sharded_embedding_lookup,
+    plan_embedding_shards,
+    pooled_embedding_lookup,
+    sequence_embedding_lookup,
+)
+from mdl_amd.optim import ShardedRowWiseAdagrad
+from oracle import oracle as O
+
+GOLD = json.loads((pathlib.Path(__file__).parent / "golden" / "reference_vectors.json").read_text())
+OPS = torch.ops.mdl_hip
+
+
+def _lookup_args(requires_grad=True):
+    torch.manual_seed(0)
+    W = [torch.randn(20, 4, requires_grad=requires_grad), torch.randn(9, 8, requires_grad=requires_grad)]
+    ids = [torch.tensor([1, 0, 5, 5, 19]), torch.tensor([[3, 4], [0, 8]]), torch.tensor([2, 2, 7])]
+    ln = [torch.tensor([2, 0, 3]), None, torch.tensor([1, 2])]
+    return (W, ids, ln, [0, 1, 1], [2, 0, 1], [1, 0, 0], [0, 0, 0], True)
+
+
+@pytest.mark.parametrize("name", ["grouped_lookup", "sequence_lookup", "rowwise_adagrad_", "grouped_rowwise_adagrad_",
+                                  "bucketize", "lengths_to_offsets", "sparse_coalesce", "grouped_lookup_backward",
+                                  "sequence_lookup_backward"])
+def test_opcheck_cpu(name):
+    if name == "grouped_lookup":
+        args = _lookup_args()
+    elif name == "grouped_lookup_backward":
+        W, ids, ln, table, pooling, exclude, pad, _ = _lookup_args(False)
+        grads = [torch.randn(3, 4), torch.randn(2, 2, 8), torch.randn(2, 8)]
+        e = torch.empty(0, dtype=torch.int32)
+        args = (W, ids, ln, table, pooling, exclude, pad, grads, e, e.clone(), torch.zeros(8), torch.zeros(0,
+                                                                                                        dtype=torch.int64))
+    elif name == "sequence_lookup":
+        args = (torch.randn(6, 4, requires_grad=True), torch.tensor([[1, 2, 0], [5, 5, 5]]), torch.tensor([2, 3]), 4,
+                False, 0, True)
+    elif name == "sequence_lookup_backward":
+        e = torch.empty(0, dtype=torch.int32)
+        args = (torch.randn(6, 4), torch.tensor([[1, 2, 0], [5, 5, 5]]), torch.tensor([2, 3]), 4, True, 0,
+                torch.randn(2, 4, 4), e, e.clone())
+    elif name == "rowwise_adagrad_":
+        args = (torch.randn(10, 4), torch.zeros(10), torch.tensor([1, 3]), torch.randn(2, 4), 0.1, 1e-8)
+    elif name == "grouped_rowwise_adagrad_":
+        args = ([torch.randn(10, 4), torch.randn(5, 2)], [torch.zeros(10), torch.zeros(5)],
+                [torch.tensor([1, 3, 3]), torch.tensor([0])], [torch.randn(3, 4), torch.randn(1, 2)],
+                [torch.tensor([2]), None], [0.1, 0.2], 1e-8)
+    elif name == "bucketize":
+        args = (torch.tensor([0, -1, 7, -(1 << 63)]), torch.tensor([1, 1, 0, 1], dtype=torch.uint8), 8, "pre_hashed",
+                True)
+    elif name == "lengths_to_offsets":
+        args = (torch.tensor([3, 0, 2]),)
+    else:
+        args = (torch.tensor([3, 1, 3]), torch.randn(3, 4), 10)
+    opcheck(getattr(OPS, name).default, args)
+
+
+def test_cpu_bucketize_matches_oracle_bit_for_bit():
+    rng = np.random.default_rng(5)
+    raw = rng.integers(-(1 << 63), (1 << 63) - 1, size=20000, dtype=np.int64, endpoint=True)
+    raw[:4] = [-(1 << 63), (1 << 63) - 1, 0, -1]
+    valid = (rng.random(raw.size) > 0.1).astype(np.uint8)
+    for buckets in (1, 8, 1 << 20, 1 << 40):
+        out, err = OPS.bucketize(torch.from_numpy(raw), torch.from_numpy(valid), buckets, "pre_hashed", True)
+        ref, zeros = O.bucketize_pre_hashed(raw, buckets, valid)
+        assert np.array_equal(out.numpy(), ref) and int(err) == zeros
+    for rows in (2, 3, 1_000_000, (1 << 40) + 2, (1 << 62) + 1):
+        out, _ = OPS.bucketize(torch.from_numpy(raw), None, rows, "mod", False)
+        assert np.array_equal(out.numpy(), O.bucketize_mod(raw, rows))
+
+
+def _modules(specs, dtype=torch.float32):
+    plan = plan_embedding_shards([EmbeddingTableSpec(n, r, d) for n, r, d in specs], world_size=1,
+                                 strategy="row_wise", table_wise_max_rows=32)
+    return [ShardedEmbedding(r, d, table_name=n, shard_spec=plan.tables[n], collect_stats=False, dtype=dtype)
+            for n, r, d in specs]
+
+
+def test_cpu_training_steps_match_oracle():
+    """Mean and sum bags plus a single-valued lookup, loss.backward() and
+    optimizer.step() on CPU parameters, three steps, against the C oracle."""
+
+    rng = np.random.default_rng(91)
+    mods = _modules([("bag_a", 300, 8), ("bag_b", 80, 4), ("single", 500, 16)])
+    opt = ShardedRowWiseAdagrad([m.weight for m in mods], lr=0.05, eps=1e-8)
+    W = [m.weight.detach().numpy().copy() for m in mods]
+    A = [np.zeros(m.weight.shape[0], np.float32) for m in mods]
+    B = 64
+    for step in range(3):
+        la = rng.integers(0, 9, size=B)
+        lb = rng.integers(1, 5, size=B)
+        xa = rng.zipf(1.2, size=int(la.sum())) % 300
+        xb = rng.integers(0, 80, size=int(lb.sum()))
+        xs = rng.integers(0, 500, size=B)
+        opt.zero_grad(set_to_none=True)
+        pooled = pooled_embedding_lookup([(mods[0], torch.from_numpy(xa), torch.from_numpy(la), "mean", "exclude"),
+                                          (mods[1], torch.from_numpy(xb), torch.from_numpy(lb), "sum", "exclude")])
+        single = grouped_sharded_embedding_lookup([(mods[2], torch.from_numpy(xs))])[0]
+        outs = [pooled[0], pooled[1], single]
+        grads = [torch.randn(o.shape) for o in outs]
+        torch.autograd.backward(outs, grads)
+        opt.step()
+        for t, (x, ln, mode) in enumerate(((xa, la, "mean"), (xb, lb, "sum"), (xs, None, "none"))):
+            r, v = O.per_id_grads(x, ln, grads[t].double().numpy(), mode, "exclude")
+            r, v = O.coalesce(r, v)
+            W[t], A[t] = O.rowwise_adagrad(W[t], A[t], r, v, 0.05, 1e-8)
+    for t, m in enumerate(mods):
+        np.testing.assert_allclose(m.weight.detach().numpy(), W[t], rtol=1e-5, atol=1e-6)
+        np.testing.assert_allclose(opt.state[m.weight]["sum"].numpy(), A[t], rtol=1e-5, atol=1e-6)
+        assert opt.state[m.weight]["step"].item() == 3.0
+
+
+def test_cpu_sequence_lookup_and_step_match_oracle():
+    rng = np.random.default_rng(92)
+    (m,) = _modules([("hist", 400, 8)])
+    opt = ShardedRowWiseAdagrad([m.weight], lr=0.05, eps=1e-8)
+    W0 = m.weight.detach().numpy().copy()
+    B, L = 12, 30
+    lengths = rng.integers(0, L + 5, size=B)
+    ids = np.zeros((B, L), dtype=np.int64)
+    for b in range(B):
+        k = min(int(lengths[b]), L)
+        ids[b, :k] = rng.zipf(1.1, size=k) % 400
+    out, mask = sequence_embedding_lookup(m, torch.from_numpy(ids), torch.from_numpy(lengths), target_length=20,
+                                          sequence_order="newest_to_oldest")
+    ref, rmask = O.sequence_gather(W0, ids, lengths, 20, "newest_to_oldest")
+    assert np.array_equal(mask.numpy(), rmask) and np.array_equal(out.detach().numpy(), ref.astype(np.float32))
+    g = rng.standard_normal(tuple(out.shape)).astype(np.float32)
+    out.backward(torch.from_numpy(g))
+    opt.step()
+    r, v = O.sequence_grads(ids, lengths, g, 20, "newest_to_oldest")
+    r, v = O.coalesce(r, v)
+    wexp, aexp = O.rowwise_adagrad(W0, np.zeros(400, np.float32), r, v, 0.05, 1e-8)
+    np.testing.assert_allclose(m.weight.detach().numpy(), wexp, rtol=1e-5, atol=1e-6)
+    np.testing.assert_allclose(opt.state[m.weight]["sum"].numpy(), aexp, rtol=1e-5, atol=1e-7)
+
+
+def _coo(rows, values, size, dtype=torch.float32):
+    return torch.sparse_coo_tensor(torch.tensor([rows], dtype=torch.int64), torch.tensor(values, dtype=dtype),
+                                   size=size)
+
+
+def test_cpu_adagrad_golden_vectors():
+    """The reference tests' cases on CPU parameters (tests/test_rowwise_adagrad.py:40-128)."""
+
+    g = GOLD["rowwise_adagrad_mean_not_sum"]
+    p = nn.Parameter(torch.zeros(*g["shape"]))
+    opt = ShardedRowWiseAdagrad([p], lr=g["lr"], initial_accumulator_value=0.0, eps=g["eps"])
+    p.grad = _coo(g["rows"], g["values"], p.shape).coalesce()
+    opt.step()
+    for r, a in g["expected_acc"].items():
+        assert abs(float(opt.state[p]["sum"][int(r)]) - a) < 1e-6
+    for r, w in g["expected_neg_weight"].items():
+        assert torch.allclose(p[int(r)].neg(), torch.tensor(w), atol=g["atol"])
+    g = GOLD["rowwise_adagrad_duplicates_coalesce"]
+    p = nn.Parameter(torch.zeros(*g["shape"]))
+    opt = ShardedRowWiseAdagrad([p], lr=g["lr"], initial_accumulator_value=0.0, eps=g["eps"])
+    p.grad = _coo(g["rows"], g["values"], p.shape)
+    opt.step()
+    assert abs(float(opt.state[p]["sum"][3]) - g["expected_acc"]["3"]) < 1e-6
+    assert int((opt.state[p]["sum"] != 0).sum()) == g["expected_nonzero_acc_rows"]
+    g = GOLD["rowwise_adagrad_empty_noop"]
+    p = nn.Parameter(torch.ones(*g["shape"]))
+    opt = ShardedRowWiseAdagrad([p], lr=g["lr"], initial_accumulator_value=g["acc0"])
+    p.grad = torch.sparse_coo_tensor(torch.empty((1, 0), dtype=torch.int64), torch.empty((0, 2)), size=p.shape)
+    opt.step()
+    assert torch.equal(p, torch.ones(*g["shape"]))
+    assert float(opt.state[p]["step"].item()) == g["expected_step"]
+    g = GOLD["rowwise_adagrad_bf16_untouched"]
+    p = nn.Parameter(torch.tensor(g["weight"], dtype=torch.bfloat16))
+    before = p.detach().clone()
+    opt = ShardedRowWiseAdagrad([p], lr=g["lr"], initial_accumulator_value=0.0, eps=g["eps"])
+    p.grad = _coo(g["rows"], g["values"], p.shape, dtype=torch.bfloat16).coalesce()
+    opt.step()
+    for r in g["untouched_rows"]:
+        assert torch.equal(p[r], before[r])
+    assert abs(float(opt.state[p]["sum"][1]) - g["expected_acc_row1"]) < 1e-6
+
+
+def test_cpu_errors_follow_the_reference():
+    (m,) = _modules([("t", 10, 4)])
+    with pytest.raises(IndexError, match=r"embedding 't' received IDs outside \[0, 10\): \[10, -1\]"):
+        m(torch.tensor([1, 10, -1]))
+    with pytest.raises(TypeError, match="torch.long"):
+        m(torch.tensor([1, 2], dtype=torch.int32))
+    opt = ShardedRowWiseAdagrad([m.weight], lr=0.1)
+    m.weight.grad = torch.zeros_like(m.weight)
+    with pytest.raises(RuntimeError, match="row-sparse COO"):
+        opt.step()
+
+
+def test_capacity_gradient_is_a_valid_coo_of_the_coalesced_sum():
+    """The lookup's gradient has one entry per id (a bound known without a
+    device read); coalescing it gives the exact coalesced gradient."""
+
+    (m,) = _modules([("t", 50, 4)])
+    ids = torch.tensor([7, 3, 7, 0, 9, 3])
+    out = m(ids)
+    g = torch.randn(out.shape)
+    out.backward(g)
+    grad = m.weight.grad
+    assert grad._indices().size(1) == ids.numel()
+    dense = torch.zeros(50, 4)
+    dense.index_add_(0, ids, g)
+    dense[0] = 0  # padding_idx gets no gradient
+    torch.testing.assert_close(grad.to_dense(), dense)
+    c = grad.coalesce()
+    assert c.indices()[0].tolist() == [3, 7, 9]
