@@ -18,6 +18,7 @@ Ops:
 ``mdl_hip::sequence_lookup``           right-aligned sequence window gather (src/model.py:2989-3100)
 ``mdl_hip::sequence_lookup_backward``  its coalesced sparse weight gradient, capacity-sized
 ``mdl_hip::sparse_coalesce``           sort + unique + segment sum of a COO gradient (src/optim.py:321-324)
+``mdl_hip::sparse_coalesce_padded``    the same, capacity-sized (no host read)
 ``mdl_hip::rowwise_adagrad_``          row-wise Adagrad of one table (src/optim.py:68-108, CPU :359-376)
 ``mdl_hip::grouped_rowwise_adagrad_``  row-wise Adagrad of many tables in one launch, row counts read on device
 
@@ -31,6 +32,7 @@ read; ``grouped_rowwise_adagrad_`` reads ``counts`` on the device.
 
 from __future__ import annotations
 
+import weakref
 from typing import Optional
 
 import numpy as np
@@ -252,10 +254,12 @@ def grouped_lookup_backward(
     weights: list[Tensor], ids: list[Tensor], lengths: list[Optional[Tensor]], table: list[int],
     pooling: list[int], exclude: list[int], padding_idx: list[int], grads: list[Tensor], keys: Tensor,
     payload: Tensor, bag_count: Tensor, offsets: Tensor,
-) -> tuple[list[Tensor], list[Tensor], Tensor]:
-    """Capacity-sized coalesced gradients ``(rows, values)`` of every table
-    and their device row counts (int64 ``[T]``).  The sort works on copies of
-    the keys and payloads, so the op leaves its inputs as they are."""
+) -> tuple[Tensor, Tensor, Tensor]:
+    """Capacity-sized coalesced gradients of every table in two flat buffers
+    -- rows int64 and value bytes, laid out by ``ops.coalesced_layout`` (cut
+    per table with ``ops.split_coalesced``) -- and their device row counts
+    (int64 ``[T]``).  The sort works on copies of the keys and payloads, so the
+    op leaves its inputs as they are."""
 
     plan = _plan(weights, table, pooling, exclude, padding_idx)
     keys = keys.clone()
@@ -269,8 +273,8 @@ def grouped_lookup_backward(
         outputs=list(grads), feats=feats, keys=keys, payload=payload,
         bag_count=bag_count if bag_count.numel() else None, error_count=torch.empty(0), count=sum(n_ids),
     )
-    rows, values, counts = ops.backward_coalesce_padded(res, grads)
-    return rows, values, counts
+    rows_all, vbuf, counts, _ = ops.backward_coalesce_padded(res, grads)
+    return rows_all, vbuf, counts
 
 
 def _per_id_grads_cpu(w: Tensor, x: Tensor, ln: Optional[Tensor], g: Tensor, pooling: int, exclude: int,
@@ -315,30 +319,35 @@ def _coalesce_padded_cpu(rows: Tensor, vals: Tensor, cap: int, dtype: torch.dtyp
 def _grouped_backward_cpu(weights, ids, lengths, table, pooling, exclude, padding_idx, grads, keys, payload,
                           bag_count, offsets):
     cap = _capacities(weights, ids, table)
+    layout = ops.coalesced_layout(weights, cap)
+    rows_all = torch.empty(max(int(layout["rows_off"][-1]), 1), dtype=torch.int64)
+    vbuf = torch.zeros(max(int(layout["val_off"][-1]), 1), dtype=torch.uint8)
+    rows, values = ops.split_coalesced(weights, rows_all, vbuf, layout)
     parts = [([], []) for _ in weights]
     for f, x in enumerate(ids):
         t = table[f]
         r, v = _per_id_grads_cpu(weights[t], x, lengths[f], grads[f], pooling[f], exclude[f], padding_idx[f])
         parts[t][0].append(r)
         parts[t][1].append(v)
-    rows, values, counts = [], [], []
+    counts = []
     for t, w in enumerate(weights):
         r = torch.cat(parts[t][0]) if parts[t][0] else torch.empty(0, dtype=torch.int64)
         v = torch.cat(parts[t][1]) if parts[t][1] else torch.empty((0, int(w.size(1))))
         orow, oval, u = _coalesce_padded_cpu(r, v, cap[t], w.dtype, int(w.size(1)))
-        rows.append(orow)
-        values.append(oval)
+        rows[t].copy_(orow)
+        values[t].copy_(oval)
         counts.append(u)
-    return rows, values, torch.tensor(counts, dtype=torch.int64)
+    return rows_all, vbuf, torch.tensor(counts, dtype=torch.int64)
 
 
 @grouped_lookup_backward.register_fake
 def _grouped_backward_fake(weights, ids, lengths, table, pooling, exclude, padding_idx, grads, keys, payload,
                            bag_count, offsets):
-    cap = _capacities(weights, ids, table)
-    rows = [w.new_empty(c, dtype=torch.int64) for w, c in zip(weights, cap)]
-    values = [w.new_empty((c, w.size(1))) for w, c in zip(weights, cap)]
-    return rows, values, weights[0].new_empty(len(weights), dtype=torch.int64)
+    layout = ops.coalesced_layout(weights, _capacities(weights, ids, table))
+    w0 = weights[0]
+    return (w0.new_empty(max(int(layout["rows_off"][-1]), 1), dtype=torch.int64),
+            w0.new_empty(max(int(layout["val_off"][-1]), 1), dtype=torch.uint8),
+            w0.new_empty(len(weights), dtype=torch.int64))
 
 
 def _lookup_setup(ctx, inputs, output):
@@ -364,9 +373,12 @@ def _lookup_backward(ctx, grad_outputs, *_unused):
             rows_f = int(ctx.lengths[f].numel()) if pooling[f] != 0 else int(ids[f].numel())
             g = torch.zeros((rows_f, int(w.size(1))), dtype=w.dtype, device=w.device)
         grads.append(g.contiguous())
-    rows, values, counts = torch.ops.mdl_hip.grouped_lookup_backward(
+    rows_all, vbuf, counts = torch.ops.mdl_hip.grouped_lookup_backward(
         weights, ids, ctx.lengths, table, pooling, exclude, padding_idx, grads, keys, payload, bag_count, offsets,
     )
+    rows, values = ops.split_coalesced(weights, rows_all, vbuf,
+                                       ops.coalesced_layout(weights, _capacities(weights, ids, table)))
+    _drop_dead_records()
     wgrads = []
     for t, w in enumerate(weights):
         g = torch.sparse_coo_tensor(rows[t].unsqueeze(0), values[t], tuple(w.shape), is_coalesced=False)
@@ -454,7 +466,9 @@ def sequence_lookup_backward(weight: Tensor, ids: Tensor, lengths: Tensor, out_l
         plan=plan, device=weight.device, ids=ids, offsets=None, outputs=[grad], feats=feats, keys=keys,
         payload=payload, bag_count=None, error_count=torch.empty(0),
     )
-    rows, values, counts = ops.backward_coalesce_padded(res, [grad.reshape(-1, int(weight.size(1)))])
+    rows_all, vbuf, counts, layout = ops.backward_coalesce_padded(res, [grad.reshape(-1, int(weight.size(1)))])
+    rows, values = ops.split_coalesced([weight], rows_all, vbuf, layout)
+    # views of two different buffers that are not returned: no output aliases another
     return rows[0], values[0], counts
 
 
@@ -524,6 +538,30 @@ def _sparse_coalesce_fake(indices, values, num_rows):
     return indices.new_empty(u), values.new_empty((u, values.size(1)))
 
 
+@torch.library.custom_op("mdl_hip::sparse_coalesce_padded", mutates_args=(), device_types=_CUDA)
+def sparse_coalesce_padded(indices: Tensor, values: Tensor, num_rows: int) -> tuple[Tensor, Tensor, Tensor]:
+    """Capacity-sized coalesce (no host read): ``(rows [n], values [n, dim],
+    count)``, the first ``count`` rows ascending and unique, the rest
+    repeating the last row with zero values."""
+
+    return ops.coalesce_rows_padded(indices, values, num_rows)
+
+
+@sparse_coalesce_padded.register_kernel("cpu")
+def _sparse_coalesce_padded_cpu(indices, values, num_rows):
+    keep = (indices >= 0) & (indices < num_rows)
+    dim = int(values.size(1))
+    r, v, u = _coalesce_padded_cpu(indices[keep], values.float()[keep], int(indices.numel()), values.dtype, dim)
+    return r, v, torch.tensor([u], dtype=torch.int64)
+
+
+@sparse_coalesce_padded.register_fake
+def _sparse_coalesce_padded_fake(indices, values, num_rows):
+    n = int(indices.numel())
+    return indices.new_empty(n, dtype=torch.int64), values.new_empty((n, values.size(1))), \
+        indices.new_empty(1, dtype=torch.int64)
+
+
 # --------------------------------------------------------------- update --
 
 
@@ -589,11 +627,14 @@ _CAPACITY_GRADS: dict[int, tuple] = {}
 
 
 def _note_capacity_grad(parameter: Tensor, rows: Tensor, values: Tensor, count: Tensor) -> None:
-    import weakref
+    _CAPACITY_GRADS[id(parameter)] = (weakref.ref(parameter), rows, values, count)
+
+
+def _drop_dead_records() -> None:
+    """Forget records of parameters that no longer exist (once per backward)."""
 
     for key in [k for k, rec in _CAPACITY_GRADS.items() if rec[0]() is None]:
         del _CAPACITY_GRADS[key]
-    _CAPACITY_GRADS[id(parameter)] = (weakref.ref(parameter), rows, values, count)
 
 
 def capacity_grad(parameter: Tensor, grad: Tensor) -> Optional[tuple[Tensor, Tensor, Tensor]]:

@@ -489,10 +489,12 @@ def forward_packed(
     if with_bag_count is None:
         with_bag_count = with_backward
     if with_backward:
-        keys = torch.empty(max(n, 1), dtype=torch.int32, device=device)
-        payload = torch.empty(max(n, 1), dtype=torch.int32, device=device)
+        alloc = torch.empty if n else torch.zeros
+        keys = alloc(max(n, 1), dtype=torch.int32, device=device)
+        payload = alloc(max(n, 1), dtype=torch.int32, device=device)
     if with_bag_count and pooled_any:
-        bag_count = torch.empty(max(total_rows_out, 1), dtype=torch.float32, device=device)
+        # zeros: the rows of unpooled features have no bag and are not written
+        bag_count = torch.zeros(max(total_rows_out, 1), dtype=torch.float32, device=device)
     check(
         lib().mdl_forward(
             feats_dev.data_ptr(), len(feats), chunks_dev.data_ptr(), n_chunks, ids_arg.data_ptr(), n,
@@ -533,7 +535,6 @@ def grouped_forward(
     id_counts = []
     bag_counts = []
     pooled_any = any(s.pooling != MDL_POOL_NONE for s in specs)
-    length_parts = []
     for f, spec in enumerate(specs):
         t = ids[f]
         if t.dtype != torch.long:
@@ -545,11 +546,21 @@ def grouped_forward(
             if ln is None or ln.ndim != 1:
                 raise ValueError("categorical bag lengths must have shape [B]")
             bag_counts.append(int(ln.numel()))
-            length_parts.append(ln.to(device=device, dtype=torch.int64))
         else:
             bag_counts.append(0)
-            if pooled_any:
-                length_parts.append(torch.full((1,), int(t.numel()), dtype=torch.int64, device=device))
+    length_parts = []
+    if pooled_any:
+        # the unpooled features' pseudo-lengths (their id counts) in one upload
+        pseudo = [c for c, s in zip(id_counts, specs) if s.pooling == MDL_POOL_NONE]
+        pseudo_dev = upload(np.asarray(pseudo, dtype=np.int64), device).view(torch.int64) if pseudo else None
+        k = 0
+        for f, spec in enumerate(specs):
+            if spec.pooling != MDL_POOL_NONE:
+                ln = lengths[f]
+                length_parts.append(ln if ln.dtype == torch.int64 else ln.to(torch.int64))
+            else:
+                length_parts.append(pseudo_dev[k: k + 1])
+                k += 1
     flat = [t.reshape(-1) for t in ids]
     all_ids = (flat[0] if len(flat) == 1 else torch.cat(flat)).contiguous()
     offsets = None
@@ -913,16 +924,46 @@ def table_capacities(res: ForwardResult) -> np.ndarray:
     return cap
 
 
+def coalesced_layout(weights: Sequence[Tensor], cap: Sequence[int]) -> dict:
+    """Where capacity-sized coalesced gradients live in two flat buffers:
+    rows of table t at ``rows_off[t]`` (int64 elements), values at byte
+    ``val_off[t]`` (each table's region 256-byte aligned)."""
+
+    cap = np.asarray(cap, dtype=np.int64)
+    T = len(weights)
+    esz = np.array([w.element_size() for w in weights], dtype=np.int64)
+    dims = np.array([int(w.size(1)) for w in weights], dtype=np.int64)
+    nbytes = cap * dims * esz
+    val_off = np.zeros(T + 1, dtype=np.int64)
+    np.cumsum((nbytes + 255) // 256 * 256, out=val_off[1:])
+    rows_off = np.zeros(T + 1, dtype=np.int64)
+    np.cumsum(cap, out=rows_off[1:])
+    return {"cap": cap, "dims": dims, "nbytes": nbytes, "val_off": val_off, "rows_off": rows_off}
+
+
+def split_coalesced(weights: Sequence[Tensor], rows_all: Tensor, vbuf: Tensor, layout: dict
+                    ) -> tuple[list[Tensor], list[Tensor]]:
+    """Per-table ``rows [cap_t]`` and ``values [cap_t, dim]`` views."""
+
+    cap, dims, nbytes, val_off = layout["cap"], layout["dims"], layout["nbytes"], layout["val_off"]
+    rows = list(rows_all[: int(layout["rows_off"][-1])].split(cap.tolist()))
+    values = [vbuf[int(val_off[t]): int(val_off[t]) + int(nbytes[t])].view(w.dtype).view(int(cap[t]), int(dims[t]))
+              for t, w in enumerate(weights)]
+    return rows, values
+
+
 def backward_coalesce_padded(
     res: ForwardResult, grads: Sequence[Tensor | None]
-) -> tuple[list[Tensor], list[Tensor], Tensor]:
+) -> tuple[Tensor, Tensor, Tensor, dict]:
     """Coalesced sparse gradient of every table without a host read.
 
-    Table t gets ``rows`` int64 ``[cap_t]`` and ``values`` ``[cap_t, dim]``
-    (its dtype), ``cap_t`` its id count: the first ``counts[t]`` entries are
+    Table t gets ``cap_t`` entries (its id count): the first ``counts[t]`` are
     the coalesced gradient (rows ascending, unique), the rest repeat the last
-    row with zero values, so the pair is a valid uncoalesced COO gradient with
-    the same sum.  ``counts`` is a device int64 ``[T]``.  Only launches.
+    row with zero values, so each table's pair is a valid uncoalesced COO
+    gradient with the same sum.  Returns ``(rows_all, values_bytes, counts,
+    layout)``: two flat buffers (see :func:`coalesced_layout`,
+    :func:`split_coalesced`) and ``counts``, a device int64 ``[T]``.  Only
+    launches.
     """
 
     plan = res.plan
@@ -935,15 +976,10 @@ def backward_coalesce_padded(
     T = len(tables)
     stream = _stream(device)
     cap = table_capacities(res)
-    esz = np.array([t.weight.element_size() for t in plan.tables], dtype=np.int64)
-    dims = np.array([int(t.weight.size(1)) for t in plan.tables], dtype=np.int64)
-    nbytes = cap * dims * esz
-    offs = np.zeros(T + 1, dtype=np.int64)
-    np.cumsum((nbytes + 255) // 256 * 256, out=offs[1:])
-    rows_off = np.zeros(T + 1, dtype=np.int64)
-    np.cumsum(cap, out=rows_off[1:])
+    layout = coalesced_layout([t.weight for t in plan.tables], cap)
+    rows_off, val_off = layout["rows_off"], layout["val_off"]
     rows_all = torch.empty(max(int(rows_off[-1]), 1), dtype=torch.int64, device=device)
-    vbuf = torch.empty(max(int(offs[-1]), 1), dtype=torch.uint8, device=device)
+    vbuf = torch.empty(max(int(val_off[-1]), 1), dtype=torch.uint8, device=device)
     urange = torch.zeros(2 * T, dtype=torch.int64, device=device)
     if n:
         pad_units = (cap + 63) // 64
@@ -952,7 +988,7 @@ def backward_coalesce_padded(
         # one upload: row and value addresses, capacities, pad-unit prefix
         host = np.concatenate([
             np.where(cap > 0, rows_all.data_ptr() + 8 * rows_off[:T], 0).astype(np.uint64).view(np.int64),
-            np.where(cap > 0, vbuf.data_ptr() + offs[:T], 0).astype(np.uint64).view(np.int64),
+            np.where(cap > 0, vbuf.data_ptr() + val_off[:T], 0).astype(np.uint64).view(np.int64),
             cap, unit_first,
         ])
         meta = upload(host, device)
@@ -983,16 +1019,11 @@ def backward_coalesce_padded(
             "mdl_backward_pad",
         )
         keep.append(meta)
-    rows_list = list(rows_all[: int(rows_off[-1])].split(cap.tolist()))
-    vals_list = []
-    for t, table in enumerate(plan.tables):
-        w = table.weight
-        vals_list.append(vbuf[int(offs[t]): int(offs[t]) + int(nbytes[t])].view(w.dtype).view(int(cap[t]), int(dims[t])))
     counts = urange[1::2] - urange[0::2]
     res.keys = None
     res.payload = None
     del keep
-    return rows_list, vals_list, counts
+    return rows_all, vbuf, counts, layout
 
 
 def grouped_rowwise_adagrad_(
@@ -1015,40 +1046,51 @@ def grouped_rowwise_adagrad_(
     if not weights:
         return
     device = weights[0].device
-    ups = np.zeros(len(weights), dtype=_lib.UPDATE_DTYPE)
     keep = []
-    unit = 0
-    for i, (w, a, r, v, c, lr) in enumerate(zip(weights, accumulators, rows, values, counts, lrs)):
-        _require_device(w, "weight")
+    wptr, sptr, rptr, vptr, cptr, nrows, caps, wstr, vstr, dims, wdt, vdt = ([] for _ in range(12))
+    for w, a, r, v, c in zip(weights, accumulators, rows, values, counts):
+        if w.device.type != "cuda":
+            _require_device(w, "weight")
         if w.ndim != 2 or w.stride(1) != 1:
             raise ValueError("row-wise Adagrad expects 2D weights with contiguous rows")
         if a.dtype != torch.float32 or not a.is_contiguous():
             raise TypeError("row-wise Adagrad accumulator must be a contiguous float32 tensor")
-        r = r.to(torch.int64).contiguous()
-        if w.dtype == torch.float32 and v.dtype != torch.float32:
+        if r.dtype != torch.int64 or not r.is_contiguous():
+            r = r.to(torch.int64).contiguous()
+        if (w.dtype == torch.float32 and v.dtype != torch.float32) or v.dtype not in (torch.float32, torch.bfloat16):
             v = v.float()
-        if v.dtype not in (torch.float32, torch.bfloat16):
-            v = v.float()
-        v = _row_major_aligned(v)
+        if not v.is_contiguous() or v.data_ptr() % 16:
+            v = _row_major_aligned(v)
         keep += [r, v]
-        cap = int(r.numel())
-        u = ups[i]
-        u["weight"] = w.data_ptr()
-        u["state"] = a.data_ptr()
-        u["rows"] = r.data_ptr()
-        u["values"] = v.data_ptr()
-        u["count"] = 0 if c is None else c.data_ptr()
-        u["num_rows"] = int(w.size(0))
-        u["capacity"] = cap
-        u["weight_stride"] = w.stride(0)
-        u["values_stride"] = v.stride(0) if v.ndim == 2 and v.size(0) else int(w.size(1))
-        u["unit_first"] = unit
-        u["dim"] = int(w.size(1))
-        u["wdtype"] = dtype_code(w.dtype)
-        u["vdtype"] = dtype_code(v.dtype)
-        u["lr"] = float(lr)
-        unit += (cap + _lib.MDL_UPDATE_UNIT - 1) // _lib.MDL_UPDATE_UNIT
-    if unit == 0:
+        wptr.append(w.data_ptr())
+        sptr.append(a.data_ptr())
+        rptr.append(r.data_ptr())
+        vptr.append(v.data_ptr())
+        cptr.append(0 if c is None else c.data_ptr())
+        nrows.append(w.size(0))
+        caps.append(r.numel())
+        wstr.append(w.stride(0))
+        vstr.append(v.stride(0) if v.ndim == 2 and v.size(0) else w.size(1))
+        dims.append(w.size(1))
+        wdt.append(dtype_code(w.dtype))
+        vdt.append(dtype_code(v.dtype))
+    ups = np.zeros(len(weights), dtype=_lib.UPDATE_DTYPE)
+    ups["weight"] = wptr
+    ups["state"] = sptr
+    ups["rows"] = rptr
+    ups["values"] = vptr
+    ups["count"] = cptr
+    ups["num_rows"] = nrows
+    ups["capacity"] = caps
+    ups["weight_stride"] = wstr
+    ups["values_stride"] = vstr
+    ups["dim"] = dims
+    ups["wdtype"] = wdt
+    ups["vdtype"] = vdt
+    ups["lr"] = np.asarray(lrs, dtype=np.float32)
+    units = (ups["capacity"] + _lib.MDL_UPDATE_UNIT - 1) // _lib.MDL_UPDATE_UNIT
+    ups["unit_first"][1:] = np.cumsum(units)[:-1]
+    if int(units.sum()) == 0:
         return
     ups_dev = upload(ups, device)
     check(
@@ -1057,6 +1099,53 @@ def grouped_rowwise_adagrad_(
         "mdl_grouped_rowwise_adagrad",
     )
     del keep
+
+
+def coalesce_rows_padded(
+    indices: Tensor, values: Tensor, num_rows: int, *, error_count: Tensor | None = None
+) -> tuple[Tensor, Tensor, Tensor]:
+    """Sort + unique + segment-sum of an uncoalesced COO gradient without a
+    host read: ``(rows [n], summed [n, dim], count)`` where the first
+    ``count`` (device int64 [1]) rows are ascending and unique and the rest
+    repeat the last row with zero values.  Indices outside ``[0, num_rows)``
+    are dropped and counted in ``error_count`` when given."""
+
+    _require_device(values, "values")
+    device = values.device
+    n = int(indices.numel())
+    dim = int(values.size(1))
+    indices = indices.to(torch.int64).contiguous()
+    values = _row_major_aligned(values)
+    plan = GroupPlan()
+    # A stand-in table of the right shape (a stride-0 view of one row): only
+    # its row count, dim and dtype are read, never its rows.
+    stand_in = torch.empty((1, dim), dtype=values.dtype, device=device).expand(int(num_rows), dim)
+    plan.tables.append(TableSpec(weight=stand_in, state=None, row_base=0))
+    plan.total_rows = int(num_rows)
+    plan.features.append(FeatureSpec(table=0, pooling=MDL_POOL_NONE, exclude_null=False, padding_idx=-1,
+                                     out_dtype=values.dtype))
+    keys = torch.empty(max(n, 1), dtype=torch.int32, device=device)
+    payload = torch.empty(max(n, 1), dtype=torch.int32, device=device)
+    err = error_count if error_count is not None else torch.zeros(1, dtype=torch.int32, device=device)
+    if n:
+        check(
+            lib().mdl_sparse_keys(indices.data_ptr(), n, int(num_rows), 0, 0, -1, keys.data_ptr(), payload.data_ptr(),
+                                  plan.sentinel, err.data_ptr(), _stream(device)),
+            "mdl_sparse_keys",
+        )
+    feats = np.zeros(1, dtype=FEATURE_DTYPE)
+    feats[0]["num_rows"] = int(num_rows)
+    feats[0]["num_ids"] = n
+    feats[0]["dim"] = dim
+    feats[0]["wdtype"] = dtype_code(values.dtype)
+    feats[0]["odtype"] = dtype_code(values.dtype)
+    feats[0]["pooling"] = MDL_POOL_NONE
+    feats[0]["padding_idx"] = -1
+    res = ForwardResult(plan=plan, device=device, ids=indices, offsets=None, outputs=[values], feats=feats, keys=keys,
+                        payload=payload, bag_count=None, error_count=err)
+    rows_all, vbuf, counts, layout = backward_coalesce_padded(res, [values])
+    rows, vals = split_coalesced([plan.tables[0].weight], rows_all, vbuf, layout)
+    return rows[0], vals[0], counts
 
 
 def coalesce_rows(

@@ -24,11 +24,12 @@ from . import embeddings, library
 
 
 def update_rows(parameter: Tensor) -> tuple[Tensor, Tensor, Tensor | None]:
-    """``(rows, values, count)`` of the parameter's sparse gradient, rows
-    unique and ascending: a gradient the lookup emitted (``count``: its row
-    count on the device), or the gradient coalesced by ``mdl_hip::sparse_coalesce``
-    (one host read to size it, like ``grad.coalesce()`` in src/optim.py:323-324),
-    stored back as ``parameter.grad`` (``count`` None: all rows)."""
+    """``(rows, values, count)`` of the parameter's sparse gradient for the
+    update, rows unique and ascending in the first ``count`` entries (a device
+    int64; None: all): a gradient the lookup emitted as it is, a coalesced one
+    as it is, any other coalesced locally by ``mdl_hip::sparse_coalesce_padded``
+    (like ``grad = grad.coalesce()`` in src/optim.py:321-324, without the host
+    read that sizes an exact coalesce)."""
 
     grad = parameter.grad
     known = library.capacity_grad(parameter, grad)
@@ -36,20 +37,23 @@ def update_rows(parameter: Tensor) -> tuple[Tensor, Tensor, Tensor | None]:
         return known
     if grad.is_coalesced():
         return grad._indices()[0], grad._values(), None
-    rows, values = torch.ops.mdl_hip.sparse_coalesce(grad._indices()[0], grad._values(), int(parameter.shape[0]))
-    parameter.grad = torch.sparse_coo_tensor(rows.unsqueeze(0), values, tuple(grad.shape), is_coalesced=True)
-    return rows, values, None
+    return torch.ops.mdl_hip.sparse_coalesce_padded(grad._indices()[0], grad._values(), int(parameter.shape[0]))
 
 
 def coalesced_grad(parameter: Tensor) -> Tensor:
-    """The parameter's sparse gradient with every row's summed value once.
+    """The parameter's sparse gradient with every row's summed value once,
+    stored back as ``parameter.grad`` (src/train.py:5730-5742).
 
     A capacity-sized gradient of the lookup is returned as it is: its entries
     past the row count repeat a row with zero values, which changes no norm
-    and no scaling (src/train.py:5730-5826 read only the values).  Any other
-    uncoalesced gradient is coalesced on the device and stored back."""
+    and no scaling (the clip reads only the values).  Any other uncoalesced
+    gradient is coalesced exactly on the device (one host read to size it)."""
 
-    update_rows(parameter)
+    grad = parameter.grad
+    if library.capacity_grad(parameter, grad) is not None or grad.is_coalesced():
+        return grad
+    rows, values = torch.ops.mdl_hip.sparse_coalesce(grad._indices()[0], grad._values(), int(parameter.shape[0]))
+    parameter.grad = torch.sparse_coo_tensor(rows.unsqueeze(0), values, tuple(grad.shape), is_coalesced=True)
     return parameter.grad
 
 

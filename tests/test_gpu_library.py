@@ -66,6 +66,22 @@ def test_opcheck_rocm(device):
     opcheck(OPS.bucketize.default, _to((torch.tensor([0, -1, 7, -(1 << 63)]), None, 8, "pre_hashed", True), device))
     opcheck(OPS.lengths_to_offsets.default, _to((torch.tensor([3, 0, 2]),), device))
     opcheck(OPS.sparse_coalesce.default, _to((torch.tensor([3, 1, 3]), torch.randn(3, 4), 10), device))
+    opcheck(OPS.sparse_coalesce_padded.default, _to((torch.tensor([3, 1, 3]), torch.randn(3, 4), 10), device))
+
+
+def test_sparse_coalesce_padded_matches_oracle(device):
+    announce("sparse_coalesce_padded")
+    rng = np.random.default_rng(63)
+    idx = (rng.zipf(1.1, size=40000) % 6000).astype(np.int64)
+    vals = rng.standard_normal((40000, 24)).astype(np.float32)
+    r, v, c = OPS.sparse_coalesce_padded(torch.from_numpy(idx).to(device), torch.from_numpy(vals).to(device), 6000)
+    er, ev = O.coalesce(idx, vals.astype(np.float64))
+    _, eabs = O.coalesce(idx, np.abs(vals.astype(np.float64)))
+    u = int(c.item())
+    assert u == er.size and r.numel() == idx.size
+    assert np.array_equal(r[:u].cpu().numpy(), er) and bool((r[u:] == er[-1]).all())
+    got = v.cpu().numpy()
+    assert np.all(np.abs(got[:u] - ev) <= 1e-5 * eabs + 1e-6) and not got[u:].any()
 
 
 def _modules(specs, device, seed):
@@ -217,7 +233,8 @@ def test_padded_coalesce_matches_oracle(device):
                               [torch.from_numpy(la).to(device), None, torch.from_numpy(lc).to(device)],
                               with_backward=True)
     grads = [torch.from_numpy(rng.standard_normal((B, d)).astype(np.float32)).to(device) for d in dims]
-    r, v, counts = ops.backward_coalesce_padded(res, grads)
+    rows_all, vbuf, counts, layout = ops.backward_coalesce_padded(res, grads)
+    r, v = ops.split_coalesced(tabs, rows_all, vbuf, layout)
     counts = counts.cpu().numpy()
     for t, (x, ln, mode) in enumerate(((xa, la, "mean"), (xb, None, "none"), (xc, lc, "sum"))):
         ri, vi = O.per_id_grads(x, ln, grads[t].double().cpu().numpy(), mode, "exclude")

@@ -41,7 +41,8 @@ def _lookup_args(requires_grad=True):
 
 
 @pytest.mark.parametrize("name", ["grouped_lookup", "sequence_lookup", "rowwise_adagrad_", "grouped_rowwise_adagrad_",
-                                  "bucketize", "lengths_to_offsets", "sparse_coalesce", "grouped_lookup_backward",
+                                  "bucketize", "lengths_to_offsets", "sparse_coalesce", "sparse_coalesce_padded",
+                                  "grouped_lookup_backward",
                                   "sequence_lookup_backward"])
 def test_opcheck_cpu(name):
     if name == "grouped_lookup":
