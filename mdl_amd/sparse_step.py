@@ -27,7 +27,7 @@ import torch
 from torch import Tensor
 
 from . import ops
-from ._lib import CHUNK_DTYPE, MDL_FLAG_IDS_FROM_OFFSETS, MDL_POOL_NONE, check, lib
+from ._lib import CHUNK_DTYPE, FEATURE_DTYPE, MDL_FLAG_IDS_FROM_OFFSETS, MDL_POOL_NONE, check, lib
 
 # Descriptor bound of a feature whose ids the offsets place: the call's id
 # count clamps the range anyway.
@@ -64,6 +64,14 @@ class SparseStep:
     of an unpooled feature, one per output row).  ``capacity`` bounds the ids
     of any batch bound later (default: this batch's).  Outputs and gradients
     are 2-D row views (e.g. column slices of one ``[B, sum(dim)]`` buffer).
+
+    Gradient accumulation (src/train.py:7007-7067, :5388-5396): with
+    ``micro_batches=k``, ``outputs`` and ``grads`` are k lists of views, one
+    per micro-batch; ``forward(micro_batch=m)`` looks up micro-batch m (bound
+    with :meth:`bind` before it) into its outputs and its own region of the
+    sort keys, and one ``sort()`` + ``apply()`` then reduces the gradients of
+    all k micro-batches together -- the sum of their sparse gradients, each
+    row updated once -- instead of coalescing an accumulated COO gradient.
     """
 
     def __init__(
@@ -78,10 +86,18 @@ class SparseStep:
         *,
         error_count: Tensor | None = None,
         capacity: int | None = None,
+        micro_batches: int = 1,
     ) -> None:
         for t in plan.tables:
             if t.state is None:
                 raise RuntimeError("every table needs a row-wise Adagrad accumulator")
+        self.k = int(micro_batches)
+        if self.k < 1:
+            raise ValueError("micro_batches must be positive")
+        if self.k == 1:
+            outputs, grads = [outputs], [grads]
+        elif len(outputs) != self.k or len(grads) != self.k:
+            raise ValueError("one list of outputs and one of gradients per micro-batch")
         self.plan = plan
         self.device = packed_ids.device
         self.ids = _as_ids(packed_ids)
@@ -100,8 +116,8 @@ class SparseStep:
         self.error_count = (
             error_count if error_count is not None else torch.zeros(1, dtype=torch.int32, device=self.device)
         )
-        out_ptrs = [o.data_ptr() for o in outputs]
-        out_strides = [o.stride(0) if o.ndim == 2 else int(o.size(-1)) for o in outputs]
+        out_ptrs = [o.data_ptr() for o in outputs[0]]
+        out_strides = [o.stride(0) if o.ndim == 2 else int(o.size(-1)) for o in outputs[0]]
         feats = ops.build_features(plan, id_counts, bag_counts, out_ptrs, out_strides)
         target = ops.forward_target_ids(feats)
         n_chunks = lib().mdl_plan_chunks(feats.ctypes.data, len(feats), target, None, 0)
@@ -115,30 +131,56 @@ class SparseStep:
             feats["flags"] |= MDL_FLAG_IDS_FROM_OFFSETS
             feats["ids_begin"] = 0
             feats["num_ids"] = _NO_BOUND
-        self.feats_fwd = feats
-        res = ops.ForwardResult(
-            plan=plan, device=self.device, ids=self.ids, offsets=None, outputs=list(outputs),
-            feats=self.feats_fwd, keys=None, payload=None, bag_count=None, error_count=self.error_count,
-        )
-        self.feats_bwd, self._grads = ops._attach_grads(res, grads)
-        self.tables = ops._tables_array(plan, self.feats_bwd)
-        self.fwd_classes = ops.feature_classes(self.feats_fwd)
-        self.bwd_classes = ops.table_classes(self.tables)
-        self.feats_fwd_dev = ops.upload(self.feats_fwd, self.device)
-        self.chunks_dev = ops.upload(chunks, self.device)
-        self.feats_bwd_dev = ops.upload(self.feats_bwd, self.device)
-        self.tables_dev = ops.upload(self.tables, self.device)
         total_rows = int(
             np.where(feats["pooling"] != MDL_POOL_NONE, feats["num_bags"], np.asarray(id_counts)).sum()
         )
+        self.rows_per_batch = max(total_rows, 1)
+        if self.rows_per_batch * self.k >= 1 << 32:
+            raise ValueError("the micro-batches' output rows exceed the 32-bit gradient-row payload")
+        # Micro-batch m: its forward descriptors (its outputs, payloads and
+        # bag counts shifted by m rows-per-batch) and its backward ones (its
+        # gradients), all features of micro-batch 0 first.
+        fwd, bwd = [], []
+        self._grads = []
+        for m in range(self.k):
+            if [o.stride(0) if o.ndim == 2 else int(o.size(-1)) for o in outputs[m]] != out_strides:
+                raise ValueError("every micro-batch's outputs need the row strides of the first's")
+            fm = feats.copy()
+            fm["out"] = [o.data_ptr() for o in outputs[m]]
+            fm["payload_base"] += m * self.rows_per_batch
+            fwd.append(fm)
+            res = ops.ForwardResult(
+                plan=plan, device=self.device, ids=self.ids, offsets=None, outputs=list(outputs[m]),
+                feats=fm, keys=None, payload=None, bag_count=None, error_count=self.error_count,
+            )
+            fb, keep = ops._attach_grads(res, grads[m])
+            bwd.append(fb)
+            self._grads += keep
+        self.feats_fwd = fwd[0]
+        self.feats_bwd = np.concatenate(bwd)
+        self.tables = ops._tables_array(plan, self.feats_bwd[: len(plan.features)])
+        if self.k > 1:
+            # a table read by k copies of its feature: the reduce finds each
+            # payload's feature by search instead of the one-feature path
+            self.tables["feature"] = -1
+        self.fwd_classes = ops.feature_classes(self.feats_fwd)
+        self.bwd_classes = ops.table_classes(self.tables)
+        self.feats_fwd_dev = ops.upload(np.concatenate(fwd), self.device)
+        self.chunks_dev = ops.upload(chunks, self.device)
+        self.feats_bwd_dev = ops.upload(self.feats_bwd, self.device)
+        self.tables_dev = ops.upload(self.tables, self.device)
         cap = max(self.capacity, 1)
-        self.keys = torch.empty(cap, dtype=torch.int32, device=self.device)
-        self.payload = torch.empty(cap, dtype=torch.int32, device=self.device)
+        self.keys = torch.empty(cap * self.k, dtype=torch.int32, device=self.device)
+        self.payload = torch.empty(cap * self.k, dtype=torch.int32, device=self.device)
         self.bag_count = (
-            torch.empty(max(total_rows, 1), dtype=torch.float32, device=self.device) if pooled_any else None
+            torch.empty(self.rows_per_batch * self.k, dtype=torch.float32, device=self.device) if pooled_any else None
         )
+        if self.k > 1:
+            self._positions = torch.arange(cap, dtype=torch.int64, device=self.device)
+            sentinel = int(plan.sentinel)
+            self._sentinel = sentinel - (1 << 32) if sentinel >= (1 << 31) else sentinel
         self.ws = ops._workspace(
-            lib().mdl_backward_workspace_bytes(self.capacity, len(self.tables), plan.max_dim), self.device
+            lib().mdl_backward_workspace_bytes(self._n(), len(self.tables), plan.max_dim), self.device
         )
         self.sumsq = torch.zeros(1, dtype=torch.float32, device=self.device)
         self.norm = torch.zeros(1, dtype=torch.float32, device=self.device)
@@ -181,13 +223,19 @@ class SparseStep:
         return None if self.offsets is None else self.offsets.data_ptr() + 8 * (self.offsets.numel() - 1)
 
     def _n(self) -> int:
+        if self.k > 1:
+            return max(self.capacity, 1) * self.k
         return self.capacity if self.dynamic else int(self.ids.numel())
 
     # ------------------------------------------------------------- steps --
 
-    def forward(self) -> None:
-        """Offsets scan + grouped lookup/pooling (+ backward sort keys)."""
+    def forward(self, micro_batch: int = 0) -> None:
+        """Offsets scan + grouped lookup/pooling (+ backward sort keys) of the
+        bound batch, as micro-batch ``micro_batch`` of an accumulated step."""
 
+        m = int(micro_batch)
+        if not 0 <= m < self.k:
+            raise ValueError(f"micro_batch must be in [0, {self.k})")
         s = self._stream()
         if self.offsets is not None:
             check(
@@ -198,15 +246,22 @@ class SparseStep:
                 "mdl_lengths_to_offsets",
             )
         ids = self.ids if self.ids.numel() else self.keys  # any valid address; nothing is read
+        F = len(self.feats_fwd)
+        region = m * max(self.capacity, 1)
         check(
             lib().mdl_forward(
-                self.feats_fwd_dev.data_ptr(), len(self.feats_fwd), self.chunks_dev.data_ptr(), self.n_chunks,
-                ids.data_ptr(), int(self.ids.numel()), ops._ptr(self.offsets), self.keys.data_ptr(),
-                self.payload.data_ptr(), self.plan.sentinel, ops._ptr(self.bag_count), self.error_count.data_ptr(),
-                self.fwd_classes, s,
+                self.feats_fwd_dev.data_ptr() + m * F * FEATURE_DTYPE.itemsize, F, self.chunks_dev.data_ptr(), self.n_chunks,
+                ids.data_ptr(), int(self.ids.numel()), ops._ptr(self.offsets), self.keys.data_ptr() + 4 * region,
+                self.payload.data_ptr() + 4 * region, self.plan.sentinel, ops._ptr(self.bag_count),
+                self.error_count.data_ptr(), self.fwd_classes, s,
             ),
             "mdl_forward",
         )
+        if self.k > 1:
+            # entries of the region past this micro-batch's ids sort last and
+            # reduce nowhere
+            live = self.offsets[-1] if self.offsets is not None else int(self.ids.numel())
+            self.keys[region: region + max(self.capacity, 1)].masked_fill_(self._positions >= live, self._sentinel)
 
     def sort(self) -> None:
         """Radix sort of the (row, gradient-row) pairs + chunk plan."""
@@ -214,8 +269,8 @@ class SparseStep:
         check(
             lib().mdl_backward_sort(
                 self.tables_dev.data_ptr(), len(self.tables), self.plan.max_dim, self.keys.data_ptr(),
-                self.payload.data_ptr(), self._n(), self._count_ptr(), self.plan.key_bits, self.ws.data_ptr(),
-                self.ws.numel(), self._stream(),
+                self.payload.data_ptr(), self._n(), self._count_ptr() if self.k == 1 else None, self.plan.key_bits,
+                self.ws.data_ptr(), self.ws.numel(), self._stream(),
             ),
             "mdl_backward_sort",
         )

@@ -718,6 +718,90 @@ def test_sparse_step_serves_batches_of_any_bag_lengths(device):
         st.bind(torch.zeros(cap + 1, dtype=torch.int64, device=device), batches[0][3])
 
 
+def test_sparse_step_accumulates_micro_batches(device):
+    """SparseStep(micro_batches=3): three micro-batches with different bag
+    lengths are looked up on the same tables into their own outputs, then one
+    sort + one reduce updates every row once.  Outputs match the oracle's
+    lookups; tables and accumulators match one row-wise Adagrad step on the
+    coalesced sum of the three micro-batches' sparse gradients, and the clip
+    norm is that sum's global norm (gradient accumulation,
+    src/train.py:7007-7067)."""
+
+    from mdl_amd.sparse_step import SparseStep
+
+    rng = np.random.default_rng(85)
+    B, k, lr, eps = 256, 3, 0.03, 1e-8
+    rows = [2500, 700, 9000, 300]
+    dims = [32, 16, 64, 24]
+    pools = ["mean", "none", "sum", "mean"]
+    W = [rng.standard_normal((r, d)).astype(np.float32) for r, d in zip(rows, dims)]
+    for w in W:
+        w[0] = 0
+    tabs = [torch.from_numpy(w.copy()).to(device) for w in W]
+    accs = [torch.from_numpy(rng.random(r).astype(np.float32)).to(device) for r in rows]
+    acc0 = [a.cpu().numpy() for a in accs]
+    plan = ops.GroupPlan()
+    for t, p in enumerate(pools):
+        plan.add_feature(tabs[t], pooling=p, null_policy="exclude", state=accs[t])
+    S = sum(dims)
+    cols = np.concatenate([[0], np.cumsum(dims)[:-1]])
+    views = [slice(int(c), int(c) + d) for c, d in zip(cols, dims)]
+    outs = [torch.empty((B, S), device=device) for _ in range(k)]
+    grads = [torch.empty((B, S), device=device) for _ in range(k)]
+
+    def batch(max_len):
+        ids, lens = [], []
+        for t, p in enumerate(pools):
+            if p == "none":
+                ids.append((rng.zipf(1.2, size=B) % rows[t]).astype(np.int64))
+                lens.append(None)
+            else:
+                ln = rng.integers(0, max_len + 1, size=B)
+                ids.append((rng.zipf(1.2, size=int(ln.sum())) % rows[t]).astype(np.int64))
+                lens.append(ln)
+        parts = [ln if ln is not None else np.array([x.size]) for x, ln in zip(ids, lens)]
+        return ids, lens, torch.from_numpy(np.concatenate(ids)).to(device), \
+            torch.from_numpy(np.concatenate(parts).astype(np.int64)).to(device)
+
+    batches = [batch(m) for m in (12, 3, 30)]
+    cap = max(int(b[2].numel()) for b in batches)
+    ids0, lens0, p0, l0 = batches[0]
+    st = SparseStep(plan, p0, l0, [x.size for x in ids0], [0 if ln is None else B for ln in lens0],
+                    [[o[:, v] for v in views] for o in outs], [[g[:, v] for v in views] for g in grads],
+                    capacity=cap, micro_batches=k)
+    g_host = []
+    for m, (ids, lens, packed, lengths) in enumerate(batches):
+        announce("sparse_step_micro_batch", m, int(packed.numel()))
+        g = rng.standard_normal((B, S)).astype(np.float32)
+        g_host.append(g)
+        grads[m].copy_(torch.from_numpy(g))
+        st.bind(packed, lengths)
+        st.forward(micro_batch=m)
+    st.sort()
+    norm, _ = st.clip(1e9)
+    st.apply(lr, eps)
+    torch.cuda.synchronize()
+    assert int(st.error_count.item()) == 0
+    sumsq = 0.0
+    for m, (ids, lens, _, _) in enumerate(batches):
+        got = outs[m].cpu().numpy()
+        for t, p in enumerate(pools):
+            ref = O.gather(W[t], ids[t]) if p == "none" else O.pool(W[t], ids[t], lens[t], p, "exclude")[0]
+            assert_close(got[:, views[t]], ref, 1e-5, 1e-6, O.pool(np.abs(W[t]), ids[t], lens[t], "sum",
+                                                                   "exclude")[0] if p != "none" else None)
+    for t, p in enumerate(pools):
+        parts = [O.per_id_grads(b[0][t], b[1][t], g_host[m][:, views[t]].astype(np.float64), p, "exclude")
+                 for m, b in enumerate(batches)]
+        r, v = O.coalesce(np.concatenate([x[0] for x in parts]), np.concatenate([x[1] for x in parts]))
+        sumsq += float((v * v).sum())
+        w_ref, a_ref = O.rowwise_adagrad(W[t], acc0[t], r, v, lr, eps)
+        assert_close(accs[t].cpu().numpy(), a_ref, 1e-5, 1e-6)
+        assert_close(tabs[t].cpu().numpy(), w_ref, 1e-5, 1e-5)
+    assert_close(norm.cpu().numpy(), np.array([np.sqrt(sumsq)]), 1e-5, 0)
+    with pytest.raises(ValueError):
+        st.forward(micro_batch=k)
+
+
 def test_sparse_step_slot_buffer_matches_oracle(device):
     """SparseStep: pooled + unpooled features written into one [B, sum(dim)]
     slot buffer, gradients read from the same layout, fused update."""
