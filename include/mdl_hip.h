@@ -219,11 +219,20 @@ int64_t mdl_plan_chunks(const mdl_feature* feats_host, int32_t num_features,
  * feature's id range is clamped into [0, num_ids), so a descriptor or bag
  * lengths that point past the array read nothing outside it (the clamp is
  * counted as an error).
+ *
+ * key_origin (device, may be NULL): position o = *key_origin (clamped into
+ * [0, num_ids]) becomes entry 0 of sort_keys/sort_payload, i.e. position i is
+ * written to entry i - o, and every feature's id range is clamped into
+ * [o, num_ids).  A plan cut into key groups (rows of 2^32 - 1 or more) looks
+ * up one group per call, with that group's first offset as the origin, so each
+ * group's keys start at entry 0 of its own arrays even when the device alone
+ * knows where its ids begin.  NULL: o = 0.
  */
 int mdl_forward(const mdl_feature* feats, int32_t num_features,
                 const mdl_chunk* chunks, int64_t num_chunks,
                 const int64_t* ids, int64_t num_ids, const int64_t* offsets,
-                uint32_t* sort_keys, uint32_t* sort_payload, uint32_t sentinel,
+                uint32_t* sort_keys, uint32_t* sort_payload,
+                const int64_t* key_origin, uint32_t sentinel,
                 float* bag_count, int32_t* error_count, uint32_t classes,
                 void* stream);
 

@@ -26,7 +26,7 @@ MDL_FLAG_EXCLUDE_NULL = 1
 MDL_FLAG_ROWS_BY_POSITION = 2
 MDL_FLAG_IDS_FROM_OFFSETS = 4
 MDL_CLASSES_UNSUPPORTED = 0x80000000
-ABI_VERSION = 4
+ABI_VERSION = 5
 MDL_BUCKET_PRE_HASHED = 0
 MDL_BUCKET_MOD = 1
 MDL_SEQ_OLDEST_TO_NEWEST = 0
@@ -111,7 +111,7 @@ SIGNATURES: dict[str, tuple] = {
     "mdl_offsets_workspace_bytes": (_SZ, [_I64]),
     "mdl_lengths_to_offsets": (_I32, [_P, _I64, _P, _P, _SZ, _P]),
     "mdl_plan_chunks": (_I64, [_P, _I32, _I32, _P, _I64]),
-    "mdl_forward": (_I32, [_P, _I32, _P, _I64, _P, _I64, _P, _P, _P, _U32, _P, _P, _U32, _P]),
+    "mdl_forward": (_I32, [_P, _I32, _P, _I64, _P, _I64, _P, _P, _P, _P, _U32, _P, _P, _U32, _P]),
     "mdl_pool_backward": (_I32, [_P, _I32, _P, _I64, _P, _I64, _P, _P, _U32, _P]),
     "mdl_feature_classes": (_U32, [_P, _I32]),
     "mdl_table_classes": (_U32, [_P, _I32]),

@@ -31,6 +31,8 @@ struct FwdArgs {
   const int64_t* offsets;
   uint32_t* keys;
   uint32_t* payload;
+  const int64_t* key_origin;  // device position that is entry 0 of keys/payload (NULL: 0)
+  int64_t key_lo;             // ids before it belong to another call (set per wave)
   float* bag_count;
   int32_t* error_count;
   uint32_t sentinel;
@@ -90,7 +92,7 @@ __device__ __forceinline__ void bind_range(Feat& f, const FwdArgs& a) {
     lo = olo;
     hi = ohi;
   }
-  lo = lo < 0 ? 0 : (lo > a.num_ids ? a.num_ids : lo);
+  lo = lo < a.key_lo ? a.key_lo : (lo > a.num_ids ? a.num_ids : lo);
   hi = hi < lo ? lo : (hi > a.num_ids ? a.num_ids : hi);
   f.ids_begin = lo;
   f.num_ids = hi - lo;
@@ -674,6 +676,17 @@ __global__ MDL_OCCUPANCY __launch_bounds__(kFwdWaves * kWave) void forward_kerne
   Feat f = load_feat(a.feats + ch.feature);
   const int v = feat_variant(f);
   if (v / kWidths != ClassOf<TW, TO, kVec>::value) return;  // another class's launch owns it
+  if (a.key_origin != nullptr) {
+    // This call's ids start at the origin: positions before it are clamped
+    // away, and position i lands in entry i - origin.
+    int64_t o = uni64(*a.key_origin);
+    o = o < 0 ? 0 : (o > a.num_ids ? a.num_ids : o);
+    a.key_lo = o;
+    if (a.keys != nullptr) {
+      a.keys -= o;
+      a.payload -= o;
+    }
+  }
   bind_range(f, a);
   if (f.pooling == MDL_POOL_NONE) {
     // The chunk may reach past a range that is shorter this call.
@@ -1054,8 +1067,8 @@ int64_t mdl_plan_chunks(const mdl_feature* feats, int32_t num_features, int32_t 
 
 int mdl_forward(const mdl_feature* feats, int32_t num_features, const mdl_chunk* chunks,
                 int64_t num_chunks, const int64_t* ids, int64_t num_ids, const int64_t* offsets,
-                uint32_t* sort_keys, uint32_t* sort_payload, uint32_t sentinel, float* bag_count,
-                int32_t* error_count, uint32_t classes, void* stream) {
+                uint32_t* sort_keys, uint32_t* sort_payload, const int64_t* key_origin, uint32_t sentinel,
+                float* bag_count, int32_t* error_count, uint32_t classes, void* stream) {
   if (num_features < 0 || num_chunks < 0 || num_ids < 0)
     return fail(MDL_ERR_INVALID, "mdl_forward: negative count");
   if (num_chunks == 0) return MDL_OK;
@@ -1071,6 +1084,8 @@ int mdl_forward(const mdl_feature* feats, int32_t num_features, const mdl_chunk*
   a.offsets = offsets;
   a.keys = sort_keys;
   a.payload = sort_payload;
+  a.key_origin = key_origin;
+  a.key_lo = 0;
   a.bag_count = bag_count;
   a.error_count = error_count;
   a.sentinel = sentinel;
@@ -1096,6 +1111,8 @@ int mdl_pool_backward(const mdl_feature* feats, int32_t num_features, const mdl_
   a.offsets = offsets;
   a.keys = nullptr;
   a.payload = nullptr;
+  a.key_origin = nullptr;
+  a.key_lo = 0;
   a.bag_count = const_cast<float*>(bag_count);
   a.error_count = nullptr;
   a.sentinel = 0;

@@ -138,6 +138,17 @@ def _check_features(weights, ids, lengths, table, pooling, exclude, padding_idx)
             raise ValueError("categorical bag lengths must have shape [B]")
 
 
+def _order(weights, table) -> Optional[list[int]]:
+    """Feature order of a device call: the callers' order, except that a call
+    over 2^32 - 1 table rows or more looks its features up sorted by table, so
+    that each key group's features are consecutive (its keys one stretch)."""
+
+    if sum(int(w.size(0)) for w in weights) < ops.KEY_SPACE:
+        return None
+    order = sorted(range(len(table)), key=lambda f: table[f])
+    return None if order == list(range(len(table))) else order
+
+
 def _plan(weights, table, pooling, exclude, padding_idx) -> ops.GroupPlan:
     plan = ops.GroupPlan()
     for w in weights:
@@ -161,6 +172,10 @@ def grouped_lookup(
     ids outside their table."""
 
     _check_features(weights, ids, lengths, table, pooling, exclude, padding_idx)
+    order = _order(weights, table)
+    if order is not None:
+        ids, lengths, table, pooling, exclude, padding_idx = (
+            [x[f] for f in order] for x in (ids, lengths, table, pooling, exclude, padding_idx))
     plan = _plan(weights, table, pooling, exclude, padding_idx)
     res = ops.grouped_forward(plan, ids, lengths, with_backward=need_backward, with_bag_count=True)
     device = weights[0].device
@@ -169,7 +184,13 @@ def grouped_lookup(
     payload = res.payload if need_backward else empty_i32.clone()
     bag_count = res.bag_count if res.bag_count is not None else torch.empty(0, dtype=torch.float32, device=device)
     offsets = res.offsets if res.offsets is not None else torch.empty(0, dtype=torch.int64, device=device)
-    return list(res.outputs), keys, payload, bag_count, offsets, res.error_count
+    outputs = list(res.outputs)
+    if order is not None:
+        back = [None] * len(order)
+        for i, f in enumerate(order):
+            back[f] = outputs[i]
+        outputs = back
+    return outputs, keys, payload, bag_count, offsets, res.error_count
 
 
 def _pool_cpu(emb: Tensor, live: Tensor, lengths: Tensor, mean: bool) -> tuple[Tensor, Tensor]:
@@ -261,6 +282,10 @@ def grouped_lookup_backward(
     (int64 ``[T]``).  The sort works on copies of the keys and payloads, so the
     op leaves its inputs as they are."""
 
+    order = _order(weights, table)
+    if order is not None:
+        ids, lengths, table, pooling, exclude, padding_idx, grads = (
+            [x[f] for f in order] for x in (ids, lengths, table, pooling, exclude, padding_idx, grads))
     plan = _plan(weights, table, pooling, exclude, padding_idx)
     keys = keys.clone()
     payload = payload.clone()

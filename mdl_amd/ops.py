@@ -260,12 +260,42 @@ class FeatureSpec:
     rows_by_position: bool = False
 
 
+# Sort keys are 32-bit: the rows of one key group stay below this, and a key
+# of the group's row count marks ids that receive no gradient.
+KEY_SPACE = 0xFFFFFFFF
+
+
+@dataclass
+class KeyGroup:
+    """Features ``[lo, hi)`` of a plan and the tables they read, whose rows
+    share one 32-bit key space (one sort and one segment reduce).
+
+    ``plan`` is the group as a plan of its own: the same table specs (their
+    ``row_base`` counted within the group) and features, table indices
+    renumbered in ``tables`` order."""
+
+    lo: int
+    hi: int
+    tables: list[int]
+    rows: int
+    plan: "GroupPlan"
+
+
 class GroupPlan:
     """Tables and features of a grouped lookup; static across steps.
 
     Features that pass the same weight tensor share one table.  Sort keys of
-    table t are ``row_base[t] + id``; the key one past the last row of the last
-    table marks ids that receive no gradient.
+    table t are ``row_base[t] + id``; the key ``sentinel`` (at least the rows of
+    every key group) marks ids that receive no gradient.
+
+    Keys are 32-bit.  A plan of 2^32 - 1 rows or more in all is cut into key
+    groups (:attr:`groups`): runs of consecutive features whose tables hold
+    fewer rows than that together, each table's rows counted from its group's
+    first.  One forward still looks up every feature; each group then has a
+    sort and a reduce of its own over its features' stretch of the keys.  A
+    table's features must then follow one another closely enough that no other
+    group's features come between them, and one table stays below 2^32 - 1
+    rows.
     """
 
     def __init__(self) -> None:
@@ -273,6 +303,8 @@ class GroupPlan:
         self.features: list[FeatureSpec] = []
         self._table_of_ptr: dict[int, int] = {}
         self.total_rows = 0
+        self._groups: list[KeyGroup] | None = None
+        self._groups_for: tuple[int, int] = (-1, -1)
 
     def add_table(self, weight: Tensor, state: Tensor | None = None, *, shared: bool = True) -> int:
         key = weight.data_ptr()
@@ -289,9 +321,9 @@ class GroupPlan:
         self.tables.append(TableSpec(weight=weight, state=state, row_base=self.total_rows))
         if shared:
             self._table_of_ptr[key] = t
+        if int(weight.size(0)) >= KEY_SPACE:
+            raise ValueError("a table of a grouped lookup holds fewer than 2^32 - 1 rows")
         self.total_rows += int(weight.size(0))
-        if self.total_rows >= 0xFFFFFFFF:
-            raise ValueError("a grouped lookup supports fewer than 2^32 - 1 rows in total")
         return t
 
     def add_feature(
@@ -329,8 +361,74 @@ class GroupPlan:
         return len(self.features) - 1
 
     @property
+    def groups(self) -> list[KeyGroup]:
+        """The key groups (one for a plan below 2^32 - 1 rows: every feature
+        and table, row bases as added)."""
+
+        shape = (len(self.tables), len(self.features))
+        if self._groups is not None and self._groups_for == shape:
+            return self._groups
+        if self.total_rows < KEY_SPACE:
+            groups = [KeyGroup(0, len(self.features), list(range(len(self.tables))), self.total_rows, self)]
+            base = 0
+            for t in self.tables:
+                t.row_base = base
+                base += int(t.weight.size(0))
+        else:
+            groups = self._split()
+        self._groups, self._groups_for = groups, shape
+        return groups
+
+    def _split(self) -> list[KeyGroup]:
+        cuts: list[tuple[int, int, list[int], int]] = []
+        owner: dict[int, int] = {}
+        lo, tabs, rows = 0, [], 0
+        for f, spec in enumerate(self.features):
+            t = spec.table
+            if t in owner and owner[t] != len(cuts):
+                raise ValueError(
+                    "a plan of 2^32 - 1 rows or more needs each table's features in one run of features "
+                    f"whose tables hold fewer rows than that (table {t} is read again by feature {f})"
+                )
+            if t in owner:
+                continue
+            r = int(self.tables[t].weight.size(0))
+            if tabs and rows + r >= KEY_SPACE:
+                cuts.append((lo, f, tabs, rows))
+                lo, tabs, rows = f, [], 0
+            owner[t] = len(cuts)
+            tabs.append(t)
+            rows += r
+        cuts.append((lo, len(self.features), tabs, rows))
+        groups = []
+        for lo, hi, tabs, rows in cuts:
+            sub = GroupPlan()
+            local = {}
+            base = 0
+            for t in tabs:
+                spec = self.tables[t]
+                spec.row_base = base
+                base += int(spec.weight.size(0))
+                local[t] = len(sub.tables)
+                sub.tables.append(spec)
+            sub.total_rows = base
+            for spec in self.features[lo:hi]:
+                sub.features.append(FeatureSpec(
+                    table=local[spec.table], pooling=spec.pooling, exclude_null=spec.exclude_null,
+                    padding_idx=spec.padding_idx, out_dtype=spec.out_dtype, rows_by_position=spec.rows_by_position,
+                ))
+            groups.append(KeyGroup(lo, hi, tabs, rows, sub))
+        return groups
+
+    @property
+    def split(self) -> bool:
+        """Whether the plan needs more than one key group."""
+
+        return len(self.groups) > 1
+
+    @property
     def sentinel(self) -> int:
-        return self.total_rows
+        return max(g.rows for g in self.groups) if self.groups else 0
 
     @property
     def key_bits(self) -> int:
@@ -400,6 +498,7 @@ def build_features(
     offsets of all features come from one scan over the concatenated lengths.
     """
 
+    plan.groups  # row bases of a plan cut into key groups
     specs = plan.features
     nf = len(specs)
     tab = [plan.tables[s.table] for s in specs]
@@ -498,7 +597,7 @@ def forward_packed(
     check(
         lib().mdl_forward(
             feats_dev.data_ptr(), len(feats), chunks_dev.data_ptr(), n_chunks, ids_arg.data_ptr(), n,
-            _ptr(offsets), _ptr(keys), _ptr(payload), plan.sentinel, _ptr(bag_count),
+            _ptr(offsets), _ptr(keys), _ptr(payload), None, plan.sentinel, _ptr(bag_count),
             error_count.data_ptr(), feature_classes(feats), stream,
         ),
         "mdl_forward",
@@ -608,6 +707,9 @@ def lane_elems(dim: int, esize: int, vec: bool) -> int:
 
 
 def _tables_array(plan: GroupPlan, feats: np.ndarray) -> np.ndarray:
+    if plan.total_rows >= KEY_SPACE:
+        raise ValueError("tables of 2^32 - 1 rows or more are keyed per key group (GroupPlan.groups)")
+    plan.groups  # row bases
     tables = np.zeros(len(plan.tables), dtype=TABLE_DTYPE)
     users: dict[int, list[int]] = {}
     for f, spec in enumerate(plan.features):
@@ -729,6 +831,22 @@ def pool_backward(
     del keep
 
 
+def _segments(res: ForwardResult, feats: np.ndarray) -> list[tuple[KeyGroup, np.ndarray, int, int]]:
+    """(key group, its backward descriptors, its first key, its key count) of
+    each key group of a forward: a group's features are consecutive, so its
+    keys are one stretch of the forward's key array."""
+
+    groups = res.plan.groups
+    if len(groups) == 1:
+        return [(groups[0], feats, 0, res.num_ids)]
+    out = []
+    for g in groups:
+        fs = np.ascontiguousarray(feats[g.lo: g.hi])
+        first = int(fs["ids_begin"][0]) if len(fs) else 0
+        out.append((g, fs, first, int(fs["num_ids"].sum())))
+    return out
+
+
 def backward_adagrad(
     res: ForwardResult,
     grads: Sequence[Tensor | None],
@@ -751,39 +869,49 @@ def backward_adagrad(
         if t.state is None:
             raise RuntimeError("every table needs a row-wise Adagrad accumulator")
     feats, keep = _attach_grads(res, grads)
-    tables = _tables_array(plan, feats)
     device = res.device
-    feats_dev = _CACHE.get(feats, device)
-    tables_dev = _CACHE.get(tables, device)
-    n = res.num_ids
-    ws = _workspace(lib().mdl_backward_workspace_bytes(n, len(tables), plan.max_dim), device)
-    classes = table_classes(tables)
     stream = _stream(device)
-    args = (feats_dev.data_ptr(), len(feats), tables_dev.data_ptr(), len(tables), plan.max_dim,
-            res.keys.data_ptr(), res.payload.data_ptr(), n, plan.key_bits, _ptr(res.bag_count))
+    segs = []
+    for g, fs, first, n in _segments(res, feats):
+        tables = _tables_array(g.plan, fs)
+        feats_dev = _CACHE.get(fs, device)
+        tables_dev = _CACHE.get(tables, device)
+        keep += [feats_dev, tables_dev]
+        args = (feats_dev.data_ptr(), len(fs), tables_dev.data_ptr(), len(tables), plan.max_dim,
+                res.keys.data_ptr() + 4 * first, res.payload.data_ptr() + 4 * first, n, plan.key_bits,
+                _ptr(res.bag_count))
+        segs.append((args, n, len(tables), table_classes(tables)))
     norm = None
     if clip_norm is None:
-        check(
-            lib().mdl_backward_adagrad(*args[:8], None, *args[8:], float(lr), float(eps), None, ws.data_ptr(),
-                                       ws.numel(), classes, stream),
-            "mdl_backward_adagrad",
-        )
+        # one workspace: each call sorts and reduces before the next one starts
+        ws = _workspace(max(lib().mdl_backward_workspace_bytes(n, T, plan.max_dim) for _, n, T, _ in segs), device)
+        for args, n, T, classes in segs:
+            check(
+                lib().mdl_backward_adagrad(*args[:8], None, *args[8:], float(lr), float(eps), None, ws.data_ptr(),
+                                           ws.numel(), classes, stream),
+                "mdl_backward_adagrad",
+            )
     else:
-        check(
-            lib().mdl_backward_sort(tables_dev.data_ptr(), len(tables), plan.max_dim, res.keys.data_ptr(),
-                                    res.payload.data_ptr(), n, None, plan.key_bits, ws.data_ptr(), ws.numel(),
-                                    stream),
-            "mdl_backward_sort",
-        )
-        sumsq = torch.empty(1, dtype=torch.float32, device=device)
-        check(lib().mdl_backward_sumsq(*args, sumsq.data_ptr(), ws.data_ptr(), ws.numel(), classes, stream),
-              "mdl_backward_sumsq")
+        sumsq = torch.empty(len(segs), dtype=torch.float32, device=device)
+        wss = []
+        for i, (args, n, T, classes) in enumerate(segs):
+            ws = _workspace(lib().mdl_backward_workspace_bytes(n, T, plan.max_dim), device)
+            wss.append(ws)
+            check(
+                lib().mdl_backward_sort(args[2], T, plan.max_dim, args[5], args[6], n, None, plan.key_bits,
+                                        ws.data_ptr(), ws.numel(), stream),
+                "mdl_backward_sort",
+            )
+            check(lib().mdl_backward_sumsq(*args, sumsq.data_ptr() + 4 * i, ws.data_ptr(), ws.numel(), classes,
+                                           stream),
+                  "mdl_backward_sumsq")
         norm, coef = clip_coefficient(sumsq, clip_norm)
-        check(
-            lib().mdl_backward_apply(*args, float(lr), float(eps), coef.data_ptr(), ws.data_ptr(), ws.numel(),
-                                     classes, stream),
-            "mdl_backward_apply",
-        )
+        for (args, n, T, classes), ws in zip(segs, wss):
+            check(
+                lib().mdl_backward_apply(*args, float(lr), float(eps), coef.data_ptr(), ws.data_ptr(), ws.numel(),
+                                         classes, stream),
+                "mdl_backward_apply",
+            )
     res.keys = None
     res.payload = None
     del keep
@@ -857,29 +985,39 @@ def backward_coalesce(res: ForwardResult, grads: Sequence[Tensor | None]) -> lis
     if res.keys is None:
         raise RuntimeError("the forward ran without backward bookkeeping")
     feats, keep = _attach_grads(res, grads)
-    tables = _tables_array(plan, feats)
     device = res.device
-    feats_dev = upload(feats, device)
-    tables_dev = upload(tables, device)
-    n = res.num_ids
-    T = len(tables)
     stream = _stream(device)
-    ws = _workspace(lib().mdl_backward_workspace_bytes(n, T, plan.max_dim), device)
-    urange = torch.zeros(2 * T, dtype=torch.int64, device=device)
-    check(
-        lib().mdl_backward_count(
-            tables_dev.data_ptr(), T, plan.max_dim, res.keys.data_ptr(), res.payload.data_ptr(), n, None,
-            plan.key_bits, urange.data_ptr(), ws.data_ptr(), ws.numel(), stream,
-        ),
-        "mdl_backward_count",
-    )
-    ur = urange.cpu().numpy().reshape(T, 2)
+    T = len(plan.tables)
+    segs = []
+    ranges = []
+    for g, fs, first, n in _segments(res, feats):
+        tables = _tables_array(g.plan, fs)
+        feats_dev = upload(fs, device)
+        tables_dev = upload(tables, device)
+        Tg = len(tables)
+        ws = _workspace(lib().mdl_backward_workspace_bytes(n, Tg, plan.max_dim), device)
+        urange = torch.zeros(2 * Tg, dtype=torch.int64, device=device)
+        keys, payload = res.keys.data_ptr() + 4 * first, res.payload.data_ptr() + 4 * first
+        check(
+            lib().mdl_backward_count(
+                tables_dev.data_ptr(), Tg, plan.max_dim, keys, payload, n, None, plan.key_bits, urange.data_ptr(),
+                ws.data_ptr(), ws.numel(), stream,
+            ),
+            "mdl_backward_count",
+        )
+        segs.append((g, fs, feats_dev, tables, tables_dev, ws, urange, keys, payload, n))
+        ranges.append(urange)
+    ur_host = torch.cat(ranges).cpu().numpy().reshape(-1, 2)
+    us = np.zeros(T, dtype=np.int64)
+    k = 0
+    for g, *_ in segs:
+        us[g.tables] = ur_host[k: k + len(g.tables), 1] - ur_host[k: k + len(g.tables), 0]
+        k += len(g.tables)
     # Two allocations for all tables, the rows split per table and the values
     # as per-table views of one byte buffer, each starting on a 256-byte
     # boundary (the kernel stores 16-byte vectors).  The kernel's output
     # addresses come from the two bases, so it is launched before the 200-odd
     # per-table views are built on the host (that loop overlaps the GPU).
-    us = (ur[:, 1] - ur[:, 0]).astype(np.int64)
     esz = np.array([t.weight.element_size() for t in plan.tables], dtype=np.int64)
     dims = np.array([int(t.weight.size(1)) for t in plan.tables], dtype=np.int64)
     nbytes = us * dims * esz
@@ -889,17 +1027,21 @@ def backward_coalesce(res: ForwardResult, grads: Sequence[Tensor | None]) -> lis
     np.cumsum(us, out=rows_off[1:])
     rows_all = torch.empty(int(rows_off[-1]), dtype=torch.int64, device=device)
     vbuf = torch.empty(int(offs[-1]), dtype=torch.uint8, device=device)
-    addr = np.zeros(2 * T, dtype=np.uint64)
-    addr[:T] = np.where(us > 0, rows_all.data_ptr() + 8 * rows_off[:T], 0).astype(np.uint64)
-    addr[T:] = np.where(us > 0, vbuf.data_ptr() + offs[:T], 0).astype(np.uint64)
-    if n:
+    for g, fs, feats_dev, tables, tables_dev, ws, urange, keys, payload, n in segs:
+        if not n:
+            continue
+        tg = np.asarray(g.tables, dtype=np.int64)
+        Tg = len(tg)
+        addr = np.zeros(2 * Tg, dtype=np.uint64)
+        addr[:Tg] = np.where(us[tg] > 0, rows_all.data_ptr() + 8 * rows_off[tg], 0).astype(np.uint64)
+        addr[Tg:] = np.where(us[tg] > 0, vbuf.data_ptr() + offs[tg], 0).astype(np.uint64)
         addr_dev = upload(addr, device)
+        keep.append(addr_dev)
         check(
             lib().mdl_backward_coalesce(
-                feats_dev.data_ptr(), len(feats), tables_dev.data_ptr(), T, plan.max_dim,
-                res.keys.data_ptr(), res.payload.data_ptr(), n, plan.key_bits, _ptr(res.bag_count),
-                urange.data_ptr(), addr_dev.data_ptr(), addr_dev.data_ptr() + 8 * T, ws.data_ptr(), ws.numel(),
-                table_classes(tables), stream,
+                feats_dev.data_ptr(), len(fs), tables_dev.data_ptr(), Tg, plan.max_dim, keys, payload, n,
+                plan.key_bits, _ptr(res.bag_count), urange.data_ptr(), addr_dev.data_ptr(),
+                addr_dev.data_ptr() + 8 * Tg, ws.data_ptr(), ws.numel(), table_classes(tables), stream,
             ),
             "mdl_backward_coalesce",
         )
@@ -970,56 +1112,75 @@ def backward_coalesce_padded(
     if res.keys is None:
         raise RuntimeError("the forward ran without backward bookkeeping")
     feats, keep = _attach_grads(res, grads)
-    tables = _tables_array(plan, feats)
     device = res.device
-    n = res.num_ids
-    T = len(tables)
+    T = len(plan.tables)
     stream = _stream(device)
     cap = table_capacities(res)
     layout = coalesced_layout([t.weight for t in plan.tables], cap)
     rows_off, val_off = layout["rows_off"], layout["val_off"]
     rows_all = torch.empty(max(int(rows_off[-1]), 1), dtype=torch.int64, device=device)
     vbuf = torch.empty(max(int(val_off[-1]), 1), dtype=torch.uint8, device=device)
-    urange = torch.zeros(2 * T, dtype=torch.int64, device=device)
-    if n:
-        pad_units = (cap + 63) // 64
-        unit_first = np.zeros(T + 1, dtype=np.int64)
+    segs = _segments(res, feats)
+    urange = torch.zeros(2 * sum(len(g.tables) for g, *_ in segs), dtype=torch.int64, device=device)
+    ws = None
+    u0 = 0
+    for g, fs, first, n in segs:
+        Tg = len(g.tables)
+        ur = urange.data_ptr() + 8 * u0
+        u0 += 2 * Tg
+        if not n:
+            continue
+        tg = np.asarray(g.tables, dtype=np.int64)
+        cg = cap[tg]
+        pad_units = (cg + 63) // 64
+        unit_first = np.zeros(Tg + 1, dtype=np.int64)
         np.cumsum(pad_units, out=unit_first[1:])
         # one upload: row and value addresses, capacities, pad-unit prefix
         host = np.concatenate([
-            np.where(cap > 0, rows_all.data_ptr() + 8 * rows_off[:T], 0).astype(np.uint64).view(np.int64),
-            np.where(cap > 0, vbuf.data_ptr() + val_off[:T], 0).astype(np.uint64).view(np.int64),
-            cap, unit_first,
+            np.where(cg > 0, rows_all.data_ptr() + 8 * rows_off[tg], 0).astype(np.uint64).view(np.int64),
+            np.where(cg > 0, vbuf.data_ptr() + val_off[tg], 0).astype(np.uint64).view(np.int64),
+            cg, unit_first,
         ])
         meta = upload(host, device)
         base = meta.data_ptr()
-        feats_dev = _CACHE.get(feats, device)
+        tables = _tables_array(g.plan, fs)
+        feats_dev = _CACHE.get(fs, device)
         tables_dev = _CACHE.get(tables, device)
-        ws = _workspace(lib().mdl_backward_workspace_bytes(n, T, plan.max_dim), device)
+        keep += [meta, feats_dev, tables_dev]
+        # one workspace: each group's calls finish before the next group's
+        need = lib().mdl_backward_workspace_bytes(n, Tg, plan.max_dim)
+        if ws is None or ws.numel() < need:
+            ws = _workspace(need, device)
+            keep.append(ws)
+        keys, payload = res.keys.data_ptr() + 4 * first, res.payload.data_ptr() + 4 * first
         check(
             lib().mdl_backward_count(
-                tables_dev.data_ptr(), T, plan.max_dim, res.keys.data_ptr(), res.payload.data_ptr(), n, None,
-                plan.key_bits, urange.data_ptr(), ws.data_ptr(), ws.numel(), stream,
+                tables_dev.data_ptr(), Tg, plan.max_dim, keys, payload, n, None, plan.key_bits, ur, ws.data_ptr(),
+                ws.numel(), stream,
             ),
             "mdl_backward_count",
         )
         check(
             lib().mdl_backward_coalesce(
-                feats_dev.data_ptr(), len(feats), tables_dev.data_ptr(), T, plan.max_dim, res.keys.data_ptr(),
-                res.payload.data_ptr(), n, plan.key_bits, _ptr(res.bag_count), urange.data_ptr(), base,
-                base + 8 * T, ws.data_ptr(), ws.numel(), table_classes(tables), stream,
+                feats_dev.data_ptr(), len(fs), tables_dev.data_ptr(), Tg, plan.max_dim, keys, payload, n,
+                plan.key_bits, _ptr(res.bag_count), ur, base, base + 8 * Tg, ws.data_ptr(), ws.numel(),
+                table_classes(tables), stream,
             ),
             "mdl_backward_coalesce",
         )
         check(
             lib().mdl_backward_pad(
-                tables_dev.data_ptr(), T, urange.data_ptr(), base, base + 8 * T, base + 16 * T, base + 24 * T,
+                tables_dev.data_ptr(), Tg, ur, base, base + 8 * Tg, base + 16 * Tg, base + 24 * Tg,
                 int(unit_first[-1]), stream,
             ),
             "mdl_backward_pad",
         )
-        keep.append(meta)
-    counts = urange[1::2] - urange[0::2]
+    if len(segs) == 1 and segs[0][0].tables == list(range(T)):
+        counts = urange[1::2] - urange[0::2]
+    else:
+        order = np.concatenate([np.asarray(g.tables, dtype=np.int64) for g, *_ in segs])
+        counts = torch.zeros(T, dtype=torch.int64, device=device)
+        counts.index_copy_(0, upload(order, device).view(torch.int64), urange[1::2] - urange[0::2])
     res.keys = None
     res.payload = None
     del keep

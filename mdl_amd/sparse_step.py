@@ -52,6 +52,26 @@ def _as_ids(t: Tensor) -> Tensor:
     return t.contiguous()
 
 
+class _KeyGroup:
+    """Device state of one key group of a step: its forward descriptors and
+    chunks, sort keys and payloads, backward descriptors, tables and
+    workspace."""
+
+    F: int
+    feats_fwd_dev: Tensor
+    chunks_dev: Tensor
+    n_chunks: int
+    fwd_classes: int
+    feats_bwd: np.ndarray
+    feats_bwd_dev: Tensor
+    tables: np.ndarray
+    tables_dev: Tensor
+    bwd_classes: int
+    keys: Tensor
+    payload: Tensor
+    ws: Tensor
+
+
 class SparseStep:
     """Fused lookup/pooling + backward + row-wise Adagrad for one layout.
 
@@ -119,13 +139,20 @@ class SparseStep:
         out_ptrs = [o.data_ptr() for o in outputs[0]]
         out_strides = [o.stride(0) if o.ndim == 2 else int(o.size(-1)) for o in outputs[0]]
         feats = ops.build_features(plan, id_counts, bag_counts, out_ptrs, out_strides)
-        target = ops.forward_target_ids(feats)
-        n_chunks = lib().mdl_plan_chunks(feats.ctypes.data, len(feats), target, None, 0)
-        if n_chunks < 0:
-            check(int(n_chunks), "mdl_plan_chunks")
-        chunks = np.zeros(max(n_chunks, 1), dtype=CHUNK_DTYPE)
-        lib().mdl_plan_chunks(feats.ctypes.data, len(feats), target, chunks.ctypes.data, n_chunks)
-        self.n_chunks = int(n_chunks)
+        groups = plan.groups
+        # Chunks of each key group, planned on this batch's id counts (a
+        # group's chunks number its features from the group's first).
+        chunks = []
+        for g in groups:
+            sub = np.ascontiguousarray(feats[g.lo: g.hi])
+            target = ops.forward_target_ids(sub)
+            nc = lib().mdl_plan_chunks(sub.ctypes.data, len(sub), target, None, 0)
+            if nc < 0:
+                check(int(nc), "mdl_plan_chunks")
+            ch = np.zeros(max(nc, 1), dtype=CHUNK_DTYPE)
+            lib().mdl_plan_chunks(sub.ctypes.data, len(sub), target, ch.ctypes.data, nc)
+            chunks.append((ch, int(nc)))
+        first_ids = feats["ids_begin"].copy()
         if self.dynamic:
             # The offsets of each call place every feature's ids.
             feats["flags"] |= MDL_FLAG_IDS_FROM_OFFSETS
@@ -139,7 +166,7 @@ class SparseStep:
             raise ValueError("the micro-batches' output rows exceed the 32-bit gradient-row payload")
         # Micro-batch m: its forward descriptors (its outputs, payloads and
         # bag counts shifted by m rows-per-batch) and its backward ones (its
-        # gradients), all features of micro-batch 0 first.
+        # gradients).
         fwd, bwd = [], []
         self._grads = []
         for m in range(self.k):
@@ -157,32 +184,57 @@ class SparseStep:
             bwd.append(fb)
             self._grads += keep
         self.feats_fwd = fwd[0]
-        self.feats_bwd = np.concatenate(bwd)
-        self.tables = ops._tables_array(plan, self.feats_bwd[: len(plan.features)])
-        if self.k > 1:
-            # a table read by k copies of its feature: the reduce finds each
-            # payload's feature by search instead of the one-feature path
-            self.tables["feature"] = -1
-        self.fwd_classes = ops.feature_classes(self.feats_fwd)
-        self.bwd_classes = ops.table_classes(self.tables)
-        self.feats_fwd_dev = ops.upload(np.concatenate(fwd), self.device)
-        self.chunks_dev = ops.upload(chunks, self.device)
-        self.feats_bwd_dev = ops.upload(self.feats_bwd, self.device)
-        self.tables_dev = ops.upload(self.tables, self.device)
-        cap = max(self.capacity, 1)
-        self.keys = torch.empty(cap * self.k, dtype=torch.int32, device=self.device)
-        self.payload = torch.empty(cap * self.k, dtype=torch.int32, device=self.device)
         self.bag_count = (
             torch.empty(self.rows_per_batch * self.k, dtype=torch.float32, device=self.device) if pooled_any else None
         )
+        cap = max(self.capacity, 1)
+        n_sort = self._n()
+        self.groups = []
+        for g, (ch, nc) in zip(groups, chunks):
+            gs = _KeyGroup()
+            gs.F = g.hi - g.lo
+            # all micro-batches' descriptors of the group's features, micro-batch 0 first
+            f_fwd = np.concatenate([fm[g.lo: g.hi] for fm in fwd])
+            gs.feats_bwd = np.concatenate([fb[g.lo: g.hi] for fb in bwd])
+            gs.tables = ops._tables_array(g.plan, np.ascontiguousarray(bwd[0][g.lo: g.hi]))
+            if self.k > 1:
+                # a table read by k copies of its feature: the reduce finds each
+                # payload's feature by search instead of the one-feature path
+                gs.tables["feature"] = -1
+            gs.fwd_classes = ops.feature_classes(np.ascontiguousarray(fwd[0][g.lo: g.hi]))
+            gs.bwd_classes = ops.table_classes(gs.tables)
+            gs.feats_fwd_dev = ops.upload(f_fwd, self.device)
+            gs.chunks_dev = ops.upload(ch, self.device)
+            gs.n_chunks = nc
+            gs.feats_bwd_dev = ops.upload(gs.feats_bwd, self.device)
+            gs.tables_dev = ops.upload(gs.tables, self.device)
+            gs.keys = torch.empty(cap * self.k, dtype=torch.int32, device=self.device)
+            gs.payload = torch.empty(cap * self.k, dtype=torch.int32, device=self.device)
+            gs.ws = ops._workspace(
+                lib().mdl_backward_workspace_bytes(n_sort, len(gs.tables), plan.max_dim), self.device
+            )
+            self.groups.append(gs)
+        G = len(self.groups)
+        if G > 1:
+            # Each group's ids are one stretch of the packed ids: its first
+            # position (the key origin of its forward) and its id count, on
+            # the device -- from the offsets scan when bag lengths place them.
+            lo = np.array([g.lo for g in groups], dtype=np.int64)
+            hi = np.array([g.hi for g in groups], dtype=np.int64)
+            if self.dynamic:
+                bags = np.append(feats["bag_base"], int(self.lengths.numel()))
+                self._gidx = ops.upload(np.concatenate([bags[lo], bags[hi]]), self.device).view(torch.int64)
+                self._gsel = torch.empty(2 * G, dtype=torch.int64, device=self.device)
+                self._gcount = torch.empty(G, dtype=torch.int64, device=self.device)
+            else:
+                ends = np.append(first_ids, int(self.ids.numel()))
+                self._gsel = ops.upload(np.concatenate([ends[lo], ends[hi]]), self.device).view(torch.int64)
+                self._gcount = ops.upload(ends[hi] - ends[lo], self.device).view(torch.int64)
         if self.k > 1:
             self._positions = torch.arange(cap, dtype=torch.int64, device=self.device)
             sentinel = int(plan.sentinel)
             self._sentinel = sentinel - (1 << 32) if sentinel >= (1 << 31) else sentinel
-        self.ws = ops._workspace(
-            lib().mdl_backward_workspace_bytes(self._n(), len(self.tables), plan.max_dim), self.device
-        )
-        self.sumsq = torch.zeros(1, dtype=torch.float32, device=self.device)
+        self.sumsq = torch.zeros(G, dtype=torch.float32, device=self.device)
         self.norm = torch.zeros(1, dtype=torch.float32, device=self.device)
         self.coef = torch.ones(1, dtype=torch.float32, device=self.device)
 
@@ -219,13 +271,17 @@ class SparseStep:
     def _stream(self) -> int:
         return torch.cuda.current_stream(self.device).cuda_stream
 
-    def _count_ptr(self):
+    def _count_ptr(self, g: int):
+        """Device address of group g's entry count (None: all of the capacity)."""
+
+        if len(self.groups) > 1:
+            return self._gcount.data_ptr() + 8 * g
         return None if self.offsets is None else self.offsets.data_ptr() + 8 * (self.offsets.numel() - 1)
 
     def _n(self) -> int:
         if self.k > 1:
             return max(self.capacity, 1) * self.k
-        return self.capacity if self.dynamic else int(self.ids.numel())
+        return self.capacity if self.dynamic or len(self.plan.groups) > 1 else int(self.ids.numel())
 
     # ------------------------------------------------------------- steps --
 
@@ -245,40 +301,49 @@ class SparseStep:
                 ),
                 "mdl_lengths_to_offsets",
             )
-        ids = self.ids if self.ids.numel() else self.keys  # any valid address; nothing is read
-        F = len(self.feats_fwd)
+        G = len(self.groups)
+        if G > 1 and self.dynamic:
+            torch.index_select(self.offsets, 0, self._gidx, out=self._gsel)
+            torch.sub(self._gsel[G:], self._gsel[:G], out=self._gcount)
+        ids = self.ids if self.ids.numel() else self.groups[0].keys  # any valid address; nothing is read
         region = m * max(self.capacity, 1)
-        check(
-            lib().mdl_forward(
-                self.feats_fwd_dev.data_ptr() + m * F * FEATURE_DTYPE.itemsize, F, self.chunks_dev.data_ptr(), self.n_chunks,
-                ids.data_ptr(), int(self.ids.numel()), ops._ptr(self.offsets), self.keys.data_ptr() + 4 * region,
-                self.payload.data_ptr() + 4 * region, self.plan.sentinel, ops._ptr(self.bag_count),
-                self.error_count.data_ptr(), self.fwd_classes, s,
-            ),
-            "mdl_forward",
-        )
-        if self.k > 1:
-            # entries of the region past this micro-batch's ids sort last and
-            # reduce nowhere
-            live = self.offsets[-1] if self.offsets is not None else int(self.ids.numel())
-            self.keys[region: region + max(self.capacity, 1)].masked_fill_(self._positions >= live, self._sentinel)
+        for g, gs in enumerate(self.groups):
+            origin = None if G == 1 else self._gsel.data_ptr() + 8 * g
+            check(
+                lib().mdl_forward(
+                    gs.feats_fwd_dev.data_ptr() + m * gs.F * FEATURE_DTYPE.itemsize, gs.F, gs.chunks_dev.data_ptr(),
+                    gs.n_chunks, ids.data_ptr(), int(self.ids.numel()), ops._ptr(self.offsets),
+                    gs.keys.data_ptr() + 4 * region, gs.payload.data_ptr() + 4 * region, origin, self.plan.sentinel,
+                    ops._ptr(self.bag_count), self.error_count.data_ptr(), gs.fwd_classes, s,
+                ),
+                "mdl_forward",
+            )
+            if self.k > 1:
+                # entries of the region past this micro-batch's ids sort last
+                # and reduce nowhere
+                if G > 1:
+                    live = self._gcount[g]
+                else:
+                    live = self.offsets[-1] if self.offsets is not None else int(self.ids.numel())
+                gs.keys[region: region + max(self.capacity, 1)].masked_fill_(self._positions >= live, self._sentinel)
 
     def sort(self) -> None:
         """Radix sort of the (row, gradient-row) pairs + chunk plan."""
 
-        check(
-            lib().mdl_backward_sort(
-                self.tables_dev.data_ptr(), len(self.tables), self.plan.max_dim, self.keys.data_ptr(),
-                self.payload.data_ptr(), self._n(), self._count_ptr() if self.k == 1 else None, self.plan.key_bits,
-                self.ws.data_ptr(), self.ws.numel(), self._stream(),
-            ),
-            "mdl_backward_sort",
-        )
+        for g, gs in enumerate(self.groups):
+            check(
+                lib().mdl_backward_sort(
+                    gs.tables_dev.data_ptr(), len(gs.tables), self.plan.max_dim, gs.keys.data_ptr(),
+                    gs.payload.data_ptr(), self._n(), self._count_ptr(g) if self.k == 1 else None,
+                    self.plan.key_bits, gs.ws.data_ptr(), gs.ws.numel(), self._stream(),
+                ),
+                "mdl_backward_sort",
+            )
 
-    def _bwd_args(self) -> tuple:
+    def _bwd_args(self, gs: "_KeyGroup") -> tuple:
         return (
-            self.feats_bwd_dev.data_ptr(), len(self.feats_bwd), self.tables_dev.data_ptr(), len(self.tables),
-            self.plan.max_dim, self.keys.data_ptr(), self.payload.data_ptr(), self._n(), self.plan.key_bits,
+            gs.feats_bwd_dev.data_ptr(), len(gs.feats_bwd), gs.tables_dev.data_ptr(), len(gs.tables),
+            self.plan.max_dim, gs.keys.data_ptr(), gs.payload.data_ptr(), self._n(), self.plan.key_bits,
             ops._ptr(self.bag_count),
         )
 
@@ -286,13 +351,14 @@ class SparseStep:
         """Segment reduction of duplicate rows + fused row-wise Adagrad
         (gradients times ``grad_scale``, a device fp32 [1], when given)."""
 
-        check(
-            lib().mdl_backward_apply(
-                *self._bwd_args(), float(lr), float(eps), ops._ptr(grad_scale), self.ws.data_ptr(),
-                self.ws.numel(), self.bwd_classes, self._stream(),
-            ),
-            "mdl_backward_apply",
-        )
+        for gs in self.groups:
+            check(
+                lib().mdl_backward_apply(
+                    *self._bwd_args(gs), float(lr), float(eps), ops._ptr(grad_scale), gs.ws.data_ptr(),
+                    gs.ws.numel(), gs.bwd_classes, self._stream(),
+                ),
+                "mdl_backward_apply",
+            )
 
     def clip(self, max_norm: float) -> tuple[Tensor, Tensor]:
         """After sort(): (pre-clip global norm, clip coefficient), on device.
@@ -300,15 +366,16 @@ class SparseStep:
         The norm is that of the coalesced gradient of every table, as the
         trainer's sparse clip computes it (src/train.py:5788-5826)."""
 
+        for g, gs in enumerate(self.groups):
+            check(
+                lib().mdl_backward_sumsq(
+                    *self._bwd_args(gs), self.sumsq.data_ptr() + 4 * g, gs.ws.data_ptr(), gs.ws.numel(),
+                    gs.bwd_classes, self._stream(),
+                ),
+                "mdl_backward_sumsq",
+            )
         check(
-            lib().mdl_backward_sumsq(
-                *self._bwd_args(), self.sumsq.data_ptr(), self.ws.data_ptr(), self.ws.numel(), self.bwd_classes,
-                self._stream(),
-            ),
-            "mdl_backward_sumsq",
-        )
-        check(
-            lib().mdl_clip_coef(self.sumsq.data_ptr(), 1, float(max_norm), self.norm.data_ptr(),
+            lib().mdl_clip_coef(self.sumsq.data_ptr(), len(self.groups), float(max_norm), self.norm.data_ptr(),
                                 self.coef.data_ptr(), self._stream()),
             "mdl_clip_coef",
         )
@@ -367,6 +434,8 @@ class SequenceStep:
         for t in plan.tables:
             if t.state is None:
                 raise RuntimeError("every table needs a row-wise Adagrad accumulator")
+        if plan.total_rows >= ops.KEY_SPACE:
+            raise NotImplementedError("sequence steps take plans of fewer than 2^32 - 1 rows")
         self.plan = plan
         self.device = ids[0].device
         self.ids = [_as_ids(t) for t in ids]

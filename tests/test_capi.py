@@ -92,13 +92,13 @@ def test_invalid_arguments_fail_before_any_launch():
     assert rc == -1 and b"table" in lib.mdl_last_error()
     rc = lib.mdl_backward_apply(None, 0, None, 1, 600, None, None, 10, 8, None, 0.1, 1e-8, None, None, 0, 0, None)
     assert rc == -4 and b"512" in lib.mdl_last_error()
-    rc = lib.mdl_forward(None, 0, None, 1, None, -1, None, None, None, 0, None, None, 0, None)
+    rc = lib.mdl_forward(None, 0, None, 1, None, -1, None, None, None, None, 0, None, None, 0, None)
     assert rc == -1
     rc = lib.mdl_rowwise_adagrad(None, _lib.MDL_F32, 10, 4, 4, None, None, 3, None, _lib.MDL_BF16, 4, 0.1,
                                  1e-8, None, None)
     assert rc == -1  # null pointers
     # zero-sized work is a no-op success without touching the device
-    assert lib.mdl_forward(None, 0, None, 0, None, 0, None, None, None, 0, None, None, 0, None) == 0
+    assert lib.mdl_forward(None, 0, None, 0, None, 0, None, None, None, None, 0, None, None, 0, None) == 0
     assert lib.mdl_rowwise_adagrad(None, 0, 0, 4, 4, None, None, 0, None, 0, 4, 0.1, 1e-8, None, None) == 0
 
 

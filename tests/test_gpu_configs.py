@@ -27,8 +27,6 @@ The tests free their tables at the end (c1 and c2 do not fit together) and
 print their progress, since each takes tens of seconds.
 """
 
-import gc
-import sys
 import time
 
 import numpy as np
@@ -37,111 +35,9 @@ import torch
 
 import bench
 from oracle import oracle as O
+from parity_helpers import RTOL, _check_update, _free, _random_state, _Snapshot, _touched, assert_close, say
 
 pytestmark = [pytest.mark.gpu, pytest.mark.timeout(900)]
-
-RTOL = {"fp32": 1e-5, "bf16": 1e-2}
-
-
-def say(*parts):
-    print("CASE", *parts, flush=True)
-    sys.stdout.flush()
-    sys.stderr.write(" ".join(str(p) for p in ("CASE",) + parts) + "\n")
-    sys.stderr.flush()
-
-
-def _checksum(t: torch.Tensor) -> tuple[int, int]:
-    """(sum, sum of squares) of the table's raw bit patterns, as int64 with
-    wrap-around; any change to any element changes it but for collisions."""
-
-    x = t.reshape(-1).view(torch.int32 if t.element_size() == 4 else torch.int16)
-    s1 = torch.zeros((), dtype=torch.int64, device=t.device)
-    s2 = torch.zeros((), dtype=torch.int64, device=t.device)
-    step = 1 << 27
-    for i in range(0, x.numel(), step):
-        part = x[i: i + step].to(torch.int64)
-        s1 += part.sum()
-        s2 += (part * part).sum()
-        del part
-    return int(s1.item()), int(s2.item())
-
-
-def assert_close(got, ref, rtol, atol, scale=None, what=""):
-    got = np.asarray(got, dtype=np.float64)
-    ref = np.asarray(ref, dtype=np.float64)
-    assert got.shape == ref.shape, (what, got.shape, ref.shape)
-    err = np.abs(got - ref)
-    mag = np.abs(ref) if scale is None else np.maximum(np.abs(ref), np.asarray(scale, dtype=np.float64))
-    bound = atol + rtol * mag
-    bad = err > bound
-    assert not bad.any(), f"{what}: {int(bad.sum())} mismatches, worst excess {float((err - bound).max())}"
-
-
-def _check_update(what, w_post, a_post, w_pre, a_pre, rows, g, s, lr, eps, rtol, atol_w, is_bf16):
-    """Touched rows against the oracle's update of the coalesced gradient.
-
-    ``g`` is the oracle's coalesced gradient (fp64) of local ``rows`` and
-    ``s`` the same coalesce over |terms|.  fp32 summation puts at most about
-    rtol * s on each gradient element, so the accumulator
-    a = a0 + sum(g^2)/dim is compared relative to a0 + sum(s^2)/dim, and the
-    weight w = w0 - lr * g / (sqrt(a) + eps) relative to |w| plus the
-    first-order effect of both errors:
-    lr * (s + |g| * a_scale / (2 sqrt(a) (sqrt(a) + eps))) / (sqrt(a) + eps).
-    Rows without a gradient must not change at all.
-    """
-
-    w_ref, a_ref = O.rowwise_adagrad(w_pre, a_pre, rows, g, lr, eps, is_bf16=is_bf16)
-    dim = w_pre.shape[1]
-    untouched = np.ones(w_pre.shape[0], dtype=bool)
-    untouched[rows] = False
-    assert np.array_equal(w_post[untouched], w_pre[untouched]), f"{what}: rows without gradient changed"
-    assert np.array_equal(a_post[untouched], a_pre[untouched]), f"{what}: state without gradient changed"
-    a_scale = a_pre[rows].astype(np.float64) + (s * s).sum(1) / dim
-    assert_close(a_post[rows], a_ref[rows], 1e-5, 1e-7, a_scale, what + " accumulators")
-    ar = a_ref[rows].astype(np.float64)
-    den = np.sqrt(ar) + eps
-    prop = lr * (s + np.abs(g) * (a_scale / (2.0 * np.maximum(np.sqrt(ar), 1e-30) * den))[:, None]) / den[:, None]
-    scale = np.abs(w_ref[rows]) + prop
-    assert_close(w_post[rows], w_ref[rows], rtol, atol_w, scale, what + " weights")
-
-
-def _free():
-    gc.collect()
-    torch.cuda.synchronize()
-    torch.cuda.empty_cache()
-
-
-def _touched(tables_ids):
-    return np.unique(np.concatenate([np.zeros(1, np.int64)] + [np.asarray(x, np.int64).ravel() for x in tables_ids]))
-
-
-class _Snapshot:
-    """Touched rows and checksums of every table, taken before the step."""
-
-    def __init__(self, tables, states, touched, device):
-        self.idx = [torch.from_numpy(u).to(device) for u in touched]
-        self.sums = [(_checksum(w), _checksum(a)) for w, a in zip(tables, states)]
-        self.w = [w.index_select(0, i).float().cpu().numpy() for w, i in zip(tables, self.idx)]
-        self.a = [a.index_select(0, i).cpu().numpy() for a, i in zip(states, self.idx)]
-
-    def after(self, tables, states):
-        w = [t.index_select(0, i).float().cpu().numpy() for t, i in zip(tables, self.idx)]
-        a = [s.index_select(0, i).cpu().numpy() for s, i in zip(states, self.idx)]
-        return w, a
-
-    def restore_and_check(self, tables, states):
-        for t, (w, a, i) in enumerate(zip(tables, states, self.idx)):
-            w.index_copy_(0, i, torch.from_numpy(self.w[t]).to(w.device).to(w.dtype))
-            a.index_copy_(0, i, torch.from_numpy(self.a[t]).to(a.device))
-            assert (_checksum(w), _checksum(a)) == self.sums[t], f"table {t}: an untouched row or state changed"
-
-
-def _random_state(states, seed):
-    gen = torch.Generator(device=states[0].device)
-    gen.manual_seed(seed)
-    for a in states:
-        a.uniform_(0.0, 2.0, generator=gen)
-
 
 @pytest.mark.parametrize("name", ["c0", "c4", "c1", "c3"])
 def test_pooled_config_full_size_matches_oracle(device, name):

@@ -1,0 +1,266 @@
+"""Plans of more than 2^32 - 1 rows on one GPU: key groups.
+
+Two dim-8 bf16 tables of 2.2e9 and 2.3e9 rows and a small fp32 table (about
+4.5e9 rows, 72 GB of weights and 18 GB of accumulators) are more rows than one
+32-bit key space holds, so the plan is cut into two key groups: the first
+table's features, then the second's and the third's.  Three paths run over
+them and are checked against the CPU oracle on compact copies of the touched
+rows (rows above 2^31 of a table and keys above 2^31 of a group included):
+
+* ``SparseStep`` (bag lengths placed on the device, each group's keys placed
+  by its key origin), with the clip norm summed over both groups;
+* the ``mdl_hip::grouped_lookup`` custom op and its backward (the drop-in's
+  path), with a feature order that reads the first table again after the
+  second, so the op must reorder its features by table;
+* ``ops.grouped_forward`` + ``ops.backward_adagrad`` with a clip that scales
+  the gradient of both groups by one coefficient.
+
+Untouched rows and accumulators of every table are checked bit for bit
+(checksums) after the SparseStep.
+"""
+
+import time
+
+import numpy as np
+import pytest
+import torch
+
+from mdl_amd import ops
+from mdl_amd.sparse_step import SparseStep
+from oracle import oracle as O
+from parity_helpers import RTOL, _check_update, _free, _random_state, _Snapshot, _touched, assert_close, say
+
+pytestmark = [pytest.mark.gpu, pytest.mark.timeout(900)]
+
+ROWS = [2_200_000_000, 2_300_000_000, 10_000]
+DIMS = [8, 8, 16]
+DTYPES = [torch.bfloat16, torch.bfloat16, torch.float32]
+LR, EPS = 0.05, 1e-8
+B = 2048
+
+
+@pytest.fixture(scope="module")
+def big(device):
+    t0 = time.time()
+    say("key_groups", "allocating", f"{sum(ROWS):.3e} rows")
+    tables = [torch.empty((r, d), dtype=dt, device=device) for r, d, dt in zip(ROWS, DIMS, DTYPES)]
+    states = [torch.empty(r, dtype=torch.float32, device=device) for r in ROWS]
+    _random_state(states, 11)
+    torch.cuda.synchronize()
+    say("key_groups", "tables ready", f"{time.time() - t0:.1f}s")
+    yield tables, states
+    del tables, states
+    _free()
+
+
+def _draw(rng, feats):
+    """Ids (uniform over the table, a hot set with the edge rows, and nulls)
+    and bag lengths of each (table, pooling) feature."""
+
+    ids, lens = [], []
+    for t, pool in feats:
+        R = ROWS[t]
+        if pool == "none":
+            ln, n = None, B
+        else:
+            ln = rng.integers(0, 16, size=B)
+            n = int(ln.sum())
+        x = rng.integers(0, R, size=n)
+        edge = np.array([R - 1, R - 2, min(1 << 31, R - 1), min((1 << 31) - 1, R - 1), 1, 2], dtype=np.int64)
+        hot = np.concatenate([edge, rng.integers(0, R, size=300)])
+        pick = rng.random(n)
+        x[pick < 0.3] = rng.choice(hot, size=int((pick < 0.3).sum()))
+        x[pick > 0.93] = 0
+        ids.append(x.astype(np.int64))
+        lens.append(ln)
+    return ids, lens
+
+
+def _set_touched(tables, touched, rng):
+    """Random values in the touched rows (the rest of a table is whatever
+    the allocation held: the checks read it only through checksums)."""
+
+    for w, u in zip(tables, touched):
+        vals = torch.from_numpy(rng.standard_normal((u.size, w.size(1))).astype(np.float32)).to(w.device)
+        w.index_copy_(0, torch.from_numpy(u).to(w.device), vals.to(w.dtype))
+
+
+def _oracle_grads(feats, ids, lens, grads, touched, snap, outs, what):
+    """Check every output; per table the coalesced gradient (rows in the
+    compact numbering, fp64 sums) and the same sums over |terms|."""
+
+    T = len(ROWS)
+    rows_t = [[] for _ in range(T)]
+    vals_t = [[] for _ in range(T)]
+    absv_t = [[] for _ in range(T)]
+    for f, ((t, pool), x, ln) in enumerate(zip(feats, ids, lens)):
+        lid = np.searchsorted(touched[t], x)
+        got = outs[f].float().cpu().numpy()
+        gf = grads[f].float().cpu().numpy().astype(np.float64)
+        rtol = RTOL["fp32" if DTYPES[t] == torch.float32 else "bf16"]
+        if pool == "none":
+            assert np.array_equal(got, snap.w[t][lid]), f"{what} feature {f}: gathered rows"
+            r, v = O.per_id_grads(lid, None, gf, "none", "exclude")
+            _, va = O.per_id_grads(lid, None, np.abs(gf), "none", "exclude")
+        else:
+            ref, _ = O.pool(snap.w[t], lid, ln, pool, "exclude")
+            mag, _ = O.pool(np.abs(snap.w[t]), lid, ln, pool, "exclude")
+            assert_close(got, ref, rtol, 1e-7, mag, f"{what} feature {f} pooled")
+            r, v = O.per_id_grads(lid, ln, gf, pool, "exclude")
+            _, va = O.per_id_grads(lid, ln, np.abs(gf), pool, "exclude")
+        rows_t[t].append(r)
+        vals_t[t].append(v)
+        absv_t[t].append(va)
+    out = []
+    for t in range(T):
+        if not rows_t[t]:
+            out.append(None)
+            continue
+        rr, g = O.coalesce(np.concatenate(rows_t[t]), np.concatenate(vals_t[t]))
+        _, s = O.coalesce(np.concatenate(rows_t[t]), np.concatenate(absv_t[t]))
+        out.append((rr, g, s))
+    return out
+
+
+def _touched_of(feats, ids):
+    per = [[] for _ in ROWS]
+    for (t, _), x in zip(feats, ids):
+        per[t].append(x)
+    return [_touched(xs) if xs else np.zeros(1, np.int64) for xs in per]
+
+
+def _plan(tables, states, feats):
+    plan = ops.GroupPlan()
+    for t, pool in feats:
+        plan.add_feature(tables[t], pooling=pool, null_policy="exclude", state=states[t])
+    return plan
+
+
+def _grads(rng, outs):
+    return [torch.from_numpy(rng.standard_normal(tuple(o.shape)).astype(np.float32)).to(o.device).to(o.dtype)
+            for o in outs]
+
+
+def test_sparse_step_over_two_key_groups_matches_oracle(device, big):
+    t0 = time.time()
+    tables, states = big
+    rng = np.random.default_rng(4500)
+    feats = [(0, "mean"), (0, "none"), (1, "sum"), (2, "none")]
+    plan = _plan(tables, states, feats)
+    assert plan.split and [(g.lo, g.hi, g.tables) for g in plan.groups] == [(0, 2, [0]), (2, 4, [1, 2])]
+    assert plan.key_bits == 32
+    ids, lens = _draw(rng, feats)
+    touched = _touched_of(feats, ids)
+    _set_touched(tables, touched, rng)
+    snap = _Snapshot(tables, states, touched, device)
+    say("key_groups", "sparse step snapshot", f"{time.time() - t0:.1f}s")
+    outs = [torch.empty((B if ln is not None else x.size, DIMS[t]), dtype=DTYPES[t], device=device)
+            for (t, _), x, ln in zip(feats, ids, lens)]
+    grads = _grads(rng, outs)
+    packed = torch.from_numpy(np.concatenate(ids)).to(device)
+    lengths = torch.from_numpy(np.concatenate(
+        [ln if ln is not None else np.array([x.size]) for x, ln in zip(ids, lens)]).astype(np.int64)).to(device)
+    st = SparseStep(plan, packed, lengths, [x.size for x in ids], [0 if ln is None else B for ln in lens],
+                    outs, grads)
+    assert len(st.groups) == 2
+    st.forward()
+    st.sort()
+    norm, coef = st.clip(1e9)
+    st.apply(LR, EPS, coef)
+    torch.cuda.synchronize()
+    assert int(st.error_count.item()) == 0
+    say("key_groups", "sparse step done", f"{time.time() - t0:.1f}s")
+    w_post, a_post = snap.after(tables, states)
+    ref = _oracle_grads(feats, ids, lens, grads, touched, snap, outs, "sparse step")
+    sumsq = 0.0
+    for t, r in enumerate(ref):
+        rr, g, s = r
+        sumsq += float((g * g).sum())
+        bf = DTYPES[t] == torch.bfloat16
+        _check_update(f"sparse step table {t}", w_post[t], a_post[t], snap.w[t], snap.a[t], rr, g, s, LR, EPS,
+                      RTOL["bf16" if bf else "fp32"], 1e-6 if bf else 1e-7, bf)
+    assert_close(norm.cpu().numpy(), np.array([np.sqrt(sumsq)]), 1e-4, 0, what="clip norm")
+    say("key_groups", "sparse step checked", f"{time.time() - t0:.1f}s")
+    snap.restore_and_check(tables, states)
+    say("key_groups", "untouched rows checked", f"{time.time() - t0:.1f}s")
+
+
+def test_grouped_lookup_op_reorders_features_across_key_groups(device, big):
+    """The drop-in's op: features [t0 mean, t1 sum, t0 none, t2 none] read
+    table 0 again after table 1; outputs come back in the caller's order and
+    the coalesced gradients of every table match the oracle."""
+
+    t0 = time.time()
+    tables, states = big
+    rng = np.random.default_rng(4501)
+    feats = [(0, "mean"), (1, "sum"), (0, "none"), (2, "none")]
+    ids, lens = _draw(rng, feats)
+    touched = _touched_of(feats, ids)
+    _set_touched(tables, touched, rng)
+    snap = _Snapshot.__new__(_Snapshot)
+    snap.idx = [torch.from_numpy(u).to(device) for u in touched]
+    snap.w = [w.index_select(0, i).float().cpu().numpy() for w, i in zip(tables, snap.idx)]
+    code = {"none": 0, "sum": 1, "mean": 2}
+    ids_dev = [torch.from_numpy(x).to(device) for x in ids]
+    lens_dev = [None if ln is None else torch.from_numpy(ln).to(device) for ln in lens]
+    outs, keys, payload, bag_count, offsets, err = torch.ops.mdl_hip.grouped_lookup(
+        tables, ids_dev, lens_dev, [t for t, _ in feats], [code[p] for _, p in feats], [1] * 4, [0] * 4, True)
+    grads = _grads(rng, outs)
+    rows_all, vbuf, counts = torch.ops.mdl_hip.grouped_lookup_backward(
+        tables, ids_dev, lens_dev, [t for t, _ in feats], [code[p] for _, p in feats], [1] * 4, [0] * 4, grads,
+        keys, payload, bag_count, offsets)
+    torch.cuda.synchronize()
+    assert int(err.item()) == 0
+    say("key_groups", "op done", f"{time.time() - t0:.1f}s")
+    cap = [0, 0, 0]
+    for (t, _), x in zip(feats, ids):
+        cap[t] += x.size
+    rows, values = ops.split_coalesced(tables, rows_all, vbuf, ops.coalesced_layout(tables, cap))
+    ref = _oracle_grads(feats, ids, lens, grads, touched, snap, outs, "op")
+    counts = counts.cpu().numpy()
+    for t, (rr, g, s) in enumerate(ref):
+        u = int(counts[t])
+        assert u == rr.size, f"op table {t}: {u} rows, oracle {rr.size}"
+        got_rows = rows[t].cpu().numpy()
+        assert np.array_equal(got_rows[:u], touched[t][rr]), f"op table {t}: rows"
+        got = values[t].float().cpu().numpy()
+        rtol = RTOL["fp32" if DTYPES[t] == torch.float32 else "bf16"]
+        assert_close(got[:u], g, rtol, 1e-6, s, f"op table {t} values")
+        # capacity padding: the last row again, zero values
+        assert (got_rows[u:] == got_rows[u - 1]).all() and not got[u:].any()
+    say("key_groups", "op checked", f"{time.time() - t0:.1f}s")
+
+
+def test_functional_backward_adagrad_clips_across_key_groups(device, big):
+    t0 = time.time()
+    tables, states = big
+    rng = np.random.default_rng(4502)
+    feats = [(0, "sum"), (1, "mean"), (1, "none"), (2, "mean")]
+    plan = _plan(tables, states, feats)
+    assert [(g.lo, g.hi) for g in plan.groups] == [(0, 1), (1, 4)]
+    ids, lens = _draw(rng, feats)
+    touched = _touched_of(feats, ids)
+    _set_touched(tables, touched, rng)
+    snap = _Snapshot.__new__(_Snapshot)
+    snap.idx = [torch.from_numpy(u).to(device) for u in touched]
+    snap.w = [w.index_select(0, i).float().cpu().numpy() for w, i in zip(tables, snap.idx)]
+    snap.a = [a.index_select(0, i).cpu().numpy() for a, i in zip(states, snap.idx)]
+    ids_dev = [torch.from_numpy(x).to(device) for x in ids]
+    lens_dev = [None if ln is None else torch.from_numpy(ln).to(device) for ln in lens]
+    res = ops.grouped_forward(plan, ids_dev, lens_dev, with_backward=True)
+    outs = res.outputs
+    grads = _grads(rng, outs)
+    ref = _oracle_grads(feats, ids, lens, grads, touched, snap, outs, "functional")
+    norm_ref = float(np.sqrt(sum(float((g * g).sum()) for _, g, _ in ref)))
+    clip = 0.3 * norm_ref
+    norm = ops.backward_adagrad(res, grads, lr=LR, eps=EPS, clip_norm=clip)
+    torch.cuda.synchronize()
+    say("key_groups", "functional step done", f"{time.time() - t0:.1f}s")
+    assert_close(norm.cpu().numpy(), np.array([norm_ref]), 1e-4, 0, what="clip norm")
+    coef = min(clip / (norm_ref + 1e-6), 1.0)
+    w_post, a_post = snap.after(tables, states)
+    for t, (rr, g, s) in enumerate(ref):
+        bf = DTYPES[t] == torch.bfloat16
+        _check_update(f"functional table {t}", w_post[t], a_post[t], snap.w[t], snap.a[t], rr, g * coef,
+                      s * coef + np.abs(g) * 1e-4, LR, EPS, RTOL["bf16" if bf else "fp32"], 1e-6 if bf else 1e-7, bf)
+    say("key_groups", "functional step checked", f"{time.time() - t0:.1f}s")
