@@ -861,6 +861,22 @@ def summarize_pmc(dirs, out_path, config, steps_run):
             "hbm_bytes_per_step": tot["FETCH_SIZE"] * 1024 * scale["FETCH_SIZE"]
             + tot["WRITE_SIZE"] * 1024 * scale["WRITE_SIZE"],
         }
+        # L2 counters of a further pass, when one was given: hit rate and
+        # the 128-byte line reads L2 sent to memory (TCC_EA0_RDREQ), of them
+        # those addressed to DRAM; rocprofv3 on gfx950 has no counter of the
+        # memory-side cache (MALL), so DRAM-addressed reads are an upper
+        # bound on the reads HBM served.
+        l2 = {}
+        for ctr in ("TCC_HIT_sum", "TCC_MISS_sum", "TCC_EA0_RDREQ_sum", "TCC_EA0_RDREQ_DRAM_sum"):
+            vals = [float(np.mean(v)) * len(v) / steps_run for n, v in per.get(ctr, {}).items()
+                    if any(p in n for p in pats)]
+            if vals:
+                l2[ctr + "_per_step"] = float(sum(vals))
+        if "TCC_HIT_sum_per_step" in l2 and "TCC_MISS_sum_per_step" in l2:
+            hm = l2["TCC_HIT_sum_per_step"] + l2["TCC_MISS_sum_per_step"]
+            l2["l2_hit_rate"] = l2["TCC_HIT_sum_per_step"] / hm if hm else None
+        if l2:
+            groups[g]["l2"] = l2
     res = {"config": config, "source_stamp": source_stamp(), "steps_run": steps_run, "copy_kernel": cname,
            "copy_bytes": COPY_BYTES,
            "copy_FETCH_KiB": f_kib,
