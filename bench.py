@@ -32,6 +32,7 @@ Workloads:
 from __future__ import annotations
 
 import argparse
+import gc
 import json
 import os
 import platform
@@ -1073,8 +1074,13 @@ def measure(name: str, args, torch, device, *, with_aux: bool = False) -> dict:
         # after every timed number above, so the extra steps change none of them
         out["aux"] = aux_measurements(torch, dev, wl, n_ids, args.steps, device, batches)
     del dev
+    # Tables held in reference cycles (autograd records, optimizer state of
+    # the drop-in loop) go now, before the next config allocates its own.
+    gc.collect()
     torch.cuda.synchronize()
     torch.cuda.empty_cache()
+    print(f"[bench] {wl.name}: done; {torch.cuda.memory_allocated(device) / 2**30:.1f} GiB still allocated",
+          file=sys.stderr, flush=True)
     out["_wl"] = wl
     out["_batch0"] = batches[0]
     return out
