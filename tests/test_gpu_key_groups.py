@@ -8,7 +8,9 @@ them and are checked against the CPU oracle on compact copies of the touched
 rows (rows above 2^31 of a table and keys above 2^31 of a group included):
 
 * ``SparseStep`` (bag lengths placed on the device, each group's keys placed
-  by its key origin), with the clip norm summed over both groups;
+  by its key origin), with the clip norm summed over both groups; its form
+  without pooled features (host-known origins); two accumulated
+  micro-batches;
 * the ``mdl_hip::grouped_lookup`` custom op and its backward (the drop-in's
   path), with a feature order that reads the first table again after the
   second, so the op must reorder its features by table;
@@ -16,7 +18,7 @@ rows (rows above 2^31 of a table and keys above 2^31 of a group included):
   the gradient of both groups by one coefficient.
 
 Untouched rows and accumulators of every table are checked bit for bit
-(checksums) after the SparseStep.
+(checksums) after every SparseStep.
 """
 
 import time
@@ -89,6 +91,26 @@ def _oracle_grads(feats, ids, lens, grads, touched, snap, outs, what):
     """Check every output; per table the coalesced gradient (rows in the
     compact numbering, fp64 sums) and the same sums over |terms|."""
 
+    return _coalesced(_oracle_parts(feats, ids, lens, grads, touched, snap, outs, what))
+
+
+def _coalesced(parts):
+    rows_t, vals_t, absv_t = parts
+    out = []
+    for t in range(len(ROWS)):
+        if not rows_t[t]:
+            out.append(None)
+            continue
+        rr, g = O.coalesce(np.concatenate(rows_t[t]), np.concatenate(vals_t[t]))
+        _, s = O.coalesce(np.concatenate(rows_t[t]), np.concatenate(absv_t[t]))
+        out.append((rr, g, s))
+    return out
+
+
+def _oracle_parts(feats, ids, lens, grads, touched, snap, outs, what):
+    """Check every output; per table the per-id gradients (compact rows,
+    fp64 values, |values|) of one batch."""
+
     T = len(ROWS)
     rows_t = [[] for _ in range(T)]
     vals_t = [[] for _ in range(T)]
@@ -111,15 +133,7 @@ def _oracle_grads(feats, ids, lens, grads, touched, snap, outs, what):
         rows_t[t].append(r)
         vals_t[t].append(v)
         absv_t[t].append(va)
-    out = []
-    for t in range(T):
-        if not rows_t[t]:
-            out.append(None)
-            continue
-        rr, g = O.coalesce(np.concatenate(rows_t[t]), np.concatenate(vals_t[t]))
-        _, s = O.coalesce(np.concatenate(rows_t[t]), np.concatenate(absv_t[t]))
-        out.append((rr, g, s))
-    return out
+    return rows_t, vals_t, absv_t
 
 
 def _touched_of(feats, ids):
@@ -183,6 +197,67 @@ def test_sparse_step_over_two_key_groups_matches_oracle(device, big):
     say("key_groups", "sparse step checked", f"{time.time() - t0:.1f}s")
     snap.restore_and_check(tables, states)
     say("key_groups", "untouched rows checked", f"{time.time() - t0:.1f}s")
+
+
+@pytest.mark.parametrize("case", ["unpooled", "micro_batches"])
+def test_sparse_step_forms_over_two_key_groups(device, big, case):
+    """SparseStep over the two key groups in its other forms: a layout
+    without pooled features (ids placed by host-known counts, each group's
+    origin and count uploaded once), and two micro-batches of a pooled layout
+    accumulated into one update."""
+
+    t0 = time.time()
+    tables, states = big
+    rng = np.random.default_rng(4510 if case == "unpooled" else 4511)
+    if case == "unpooled":
+        feats = [(0, "none"), (1, "none"), (2, "none")]
+        k = 1
+    else:
+        feats = [(0, "mean"), (1, "sum"), (2, "none")]
+        k = 2
+    plan = _plan(tables, states, feats)
+    assert [(g.lo, g.hi) for g in plan.groups] == [(0, 1), (1, 3)]
+    draws = [_draw(rng, feats) for _ in range(k)]
+    per = [[] for _ in ROWS]
+    for ids, _ in draws:
+        for (t, _), x in zip(feats, ids):
+            per[t].append(x)
+    touched = [_touched(xs) for xs in per]
+    _set_touched(tables, touched, rng)
+    snap = _Snapshot(tables, states, touched, device)
+    outs = [[torch.empty((B if ln is not None else x.size, DIMS[t]), dtype=DTYPES[t], device=device)
+             for (t, _), x, ln in zip(feats, ids, lens)] for ids, lens in draws]
+    grads = [_grads(rng, o) for o in outs]
+    packed = [torch.from_numpy(np.concatenate(ids)).to(device) for ids, _ in draws]
+    lengths = [None if case == "unpooled" else torch.from_numpy(np.concatenate(
+        [ln if ln is not None else np.array([x.size]) for x, ln in zip(ids, lens)]).astype(np.int64)).to(device)
+        for ids, lens in draws]
+    ids0, lens0 = draws[0]
+    st = SparseStep(plan, packed[0], lengths[0], [x.size for x in ids0], [0 if ln is None else B for ln in lens0],
+                    outs[0] if k == 1 else outs, grads[0] if k == 1 else grads,
+                    capacity=max(int(p.numel()) for p in packed), micro_batches=k)
+    assert len(st.groups) == 2
+    for m in range(k):
+        st.bind(packed[m], lengths[m])
+        st.forward(micro_batch=m)
+    st.sort()
+    st.apply(LR, EPS)
+    torch.cuda.synchronize()
+    assert int(st.error_count.item()) == 0
+    say("key_groups", case, "step done", f"{time.time() - t0:.1f}s")
+    w_post, a_post = snap.after(tables, states)
+    parts = [[] for _ in range(3)]
+    for m, (ids, lens) in enumerate(draws):
+        got = _oracle_parts(feats, ids, lens, grads[m], touched, snap, outs[m], f"{case} micro-batch {m}")
+        for j in range(3):
+            parts[j].append(got[j])
+    merged = tuple([sum((p[t] for p in parts[j]), []) for t in range(len(ROWS))] for j in range(3))
+    for t, (rr, g, s) in enumerate(_coalesced(merged)):
+        bf = DTYPES[t] == torch.bfloat16
+        _check_update(f"{case} table {t}", w_post[t], a_post[t], snap.w[t], snap.a[t], rr, g, s, LR, EPS,
+                      RTOL["bf16" if bf else "fp32"], 1e-6 if bf else 1e-7, bf)
+    snap.restore_and_check(tables, states)
+    say("key_groups", case, "checked", f"{time.time() - t0:.1f}s")
 
 
 def test_grouped_lookup_op_reorders_features_across_key_groups(device, big):
