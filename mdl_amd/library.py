@@ -33,6 +33,7 @@ read; ``grouped_rowwise_adagrad_`` reads ``counts`` on the device.
 from __future__ import annotations
 
 import weakref
+from collections import OrderedDict
 from typing import Optional
 
 import numpy as np
@@ -149,15 +150,41 @@ def _order(weights, table) -> Optional[list[int]]:
     return None if order == list(range(len(table))) else order
 
 
+# Layouts seen by the device ops, most recent last: what a plan of the same
+# weights (addresses, shapes, dtypes) and features derives on the host -- row
+# bases, feature specs and the memo of descriptor columns -- so a training
+# loop builds each layout's host arrays once.  Entries hold addresses and
+# sizes, never tensors: a freed table keeps nothing alive, and a new table
+# at the same address with the same shape and dtype is described the same.
+_LAYOUTS: "OrderedDict[tuple, dict]" = OrderedDict()
+_LAYOUTS_MAX = 16
+
+
 def _plan(weights, table, pooling, exclude, padding_idx) -> ops.GroupPlan:
-    plan = ops.GroupPlan()
-    for w in weights:
-        plan.add_table(w, None, shared=False)
-    for f in range(len(table)):
-        plan.features.append(ops.FeatureSpec(
-            table=int(table[f]), pooling=int(pooling[f]), exclude_null=bool(exclude[f]),
-            padding_idx=int(padding_idx[f]), out_dtype=weights[table[f]].dtype,
-        ))
+    key = (weights[0].device, tuple((w.data_ptr(), w.shape, w.dtype, w.stride(0)) for w in weights),
+           tuple(table), tuple(pooling), tuple(exclude), tuple(padding_idx))
+    entry = _LAYOUTS.get(key)
+    if entry is None:
+        plan = ops.GroupPlan()
+        for w in weights:
+            plan.add_table(w, None, shared=False)
+        for f in range(len(table)):
+            plan.features.append(ops.FeatureSpec(
+                table=int(table[f]), pooling=int(pooling[f]), exclude_null=bool(exclude[f]),
+                padding_idx=int(padding_idx[f]), out_dtype=weights[table[f]].dtype,
+            ))
+        entry = {"bases": [t.row_base for t in plan.tables], "total": plan.total_rows,
+                 "features": plan.features, "memo": {}}
+        _LAYOUTS[key] = entry
+        if len(_LAYOUTS) > _LAYOUTS_MAX:
+            _LAYOUTS.popitem(last=False)
+    else:
+        _LAYOUTS.move_to_end(key)
+        plan = ops.GroupPlan()
+        plan.tables = [ops.TableSpec(weight=w, state=None, row_base=b) for w, b in zip(weights, entry["bases"])]
+        plan.features = entry["features"]
+        plan.total_rows = entry["total"]
+    plan._memo = entry["memo"]
     return plan
 
 

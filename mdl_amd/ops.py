@@ -305,6 +305,10 @@ class GroupPlan:
         self.total_rows = 0
         self._groups: list[KeyGroup] | None = None
         self._groups_for: tuple[int, int] = (-1, -1)
+        # Host arrays derived from this layout alone (addresses, sizes and
+        # codes, no tensor references), shared by every plan of the same
+        # layout when the plan comes from ``memoized_plan``.
+        self._memo: dict | None = None
 
     def add_table(self, weight: Tensor, state: Tensor | None = None, *, shared: bool = True) -> int:
         key = weight.data_ptr()
@@ -483,6 +487,34 @@ class _UploadCache:
 _CACHE = _UploadCache()
 
 
+def _static_features(plan: GroupPlan) -> np.ndarray:
+    """The descriptor columns that depend on the layout alone (tables,
+    dims, dtypes, pooling, flags); the per-call columns are zero."""
+
+    specs = plan.features
+    nf = len(specs)
+    tab = [plan.tables[s.table] for s in specs]
+    feats = np.zeros(nf, dtype=FEATURE_DTYPE)
+    feats["weight"] = [t.weight.data_ptr() for t in tab]
+    feats["state"] = [t.state.data_ptr() if t.state is not None else 0 for t in tab]
+    feats["num_rows"] = [int(t.weight.size(0)) for t in tab]
+    feats["row_base"] = [t.row_base for t in tab]
+    feats["dim"] = [int(t.weight.size(1)) for t in tab]
+    feats["wdtype"] = [dtype_code(t.weight.dtype) for t in tab]
+    feats["odtype"] = [dtype_code(s.out_dtype) for s in specs]
+    feats["pooling"] = np.array([s.pooling for s in specs], dtype=np.int32)
+    feats["flags"] = [
+        (MDL_FLAG_EXCLUDE_NULL if s.exclude_null else 0) | (MDL_FLAG_ROWS_BY_POSITION if s.rows_by_position else 0)
+        for s in specs
+    ]
+    feats["padding_idx"] = [s.padding_idx for s in specs]
+    feats["table"] = [s.table for s in specs]
+    for s, t in zip(specs, tab):
+        if t.weight.dtype == torch.float32 and s.out_dtype != torch.float32:
+            raise TypeError("float32 tables produce float32 outputs")
+    return feats
+
+
 def build_features(
     plan: GroupPlan,
     id_counts: Sequence[int],
@@ -499,41 +531,28 @@ def build_features(
     """
 
     plan.groups  # row bases of a plan cut into key groups
-    specs = plan.features
-    nf = len(specs)
-    tab = [plan.tables[s.table] for s in specs]
-    pool = np.array([s.pooling for s in specs], dtype=np.int32)
-    pooled = pool != MDL_POOL_NONE
+    memo = plan._memo
+    static = memo.get("feats") if memo is not None else None
+    if static is None:
+        static = _static_features(plan)
+        if memo is not None:
+            memo["feats"] = static
+    nf = len(static)
+    pooled = static["pooling"] != MDL_POOL_NONE
     pooled_any = bool(pooled.any())
     ids = np.asarray(id_counts, dtype=np.int64)
     bags = np.where(pooled, np.asarray(bag_counts, dtype=np.int64), 0)
     rows_out = np.where(pooled, bags, ids)
     bag_slots = np.where(pooled, bags, 1 if pooled_any else 0)
-    feats = np.zeros(nf, dtype=FEATURE_DTYPE)
-    feats["weight"] = [t.weight.data_ptr() for t in tab]
-    feats["state"] = [t.state.data_ptr() if t.state is not None else 0 for t in tab]
+    feats = static.copy()
     feats["out"] = np.asarray(out_ptrs, dtype=np.uint64)
-    feats["num_rows"] = [int(t.weight.size(0)) for t in tab]
     feats["out_stride"] = np.asarray(out_strides, dtype=np.int64)
-    feats["row_base"] = [t.row_base for t in tab]
-    feats["payload_base"] = np.concatenate(([0], np.cumsum(rows_out)[:-1])) if nf else []
-    feats["ids_begin"] = np.concatenate(([0], np.cumsum(ids)[:-1])) if nf else []
+    if nf:
+        feats["payload_base"][1:] = np.cumsum(rows_out)[:-1]
+        feats["ids_begin"][1:] = np.cumsum(ids)[:-1]
+        feats["bag_base"][1:] = np.cumsum(bag_slots)[:-1]
     feats["num_ids"] = ids
-    feats["bag_base"] = np.concatenate(([0], np.cumsum(bag_slots)[:-1])) if nf else []
     feats["num_bags"] = bags
-    feats["dim"] = [int(t.weight.size(1)) for t in tab]
-    feats["wdtype"] = [dtype_code(t.weight.dtype) for t in tab]
-    feats["odtype"] = [dtype_code(s.out_dtype) for s in specs]
-    feats["pooling"] = pool
-    feats["flags"] = [
-        (MDL_FLAG_EXCLUDE_NULL if s.exclude_null else 0) | (MDL_FLAG_ROWS_BY_POSITION if s.rows_by_position else 0)
-        for s in specs
-    ]
-    feats["padding_idx"] = [s.padding_idx for s in specs]
-    feats["table"] = [s.table for s in specs]
-    for s, t in zip(specs, tab):
-        if t.weight.dtype == torch.float32 and s.out_dtype != torch.float32:
-            raise TypeError("float32 tables produce float32 outputs")
     if int(rows_out.sum()) >= 0xFFFFFFFF:
         raise ValueError("a grouped lookup supports fewer than 2^32 - 1 output rows")
     return feats
@@ -709,6 +728,18 @@ def lane_elems(dim: int, esize: int, vec: bool) -> int:
 def _tables_array(plan: GroupPlan, feats: np.ndarray) -> np.ndarray:
     if plan.total_rows >= KEY_SPACE:
         raise ValueError("tables of 2^32 - 1 rows or more are keyed per key group (GroupPlan.groups)")
+    memo = plan._memo
+    key = ("tables", feats["odtype"].tobytes())
+    if memo is not None and key in memo:
+        return memo[key]
+    tables = _build_tables_array(plan, feats)
+    if memo is not None:
+        tables.setflags(write=False)
+        memo[key] = tables
+    return tables
+
+
+def _build_tables_array(plan: GroupPlan, feats: np.ndarray) -> np.ndarray:
     plan.groups  # row bases
     tables = np.zeros(len(plan.tables), dtype=TABLE_DTYPE)
     users: dict[int, list[int]] = {}
@@ -1066,15 +1097,21 @@ def table_capacities(res: ForwardResult) -> np.ndarray:
     return cap
 
 
-def coalesced_layout(weights: Sequence[Tensor], cap: Sequence[int]) -> dict:
+def coalesced_layout(weights: Sequence[Tensor], cap: Sequence[int], memo: dict | None = None) -> dict:
     """Where capacity-sized coalesced gradients live in two flat buffers:
     rows of table t at ``rows_off[t]`` (int64 elements), values at byte
-    ``val_off[t]`` (each table's region 256-byte aligned)."""
+    ``val_off[t]`` (each table's region 256-byte aligned).  ``memo``: a
+    layout's memo holding its tables' element sizes and dims."""
 
     cap = np.asarray(cap, dtype=np.int64)
     T = len(weights)
-    esz = np.array([w.element_size() for w in weights], dtype=np.int64)
-    dims = np.array([int(w.size(1)) for w in weights], dtype=np.int64)
+    sizes = memo.get("esz_dims") if memo is not None else None
+    if sizes is None:
+        sizes = (np.array([w.element_size() for w in weights], dtype=np.int64),
+                 np.array([int(w.size(1)) for w in weights], dtype=np.int64))
+        if memo is not None:
+            memo["esz_dims"] = sizes
+    esz, dims = sizes
     nbytes = cap * dims * esz
     val_off = np.zeros(T + 1, dtype=np.int64)
     np.cumsum((nbytes + 255) // 256 * 256, out=val_off[1:])
@@ -1116,7 +1153,7 @@ def backward_coalesce_padded(
     T = len(plan.tables)
     stream = _stream(device)
     cap = table_capacities(res)
-    layout = coalesced_layout([t.weight for t in plan.tables], cap)
+    layout = coalesced_layout([t.weight for t in plan.tables], cap, memo=plan._memo)
     rows_off, val_off = layout["rows_off"], layout["val_off"]
     rows_all = torch.empty(max(int(rows_off[-1]), 1), dtype=torch.int64, device=device)
     vbuf = torch.empty(max(int(val_off[-1]), 1), dtype=torch.uint8, device=device)
@@ -1207,9 +1244,9 @@ def grouped_rowwise_adagrad_(
     if not weights:
         return
     device = weights[0].device
-    keep = []
-    wptr, sptr, rptr, vptr, cptr, nrows, caps, wstr, vstr, dims, wdt, vdt = ([] for _ in range(12))
-    for w, a, r, v, c in zip(weights, accumulators, rows, values, counts):
+    rows = list(rows)
+    values = list(values)
+    for i, (w, a, r, v) in enumerate(zip(weights, accumulators, rows, values)):
         if w.device.type != "cuda":
             _require_device(w, "weight")
         if w.ndim != 2 or w.stride(1) != 1:
@@ -1217,37 +1254,26 @@ def grouped_rowwise_adagrad_(
         if a.dtype != torch.float32 or not a.is_contiguous():
             raise TypeError("row-wise Adagrad accumulator must be a contiguous float32 tensor")
         if r.dtype != torch.int64 or not r.is_contiguous():
-            r = r.to(torch.int64).contiguous()
+            rows[i] = r.to(torch.int64).contiguous()
         if (w.dtype == torch.float32 and v.dtype != torch.float32) or v.dtype not in (torch.float32, torch.bfloat16):
-            v = v.float()
+            v = values[i] = v.float()
         if not v.is_contiguous() or v.data_ptr() % 16:
-            v = _row_major_aligned(v)
-        keep += [r, v]
-        wptr.append(w.data_ptr())
-        sptr.append(a.data_ptr())
-        rptr.append(r.data_ptr())
-        vptr.append(v.data_ptr())
-        cptr.append(0 if c is None else c.data_ptr())
-        nrows.append(w.size(0))
-        caps.append(r.numel())
-        wstr.append(w.stride(0))
-        vstr.append(v.stride(0) if v.ndim == 2 and v.size(0) else w.size(1))
-        dims.append(w.size(1))
-        wdt.append(dtype_code(w.dtype))
-        vdt.append(dtype_code(v.dtype))
+            values[i] = _row_major_aligned(v)
+    keep = rows + values
     ups = np.zeros(len(weights), dtype=_lib.UPDATE_DTYPE)
-    ups["weight"] = wptr
-    ups["state"] = sptr
-    ups["rows"] = rptr
-    ups["values"] = vptr
-    ups["count"] = cptr
-    ups["num_rows"] = nrows
-    ups["capacity"] = caps
-    ups["weight_stride"] = wstr
-    ups["values_stride"] = vstr
-    ups["dim"] = dims
-    ups["wdtype"] = wdt
-    ups["vdtype"] = vdt
+    ups["weight"] = [w.data_ptr() for w in weights]
+    ups["state"] = [a.data_ptr() for a in accumulators]
+    ups["rows"] = [r.data_ptr() for r in rows]
+    ups["values"] = [v.data_ptr() for v in values]
+    ups["count"] = [0 if c is None else c.data_ptr() for c in counts]
+    shapes = [w.shape for w in weights]
+    ups["num_rows"] = [sh[0] for sh in shapes]
+    ups["dim"] = [sh[1] for sh in shapes]
+    ups["capacity"] = [r.numel() for r in rows]
+    ups["weight_stride"] = [w.stride(0) for w in weights]
+    ups["values_stride"] = [v.stride(0) if v.ndim == 2 and v.size(0) else sh[1] for v, sh in zip(values, shapes)]
+    ups["wdtype"] = [dtype_code(w.dtype) for w in weights]
+    ups["vdtype"] = [dtype_code(v.dtype) for v in values]
     ups["lr"] = np.asarray(lrs, dtype=np.float32)
     units = (ups["capacity"] + _lib.MDL_UPDATE_UNIT - 1) // _lib.MDL_UPDATE_UNIT
     ups["unit_first"][1:] = np.cumsum(units)[:-1]
