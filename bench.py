@@ -509,7 +509,8 @@ def aux_measurements(torch, dev, wl, n_ids: float, steps: int, device, batches=N
       src/benchmark.py:1246-1250) of one step's worth of raw int64 ids, HIP
       events around 20 back-to-back launches queued behind a spin kernel, so
       the host's launch time does not show; 16 algorithmic bytes per id
-      (read 8, write 8).
+      (read 8, write 8);
+    * list features to CSR bags (mdl_bag_truncate), timed the same way.
     """
 
     from mdl_amd import ops
@@ -549,6 +550,44 @@ def aux_measurements(torch, dev, wl, n_ids: float, steps: int, device, batches=N
             "achieved_gbps": nbytes / (ms * 1e-3) / 1e9, "frac": nbytes / (ms * 1e-3) / 1e9 / PEAK_HBM_GBPS,
         }
     del raw
+    # list features to CSR bags on the device (mdl_bag_truncate: the Arrow
+    # truncation, flatten and pre_hashed bucketing of src/dataloader.py:
+    # 8565-8665 and :8463-8493): the workload's bag features as raw lists of
+    # up to 48 ids per row, the last 32 kept.  Algorithmic bytes: list offsets
+    # read, kept raw ids read, capacity-sized ids written (zeros past the
+    # kept total), lengths and kept offsets written.
+    bag_rows = sum(wl.batch for f in wl.features if f.pooling != "none")
+    if bag_rows:
+        rng = np.random.default_rng(11)
+        lengths = rng.integers(1, 49, size=bag_rows)
+        offsets_h = np.zeros(bag_rows + 1, dtype=np.int64)
+        np.cumsum(lengths, out=offsets_h[1:])
+        n_in = int(offsets_h[-1])
+        raw = torch.randint(1, 1 << 62, (n_in,), dtype=torch.int64, device=device, generator=gen)
+        offsets = torch.from_numpy(offsets_h).to(device)
+        kept = int(np.minimum(lengths, 32).sum())
+        call = lambda: ops.bag_truncate(raw, offsets, max_length=32, truncation="tail",  # noqa: E731
+                                        bucket="pre_hashed", num_buckets=1 << 20, validate_nonzero=False)
+        for _ in range(3):
+            call()
+        torch.cuda.synchronize()
+        e0 = torch.cuda.Event(enable_timing=True)
+        e1 = torch.cuda.Event(enable_timing=True)
+        torch.cuda._sleep(20_000_000)
+        e0.record()
+        for _ in range(reps):
+            call()
+        e1.record()
+        torch.cuda.synchronize()
+        ms = e0.elapsed_time(e1) / reps
+        nbytes = 8.0 * (bag_rows + 1) + 8.0 * kept + 8.0 * n_in + 8.0 * bag_rows + 8.0 * (bag_rows + 1)
+        out["bag_truncate"] = {
+            "rows": bag_rows, "ids_in": n_in, "ids_kept": kept, "ms": ms, "alg_bytes": nbytes,
+            "achieved_gbps": nbytes / (ms * 1e-3) / 1e9, "frac": nbytes / (ms * 1e-3) / 1e9 / PEAK_HBM_GBPS,
+            "what": "mdl_bag_truncate: tail-truncate to 32, flatten, pre_hashed bucketing (2^20), one call "
+                    "(three launches: kept counts, offsets scan, gather)",
+        }
+        del raw, offsets
     # the stand-alone row-wise Adagrad (fused_rowwise_adagrad_update,
     # src/optim.py:68-108) on 1 M unique rows of the largest table: a weight
     # row read and written, its gradient row read, 8-byte row index and 4-byte

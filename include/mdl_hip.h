@@ -58,7 +58,8 @@ enum { MDL_FLAG_EXCLUDE_NULL = 1, MDL_FLAG_ROWS_BY_POSITION = 2, MDL_FLAG_IDS_FR
  * encoder of src/model.py:3782-3890 serves any batch).  Forward chunks of an
  * unpooled feature past its range this call do nothing. */
 
-enum { MDL_BUCKET_PRE_HASHED = 0, MDL_BUCKET_MOD = 1 };
+enum { MDL_BUCKET_PRE_HASHED = 0, MDL_BUCKET_MOD = 1, MDL_BUCKET_NONE = 2 };
+enum { MDL_TRUNCATE_HEAD = 0, MDL_TRUNCATE_TAIL = 1 };
 
 /* Row-access classes of a feature or table: weight dtype x output/gradient
  * dtype x whether every row access is 16-byte aligned.  Kernels are
@@ -168,6 +169,39 @@ int32_t mdl_abi_version(void);
 int mdl_bucketize(const int64_t* raw, const uint8_t* valid, int64_t n,
                   int64_t num_buckets, int32_t mode, int32_t validate_nonzero,
                   int64_t* out, int32_t* error_count, void* stream);
+
+/*
+ * List features to CSR bags: truncation, flattening and bucketing in one
+ * call.  Replaces the Arrow path of src/dataloader.py:8565-8665
+ * (_list_truncate_array: head keeps a row's first max_length elements, tail
+ * its last; pc.list_value_length with nulls as 0; pc.list_flatten) followed
+ * by the bucketing of src/dataloader.py:8463-8493 (see mdl_bucketize).
+ *   in_offsets [rows+1]: row r holds raw[in_offsets[r] .. in_offsets[r+1])
+ *                        (Arrow list offsets; any base);
+ *   row_valid  [rows]  : 0 = null row, length 0 (may be NULL: all present);
+ *   raw, elem_valid [n_in]: element values and validity (elem_valid may be
+ *                        NULL); a null element keeps its slot and buckets to 0;
+ *   max_length < 0     : no truncation; truncation MDL_TRUNCATE_HEAD / _TAIL;
+ *   bucket_mode        : MDL_BUCKET_PRE_HASHED / MDL_BUCKET_MOD as in
+ *                        mdl_bucketize, or MDL_BUCKET_NONE (values copied,
+ *                        nulls 0; num_buckets unused).
+ * Writes lengths [rows] (the kept counts), out_offsets [rows+1] (their
+ * exclusive scan; the kept total is out_offsets[rows], in device memory) and
+ * values[j] for j < values_capacity: the bucketed kept elements in row order,
+ * zeros past the total (values_capacity = n_in always suffices; a smaller one
+ * keeps the first values_capacity).  Row offsets outside [0, n_in] or
+ * decreasing are clamped and counted in *error_count, as are non-null zeros
+ * under pre_hashed with validate_nonzero (error_count may be NULL).
+ * Nothing is read back to the host.
+ */
+size_t mdl_bag_truncate_workspace_bytes(int64_t rows);
+int mdl_bag_truncate(const int64_t* in_offsets, const uint8_t* row_valid, int64_t rows,
+                     const int64_t* raw, const uint8_t* elem_valid, int64_t n_in,
+                     int64_t max_length, int32_t truncation, int32_t bucket_mode,
+                     int64_t num_buckets, int32_t validate_nonzero, int64_t* lengths,
+                     int64_t* out_offsets, int64_t* values, int64_t values_capacity,
+                     int32_t* error_count, void* workspace, size_t workspace_bytes,
+                     void* stream);
 
 /* --------------------------------------------------------------- offsets --- */
 

@@ -29,6 +29,9 @@ MDL_CLASSES_UNSUPPORTED = 0x80000000
 ABI_VERSION = 5
 MDL_BUCKET_PRE_HASHED = 0
 MDL_BUCKET_MOD = 1
+MDL_BUCKET_NONE = 2
+MDL_TRUNCATE_HEAD = 0
+MDL_TRUNCATE_TAIL = 1
 MDL_SEQ_OLDEST_TO_NEWEST = 0
 MDL_SEQ_NEWEST_TO_OLDEST = 1
 
@@ -108,6 +111,11 @@ SIGNATURES: dict[str, tuple] = {
     "mdl_last_error": (ctypes.c_char_p, []),
     "mdl_abi_version": (_I32, []),
     "mdl_bucketize": (_I32, [_P, _P, _I64, _I64, _I32, _I32, _P, _P, _P]),
+    "mdl_bag_truncate_workspace_bytes": (_SZ, [_I64]),
+    "mdl_bag_truncate": (
+        _I32,
+        [_P, _P, _I64, _P, _P, _I64, _I64, _I32, _I32, _I64, _I32, _P, _P, _P, _I64, _P, _P, _SZ, _P],
+    ),
     "mdl_offsets_workspace_bytes": (_SZ, [_I64]),
     "mdl_lengths_to_offsets": (_I32, [_P, _I64, _P, _P, _SZ, _P]),
     "mdl_plan_chunks": (_I64, [_P, _I32, _I32, _P, _I64]),

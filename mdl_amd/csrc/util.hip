@@ -21,7 +21,35 @@ int check_hip(hipError_t err, const char* what) {
 
 // ------------------------------------------------------------ bucketing --
 
-// mod_magic = ceil(2^64 / m) for the mod rule's m = num_buckets - 1 >= 2.
+// Bucket of one raw value (0 for a null).  mod_magic = ceil(2^64 / m) for
+// the mod rule's m = num_buckets - 1 >= 2.
+__device__ __forceinline__ int64_t bucket_of(int64_t v, bool present, int64_t num_buckets, int32_t mode,
+                                             int32_t validate_nonzero, uint64_t mod_magic, int& bad) {
+  if (!present) return 0;
+  if (mode == MDL_BUCKET_NONE) return v;
+  if (mode == MDL_BUCKET_PRE_HASHED) {
+    // Unsigned low bits of the signed hash: identical to the signed modulo
+    // for a power-of-two bucket count, INT64_MIN included.
+    bad += (validate_nonzero && v == 0);
+    return (int64_t)(((uint64_t)v & (uint64_t)(num_buckets - 1)) + 1u);
+  }
+  // 1 + floormod(v - 1, m) without forming v - 1 or dividing: the sign goes
+  // first (x = v or ~v = -v - 1, both below 2^63, INT64_MIN included), and
+  // mulhi(x, ceil(2^64 / m)) is floor(x / m) or one more, which one add of m
+  // corrects.
+  const uint64_t m = (uint64_t)(num_buckets - 1);
+  uint64_t fm1 = 0;  // floormod(v - 1, m)
+  if (m > 1) {
+    const bool neg = v < 0;
+    const uint64_t x = neg ? ~(uint64_t)v : (uint64_t)v;
+    uint64_t rem = x - __umul64hi(x, mod_magic) * m;
+    if ((int64_t)rem < 0) rem += m;
+    const uint64_t fm = neg ? m - 1 - rem : rem;  // floormod(v, m)
+    fm1 = fm == 0 ? m - 1 : fm - 1;
+  }
+  return (int64_t)(1 + fm1);
+}
+
 __global__ void bucketize_kernel(const int64_t* __restrict__ raw, const uint8_t* __restrict__ valid,
                                  int64_t n, int64_t num_buckets, int32_t mode,
                                  int32_t validate_nonzero, int64_t* __restrict__ out,
@@ -30,35 +58,105 @@ __global__ void bucketize_kernel(const int64_t* __restrict__ raw, const uint8_t*
   const int64_t stride = (int64_t)gridDim.x * blockDim.x;
   int bad = 0;
   for (; i < n; i += stride) {
-    const int64_t v = raw[i];
     const bool present = valid == nullptr || valid[i] != 0;
-    int64_t r = 0;
-    if (present) {
-      if (mode == MDL_BUCKET_PRE_HASHED) {
-        // Unsigned low bits of the signed hash: identical to the signed
-        // modulo for a power-of-two bucket count, INT64_MIN included.
-        r = (int64_t)(((uint64_t)v & (uint64_t)(num_buckets - 1)) + 1u);
-        bad += (validate_nonzero && v == 0);
-      } else {
-        // 1 + floormod(v - 1, m) without forming v - 1 or dividing: the sign
-        // goes first (x = v or ~v = -v - 1, both below 2^63, INT64_MIN
-        // included), and mulhi(x, ceil(2^64 / m)) is floor(x / m) or one
-        // more, which one add of m corrects.
-        const uint64_t m = (uint64_t)(num_buckets - 1);
-        uint64_t fm1 = 0;  // floormod(v - 1, m)
-        if (m > 1) {
-          const bool neg = v < 0;
-          const uint64_t x = neg ? ~(uint64_t)v : (uint64_t)v;
-          uint64_t rem = x - __umul64hi(x, mod_magic) * m;
-          if ((int64_t)rem < 0) rem += m;
-          const uint64_t fm = neg ? m - 1 - rem : rem;  // floormod(v, m)
-          fm1 = fm == 0 ? m - 1 : fm - 1;
-        }
-        r = (int64_t)(1 + fm1);
-      }
-    }
-    out[i] = r;
+    out[i] = bucket_of(raw[i], present, num_buckets, mode, validate_nonzero, mod_magic, bad);
   }
+  if (error_count != nullptr && bad) atomicAdd(error_count, bad);
+}
+
+static uint64_t mod_magic_for(int32_t mode, int64_t num_buckets) {
+  const uint64_t m = (uint64_t)(num_buckets - 1);
+  return mode == MDL_BUCKET_MOD && m > 1 ? UINT64_MAX / m + 1 : 0;  // ceil(2^64 / m)
+}
+
+static int validate_bucket_mode(const char* who, int32_t mode, int64_t num_buckets) {
+  if (mode == MDL_BUCKET_PRE_HASHED) {
+    if (num_buckets <= 0 || (num_buckets & (num_buckets - 1)) != 0)
+      return fail(MDL_ERR_INVALID, "pre_hashed num_buckets must be a positive power of two");
+  } else if (mode == MDL_BUCKET_MOD) {
+    if (num_buckets <= 1) return fail(MDL_ERR_INVALID, "mod bucketing needs num_buckets > 1");
+  } else {
+    return fail(MDL_ERR_INVALID, std::string(who) + ": unknown bucketing mode");
+  }
+  return MDL_OK;
+}
+
+// ------------------------------------------------------ list truncation --
+
+// Kept count and first kept element of every row.  Offsets outside [0, n_in]
+// or decreasing are clamped (and counted); a null row keeps nothing.
+__global__ void bag_take_kernel(const int64_t* __restrict__ in_offsets, const uint8_t* __restrict__ row_valid,
+                                int64_t rows, int64_t n_in, int64_t max_length, int32_t truncation,
+                                int64_t* __restrict__ lengths, int64_t* __restrict__ starts,
+                                int32_t* __restrict__ error_count) {
+  const int64_t r = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (r >= rows) return;
+  int64_t lo = in_offsets[r], hi = in_offsets[r + 1];
+  int bad = 0;
+  if (lo < 0 || lo > n_in) {
+    lo = lo < 0 ? 0 : n_in;
+    bad = 1;
+  }
+  if (hi < lo || hi > n_in) {
+    hi = hi < lo ? lo : n_in;
+    bad = 1;
+  }
+  int64_t len = hi - lo;
+  if (row_valid != nullptr && row_valid[r] == 0) len = 0;
+  const int64_t take = max_length >= 0 && len > max_length ? max_length : len;
+  lengths[r] = take;
+  starts[r] = truncation == MDL_TRUNCATE_HEAD ? lo : hi - take;
+  if (bad && error_count != nullptr) atomicAdd(error_count, 1);
+}
+
+// The row holding kept entry j: the last r in [lo, hi] with off[r] <= j.
+__device__ __forceinline__ int64_t row_of(const int64_t* off, int64_t lo, int64_t hi, int64_t j) {
+  while (lo < hi) {
+    const int64_t mid = (lo + hi + 1) >> 1;
+    if (off[mid] <= j) lo = mid;
+    else hi = mid - 1;
+  }
+  return lo;
+}
+
+constexpr int kGatherThreads = 256;  // rows per block pass, one thread each to stage them
+
+// Each block pass takes 256 consecutive rows: it stages their kept offsets
+// and first source elements in LDS (coalesced), then walks their kept
+// entries -- one contiguous stretch of the output -- 256 at a time, each
+// thread finding its row by a search in LDS.  The grid then zeroes the
+// entries past the kept total.
+__global__ __launch_bounds__(kGatherThreads) void bag_gather_kernel(
+    const int64_t* __restrict__ out_offsets, const int64_t* __restrict__ starts, int64_t rows,
+    const int64_t* __restrict__ raw, const uint8_t* __restrict__ elem_valid, int64_t num_buckets, int32_t mode,
+    int32_t validate_nonzero, uint64_t mod_magic, int64_t* __restrict__ values, int64_t capacity,
+    int32_t* __restrict__ error_count) {
+  __shared__ int64_t s_off[kGatherThreads + 1];
+  __shared__ int64_t s_start[kGatherThreads];
+  const int tid = threadIdx.x;
+  int bad = 0;
+  for (int64_t r0 = (int64_t)blockIdx.x * kGatherThreads; r0 < rows; r0 += (int64_t)gridDim.x * kGatherThreads) {
+    const int nr = rows - r0 < kGatherThreads ? (int)(rows - r0) : kGatherThreads;
+    if (tid < nr) {
+      s_off[tid] = out_offsets[r0 + tid];
+      s_start[tid] = starts[r0 + tid];
+    }
+    if (tid == 0) s_off[nr] = out_offsets[r0 + nr];
+    __syncthreads();
+    const int64_t b = s_off[0];
+    const int64_t e = s_off[nr] < capacity ? s_off[nr] : capacity;
+    for (int64_t j = b + tid; j < e; j += kGatherThreads) {
+      const int64_t r = row_of(s_off, 0, nr - 1, j);
+      const int64_t src = s_start[r] + (j - s_off[r]);
+      const bool present = elem_valid == nullptr || elem_valid[src] != 0;
+      values[j] = bucket_of(raw[src], present, num_buckets, mode, validate_nonzero, mod_magic, bad);
+    }
+    __syncthreads();  // the next pass restages the LDS
+  }
+  const int64_t total = out_offsets[rows];
+  for (int64_t j = total + (int64_t)blockIdx.x * kGatherThreads + tid; j < capacity;
+       j += (int64_t)gridDim.x * kGatherThreads)
+    values[j] = 0;
   if (error_count != nullptr && bad) atomicAdd(error_count, bad);
 }
 
@@ -167,23 +265,61 @@ int mdl_bucketize(const int64_t* raw, const uint8_t* valid, int64_t n, int64_t n
                   int32_t mode, int32_t validate_nonzero, int64_t* out, int32_t* error_count,
                   void* stream) {
   if (n < 0) return fail(MDL_ERR_INVALID, "mdl_bucketize: negative n");
-  if (mode == MDL_BUCKET_PRE_HASHED) {
-    if (num_buckets <= 0 || (num_buckets & (num_buckets - 1)) != 0)
-      return fail(MDL_ERR_INVALID, "pre_hashed num_buckets must be a positive power of two");
-  } else if (mode == MDL_BUCKET_MOD) {
-    if (num_buckets <= 1) return fail(MDL_ERR_INVALID, "mod bucketing needs num_buckets > 1");
-  } else {
-    return fail(MDL_ERR_INVALID, "mdl_bucketize: unknown mode");
-  }
+  int rc = validate_bucket_mode("mdl_bucketize", mode, num_buckets);
+  if (rc) return rc;
   if (n == 0) return MDL_OK;
   if (raw == nullptr || out == nullptr) return fail(MDL_ERR_INVALID, "mdl_bucketize: null pointer");
   int64_t blocks = (n + 255) / 256;
   if (blocks > 65536) blocks = 65536;
-  const uint64_t m = (uint64_t)(num_buckets - 1);
-  const uint64_t mod_magic = mode == MDL_BUCKET_MOD && m > 1 ? UINT64_MAX / m + 1 : 0;  // ceil(2^64 / m)
   hipLaunchKernelGGL(bucketize_kernel, dim3((unsigned)blocks), dim3(256), 0, as_stream(stream), raw,
-                     valid, n, num_buckets, mode, validate_nonzero, out, error_count, mod_magic);
+                     valid, n, num_buckets, mode, validate_nonzero, out, error_count,
+                     mod_magic_for(mode, num_buckets));
   MDL_CHECK_LAUNCH("bucketize_kernel");
+  return MDL_OK;
+}
+
+size_t mdl_bag_truncate_workspace_bytes(int64_t rows) {
+  const size_t scan = (mdl_offsets_workspace_bytes(rows) + 255) & ~size_t(255);
+  return scan + (size_t)(rows > 0 ? rows : 1) * sizeof(int64_t);
+}
+
+int mdl_bag_truncate(const int64_t* in_offsets, const uint8_t* row_valid, int64_t rows, const int64_t* raw,
+                     const uint8_t* elem_valid, int64_t n_in, int64_t max_length, int32_t truncation,
+                     int32_t bucket_mode, int64_t num_buckets, int32_t validate_nonzero, int64_t* lengths,
+                     int64_t* out_offsets, int64_t* values, int64_t values_capacity, int32_t* error_count,
+                     void* workspace, size_t workspace_bytes, void* stream) {
+  if (rows < 0 || n_in < 0 || values_capacity < 0)
+    return fail(MDL_ERR_INVALID, "mdl_bag_truncate: negative count");
+  if (truncation != MDL_TRUNCATE_HEAD && truncation != MDL_TRUNCATE_TAIL)
+    return fail(MDL_ERR_INVALID, "mdl_bag_truncate: truncation must be head or tail");
+  if (bucket_mode != MDL_BUCKET_NONE) {
+    int rc = validate_bucket_mode("mdl_bag_truncate", bucket_mode, num_buckets);
+    if (rc) return rc;
+  }
+  if (out_offsets == nullptr || (rows > 0 && (in_offsets == nullptr || lengths == nullptr)) ||
+      (values_capacity > 0 && values == nullptr) || (values_capacity > 0 && n_in > 0 && raw == nullptr))
+    return fail(MDL_ERR_INVALID, "mdl_bag_truncate: null pointer");
+  if (workspace_bytes < mdl_bag_truncate_workspace_bytes(rows) || workspace == nullptr)
+    return fail(MDL_ERR_WORKSPACE, "mdl_bag_truncate: workspace too small");
+  hipStream_t s = as_stream(stream);
+  const size_t scan_bytes = (mdl_offsets_workspace_bytes(rows) + 255) & ~size_t(255);
+  int64_t* starts = reinterpret_cast<int64_t*>(static_cast<char*>(workspace) + scan_bytes);
+  if (rows > 0) {
+    hipLaunchKernelGGL(bag_take_kernel, dim3((unsigned)((rows + 255) / 256)), dim3(256), 0, s, in_offsets,
+                       row_valid, rows, n_in, max_length, truncation, lengths, starts, error_count);
+    MDL_CHECK_LAUNCH("bag_take_kernel");
+  }
+  int rc = mdl_lengths_to_offsets(lengths, rows, out_offsets, workspace, scan_bytes, stream);
+  if (rc) return rc;
+  if (values_capacity == 0) return MDL_OK;
+  int64_t blocks = (rows + kGatherThreads - 1) / kGatherThreads;
+  if (blocks < 256) blocks = 256;  // the zero fill past the kept total needs a grid of its own size
+  if (blocks > 65536) blocks = 65536;
+  hipLaunchKernelGGL(bag_gather_kernel, dim3((unsigned)blocks), dim3(kGatherThreads), 0, s, out_offsets, starts,
+                     rows, raw,
+                     elem_valid, num_buckets, bucket_mode, validate_nonzero, mod_magic_for(bucket_mode, num_buckets),
+                     values, values_capacity, error_count);
+  MDL_CHECK_LAUNCH("bag_gather_kernel");
   return MDL_OK;
 }
 

@@ -94,6 +94,78 @@ def _bucketize_fake(raw, valid, num_buckets, mode, validate_nonzero):
     return torch.empty_like(raw), raw.new_empty(1, dtype=torch.int32)
 
 
+def _bucket_values_cpu(raw: Tensor, present: Tensor, num_buckets: int, mode: str,
+                       validate_nonzero: bool) -> tuple[Tensor, int]:
+    """Ids of raw values (0 for nulls) and the count of non-null zeros under
+    a validated pre_hashed rule."""
+
+    if mode == "none":
+        return torch.where(present, raw, 0), 0
+    out, err = _bucketize_cpu(raw, present.to(torch.uint8), num_buckets, mode, validate_nonzero)
+    return out, int(err[0])
+
+
+@torch.library.custom_op("mdl_hip::bag_truncate", mutates_args=(), device_types=_CUDA)
+def bag_truncate(values: Tensor, offsets: Tensor, valid: Optional[Tensor], row_valid: Optional[Tensor],
+                 max_length: int, truncation: str, bucket: str, num_buckets: int,
+                 validate_nonzero: bool) -> tuple[Tensor, Tensor, Tensor, Tensor]:
+    """List feature -> CSR bag: ``(ids [n_in], lengths [rows], offsets
+    [rows+1], error count [1])``; ids past the kept total (``offsets[-1]``)
+    are 0.  ``max_length < 0``: no truncation.  The error count adds rows
+    whose offsets fall outside the values (clamped) and non-null zeros under
+    a validated pre_hashed rule."""
+
+    err = torch.zeros(1, dtype=torch.int32, device=values.device)
+    ids, lengths, out_offsets = ops.bag_truncate(
+        values, offsets, valid=valid, row_valid=row_valid, max_length=None if max_length < 0 else max_length,
+        truncation=truncation, bucket=bucket, num_buckets=num_buckets, validate_nonzero=validate_nonzero,
+        error_count=err)
+    return ids, lengths, out_offsets, err
+
+
+@bag_truncate.register_kernel("cpu")
+def _bag_truncate_cpu(values, offsets, valid, row_valid, max_length, truncation, bucket, num_buckets,
+                      validate_nonzero):
+    if values.dtype != torch.int64 or offsets.dtype != torch.int64:
+        raise TypeError("list values and offsets must be torch.int64")
+    if truncation not in ops.TRUNCATIONS:
+        raise ValueError(f"unsupported list truncation {truncation!r}")
+    if bucket not in ops.BUCKET_MODES:
+        raise ValueError(f"bucket must be one of {sorted(ops.BUCKET_MODES)}")
+    n_in = int(values.numel())
+    rows = int(offsets.numel()) - 1
+    if rows < 0:
+        raise ValueError("list offsets need at least one entry")
+    lo_raw, hi_raw = offsets[:-1], offsets[1:]
+    lo = lo_raw.clamp(0, n_in)
+    hi = torch.maximum(hi_raw.clamp(max=n_in), lo)
+    bad = int(((lo_raw < 0) | (lo_raw > n_in) | (hi_raw < lo) | (hi_raw > n_in)).sum())
+    length = hi - lo
+    if row_valid is not None:
+        length = torch.where(row_valid != 0, length, 0)
+    take = length if max_length < 0 else length.clamp(max=max_length)
+    starts = lo if truncation == "head" else hi - take
+    total = int(take.sum())
+    row_ids = torch.repeat_interleave(torch.arange(rows), take)
+    within = torch.arange(total) - torch.repeat_interleave(torch.cumsum(take, 0) - take, take)
+    src = starts[row_ids] + within
+    present = valid[src] != 0 if valid is not None else torch.ones(total, dtype=torch.bool)
+    kept, zeros = _bucket_values_cpu(values[src], present, num_buckets, bucket, validate_nonzero)
+    ids = torch.zeros(n_in, dtype=torch.int64)
+    ids[:total] = kept
+    out_offsets = torch.zeros(rows + 1, dtype=torch.int64)
+    torch.cumsum(take, 0, out=out_offsets[1:])
+    return ids, take.clone(), out_offsets, torch.tensor([bad + zeros], dtype=torch.int32)
+
+
+@bag_truncate.register_fake
+def _bag_truncate_fake(values, offsets, valid, row_valid, max_length, truncation, bucket, num_buckets,
+                       validate_nonzero):
+    rows = offsets.size(0) - 1
+    return (values.new_empty(values.size(0), dtype=torch.int64), offsets.new_empty(rows, dtype=torch.int64),
+            offsets.new_empty(rows + 1, dtype=torch.int64), values.new_empty(1, dtype=torch.int32))
+
+
 @torch.library.custom_op("mdl_hip::lengths_to_offsets", mutates_args=(), device_types=_CUDA)
 def lengths_to_offsets(lengths: Tensor) -> Tensor:
     return ops.lengths_to_offsets(lengths)

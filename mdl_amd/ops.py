@@ -147,6 +147,73 @@ def bucketize(
     return out
 
 
+BUCKET_MODES = {"none": _lib.MDL_BUCKET_NONE, "pre_hashed": _lib.MDL_BUCKET_PRE_HASHED, "mod": _lib.MDL_BUCKET_MOD}
+TRUNCATIONS = {"head": _lib.MDL_TRUNCATE_HEAD, "tail": _lib.MDL_TRUNCATE_TAIL}
+
+
+def bag_truncate(
+    values: Tensor,
+    offsets: Tensor,
+    *,
+    valid: Tensor | None = None,
+    row_valid: Tensor | None = None,
+    max_length: int | None = None,
+    truncation: str = "tail",
+    bucket: str = "none",
+    num_buckets: int = 0,
+    validate_nonzero: bool = True,
+    error_count: Tensor | None = None,
+) -> tuple[Tensor, Tensor, Tensor]:
+    """List feature -> CSR bag on the device: ``(ids [n_in], lengths [rows],
+    out_offsets [rows+1])``.
+
+    Row r of the list array holds ``values[offsets[r]:offsets[r+1]]``
+    (Arrow list layout); a null row (``row_valid == 0``) keeps nothing, a null
+    element (``valid == 0``) keeps its slot and becomes id 0.  ``max_length``
+    keeps a row's first (``head``) or last (``tail``) elements
+    (src/dataloader.py:8565-8604); the kept elements are bucketed
+    (``bucket``: ``none``, ``pre_hashed`` or ``mod``, as :func:`bucketize`).
+    ``ids`` is capacity-sized: the kept total is ``out_offsets[-1]`` (on the
+    device) and entries past it are 0, so nothing is read back.
+    """
+
+    _require_device(values, "list values")
+    if values.dtype != torch.int64 or offsets.dtype != torch.int64:
+        raise TypeError("list values and offsets must be torch.int64")
+    if bucket not in BUCKET_MODES:
+        raise ValueError(f"bucket must be one of {sorted(BUCKET_MODES)}")
+    if truncation not in TRUNCATIONS:
+        raise ValueError(f"unsupported list truncation {truncation!r}")
+    if max_length is not None and max_length < 0:
+        raise ValueError(f"max_length must be non-negative, got {max_length}")
+    device = values.device
+    values = values.contiguous()
+    offsets = offsets.to(device).contiguous()
+    rows = int(offsets.numel()) - 1
+    if rows < 0:
+        raise ValueError("list offsets need at least one entry")
+    if valid is not None:
+        valid = valid.to(device=device, dtype=torch.uint8).contiguous()
+    if row_valid is not None:
+        row_valid = row_valid.to(device=device, dtype=torch.uint8).contiguous()
+    n_in = int(values.numel())
+    ids = torch.empty(n_in, dtype=torch.int64, device=device)
+    lengths = torch.empty(max(rows, 0), dtype=torch.int64, device=device)
+    out_offsets = torch.empty(rows + 1, dtype=torch.int64, device=device)
+    ws = _workspace(lib().mdl_bag_truncate_workspace_bytes(rows), device)
+    check(
+        lib().mdl_bag_truncate(
+            offsets.data_ptr(), _ptr(row_valid), rows, _ptr(values) if n_in else None, _ptr(valid), n_in,
+            -1 if max_length is None else int(max_length), TRUNCATIONS[truncation], BUCKET_MODES[bucket],
+            int(num_buckets), 1 if validate_nonzero else 0, _ptr(lengths) if rows else None,
+            out_offsets.data_ptr(), _ptr(ids) if n_in else None, n_in, _ptr(error_count), ws.data_ptr(),
+            ws.numel(), _stream(device),
+        ),
+        "mdl_bag_truncate",
+    )
+    return ids, lengths, out_offsets
+
+
 def lengths_to_offsets(lengths: Tensor) -> Tensor:
     """``[0, cumsum(lengths)]`` as int64 on the device."""
 

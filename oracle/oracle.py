@@ -16,6 +16,10 @@ pinned (see ``tests/test_oracle.py``):
 * bucketize_mod -- src/benchmark.py:1246-1250; pinned by Python's floor-mod
   ``1 + (v - 1) % (N - 1)`` on random int64 including the extremes.
 * bag_csr (host, in mdl_amd.features) -- pinned by the same golden vectors.
+* bag_truncate -- src/dataloader.py:8565-8640 (Arrow list truncation,
+  lengths, flatten); pinned by the same golden vectors in Arrow layout, by
+  pyarrow's own ``list_slice`` / ``list_value_length`` / ``list_flatten``
+  (library) and by the per-row brute force ``bag_csr`` on random lists.
 * pool -- src/model.py:509-570; pinned by the closed-form vectors of
   tests/test_multivalue_features.py:95-120 and by torch's
   ``F.embedding_bag(mode="sum"/"mean")`` and ``_mean_pool``-style index_add_
@@ -136,6 +140,29 @@ def bucketize_mod(raw: np.ndarray, num_embeddings: int, valid: np.ndarray | None
 
 
 # ----------------------------------------------------------------- forward --
+
+
+def bag_truncate(offsets: np.ndarray, values: np.ndarray, valid: np.ndarray | None, row_valid: np.ndarray | None,
+                 max_length: int | None, truncation: str):
+    """List array -> (kept raw values, their validity, per-row kept lengths):
+    the reference's truncation of Arrow lists (src/dataloader.py:8565-8604,
+    head = ``list_slice(0, max_length)``, tail = the last ``max_length``
+    elements by rebuilt offsets) then ``list_value_length`` with nulls as 0
+    and ``list_flatten`` (:8634-8640).  Offsets are assumed well formed."""
+
+    offsets = np.asarray(offsets, dtype=np.int64)
+    lengths = offsets[1:] - offsets[:-1]
+    if row_valid is not None:
+        lengths = np.where(np.asarray(row_valid) != 0, lengths, 0)
+    take = lengths if max_length is None else np.minimum(lengths, int(max_length))
+    starts = offsets[:-1] if truncation == "head" else offsets[1:] - take
+    total = int(take.sum())
+    row_ids = np.repeat(np.arange(take.size, dtype=np.int64), take)
+    within = np.arange(total, dtype=np.int64) - np.repeat(np.cumsum(take) - take, take)
+    src = starts[row_ids] + within
+    vals = np.asarray(values, dtype=np.int64)[src]
+    ok = np.ones(total, dtype=np.uint8) if valid is None else (np.asarray(valid)[src] != 0).astype(np.uint8)
+    return vals, ok, take.astype(np.int64)
 
 
 def offsets_of(lengths: np.ndarray) -> np.ndarray:

@@ -1,0 +1,158 @@
+"""List-feature truncation to CSR bags (host side, no GPU).
+
+The oracle's ``bag_truncate`` restates the reference's Arrow truncation
+(src/dataloader.py:8565-8640); it is pinned here by the reference's golden
+vectors in Arrow layout, by pyarrow's own list kernels and by the per-row
+brute force ``bag_csr``.  The ``mdl_hip::bag_truncate`` op's CPU kernel (the
+product's vectorised path) is then checked against the oracle.
+"""
+
+import json
+from pathlib import Path
+
+import numpy as np
+import pyarrow as pa
+import pyarrow.compute as pc
+import pytest
+import torch
+
+import mdl_amd  # noqa: F401  (registers the mdl_hip ops)
+from mdl_amd.features import bag_csr, bag_csr_arrow, bag_csr_tensor
+from oracle import oracle as O
+
+GOLD = json.loads((Path(__file__).parent / "golden" / "reference_vectors.json").read_text())
+
+
+def _random_lists(rng, rows, max_len, null_rows=0.1, null_elems=0.1):
+    out = []
+    for _ in range(rows):
+        if rng.random() < null_rows:
+            out.append(None)
+            continue
+        n = int(rng.integers(0, max_len + 1))
+        vals = rng.integers(-(1 << 63), (1 << 63) - 1, size=n, dtype=np.int64, endpoint=True).tolist()
+        out.append([None if rng.random() < null_elems else v for v in vals])
+    return out
+
+
+def _arrow_parts(array):
+    offsets = array.offsets.to_numpy(zero_copy_only=False).astype(np.int64)
+    raw = pc.fill_null(array.values, 0).to_numpy(zero_copy_only=False).astype(np.int64)
+    valid = array.values.is_valid().to_numpy(zero_copy_only=False).astype(np.uint8)
+    row_valid = array.is_valid().to_numpy(zero_copy_only=False).astype(np.uint8)
+    return offsets, raw, valid, row_valid
+
+
+@pytest.mark.parametrize("key", ["bag_head_truncation", "bag_tail_truncation"])
+def test_oracle_bag_truncate_golden(key):
+    g = GOLD[key]
+    offsets, raw, valid, row_valid = _arrow_parts(pa.array(g["rows"], type=pa.list_(pa.int64())))
+    vals, ok, lengths = O.bag_truncate(offsets, raw, valid, row_valid, g["max_length"], g["truncation"])
+    ids, _ = O.bucketize_pre_hashed(vals, g["num_buckets"], ok)
+    assert lengths.tolist() == g["expected_lengths"]
+    assert ids.tolist() == g["expected_values"]
+
+
+@pytest.mark.parametrize("truncation", ["head", "tail"])
+@pytest.mark.parametrize("max_length", [None, 0, 1, 3, 7])
+def test_oracle_bag_truncate_matches_brute_force_and_arrow(truncation, max_length):
+    rng = np.random.default_rng(31 + (max_length or 0))
+    rows = _random_lists(rng, 300, 9)
+    array = pa.array(rows, type=pa.list_(pa.int64()))
+    offsets, raw, valid, row_valid = _arrow_parts(array)
+    vals, ok, lengths = O.bag_truncate(offsets, raw, valid, row_valid, max_length, truncation)
+    flat, bvalid, blengths = bag_csr(rows, max_length=max_length, truncation=truncation)
+    assert lengths.tolist() == blengths.tolist()
+    assert (vals * ok).tolist() == flat.tolist() and ok.tolist() == bvalid.tolist()
+    if truncation == "head" and max_length is not None:
+        # pyarrow's own kernels: list_slice, list_value_length (nulls 0), list_flatten
+        sliced = pc.list_slice(array, 0, max_length)
+        assert pc.fill_null(pc.list_value_length(sliced), 0).to_pylist() == lengths.tolist()
+        flat_arrow = pc.list_flatten(sliced)
+        assert pc.fill_null(flat_arrow, 0).to_pylist() == (vals * ok).tolist()
+        assert flat_arrow.is_valid().to_pylist() == [bool(x) for x in ok]
+
+
+def test_oracle_bag_truncate_sliced_arrow_array():
+    rng = np.random.default_rng(5)
+    rows = _random_lists(rng, 120, 6)
+    array = pa.array(rows, type=pa.list_(pa.int64())).slice(17, 60)
+    offsets, raw, valid, row_valid = _arrow_parts(array)
+    assert offsets[0] != 0
+    vals, ok, lengths = O.bag_truncate(offsets, raw, valid, row_valid, 4, "tail")
+    flat, bvalid, blengths = bag_csr(rows[17:77], max_length=4, truncation="tail")
+    assert lengths.tolist() == blengths.tolist() and (vals * ok).tolist() == flat.tolist()
+
+
+def _op_cpu(offsets, raw, valid, row_valid, max_length, truncation, bucket, nb, validate=True):
+    t = lambda a, dt=torch.int64: None if a is None else torch.from_numpy(np.asarray(a)).to(dt)  # noqa: E731
+    return torch.ops.mdl_hip.bag_truncate(t(raw), t(offsets), t(valid, torch.uint8), t(row_valid, torch.uint8),
+                                          -1 if max_length is None else max_length, truncation, bucket, nb,
+                                          validate)
+
+
+@pytest.mark.parametrize("bucket,nb", [("none", 0), ("pre_hashed", 1 << 20), ("mod", 1_000_003)])
+@pytest.mark.parametrize("truncation", ["head", "tail"])
+def test_bag_truncate_cpu_kernel_matches_oracle(bucket, nb, truncation):
+    rng = np.random.default_rng(77)
+    array = pa.array(_random_lists(rng, 500, 12), type=pa.list_(pa.int64()))
+    offsets, raw, valid, row_valid = _arrow_parts(array)
+    raw[raw == 0] = 1  # zeros are the error case, tested below
+    ids, lengths, out_offsets, err = _op_cpu(offsets, raw, valid, row_valid, 5, truncation, bucket, nb)
+    vals, ok, ref_lengths = O.bag_truncate(offsets, raw, valid, row_valid, 5, truncation)
+    if bucket == "none":
+        ref = vals * ok
+    elif bucket == "pre_hashed":
+        ref, _ = O.bucketize_pre_hashed(vals, nb, ok)
+    else:
+        ref = O.bucketize_mod(vals, nb, ok)
+    total = int(ref_lengths.sum())
+    assert lengths.tolist() == ref_lengths.tolist()
+    assert out_offsets.tolist() == O.offsets_of(ref_lengths).tolist()
+    assert ids[:total].tolist() == ref.tolist() and not ids[total:].any()
+    assert int(err[0]) == 0
+
+
+def test_bag_truncate_cpu_kernel_counts_zeros_and_bad_offsets():
+    offsets = np.array([0, 2, 5, 5], dtype=np.int64)
+    raw = np.array([0, 3, 4, 0, 6], dtype=np.int64)
+    valid = np.array([1, 1, 1, 0, 1], dtype=np.uint8)
+    _, _, _, err = _op_cpu(offsets, raw, valid, None, None, "head", "pre_hashed", 8)
+    assert int(err[0]) == 1  # the null zero is not counted
+    _, _, _, err = _op_cpu(offsets, raw, valid, None, None, "head", "pre_hashed", 8, validate=False)
+    assert int(err[0]) == 0
+    bad = np.array([0, 7, 3, -1], dtype=np.int64)  # past the values, decreasing, negative
+    ids, lengths, out_offsets, err = _op_cpu(bad, raw, None, None, None, "tail", "none", 0)
+    assert lengths.tolist() == [5, 0, 0] and int(err[0]) == 3
+    assert ids.tolist() == raw.tolist()
+
+
+def test_bag_csr_tensor_errors_and_capacity_form():
+    raw = torch.tensor([5, 0, 7], dtype=torch.int64)
+    offsets = torch.tensor([0, 2, 3], dtype=torch.int64)
+    with pytest.raises(ValueError, match="non-null zero"):
+        bag_csr_tensor(raw, offsets, bucket="pre_hashed", num_buckets=8)
+    with pytest.raises(ValueError, match="offsets outside"):
+        bag_csr_tensor(raw, torch.tensor([0, 4, 3], dtype=torch.int64))
+    out = bag_csr_tensor(raw, offsets, max_length=1, truncation="tail", exact=False)
+    assert out["values"].tolist() == [0, 7, 0] and out["offsets"].tolist() == [0, 1, 2]
+    assert int(out["errors"][0]) == 0
+
+
+@pytest.mark.parametrize("key", ["bag_head_truncation", "bag_tail_truncation"])
+def test_bag_csr_arrow_golden_cpu(key):
+    g = GOLD[key]
+    out = bag_csr_arrow(pa.array(g["rows"], type=pa.list_(pa.int64())), max_length=g["max_length"],
+                        truncation=g["truncation"], bucket="pre_hashed", num_buckets=g["num_buckets"])
+    assert out["values"].tolist() == g["expected_values"]
+    assert out["lengths"].tolist() == g["expected_lengths"]
+
+
+def test_bag_truncate_opcheck_cpu():
+    rng = np.random.default_rng(3)
+    array = pa.array(_random_lists(rng, 40, 6), type=pa.list_(pa.int64()))
+    offsets, raw, valid, row_valid = _arrow_parts(array)
+    raw[raw == 0] = 1
+    args = (torch.from_numpy(raw), torch.from_numpy(offsets), torch.from_numpy(valid), torch.from_numpy(row_valid),
+            3, "tail", "pre_hashed", 64, True)
+    torch.library.opcheck(torch.ops.mdl_hip.bag_truncate.default, args)
