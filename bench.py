@@ -1076,6 +1076,15 @@ def measure(name: str, args, torch, device, *, with_aux: bool = False) -> dict:
     dom = kernels[dom_name]
     traffic = None
     tr, why = load_traffic(wl.name)
+    if tr is not None:
+        # counter bytes of each launch group per looked-up row (the
+        # per-row traffic figure of the measurement plan), with its L2 hit rate
+        for kname, g in tr.get("groups", {}).items():
+            rec = kernels.setdefault(kname, {"kernel": kname})
+            rec["counter_bytes"] = g["hbm_bytes_per_step"]
+            rec["counter_bytes_per_looked_up_row"] = g["hbm_bytes_per_step"] / max(n_ids, 1.0)
+            if "l2" in g and g["l2"].get("l2_hit_rate") is not None:
+                rec["l2_hit_rate"] = g["l2"]["l2_hit_rate"]
     if tr is not None and "hbm_bytes_per_step" in tr.get("groups", {}).get(dom_name, {}):
         traffic = tr["groups"][dom_name]["hbm_bytes_per_step"]
         dom["traffic_source"] = (f"profiles/{wl.name}_traffic.json (rocprofv3 FETCH_SIZE/WRITE_SIZE, copy-calibrated; "
