@@ -382,6 +382,11 @@ class SparseStep:
         return self.norm, self.coef
 
     def step(self, lr: float, eps: float, clip_norm: float | None = None) -> None:
+        """Forward, sort and update of the bound batch (one micro-batch)."""
+
+        if self.k > 1:
+            raise ValueError("a step of several micro-batches is forward(micro_batch=m) for each m, then "
+                             "sort() and apply()")
         self.forward()
         self.sort()
         if clip_norm is None:

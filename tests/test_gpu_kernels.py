@@ -800,6 +800,8 @@ def test_sparse_step_accumulates_micro_batches(device):
     assert_close(norm.cpu().numpy(), np.array([np.sqrt(sumsq)]), 1e-5, 0)
     with pytest.raises(ValueError):
         st.forward(micro_batch=k)
+    with pytest.raises(ValueError):
+        st.step(lr, eps)
 
 
 def test_sparse_step_slot_buffer_matches_oracle(device):
