@@ -422,6 +422,11 @@ class SequenceStep:
     entries (the positions that reach the window), placed each step by one
     scan of those clamped lengths on the device, so the backward sorts no
     padding and any lengths of a later batch are honoured.
+
+    ``micro_batches=k`` accumulates gradients as ``SparseStep`` does: k
+    lists of outputs, masks and gradients; ``forward(micro_batch=m)`` for each
+    bound micro-batch, then one ``sort()`` + ``apply()`` update every row once
+    with the sum of the k micro-batches' gradients (src/train.py:5388-5396).
     """
 
     def __init__(
@@ -435,19 +440,28 @@ class SequenceStep:
         *,
         order: str = "oldest_to_newest",
         error_count: Tensor | None = None,
+        micro_batches: int = 1,
     ) -> None:
         for t in plan.tables:
             if t.state is None:
                 raise RuntimeError("every table needs a row-wise Adagrad accumulator")
         if plan.total_rows >= ops.KEY_SPACE:
             raise NotImplementedError("sequence steps take plans of fewer than 2^32 - 1 rows")
+        self.k = int(micro_batches)
+        if self.k < 1:
+            raise ValueError("micro_batches must be positive")
+        if self.k == 1:
+            outputs, masks, grads = [outputs], [masks], [grads]
+        elif not len(outputs) == len(masks) == len(grads) == self.k:
+            raise ValueError("one list of outputs, masks and gradients per micro-batch")
         self.plan = plan
         self.device = ids[0].device
         self.ids = [_as_ids(t) for t in ids]
         self.lengths = [t.to(torch.int64).contiguous() for t in lengths]
-        self.outputs = list(outputs)
-        self.masks = list(masks)
-        self.grads = [g.contiguous() for g in grads]
+        self.all_outputs = [list(o) for o in outputs]
+        self.all_masks = [list(m) for m in masks]
+        self.all_grads = [[g.contiguous() for g in gs] for gs in grads]
+        self.outputs, self.masks, self.grads = self.all_outputs[0], self.all_masks[0], self.all_grads[0]
         if order not in ("oldest_to_newest", "newest_to_oldest"):
             raise ValueError("order must be oldest_to_newest or newest_to_oldest")
         self.order = ops._lib.MDL_SEQ_OLDEST_TO_NEWEST if order == "oldest_to_newest" else ops._lib.MDL_SEQ_NEWEST_TO_OLDEST
@@ -456,6 +470,9 @@ class SequenceStep:
         )
         self.batch = [int(t.size(0)) for t in self.ids]
         self.caps = [min(int(i.size(1)), int(o.size(1))) for i, o in zip(self.ids, self.outputs)]
+        for m in range(1, self.k):
+            if [tuple(o.shape) for o in self.all_outputs[m]] != [tuple(o.shape) for o in self.outputs]:
+                raise ValueError("every micro-batch's windows need the shapes of the first's")
         self.row_base = np.concatenate([[0], np.cumsum(self.batch)]).astype(np.int64)
         total_rows = int(self.row_base[-1])
         # Entries a step can hold: every row at its cap.
@@ -464,31 +481,49 @@ class SequenceStep:
         self.offsets = torch.empty(total_rows + 1, dtype=torch.int64, device=self.device)
         self.scan_ws = ops._workspace(lib().mdl_offsets_workspace_bytes(total_rows), self.device)
         cap = max(self.capacity, 1)
-        self.keys = torch.empty(cap, dtype=torch.int32, device=self.device)
-        self.payload = torch.empty(cap, dtype=torch.int32, device=self.device)
+        self.keys = torch.empty(cap * self.k, dtype=torch.int32, device=self.device)
+        self.payload = torch.empty(cap * self.k, dtype=torch.int32, device=self.device)
+        # Window positions of one micro-batch; micro-batch m's payloads (and
+        # gradient rows) follow micro-batch m - 1's.
+        positions = int(sum(int(o.size(0)) * int(o.size(1)) for o in self.outputs))
+        if positions * self.k >= 1 << 32:
+            raise ValueError("the micro-batches' window positions exceed the 32-bit gradient-row payload")
         feats = []
-        self.fwd_feats = []
-        payload_base = 0
-        for f, spec in enumerate(plan.features):
-            table = plan.tables[spec.table]
-            out = self.outputs[f]
-            B, L_out, _ = out.shape
-            rec = ops.sequence_feature(
-                table.weight, state=table.state, padding_idx=spec.padding_idx, out_dtype=spec.out_dtype,
-                row_base=table.row_base, payload_base=payload_base, grad=self.grads[f],
-            )
-            rec["table"] = spec.table
-            feats.append(rec)
-            self.fwd_feats.append(rec.copy())
-            payload_base += int(B) * int(L_out)
+        self.fwd_feats = []  # [m][f]
+        for m in range(self.k):
+            per = []
+            payload_base = m * positions
+            for f, spec in enumerate(plan.features):
+                table = plan.tables[spec.table]
+                out = self.all_outputs[m][f]
+                B, L_out, _ = out.shape
+                rec = ops.sequence_feature(
+                    table.weight, state=table.state, padding_idx=spec.padding_idx, out_dtype=spec.out_dtype,
+                    row_base=table.row_base, payload_base=payload_base, grad=self.all_grads[m][f],
+                )
+                rec["table"] = spec.table
+                feats.append(rec)
+                per.append(rec.copy())
+                payload_base += int(B) * int(L_out)
+            self.fwd_feats.append(per)
         self.feats_bwd = np.concatenate(feats)
-        self.tables = ops._tables_array(plan, self.feats_bwd)
+        self.tables = ops._tables_array(plan, self.feats_bwd[: len(plan.features)])
+        if self.k > 1:
+            # a table read by k copies of its feature: the reduce finds each
+            # payload's feature by search
+            self.tables["feature"] = -1
+            self._positions = torch.arange(cap, dtype=torch.int64, device=self.device)
+            sentinel = int(plan.sentinel)
+            self._sentinel = sentinel - (1 << 32) if sentinel >= (1 << 31) else sentinel
         self.bwd_classes = ops.table_classes(self.tables)
         self.feats_bwd_dev = ops.upload(self.feats_bwd, self.device)
         self.tables_dev = ops.upload(self.tables, self.device)
         self.ws = ops._workspace(
-            lib().mdl_backward_workspace_bytes(self.capacity, len(self.tables), plan.max_dim), self.device
+            lib().mdl_backward_workspace_bytes(self._n(), len(self.tables), plan.max_dim), self.device
         )
+
+    def _n(self) -> int:
+        return max(self.capacity, 1) * self.k if self.k > 1 else self.capacity
 
     def bind(self, ids: Sequence[Tensor] | None = None, lengths: Sequence[Tensor] | None = None) -> None:
         """Point the next steps at another batch (same shapes; any lengths)."""
@@ -513,8 +548,15 @@ class SequenceStep:
     def _stream(self) -> int:
         return torch.cuda.current_stream(self.device).cuda_stream
 
-    def forward(self) -> None:
+    def forward(self, micro_batch: int = 0) -> None:
+        """Window gather (+ packed sort keys) of the bound batch, as
+        micro-batch ``micro_batch`` of an accumulated step."""
+
+        mb = int(micro_batch)
+        if not 0 <= mb < self.k:
+            raise ValueError(f"micro_batch must be in [0, {self.k})")
         s = self._stream()
+        region = mb * max(self.capacity, 1)
         # Entries each row keeps (its positions that reach the window), then
         # one scan over every feature's rows places them.
         for f, ln in enumerate(self.lengths):
@@ -526,24 +568,31 @@ class SequenceStep:
                                          self.scan_ws.data_ptr(), self.scan_ws.numel(), s),
             "mdl_lengths_to_offsets",
         )
-        for f, rec in enumerate(self.fwd_feats):
+        for f, rec in enumerate(self.fwd_feats[mb]):
             ids = self.ids[f]
-            out = self.outputs[f]
+            out = self.all_outputs[mb][f]
             check(
                 lib().mdl_sequence_forward(
                     rec.ctypes.data, ids.data_ptr(), self.lengths[f].data_ptr(), ids.size(0), ids.size(1),
-                    out.size(1), self.order, out.data_ptr(), self.masks[f].data_ptr(), self.keys.data_ptr(),
-                    self.payload.data_ptr(), self.offsets.data_ptr() + 8 * int(self.row_base[f]), self.plan.sentinel,
+                    out.size(1), self.order, out.data_ptr(), self.all_masks[mb][f].data_ptr(),
+                    self.keys.data_ptr() + 4 * region, self.payload.data_ptr() + 4 * region,
+                    self.offsets.data_ptr() + 8 * int(self.row_base[f]), self.plan.sentinel,
                     self.error_count.data_ptr(), s,
                 ),
                 "mdl_sequence_forward",
             )
+        if self.k > 1:
+            # entries of the region past this micro-batch's keys sort last and
+            # reduce nowhere
+            live = self.offsets[int(self.row_base[-1])]
+            self.keys[region: region + max(self.capacity, 1)].masked_fill_(self._positions >= live, self._sentinel)
 
     def sort(self) -> None:
         check(
             lib().mdl_backward_sort(
                 self.tables_dev.data_ptr(), len(self.tables), self.plan.max_dim, self.keys.data_ptr(),
-                self.payload.data_ptr(), self.capacity, self.offsets.data_ptr() + 8 * int(self.row_base[-1]),
+                self.payload.data_ptr(), self._n(),
+                self.offsets.data_ptr() + 8 * int(self.row_base[-1]) if self.k == 1 else None,
                 self.plan.key_bits, self.ws.data_ptr(), self.ws.numel(), self._stream(),
             ),
             "mdl_backward_sort",
@@ -553,7 +602,7 @@ class SequenceStep:
         check(
             lib().mdl_backward_apply(
                 self.feats_bwd_dev.data_ptr(), len(self.feats_bwd), self.tables_dev.data_ptr(), len(self.tables),
-                self.plan.max_dim, self.keys.data_ptr(), self.payload.data_ptr(), self.capacity, self.plan.key_bits,
+                self.plan.max_dim, self.keys.data_ptr(), self.payload.data_ptr(), self._n(), self.plan.key_bits,
                 None, float(lr), float(eps), None, self.ws.data_ptr(), self.ws.numel(), self.bwd_classes,
                 self._stream(),
             ),
@@ -569,6 +618,11 @@ class SequenceStep:
         self._graph.replay()
 
     def step(self, lr: float, eps: float) -> None:
+        """Forward, sort and update of the bound batch (one micro-batch)."""
+
+        if self.k > 1:
+            raise ValueError("a step of several micro-batches is forward(micro_batch=m) for each m, then "
+                             "sort() and apply()")
         self.forward()
         self.sort()
         self.apply(lr, eps)

@@ -998,6 +998,70 @@ def test_sequence_step_rebound_to_longer_rows_matches_oracle(device):
         A = acc.cpu().numpy().copy()
 
 
+def test_sequence_step_accumulates_micro_batches(device):
+    """SequenceStep(micro_batches=2) over two sequence features sharing no
+    table: each micro-batch's windows match the oracle, and one sort + reduce
+    applies one row-wise Adagrad step on the coalesced sum of both
+    micro-batches' window gradients."""
+    from mdl_amd.sparse_step import SequenceStep
+
+    rng = np.random.default_rng(86)
+    B, L, k, lr, eps = 40, 96, 2, 0.03, 1e-8
+    rows = [5000, 800]
+    dims = [32, 16]
+    tabs = [_table(rng, r, d, torch.float32, device) for r, d in zip(rows, dims)]
+    accs = [torch.from_numpy(rng.random(r).astype(np.float32)).to(device) for r in rows]
+    W = [to_np(t).copy() for t in tabs]
+    A = [a.cpu().numpy().copy() for a in accs]
+    plan = ops.GroupPlan()
+    for t, a in zip(tabs, accs):
+        plan.add_feature(t, pooling="none", state=a)
+    outs = [[torch.empty((B, L, d), device=device) for d in dims] for _ in range(k)]
+    masks = [[torch.empty((B, L), dtype=torch.bool, device=device) for _ in dims] for _ in range(k)]
+    grads = [[torch.empty((B, L, d), device=device) for d in dims] for _ in range(k)]
+
+    def seq(r, max_len):
+        ln = rng.integers(0, max_len + 1, size=B)
+        m = np.zeros((B, L), dtype=np.int64)
+        for b in range(B):
+            n = min(int(ln[b]), L)
+            m[b, :n] = rng.zipf(1.1, size=n) % r
+        return m, ln
+
+    batches = [[seq(r, mx) for r in rows] for mx in (30, L + 20)]
+    st = SequenceStep(plan, [torch.from_numpy(b[0]).to(device) for b in batches[0]],
+                      [torch.from_numpy(b[1]).to(device) for b in batches[0]], outs, masks, grads, micro_batches=k)
+    g_host = []
+    for m, batch in enumerate(batches):
+        announce("sequence_micro_batch", m)
+        gm = []
+        for f, d in enumerate(dims):
+            g = rng.standard_normal((B, L, d)).astype(np.float32)
+            grads[m][f].copy_(torch.from_numpy(g))
+            gm.append(g)
+        g_host.append(gm)
+        st.bind([torch.from_numpy(b[0]).to(device) for b in batch], [torch.from_numpy(b[1]).to(device) for b in batch])
+        st.forward(micro_batch=m)
+    st.sort()
+    st.apply(lr, eps)
+    torch.cuda.synchronize()
+    assert int(st.error_count.item()) == 0
+    for f in range(len(rows)):
+        parts = []
+        for m, batch in enumerate(batches):
+            ids, ln = batch[f]
+            ref, rmask = O.sequence_window(W[f], ids, ln, L)
+            assert np.array_equal(masks[m][f].cpu().numpy(), rmask), (m, f)
+            assert np.array_equal(outs[m][f].cpu().numpy(), ref), (m, f)
+            parts.append(O.sequence_grads(ids, ln, g_host[m][f], L))
+        rr, vv = O.coalesce(np.concatenate([p[0] for p in parts]), np.concatenate([p[1] for p in parts]))
+        wexp, aexp = O.rowwise_adagrad(W[f], A[f], rr, vv, lr, eps)
+        assert_close(accs[f].cpu().numpy(), aexp, 1e-5, 1e-7)
+        assert_close(to_np(tabs[f]), wexp, 1e-5, 1e-6)
+    with pytest.raises(ValueError):
+        st.step(lr, eps)
+
+
 @pytest.mark.parametrize("clip", [None, 0.5])
 def test_sparse_step_graph_replays_match_eager(device, clip):
     """Every replay of a captured step equals an eager step bit for bit, with
