@@ -114,6 +114,7 @@ class SparseStep:
         self.k = int(micro_batches)
         if self.k < 1:
             raise ValueError("micro_batches must be positive")
+        self._looked_up: set[int] = set()  # micro-batches forwarded since the last sort
         if self.k == 1:
             outputs, grads = [outputs], [grads]
         elif len(outputs) != self.k or len(grads) != self.k:
@@ -292,6 +293,7 @@ class SparseStep:
         m = int(micro_batch)
         if not 0 <= m < self.k:
             raise ValueError(f"micro_batch must be in [0, {self.k})")
+        self._looked_up.add(m)
         s = self._stream()
         if self.offsets is not None:
             check(
@@ -327,9 +329,19 @@ class SparseStep:
                     live = self.offsets[-1] if self.offsets is not None else int(self.ids.numel())
                 gs.keys[region: region + max(self.capacity, 1)].masked_fill_(self._positions >= live, self._sentinel)
 
+    def _check_micro_batches(self) -> None:
+        # Every region of the keys must hold this step's lookup: a region left
+        # from an earlier step would apply its gradients a second time.
+        if self.k > 1:
+            if len(self._looked_up) != self.k:
+                missing = sorted(set(range(self.k)) - self._looked_up)
+                raise RuntimeError(f"micro-batches {missing} were not looked up since the last sort")
+            self._looked_up.clear()
+
     def sort(self) -> None:
         """Radix sort of the (row, gradient-row) pairs + chunk plan."""
 
+        self._check_micro_batches()
         for g, gs in enumerate(self.groups):
             check(
                 lib().mdl_backward_sort(
@@ -450,6 +462,7 @@ class SequenceStep:
         self.k = int(micro_batches)
         if self.k < 1:
             raise ValueError("micro_batches must be positive")
+        self._looked_up: set[int] = set()  # micro-batches forwarded since the last sort
         if self.k == 1:
             outputs, masks, grads = [outputs], [masks], [grads]
         elif not len(outputs) == len(masks) == len(grads) == self.k:
@@ -555,6 +568,7 @@ class SequenceStep:
         mb = int(micro_batch)
         if not 0 <= mb < self.k:
             raise ValueError(f"micro_batch must be in [0, {self.k})")
+        self._looked_up.add(mb)
         s = self._stream()
         region = mb * max(self.capacity, 1)
         # Entries each row keeps (its positions that reach the window), then
@@ -587,7 +601,10 @@ class SequenceStep:
             live = self.offsets[int(self.row_base[-1])]
             self.keys[region: region + max(self.capacity, 1)].masked_fill_(self._positions >= live, self._sentinel)
 
+    _check_micro_batches = SparseStep._check_micro_batches
+
     def sort(self) -> None:
+        self._check_micro_batches()
         check(
             lib().mdl_backward_sort(
                 self.tables_dev.data_ptr(), len(self.tables), self.plan.max_dim, self.keys.data_ptr(),

@@ -802,6 +802,9 @@ def test_sparse_step_accumulates_micro_batches(device):
         st.forward(micro_batch=k)
     with pytest.raises(ValueError):
         st.step(lr, eps)
+    st.forward(micro_batch=0)
+    with pytest.raises(RuntimeError, match=r"micro-batches \[1, 2\] were not looked up"):
+        st.sort()
 
 
 def test_sparse_step_slot_buffer_matches_oracle(device):
