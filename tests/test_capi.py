@@ -206,3 +206,24 @@ def test_too_wide_rows_are_refused_not_skipped(dim, dtype):
 
 def test_abi_version_matches_binding():
     assert _lib.lib().mdl_abi_version() == _lib.ABI_VERSION
+
+
+def test_bag_truncate_refuses_bad_arguments_before_any_launch():
+    lib = _lib.lib()
+    ws_bytes = lib.mdl_bag_truncate_workspace_bytes(4)
+    assert ws_bytes >= lib.mdl_offsets_workspace_bytes(4) + 4 * 8
+    p = 4096  # never dereferenced: every call below fails its checks first
+
+    def call(rows=4, n_in=8, max_length=3, trunc=_lib.MDL_TRUNCATE_TAIL, mode=_lib.MDL_BUCKET_NONE, buckets=0,
+             cap=8, ws=ws_bytes, out_offsets=p):
+        return lib.mdl_bag_truncate(p, None, rows, p, None, n_in, max_length, trunc, mode, buckets, 1, p,
+                                    out_offsets, p, cap, None, p, ws, None)
+
+    assert call(rows=-1) == -1 and b"negative" in lib.mdl_last_error()
+    assert call(cap=-1) == -1
+    assert call(trunc=7) == -1 and b"head or tail" in lib.mdl_last_error()
+    assert call(mode=9) == -1 and b"unknown bucketing mode" in lib.mdl_last_error()
+    assert call(mode=_lib.MDL_BUCKET_PRE_HASHED, buckets=6) == -1 and b"power of two" in lib.mdl_last_error()
+    assert call(mode=_lib.MDL_BUCKET_MOD, buckets=1) == -1
+    assert call(out_offsets=None) == -1 and b"null pointer" in lib.mdl_last_error()
+    assert call(ws=ws_bytes - 1) != 0 and b"workspace" in lib.mdl_last_error()
