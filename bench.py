@@ -1134,6 +1134,83 @@ def measure(name: str, args, torch, device, *, with_aux: bool = False) -> dict:
     return out
 
 
+def ceilings(torch, device) -> dict:
+    """What this MI355X sustains on the access patterns of the path, measured
+    with the product's own kernels and torch's copy: device copies of 256 MiB
+    to 4 GiB, the library's streaming bucketize (8 bytes read, 8 written per
+    id) on 32 M to 512 M ids, and gathers of 16 M uniformly random rows (no reuse) of
+    16..512 bytes from one 64 GiB-class table through ``mdl_forward``
+    (unpooled), each timed with HIP events over 10 launches behind a spin
+    kernel.  The gather's rows/s at small rows is the request ceiling the
+    step's kernels are compared with."""
+
+    from mdl_amd import ops
+
+    out = {}
+    reps = 10
+
+    def timed(fn):
+        for _ in range(2):
+            fn()
+        torch.cuda.synchronize()
+        e0 = torch.cuda.Event(enable_timing=True)
+        e1 = torch.cuda.Event(enable_timing=True)
+        torch.cuda._sleep(20_000_000)
+        e0.record()
+        for _ in range(reps):
+            fn()
+        e1.record()
+        torch.cuda.synchronize()
+        return e0.elapsed_time(e1) / reps
+
+    copies = []
+    for nbytes in (1 << 28, 1 << 30, 1 << 32):
+        src = torch.empty(nbytes // 4, dtype=torch.float32, device=device).fill_(1.0)
+        dst = torch.empty_like(src)
+        ms = timed(lambda: dst.copy_(src))
+        copies.append({"bytes_read": nbytes, "ms": ms, "gbps": 2.0 * nbytes / (ms * 1e-3) / 1e9})
+        del src, dst
+    out["torch_copy"] = copies
+    # the library's own streaming kernel: mdl_bucketize reads 8 and writes 8
+    # bytes per id, coalesced
+    streams = []
+    for n in (1 << 25, 1 << 27, 1 << 29):
+        raw = torch.randint(1, 1 << 62, (n,), dtype=torch.int64, device=device)
+        ids = torch.empty_like(raw)
+        ms = timed(lambda: ops.bucketize(raw, 1 << 20, validate_nonzero=False))
+        streams.append({"ids": n, "bytes": 16.0 * n, "ms": ms, "gbps": 16.0 * n / (ms * 1e-3) / 1e9})
+        del raw, ids
+        gc.collect()
+        torch.cuda.empty_cache()
+    out["stream_bucketize"] = streams
+    torch.cuda.empty_cache()
+    n = 1 << 24
+    gen = torch.Generator(device=device)
+    gen.manual_seed(5)
+    rows_out = []
+    for row_bytes in (16, 32, 64, 128, 256, 512):
+        dim = row_bytes // 4
+        rows = (48 << 30) // row_bytes  # 48 GiB of rows: far beyond L2 and the memory-side cache
+        table = torch.empty((rows, dim), dtype=torch.float32, device=device)
+        ids = torch.randint(0, rows, (n,), dtype=torch.int64, device=device, generator=gen)
+        plan = ops.GroupPlan()
+        plan.add_feature(table, pooling="none")
+        outbuf = torch.empty((n, dim), dtype=torch.float32, device=device)
+        ms = timed(lambda: ops.grouped_forward(plan, [ids], [None], with_backward=False, outputs=[outbuf]))
+        lines = -(-row_bytes // 128)  # 128-byte lines a row read costs
+        rows_out.append({
+            "row_bytes": row_bytes, "rows": n, "ms": ms, "rows_per_s": n / (ms * 1e-3),
+            "row_read_gbps": n * row_bytes / (ms * 1e-3) / 1e9,
+            "line_reads_per_s": n * lines / (ms * 1e-3),
+            "write_gbps": n * row_bytes / (ms * 1e-3) / 1e9,
+        })
+        del table, ids, outbuf, plan
+        gc.collect()
+        torch.cuda.empty_cache()
+    out["random_row_gather"] = rows_out
+    return out
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -1160,6 +1237,8 @@ def main() -> int:
                     help="summarise rocprofv3 --kernel-trace databases into --trace-out and exit (no GPU)")
     ap.add_argument("--trace-out", default=None)
     ap.add_argument("--trace-command", default="")
+    ap.add_argument("--ceilings", action="store_true",
+                    help="measure the copy and random-row-gather ceilings of this GPU and exit (one JSON line)")
     ap.add_argument("--layout", choices=["slot", "feature"], default="slot",
                     help="pooled outputs and their gradients: one [B, sum(dim)] token-slot buffer, or one [B, dim] "
                          "tensor per feature")
@@ -1183,6 +1262,9 @@ def main() -> int:
     import torch
 
     device = torch.device("cuda:0")
+    if args.ceilings:
+        print(json.dumps(ceilings(torch, device)), flush=True)
+        return 0
     head = measure(args.config, args, torch, device,
                    with_aux=not args.no_aux and not args.calibrate_copy)
     wl = head.pop("_wl")

@@ -9,6 +9,7 @@ synchronises the device unless its docstring says so.
 from __future__ import annotations
 
 import ctypes
+import weakref
 from dataclasses import dataclass, field
 from typing import Sequence
 
@@ -339,13 +340,20 @@ class KeyGroup:
 
     ``plan`` is the group as a plan of its own: the same table specs (their
     ``row_base`` counted within the group) and features, table indices
-    renumbered in ``tables`` order."""
+    renumbered in ``tables`` order.  A group that is the whole plan refers to
+    it weakly, so a plan and its groups form no reference cycle that would
+    keep its tables alive until the next garbage collection."""
 
     lo: int
     hi: int
     tables: list[int]
     rows: int
-    plan: "GroupPlan"
+    _plan: object
+
+    @property
+    def plan(self) -> "GroupPlan":
+        p = self._plan
+        return p() if isinstance(p, weakref.ref) else p
 
 
 class GroupPlan:
@@ -440,7 +448,8 @@ class GroupPlan:
         if self._groups is not None and self._groups_for == shape:
             return self._groups
         if self.total_rows < KEY_SPACE:
-            groups = [KeyGroup(0, len(self.features), list(range(len(self.tables))), self.total_rows, self)]
+            groups = [KeyGroup(0, len(self.features), list(range(len(self.tables))), self.total_rows,
+                               weakref.ref(self))]
             base = 0
             for t in self.tables:
                 t.row_base = base
