@@ -3,7 +3,7 @@
 Two dim-8 bf16 tables of 2.2e9 and 2.3e9 rows and a small fp32 table (about
 4.5e9 rows, 72 GB of weights and 18 GB of accumulators) are more rows than one
 32-bit key space holds, so the plan is cut into two key groups: the first
-table's features, then the second's and the third's.  Three paths run over
+table's features, then the second's and the third's.  These paths run over
 them and are checked against the CPU oracle on compact copies of the touched
 rows (rows above 2^31 of a table and keys above 2^31 of a group included):
 
@@ -15,7 +15,9 @@ rows (rows above 2^31 of a table and keys above 2^31 of a group included):
   path), with a feature order that reads the first table again after the
   second, so the op must reorder its features by table;
 * ``ops.grouped_forward`` + ``ops.backward_adagrad`` with a clip that scales
-  the gradient of both groups by one coefficient.
+  the gradient of both groups by one coefficient;
+* the drop-in modules (``ShardedEmbedding`` lookups, ``loss.backward()``,
+  ``ShardedRowWiseAdagrad.step()``).
 
 Untouched rows and accumulators of every table are checked bit for bit
 (checksums) after every SparseStep.
@@ -339,3 +341,63 @@ def test_functional_backward_adagrad_clips_across_key_groups(device, big):
         _check_update(f"functional table {t}", w_post[t], a_post[t], snap.w[t], snap.a[t], rr, g * coef,
                       s * coef + np.abs(g) * 1e-4, LR, EPS, RTOL["bf16" if bf else "fp32"], 1e-6 if bf else 1e-7, bf)
     say("key_groups", "functional step checked", f"{time.time() - t0:.1f}s")
+
+
+def test_dropin_modules_train_across_key_groups(device, big):
+    """ShardedEmbedding modules over the three tables and ShardedRowWiseAdagrad:
+    a pooled call over tables 0 and 1 (4.5e9 rows: two key groups) and an
+    unpooled call over tables 0 and 2, loss.backward() (table 0's two sparse
+    gradients accumulate), opt.step() -- every touched row and accumulator
+    against one oracle update of each table's coalesced gradient."""
+
+    from torch import nn
+
+    from mdl_amd.embeddings import (EmbeddingShardSpec, ShardedEmbedding, grouped_sharded_embedding_lookup,
+                                    pooled_embedding_lookup)
+    from mdl_amd.optim import ShardedRowWiseAdagrad
+
+    t0 = time.time()
+    tables, states = big
+    rng = np.random.default_rng(4503)
+    mods = []
+    for t, w in enumerate(tables):
+        spec = EmbeddingShardSpec(table_name=f"kg_{t}", strategy="row_wise", world_size=1)
+        m = ShardedEmbedding(2, int(w.size(1)), table_name=f"kg_{t}", shard_spec=spec, collect_stats=False,
+                             dtype=w.dtype).to(device)
+        m.weight = nn.Parameter(w)
+        m.num_embeddings = int(w.size(0))
+        mods.append(m)
+    opt = ShardedRowWiseAdagrad([m.weight for m in mods], lr=LR, eps=EPS)
+    for m, a in zip(mods, states):
+        opt.state[m.weight]["sum"] = a
+    feats = [(0, "mean"), (1, "sum"), (0, "none"), (2, "none")]
+    ids, lens = _draw(rng, feats)
+    touched = _touched_of(feats, ids)
+    _set_touched(tables, touched, rng)
+    snap = _Snapshot.__new__(_Snapshot)
+    snap.idx = [torch.from_numpy(u).to(device) for u in touched]
+    snap.w = [w.index_select(0, i).float().cpu().numpy() for w, i in zip(tables, snap.idx)]
+    snap.a = [a.index_select(0, i).cpu().numpy() for a, i in zip(states, snap.idx)]
+    x = [torch.from_numpy(v).to(device) for v in ids]
+    pooled = pooled_embedding_lookup([(mods[0], x[0], torch.from_numpy(lens[0]).to(device), "mean", "exclude"),
+                                      (mods[1], x[1], torch.from_numpy(lens[1]).to(device), "sum", "exclude")])
+    single = grouped_sharded_embedding_lookup([(mods[0], x[2]), (mods[2], x[3])])
+    outs = pooled + single
+    grads = _grads(rng, outs)
+    torch.autograd.backward(outs, grads)
+    opt.step()
+    torch.cuda.synchronize()
+    say("key_groups", "drop-in step done", f"{time.time() - t0:.1f}s")
+    w_post, a_post = snap.after(tables, states)
+    ref = _oracle_grads(feats, ids, lens, grads, touched, snap, [o.detach() for o in outs], "drop-in")
+    for t, (rr, g, s) in enumerate(ref):
+        # the drop-in's sparse gradients are stored in the table's dtype, as
+        # the reference's are: bf16 tables take the bf16 tolerance for state
+        bf = DTYPES[t] == torch.bfloat16
+        _check_update(f"drop-in table {t}", w_post[t], a_post[t], snap.w[t], snap.a[t], rr, g, s, LR, EPS,
+                      RTOL["bf16" if bf else "fp32"], 1e-6 if bf else 1e-7, bf,
+                      acc_rtol=RTOL["bf16" if bf else "fp32"])
+    say("key_groups", "drop-in step checked", f"{time.time() - t0:.1f}s")
+    for m in mods:
+        m.weight = None
+    del opt, mods
