@@ -700,7 +700,6 @@ def dropin_loop(torch, dev, wl, device, steps: int = 10) -> dict:
             "what": "ShardedEmbedding modules (pooled_embedding_lookup + grouped_sharded_embedding_lookup), "
                     "loss.backward() -> capacity-sized coalesced sparse grads, ShardedRowWiseAdagrad.step() "
                     "(one grouped launch); timed steps under torch.cuda.set_sync_debug_mode('error')"}
-    return out
 
 
 # ------------------------------------------------------------ cpu baseline --
