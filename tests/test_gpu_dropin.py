@@ -171,6 +171,55 @@ def test_state_dict_round_trip_keeps_fp32_accumulator(device):
     assert st["sum"].dtype == torch.float32
 
 
+def test_aliased_requests_merge_into_one_update(device):
+    """One table in several requests of one grouped call, and in a pooled and
+    a direct lookup of the same step (the reference's grouped alias worker,
+    tests/test_sharded_embedding.py:198-258, at world size 1): the outputs are
+    F.embedding's, and the table gets one row-wise Adagrad update with the sum
+    of every request's gradient."""
+
+    announce("aliased_requests")
+    user, item = _modules(device, [("user", 13, 4), ("item", 19, 4)])
+    full = [torch.arange(13 * 4, dtype=torch.float32).view(13, 4) / 10.0,
+            torch.arange(19 * 4, dtype=torch.float32).view(19, 4) / 11.0]
+    for m, w in zip((user, item), full):
+        w[0].zero_()
+        m.load_full_weight_(w.to(device))
+    user_ids = torch.tensor([1, 1, 4, 0])
+    item_ids = torch.tensor([2, 8, 8])
+    repeated_user_ids = torch.tensor([4, 7])
+    bag_ids = torch.tensor([7, 0, 3, 3, 12])
+    bag_lengths = torch.tensor([2, 0, 3])
+    opt = ShardedRowWiseAdagrad([user.weight, item.weight], lr=0.15, eps=1e-8)
+    actual = grouped_sharded_embedding_lookup(
+        [(user, user_ids.to(device)), (item, item_ids.to(device)), (user, repeated_user_ids.to(device))]
+    )
+    pooled = pooled_embedding_lookup([(user, bag_ids.to(device), bag_lengths.to(device), "mean", "exclude")])[0]
+    expected = [F.embedding(user_ids, full[0], padding_idx=0), F.embedding(item_ids, full[1], padding_idx=0),
+                F.embedding(repeated_user_ids, full[0], padding_idx=0)]
+    for a, e in zip(actual, expected):
+        torch.testing.assert_close(a.cpu(), e)
+    loss = sum(o.square().sum() for o in actual) + pooled.square().sum()
+    loss.backward()
+    opt.step()
+
+    def grads(ids, lengths, out, mode):
+        return O.per_id_grads(ids.numpy(), None if lengths is None else lengths.numpy(),
+                              2.0 * out.detach().double().cpu().numpy(), mode, "exclude")
+
+    parts = {0: [grads(user_ids, None, actual[0], "none"), grads(repeated_user_ids, None, actual[2], "none"),
+                 grads(bag_ids, bag_lengths, pooled, "mean")],
+             1: [grads(item_ids, None, actual[1], "none")]}
+    for t, m in enumerate((user, item)):
+        rows = np.concatenate([r for r, _ in parts[t]])
+        vals = np.concatenate([v for _, v in parts[t]])
+        r, v = O.coalesce(rows, vals)
+        w_ref, a_ref = O.rowwise_adagrad(full[t].numpy(), np.zeros(full[t].shape[0], np.float32), r, v, 0.15, 1e-8)
+        got = m.weight.detach().cpu().numpy()
+        assert np.allclose(got, w_ref, rtol=1e-5, atol=1e-6), t
+        assert np.allclose(opt.state[m.weight]["sum"].cpu().numpy(), a_ref, rtol=1e-5, atol=1e-7), t
+
+
 @pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
 def test_training_steps_match_oracle(device, dtype):
     """Lookups + mean/sum pooling + loss.backward() + optimizer.step(), 3 steps."""
