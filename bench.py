@@ -1110,6 +1110,10 @@ def measure(name: str, args, torch, device, *, with_aux: bool = False) -> dict:
             "unit": "GB/s",
             "frac": dom["achieved_gbps"] / PEAK_HBM_GBPS,
             "traffic": traffic,
+            # the measured traffic over the same time against the same peak:
+            # how busy HBM is in the bytes it moves (whole lines), where frac
+            # counts only the bytes the algorithm needs
+            "traffic_frac": None if traffic is None else traffic / (dom["ms"] * 1e-3) / 1e9 / PEAK_HBM_GBPS,
             "kernel_ms": dom["ms"],
             "alg_bytes_per_launch": dom["alg_bytes_per_launch"],
         },
