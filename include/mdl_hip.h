@@ -71,13 +71,11 @@ enum { MDL_TRUNCATE_HEAD = 0, MDL_TRUNCATE_TAIL = 1 };
  * (1 << variant) is set, 0 meaning all.  mdl_feature_classes and
  * mdl_table_classes compute the mask of a host descriptor array with the
  * kernels' own rule; a mask that misses a present variant skips its rows.
- * mdl_table_classes also sets MDL_CLASSES_UNSUPPORTED when a table's rows
- * are wider than the backward reduce covers (dim > 64 * C for the table's
- * lane width C: fp32 rows beyond 256 elements unless dim is a multiple of 8,
- * any row beyond 512, rows that are not 16-byte aligned beyond 64); every
- * backward call that reduces rows returns MDL_ERR_UNSUPPORTED for a mask with
- * that bit (a mask of 0 skips the check: the caller vouches for the widths,
- * and rows of a too-wide table are then left untouched). */
+ * Rows of any width are reduced: a row wider than 64 lanes of C elements
+ * cover (dim > 64 * C) is walked by one wave in column blocks of 64 * C.
+ * MDL_CLASSES_UNSUPPORTED is reserved: mdl_table_classes never sets it, and
+ * every backward call that reduces rows returns MDL_ERR_UNSUPPORTED for a
+ * mask carrying it. */
 #define MDL_CLASSES_UNSUPPORTED 0x80000000u
 enum {
   MDL_CLASS_F32_VEC = 0, MDL_CLASS_F32 = 1, MDL_CLASS_BF16_VEC = 2,

@@ -625,10 +625,134 @@ __device__ __forceinline__ void reduce_chunk_body(const BwdArgs& a, int64_t c, c
   if (lane == 0) a.chunk_flags[c] = (head_open ? kHeadOpen : 0) | (tail_open ? kTailOpen : 0) | (single ? kSingle : 0);
 }
 
+
+// The row-wise Adagrad update of a wide row (dim > 64 * C) whose summed
+// gradient has squared norm ss: the accumulator first, then each column block
+// of the row from grad(b, v), which yields block b of the summed gradient.
+// The arithmetic is Reducer::finish's.
+template <int kMode, typename TW, typename TG, int C, typename GradOf>
+__device__ __forceinline__ void wide_update(const Reducer<kMode, TW, TG, C>& R, uint32_t key, float ss,
+                                            GradOf&& grad) {
+  constexpr int kSpan = kWave * C;
+  const BwdArgs& a = R.a;
+  const int lane = lane_id();
+  const int64_t row = (int64_t)key - R.row_base;
+  const float acc = ld_policy<kUpdatePolicy>(R.state + row) + (ss * (R.scale * R.scale)) / R.fdim;
+  if (lane == 0) st_policy<kUpdatePolicy>(R.state + row, acc);
+  const float den = sqrtf(acc) + a.eps;
+  const int nblk = (R.dim + kSpan - 1) / kSpan;
+  for (int b = 0; b < nblk; ++b) {
+    float v[C];
+    grad(b, v);
+    const int col = b * kSpan + lane * C;
+    if (col < R.dim) {
+      float w[C];
+      RowIO<TW, C>::template load<kUpdatePolicy>(R.W + row * R.dim + col, w);
+#pragma unroll
+      for (int k = 0; k < C; ++k) w[k] = w[k] - a.lr * ((v[k] * R.scale) / den);
+      RowIO<TW, C>::template store<kUpdatePolicy>(R.W + row * R.dim + col, w);
+    }
+  }
+}
+
+// Rows wider than the wave's lanes cover at once (dim > 64 * C): the wave
+// takes the chunk's runs one at a time and walks each row in column blocks of
+// 64 * C elements, reading a run's gradient rows once per block -- twice for
+// the update, whose step needs the squared norm of the whole row before any
+// element changes (as adagrad_wide_rows does).  Runs cross chunks as in the
+// main path: a run that began in an earlier chunk and ends here leaves its
+// part in part_first, the run open at the chunk's end in part_last, for the
+// fix-up.  Entries of a run add up in their sorted order (deterministic).
+// Wide rows are rare (the reference's tables are 8-128 wide); this path is
+// general rather than fast.
+template <int kMode, bool kOne, typename TW, typename TG, int C>
+__device__ void reduce_chunk_wide(const BwdArgs& a, int64_t c, const ChunkDesc& d,
+                                  const Reducer<kMode, TW, TG, C>& R, const ChunkStage& st) {
+  constexpr int kSpan = kWave * C;
+  constexpr int kU = 4;  // entries whose gradient rows load together
+  const int lane = lane_id();
+  const int len = d.len;
+  const int nblk = (R.dim + kSpan - 1) / kSpan;
+  const bool head_open = st.key[0] == st.key[1];
+  const bool tail_open = st.key[len + 1] == st.key[len];
+  const bool single = head_open && tail_open && st.key[1] == st.key[len];
+  // Sum of entries [i0, i1)'s gradients over this lane's C columns of block b.
+  auto run_sum = [&](int i0, int i1, int b, float (&v)[C]) {
+    const int col = b * kSpan + lane * C;
+    const bool col_ok = col < R.dim;
+    zero(v);
+    for (int e = i0; e < i1; e += kU) {
+      float g[kU][C], inv[kU];
+#pragma unroll
+      for (int u = 0; u < kU; ++u) {
+        const bool ok = e + u < i1;
+        const uint32_t pay = st.pay[ok ? e + u : i0];
+        bool mean = false;
+        const TG* gp = R.template grad_row<kOne>(pay, mean);
+        RowIO<TG, C>::load(ok && col_ok ? gp + col : zero_row<TG>(), g[u]);
+        const float cnt = ld_policy(ok && mean ? a.bag_count + pay : zero_row<float>());
+        inv[u] = mean ? __builtin_amdgcn_rcpf(fmaxf(cnt, 1.f)) : 1.f;
+      }
+#pragma unroll
+      for (int u = 0; u < kU; ++u)
+#pragma unroll
+        for (int k = 0; k < C; ++k) v[k] = fmaf(g[u][k], inv[u], v[k]);
+    }
+  };
+  auto to_parts = [&](float* part, int i0, int i1) {
+    for (int b = 0; b < nblk; ++b) {
+      float v[C];
+      run_sum(i0, i1, b, v);
+      const int col = b * kSpan + lane * C;
+      if (col < R.dim) {
+#pragma unroll
+        for (int k = 0; k < C; ++k) part[c * a.max_dim + col + k] = v[k];
+      }
+    }
+  };
+  const int64_t hb = kMode == kModeCoalesce ? a.head_base[c] : 0;
+  float ss_acc = 0.f;
+  for (int i = 0; i < len;) {
+    const uint32_t key = st.key[i + 1];
+    int j = i + 1;
+    while (j < len && st.key[j + 1] == key) ++j;  // the run is entries [i, j)
+    if (j == len && tail_open) {
+      to_parts(a.part_last, i, j);  // continues in the next chunk (the whole chunk when single)
+    } else if (i == 0 && head_open) {
+      to_parts(a.part_first, i, j);  // began in an earlier chunk: the fix-up finishes it
+    } else if (kMode == kModeCoalesce) {
+      const int64_t local = hb + (int64_t)st.hc[j] - 1 - a.unique_range[2 * R.t];
+      int64_t* rows = (int64_t*)a.rows_addr[R.t];
+      TW* vals = (TW*)a.values_addr[R.t];
+      if (lane == 0) st_policy(rows + local, (int64_t)key - R.row_base);
+      for (int b = 0; b < nblk; ++b) {
+        float v[C];
+        run_sum(i, j, b, v);
+        const int col = b * kSpan + lane * C;
+        if (col < R.dim) RowIO<TW, C>::template store<kUpdatePolicy>(vals + local * R.dim + col, v);
+      }
+    } else {
+      float ss = 0.f;
+      for (int b = 0; b < nblk; ++b) {
+        float v[C];
+        run_sum(i, j, b, v);
+        ss += R.row_sumsq(v);
+      }
+      if (kMode == kModeSumsq) {
+        ss_acc += ss;
+      } else if (R.row_ok(key)) {
+        wide_update(R, key, ss, [&](int b, float (&v)[C]) { run_sum(i, j, b, v); });
+      }
+    }
+    i = j;
+  }
+  if (kMode == kModeSumsq && lane == 0) a.chunk_ss[c] = ss_acc;
+  if (lane == 0) a.chunk_flags[c] = (head_open ? kHeadOpen : 0) | (tail_open ? kTailOpen : 0) | (single ? kSingle : 0);
+}
+
 template <int kMode, typename TW, typename TG, int C>
 __device__ __forceinline__ void reduce_chunk(const BwdArgs& a, int64_t c, const ChunkDesc& d, ChunkStage& st) {
   Reducer<kMode, TW, TG, C> R(a, d.table);
-  if (R.dim > kWave * C) return;  // flagged by mdl_table_classes; the call is refused
   const int lane = lane_id();
   const uint32_t kNone = 0xffffffffu;
   const int len = d.len;
@@ -659,14 +783,71 @@ __device__ __forceinline__ void reduce_chunk(const BwdArgs& a, int64_t c, const 
     __builtin_amdgcn_wave_barrier();
     __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
   }
-  if (R.single >= 0) reduce_chunk_body<kMode, true, TW, TG, C>(a, c, d, R, st);
-  else reduce_chunk_body<kMode, false, TW, TG, C>(a, c, d, R, st);
+  if (R.dim > kWave * C) {
+    if (R.single >= 0) reduce_chunk_wide<kMode, true, TW, TG, C>(a, c, d, R, st);
+    else reduce_chunk_wide<kMode, false, TW, TG, C>(a, c, d, R, st);
+  } else if (R.single >= 0) {
+    reduce_chunk_body<kMode, true, TW, TG, C>(a, c, d, R, st);
+  } else {
+    reduce_chunk_body<kMode, false, TW, TG, C>(a, c, d, R, st);
+  }
+}
+
+
+// The fix-up of a wide row (dim > 64 * C): the run's parts, chunk s's to
+// chunk c - 1's part_last and chunk c's part_first, added in chunk order per
+// column block; the update reads them twice (squared norm, then the step).
+template <int kMode, typename TW, typename TG, int C>
+__device__ void fixup_chunk_wide(const BwdArgs& a, int64_t c, const ChunkDesc& d,
+                                 const Reducer<kMode, TW, TG, C>& R, int64_t s) {
+  constexpr int kSpan = kWave * C;
+  const int lane = lane_id();
+  const int nblk = (R.dim + kSpan - 1) / kSpan;
+  auto parts = [&](int b, float (&v)[C]) {
+    const int col = b * kSpan + lane * C;
+    zero(v);
+    if (col < R.dim) {
+      for (int64_t q = s; q < c; ++q) {
+        const float* pl = a.part_last + q * a.max_dim + col;
+#pragma unroll
+        for (int k = 0; k < C; ++k) v[k] += pl[k];
+      }
+      const float* pf = a.part_first + c * a.max_dim + col;
+#pragma unroll
+      for (int k = 0; k < C; ++k) v[k] += pf[k];
+    }
+  };
+  const uint32_t key = a.keys[d.begin];
+  if (kMode == kModeCoalesce) {
+    const int64_t local = a.head_base[c] - 1 - a.unique_range[2 * R.t];
+    int64_t* rows = (int64_t*)a.rows_addr[R.t];
+    TW* vals = (TW*)a.values_addr[R.t];
+    if (lane == 0) st_policy(rows + local, (int64_t)key - R.row_base);
+    for (int b = 0; b < nblk; ++b) {
+      float v[C];
+      parts(b, v);
+      const int col = b * kSpan + lane * C;
+      if (col < R.dim) RowIO<TW, C>::template store<kUpdatePolicy>(vals + local * R.dim + col, v);
+    }
+    return;
+  }
+  float ss = 0.f;
+  for (int b = 0; b < nblk; ++b) {
+    float v[C];
+    parts(b, v);
+    ss += R.row_sumsq(v);
+  }
+  if (kMode == kModeSumsq) {
+    // The reduce of chunk c wrote its own runs' share before this launch.
+    if (lane == 0) a.chunk_ss[c] += ss;
+  } else if (R.row_ok(key)) {
+    wide_update(R, key, ss, parts);
+  }
 }
 
 template <int kMode, typename TW, typename TG, int C>
 __device__ __forceinline__ void fixup_chunk(const BwdArgs& a, int64_t c, const ChunkDesc& d, int32_t flags) {
   Reducer<kMode, TW, TG, C> R(a, d.table);
-  if (R.dim > kWave * C) return;  // flagged by mdl_table_classes; the call is refused
   // Walk back over chunks that lie wholly inside the run to the chunk holding
   // its first entry (never past the table's first chunk).
   // The wave reads 64 chunks' flags per step (a Zipf head row spans many
@@ -683,6 +864,10 @@ __device__ __forceinline__ void fixup_chunk(const BwdArgs& a, int64_t c, const C
       break;
     }
     s -= kWave;
+  }
+  if (R.dim > kWave * C) {
+    fixup_chunk_wide<kMode, TW, TG, C>(a, c, d, R, s);
+    return;
   }
   float v[C];
   zero(v);
@@ -779,8 +964,6 @@ __global__ MDL_OCCUPANCY __launch_bounds__(kBwdWaves * kWave) void bwd_reduce_ke
 static int validate_tables(const char* who, int32_t T, int32_t max_dim, int64_t n) {
   if (T <= 0) return fail(MDL_ERR_INVALID, std::string(who) + ": need at least one table");
   if (max_dim <= 0) return fail(MDL_ERR_INVALID, std::string(who) + ": max_dim must be positive");
-  if (max_dim > kWave * MDL_MAX_WIDTH)
-    return fail(MDL_ERR_UNSUPPORTED, std::string(who) + ": rows wider than 512 elements");
   if (n < 0 || n > 0xffffffffll) return fail(MDL_ERR_UNSUPPORTED, std::string(who) + ": n outside [0, 2^32)");
   return MDL_OK;
 }
@@ -788,7 +971,7 @@ static int validate_tables(const char* who, int32_t T, int32_t max_dim, int64_t 
 static int validate_classes(const char* who, uint32_t classes) {
   if (classes & MDL_CLASSES_UNSUPPORTED)
     return fail(MDL_ERR_UNSUPPORTED,
-                std::string(who) + ": a table's rows are wider than its lanes cover (dim > 64 x lane width)");
+                std::string(who) + ": the class mask carries the reserved MDL_CLASSES_UNSUPPORTED bit");
   return MDL_OK;
 }
 
@@ -875,7 +1058,7 @@ struct LaunchReduce {
 static int run_reduce(const BwdArgs& a, uint32_t variants, hipStream_t s) {
   if (variants & MDL_CLASSES_UNSUPPORTED)
     return fail(MDL_ERR_UNSUPPORTED,
-                "backward: a table's rows are wider than its lanes cover (dim > 64 x lane width)");
+                "backward: the class mask carries the reserved MDL_CLASSES_UNSUPPORTED bit");
   const int64_t blocks = (a.max_chunks + kBwdWaves - 1) / kBwdWaves;
   if (blocks > 0x7fffffffll) return fail(MDL_ERR_UNSUPPORTED, "backward: too many chunks");
   int rc = for_each_class(variants, LaunchReduce<false>{a, s, blocks});
@@ -990,7 +1173,6 @@ uint32_t mdl_table_classes(const mdl_table* tables, int32_t num_tables) {
     const mdl_table& t = tables[i];
     const int v = variant_of(t.wdtype, t.gdtype, table_vec_of(t.weight, t.dim, t.wdtype), t.dim);
     m |= 1u << v;
-    if (t.dim > kWave * variant_elems(v)) m |= MDL_CLASSES_UNSUPPORTED;
   }
   return m;
 }

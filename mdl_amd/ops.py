@@ -836,13 +836,6 @@ def _build_tables_array(plan: GroupPlan, feats: np.ndarray) -> np.ndarray:
         if len(gd) > 1:
             raise TypeError("features that share a table must share an output dtype")
         rec["gdtype"] = gd.pop() if gd else dtype_code(w.dtype)
-        esize = w.element_size()
-        vec = w.data_ptr() % 16 == 0 and (int(w.size(1)) * esize) % 16 == 0
-        lanes_cover = 64 * lane_elems(int(w.size(1)), esize, vec)
-        if int(w.size(1)) > lanes_cover:
-            raise NotImplementedError(
-                f"backward supports rows of at most {lanes_cover} elements for this table layout"
-            )
     return tables
 
 
@@ -1465,11 +1458,6 @@ def coalesce_rows(
     tables[0]["wdtype"] = dtype_code(values.dtype)
     tables[0]["feature"] = 0
     tables[0]["gdtype"] = dtype_code(values.dtype)
-    if table_classes(tables) & _lib.MDL_CLASSES_UNSUPPORTED:
-        raise NotImplementedError(
-            f"coalescing rows of {dim} {values.dtype} elements is not supported: the reduce covers at most 64 "
-            "lanes of one 16-byte vector (one element when rows are not 16-byte aligned)"
-        )
     res = ForwardResult(
         plan=plan, device=device, ids=indices, offsets=None, outputs=[values], feats=feats,
         keys=keys, payload=payload, bag_count=None, error_count=err,

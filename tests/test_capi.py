@@ -90,8 +90,11 @@ def test_invalid_arguments_fail_before_any_launch():
     rc = lib.mdl_backward_adagrad(None, 0, None, 0, 8, None, None, 10, None, 8, None, 0.1, 1e-8, None, None, 0, 0,
                                   None)
     assert rc == -1 and b"table" in lib.mdl_last_error()
+    rc = lib.mdl_backward_apply(None, 0, None, 1, 0, None, None, 10, 8, None, 0.1, 1e-8, None, None, 0, 0, None)
+    assert rc == -1 and b"max_dim" in lib.mdl_last_error()
+    # rows of any width pass validation (wide ones are walked in column blocks): no workspace is what fails
     rc = lib.mdl_backward_apply(None, 0, None, 1, 600, None, None, 10, 8, None, 0.1, 1e-8, None, None, 0, 0, None)
-    assert rc == -4 and b"512" in lib.mdl_last_error()
+    assert rc == -3
     rc = lib.mdl_forward(None, 0, None, 1, None, -1, None, None, None, None, 0, None, None, 0, None)
     assert rc == -1
     rc = lib.mdl_rowwise_adagrad(None, _lib.MDL_F32, 10, 4, 4, None, None, 3, None, _lib.MDL_BF16, 4, 0.1,
@@ -159,12 +162,13 @@ def test_lane_width_rule(dim, esize, vec, expect):
 
 
 def test_lane_width_rule_matches_the_library():
-    """The host rule (used to reject rows too wide for the backward) and the
-    library's variant of a table agree for every dim and dtype."""
+    """The host rule and the library's variant of a table agree for every dim
+    and dtype, rows wider than 64 lanes cover included (the reduce walks them
+    in column blocks, so no mask carries the reserved unsupported bit)."""
     lib = _lib.lib()
     tables = np.zeros(1, dtype=_lib.TABLE_DTYPE)
     for wd, esize in ((_lib.MDL_F32, 4), (_lib.MDL_BF16, 2)):
-        for dim in range(1, 300):
+        for dim in list(range(1, 300)) + [520, 600, 1024, 1030]:
             tables["wdtype"] = wd
             tables["gdtype"] = wd
             tables["dim"] = dim
@@ -174,14 +178,15 @@ def test_lane_width_rule_matches_the_library():
             c = ops.lane_elems(dim, esize, vec)
             cls = (0 if wd == _lib.MDL_F32 else 2) + (0 if vec else 1)
             w = 0 if c == 1 else {4: 0, 8: 1, 16: 2}[c]
-            wide = _lib.MDL_CLASSES_UNSUPPORTED if dim > 64 * c else 0
-            assert m == (1 << (3 * cls + w)) | wide, (wd, dim)
+            assert m == 1 << (3 * cls + w), (wd, dim)
 
 
 @pytest.mark.parametrize("dim,dtype", [(66, "f32"), (100, "bf16"), (300, "f32"), (600, "f32")])
-def test_too_wide_rows_are_refused_not_skipped(dim, dtype):
-    """Rows the backward reduce cannot cover are reported by the class mask,
-    and every reducing call refuses that mask before it launches anything."""
+def test_wide_rows_have_a_class_and_the_reserved_bit_is_refused(dim, dtype):
+    """Rows wider than 64 lanes cover get their table's ordinary class (the
+    reduce walks them in column blocks); a mask carrying the reserved
+    MDL_CLASSES_UNSUPPORTED bit is refused by every reducing call before it
+    launches anything."""
 
     lib = _lib.lib()
     tables = np.zeros(1, dtype=_lib.TABLE_DTYPE)
@@ -191,7 +196,8 @@ def test_too_wide_rows_are_refused_not_skipped(dim, dtype):
     tables["dim"] = dim
     tables["weight"] = 4096
     m = lib.mdl_table_classes(tables.ctypes.data, 1)
-    assert m & _lib.MDL_CLASSES_UNSUPPORTED
+    assert m and not m & _lib.MDL_CLASSES_UNSUPPORTED
+    m |= _lib.MDL_CLASSES_UNSUPPORTED
     for call in (
         lambda: lib.mdl_backward_apply(None, 1, None, 1, 512, None, None, 10, 8, None, 0.1, 1e-8, None, None, 0,
                                        m, None),
@@ -201,7 +207,7 @@ def test_too_wide_rows_are_refused_not_skipped(dim, dtype):
         lambda: lib.mdl_backward_adagrad(None, 1, None, 1, 512, None, None, 10, None, 8, None, 0.1, 1e-8, None, None,
                                          0, m, None),
     ):
-        assert call() == -4 and b"wider" in lib.mdl_last_error()
+        assert call() == -4 and b"reserved" in lib.mdl_last_error()
 
 
 def test_abi_version_matches_binding():

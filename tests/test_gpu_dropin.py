@@ -225,8 +225,22 @@ def test_training_steps_match_oracle(device, dtype):
     """Lookups + mean/sum pooling + loss.backward() + optimizer.step(), 3 steps."""
 
     announce("training_steps", dtype)
-    rng = np.random.default_rng(90)
-    specs = [("bag_a", 2000, 32), ("bag_b", 500, 16), ("single", 3000, 64)]
+    _train_and_check(device, dtype, [("bag_a", 2000, 32), ("bag_b", 500, 16), ("single", 3000, 64)], seed=90)
+
+
+@pytest.mark.parametrize("dtype,dims", [(torch.float32, (600, 66, 1030)), (torch.bfloat16, (600, 100, 72))])
+def test_wide_rows_train_like_the_reference(device, dtype, dims):
+    """Tables of any width train, as with the reference's F.embedding and
+    Triton update: rows wider than 64 lanes cover, aligned or not (fp32 600,
+    1030 and 66, bf16 600 and 100)."""
+
+    announce("training_steps_wide", dtype, dims)
+    _train_and_check(device, dtype, [("bag_a", 2000, dims[0]), ("bag_b", 500, dims[1]), ("single", 3000, dims[2])],
+                     seed=91)
+
+
+def _train_and_check(device, dtype, specs, seed):
+    rng = np.random.default_rng(seed)
     mods = _modules(device, specs)
     for m in mods:
         with torch.no_grad():
@@ -234,15 +248,23 @@ def test_training_steps_match_oracle(device, dtype):
             w[0] = 0
             m.weight.data = w.to(dtype).to(device)
     opt = ShardedRowWiseAdagrad([m.weight for m in mods], lr=0.05, eps=1e-8)
-    W = [m.weight.detach().float().cpu().numpy().copy() for m in mods]
-    A = [np.zeros(m.weight.shape[0], np.float32) for m in mods]
+    # fp32: 1e-5 relative; bf16 storage: 1e-2 relative.  A bf16 table's
+    # sparse gradient is stored in bf16, as the reference's is, so the oracle
+    # rounds its coalesced gradient to bf16 before the fp32 update too (else a
+    # weight that the step moves across zero differs by that rounding times
+    # the step, not by a fraction of itself).  Each step is checked from the
+    # tables and accumulators it started from: a one-unit bf16 rounding
+    # difference of one step then cannot grow over the next ones.
+    tol = 1e-5 if dtype == torch.float32 else 1e-2
     B = 128
     for step in range(3):
+        W = [m.weight.detach().float().cpu().numpy().copy() for m in mods]
+        A = [opt.state[m.weight]["sum"].cpu().numpy().copy() for m in mods]
         la = rng.integers(0, 12, size=B)
         lb = rng.integers(1, 5, size=B)
-        xa = rng.zipf(1.2, size=int(la.sum())) % 2000
-        xb = rng.integers(0, 500, size=int(lb.sum()))
-        xs = rng.integers(0, 3000, size=B)
+        xa = rng.zipf(1.2, size=int(la.sum())) % specs[0][1]
+        xb = rng.integers(0, specs[1][1], size=int(lb.sum()))
+        xs = rng.integers(0, specs[2][1], size=B)
         opt.zero_grad(set_to_none=True)
         pooled = pooled_embedding_lookup([
             (mods[0], torch.from_numpy(xa).to(device), torch.from_numpy(la).to(device), "mean", "exclude"),
@@ -260,15 +282,13 @@ def test_training_steps_match_oracle(device, dtype):
         rs, vs = O.per_id_grads(xs, None, grads[2].float().cpu().numpy(), "none", "exclude")
         for t, (r, v) in enumerate(((ra, va), (rb, vb), (rs, vs))):
             r, v = O.coalesce(r, v)
-            W[t], A[t] = O.rowwise_adagrad(W[t], A[t], r, v, 0.05, 1e-8, is_bf16=dtype == torch.bfloat16)
-    # fp32: 1e-5 relative; bf16 storage: 1e-2 relative (the sparse gradient
-    # values are bf16, as the reference's are, before the fp32 update)
-    tol = 1e-5 if dtype == torch.float32 else 1e-2
-    for t, m in enumerate(mods):
-        got = m.weight.detach().float().cpu().numpy()
-        assert np.all(np.abs(got - W[t]) <= tol * np.abs(W[t]) + tol * 1e-1), t
-        s = opt.state[m.weight]["sum"].cpu().numpy()
-        assert np.all(np.abs(s - A[t]) <= tol * np.abs(A[t]) + 1e-6), t
+            if dtype == torch.bfloat16:
+                v = torch.from_numpy(v).to(torch.bfloat16).double().numpy()
+            w_ref, a_ref = O.rowwise_adagrad(W[t], A[t], r, v, 0.05, 1e-8, is_bf16=dtype == torch.bfloat16)
+            got = mods[t].weight.detach().float().cpu().numpy()
+            assert np.all(np.abs(got - w_ref) <= tol * np.abs(w_ref) + tol * 1e-1), (step, t)
+            st = opt.state[mods[t].weight]["sum"].cpu().numpy()
+            assert np.all(np.abs(st - a_ref) <= tol * np.abs(a_ref) + 1e-6), (step, t)
 
 
 @pytest.mark.parametrize("order", ["oldest_to_newest", "newest_to_oldest"])

@@ -619,15 +619,89 @@ def test_coalesce_rows_matches_torch(device):
     assert_close(v.cpu().numpy(), vv, 1e-5, 1e-6, vabs)
 
 
-@pytest.mark.parametrize("dim,dtype", [(66, torch.float32), (100, torch.bfloat16), (600, torch.float32)])
-def test_coalesce_rows_refuses_rows_too_wide(device, dim, dtype):
-    """The backward reduce covers 64 lanes of a row; wider rows raise
-    instead of returning unwritten memory as a gradient."""
-    announce("coalesce_rows_too_wide", dim, dtype)
-    idx = torch.tensor([3, 1, 3], dtype=torch.int64, device=device)
-    vals = torch.ones((3, dim), dtype=dtype, device=device)
-    with pytest.raises(NotImplementedError):
-        ops.coalesce_rows(idx, vals, 10)
+# Rows wider than 64 lanes cover (fp32 300 with 4 per lane, 600 and 1030
+# unaligned, 66 unaligned; bf16 100 unaligned, 600 with 8 per lane): one wave
+# per run walks them in column blocks.
+WIDE = [(66, torch.float32), (300, torch.float32), (600, torch.float32), (1030, torch.float32),
+        (100, torch.bfloat16), (600, torch.bfloat16)]
+
+
+@pytest.mark.parametrize("dim,dtype", WIDE)
+def test_coalesce_rows_wide_rows_match_oracle(device, dim, dtype):
+    announce("coalesce_rows_wide", dim, dtype)
+    rng = np.random.default_rng(72 + dim)
+    n, rows = 6000, 900
+    idx = (rng.zipf(1.2, size=n) % rows).astype(np.int64)
+    idx[: n // 3] = 5  # a run over many chunks (the fix-up)
+    vals = torch.from_numpy(rng.standard_normal((n, dim)).astype(np.float32)).to(dtype)
+    r, v = ops.coalesce_rows(torch.from_numpy(idx).to(device), vals.to(device), rows)
+    rr, vv = O.coalesce(idx, vals.float().numpy().astype(np.float64))
+    _, vabs = O.coalesce(idx, np.abs(vals.float().numpy().astype(np.float64)))
+    assert np.array_equal(r.cpu().numpy(), rr)
+    assert_close(to_np(v), vv, RTOL[dtype], 1e-5 if dtype == torch.float32 else 1e-2, vabs)
+
+
+@pytest.mark.parametrize("hot", [False, True])
+@pytest.mark.parametrize("dim,dtype", WIDE)
+def test_fused_backward_wide_rows_match_oracle(device, dim, dtype, hot):
+    """Pooled (mean, sum) and unpooled features on a wide table beside a
+    narrow one, through the fused reduce + row-wise Adagrad, the coalesce and
+    the clip's squared norm."""
+
+    announce("fused_backward_wide", dim, dtype, hot)
+    rng = np.random.default_rng(80 + dim + hot)
+    rows, dims = [700, 3000], [dim, 32]
+    B = 200
+    tabs = [_table(rng, r, d, dtype, device) for r, d in zip(rows, dims)]
+    states = [torch.from_numpy(rng.random(r).astype(np.float32)).to(device) for r in rows]
+    plan = ops.GroupPlan()
+    ids, lens, meta = [], [], []
+    for t, mode in ((0, "mean"), (1, "sum"), (0, "none"), (0, "sum")):
+        plan.add_feature(tabs[t], pooling=mode, null_policy="exclude", state=states[t])
+        ln = None if mode == "none" else rng.integers(0, 30, size=B)
+        m = B if ln is None else int(ln.sum())
+        x = (rng.zipf(1.2, size=m) % rows[t]) if hot else rng.integers(0, rows[t], size=m)
+        if hot:
+            x[: m // 2] = 7
+        x[::13] = 0
+        ids.append(torch.from_numpy(np.asarray(x, dtype=np.int64)).to(device))
+        lens.append(None if ln is None else torch.from_numpy(ln).to(device))
+        meta.append((t, mode, np.asarray(x), ln))
+    res = ops.grouped_forward(plan, ids, lens, with_backward=True)
+    grads = [torch.from_numpy(rng.standard_normal(tuple(o.shape)).astype(np.float32)).to(dtype).to(device)
+             for o in res.outputs]
+    expect, vabs = [], []
+    for t in range(2):
+        rs, vs = [], []
+        for f, (tt, mode, x, ln) in enumerate(meta):
+            if tt == t:
+                r, v = O.per_id_grads(x, ln, to_np(grads[f]).reshape(-1, dims[t]), mode, "exclude")
+                rs.append(r)
+                vs.append(v)
+        expect.append(O.coalesce(np.concatenate(rs), np.concatenate(vs)))
+        vabs.append(O.coalesce(np.concatenate(rs), np.abs(np.concatenate(vs)))[1])
+    tol = 1e-5 if dtype == torch.float32 else 1e-2
+    out = ops.backward_coalesce(res, grads)
+    for t in range(2):
+        rows_t, vals_t = out[t]
+        assert np.array_equal(rows_t.cpu().numpy(), expect[t][0]), t
+        assert_close(to_np(vals_t), expect[t][1], RTOL[dtype], tol, vabs[t])
+    # The clipped update (sort, squared norm, coefficient, apply) with a bound
+    # the norm stays under: the coefficient is 1 and the step the plain one.
+    w0 = [to_np(t).copy() for t in tabs]
+    a0 = [s.cpu().numpy().copy() for s in states]
+    lr, eps = 0.01, 1e-8
+    res = ops.grouped_forward(plan, ids, lens, with_backward=True)
+    norm = ops.backward_adagrad(res, grads, lr=lr, eps=eps, clip_norm=1e30)
+    ref = np.sqrt(sum(float((v.astype(np.float64) ** 2).sum()) for _, v in expect))
+    assert abs(float(norm.item()) - ref) <= 1e-4 * ref
+    for t in range(2):
+        rr, vv = expect[t]
+        wexp, aexp = O.rowwise_adagrad(w0[t], a0[t], rr, vv, lr, eps, is_bf16=dtype == torch.bfloat16)
+        assert_close(states[t].cpu().numpy(), aexp, 1e-5, 1e-7)
+        assert_close(to_np(tabs[t]), wexp, RTOL[dtype], 1e-6 if dtype == torch.float32 else 1e-2)
+        untouched = np.setdiff1d(np.arange(rows[t]), rr)
+        assert np.array_equal(to_np(tabs[t])[untouched], w0[t][untouched])
 
 
 def _oracle_step_pooled(W, rows, dims, pools, ids, lens, grad, lr, eps, accs=None):
