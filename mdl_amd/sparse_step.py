@@ -421,6 +421,28 @@ class SparseStep:
         self._graph.replay()
 
 
+class _SeqGroup:
+    """Device state of one key group of a sequence step: the packed sort
+    entries of its features (one scan over their rows places them), its
+    tables, backward descriptors and workspace."""
+
+    lo: int
+    hi: int
+    r0: int
+    r1: int
+    cap: int
+    offsets: Tensor
+    scan_ws: Tensor
+    keys: Tensor
+    payload: Tensor
+    feats_bwd: np.ndarray
+    feats_bwd_dev: Tensor
+    tables: np.ndarray
+    tables_dev: Tensor
+    bwd_classes: int
+    ws: Tensor
+
+
 class SequenceStep:
     """Fused step over sequence features (long user-behaviour histories).
 
@@ -434,6 +456,11 @@ class SequenceStep:
     entries (the positions that reach the window), placed each step by one
     scan of those clamped lengths on the device, so the backward sorts no
     padding and any lengths of a later batch are honoured.
+
+    A plan of 2^32 - 1 rows or more is cut into key groups
+    (``GroupPlan.groups``): each group's features pack their entries into a
+    key buffer of their own, placed by a scan over their rows only, and each
+    group has its own sort and reduce.
 
     ``micro_batches=k`` accumulates gradients as ``SparseStep`` does: k
     lists of outputs, masks and gradients; ``forward(micro_batch=m)`` for each
@@ -457,8 +484,6 @@ class SequenceStep:
         for t in plan.tables:
             if t.state is None:
                 raise RuntimeError("every table needs a row-wise Adagrad accumulator")
-        if plan.total_rows >= ops.KEY_SPACE:
-            raise NotImplementedError("sequence steps take plans of fewer than 2^32 - 1 rows")
         self.k = int(micro_batches)
         if self.k < 1:
             raise ValueError("micro_batches must be positive")
@@ -468,6 +493,7 @@ class SequenceStep:
         elif not len(outputs) == len(masks) == len(grads) == self.k:
             raise ValueError("one list of outputs, masks and gradients per micro-batch")
         self.plan = plan
+        groups = plan.groups  # row bases of the tables within their key group
         self.device = ids[0].device
         self.ids = [_as_ids(t) for t in ids]
         self.lengths = [t.to(torch.int64).contiguous() for t in lengths]
@@ -491,17 +517,11 @@ class SequenceStep:
         # Entries a step can hold: every row at its cap.
         self.capacity = int(sum(b * c for b, c in zip(self.batch, self.caps)))
         self.key_len = torch.empty(max(total_rows, 1), dtype=torch.int64, device=self.device)
-        self.offsets = torch.empty(total_rows + 1, dtype=torch.int64, device=self.device)
-        self.scan_ws = ops._workspace(lib().mdl_offsets_workspace_bytes(total_rows), self.device)
-        cap = max(self.capacity, 1)
-        self.keys = torch.empty(cap * self.k, dtype=torch.int32, device=self.device)
-        self.payload = torch.empty(cap * self.k, dtype=torch.int32, device=self.device)
         # Window positions of one micro-batch; micro-batch m's payloads (and
         # gradient rows) follow micro-batch m - 1's.
         positions = int(sum(int(o.size(0)) * int(o.size(1)) for o in self.outputs))
         if positions * self.k >= 1 << 32:
             raise ValueError("the micro-batches' window positions exceed the 32-bit gradient-row payload")
-        feats = []
         self.fwd_feats = []  # [m][f]
         for m in range(self.k):
             per = []
@@ -515,28 +535,42 @@ class SequenceStep:
                     row_base=table.row_base, payload_base=payload_base, grad=self.all_grads[m][f],
                 )
                 rec["table"] = spec.table
-                feats.append(rec)
-                per.append(rec.copy())
+                per.append(rec)
                 payload_base += int(B) * int(L_out)
             self.fwd_feats.append(per)
-        self.feats_bwd = np.concatenate(feats)
-        self.tables = ops._tables_array(plan, self.feats_bwd[: len(plan.features)])
         if self.k > 1:
-            # a table read by k copies of its feature: the reduce finds each
-            # payload's feature by search
-            self.tables["feature"] = -1
-            self._positions = torch.arange(cap, dtype=torch.int64, device=self.device)
+            self._positions = torch.arange(max(self.capacity, 1), dtype=torch.int64, device=self.device)
             sentinel = int(plan.sentinel)
             self._sentinel = sentinel - (1 << 32) if sentinel >= (1 << 31) else sentinel
-        self.bwd_classes = ops.table_classes(self.tables)
-        self.feats_bwd_dev = ops.upload(self.feats_bwd, self.device)
-        self.tables_dev = ops.upload(self.tables, self.device)
-        self.ws = ops._workspace(
-            lib().mdl_backward_workspace_bytes(self._n(), len(self.tables), plan.max_dim), self.device
-        )
+        self.groups: list[_SeqGroup] = []
+        for g in groups:
+            gs = _SeqGroup()
+            gs.lo, gs.hi = g.lo, g.hi
+            gs.r0, gs.r1 = int(self.row_base[g.lo]), int(self.row_base[g.hi])
+            gs.cap = int(sum(self.batch[f] * self.caps[f] for f in range(g.lo, g.hi)))
+            cap = max(gs.cap, 1)
+            gs.offsets = torch.empty(gs.r1 - gs.r0 + 1, dtype=torch.int64, device=self.device)
+            gs.scan_ws = ops._workspace(lib().mdl_offsets_workspace_bytes(gs.r1 - gs.r0), self.device)
+            gs.keys = torch.empty(cap * self.k, dtype=torch.int32, device=self.device)
+            gs.payload = torch.empty(cap * self.k, dtype=torch.int32, device=self.device)
+            # the group's features of every micro-batch, micro-batch 0 first
+            # (payload bases ascending, as the reduce's feature search needs)
+            gs.feats_bwd = np.concatenate([self.fwd_feats[m][f] for m in range(self.k) for f in range(g.lo, g.hi)])
+            gs.tables = ops._tables_array(g.plan, gs.feats_bwd[: g.hi - g.lo]).copy()
+            if self.k > 1:
+                # a table read by k copies of its feature: the reduce finds each
+                # payload's feature by search
+                gs.tables["feature"] = -1
+            gs.bwd_classes = ops.table_classes(gs.tables)
+            gs.feats_bwd_dev = ops.upload(gs.feats_bwd, self.device)
+            gs.tables_dev = ops.upload(gs.tables, self.device)
+            gs.ws = ops._workspace(
+                lib().mdl_backward_workspace_bytes(self._n(gs), len(gs.tables), plan.max_dim), self.device
+            )
+            self.groups.append(gs)
 
-    def _n(self) -> int:
-        return max(self.capacity, 1) * self.k if self.k > 1 else self.capacity
+    def _n(self, gs: _SeqGroup) -> int:
+        return max(gs.cap, 1) * self.k if self.k > 1 else gs.cap
 
     def bind(self, ids: Sequence[Tensor] | None = None, lengths: Sequence[Tensor] | None = None) -> None:
         """Point the next steps at another batch (same shapes; any lengths)."""
@@ -556,7 +590,9 @@ class SequenceStep:
     def count(self) -> Tensor:
         """Device int64 [1]: packed sort entries of the bound batch."""
 
-        return self.offsets[-1:]
+        if len(self.groups) == 1:
+            return self.groups[0].offsets[-1:]
+        return torch.stack([gs.offsets[-1] for gs in self.groups]).sum().reshape(1)
 
     def _stream(self) -> int:
         return torch.cuda.current_stream(self.device).cuda_stream
@@ -570,61 +606,66 @@ class SequenceStep:
             raise ValueError(f"micro_batch must be in [0, {self.k})")
         self._looked_up.add(mb)
         s = self._stream()
-        region = mb * max(self.capacity, 1)
         # Entries each row keeps (its positions that reach the window), then
-        # one scan over every feature's rows places them.
+        # one scan over each key group's rows places them.
         for f, ln in enumerate(self.lengths):
             b0, b1 = int(self.row_base[f]), int(self.row_base[f + 1])
             torch.clamp(ln, 0, self.caps[f], out=self.key_len[b0:b1])
-        nrows = int(self.row_base[-1])
-        check(
-            lib().mdl_lengths_to_offsets(self.key_len.data_ptr(), nrows, self.offsets.data_ptr(),
-                                         self.scan_ws.data_ptr(), self.scan_ws.numel(), s),
-            "mdl_lengths_to_offsets",
-        )
-        for f, rec in enumerate(self.fwd_feats[mb]):
-            ids = self.ids[f]
-            out = self.all_outputs[mb][f]
+        for gs in self.groups:
+            nrows = gs.r1 - gs.r0
             check(
-                lib().mdl_sequence_forward(
-                    rec.ctypes.data, ids.data_ptr(), self.lengths[f].data_ptr(), ids.size(0), ids.size(1),
-                    out.size(1), self.order, out.data_ptr(), self.all_masks[mb][f].data_ptr(),
-                    self.keys.data_ptr() + 4 * region, self.payload.data_ptr() + 4 * region,
-                    self.offsets.data_ptr() + 8 * int(self.row_base[f]), self.plan.sentinel,
-                    self.error_count.data_ptr(), s,
-                ),
-                "mdl_sequence_forward",
+                lib().mdl_lengths_to_offsets(self.key_len.data_ptr() + 8 * gs.r0, nrows, gs.offsets.data_ptr(),
+                                             gs.scan_ws.data_ptr(), gs.scan_ws.numel(), s),
+                "mdl_lengths_to_offsets",
             )
-        if self.k > 1:
-            # entries of the region past this micro-batch's keys sort last and
-            # reduce nowhere
-            live = self.offsets[int(self.row_base[-1])]
-            self.keys[region: region + max(self.capacity, 1)].masked_fill_(self._positions >= live, self._sentinel)
+            region = mb * max(gs.cap, 1)
+            for f in range(gs.lo, gs.hi):
+                rec = self.fwd_feats[mb][f]
+                ids = self.ids[f]
+                out = self.all_outputs[mb][f]
+                check(
+                    lib().mdl_sequence_forward(
+                        rec.ctypes.data, ids.data_ptr(), self.lengths[f].data_ptr(), ids.size(0), ids.size(1),
+                        out.size(1), self.order, out.data_ptr(), self.all_masks[mb][f].data_ptr(),
+                        gs.keys.data_ptr() + 4 * region, gs.payload.data_ptr() + 4 * region,
+                        gs.offsets.data_ptr() + 8 * (int(self.row_base[f]) - gs.r0), self.plan.sentinel,
+                        self.error_count.data_ptr(), s,
+                    ),
+                    "mdl_sequence_forward",
+                )
+            if self.k > 1:
+                # entries of the region past this micro-batch's keys sort last
+                # and reduce nowhere
+                cap = max(gs.cap, 1)
+                live = gs.offsets[nrows]
+                gs.keys[region: region + cap].masked_fill_(self._positions[:cap] >= live, self._sentinel)
 
     _check_micro_batches = SparseStep._check_micro_batches
 
     def sort(self) -> None:
         self._check_micro_batches()
-        check(
-            lib().mdl_backward_sort(
-                self.tables_dev.data_ptr(), len(self.tables), self.plan.max_dim, self.keys.data_ptr(),
-                self.payload.data_ptr(), self._n(),
-                self.offsets.data_ptr() + 8 * int(self.row_base[-1]) if self.k == 1 else None,
-                self.plan.key_bits, self.ws.data_ptr(), self.ws.numel(), self._stream(),
-            ),
-            "mdl_backward_sort",
-        )
+        for gs in self.groups:
+            check(
+                lib().mdl_backward_sort(
+                    gs.tables_dev.data_ptr(), len(gs.tables), self.plan.max_dim, gs.keys.data_ptr(),
+                    gs.payload.data_ptr(), self._n(gs),
+                    gs.offsets.data_ptr() + 8 * (gs.r1 - gs.r0) if self.k == 1 else None,
+                    self.plan.key_bits, gs.ws.data_ptr(), gs.ws.numel(), self._stream(),
+                ),
+                "mdl_backward_sort",
+            )
 
     def apply(self, lr: float, eps: float) -> None:
-        check(
-            lib().mdl_backward_apply(
-                self.feats_bwd_dev.data_ptr(), len(self.feats_bwd), self.tables_dev.data_ptr(), len(self.tables),
-                self.plan.max_dim, self.keys.data_ptr(), self.payload.data_ptr(), self._n(), self.plan.key_bits,
-                None, float(lr), float(eps), None, self.ws.data_ptr(), self.ws.numel(), self.bwd_classes,
-                self._stream(),
-            ),
-            "mdl_backward_apply",
-        )
+        for gs in self.groups:
+            check(
+                lib().mdl_backward_apply(
+                    gs.feats_bwd_dev.data_ptr(), len(gs.feats_bwd), gs.tables_dev.data_ptr(), len(gs.tables),
+                    self.plan.max_dim, gs.keys.data_ptr(), gs.payload.data_ptr(), self._n(gs), self.plan.key_bits,
+                    None, float(lr), float(eps), None, gs.ws.data_ptr(), gs.ws.numel(), gs.bwd_classes,
+                    self._stream(),
+                ),
+                "mdl_backward_apply",
+            )
 
     def capture(self, lr: float, eps: float) -> None:
         """One HIP graph of step(lr, eps); see SparseStep.capture."""
