@@ -154,11 +154,14 @@ class ShardedRowWiseAdagrad(torch.optim.Optimizer):
         """Bump the CPU step counter; return the decayed learning rate."""
 
         step_tensor = self.state[parameter]["step"]
-        step = float(step_tensor) + 1.0
-        step_tensor.fill_(step)
         lr = float(group["lr"])
         lr_decay = float(group["lr_decay"])
-        return lr if lr_decay == 0.0 else lr / (1.0 + (step - 1.0) * lr_decay)
+        if lr_decay == 0.0:
+            step_tensor.add_(1.0)  # the rate does not read the count
+            return lr
+        step = float(step_tensor) + 1.0
+        step_tensor.fill_(step)
+        return lr / (1.0 + (step - 1.0) * lr_decay)
 
     @torch.no_grad()
     def step(self, closure: Callable[[], Tensor] | None = None) -> Tensor | None:

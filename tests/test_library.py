@@ -161,6 +161,32 @@ def _coo(rows, values, size, dtype=torch.float32):
                                    size=size)
 
 
+def test_cpu_adagrad_lr_decay_and_step_counts():
+    """The step count of every parameter with a gradient goes up by one per
+    step, and lr_decay scales the rate by 1 / (1 + (step - 1) * lr_decay)
+    (src/optim.py:335-341); a parameter without a gradient keeps its count."""
+
+    rng = np.random.default_rng(5)
+    w0 = rng.standard_normal((12, 4)).astype(np.float32)
+    p = nn.Parameter(torch.from_numpy(w0.copy()))
+    idle = nn.Parameter(torch.zeros(3, 4))
+    lr, decay, eps = 0.2, 0.5, 1e-8
+    opt = ShardedRowWiseAdagrad([p, idle], lr=lr, lr_decay=decay, initial_accumulator_value=0.1, eps=eps)
+    W, A = w0.astype(np.float64), np.full(12, 0.1, np.float32)
+    for step in range(1, 4):
+        rows = rng.integers(0, 12, size=6)
+        vals = rng.standard_normal((6, 4)).astype(np.float32)
+        p.grad = torch.sparse_coo_tensor(torch.from_numpy(rows).unsqueeze(0), torch.from_numpy(vals), size=p.shape)
+        idle.grad = None
+        opt.step()
+        r, v = O.coalesce(rows, vals.astype(np.float64))
+        W, A = O.rowwise_adagrad(W, A, r, v, lr / (1.0 + (step - 1) * decay), eps)
+        assert float(opt.state[p]["step"].item()) == float(step)
+        assert float(opt.state[idle]["step"].item()) == 0.0
+        assert np.allclose(p.detach().numpy(), W, rtol=1e-5, atol=1e-6)
+        assert np.allclose(opt.state[p]["sum"].numpy(), A, rtol=1e-5, atol=1e-7)
+
+
 def test_cpu_adagrad_golden_vectors():
     """The reference tests' cases on CPU parameters (tests/test_rowwise_adagrad.py:40-128)."""
 
