@@ -389,12 +389,38 @@ def _grouped_lookup(
         if policy not in ("exclude", "include_as_padding"):
             raise ValueError(f"unsupported categorical bag null policy {policy!r}")
     need_backward = torch.is_grad_enabled() and any(w.requires_grad for w in weights)
-    outputs, _, _, _, _, err = torch.ops.mdl_hip.grouped_lookup(
-        weights, list(ids), list(lengths), table, [_POOLING_CODES[p] for p in poolings],
-        [1 if p == "exclude" else 0 for p in null_policies], [int(m.padding_idx) for m in modules], need_backward,
-    )
-    _check_ids(modules, list(ids), err)
+    spec = (table, [_POOLING_CODES[p] for p in poolings], [1 if p == "exclude" else 0 for p in null_policies],
+            [int(m.padding_idx) for m in modules])
+    ids = list(ids)
+    if need_backward:
+        *outputs, err = _GroupedLookup.apply(spec, ids, list(lengths), *weights)
+    else:
+        outputs, _, _, _, _, err = torch.ops.mdl_hip.grouped_lookup(weights, ids, list(lengths), *spec, False)
+    _check_ids(modules, ids, err)
     return list(outputs)
+
+
+class _GroupedLookup(torch.autograd.Function):
+    """``mdl_hip::grouped_lookup`` with its registered backward
+    (``library._lookup_backward``), as one autograd node whose inputs are the
+    tables themselves.  The op's own autograd registration flattens its list
+    arguments (every id tensor, length and per-feature code) on each call; for
+    the modules' calls over hundreds of features that costs more host time
+    than the rest of the forward (about 0.35 ms per call at 200 features)."""
+
+    @staticmethod
+    def forward(ctx, spec, ids, lengths, *weights):
+        outputs, keys, payload, bag_count, offsets, err = torch.ops.mdl_hip.grouped_lookup(
+            list(weights), ids, lengths, *spec, True)
+        library._lookup_setup(ctx, (list(weights), ids, lengths, *spec, True),
+                              (outputs, keys, payload, bag_count, offsets, err))
+        ctx.mark_non_differentiable(err)
+        return (*outputs, err)
+
+    @staticmethod
+    def backward(ctx, *grad_outputs):
+        weight_grads = library._lookup_backward(ctx, list(grad_outputs[:-1]))[0]
+        return (None, None, None, *weight_grads)
 
 
 # ----------------------------------------------------------------- module --
