@@ -464,3 +464,70 @@ def test_sequence_step_over_two_key_groups_matches_oracle(device, big, order):
                       RTOL["bf16" if bf else "fp32"], 1e-6 if bf else 1e-7, bf)
     snap.restore_and_check(tables, states)
     say("key_groups", "sequence step checked", order, f"{time.time() - t0:.1f}s")
+
+
+def test_sequence_step_micro_batches_over_two_key_groups(device, big):
+    """SequenceStep(micro_batches=2) over the 4.5e9-row plan: each key group
+    holds both micro-batches' window entries in regions of its key buffer,
+    and one sort + reduce per group applies one row-wise Adagrad step on the
+    coalesced sum of both micro-batches' window gradients."""
+
+    from mdl_amd.sparse_step import SequenceStep
+
+    t0 = time.time()
+    tables, states = big
+    rng = np.random.default_rng(4700)
+    k, Bs, L_in, L_out = 2, 64, 90, 80
+    plan = ops.GroupPlan()
+    for t in range(3):
+        plan.add_feature(tables[t], pooling="none", state=states[t])
+
+    def batch(max_len):
+        ids, lens = [], []
+        for t in range(3):
+            R = ROWS[t]
+            ln = rng.integers(0, max_len + 1, size=Bs)
+            hot = np.concatenate([[R - 1, min(1 << 31, R - 1), 2], rng.integers(0, R, size=100)])
+            m = np.where(rng.random((Bs, L_in)) < 0.5, rng.choice(hot, size=(Bs, L_in)),
+                         rng.integers(0, R, size=(Bs, L_in)))
+            m[np.arange(L_in)[None, :] >= ln[:, None]] = 0
+            ids.append(m.astype(np.int64))
+            lens.append(ln)
+        return ids, lens
+
+    batches = [batch(40), batch(L_in)]
+    touched = [_touched([b[0][t] for b in batches]) for t in range(3)]
+    _set_touched(tables, touched, rng)
+    snap = _Snapshot(tables, states, touched, device)
+    outs = [[torch.empty((Bs, L_out, DIMS[t]), dtype=DTYPES[t], device=device) for t in range(3)] for _ in range(k)]
+    masks = [[torch.empty((Bs, L_out), dtype=torch.bool, device=device) for _ in range(3)] for _ in range(k)]
+    grads = [_grads(rng, o) for o in outs]
+    dev = [([torch.from_numpy(m).to(device) for m in ids], [torch.from_numpy(ln).to(device) for ln in lens])
+           for ids, lens in batches]
+    st = SequenceStep(plan, dev[0][0], dev[0][1], outs, masks, grads, micro_batches=k)
+    assert len(st.groups) == 2
+    for m in range(k):
+        st.bind(*dev[m])
+        st.forward(micro_batch=m)
+    st.sort()
+    st.apply(LR, EPS)
+    torch.cuda.synchronize()
+    assert int(st.error_count.item()) == 0
+    say("key_groups", "sequence micro-batches done", f"{time.time() - t0:.1f}s")
+    w_post, a_post = snap.after(tables, states)
+    for t in range(3):
+        rows, vals, absv = [], [], []
+        for m, (ids, lens) in enumerate(batches):
+            mask, src = O.sequence_positions(ids[t], lens[t], L_out)
+            assert np.array_equal(masks[m][t].cpu().numpy(), mask), (m, t)
+            r, v = O.sequence_grads(ids[t], lens[t], grads[m][t].float().cpu().numpy(), L_out)
+            rows.append(np.searchsorted(touched[t], r))
+            vals.append(v)
+            absv.append(np.abs(v))
+        rr, gg = O.coalesce(np.concatenate(rows), np.concatenate(vals))
+        _, ss = O.coalesce(np.concatenate(rows), np.concatenate(absv))
+        bf = DTYPES[t] == torch.bfloat16
+        _check_update(f"sequence micro-batches table {t}", w_post[t], a_post[t], snap.w[t], snap.a[t], rr, gg, ss,
+                      LR, EPS, RTOL["bf16" if bf else "fp32"], 1e-6 if bf else 1e-7, bf)
+    snap.restore_and_check(tables, states)
+    say("key_groups", "sequence micro-batches checked", f"{time.time() - t0:.1f}s")
