@@ -1101,6 +1101,10 @@ def measure(name: str, args, torch, device, *, with_aux: bool = False) -> dict:
         "dtype": "f32" if wl.dtype == "fp32" else "bf16-storage/f32-accumulate",
         "hbm_gbps_achieved": b_alg / (ms * 1e-3) / 1e9,
         "roofline_fraction_step": b_alg / (ms * 1e-3) / 1e9 / PEAK_HBM_GBPS,
+        # every launch group's measured traffic over the step time: how busy
+        # HBM is over the whole step in the whole lines it moves
+        "traffic_fraction_step": (None if tr is None else sum(g["hbm_bytes_per_step"] for g in tr["groups"].values())
+                                  / (ms * 1e-3) / 1e9 / PEAK_HBM_GBPS),
         "B_alg_bytes_per_step": b_alg,
         "roofline": {
             "kernel": dom["kernel"],
@@ -1296,6 +1300,7 @@ def main() -> int:
         },
         "hbm_gbps_achieved": head["hbm_gbps_achieved"],
         "roofline_fraction_step": head["roofline_fraction_step"],
+        "traffic_fraction_step": head["traffic_fraction_step"],
         "B_alg_bytes_per_step": head["B_alg_bytes_per_step"],
         "roofline": head["roofline"],
         "kernels": head["kernels"],
