@@ -59,7 +59,7 @@ def _bag(rng, B, dim, max_len, dtype, device, null_every=4):
 
 
 @pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
-@pytest.mark.parametrize("dim", [1, 6, 16, 64, 200])
+@pytest.mark.parametrize("dim", [1, 6, 16, 64, 130, 200, 600])
 @pytest.mark.parametrize("policy", ["exclude", "include_as_padding"])
 def test_flat_mean_pool_forward_backward_match_oracle(device, dtype, dim, policy):
     announce("pool_flat", dtype, dim, policy)
