@@ -1,0 +1,82 @@
+"""Host logic of the drop-in embedding API on CPU, written like the
+reference's own tests: shard planning and its fingerprint
+(tests/test_sharded_embedding.py:596-646), the local-bytes cost model
+(tests/test_rowwise_adagrad.py:174-213) and the per-table lookup statistics
+(src/embeddings.py:26-59,813-814,1754-1765)."""
+
+import torch
+from torch import nn
+
+from mdl_amd.embeddings import (
+    EmbeddingTableSpec,
+    ShardedEmbedding,
+    consume_sharded_embedding_stats,
+    embedding_local_bytes,
+    embedding_stats_host_sync,
+    grouped_sharded_embedding_lookup,
+    plan_embedding_shards,
+    sharded_embedding_modules,
+)
+
+
+def test_embedding_local_bytes_formulas():
+    assert embedding_local_bytes(rows=1000, embedding_dim=64, weight_element_size=2,
+                                 optimizer_state_layout="full") == 1000 * 64 * (2 + 4)
+    assert embedding_local_bytes(rows=1000, embedding_dim=64, weight_element_size=2,
+                                 optimizer_state_layout="rowwise") == 1000 * (64 * 2 + 4)
+
+
+def test_plan_default_layout_is_full_and_rowwise_changes_fingerprint():
+    specs = [EmbeddingTableSpec(name="a", num_embeddings=100, embedding_dim=8, element_size=2),
+             EmbeddingTableSpec(name="b", num_embeddings=50, embedding_dim=4, element_size=2)]
+    full = plan_embedding_shards(specs, world_size=2, strategy="row_wise", table_wise_max_rows=1)
+    rowwise = plan_embedding_shards(specs, world_size=2, strategy="row_wise", table_wise_max_rows=1,
+                                    optimizer_state_layout="rowwise")
+    assert full.fingerprint != rowwise.fingerprint
+
+
+def test_auto_uses_row_wise_for_large_and_lpt_for_small_tables():
+    specs = [EmbeddingTableSpec("large", 1000, 8), EmbeddingTableSpec("small_a", 20, 8),
+             EmbeddingTableSpec("small_b", 10, 8)]
+    first = plan_embedding_shards(specs, world_size=2, strategy="auto", table_wise_max_rows=32)
+    second = plan_embedding_shards(reversed(specs), world_size=2, strategy="auto", table_wise_max_rows=32)
+    assert first.fingerprint == second.fingerprint
+    assert first.tables["large"].strategy == "row_wise"
+    assert first.tables["small_a"].strategy == "table_wise"
+    assert first.tables["small_a"].table_owner != first.tables["small_b"].table_owner
+
+
+def test_rowwise_cost_model_matches_embedding_local_bytes():
+    plan = plan_embedding_shards([EmbeddingTableSpec("t0", 1000, 64, element_size=2)], world_size=2,
+                                 strategy="row_wise", table_wise_max_rows=1, optimizer_state_layout="rowwise")
+    shard = plan.tables["t0"]
+    assert sum(shard.local_rows(1000, rank) for rank in range(2)) == 1000
+    for rank in range(2):
+        rows = shard.local_rows(1000, rank)
+        assert embedding_local_bytes(rows=rows, embedding_dim=64, weight_element_size=2,
+                                     optimizer_state_layout="rowwise") == rows * (64 * 2 + 4)
+
+
+def _model():
+    plan = plan_embedding_shards([EmbeddingTableSpec("a", 16, 4), EmbeddingTableSpec("b", 12, 4)], world_size=1,
+                                 strategy="row_wise", table_wise_max_rows=32)
+    model = nn.ModuleDict({
+        "a": ShardedEmbedding(16, 4, table_name="a", shard_spec=plan.tables["a"]),
+        "b": ShardedEmbedding(12, 4, table_name="b", shard_spec=plan.tables["b"], collect_stats=False),
+    })
+    return model
+
+
+def test_lookup_statistics_are_recorded_and_consumed():
+    model = _model()
+    assert [m.table_name for m in sharded_embedding_modules(model)] == ["a", "b"]
+    model["a"](torch.tensor([1, 2, 3]))
+    grouped_sharded_embedding_lookup([(model["a"], torch.tensor([[4, 5], [0, 6]])), (model["b"], torch.tensor([7]))])
+    stats = consume_sharded_embedding_stats(model)
+    # only tables that collect statistics report; a single-GPU lookup moves nothing
+    assert [s.table_name for s in stats] == ["a"]
+    assert stats[0].raw_ids == 7 and stats[0].active_ids == 7 and stats[0].sent_ids == 0
+    assert consume_sharded_embedding_stats(model)[0].raw_ids == 0  # consumed
+    with embedding_stats_host_sync(False):
+        model["a"](torch.tensor([1, 2]))
+    assert consume_sharded_embedding_stats(model)[0].raw_ids == 0
