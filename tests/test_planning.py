@@ -80,3 +80,26 @@ def test_lookup_statistics_are_recorded_and_consumed():
     with embedding_stats_host_sync(False):
         model["a"](torch.tensor([1, 2]))
     assert consume_sharded_embedding_stats(model)[0].raw_ids == 0
+
+
+def test_table_initialisation_matches_the_reference_bit_for_bit():
+    """Golden weights written by the reference's own ShardedEmbedding
+    (tests/golden/make_init_vectors.py): the seed from torch.initial_seed(),
+    the table name's sha256 and the rank, N(0, init_std), the padding row
+    zeroed -- so a checkpoint-free run starts from the reference's tables."""
+
+    import json
+    import pathlib
+
+    cases = json.loads((pathlib.Path(__file__).parent / "golden" / "init_vectors.json").read_text())
+    assert cases
+    for c in cases:
+        plan = plan_embedding_shards([EmbeddingTableSpec(c["name"], c["rows"], c["dim"])], world_size=1,
+                                     strategy="row_wise", table_wise_max_rows=1)
+        torch.manual_seed(c["seed"])
+        m = ShardedEmbedding(c["rows"], c["dim"], table_name=c["name"], shard_spec=plan.tables[c["name"]],
+                             padding_idx=c["padding_idx"], init_std=c["init_std"], dtype=getattr(torch, c["dtype"]),
+                             collect_stats=False)
+        expect = torch.tensor(c["weight"], dtype=torch.float32).to(getattr(torch, c["dtype"]))
+        assert torch.equal(m.weight.detach(), expect), c["name"]
+        assert not m.weight[c["padding_idx"]].any()
