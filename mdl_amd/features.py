@@ -4,9 +4,10 @@ Mirrors the reference's ``pre_hashed`` encoding (src/features.py:360-376,
 vectorised in src/dataloader.py:8463-8493 and :10173-10186), its list
 truncation (src/dataloader.py:8565-8665) and the benchmark's ``mod`` id rule
 (src/benchmark.py:1246-1250).  Bucketing of id tensors runs on the GPU
-(``mdl_bucketize``), and so does a list feature's whole truncation, flatten
-and bucketing (``mdl_bag_truncate``: :func:`bag_csr_tensor`,
-:func:`bag_csr_arrow`); the scalar function keeps the reference's Python API.
+(``mdl_bucketize``; host tensors take the op's CPU kernel), and so does a
+list feature's whole truncation, flatten and bucketing (``mdl_bag_truncate``:
+:func:`bag_csr_tensor`, :func:`bag_csr_arrow`); the scalar function keeps the
+reference's Python API.
 """
 
 from __future__ import annotations
@@ -45,29 +46,31 @@ def pre_hashed_bucket_tensor(
     validate_nonzero: bool = True,
     name: str = "feature",
 ) -> Tensor:
-    """Bucket a device tensor of raw hashes; nulls (``valid == 0``) become 0.
+    """Bucket a tensor of raw int64 hashes; nulls (``valid == 0``) become 0.
 
-    With ``validate_nonzero`` a non-null zero raises ``ValueError`` (one device
-    sync, like the reference's pyarrow scan for zeros).
+    Runs the ``mdl_hip::bucketize`` op: the HIP kernel for a ROCm tensor, the
+    op's CPU kernel for a host tensor (the reference buckets on the host,
+    src/dataloader.py:8463-8493).  With ``validate_nonzero`` a non-null zero
+    raises ``ValueError`` (one read of the zero count, like the reference's
+    pyarrow scan for zeros).
     """
 
     if num_buckets <= 0 or num_buckets & (num_buckets - 1):
         raise ValueError("pre_hashed num_buckets must be a positive power of two")
-    err = torch.zeros(1, dtype=torch.int32, device=raw.device) if validate_nonzero else None
-    out = ops.bucketize(
-        raw, num_buckets, mode="pre_hashed", valid=valid, validate_nonzero=validate_nonzero, error_count=err
-    )
-    if err is not None and int(err.item()):
+    out, err = torch.ops.mdl_hip.bucketize(raw, valid, int(num_buckets), "pre_hashed", bool(validate_nonzero))
+    if validate_nonzero and int(err.item()):
         raise ValueError(f"pre_hashed input {name!r} contains non-null zero values")
     return out
 
 
 def mod_bucket_tensor(raw: Tensor, num_embeddings: int) -> Tensor:
-    """``1 + ((raw - 1) mod (num_embeddings - 1))`` with Python floor-mod."""
+    """``1 + ((raw - 1) mod (num_embeddings - 1))`` with Python floor-mod, and
+    zeros for a table of one row (src/benchmark.py:1232-1233,1246-1250); on
+    either device, through the ``mdl_hip::bucketize`` op."""
 
     if num_embeddings <= 1:
         return torch.zeros_like(raw)
-    return ops.bucketize(raw, num_embeddings, mode="mod", validate_nonzero=False)
+    return torch.ops.mdl_hip.bucketize(raw, None, int(num_embeddings), "mod", False)[0]
 
 
 def bag_csr(

@@ -1,4 +1,4 @@
-"""List-feature truncation to CSR bags (host side, no GPU).
+"""Id bucketing and list-feature truncation to CSR bags (host side, no GPU).
 
 The oracle's ``bag_truncate`` restates the reference's Arrow truncation
 (src/dataloader.py:8565-8640); it is pinned here by the reference's golden
@@ -17,7 +17,10 @@ import pytest
 import torch
 
 import mdl_amd  # noqa: F401  (registers the mdl_hip ops)
-from mdl_amd.features import bag_csr, bag_csr_arrow, bag_csr_tensor
+from mdl_amd.features import (
+    INT64_MAX, INT64_MIN, bag_csr, bag_csr_arrow, bag_csr_tensor, mod_bucket_tensor, pre_hashed_bucket,
+    pre_hashed_bucket_tensor,
+)
 from oracle import oracle as O
 
 GOLD = json.loads((Path(__file__).parent / "golden" / "reference_vectors.json").read_text())
@@ -156,3 +159,49 @@ def test_bag_truncate_opcheck_cpu():
     args = (torch.from_numpy(raw), torch.from_numpy(offsets), torch.from_numpy(valid), torch.from_numpy(row_valid),
             3, "tail", "pre_hashed", 64, True)
     torch.library.opcheck(torch.ops.mdl_hip.bag_truncate.default, args)
+
+
+def test_pre_hashed_bucket_scalar_follows_the_reference():
+    """The scalar API on the reference's golden values and errors
+    (tests/test_direct_id.py:183-189, src/features.py:360-376)."""
+
+    g = GOLD["pre_hashed_scalar"]
+    for raw, want in g["cases"]:
+        assert pre_hashed_bucket(raw, g["num_buckets"]) == want
+    assert pre_hashed_bucket(1, 8) == 2 and pre_hashed_bucket(7, 8) == 8 and pre_hashed_bucket(9, 8) == 2
+    with pytest.raises(ValueError, match="must not be zero"):
+        pre_hashed_bucket(0, 8)
+    with pytest.raises(TypeError, match="must be an int64"):
+        pre_hashed_bucket(True, 8)
+    with pytest.raises(TypeError, match="must be an int64"):
+        pre_hashed_bucket(3.0, 8)
+    with pytest.raises(ValueError, match="outside signed int64"):
+        pre_hashed_bucket(1 << 63, 8)
+    with pytest.raises(ValueError, match="power of two"):
+        pre_hashed_bucket(5, 6)
+
+
+def test_bucket_tensors_on_the_host_follow_the_reference():
+    """The tensor forms on CPU tensors (the op's CPU kernel), on the golden
+    columns of tests/test_direct_id.py:191-240 and, for the mod rule, on
+    random int64 values against Python's floor-mod (src/benchmark.py:1246-1250)."""
+
+    g = GOLD["pre_hashed_column_with_nulls"]
+    valid = torch.tensor([v is not None for v in g["raw"]])
+    raw = torch.tensor([0 if v is None else v for v in g["raw"]], dtype=torch.int64)
+    assert pre_hashed_bucket_tensor(raw, g["num_buckets"], valid=valid).tolist() == g["expected"]
+    z = GOLD["pre_hashed_zero_unvalidated"]
+    zraw = torch.tensor(z["raw"], dtype=torch.int64)
+    with pytest.raises(ValueError, match="non-null zero"):
+        pre_hashed_bucket_tensor(zraw, z["num_buckets"], name="item_hash")
+    assert pre_hashed_bucket_tensor(zraw, z["num_buckets"], validate_nonzero=False).tolist() == z["expected"]
+    # a null zero is not an error
+    assert pre_hashed_bucket_tensor(zraw, 8, valid=torch.tensor([True, False])).tolist() == [2, 0]
+
+    rng = np.random.default_rng(9)
+    vals = rng.integers(INT64_MIN, INT64_MAX, size=2000, dtype=np.int64, endpoint=True)
+    vals[:4] = [INT64_MIN, INT64_MAX, 0, 1]
+    for n in (2, 3, 1_000_000, 999_999_937, (1 << 62) + 1):
+        got = mod_bucket_tensor(torch.from_numpy(vals), n).tolist()
+        assert got == [1 + ((int(v) - 1) % (n - 1)) for v in vals], n
+    assert mod_bucket_tensor(torch.from_numpy(vals), 1).tolist() == [0] * len(vals)

@@ -120,3 +120,34 @@ def test_bag_truncate_opcheck_rocm(device):
     t = lambda a, dt=torch.int64: torch.from_numpy(a).to(dt).to(device)  # noqa: E731
     args = (t(raw), t(offsets), t(valid, torch.uint8), t(row_valid, torch.uint8), 3, "tail", "pre_hashed", 64, True)
     torch.library.opcheck(torch.ops.mdl_hip.bag_truncate.default, args)
+
+
+def test_bucket_tensors_on_the_device_equal_the_host(device):
+    """``pre_hashed_bucket_tensor`` / ``mod_bucket_tensor`` on ROCm tensors
+    (``mdl_bucketize``): the reference's golden columns, and bit-equal to the
+    op's CPU kernel (pinned in tests/test_features.py) on 1 M random int64
+    hashes with nulls, for both rules."""
+
+    from mdl_amd.features import mod_bucket_tensor, pre_hashed_bucket_tensor
+
+    announce("bucket_tensors")
+    g = GOLD["pre_hashed_column_with_nulls"]
+    valid = torch.tensor([v is not None for v in g["raw"]], device=device)
+    raw = torch.tensor([0 if v is None else v for v in g["raw"]], dtype=torch.int64, device=device)
+    assert pre_hashed_bucket_tensor(raw, g["num_buckets"], valid=valid).tolist() == g["expected"]
+    zraw = torch.tensor([1, 0], dtype=torch.int64, device=device)
+    with pytest.raises(ValueError, match="non-null zero"):
+        pre_hashed_bucket_tensor(zraw, 8)
+    assert pre_hashed_bucket_tensor(zraw, 8, validate_nonzero=False).tolist() == [2, 1]
+
+    rng = np.random.default_rng(31)
+    host = torch.from_numpy(rng.integers(-(1 << 63), (1 << 63) - 1, size=1 << 20, dtype=np.int64, endpoint=True))
+    host[:3] = torch.tensor([-(1 << 63), (1 << 63) - 1, 1])
+    nulls = torch.from_numpy(rng.random(host.numel()) >= 0.05)
+    host_nz = torch.where(host == 0, torch.ones_like(host), host)
+    for nb in (8, 1 << 20, 1 << 62):
+        want = pre_hashed_bucket_tensor(host_nz, nb, valid=nulls)
+        got = pre_hashed_bucket_tensor(host_nz.to(device), nb, valid=nulls.to(device))
+        assert torch.equal(got.cpu(), want), nb
+    for n in (2, 1_000_000, 999_999_937, (1 << 62) + 1):
+        assert torch.equal(mod_bucket_tensor(host.to(device), n).cpu(), mod_bucket_tensor(host, n)), n

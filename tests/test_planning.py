@@ -2,12 +2,15 @@
 reference's own tests: shard planning and its fingerprint
 (tests/test_sharded_embedding.py:596-646), the local-bytes cost model
 (tests/test_rowwise_adagrad.py:174-213) and the per-table lookup statistics
-(src/embeddings.py:26-59,813-814,1754-1765)."""
+(src/embeddings.py:26-59,813-814,1754-1765), row ownership and the
+communication-stats record (src/embeddings.py:163-188,198-240)."""
 
+import pytest
 import torch
 from torch import nn
 
 from mdl_amd.embeddings import (
+    EmbeddingCommunicationStats,
     EmbeddingTableSpec,
     ShardedEmbedding,
     consume_sharded_embedding_stats,
@@ -15,6 +18,7 @@ from mdl_amd.embeddings import (
     embedding_stats_host_sync,
     grouped_sharded_embedding_lookup,
     plan_embedding_shards,
+    set_embedding_stats_host_sync,
     sharded_embedding_modules,
 )
 
@@ -103,3 +107,64 @@ def test_table_initialisation_matches_the_reference_bit_for_bit():
         expect = torch.tensor(c["weight"], dtype=torch.float32).to(getattr(torch, c["dtype"]))
         assert torch.equal(m.weight.detach(), expect), c["name"]
         assert not m.weight[c["padding_idx"]].any()
+
+
+def test_row_ownership_and_local_row_ids():
+    """Row-wise shards own ``(id + offset) mod W`` and store row ``id div W``;
+    a table-wise shard owns every id at its global row (src/embeddings.py:163-188)."""
+
+    plan = plan_embedding_shards([EmbeddingTableSpec("big", 1000, 8), EmbeddingTableSpec("small", 10, 8)],
+                                 world_size=3, strategy="auto", table_wise_max_rows=100)
+    big, small = plan.tables["big"], plan.tables["small"]
+    assert big.strategy == "row_wise" and small.strategy == "table_wise"
+    ids = torch.arange(0, 20)
+    owners = big.owner(ids)
+    assert torch.equal(owners, (ids + big.cyclic_offset) % 3)
+    assert torch.equal(big.local_row_ids(ids), ids // 3)
+    # every global row has exactly one (owner, local row), and each owner's
+    # local rows fill [0, local_rows) without gaps
+    all_ids = torch.arange(1000)
+    o, local = big.owner(all_ids), big.local_row_ids(all_ids)
+    for rank in range(3):
+        mine = local[o == rank]
+        assert mine.numel() == big.local_rows(1000, rank)
+        assert torch.equal(mine.sort().values, torch.arange(mine.numel()))
+    assert torch.equal(small.owner(ids), torch.full_like(ids, small.table_owner))
+    assert torch.equal(small.local_row_ids(ids), ids)
+    assert [small.local_rows(10, r) for r in range(3)] == [10 if r == small.table_owner else 0 for r in range(3)]
+
+
+def test_communication_stats_add_up():
+    a = EmbeddingCommunicationStats("t", raw_ids=5, forward_sent_bytes=10, backward_received_bytes=3)
+    b = EmbeddingCommunicationStats("t", raw_ids=2, forward_received_bytes=7, backward_sent_bytes=1)
+    a.add_(b)
+    assert a.raw_ids == 7 and a.total_communication_bytes == 21
+    with pytest.raises(ValueError, match="different tables"):
+        a.add_(EmbeddingCommunicationStats("u"))
+
+
+def test_stats_host_sync_switch_is_thread_local_and_restored():
+    import threading
+
+    set_embedding_stats_host_sync(False)
+    try:
+        model = _model()
+        model["a"](torch.tensor([1, 2, 3]))
+        assert consume_sharded_embedding_stats(model)[0].raw_ids == 0  # no host reads, nothing counted
+        seen = []
+        t = threading.Thread(target=lambda: seen.append(_host_sync_enabled()))
+        t.start()
+        t.join()
+        assert seen == [True]  # another thread keeps the default
+        with embedding_stats_host_sync(True):
+            model["a"](torch.tensor([1, 2, 3]))
+        assert consume_sharded_embedding_stats(model)[0].raw_ids == 3
+        assert not _host_sync_enabled()  # restored
+    finally:
+        set_embedding_stats_host_sync(True)
+
+
+def _host_sync_enabled():
+    from mdl_amd import embeddings
+
+    return getattr(embeddings._STATS_HOST_SYNC, "enabled", True)
