@@ -340,3 +340,35 @@ def test_sequence_lookup_forward_backward_step(device, order):
     assert np.all(np.abs(got - wexp) <= 1e-5 * np.abs(wexp) + 1e-6)
     s = opt.state[m.weight]["sum"].cpu().numpy()
     assert np.all(np.abs(s - aexp) <= 1e-5 * np.abs(aexp) + 1e-6)
+
+
+def test_fused_rowwise_adagrad_update_public_function(device):
+    """``fused_rowwise_adagrad_update`` as the reference calls it
+    (src/optim.py:68-108): the golden case of tests/test_rowwise_adagrad.py:40-62
+    through the function itself, bf16 values on fp32 weights (upcast, as the
+    reference does), bf16 weights, and no rows as a no-op."""
+
+    from mdl_amd.optim import fused_rowwise_adagrad_update
+
+    announce("fused_rowwise_adagrad_update")
+    g = GOLD["rowwise_adagrad_mean_not_sum"]
+    for vdtype in (torch.float32, torch.bfloat16):
+        p = torch.zeros(*g["shape"], device=device)
+        acc = torch.zeros(g["shape"][0], device=device)
+        rows = torch.tensor(g["rows"], device=device)
+        fused_rowwise_adagrad_update(p, acc, rows, torch.tensor(g["values"], dtype=vdtype, device=device),
+                                     lr=g["lr"], eps=g["eps"])
+        for r, a in g["expected_acc"].items():
+            assert abs(float(acc[int(r)]) - a) < 1e-6
+        for r, w in g["expected_neg_weight"].items():
+            assert torch.allclose(p[int(r)].neg().cpu(), torch.tensor(w), atol=g["atol"])
+    pb = torch.zeros(*g["shape"], dtype=torch.bfloat16, device=device)
+    acc = torch.zeros(g["shape"][0], device=device)
+    fused_rowwise_adagrad_update(pb, acc, torch.tensor(g["rows"], device=device),
+                                 torch.tensor(g["values"], device=device), lr=g["lr"], eps=g["eps"])
+    for r, w in g["expected_neg_weight"].items():  # one rounding to bf16
+        assert torch.equal(pb[int(r)].neg().cpu(), torch.tensor(w).to(torch.bfloat16))
+    before = pb.clone()
+    fused_rowwise_adagrad_update(pb, acc, torch.empty(0, dtype=torch.int64, device=device),
+                                 torch.empty((0, 2), device=device), lr=1.0, eps=1e-8)
+    assert torch.equal(pb, before)

@@ -253,3 +253,22 @@ def test_capacity_gradient_is_a_valid_coo_of_the_coalesced_sum():
     torch.testing.assert_close(grad.to_dense(), dense)
     c = grad.coalesce()
     assert c.indices()[0].tolist() == [3, 7, 9]
+
+
+def test_cpu_fused_rowwise_adagrad_update_public_function():
+    """``fused_rowwise_adagrad_update`` on CPU tensors (the op's CPU kernel,
+    the reference's CPU update rule src/optim.py:359-376) on the golden case of
+    tests/test_rowwise_adagrad.py:40-62, with fp32 and bf16 values."""
+
+    from mdl_amd.optim import fused_rowwise_adagrad_update
+
+    g = GOLD["rowwise_adagrad_mean_not_sum"]
+    for vdtype in (torch.float32, torch.bfloat16):
+        p = torch.zeros(*g["shape"])
+        acc = torch.zeros(g["shape"][0])
+        fused_rowwise_adagrad_update(p, acc, torch.tensor(g["rows"]), torch.tensor(g["values"], dtype=vdtype),
+                                     lr=g["lr"], eps=g["eps"])
+        for r, a in g["expected_acc"].items():
+            assert abs(float(acc[int(r)]) - a) < 1e-6
+        for r, w in g["expected_neg_weight"].items():
+            assert torch.allclose(p[int(r)].neg(), torch.tensor(w), atol=g["atol"])
