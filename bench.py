@@ -647,7 +647,7 @@ def dropin_loop(torch, dev, wl, device, steps: int = 10) -> dict:
     for m, acc in zip(mods, dev.states):
         opt.state[m.weight]["sum"] = acc
     cols = np.concatenate([[0], np.cumsum([wl.dims[f.table] for f in wl.features])[:-1]])
-    grads = [dev.grad[:, int(c): int(c) + wl.dims[f.table]].contiguous() for f, c in zip(wl.features, cols)]
+    grads = [dev.grad[:, int(c): int(c) + wl.dims[f.table]] for f, c in zip(wl.features, cols)]
     feats = []
     for packed, lens in dev.batches:
         req_pool, req_single, g_pool, g_single = [], [], [], []
@@ -666,13 +666,16 @@ def dropin_loop(torch, dev, wl, device, steps: int = 10) -> dict:
                 req_pool.append((mods[feat.table], x, lens[lofs: lofs + nb], feat.pooling, "exclude"))
                 g_pool.append(grads[f])
                 lofs += nb
-        feats.append((req_pool, req_single, g_pool + g_single))
+        feats.append((req_pool, req_single, torch.cat(g_pool + g_single, dim=1)))
 
+    # The model concatenates the per-feature embeddings into its token slots
+    # (src/model.py:4395-4420), so one [B, sum(D)] gradient comes back and
+    # each feature's share arrives as a column slice of it.
     def one(i):
-        req_pool, req_single, gs = feats[i % len(feats)]
+        req_pool, req_single, g_tokens = feats[i % len(feats)]
         opt.zero_grad(set_to_none=True)
         outs = pooled_embedding_lookup(req_pool) + grouped_sharded_embedding_lookup(req_single)
-        torch.autograd.backward(outs, gs)
+        torch.cat(outs, dim=1).backward(g_tokens)
         opt.step()
 
     for i in range(2):
@@ -698,7 +701,8 @@ def dropin_loop(torch, dev, wl, device, steps: int = 10) -> dict:
         ms = (time.perf_counter() - t0) * 1e3 / steps
     return {"ms_per_step": ms, "steps": steps, "no_host_sync": clean,
             "what": "ShardedEmbedding modules (pooled_embedding_lookup + grouped_sharded_embedding_lookup), "
-                    "loss.backward() -> capacity-sized coalesced sparse grads, ShardedRowWiseAdagrad.step() "
+                    "their outputs concatenated into [B, sum(D)] token slots, backward of one [B, sum(D)] "
+                    "gradient -> capacity-sized coalesced sparse grads, ShardedRowWiseAdagrad.step() "
                     "(one grouped launch); timed steps under torch.cuda.set_sync_debug_mode('error')"}
 
 

@@ -391,7 +391,7 @@ def grouped_lookup_backward(
     n_ids = [int(x.numel()) for x in ids]
     bags = [int(lengths[f].numel()) if pooling[f] != 0 else 0 for f in range(len(ids))]
     feats = ops.build_features(plan, n_ids, bags, [g.data_ptr() for g in grads],
-                               [int(g.size(-1)) for g in grads])
+                               [int(g.stride(0)) if g.ndim == 2 else int(g.size(-1)) for g in grads])
     res = ops.ForwardResult(
         plan=plan, device=weights[0].device, ids=ids[0], offsets=offsets if offsets.numel() else None,
         outputs=list(grads), feats=feats, keys=keys, payload=payload,
@@ -496,7 +496,9 @@ def _lookup_backward(ctx, grad_outputs, *_unused):
         if g is None:
             rows_f = int(ctx.lengths[f].numel()) if pooling[f] != 0 else int(ids[f].numel())
             g = torch.zeros((rows_f, int(w.size(1))), dtype=w.dtype, device=w.device)
-        grads.append(g.contiguous())
+        # Row-strided gradients (column slices of one [B, sum(D)] gradient, as
+        # a concatenation of the outputs hands back) are read in place.
+        grads.append(g if g.ndim == 2 and g.stride(-1) == 1 else g.contiguous())
     rows_all, vbuf, counts = torch.ops.mdl_hip.grouped_lookup_backward(
         weights, ids, ctx.lengths, table, pooling, exclude, padding_idx, grads, keys, payload, bag_count, offsets,
     )

@@ -372,3 +372,52 @@ def test_fused_rowwise_adagrad_update_public_function(device):
     fused_rowwise_adagrad_update(pb, acc, torch.empty(0, dtype=torch.int64, device=device),
                                  torch.empty((0, 2), device=device), lr=1.0, eps=1e-8)
     assert torch.equal(pb, before)
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+def test_concatenated_outputs_train_like_separate_ones(device, dtype):
+    """A model that concatenates the lookups into its token slots
+    (src/model.py:4395-4420) hands each feature's backward a column slice of
+    one [B, sum(D)] gradient.  The slices are read in place and the step
+    leaves every weight and accumulator bit-identical to the same gradients
+    given as separate contiguous tensors."""
+
+    announce("concatenated_outputs", dtype)
+    specs = [("p0", 5000, 16), ("p1", 900, 24), ("s0", 20000, 32), ("s1", 70, 8), ("p2", 3000, 12)]
+    rng = np.random.default_rng(41)
+    B = 512
+    ids, lens = {}, {}
+    for n, r, _ in specs:
+        if n.startswith("p"):
+            ln = rng.integers(0, 7, size=B)
+            lens[n] = torch.from_numpy(ln).to(device)
+            ids[n] = torch.from_numpy(np.minimum(rng.zipf(1.2, size=int(ln.sum())) - 1, r - 1)).to(device)
+        else:
+            ids[n] = torch.from_numpy(np.minimum(rng.zipf(1.2, size=B) - 1, r - 1)).to(device)
+    g_tokens = torch.randn(B, sum(d for _, _, d in specs), generator=torch.Generator().manual_seed(5)).to(dtype)
+    results = []
+    for concat in (True, False):
+        torch.manual_seed(3)
+        mods = [m.to(dtype) for m in _modules(device, specs)]
+        opt = ShardedRowWiseAdagrad([m.weight for m in mods], lr=0.05, eps=1e-8)
+        by_name = {n: m for (n, _, _), m in zip(specs, mods)}
+        for _ in range(2):
+            opt.zero_grad(set_to_none=True)
+            outs = pooled_embedding_lookup(
+                [(by_name[n], ids[n], lens[n], "mean" if n != "p2" else "sum", "exclude") for n, _, _ in specs
+                 if n.startswith("p")])
+            outs += grouped_sharded_embedding_lookup([(by_name[n], ids[n]) for n, _, _ in specs if n.startswith("s")])
+            order = [n for n, _, _ in specs if n.startswith("p")] + [n for n, _, _ in specs if n.startswith("s")]
+            dims = {n: d for n, _, d in specs}
+            cols = np.concatenate([[0], np.cumsum([dims[n] for n in order])[:-1]])
+            g = g_tokens[:, : sum(dims.values())].to(device)
+            if concat:
+                torch.cat(outs, dim=1).backward(g)
+            else:
+                parts = [g[:, int(c): int(c) + dims[n]].contiguous() for n, c in zip(order, cols)]
+                torch.autograd.backward(outs, parts)
+            opt.step()
+        torch.cuda.synchronize()
+        results.append([m.weight.detach().clone() for m in mods] + [opt.state[m.weight]["sum"].clone() for m in mods])
+    for a, b in zip(*results):
+        assert torch.equal(a, b)
