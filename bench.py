@@ -1153,7 +1153,8 @@ def ceilings(torch, device) -> dict:
     16..512 bytes from one 64 GiB-class table through ``mdl_forward``
     (unpooled), each timed with HIP events over 10 launches behind a spin
     kernel.  The gather's rows/s at small rows is the request ceiling the
-    step's kernels are compared with."""
+    step's kernels are compared with; the same gather over tables of 1 to 192
+    GiB shows whether address translation bounds it."""
 
     from mdl_amd import ops
 
@@ -1219,6 +1220,27 @@ def ceilings(torch, device) -> dict:
         gc.collect()
         torch.cuda.empty_cache()
     out["random_row_gather"] = rows_out
+    # Address translation: the same gather of 16 M uniformly random rows from
+    # tables of 1 GiB to 192 GiB (c4's 8 large bf16 tables hold 192 GB).  A
+    # rate that holds as the footprint grows past what the TLBs map says the
+    # gathers are bound by memory requests, not by page walks.
+    footprint = []
+    for row_bytes in (64, 128):
+        dim = row_bytes // 4
+        for gib in (1, 16, 64, 192):
+            rows = (gib << 30) // row_bytes
+            table = torch.empty((rows, dim), dtype=torch.float32, device=device)
+            ids = torch.randint(0, rows, (n,), dtype=torch.int64, device=device, generator=gen)
+            plan = ops.GroupPlan()
+            plan.add_feature(table, pooling="none")
+            outbuf = torch.empty((n, dim), dtype=torch.float32, device=device)
+            ms = timed(lambda: ops.grouped_forward(plan, [ids], [None], with_backward=False, outputs=[outbuf]))
+            footprint.append({"row_bytes": row_bytes, "table_gib": gib, "rows": n, "ms": ms,
+                              "rows_per_s": n / (ms * 1e-3)})
+            del table, ids, outbuf, plan
+            gc.collect()
+            torch.cuda.empty_cache()
+    out["random_row_footprint"] = footprint
     return out
 
 
