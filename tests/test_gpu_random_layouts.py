@@ -1,0 +1,136 @@
+"""Randomised layouts through the fused step, checked against the oracle.
+
+Each seed draws a whole plan: 2-8 tables of 2 to 200 k rows, widths from 1
+to 300 (rows narrower than a lane's vector, unaligned rows, rows wider than
+a wave covers), fp32 or bf16 per table, 2-10 features over them (tables
+read by several features, pooled by sum or mean under either null policy,
+or unpooled), bags of 0-12 ids, Zipf or uniform ids with padding ids and
+ids outside their table.  One ``SparseStep`` step (lookup, sort, segment
+reduce, row-wise Adagrad) is compared with ``oracle.sparse_step`` on the
+outputs, every weight row and every accumulator (src/model.py:509-678,
+src/optim.py:31-62,299-357), and the step's error count with the number of
+ids outside their table (src/embeddings.py:140-147).
+"""
+
+import sys
+
+import numpy as np
+import pytest
+import torch
+
+from mdl_amd import ops
+from mdl_amd.sparse_step import SparseStep
+from oracle import oracle as O
+from parity_helpers import assert_close
+
+pytestmark = pytest.mark.gpu
+
+WIDTHS = [1, 2, 3, 4, 8, 12, 16, 24, 32, 48, 64, 100, 128, 130, 256, 300]
+
+
+def announce(*parts):
+    print("CASE", *parts, flush=True)
+    sys.stdout.flush()
+
+
+def _draw(seed):
+    rng = np.random.default_rng(1000 + seed)
+    T = int(rng.integers(2, 9))
+    rows = [int(np.exp(rng.uniform(np.log(2), np.log(200_000)))) for _ in range(T)]
+    dims = [int(rng.choice(WIDTHS)) for _ in range(T)]
+    bf16 = [bool(rng.random() < 0.4) for _ in range(T)]
+    F = int(rng.integers(2, 11))
+    feats = []
+    for f in range(F):
+        t = int(rng.integers(0, T)) if (f >= T or rng.random() < 0.3) else f
+        feats.append({"table": t, "pooling": int(rng.choice([0, 1, 2])), "exclude": int(rng.integers(0, 2))})
+    return rng, rows, dims, bf16, feats
+
+
+def _ids(rng, n, rows):
+    zipf = rng.random() < 0.5
+    x = (rng.zipf(1.2, size=n) - 1) % rows if zipf else rng.integers(0, rows, size=n)
+    x = x.astype(np.int64)
+    x[rng.random(n) < 0.05] = 0                                # padding / null ids
+    bad = rng.random(n) < 0.01
+    x[bad] = np.where(rng.random(int(bad.sum())) < 0.5, rows + rng.integers(0, 5, int(bad.sum())), -1)
+    return x
+
+
+@pytest.mark.parametrize("seed", range(40))
+def test_random_layout_step_matches_oracle(device, seed):
+    rng, rows, dims, bf16, feats = _draw(seed)
+    B = int(rng.integers(1, 700))
+    announce("random_layout", seed, rows, dims, bf16, feats, B)
+    W0 = []
+    for r, d, b in zip(rows, dims, bf16):
+        w = rng.standard_normal((r, d)).astype(np.float32)
+        if b:
+            w = torch.from_numpy(w).to(torch.bfloat16).float().numpy()
+        W0.append(w)
+    A0 = [rng.random(r).astype(np.float32) for r in rows]
+    tabs = [torch.from_numpy(w).to(torch.bfloat16 if b else torch.float32).to(device) for w, b in zip(W0, bf16)]
+    accs = [torch.from_numpy(a.copy()).to(device) for a in A0]
+    plan = ops.GroupPlan()
+    for f in feats:
+        plan.add_feature(tabs[f["table"]], pooling={0: "none", 1: "sum", 2: "mean"}[f["pooling"]],
+                         null_policy="exclude" if f["exclude"] else "include_as_padding", state=accs[f["table"]])
+    ids, lens, parts = [], [], []
+    for f in feats:
+        t = f["table"]
+        if f["pooling"] == 0:
+            x = _ids(rng, B, rows[t])
+            lens.append(None)
+            parts.append(np.array([B]))
+        else:
+            ln = rng.integers(0, 13, size=B)
+            ln[rng.random(B) < 0.1] = 0
+            x = _ids(rng, int(ln.sum()), rows[t])
+            lens.append(ln)
+            parts.append(ln)
+        ids.append(x)
+    fdims = [dims[f["table"]] for f in feats]
+    fdt = [torch.bfloat16 if bf16[f["table"]] else torch.float32 for f in feats]
+    S = sum(fdims)
+    cols = np.concatenate([[0], np.cumsum(fdims)[:-1]]).astype(np.int64)
+    g_slot = rng.standard_normal((B, S))
+    outs = [torch.empty((B, d), dtype=dt, device=device) for d, dt in zip(fdims, fdt)]
+    grads = []
+    for f, (c, d, dt) in enumerate(zip(cols, fdims, fdt)):
+        g = torch.from_numpy(g_slot[:, c: c + d].astype(np.float32)).to(dt)
+        g_slot[:, c: c + d] = g.double().numpy()  # the oracle sees the rounded gradient
+        grads.append(g.to(device))
+    err = torch.zeros(1, dtype=torch.int32, device=device)
+    step = SparseStep(plan, torch.from_numpy(np.concatenate(ids)).to(device),
+                      torch.from_numpy(np.concatenate(parts)).to(device), [x.size for x in ids],
+                      [0 if ln is None else B for ln in lens], outs, grads, error_count=err)
+    lr, eps = 0.03, 1e-8
+    step.step(lr, eps)
+    torch.cuda.synchronize()
+
+    ofeats, offs, bag_off, ids_off = [], [], 0, 0
+    for f, x, ln, c in zip(feats, ids, lens, cols):
+        ofeats.append({"table": f["table"], "pooling": f["pooling"], "exclude": f["exclude"], "ids_off": ids_off,
+                       "bag_off": bag_off, "num_bags": 0 if ln is None else B, "out_col": int(c)})
+        if ln is not None:
+            o = O.offsets_of(ln)
+            offs.append(o)
+            bag_off += len(o)
+        ids_off += x.size
+    off_all = np.concatenate(offs) if offs else np.zeros(1, np.int64)
+    tables = [{"W": w.copy(), "acc": a.copy(), "is_bf16": b} for w, a, b in zip(W0, A0, bf16)]
+    ref = O.sparse_step(ofeats, tables, np.concatenate(ids), off_all, S, g_slot, lr, eps)
+    absw = [{"W": np.abs(w), "acc": np.zeros_like(a)} for w, a in zip(W0, A0)]
+    mag = O.sparse_step(ofeats, absw, np.concatenate(ids), off_all, S, np.zeros_like(g_slot), 0.0, 1.0)
+
+    n_bad = sum(int(((x < 0) | (x >= rows[f["table"]])).sum()) for f, x in zip(feats, ids))
+    assert int(err.item()) == n_bad
+    for f, (o, c, d) in enumerate(zip(outs, cols, fdims)):
+        rt = 1e-2 if fdt[f] == torch.bfloat16 else 1e-5
+        assert_close(o.float().cpu().numpy(), ref[:, c: c + d], rt, 1e-6 if rt < 1e-3 else 1e-2,
+                     mag[:, c: c + d], what=f"output of feature {f}")
+    for t in range(len(rows)):
+        rt = 1e-2 if bf16[t] else 1e-5
+        assert_close(tabs[t].float().cpu().numpy(), tables[t]["W"], rt, 1e-6 if not bf16[t] else 1e-2,
+                     what=f"weights of table {t}")
+        assert_close(accs[t].cpu().numpy(), tables[t]["acc"], 1e-5, 1e-7, what=f"accumulators of table {t}")
