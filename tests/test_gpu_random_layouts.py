@@ -9,7 +9,8 @@ ids outside their table.  One ``SparseStep`` step (lookup, sort, segment
 reduce, row-wise Adagrad) is compared with ``oracle.sparse_step`` on the
 outputs, every weight row and every accumulator (src/model.py:509-678,
 src/optim.py:31-62,299-357), and the step's error count with the number of
-ids outside their table (src/embeddings.py:140-147).
+ids outside their table (src/embeddings.py:140-147).  The drop-in modules
+and optimizer are then trained under drawn request lists the same way.
 """
 
 import sys
@@ -21,7 +22,7 @@ import torch
 from mdl_amd import ops
 from mdl_amd.sparse_step import SparseStep
 from oracle import oracle as O
-from parity_helpers import assert_close
+from parity_helpers import _check_update, assert_close
 
 pytestmark = pytest.mark.gpu
 
@@ -134,3 +135,85 @@ def test_random_layout_step_matches_oracle(device, seed):
         assert_close(tabs[t].float().cpu().numpy(), tables[t]["W"], rt, 1e-6 if not bf16[t] else 1e-2,
                      what=f"weights of table {t}")
         assert_close(accs[t].cpu().numpy(), tables[t]["acc"], 1e-5, 1e-7, what=f"accumulators of table {t}")
+
+
+@pytest.mark.parametrize("seed", range(12))
+def test_random_dropin_training_matches_oracle(device, seed):
+    """The drop-in modules under drawn request lists: 3-7 ``ShardedEmbedding``
+    tables (widths 1-300, fp32 or bf16 each), pooled requests (sum or mean,
+    either null policy) through ``pooled_embedding_lookup``, unpooled ones
+    through ``grouped_sharded_embedding_lookup``, a table requested several
+    times in one step (its gradients merge), two ``ShardedRowWiseAdagrad``
+    steps.  Each step is checked from the weights and accumulators it began
+    with against the oracle, within bounds set by the same sums over |terms|
+    (a row whose terms cancel keeps an fp32 error of rtol * sum|terms|):
+    per-id gradients of every request
+    (src/model.py:564-570), coalesced per table (src/optim.py:321-324), the
+    row-wise update (src/optim.py:31-62); a bf16 table's gradient is stored
+    in bf16 as the reference's is."""
+
+    from mdl_amd.embeddings import (EmbeddingTableSpec, ShardedEmbedding, grouped_sharded_embedding_lookup,
+                                    plan_embedding_shards, pooled_embedding_lookup)
+    from mdl_amd.optim import ShardedRowWiseAdagrad
+
+    rng = np.random.default_rng(5000 + seed)
+    T = int(rng.integers(3, 8))
+    rows = [int(np.exp(rng.uniform(np.log(3), np.log(100_000)))) for _ in range(T)]
+    dims = [int(rng.choice(WIDTHS)) for _ in range(T)]
+    bf16 = [bool(rng.random() < 0.4) for _ in range(T)]
+    announce("random_dropin", seed, rows, dims, bf16)
+    specs = [(f"t{t}", rows[t], dims[t]) for t in range(T)]
+    plan = plan_embedding_shards([EmbeddingTableSpec(n, r, d) for n, r, d in specs], world_size=1,
+                                 strategy="row_wise", table_wise_max_rows=32)
+    mods = []
+    for (n, r, d), b in zip(specs, bf16):
+        m = ShardedEmbedding(r, d, table_name=n, shard_spec=plan.tables[n], collect_stats=False,
+                             dtype=torch.bfloat16 if b else torch.float32).to(device)
+        mods.append(m)
+    opt = ShardedRowWiseAdagrad([m.weight for m in mods], lr=0.05, eps=1e-8)
+    B = int(rng.integers(1, 300))
+    for step in range(2):
+        W = [m.weight.detach().float().cpu().numpy().copy() for m in mods]
+        A = [opt.state[m.weight]["sum"].cpu().numpy().copy() for m in mods]
+        pooled_req, single_req, ref_req = [], [], []
+        for _ in range(int(rng.integers(2, 9))):
+            t = int(rng.integers(0, T))
+            if rng.random() < 0.6:
+                ln = rng.integers(0, 9, size=B)
+                x = np.minimum(rng.zipf(1.2, size=int(ln.sum())) - 1, rows[t] - 1)
+                mode = "mean" if rng.random() < 0.5 else "sum"
+                pol = "exclude" if rng.random() < 0.5 else "include_as_padding"
+                pooled_req.append((mods[t], torch.from_numpy(x).to(device), torch.from_numpy(ln).to(device), mode, pol))
+                ref_req.append(("p", t, x, ln, mode, pol))
+            else:
+                x = rng.integers(0, rows[t], size=B)
+                single_req.append((mods[t], torch.from_numpy(x).to(device)))
+                ref_req.append(("s", t, x, None, "none", "exclude"))
+        opt.zero_grad(set_to_none=True)
+        outs = (pooled_embedding_lookup(pooled_req) if pooled_req else []) + \
+               (grouped_sharded_embedding_lookup(single_req) if single_req else [])
+        order = [r for r in ref_req if r[0] == "p"] + [r for r in ref_req if r[0] == "s"]
+        grads = [torch.from_numpy(rng.standard_normal(tuple(o.shape)).astype(np.float32)).to(o.dtype).to(device)
+                 for o in outs]
+        torch.autograd.backward(outs, grads)
+        opt.step()
+        per_table = {t: ([], [], []) for t in range(T)}
+        for (kind, t, x, ln, mode, pol), g in zip(order, grads):
+            gh = g.float().cpu().numpy()
+            r, v = O.per_id_grads(x, ln, gh, mode, pol)
+            _, va = O.per_id_grads(x, ln, np.abs(gh), mode, pol)
+            per_table[t][0].append(r)
+            per_table[t][1].append(v.reshape(-1, dims[t]))
+            per_table[t][2].append(va.reshape(-1, dims[t]))
+        for t in range(T):
+            if per_table[t][0]:
+                r, v = O.coalesce(np.concatenate(per_table[t][0]), np.concatenate(per_table[t][1]))
+                _, va = O.coalesce(np.concatenate(per_table[t][0]), np.concatenate(per_table[t][2]))
+            else:
+                r, v, va = np.zeros(0, np.int64), np.zeros((0, dims[t])), np.zeros((0, dims[t]))
+            if bf16[t]:
+                v = torch.from_numpy(v).to(torch.bfloat16).double().numpy()
+            rt = 1e-2 if bf16[t] else 1e-5
+            _check_update(f"step {step} table {t}", mods[t].weight.detach().float().cpu().numpy(),
+                          opt.state[mods[t].weight]["sum"].cpu().numpy(), W[t], A[t], r, v, va, 0.05, 1e-8,
+                          rt, 1e-6 if bf16[t] else 1e-7, bf16[t], acc_rtol=rt)
