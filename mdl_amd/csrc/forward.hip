@@ -605,6 +605,74 @@ __device__ __forceinline__ void pooled_chunk(const Feat& f, int64_t first_bag, i
   }
 }
 
+// A chunk whose bags hold one id each (single-id bags, as c4's): bag b's
+// pooled row is the row staged for its id, or zeros for an id that pools with
+// weight 0, and its weight is 1 or 0, so the chunk is a gather of the staged
+// rows straight to the output rows -- no walk, no staged output, two groups
+// of row loads in flight as in gather_chunk.  The rows are 0 + row, the bits
+// the walk gives (its sum starts at +0; a mean divides by max(1, 1) = 1).
+template <typename TW, typename TO, int C>
+__device__ __forceinline__ void unit_bags_chunk(const Feat& f, int64_t first_bag, int nb, const PoolStage& st,
+                                                const FwdArgs& a) {
+  constexpr int kUnroll = unroll_for<C>();
+  const int lane = lane_id();
+  const int L = lanes_for(f.dim, C);
+  const int G = kWave / L;
+  const int slot = lane / L, sub = lane % L;
+  const int ncb = (f.dim + L * C - 1) / (L * C);
+  const TW* W = static_cast<const TW*>(f.weight);
+  TO* out = static_cast<TO*>(f.out);
+  const int step = G * kUnroll;
+  constexpr bool kSplit = MDL_SPLIT_ROWS && std::is_same_v<TW, float> && std::is_same_v<TO, float> && C == 8;
+  for (int cb = 0; cb < ncb; ++cb) {
+    const int col = kSplit ? cb * L * C + sub * 4 : (cb * L + sub) * C;
+    const bool col_ok = col < f.dim;
+    const int pieces = kSplit ? (col + 4 * L < f.dim ? 2 : 1) : 0;
+    auto load_rows = [&](int base, float (&v)[kUnroll][C]) {
+#pragma unroll
+      for (int u = 0; u < kUnroll; ++u) {
+        const int i = base + u * G + slot;
+        const uint32_t r = i < nb ? st.row[i] : kNoRow;
+        const bool ok = r != kNoRow && col_ok;
+        if constexpr (kSplit)
+          RowIO<float, C>::load_pieces(ok ? W + (int64_t)r * f.dim + col : zero_row<float>(), 4 * L,
+                                       ok ? pieces : 0, v[u]);
+        else
+          RowIO<TW, C>::load(ok ? W + (int64_t)r * f.dim + col : zero_row<TW>(), v[u]);
+      }
+    };
+    auto store_rows = [&](int base, const float (&v)[kUnroll][C]) {
+#pragma unroll
+      for (int u = 0; u < kUnroll; ++u) {
+        const int i = base + u * G + slot;
+        if (i < nb && col_ok) {
+          float r[C];
+#pragma unroll
+          for (int k = 0; k < C; ++k) r[k] = 0.f + v[u][k];
+          if constexpr (kSplit)
+            RowIO<float, C>::template store_pieces<kOutPolicy>(out + (first_bag + i) * f.out_stride + col, 4 * L,
+                                                               pieces, r);
+          else
+            RowIO<TO, C>::template store<kOutPolicy>(out + (first_bag + i) * f.out_stride + col, r);
+        }
+      }
+    };
+    float va[kUnroll][C], vb[kUnroll][C];
+    load_rows(0, va);
+    for (int base = 0; base < nb; base += 2 * step) {
+      const bool more = base + step < nb;
+      if (more) load_rows(base + step, vb);
+      store_rows(base, va);
+      if (!more) break;
+      if (base + 2 * step < nb) load_rows(base + 2 * step, va);
+      store_rows(base + step, vb);
+    }
+  }
+  if (a.bag_count != nullptr)
+    for (int i = lane; i < nb; i += kWave)
+      st_policy(a.bag_count + f.payload_base + first_bag + i, st.row[i] != kNoRow ? 1.f : 0.f);
+}
+
 // Sort keys and payloads of a pooled chunk, one id per lane so the stores
 // coalesce; an id's bag comes from a binary search of the staged bounds,
 // resumed from the lane's previous id.  Returns the invalid ids among those
@@ -702,8 +770,17 @@ __global__ MDL_OCCUPANCY __launch_bounds__(kFwdWaves * kWave) void forward_kerne
   }
   int bad = 0;
   const PoolChunk pc = stage_pooled(f, ch.first, ch.count, s_st[w], a, bad);
+  // Every bag of the chunk one id long (bounds 0, 1, ..., nb after staging,
+  // every row staged): a gather instead of the walk.
+  bool unit = pc.len == ch.count && pc.lim == pc.len;
+  if (unit) {
+    bool off = false;
+    for (int b = lane_id(); b < ch.count; b += kWave) off |= s_st[w].off[b + 1] - s_st[w].off[b] != 1;
+    unit = __ballot(off) == 0;
+  }
   with_width<TW, kVec>(v % kWidths, [&]<int C>() {
-    pooled_chunk<TW, TO, C>(f, ch.first, ch.count, s_st[w], pc, s_out[w], a);
+    if (unit) unit_bags_chunk<TW, TO, C>(f, ch.first, ch.count, s_st[w], a);
+    else pooled_chunk<TW, TO, C>(f, ch.first, ch.count, s_st[w], pc, s_out[w], a);
   });
   // After the walk, so that its stores never hold up the walk's loads.
   bad += pooled_keys(f, ch.first, ch.count, s_st[w], pc, a);

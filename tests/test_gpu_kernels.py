@@ -1199,3 +1199,75 @@ def test_sequence_step_graph_replays_match_eager(device):
         assert torch.equal(out_g, out_e), f"replay {r}: window"
         assert torch.equal(tab_g, tab_e), f"replay {r}: table"
         assert torch.equal(acc_g, acc_e), f"replay {r}: state"
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+@pytest.mark.parametrize("dim", [3, 16, 64, 130, 300])
+def test_single_id_bags_match_oracle(device, dtype, dim):
+    """Pooled features whose bags hold one id each (c4's) take a gather
+    instead of the pooled walk: each output row is its id's row bit for bit
+    (zeros for a null under "exclude" and for ids outside the table), the bag
+    weights feed the mean's backward, and a feature with one two-id bag per
+    chunk takes the walk on the same ids.  Sum and mean, both null policies,
+    through the fused step against the oracle."""
+
+    from mdl_amd.sparse_step import SparseStep
+
+    announce("single_id_bags", dtype, dim)
+    rng = np.random.default_rng(95 + dim)
+    B, rows = 2000, 5000
+    bf16 = dtype == torch.bfloat16
+    cases = [("sum", "exclude", False), ("mean", "exclude", False), ("mean", "include_as_padding", False),
+             ("sum", "include_as_padding", False), ("mean", "exclude", True)]
+    W0 = [rng.standard_normal((rows, dim)).astype(np.float32) for _ in cases]
+    if bf16:
+        W0 = [torch.from_numpy(w).to(torch.bfloat16).float().numpy() for w in W0]
+    tabs = [torch.from_numpy(w).to(dtype).to(device) for w in W0]
+    A0 = [rng.random(rows).astype(np.float32) for _ in cases]
+    accs = [torch.from_numpy(a.copy()).to(device) for a in A0]
+    plan = ops.GroupPlan()
+    ids, lens = [], []
+    for t, (mode, pol, two) in enumerate(cases):
+        plan.add_feature(tabs[t], pooling=mode, null_policy=pol, state=accs[t])
+        ln = np.ones(B, dtype=np.int64)
+        if two:
+            ln[::97] = 2  # one two-id bag in most chunks: the walk
+        x = (rng.zipf(1.2, size=int(ln.sum())) - 1) % rows
+        x[rng.random(x.size) < 0.05] = 0
+        x[rng.random(x.size) < 0.01] = rows + 3
+        ids.append(x.astype(np.int64))
+        lens.append(ln)
+    S = dim * len(cases)
+    outs = [torch.empty((B, dim), dtype=dtype, device=device) for _ in cases]
+    g_slot = rng.standard_normal((B, S))
+    grads = []
+    for t in range(len(cases)):
+        g = torch.from_numpy(g_slot[:, t * dim: (t + 1) * dim].astype(np.float32)).to(dtype)
+        g_slot[:, t * dim: (t + 1) * dim] = g.double().numpy()
+        grads.append(g.to(device))
+    err = torch.zeros(1, dtype=torch.int32, device=device)
+    st = SparseStep(plan, torch.from_numpy(np.concatenate(ids)).to(device),
+                    torch.from_numpy(np.concatenate(lens)).to(device), [x.size for x in ids], [B] * len(cases),
+                    outs, grads, error_count=err)
+    st.step(0.03, 1e-8)
+    torch.cuda.synchronize()
+    feats, offs, bag_off, ids_off = [], [], 0, 0
+    for t, ((mode, pol, _), x, ln) in enumerate(zip(cases, ids, lens)):
+        feats.append({"table": t, "pooling": 1 if mode == "sum" else 2, "exclude": int(pol == "exclude"),
+                      "ids_off": ids_off, "bag_off": bag_off, "num_bags": B, "out_col": t * dim})
+        o = O.offsets_of(ln)
+        offs.append(o)
+        bag_off += len(o)
+        ids_off += x.size
+    tables = [{"W": w.copy(), "acc": a.copy(), "is_bf16": bf16} for w, a in zip(W0, A0)]
+    ref = O.sparse_step(feats, tables, np.concatenate(ids), np.concatenate(offs), S, g_slot, 0.03, 1e-8)
+    assert int(err.item()) == sum(int((x >= rows).sum()) for x in ids)
+    for t, (mode, pol, two) in enumerate(cases):
+        got = outs[t].float().cpu().numpy()
+        want = ref[:, t * dim: (t + 1) * dim]
+        if two:
+            assert_close(got, want, RTOL[dtype], 1e-6 if not bf16 else 1e-2)
+        else:
+            assert np.array_equal(got, want.astype(np.float32)), f"{mode}/{pol} output"
+        assert_close(tabs[t].float().cpu().numpy(), tables[t]["W"], RTOL[dtype], 1e-6 if not bf16 else 1e-2)
+        assert_close(accs[t].cpu().numpy(), tables[t]["acc"], 1e-5, 1e-7)
