@@ -231,7 +231,15 @@ def draw_batch(rng: np.random.Generator, wl: Workload):
 
 
 def algorithmic_bytes(wl: Workload, ids, lengths) -> dict:
-    """Per-step algorithmic HBM bytes (SURVEY 8(d) formula) and its parts."""
+    """Per-step algorithmic HBM bytes and their parts.  Pooled workloads:
+    sum over tables t of 16 n_t + 16 (b_t + 1) + 3 U_t D_t s_w + 8 U_t, plus
+    2 B D_f 4 per feature f -- ids and offsets read by the forward and the
+    backward, each distinct row read by the lookup and read and written by
+    the update, its fp32 state read and written, the fp32 pooled output
+    written and its gradient read (n_t ids, b_t bags and U_t distinct rows of
+    table t, s_w bytes per weight).  Sequences replace the pooled output by
+    the padded window and its mask and read the gradient at the valid
+    positions only."""
 
     esize = 4 if wl.dtype == "fp32" else 2
     if wl.kind == "sequence":
