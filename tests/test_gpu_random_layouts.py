@@ -15,6 +15,7 @@ and optimizer are then trained under drawn request lists, and
 """
 
 import sys
+from types import SimpleNamespace
 
 import numpy as np
 import pytest
@@ -59,11 +60,11 @@ def _ids(rng, n, rows):
     return x
 
 
-@pytest.mark.parametrize("seed", range(40))
-def test_random_layout_step_matches_oracle(device, seed):
+def _random_step(device, seed, error_count=None):
+    """The drawn layout of ``seed`` as a ``SparseStep`` with its host data."""
+
     rng, rows, dims, bf16, feats = _draw(seed)
     B = int(rng.integers(1, 700))
-    announce("random_layout", seed, rows, dims, bf16, feats, B)
     W0 = []
     for r, d, b in zip(rows, dims, bf16):
         w = rng.standard_normal((r, d)).astype(np.float32)
@@ -102,10 +103,22 @@ def test_random_layout_step_matches_oracle(device, seed):
         g = torch.from_numpy(g_slot[:, c: c + d].astype(np.float32)).to(dt)
         g_slot[:, c: c + d] = g.double().numpy()  # the oracle sees the rounded gradient
         grads.append(g.to(device))
-    err = torch.zeros(1, dtype=torch.int32, device=device)
     step = SparseStep(plan, torch.from_numpy(np.concatenate(ids)).to(device),
                       torch.from_numpy(np.concatenate(parts)).to(device), [x.size for x in ids],
-                      [0 if ln is None else B for ln in lens], outs, grads, error_count=err)
+                      [0 if ln is None else B for ln in lens], outs, grads, error_count=error_count)
+    return SimpleNamespace(step=step, rows=rows, dims=dims, bf16=bf16, feats=feats, B=B, W0=W0, A0=A0, tabs=tabs,
+                           accs=accs, ids=ids, lens=lens, fdims=fdims, fdt=fdt, S=S, cols=cols, g_slot=g_slot,
+                           outs=outs)
+
+
+@pytest.mark.parametrize("seed", range(40))
+def test_random_layout_step_matches_oracle(device, seed):
+    err = torch.zeros(1, dtype=torch.int32, device=device)
+    z = _random_step(device, seed, err)
+    announce("random_layout", seed, z.rows, z.dims, z.bf16, z.feats, z.B)
+    rows, bf16, feats, B, W0, A0, tabs, accs = z.rows, z.bf16, z.feats, z.B, z.W0, z.A0, z.tabs, z.accs
+    ids, lens, fdims, fdt, S, cols, g_slot, outs, step = (z.ids, z.lens, z.fdims, z.fdt, z.S, z.cols, z.g_slot,
+                                                          z.outs, z.step)
     lr, eps = 0.03, 1e-8
     step.step(lr, eps)
     torch.cuda.synchronize()
@@ -299,3 +312,27 @@ def test_random_sequence_step_matches_oracle(device, seed):
         rt = 1e-2 if bf16[t] else 1e-5
         _check_update(f"table {t}", tabs[t].float().cpu().numpy(), accs[t].cpu().numpy(), W0[t], A0[t], r, v, va,
                       lr, eps, rt, 1e-6 if bf16[t] else 1e-7, bf16[t])
+
+
+@pytest.mark.parametrize("seed", range(8))
+def test_random_layout_graph_replays_match_eager(device, seed):
+    """A captured step of a drawn layout (every kernel variant the layout
+    needs: widths, dtypes, aliased tables, the clip on odd seeds) replays bit
+    for bit like eager steps on an identical copy, with eager work and a
+    synchronisation between the replays."""
+
+    eager = _random_step(device, seed)
+    graph = _random_step(device, seed)
+    clip = 1.0 if seed % 2 else None
+    announce("random_layout_graph", seed, eager.rows, eager.dims, eager.bf16, eager.feats, eager.B, clip)
+    lr, eps = 0.03, 1e-8
+    eager.step.step(lr, eps, clip)
+    graph.step.step(lr, eps, clip)  # loads the kernels before the recording
+    graph.step.capture(lr, eps, clip)
+    for r in range(3):
+        eager.step.step(lr, eps, clip)
+        graph.step.replay()
+        torch.cuda.synchronize()
+        _ = float(graph.tabs[0].double().sum())  # eager work between replays
+        for a, b in zip(graph.outs + graph.tabs + graph.accs, eager.outs + eager.tabs + eager.accs):
+            assert torch.equal(a, b), f"replay {r}"
