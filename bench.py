@@ -235,11 +235,13 @@ def algorithmic_bytes(wl: Workload, ids, lengths) -> dict:
     sum over tables t of 16 n_t + 16 (b_t + 1) + 3 U_t D_t s_w + 8 U_t, plus
     2 B D_f 4 per feature f -- ids and offsets read by the forward and the
     backward, each distinct row read by the lookup and read and written by
-    the update, its fp32 state read and written, the fp32 pooled output
-    written and its gradient read (n_t ids, b_t bags and U_t distinct rows of
-    table t, s_w bytes per weight).  Sequences replace the pooled output by
-    the padded window and its mask and read the gradient at the valid
-    positions only."""
+    the update, its fp32 state read and written, the pooled output written
+    and its gradient read (n_t ids, b_t bags and U_t distinct rows of table
+    t, s_w bytes per weight).  The output and its gradient are counted at
+    their element size s_o, which is the tables' (4 fp32, 2 bf16): the
+    step's buffers hold bf16 for bf16 tables, so 2 B D_f s_o per feature.
+    Sequences replace the pooled output by the padded window and its mask
+    and read the gradient at the valid positions only."""
 
     esize = 4 if wl.dtype == "fp32" else 2
     if wl.kind == "sequence":
@@ -261,7 +263,7 @@ def algorithmic_bytes(wl: Workload, ids, lengths) -> dict:
             # ids + lengths read twice, distinct rows 3x, state, padded output +
             # mask, gradient rows at the valid positions
             total += 16 * n + 16 * (wl.batch + 1) + 3 * u * d * esize + 8 * u
-            total += wl.batch * pad * d * 4 + wl.batch * pad + n * d * 4
+            total += wl.batch * pad * d * esize + wl.batch * pad + n * d * esize
         return {"B_alg": total, "n_ids": n_ids, "unique_rows": uniq, "fwd_unique_row_bytes": fwd_rows,
                 "sum_dim": sum(wl.dims[f.table] for f in wl.features)}
     n_t = {}
@@ -284,7 +286,9 @@ def algorithmic_bytes(wl: Workload, ids, lengths) -> dict:
         total += 16 * n + 16 * (bags_t[t] + 1) + 3 * u * d * esize + 8 * u
         fwd_unique_rows_bytes += u * d * esize
     sum_d = sum(wl.dims[f.table] for f in wl.features)
-    total += 2 * wl.batch * sum_d * 4
+    # output and gradient in the output dtype (DeviceStep allocates both in
+    # the tables' dtype)
+    total += 2 * wl.batch * sum_d * esize
     return {
         "B_alg": total,
         "n_ids": n_ids,

@@ -176,7 +176,11 @@ int mdl_bucketize(const int64_t* raw, const uint8_t* valid, int64_t n,
  * by the bucketing of src/dataloader.py:8463-8493 (see mdl_bucketize).
  *   in_offsets [rows+1]: row r holds raw[in_offsets[r] .. in_offsets[r+1])
  *                        (Arrow list offsets; any base);
- *   row_valid  [rows]  : 0 = null row, length 0 (may be NULL: all present);
+ *   row_valid  [rows]  : 0 = null row, length 0 (may be NULL: all present),
+ *                        except under tail truncation, which follows the
+ *                        reference in reading the raw offsets of every row
+ *                        (src/dataloader.py:8583-8604): a null row keeps the
+ *                        last max_length elements of its span;
  *   raw, elem_valid [n_in]: element values and validity (elem_valid may be
  *                        NULL); a null element keeps its slot and buckets to 0;
  *   max_length < 0     : no truncation; truncation MDL_TRUNCATE_HEAD / _TAIL;
@@ -294,22 +298,26 @@ int mdl_pool_backward(const mdl_feature* feats, int32_t num_features,
 /*
  * Sequence gather without pooling, right-aligned into a padded window
  * (src/model.py:3022-3072, alignment :2989-3020, order :3074-3100).
- * ids: [batch, in_len] right-padded; lengths: [batch] (clamped to out_len).
+ * ids: [batch, in_len] right-padded; lengths: [batch].
  * out: [batch, out_len, dim] (odtype); mask: [batch, out_len] bytes.
- * Position p of row b is valid when p >= out_len - len_b; it holds
- * weight[ids[b, p - start]] (oldest_to_newest) or weight[ids[b, len_b-1-(p-start)]]
- * (newest_to_oldest); invalid positions hold 0.
+ * Row b has len_b = clamp(lengths[b], 0, out_len) window entries (none when
+ * in_len == 0); entry rel of row b sits at position p = out_len - len_b + rel
+ * (mask 1) and holds weight[ids[b, src]] with src = min(rel, in_len - 1)
+ * (oldest_to_newest) or min(len_b - 1 - rel, in_len - 1) (newest_to_oldest):
+ * a length past the input width repeats the last input element, as the
+ * reference's clamp of the source position does (:3011-3016).  Other
+ * positions hold 0 (mask 0).
  * feature->out is ignored (out is passed here); feature->payload_base and
- * row_base are used when sort_keys is not NULL: for input position (b, k),
- * sort_keys[k + b*in_len] = row_base + id (sentinel when k >= len_b or padding),
- * payload = payload_base + b*out_len + p(k).  With key_offsets (device int64
- * [batch + 1], nondecreasing; NULL for the dense layout above) the keys are
- * packed: position k < cap_b = key_offsets[b+1] - key_offsets[b] (at most
- * in_len) of row b goes to key_offsets[b] + k and nothing is written past
- * the cap, so a backward over the key_offsets[batch] packed entries sorts no
- * padding.  With cap_b = min(len_b, in_len, out_len) every valid position is
- * kept; a row longer than its cap loses the rest, a shorter one pads its
- * cap with sentinels.
+ * row_base are used when sort_keys is not NULL: for window entry (b, rel),
+ * sort_keys[rel + b*out_len] = row_base + id (sentinel when rel >= len_b or
+ * padding), payload = payload_base + b*out_len + p, so the key arrays hold
+ * batch*out_len entries.  With key_offsets (device int64 [batch + 1],
+ * nondecreasing; NULL for the dense layout above) the keys are packed: entry
+ * rel < cap_b = key_offsets[b+1] - key_offsets[b] (at most out_len) of row b
+ * goes to key_offsets[b] + rel and nothing is written past the cap, so a
+ * backward over the key_offsets[batch] packed entries sorts no padding.
+ * With cap_b = len_b every window entry is kept; a row longer than its cap
+ * loses the rest, a shorter one pads its cap with sentinels.
  */
 int mdl_sequence_forward(const mdl_feature* feature_host, const int64_t* ids,
                          const int64_t* lengths, int64_t batch, int64_t in_len,
@@ -468,7 +476,9 @@ int mdl_backward_coalesce(const mdl_feature* feats, int32_t num_features,
  * max_dim 128 need 45 MiB).  Every call on one GPU shares that GPU's array
  * and leaves its contents behind (the call initialises what it reads), so
  * calls that overlap on one GPU -- on different streams or host threads --
- * race.  Otherwise the same arguments and results as mdl_backward_adagrad.
+ * race.  The scratch used is the current device's: a non-null stream must
+ * belong to the current device, else the call returns MDL_ERR_INVALID.
+ * Otherwise the same arguments and results as mdl_backward_adagrad.
  */
 size_t mdl_noalloc_scratch_bytes(void);
 int mdl_backward_adagrad_noalloc(const mdl_feature* feats, int32_t num_features,

@@ -535,9 +535,11 @@ __device__ __forceinline__ void reduce_chunk_body(const BwdArgs& a, int64_t c, c
 #pragma unroll
     for (int u = 0; u < U; ++u) {
       // (an entry past the slice adds its zero row and finishes nothing)
-      const float inv = mean[u] ? __builtin_amdgcn_rcpf(fmaxf(cnt[u], 1.f)) : 1.f;
+      // grad / max(count, 1) rounded once, then added: the reference's
+      // division (src/model.py:570) and its autograd
+      const BagDivisor div(mean[u] ? fmaxf(cnt[u], 1.f) : 1.f);
 #pragma unroll
-      for (int k = 0; k < C; ++k) acc[k] = fmaf(v[u][k], inv, acc[k]);
+      for (int k = 0; k < C; ++k) acc[k] += div(v[u][k]);
       if (fin[u]) {
         if (own[u]) {
           R.finish(key[u], acc, acc0[u], w[u], coalesce ? hb + (int64_t)st.hc[j + u + 1] - 1 : 0, ss_acc);
@@ -682,7 +684,7 @@ __device__ void reduce_chunk_wide(const BwdArgs& a, int64_t c, const ChunkDesc& 
     const bool col_ok = col < R.dim;
     zero(v);
     for (int e = i0; e < i1; e += kU) {
-      float g[kU][C], inv[kU];
+      float g[kU][C], den[kU];
 #pragma unroll
       for (int u = 0; u < kU; ++u) {
         const bool ok = e + u < i1;
@@ -691,12 +693,14 @@ __device__ void reduce_chunk_wide(const BwdArgs& a, int64_t c, const ChunkDesc& 
         const TG* gp = R.template grad_row<kOne>(pay, mean);
         RowIO<TG, C>::load(ok && col_ok ? gp + col : zero_row<TG>(), g[u]);
         const float cnt = ld_policy(ok && mean ? a.bag_count + pay : zero_row<float>());
-        inv[u] = mean ? __builtin_amdgcn_rcpf(fmaxf(cnt, 1.f)) : 1.f;
+        den[u] = mean ? fmaxf(cnt, 1.f) : 1.f;
       }
 #pragma unroll
-      for (int u = 0; u < kU; ++u)
+      for (int u = 0; u < kU; ++u) {
+        const BagDivisor div(den[u]);
 #pragma unroll
-        for (int k = 0; k < C; ++k) v[k] = fmaf(g[u][k], inv[u], v[k]);
+        for (int k = 0; k < C; ++k) v[k] += div(g[u][k]);
+      }
     }
   };
   auto to_parts = [&](float* part, int i0, int i1) {
@@ -1129,11 +1133,23 @@ constexpr int kMaxDevices = 64;
 static std::mutex g_scratch_mu;
 static void* g_scratch_ptr[kMaxDevices];
 
-static int scratch_for_current_device(void** out) {
+// The scratch of the device the call runs on: the current device, which a
+// non-null stream must belong to (its kernels run on the stream's device, and
+// the array's address differs per device).
+static int scratch_for_stream(hipStream_t stream, void** out) {
   int dev = -1;
   hipError_t e = hipGetDevice(&dev);
   if (e != hipSuccess) return check_hip(e, "hipGetDevice");
   if (dev < 0 || dev >= kMaxDevices) return fail(MDL_ERR_UNSUPPORTED, "mdl_backward_adagrad_noalloc: device index");
+  if (stream != nullptr) {
+    hipDevice_t sdev = -1;
+    e = hipStreamGetDevice(stream, &sdev);
+    if (e != hipSuccess) return check_hip(e, "hipStreamGetDevice");
+    if ((int)sdev != dev)
+      return fail(MDL_ERR_INVALID, "mdl_backward_adagrad_noalloc: the stream belongs to device " +
+                                       std::to_string((int)sdev) + " but device " + std::to_string(dev) +
+                                       " is current; make the stream's device current");
+  }
   std::lock_guard<std::mutex> lock(g_scratch_mu);
   if (g_scratch_ptr[dev] == nullptr) {
     void* p = nullptr;
@@ -1333,7 +1349,7 @@ int mdl_backward_adagrad_noalloc(const mdl_feature* feats, int32_t num_features,
                                          std::to_string(kNoAllocScratchBytes) +
                                          " (fewer entries, tables or a smaller max_dim fit)");
   void* ws = nullptr;
-  rc = scratch_for_current_device(&ws);
+  rc = scratch_for_stream(as_stream(stream), &ws);
   if (rc) return rc;
   return mdl_backward_adagrad(feats, num_features, tables, num_tables, max_dim, sort_keys, sort_payload, n, count,
                               key_bits, bag_count, lr, eps, grad_scale, ws, kNoAllocScratchBytes, classes, stream);

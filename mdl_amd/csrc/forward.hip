@@ -444,10 +444,12 @@ __device__ __forceinline__ void pooled_chunk(const Feat& f, int64_t first_bag, i
 
   // Pooled row of bag b from its sum and weight: staged, or stored at once.
   auto emit_row = [&](int bag, const float (&sum)[C], float wsum, int col, bool col_ok, bool emit_cnt) {
-    const float inv = mean ? __builtin_amdgcn_rcpf(fmaxf(wsum, 1.f)) : 1.f;
+    // sums / max(count, 1), the reference's division (src/model.py:570),
+    // once per pooled row
+    const float den = mean ? fmaxf(wsum, 1.f) : 1.f;
     float r[C];
 #pragma unroll
-    for (int k = 0; k < C; ++k) r[k] = sum[k] * inv;
+    for (int k = 0; k < C; ++k) r[k] = sum[k] / den;
     if (staged) {
       if (col_ok) {
         if constexpr (kSplit) lds_put_pieces<C>(s_out + bag * f.dim + col, 4 * L, pieces_of(col), r);
@@ -847,9 +849,10 @@ __device__ __forceinline__ void unpool_chunk(const Feat& f, int64_t first_bag, i
         // outside [0, num_rows).
         const int64_t src = by_pos ? row : id[u];
         const bool dead = (exclude && id[u] == 0) || (uint64_t)src >= (uint64_t)f.num_rows;
-        const float sc = dead ? 0.f : (mean ? __builtin_amdgcn_rcpf(fmaxf(cnt[u], 1.f)) : 1.f);
+        // grad / max(count, 1): the autograd of the reference's division
+        const BagDivisor div(mean ? fmaxf(cnt[u], 1.f) : 1.f);
 #pragma unroll
-        for (int k = 0; k < C; ++k) v[u][k] *= sc;
+        for (int k = 0; k < C; ++k) v[u][k] = dead ? 0.f : div(v[u][k]);
         if (valid[u] && col_ok) RowIO<TW, C>::store(dst + row * f.dim + col, v[u]);
       }
     }
@@ -910,11 +913,22 @@ struct SeqArgs {
   int32_t* error_count;
 };
 
+// Valid window positions of row b: the length clamped to [0, out_len], and
+// none when the input is empty (src/model.py:2998-3011).  A length past the
+// input width keeps its positions: each one past the input repeats the last
+// input element (the reference clamps the source position to in_len - 1,
+// :3014-3016), see seq_src.
 __device__ __forceinline__ int64_t seq_len(const SeqArgs& a, int64_t b) {
+  if (a.in_len <= 0) return 0;
   int64_t n = a.lengths[b];
   n = n < 0 ? 0 : n;
-  n = n > a.out_len ? a.out_len : n;
-  return n > a.in_len ? a.in_len : n;
+  return n > a.out_len ? a.out_len : n;
+}
+
+// Input position of window entry rel in [0, len) of a row.
+__device__ __forceinline__ int64_t seq_src(const SeqArgs& a, int64_t len, int64_t rel) {
+  const int64_t k = a.order == MDL_SEQ_OLDEST_TO_NEWEST ? rel : len - 1 - rel;
+  return k < a.in_len ? k : a.in_len - 1;
 }
 
 // One wave per chunk of kSeqRows output positions [p0, p0 + np) of one row
@@ -947,7 +961,6 @@ __device__ __forceinline__ void seq_chunk(const SeqArgs& a, int64_t b, int64_t p
   const int nz = start <= p0 ? 0 : (start - p0 < np ? (int)(start - p0) : np);
   const int count = np - nz;
   const int64_t k0 = p0 + nz - start;  // run position of the chunk's first id
-  const bool forward = a.order == MDL_SEQ_OLDEST_TO_NEWEST;
   const int64_t* ids = a.ids + b * a.in_len;
   const int step = G * kUnroll;
   int bad = 0;
@@ -962,7 +975,7 @@ __device__ __forceinline__ void seq_chunk(const SeqArgs& a, int64_t b, int64_t p
 #pragma unroll
       for (int u = 0; u < kUnroll; ++u) {
         const int i = base + u * G + slot;
-        nid[u] = i < count ? ids[forward ? k0 + i : len - 1 - (k0 + i)] : 0;
+        nid[u] = i < count ? ids[seq_src(a, len, k0 + i)] : 0;
       }
     };
     auto load_rows = [&](int base, float (&v)[kUnroll][C]) {
@@ -1039,35 +1052,38 @@ __global__ MDL_OCCUPANCY __launch_bounds__(kFwdWaves * kWave) void sequence_kern
   with_width<TW, kVec>(width, [&]<int C>() { seq_chunk<TW, TO, C>(a, b, p0, np); });
 }
 
-// Sort keys/payloads of the input positions (b, k) of a sequence feature; one
-// block per kSeqKeys positions of one row, so the row's length is one load.
-// Dense: position k of row b at b * in_len + k.  Packed (key_offsets): the
-// row's first cap = key_offsets[b + 1] - key_offsets[b] positions (at most
-// in_len) at key_offsets[b] + k, so the sort sees no padding; a row longer
-// than its cap loses the rest, a shorter one fills it with sentinels.
+// Sort keys/payloads of the window entries (b, rel), rel in [0, len_b), of a
+// sequence feature: entry rel sits at window position p = out_len - len_b +
+// rel and reads input position seq_src(rel), so an input element that the
+// window repeats gets one entry per position.  One block per kSeqKeys entries
+// of one row, so the row's length is one load.  Dense: entry rel of row b at
+// b * out_len + rel.  Packed (key_offsets): the row's first cap =
+// key_offsets[b + 1] - key_offsets[b] entries (at most out_len) at
+// key_offsets[b] + rel, so the sort sees no padding; a row longer than its
+// cap loses the rest, a shorter one fills it with sentinels.
 constexpr int kSeqKeys = 1024;
 
 __global__ __launch_bounds__(256) void sequence_keys_kernel(SeqArgs a) {
-  const int64_t per_row = (a.in_len + kSeqKeys - 1) / kSeqKeys;
+  const int64_t per_row = (a.out_len + kSeqKeys - 1) / kSeqKeys;
   const int64_t b = (int64_t)blockIdx.x / per_row;
   const int64_t kb = ((int64_t)blockIdx.x - b * per_row) * kSeqKeys;
   const int64_t len = seq_len(a, b);
   const int64_t start = a.out_len - len;
   const bool packed = a.key_offsets != nullptr;
-  int64_t base = b * a.in_len, cap = a.in_len;
+  int64_t base = b * a.out_len, cap = a.out_len;
   if (packed) {
     base = a.key_offsets[b];
     cap = a.key_offsets[b + 1] - base;
-    cap = cap < 0 ? 0 : (cap > a.in_len ? a.in_len : cap);
+    cap = cap < 0 ? 0 : (cap > a.out_len ? a.out_len : cap);
   }
   for (int j = threadIdx.x; j < kSeqKeys; j += 256) {
-    const int64_t k = kb + j;
-    if (k >= cap) break;
-    const int64_t id = a.ids[b * a.in_len + k];
-    const bool valid = k < len && (uint64_t)id < (uint64_t)a.f.num_rows && id != a.f.padding_idx;
-    const int64_t p = a.order == MDL_SEQ_OLDEST_TO_NEWEST ? start + k : start + (len - 1 - k);
-    a.keys[base + k] = valid ? (uint32_t)(a.f.row_base + id) : a.sentinel;
-    a.payload[base + k] = valid ? (uint32_t)(a.f.payload_base + b * a.out_len + p) : 0u;
+    const int64_t rel = kb + j;
+    if (rel >= cap) break;
+    const bool in_window = rel < len;
+    const int64_t id = in_window ? a.ids[b * a.in_len + seq_src(a, len, rel)] : 0;
+    const bool valid = in_window && (uint64_t)id < (uint64_t)a.f.num_rows && id != a.f.padding_idx;
+    a.keys[base + rel] = valid ? (uint32_t)(a.f.row_base + id) : a.sentinel;
+    a.payload[base + rel] = valid ? (uint32_t)(a.f.payload_base + b * a.out_len + start + rel) : 0u;
   }
 }
 
@@ -1251,8 +1267,8 @@ int mdl_sequence_forward(const mdl_feature* feature, const int64_t* ids, const i
     const int rc = for_each_class(1u << v, LaunchSequence{a, blocks, v % kWidths, s});
     if (rc != MDL_OK) return rc;
   }
-  if (sort_keys != nullptr && batch > 0 && in_len > 0) {
-    const int64_t blocks = batch * ((in_len + kSeqKeys - 1) / kSeqKeys);
+  if (sort_keys != nullptr && batch > 0 && out_len > 0) {
+    const int64_t blocks = batch * ((out_len + kSeqKeys - 1) / kSeqKeys);
     if (blocks > 0x7fffffff) return fail(MDL_ERR_UNSUPPORTED, "mdl_sequence_forward: too many positions");
     hipLaunchKernelGGL(sequence_keys_kernel, dim3((unsigned)blocks), dim3(256), 0, s, a);
     MDL_CHECK_LAUNCH("sequence_keys_kernel");

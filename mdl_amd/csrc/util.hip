@@ -102,7 +102,11 @@ __global__ void bag_take_kernel(const int64_t* __restrict__ in_offsets, const ui
     bad = 1;
   }
   int64_t len = hi - lo;
-  if (row_valid != nullptr && row_valid[r] == 0) len = 0;
+  // A null row keeps nothing, except under tail truncation: the reference
+  // rebuilds tail-truncated lists from the raw offsets (src/dataloader.py:
+  // 8583-8604), so a null row with a non-empty span keeps its last elements.
+  const bool tail_cut = truncation == MDL_TRUNCATE_TAIL && max_length >= 0;
+  if (row_valid != nullptr && row_valid[r] == 0 && !tail_cut) len = 0;
   const int64_t take = max_length >= 0 && len > max_length ? max_length : len;
   lengths[r] = take;
   starts[r] = truncation == MDL_TRUNCATE_HEAD ? lo : hi - take;

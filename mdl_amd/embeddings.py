@@ -201,8 +201,11 @@ def plan_embedding_shards(
 ) -> EmbeddingShardingPlan:
     """Deterministic placement: row-wise cyclic tables, then LPT for small ones.
 
-    Same plan and fingerprint as src/embeddings.py:275-353, so checkpoints
-    keyed by the fingerprint stay loadable.
+    Same steps as src/embeddings.py:275-353, because what they produce is
+    interface: the model reads ``plan.tables[name]`` to give each module its
+    shard spec (src/model.py:2856-2859), checkpoints persist
+    ``asdict(shard_spec)`` (src/checkpoint.py:447-464), and ``fingerprint``
+    is a public field of the returned plan that only the same steps give.
     """
 
     if world_size <= 0:

@@ -141,7 +141,8 @@ def _bag_truncate_cpu(values, offsets, valid, row_valid, max_length, truncation,
     hi = torch.maximum(hi_raw.clamp(max=n_in), lo)
     bad = int(((lo_raw < 0) | (lo_raw > n_in) | (hi_raw < lo) | (hi_raw > n_in)).sum())
     length = hi - lo
-    if row_valid is not None:
+    if row_valid is not None and not (truncation == "tail" and max_length >= 0):
+        # tail truncation reads every row's raw offsets (src/dataloader.py:8583-8604)
         length = torch.where(row_valid != 0, length, 0)
     take = length if max_length < 0 else length.clamp(max=max_length)
     starts = lo if truncation == "head" else hi - take
@@ -416,9 +417,12 @@ def _per_id_grads_cpu(w: Tensor, x: Tensor, ln: Optional[Tensor], g: Tensor, poo
     counts = torch.zeros(batch, dtype=torch.float32)
     if seg.numel():
         counts.index_add_(0, seg, live.float())
-    scale = live.float() / (counts.clamp(min=1)[seg] if pooling == 2 else 1.0)
+    per_id = g[seg]
+    if pooling == 2:
+        # the autograd of sums / counts.clamp(min=1) (src/model.py:570): a division
+        per_id = per_id / counts.clamp(min=1)[seg].unsqueeze(-1)
     keep = live & flat.ne(padding_idx)
-    return flat[keep], (g[seg] * scale.unsqueeze(-1))[keep]
+    return flat[keep], per_id[keep]
 
 
 def _coalesce_padded_cpu(rows: Tensor, vals: Tensor, cap: int, dtype: torch.dtype, dim: int):
@@ -539,15 +543,21 @@ def sequence_lookup(weight: Tensor, ids: Tensor, lengths: Tensor, out_len: int, 
 
 
 def _window_cpu(ids: Tensor, lengths: Tensor, out_len: int, newest_first: bool):
-    """(mask [B, out_len], source position [B, out_len]) of the window."""
+    """(mask [B, out_len], source position [B, out_len]) of the window: the
+    reference's clamp of the lengths to the output width and of the source
+    position to the input width (src/model.py:2998-3016), so a length past
+    the input repeats its last element; an empty input masks everything."""
 
     batch, in_len = ids.shape
-    n = lengths.to(torch.int64).clamp(min=0).clamp(max=min(out_len, in_len))
+    n = lengths.to(torch.int64).clamp(min=0).clamp(max=out_len)
+    if in_len == 0:
+        n = torch.zeros_like(n)
     start = out_len - n
     p = torch.arange(out_len).unsqueeze(0)
     mask = p >= start.unsqueeze(1)
     rel = p - start.unsqueeze(1)
     src = (n.unsqueeze(1) - 1 - rel) if newest_first else rel
+    src = src.clamp(max=max(in_len - 1, 0))
     return mask, torch.where(mask, src, 0)
 
 
@@ -567,7 +577,7 @@ def _sequence_lookup_cpu(weight, ids, lengths, out_len, newest_first, padding_id
 @sequence_lookup.register_fake
 def _sequence_lookup_fake(weight, ids, lengths, out_len, newest_first, padding_idx, need_backward):
     batch = ids.size(0)
-    nk = max(int(ids.numel()), 1) if (need_backward and _is_rocm(weight)) else 0
+    nk = max(int(batch * out_len), 1) if (need_backward and _is_rocm(weight)) else 0
     return (weight.new_empty((batch, out_len, weight.size(1))), ids.new_empty((batch, out_len), dtype=torch.bool),
             ids.new_empty(nk, dtype=torch.int32), ids.new_empty(nk, dtype=torch.int32),
             ids.new_empty(1, dtype=torch.int32))
@@ -578,19 +588,21 @@ def sequence_lookup_backward(weight: Tensor, ids: Tensor, lengths: Tensor, out_l
                              padding_idx: int, grad: Tensor, keys: Tensor, payload: Tensor
                              ) -> tuple[Tensor, Tensor, Tensor]:
     """Capacity-sized coalesced gradient of the window gather (capacity: the
-    input positions, ``ids.numel()``) and its device row count (int64 [1]).
-    The sort works on copies of the keys and payloads."""
+    window positions, ``batch * out_len``) and its device row count (int64
+    [1]).  The sort works on copies of the keys and payloads."""
 
+    n = int(ids.size(0)) * int(out_len)
+    if keys.numel() < n or payload.numel() < n:
+        raise ValueError("sequence sort keys hold one entry per window position (batch * out_len)")
     keys = keys.clone()
     payload = payload.clone()
     plan = ops.GroupPlan()
     plan.add_feature(weight, pooling="none", padding_idx=padding_idx)
-    n = int(ids.numel())
     feats = ops.sequence_feature(weight, padding_idx=padding_idx)
     feats["num_ids"] = n
     res = ops.ForwardResult(
         plan=plan, device=weight.device, ids=ids, offsets=None, outputs=[grad], feats=feats, keys=keys,
-        payload=payload, bag_count=None, error_count=torch.empty(0),
+        payload=payload, bag_count=None, error_count=torch.empty(0), count=n,
     )
     rows_all, vbuf, counts, layout = ops.backward_coalesce_padded(res, [grad.reshape(-1, int(weight.size(1)))])
     rows, values = ops.split_coalesced([weight], rows_all, vbuf, layout)
@@ -604,14 +616,14 @@ def _sequence_backward_cpu(weight, ids, lengths, out_len, newest_first, padding_
     rows = torch.gather(ids, 1, src) if ids.size(1) else torch.zeros_like(src)
     keep = mask & (rows >= 0) & (rows < weight.size(0)) & rows.ne(padding_idx)
     dim = int(weight.size(1))
-    r, v, u = _coalesce_padded_cpu(rows[keep], grad.float()[keep].reshape(-1, dim), int(ids.numel()), weight.dtype,
-                                   dim)
+    r, v, u = _coalesce_padded_cpu(rows[keep], grad.float()[keep].reshape(-1, dim), int(ids.size(0)) * int(out_len),
+                                   weight.dtype, dim)
     return r, v, torch.tensor([u], dtype=torch.int64)
 
 
 @sequence_lookup_backward.register_fake
 def _sequence_backward_fake(weight, ids, lengths, out_len, newest_first, padding_idx, grad, keys, payload):
-    n = int(ids.numel())
+    n = int(ids.size(0)) * int(out_len)
     return (weight.new_empty(n, dtype=torch.int64), weight.new_empty((n, weight.size(1))),
             weight.new_empty(1, dtype=torch.int64))
 

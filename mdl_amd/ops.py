@@ -169,7 +169,9 @@ def bag_truncate(
     out_offsets [rows+1])``.
 
     Row r of the list array holds ``values[offsets[r]:offsets[r+1]]``
-    (Arrow list layout); a null row (``row_valid == 0``) keeps nothing, a null
+    (Arrow list layout); a null row (``row_valid == 0``) keeps nothing (under
+    tail truncation it keeps the last elements of its offsets span, as the
+    reference's rebuild from raw offsets does, src/dataloader.py:8583-8604), a null
     element (``valid == 0``) keeps its slot and becomes id 0.  ``max_length``
     keeps a row's first (``head``) or last (``tail``) elements
     (src/dataloader.py:8565-8604); the kept elements are bucketed
@@ -1606,7 +1608,10 @@ def sequence_lookup(
     plan = GroupPlan()
     plan.add_feature(weight, pooling="none", padding_idx=padding_idx)
     device = ids.device
-    n = int(ids.numel())
+    if ids.ndim != 2:
+        raise ValueError("sequence ids must be [batch, length]")
+    # one sort entry per window position
+    n = int(ids.size(0)) * int(ids.size(1) if out_len is None else out_len)
     keys = payload = None
     if with_backward:
         keys = torch.empty(max(n, 1), dtype=torch.int32, device=device)
@@ -1620,5 +1625,5 @@ def sequence_lookup(
     feats = sequence_feature(weight, padding_idx=padding_idx)
     return ForwardResult(
         plan=plan, device=device, ids=ids, offsets=None, outputs=[out], feats=feats, keys=keys,
-        payload=payload, bag_count=None, error_count=error_count, keep=[mask],
+        payload=payload, bag_count=None, error_count=error_count, keep=[mask], count=n,
     )

@@ -508,7 +508,9 @@ class SequenceStep:
             error_count if error_count is not None else torch.zeros(1, dtype=torch.int32, device=self.device)
         )
         self.batch = [int(t.size(0)) for t in self.ids]
-        self.caps = [min(int(i.size(1)), int(o.size(1))) for i, o in zip(self.ids, self.outputs)]
+        # Sort entries a row can hold: its window entries, at most the
+        # window's width (none for an empty input).
+        self.caps = [int(o.size(1)) if int(i.size(1)) > 0 else 0 for i, o in zip(self.ids, self.outputs)]
         for m in range(1, self.k):
             if [tuple(o.shape) for o in self.all_outputs[m]] != [tuple(o.shape) for o in self.outputs]:
                 raise ValueError("every micro-batch's windows need the shapes of the first's")

@@ -148,11 +148,14 @@ def bag_truncate(offsets: np.ndarray, values: np.ndarray, valid: np.ndarray | No
     the reference's truncation of Arrow lists (src/dataloader.py:8565-8604,
     head = ``list_slice(0, max_length)``, tail = the last ``max_length``
     elements by rebuilt offsets) then ``list_value_length`` with nulls as 0
-    and ``list_flatten`` (:8634-8640).  Offsets are assumed well formed."""
+    and ``list_flatten`` (:8634-8640).  The tail rebuild reads the raw
+    offsets of every row and makes a list array without a validity bitmap,
+    so a null row keeps the last elements of its span there.  Offsets are
+    assumed well formed."""
 
     offsets = np.asarray(offsets, dtype=np.int64)
     lengths = offsets[1:] - offsets[:-1]
-    if row_valid is not None:
+    if row_valid is not None and not (truncation == "tail" and max_length is not None):
         lengths = np.where(np.asarray(row_valid) != 0, lengths, 0)
     take = lengths if max_length is None else np.minimum(lengths, int(max_length))
     starts = offsets[:-1] if truncation == "head" else offsets[1:] - take
@@ -250,39 +253,61 @@ def pool_rows_backward(indices: np.ndarray, lengths: np.ndarray, grad: np.ndarra
 
 def sequence_gather(weight: np.ndarray, ids: np.ndarray, lengths: np.ndarray, out_len: int,
                     order: str = "oldest_to_newest"):
-    """Right-aligned padded gather + mask (src/model.py:2989-3100), brute force."""
+    """Right-aligned padded gather + mask, brute force, in the reference's
+    two steps: ``_right_aligned_sequence`` (src/model.py:2989-3020: lengths
+    clamped to [0, out_len], source position p - shift clamped to
+    [0, in_len - 1], positions before the shift masked; an empty input gives
+    an all-False mask), then for newest_to_oldest the reversal of the valid
+    stretch in ``_align_sequence_inputs`` (:3074-3100, source position
+    clamped to [0, out_len - 1])."""
 
     w = np.asarray(weight, dtype=np.float64)
     ids = np.asarray(ids, dtype=np.int64)
     B, in_len = ids.shape
     out = np.zeros((B, out_len, w.shape[1]), dtype=np.float64)
     mask = np.zeros((B, out_len), dtype=bool)
+    if out_len == 0 or in_len == 0:
+        return out, mask
+    aligned = np.zeros_like(out)
     for b in range(B):
-        n = int(min(max(int(lengths[b]), 0), out_len, in_len))
+        n = min(max(int(lengths[b]), 0), out_len)
+        shift = out_len - n
+        for p in range(out_len):
+            src = min(max(p - shift, 0), in_len - 1)
+            mask[b, p] = p >= shift
+            aligned[b, p] = w[ids[b, src]] if mask[b, p] else 0.0
+    if order == "oldest_to_newest":
+        return aligned, mask
+    for b in range(B):
+        n = min(max(int(lengths[b]), 0), out_len)
         start = out_len - n
-        for p in range(start, out_len):
-            k = p - start if order == "oldest_to_newest" else n - 1 - (p - start)
-            out[b, p] = w[ids[b, k]]
-            mask[b, p] = True
+        for p in range(out_len):
+            src = min(max(out_len - 1 - (p - start), 0), out_len - 1)
+            out[b, p] = aligned[b, src] if mask[b, p] else 0.0
     return out, mask
 
 
 def sequence_positions(ids: np.ndarray, lengths: np.ndarray, out_len: int, order: str = "oldest_to_newest"):
     """Window layout of the right-aligned gather (src/model.py:2989-3100),
     vectorised: ``(mask [B, out_len], src [B, out_len])`` where ``src[b, p]``
-    is the input position k whose id lands on window position p (valid where
-    mask is set: p >= out_len - n_b with n_b = min(max(len_b, 0), out_len,
-    in_len); k = p - start oldest first, n_b - 1 - (p - start) newest first).
+    is the input position whose id lands on window position p (valid where
+    mask is set: p >= out_len - n_b with n_b = min(max(len_b, 0), out_len),
+    and no position when in_len is 0); with rel = p - start, the position is
+    min(rel, in_len - 1) oldest first and min(n_b - 1 - rel, in_len - 1)
+    newest first, so a length past the input repeats the last element.
     Pinned against the per-position loop of ``sequence_gather``."""
 
     ids = np.asarray(ids, dtype=np.int64)
     B, in_len = ids.shape
-    n = np.minimum(np.minimum(np.maximum(np.asarray(lengths, dtype=np.int64), 0), out_len), in_len)
+    n = np.minimum(np.maximum(np.asarray(lengths, dtype=np.int64), 0), out_len)
+    if in_len == 0:
+        n = np.zeros_like(n)
     start = out_len - n
     p = np.arange(out_len, dtype=np.int64)[None, :]
     mask = p >= start[:, None]
     rel = p - start[:, None]
     src = rel if order == "oldest_to_newest" else n[:, None] - 1 - rel
+    src = np.minimum(src, max(in_len - 1, 0))
     src = np.where(mask, src, 0)
     return mask, src
 

@@ -36,6 +36,44 @@ def _checksum(t: torch.Tensor) -> tuple[int, int]:
     return int(s1.item()), int(s2.item())
 
 
+class ErrorStats:
+    """Observed error against |ref|, per category (e.g. "c1 weights"): the
+    worst relative error |got - ref| / |ref| over elements with ref != 0,
+    how many elements exceed the plain relative tolerance, and the worst
+    ratio of the error to the bound the check applies (<= 1 passes).  The
+    full-size tests print one line per category, so each run records how
+    close the results come to the plain 1e-5 / 1e-2 relative figures, beside
+    the first-order bounds over |terms| that they are checked against."""
+
+    def __init__(self):
+        self.cats: dict[str, dict] = {}
+
+    def add(self, what: str, err, ref, bound, rtol: float):
+        cat = " ".join(what.split()[:1] + [w for w in what.split()[1:] if not w.isdigit()][-1:])
+        c = self.cats.setdefault(cat, {"n": 0, "nonzero": 0, "over_rtol": 0, "worst_rel": 0.0,
+                                       "worst_bound_ratio": 0.0, "rtol": rtol})
+        mag = np.abs(ref)
+        nz = mag > 0
+        rel = np.where(nz, err / np.where(nz, mag, 1.0), 0.0)
+        c["n"] += int(err.size)
+        c["nonzero"] += int(nz.sum())
+        c["over_rtol"] += int((rel > rtol).sum())
+        if err.size:
+            c["worst_rel"] = max(c["worst_rel"], float(rel.max()))
+            c["worst_bound_ratio"] = max(c["worst_bound_ratio"], float((err / bound).max()))
+
+    def report(self, prefix: str = ""):
+        for cat, c in sorted(self.cats.items()):
+            if prefix and not cat.startswith(prefix):
+                continue
+            say("ERR", cat, f"elements {c['n']}", f"worst |err|/|ref| {c['worst_rel']:.3e}",
+                f"over {c['rtol']:g} relative: {c['over_rtol']} of {c['nonzero']}",
+                f"worst err/bound {c['worst_bound_ratio']:.3f}")
+
+
+STATS = ErrorStats()
+
+
 def assert_close(got, ref, rtol, atol, scale=None, what=""):
     got = np.asarray(got, dtype=np.float64)
     ref = np.asarray(ref, dtype=np.float64)
@@ -43,6 +81,7 @@ def assert_close(got, ref, rtol, atol, scale=None, what=""):
     err = np.abs(got - ref)
     mag = np.abs(ref) if scale is None else np.maximum(np.abs(ref), np.asarray(scale, dtype=np.float64))
     bound = atol + rtol * mag
+    STATS.add(what, err, ref, bound, rtol)
     bad = err > bound
     assert not bad.any(), f"{what}: {int(bad.sum())} mismatches, worst excess {float((err - bound).max())}"
 

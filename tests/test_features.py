@@ -87,6 +87,47 @@ def test_oracle_bag_truncate_sliced_arrow_array():
     assert lengths.tolist() == blengths.tolist() and (vals * ok).tolist() == flat.tolist()
 
 
+@pytest.mark.parametrize("truncation", ["head", "tail"])
+def test_null_row_with_a_non_empty_span(truncation):
+    """A null list row whose offsets span elements (Arrow allows it: a mask
+    given to ListArray.from_arrays, or a filter, leaves one).  Head
+    truncation (list_slice, src/dataloader.py:8576-8577) keeps the row null,
+    so its length is 0; the tail rebuild (:8583-8604) reads the raw offsets of
+    every row and builds a list array without a validity bitmap, so the row
+    keeps its last elements.  Expected values come from pyarrow's kernels
+    run through those steps."""
+
+    offsets = pa.array([0, 3, 7, 9], pa.int32())
+    values = pa.array([11, 12, 13, 21, 22, 23, 24, 31, 32], pa.int64())
+    array = pa.ListArray.from_arrays(offsets, values, mask=pa.array([False, True, False]))
+    assert array.null_count == 1 and array.offsets.to_pylist() == [0, 3, 7, 9]
+    max_length = 2
+    if truncation == "head":
+        cut = pc.list_slice(array, 0, max_length)
+    else:
+        off = array.offsets.to_numpy(zero_copy_only=False).astype(np.int64)
+        lengths = off[1:] - off[:-1]
+        take = np.minimum(lengths, max_length)
+        starts = off[:-1] + (lengths - take)
+        idx = np.concatenate([np.arange(a, a + k) for a, k in zip(starts, take)])
+        new_offsets = np.concatenate([[0], np.cumsum(take)])
+        cut = pa.ListArray.from_arrays(pa.array(new_offsets, pa.int32()), pc.take(array.values, pa.array(idx)))
+    exp_lengths = pc.fill_null(pc.list_value_length(cut), 0).to_pylist()
+    exp_values = pc.list_flatten(cut).to_pylist()
+    assert exp_lengths == ([2, 0, 2] if truncation == "head" else [2, 2, 2])
+    offs, raw, valid, row_valid = _arrow_parts(array)
+    vals, ok, lengths = O.bag_truncate(offs, raw, valid, row_valid, max_length, truncation)
+    assert lengths.tolist() == exp_lengths and vals.tolist() == exp_values and ok.all()
+    ids, lens, out_offsets, err = _op_cpu(offs, raw, valid, row_valid, max_length, truncation, "none", 0)
+    assert lens.tolist() == exp_lengths and ids[: len(exp_values)].tolist() == exp_values
+    assert int(err[0]) == 0
+    # without truncation a null row has length 0 (list_value_length, nulls as 0)
+    vals, ok, lengths = O.bag_truncate(offs, raw, valid, row_valid, None, truncation)
+    assert lengths.tolist() == [3, 0, 2]
+    ids, lens, _, _ = _op_cpu(offs, raw, valid, row_valid, None, truncation, "none", 0)
+    assert lens.tolist() == [3, 0, 2]
+
+
 def _op_cpu(offsets, raw, valid, row_valid, max_length, truncation, bucket, nb, validate=True):
     t = lambda a, dt=torch.int64: None if a is None else torch.from_numpy(np.asarray(a)).to(dt)  # noqa: E731
     return torch.ops.mdl_hip.bag_truncate(t(raw), t(offsets), t(valid, torch.uint8), t(row_valid, torch.uint8),

@@ -35,7 +35,7 @@ import torch
 
 import bench
 from oracle import oracle as O
-from parity_helpers import RTOL, _check_update, _free, _random_state, _Snapshot, _touched, assert_close, say
+from parity_helpers import RTOL, STATS, _check_update, _free, _random_state, _Snapshot, _touched, assert_close, say
 
 pytestmark = [pytest.mark.gpu, pytest.mark.timeout(900)]
 
@@ -98,6 +98,7 @@ def test_pooled_config_full_size_matches_oracle(device, name):
         say(name, "updates checked", f"{time.time() - t0:.1f}s")
         snap.restore_and_check(dev.tables, dev.states)
         say(name, "untouched rows checked", f"{time.time() - t0:.1f}s")
+        STATS.report(name)
     finally:
         del dev
         _free()
@@ -141,6 +142,7 @@ def test_sequence_config_full_size_matches_oracle(device):
             say("c2", f"feature {f} checked", f"{time.time() - t0:.1f}s")
         snap.restore_and_check(dev.tables, dev.states)
         say("c2", "untouched rows checked", f"{time.time() - t0:.1f}s")
+        STATS.report("c2")
     finally:
         del dev
         _free()

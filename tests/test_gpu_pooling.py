@@ -49,6 +49,43 @@ def test_padded_bag_pooling_path_still_supported(device):
     torch.testing.assert_close(excluded.cpu(), torch.tensor(g["expected_exclude"]))
 
 
+@pytest.mark.parametrize("policy", ["exclude", "include_as_padding"])
+@pytest.mark.parametrize("dim", [1, 8, 64, 130])
+def test_mean_pool_divides_like_the_reference_bit_for_bit(device, policy, dim):
+    """Mean pooling is ``sums / counts.clamp(min=1)`` (src/model.py:570), a
+    correctly rounded division, forward and backward, not a multiplication
+    by an approximate reciprocal.  Integer-valued rows make every bag sum
+    exact in fp32 whatever the summation order, so the pooled rows must equal
+    torch's fp32 division bit for bit; the per-position gradient of each row
+    must equal torch's ``grad / count`` bit for bit (bag counts 1 to 32, many
+    of them not powers of two, and a few past 255)."""
+
+    announce("pool_division_bits", policy, dim)
+    rng = np.random.default_rng(90 + dim)
+    B = 400
+    lengths = rng.integers(0, 33, size=B)
+    lengths[:4] = [255, 256, 300, 701]  # counts past the kernels' reciprocal table
+    n = int(lengths.sum())
+    ids = rng.integers(1, 1000, size=n)
+    ids[rng.random(n) < 0.2] = 0
+    emb_host = rng.integers(-64, 65, size=(n, dim)).astype(np.float32)
+    emb = torch.from_numpy(emb_host).to(device).requires_grad_(True)
+    t_ids = torch.from_numpy(ids).to(device)
+    t_len = torch.from_numpy(lengths).to(device)
+    out = _mean_pool_categorical_bag(emb, t_ids, t_len, policy)
+    seg = torch.repeat_interleave(torch.arange(B), torch.from_numpy(lengths))
+    w = (torch.from_numpy(ids) != 0).float() if policy == "exclude" else torch.ones(n)
+    sums = torch.zeros(B, dim, dtype=torch.float64).index_add_(0, seg, torch.from_numpy(emb_host).double()
+                                                                * w.double().unsqueeze(-1))
+    counts = torch.zeros(B).index_add_(0, seg, w)
+    ref = sums.float() / counts.clamp(min=1).unsqueeze(-1)  # exact sums, one fp32 division
+    assert torch.equal(out.detach().cpu(), ref)
+    g = torch.from_numpy(rng.standard_normal((B, dim)).astype(np.float32))
+    out.backward(g.to(device))
+    ref_grad = (g / counts.clamp(min=1).unsqueeze(-1))[seg] * w.unsqueeze(-1)
+    assert torch.equal(emb.grad.cpu(), ref_grad)
+
+
 def _bag(rng, B, dim, max_len, dtype, device, null_every=4):
     lengths = rng.integers(0, max_len + 1, size=B)
     n = int(lengths.sum())

@@ -301,6 +301,71 @@ def test_sequence_gather_closed_forms():
     assert out[0, :, 0].tolist() == [0.0, 4.0, 3.0]
 
 
+def test_sequence_gather_length_past_the_input():
+    """A length past the input width (hand-traced through
+    src/model.py:3011-3016 and :3091-3099): input [e0, e1], length 3, width 4
+    gives [0, e0, e1, e1] with mask [F, T, T, T]; newest first the valid
+    stretch reverses to [0, e1, e1, e0].  An empty input masks everything
+    (:3000-3009)."""
+
+    W = np.arange(10, dtype=np.float32)[:, None] * np.ones((1, 2), np.float32)
+    ids = np.array([[5, 7]])
+    out, mask = O.sequence_gather(W, ids, np.array([3]), 4)
+    assert mask.tolist() == [[False, True, True, True]]
+    assert out[0, :, 0].tolist() == [0.0, 5.0, 7.0, 7.0]
+    out, mask = O.sequence_gather(W, ids, np.array([3]), 4, "newest_to_oldest")
+    assert mask.tolist() == [[False, True, True, True]]
+    assert out[0, :, 0].tolist() == [0.0, 7.0, 7.0, 5.0]
+    out, mask = O.sequence_gather(W, np.zeros((2, 0), np.int64), np.array([3, 0]), 4)
+    assert not mask.any() and out.sum() == 0
+    for order in ("oldest_to_newest", "newest_to_oldest"):
+        m, src = O.sequence_positions(ids, np.array([3]), 4, order)
+        ref, rmask = O.sequence_gather(W, ids, np.array([3]), 4, order)
+        assert np.array_equal(m, rmask)
+        assert np.array_equal(np.where(m, W[np.take_along_axis(ids, src, 1)][..., 0], 0), ref[..., 0])
+
+
+def _reference_window_torch(emb: torch.Tensor, lengths: torch.Tensor, out_len: int, order: str):
+    """The reference's window steps written with torch ops, for pinning: the
+    gather/clamp/mask of src/model.py:2998-3020, then the reversal of
+    :3091-3099 for newest_to_oldest."""
+
+    B, L, D = emb.shape
+    if L == 0:
+        return emb.new_zeros(B, out_len, D), torch.zeros(B, out_len, dtype=torch.bool)
+    n = lengths.clamp(min=0, max=out_len)
+    pos = torch.arange(out_len).view(1, -1)
+    shifts = (out_len - n).view(-1, 1)
+    src = (pos - shifts).clamp(min=0, max=L - 1)
+    mask = pos >= shifts
+    aligned = emb.gather(1, src.unsqueeze(-1).expand(-1, -1, D)) * mask.unsqueeze(-1).to(emb.dtype)
+    if order == "oldest_to_newest":
+        return aligned, mask
+    starts = (out_len - n).view(-1, 1)
+    src2 = (out_len - 1 - (pos - starts)).clamp(min=0, max=out_len - 1)
+    rev = aligned.gather(1, src2.unsqueeze(-1).expand(-1, -1, D))
+    return rev * mask.unsqueeze(-1).to(rev.dtype), mask
+
+
+@pytest.mark.parametrize("order", ["oldest_to_newest", "newest_to_oldest"])
+def test_sequence_gather_matches_reference_steps_in_torch(order):
+    """The oracle's window against the reference's torch steps (restated in
+    the test with library gathers), over lengths past the input and the
+    window, zero and negative lengths."""
+
+    rng = np.random.default_rng(23)
+    W = rng.standard_normal((40, 3))
+    B, L_in = 10, 6
+    ids = rng.integers(0, 40, size=(B, L_in))
+    lengths = np.array([0, 1, 3, 6, 8, -2, 5, 12, 2, 7])
+    emb = torch.from_numpy(W)[torch.from_numpy(ids)]
+    for out_len in (1, 4, 6, 9):
+        ref, rmask = _reference_window_torch(emb, torch.from_numpy(lengths), out_len, order)
+        out, mask = O.sequence_gather(W, ids, lengths, out_len, order)
+        assert np.array_equal(mask, rmask.numpy())
+        assert np.array_equal(out, ref.numpy())
+
+
 @pytest.mark.parametrize("order", ["oldest_to_newest", "newest_to_oldest"])
 def test_sequence_window_equals_per_position_gather(order):
     """The vectorised window (used at full config sizes) against the
@@ -327,21 +392,21 @@ def test_sequence_grads_match_embedding_autograd(order):
     (library routine, CPU)."""
 
     rng = np.random.default_rng(22)
-    rows, dim, B, L_in, out_len = 30, 4, 6, 8, 6
+    rows, dim, B, L_in = 30, 4, 6, 8
     ids = rng.integers(0, rows, size=(B, L_in))
     ids[:, 1] = 0  # padding inside sequences
     lengths = np.array([0, 2, 8, 5, 11, 1])
-    grad = rng.standard_normal((B, out_len, dim))
-    r, v = O.sequence_grads(ids, lengths, grad, out_len, order)
-    dense = np.zeros((rows, dim))
-    np.add.at(dense, r, v)
-    W = torch.zeros((rows, dim), dtype=torch.float64, requires_grad=True)
-    emb = torch.nn.functional.embedding(torch.from_numpy(ids), W, padding_idx=0)
-    mask, src = O.sequence_positions(ids, lengths, out_len, order)
-    idx = torch.from_numpy(src)[:, :, None].expand(B, out_len, dim)
-    win = torch.gather(emb, 1, idx) * torch.from_numpy(mask)[:, :, None]
-    (win * torch.from_numpy(grad)).sum().backward()
-    np.testing.assert_allclose(dense, W.grad.numpy(), rtol=1e-12, atol=1e-12)
+    # width 10: lengths 11 and 8 < 10 < 11 reach past the input (repeated last element)
+    for out_len in (6, 10):
+        grad = rng.standard_normal((B, out_len, dim))
+        r, v = O.sequence_grads(ids, lengths, grad, out_len, order)
+        dense = np.zeros((rows, dim))
+        np.add.at(dense, r, v)
+        W = torch.zeros((rows, dim), dtype=torch.float64, requires_grad=True)
+        emb = torch.nn.functional.embedding(torch.from_numpy(ids), W, padding_idx=0)
+        win, _ = _reference_window_torch(emb, torch.from_numpy(lengths), out_len, order)
+        (win * torch.from_numpy(grad)).sum().backward()
+        np.testing.assert_allclose(dense, W.grad.numpy(), rtol=1e-12, atol=1e-12)
 
 
 def test_sparse_step_equals_composition():
