@@ -635,16 +635,31 @@ def aux_measurements(torch, dev, wl, n_ids: float, steps: int, device, batches=N
     # reference's modules runs (src/model.py:3782-3890, src/train.py:7060-7188),
     # timed under the sync debug mode that raises on any host synchronisation
     if batches is not None:
-        out["dropin_step"] = dropin_loop(torch, dev, wl, device, steps=min(steps, 10))
+        out["dropin_step"] = dropin_loop(torch, dev, wl, device, steps=min(steps, 10), mode="capacity")
+        out["dropin_step_clipped"] = dropin_loop(torch, dev, wl, device, steps=min(steps, 10), mode="capacity",
+                                                 clip_norm=1.0)
+        out["dropin_step_coalesced"] = dropin_loop(torch, dev, wl, device, steps=min(steps, 10), mode="coalesced")
     return out
 
 
-def dropin_loop(torch, dev, wl, device, steps: int = 10) -> dict:
+def dropin_loop(torch, dev, wl, device, steps: int = 10, mode: str = "capacity",
+                clip_norm: float | None = None) -> dict:
+    """The modules' training loop over the bench's tables, in one of the
+    sparse-gradient modes: "capacity" (no host read; timed under the sync
+    debug mode that raises on any), "coalesced" (exact coalesced gradients,
+    one batched read of the row counts per backward).  ``clip_norm`` adds the
+    trainer's sparse clip through ``mdl_amd.clip`` between backward and step."""
+
     from torch import nn
 
+    import mdl_amd.library as L
+    from mdl_amd.clip import _clip_sparse_grad_norm
     from mdl_amd.embeddings import (EmbeddingShardSpec, ShardedEmbedding, grouped_sharded_embedding_lookup,
                                     pooled_embedding_lookup)
     from mdl_amd.optim import ShardedRowWiseAdagrad
+
+    prev_mode = L.sparse_grad_mode()
+    L.set_sparse_grad_mode(mode)
 
     mods = []
     for t, w in enumerate(dev.tables):
@@ -683,39 +698,51 @@ def dropin_loop(torch, dev, wl, device, steps: int = 10) -> dict:
     # The model concatenates the per-feature embeddings into its token slots
     # (src/model.py:4395-4420), so one [B, sum(D)] gradient comes back and
     # each feature's share arrives as a column slice of it.
+    weights = [m.weight for m in mods]
+
     def one(i):
         req_pool, req_single, g_tokens = feats[i % len(feats)]
         opt.zero_grad(set_to_none=True)
         outs = pooled_embedding_lookup(req_pool) + grouped_sharded_embedding_lookup(req_single)
         torch.cat(outs, dim=1).backward(g_tokens)
+        if clip_norm is not None:
+            _clip_sparse_grad_norm([], weights, clip_norm)
         opt.step()
 
-    for i in range(2):
-        one(i)
-    torch.cuda.synchronize()
-    clean = True
-    torch.cuda.set_sync_debug_mode("error")
     try:
-        t0 = time.perf_counter()
-        for i in range(steps):
-            one(i)
-        torch.cuda.set_sync_debug_mode("default")
-        torch.cuda.synchronize()
-        ms = (time.perf_counter() - t0) * 1e3 / steps
-    except RuntimeError:
-        clean = False
-        torch.cuda.set_sync_debug_mode("default")
-        torch.cuda.synchronize()
-        t0 = time.perf_counter()
-        for i in range(steps):
+        for i in range(2):
             one(i)
         torch.cuda.synchronize()
-        ms = (time.perf_counter() - t0) * 1e3 / steps
-    return {"ms_per_step": ms, "steps": steps, "no_host_sync": clean,
+        clean = mode == "capacity"
+        if clean:
+            torch.cuda.set_sync_debug_mode("error")
+        try:
+            t0 = time.perf_counter()
+            for i in range(steps):
+                one(i)
+            torch.cuda.set_sync_debug_mode("default")
+            torch.cuda.synchronize()
+            ms = (time.perf_counter() - t0) * 1e3 / steps
+        except RuntimeError:
+            clean = False
+            torch.cuda.set_sync_debug_mode("default")
+            torch.cuda.synchronize()
+            t0 = time.perf_counter()
+            for i in range(steps):
+                one(i)
+            torch.cuda.synchronize()
+            ms = (time.perf_counter() - t0) * 1e3 / steps
+    finally:
+        L.set_sparse_grad_mode(prev_mode)
+    grads_what = ("capacity-sized coalesced sparse grads (no host read)" if mode == "capacity" else
+                  "exact coalesced sparse grads (is_coalesced, one batched read of the row counts per backward)")
+    return {"ms_per_step": ms, "steps": steps, "mode": mode, "clip_norm": clip_norm, "no_host_sync": clean,
             "what": "ShardedEmbedding modules (pooled_embedding_lookup + grouped_sharded_embedding_lookup), "
                     "their outputs concatenated into [B, sum(D)] token slots, backward of one [B, sum(D)] "
-                    "gradient -> capacity-sized coalesced sparse grads, ShardedRowWiseAdagrad.step() "
-                    "(one grouped launch); timed steps under torch.cuda.set_sync_debug_mode('error')"}
+                    f"gradient -> {grads_what}, "
+                    + ("mdl_amd.clip._clip_sparse_grad_norm, " if clip_norm is not None else "")
+                    + "ShardedRowWiseAdagrad.step() (one call, one grouped launch)"
+                    + ("; timed steps under torch.cuda.set_sync_debug_mode('error')" if mode == "capacity" else "")}
 
 
 # ------------------------------------------------------------ cpu baseline --

@@ -1,17 +1,21 @@
-"""The sparse path as torch.library custom ops, namespace ``mdl_hip``.
+"""The sparse path as torch.library operators, namespace ``mdl_hip``.
 
-Each op has one schema and three implementations:
+The schemas and their ROCm kernels live in the C++ extension
+``libmdl_torch.so`` (mdl_amd/csrc/torch_ops.cpp), which calls the
+hand-written gfx950 kernels of libmdl_hip.so through its C ABI on the current
+HIP stream; importing this module loads it and raises when it is missing.
+This module registers on those schemas:
 
-* ROCm devices: the hand-written gfx950 kernels of libmdl_hip.so, through
-  its C ABI (``mdl_amd.ops``);
-* CPU: PyTorch CPU operations with the reference's CPU semantics, so
+* CPU kernels: PyTorch CPU operations with the reference's CPU semantics, so
   modules whose parameters live on the CPU work as in the reference
   (src/embeddings.py:468-473, src/model.py:509-678, src/optim.py:359-376);
-* fake tensors: shapes only, for tracing and ``torch.compile``.
+* fake kernels: shapes only, for tracing and ``torch.compile``;
+* the autograd formulas of the two lookups.
 
-Ops:
+Public ops:
 
 ``mdl_hip::bucketize``                 pre_hashed / mod bucketing (src/features.py:360-376, src/benchmark.py:1246-1250)
+``mdl_hip::bag_truncate``              list features to CSR bags (src/dataloader.py:8565-8665)
 ``mdl_hip::lengths_to_offsets``        CSR offsets of bag lengths
 ``mdl_hip::grouped_lookup``            grouped lookup + sum/mean bag pooling (src/embeddings.py:1646-1709, src/model.py:509-678)
 ``mdl_hip::grouped_lookup_backward``   its coalesced sparse weight gradients, capacity-sized (no host read)
@@ -22,47 +26,112 @@ Ops:
 ``mdl_hip::rowwise_adagrad_``          row-wise Adagrad of one table (src/optim.py:68-108, CPU :359-376)
 ``mdl_hip::grouped_rowwise_adagrad_``  row-wise Adagrad of many tables in one launch, row counts read on device
 
-Capacity-sized gradients: table t's gradient has ``cap_t`` entries (its id
-count, a bound on its distinct rows that the host knows from the shapes);
-the first ``counts[t]`` are the coalesced rows (ascending, unique) and the
-rest repeat the last row with zero values.  The pair is a valid uncoalesced
-COO gradient with the coalesced sum, and its size needs no device-to-host
-read; ``grouped_rowwise_adagrad_`` reads ``counts`` on the device.
+The C++ extension also defines the whole-step helpers the modules call
+(``grouped_lookup_weight_grads``, ``rowwise_adagrad_step_``, ...) and the
+fused step's launches (``packed_forward_``, ``fused_backward_rowwise_adagrad_``,
+...).
+
+Sparse gradients of the lookups come in one of two modes
+(:func:`set_sparse_grad_mode`):
+
+* ``"coalesced"`` (default): each table's gradient is coalesced -- rows
+  ascending and unique, ``is_coalesced()`` true -- so the trainer's
+  ``grad.coalesce()`` (src/train.py:5738, src/optim.py:323-324) returns it as
+  it is.  Sizing them costs one batched device-to-host read of every table's
+  row count per backward.
+* ``"capacity"``: table t's gradient has ``cap_t`` entries (its id count, a
+  bound on its distinct rows that the host knows from the shapes); the first
+  U_t are the coalesced rows and the rest repeat the last row with zero
+  values.  The pair is a valid uncoalesced COO gradient with the coalesced
+  sum and needs no host read; ``ShardedRowWiseAdagrad`` and ``mdl_amd.clip``
+  read U_t on the device.  A trainer that keeps the reference's
+  ``grad.coalesce()`` would coalesce such gradients again through ATen.
 """
 
 from __future__ import annotations
 
-import weakref
-from collections import OrderedDict
+import os
+from pathlib import Path
 from typing import Optional
 
-import numpy as np
 import torch
 from torch import Tensor
 
 from . import _lib, ops
 
+TORCH_LIB_PATH = Path(__file__).resolve().parent / "libmdl_torch.so"
+
 _POOL = {0: "none", 1: "sum", 2: "mean"}
 _CUDA = "cuda"
+
+
+def _load() -> None:
+    _lib.lib()  # the C ABI and its version check
+    if not TORCH_LIB_PATH.exists():
+        raise RuntimeError(
+            f"{TORCH_LIB_PATH.name} not found at {TORCH_LIB_PATH}; build it with `python -m mdl_amd.build` "
+            "(the torch.library extension of the mdl_hip operators)"
+        )
+    torch.ops.load_library(str(TORCH_LIB_PATH))
+
+
+_load()
+
+_GRAD_MODES = ("coalesced", "capacity")
+_grad_mode = os.environ.get("MDL_SPARSE_GRADS", "coalesced")
+if _grad_mode not in _GRAD_MODES:
+    raise ValueError(f"MDL_SPARSE_GRADS must be one of {_GRAD_MODES}, got {_grad_mode!r}")
+
+
+def set_sparse_grad_mode(mode: str) -> None:
+    """``"coalesced"`` (exact coalesced sparse gradients, one device-to-host
+    read per backward) or ``"capacity"`` (capacity-sized gradients, no host
+    read); see the module docstring."""
+
+    global _grad_mode
+    if mode not in _GRAD_MODES:
+        raise ValueError(f"sparse gradient mode must be one of {_GRAD_MODES}")
+    _grad_mode = mode
+
+
+def sparse_grad_mode() -> str:
+    return _grad_mode
 
 
 def _is_rocm(t: Tensor) -> bool:
     return t.device.type == _CUDA
 
 
+def _eager(t: Tensor) -> bool:
+    """A plain tensor with data, not a fake or functional one being traced."""
+
+    return type(t) is Tensor or type(t) is torch.nn.Parameter
+
+
+def _cpu_kernel(name: str):
+    """Register the decorated function as the CPU kernel of mdl_hip::name."""
+
+    def deco(fn):
+        torch.library.register_kernel(f"mdl_hip::{name}", "cpu", fn)
+        return fn
+
+    return deco
+
+
+def _fake_kernel(name: str):
+    """Register the decorated function as the fake kernel of mdl_hip::name."""
+
+    def deco(fn):
+        torch.library.register_fake(f"mdl_hip::{name}", fn)
+        return fn
+
+    return deco
+
+
 # ------------------------------------------------------------- bucketing --
 
 
-@torch.library.custom_op("mdl_hip::bucketize", mutates_args=(), device_types=_CUDA)
-def bucketize(raw: Tensor, valid: Optional[Tensor], num_buckets: int, mode: str,
-              validate_nonzero: bool) -> tuple[Tensor, Tensor]:
-    err = torch.zeros(1, dtype=torch.int32, device=raw.device)
-    out = ops.bucketize(raw, num_buckets, mode=mode, valid=valid, validate_nonzero=validate_nonzero,
-                        error_count=err)
-    return out, err
-
-
-@bucketize.register_kernel("cpu")
+@_cpu_kernel("bucketize")
 def _bucketize_cpu(raw, valid, num_buckets, mode, validate_nonzero):
     if raw.dtype != torch.int64:
         raise TypeError("raw ids must be torch.int64")
@@ -89,7 +158,7 @@ def _bucketize_cpu(raw, valid, num_buckets, mode, validate_nonzero):
     return out, torch.tensor([count], dtype=torch.int32)
 
 
-@bucketize.register_fake
+@_fake_kernel("bucketize")
 def _bucketize_fake(raw, valid, num_buckets, mode, validate_nonzero):
     return torch.empty_like(raw), raw.new_empty(1, dtype=torch.int32)
 
@@ -105,25 +174,7 @@ def _bucket_values_cpu(raw: Tensor, present: Tensor, num_buckets: int, mode: str
     return out, int(err[0])
 
 
-@torch.library.custom_op("mdl_hip::bag_truncate", mutates_args=(), device_types=_CUDA)
-def bag_truncate(values: Tensor, offsets: Tensor, valid: Optional[Tensor], row_valid: Optional[Tensor],
-                 max_length: int, truncation: str, bucket: str, num_buckets: int,
-                 validate_nonzero: bool) -> tuple[Tensor, Tensor, Tensor, Tensor]:
-    """List feature -> CSR bag: ``(ids [n_in], lengths [rows], offsets
-    [rows+1], error count [1])``; ids past the kept total (``offsets[-1]``)
-    are 0.  ``max_length < 0``: no truncation.  The error count adds rows
-    whose offsets fall outside the values (clamped) and non-null zeros under
-    a validated pre_hashed rule."""
-
-    err = torch.zeros(1, dtype=torch.int32, device=values.device)
-    ids, lengths, out_offsets = ops.bag_truncate(
-        values, offsets, valid=valid, row_valid=row_valid, max_length=None if max_length < 0 else max_length,
-        truncation=truncation, bucket=bucket, num_buckets=num_buckets, validate_nonzero=validate_nonzero,
-        error_count=err)
-    return ids, lengths, out_offsets, err
-
-
-@bag_truncate.register_kernel("cpu")
+@_cpu_kernel("bag_truncate")
 def _bag_truncate_cpu(values, offsets, valid, row_valid, max_length, truncation, bucket, num_buckets,
                       validate_nonzero):
     if values.dtype != torch.int64 or offsets.dtype != torch.int64:
@@ -159,7 +210,7 @@ def _bag_truncate_cpu(values, offsets, valid, row_valid, max_length, truncation,
     return ids, take.clone(), out_offsets, torch.tensor([bad + zeros], dtype=torch.int32)
 
 
-@bag_truncate.register_fake
+@_fake_kernel("bag_truncate")
 def _bag_truncate_fake(values, offsets, valid, row_valid, max_length, truncation, bucket, num_buckets,
                        validate_nonzero):
     rows = offsets.size(0) - 1
@@ -167,19 +218,14 @@ def _bag_truncate_fake(values, offsets, valid, row_valid, max_length, truncation
             offsets.new_empty(rows + 1, dtype=torch.int64), values.new_empty(1, dtype=torch.int32))
 
 
-@torch.library.custom_op("mdl_hip::lengths_to_offsets", mutates_args=(), device_types=_CUDA)
-def lengths_to_offsets(lengths: Tensor) -> Tensor:
-    return ops.lengths_to_offsets(lengths)
-
-
-@lengths_to_offsets.register_kernel("cpu")
+@_cpu_kernel("lengths_to_offsets")
 def _offsets_cpu(lengths):
     out = torch.zeros(lengths.numel() + 1, dtype=torch.int64)
     torch.cumsum(lengths.to(torch.int64), 0, out=out[1:])
     return out
 
 
-@lengths_to_offsets.register_fake
+@_fake_kernel("lengths_to_offsets")
 def _offsets_fake(lengths):
     return lengths.new_empty(lengths.numel() + 1, dtype=torch.int64)
 
@@ -213,84 +259,13 @@ def _check_features(weights, ids, lengths, table, pooling, exclude, padding_idx)
 
 
 def _order(weights, table) -> Optional[list[int]]:
-    """Feature order of a device call: the callers' order, except that a call
-    over 2^32 - 1 table rows or more looks its features up sorted by table, so
-    that each key group's features are consecutive (its keys one stretch)."""
+    """Feature order of a device call (the C++ extension's rule): the
+    callers' order (None), except that a call over 2^32 - 1 table rows or more
+    looks its features up sorted by table, so that each key group's features
+    are consecutive (its keys one stretch)."""
 
-    if sum(int(w.size(0)) for w in weights) < ops.KEY_SPACE:
-        return None
-    order = sorted(range(len(table)), key=lambda f: table[f])
-    return None if order == list(range(len(table))) else order
-
-
-# Layouts seen by the device ops, most recent last: what a plan of the same
-# weights (addresses, shapes, dtypes) and features derives on the host -- row
-# bases, feature specs and the memo of descriptor columns -- so a training
-# loop builds each layout's host arrays once.  Entries hold addresses and
-# sizes, never tensors: a freed table keeps nothing alive, and a new table
-# at the same address with the same shape and dtype is described the same.
-_LAYOUTS: "OrderedDict[tuple, dict]" = OrderedDict()
-_LAYOUTS_MAX = 16
-
-
-def _plan(weights, table, pooling, exclude, padding_idx) -> ops.GroupPlan:
-    key = (weights[0].device, tuple((w.data_ptr(), w.shape, w.dtype, w.stride(0)) for w in weights),
-           tuple(table), tuple(pooling), tuple(exclude), tuple(padding_idx))
-    entry = _LAYOUTS.get(key)
-    if entry is None:
-        plan = ops.GroupPlan()
-        for w in weights:
-            plan.add_table(w, None, shared=False)
-        for f in range(len(table)):
-            plan.features.append(ops.FeatureSpec(
-                table=int(table[f]), pooling=int(pooling[f]), exclude_null=bool(exclude[f]),
-                padding_idx=int(padding_idx[f]), out_dtype=weights[table[f]].dtype,
-            ))
-        entry = {"bases": [t.row_base for t in plan.tables], "total": plan.total_rows,
-                 "features": plan.features, "memo": {}}
-        _LAYOUTS[key] = entry
-        if len(_LAYOUTS) > _LAYOUTS_MAX:
-            _LAYOUTS.popitem(last=False)
-    else:
-        _LAYOUTS.move_to_end(key)
-        plan = ops.GroupPlan()
-        plan.tables = [ops.TableSpec(weight=w, state=None, row_base=b) for w, b in zip(weights, entry["bases"])]
-        plan.features = entry["features"]
-        plan.total_rows = entry["total"]
-    plan._memo = entry["memo"]
-    return plan
-
-
-@torch.library.custom_op("mdl_hip::grouped_lookup", mutates_args=(), device_types=_CUDA)
-def grouped_lookup(
-    weights: list[Tensor], ids: list[Tensor], lengths: list[Optional[Tensor]], table: list[int],
-    pooling: list[int], exclude: list[int], padding_idx: list[int], need_backward: bool,
-) -> tuple[list[Tensor], Tensor, Tensor, Tensor, Tensor, Tensor]:
-    """Outputs per feature (``[*ids.shape, dim]`` unpooled, ``[B, dim]``
-    pooled) and the backward's bookkeeping: sort keys and payloads (empty
-    without ``need_backward``), bag counts, the offsets scan and the count of
-    ids outside their table."""
-
-    _check_features(weights, ids, lengths, table, pooling, exclude, padding_idx)
-    order = _order(weights, table)
-    if order is not None:
-        ids, lengths, table, pooling, exclude, padding_idx = (
-            [x[f] for f in order] for x in (ids, lengths, table, pooling, exclude, padding_idx))
-    plan = _plan(weights, table, pooling, exclude, padding_idx)
-    res = ops.grouped_forward(plan, ids, lengths, with_backward=need_backward, with_bag_count=True)
-    device = weights[0].device
-    empty_i32 = torch.empty(0, dtype=torch.int32, device=device)
-    keys = res.keys if need_backward else empty_i32
-    payload = res.payload if need_backward else empty_i32.clone()
-    bag_count = res.bag_count if res.bag_count is not None else torch.empty(0, dtype=torch.float32, device=device)
-    offsets = res.offsets if res.offsets is not None else torch.empty(0, dtype=torch.int64, device=device)
-    outputs = list(res.outputs)
-    if order is not None:
-        back = [None] * len(order)
-        for i, f in enumerate(order):
-            back[f] = outputs[i]
-        outputs = back
-    return outputs, keys, payload, bag_count, offsets, res.error_count
+    order = torch.ops.mdl_hip.lookup_order(list(weights), [int(t) for t in table])
+    return list(order) if order else None
 
 
 def _pool_cpu(emb: Tensor, live: Tensor, lengths: Tensor, mean: bool) -> tuple[Tensor, Tensor]:
@@ -309,7 +284,7 @@ def _pool_cpu(emb: Tensor, live: Tensor, lengths: Tensor, mean: bool) -> tuple[T
     return sums, counts
 
 
-@grouped_lookup.register_kernel("cpu")
+@_cpu_kernel("grouped_lookup")
 def _grouped_lookup_cpu(weights, ids, lengths, table, pooling, exclude, padding_idx, need_backward):
     _check_features(weights, ids, lengths, table, pooling, exclude, padding_idx)
     n_ids, rows_out, n_len, pooled_any = _layout(ids, lengths, pooling)
@@ -346,7 +321,7 @@ def _grouped_lookup_cpu(weights, ids, lengths, table, pooling, exclude, padding_
     return outputs, empty, empty.clone(), bag_count, offsets, torch.tensor([bad], dtype=torch.int32)
 
 
-@grouped_lookup.register_fake
+@_fake_kernel("grouped_lookup")
 def _grouped_lookup_fake(weights, ids, lengths, table, pooling, exclude, padding_idx, need_backward):
     n_ids, rows_out, n_len, pooled_any = _layout(ids, lengths, pooling)
     outputs = []
@@ -368,38 +343,6 @@ def _capacities(weights, ids, table) -> list[int]:
     for f, x in enumerate(ids):
         cap[table[f]] += int(x.numel())
     return cap
-
-
-@torch.library.custom_op("mdl_hip::grouped_lookup_backward", mutates_args=(), device_types=_CUDA)
-def grouped_lookup_backward(
-    weights: list[Tensor], ids: list[Tensor], lengths: list[Optional[Tensor]], table: list[int],
-    pooling: list[int], exclude: list[int], padding_idx: list[int], grads: list[Tensor], keys: Tensor,
-    payload: Tensor, bag_count: Tensor, offsets: Tensor,
-) -> tuple[Tensor, Tensor, Tensor]:
-    """Capacity-sized coalesced gradients of every table in two flat buffers
-    -- rows int64 and value bytes, laid out by ``ops.coalesced_layout`` (cut
-    per table with ``ops.split_coalesced``) -- and their device row counts
-    (int64 ``[T]``).  The sort works on copies of the keys and payloads, so the
-    op leaves its inputs as they are."""
-
-    order = _order(weights, table)
-    if order is not None:
-        ids, lengths, table, pooling, exclude, padding_idx, grads = (
-            [x[f] for f in order] for x in (ids, lengths, table, pooling, exclude, padding_idx, grads))
-    plan = _plan(weights, table, pooling, exclude, padding_idx)
-    keys = keys.clone()
-    payload = payload.clone()
-    n_ids = [int(x.numel()) for x in ids]
-    bags = [int(lengths[f].numel()) if pooling[f] != 0 else 0 for f in range(len(ids))]
-    feats = ops.build_features(plan, n_ids, bags, [g.data_ptr() for g in grads],
-                               [int(g.stride(0)) if g.ndim == 2 else int(g.size(-1)) for g in grads])
-    res = ops.ForwardResult(
-        plan=plan, device=weights[0].device, ids=ids[0], offsets=offsets if offsets.numel() else None,
-        outputs=list(grads), feats=feats, keys=keys, payload=payload,
-        bag_count=bag_count if bag_count.numel() else None, error_count=torch.empty(0), count=sum(n_ids),
-    )
-    rows_all, vbuf, counts, _ = ops.backward_coalesce_padded(res, grads)
-    return rows_all, vbuf, counts
 
 
 def _per_id_grads_cpu(w: Tensor, x: Tensor, ln: Optional[Tensor], g: Tensor, pooling: int, exclude: int,
@@ -443,7 +386,7 @@ def _coalesce_padded_cpu(rows: Tensor, vals: Tensor, cap: int, dtype: torch.dtyp
     return out_rows, out_vals, u
 
 
-@grouped_lookup_backward.register_kernel("cpu")
+@_cpu_kernel("grouped_lookup_backward")
 def _grouped_backward_cpu(weights, ids, lengths, table, pooling, exclude, padding_idx, grads, keys, payload,
                           bag_count, offsets):
     cap = _capacities(weights, ids, table)
@@ -468,7 +411,7 @@ def _grouped_backward_cpu(weights, ids, lengths, table, pooling, exclude, paddin
     return rows_all, vbuf, torch.tensor(counts, dtype=torch.int64)
 
 
-@grouped_lookup_backward.register_fake
+@_fake_kernel("grouped_lookup_backward")
 def _grouped_backward_fake(weights, ids, lengths, table, pooling, exclude, padding_idx, grads, keys, payload,
                            bag_count, offsets):
     layout = ops.coalesced_layout(weights, _capacities(weights, ids, table))
@@ -494,52 +437,41 @@ def _lookup_backward(ctx, grad_outputs, *_unused):
     ids = list(saved[ctx.nw: ctx.nw + ctx.nf])
     keys, payload, bag_count, offsets = saved[ctx.nw + ctx.nf:]
     table, pooling, exclude, padding_idx = ctx.spec
-    grads = []
-    for f, g in enumerate(grad_outputs):
-        w = weights[table[f]]
+    grads = list(grad_outputs)
+    for f, g in enumerate(grads):
         if g is None:
+            w = weights[table[f]]
             rows_f = int(ctx.lengths[f].numel()) if pooling[f] != 0 else int(ids[f].numel())
-            g = torch.zeros((rows_f, int(w.size(1))), dtype=w.dtype, device=w.device)
-        # Row-strided gradients (column slices of one [B, sum(D)] gradient, as
-        # a concatenation of the outputs hands back) are read in place.
-        grads.append(g if g.ndim == 2 and g.stride(-1) == 1 else g.contiguous())
-    rows_all, vbuf, counts = torch.ops.mdl_hip.grouped_lookup_backward(
-        weights, ids, ctx.lengths, table, pooling, exclude, padding_idx, grads, keys, payload, bag_count, offsets,
-    )
-    rows, values = ops.split_coalesced(weights, rows_all, vbuf,
-                                       ops.coalesced_layout(weights, _capacities(weights, ids, table)))
-    _drop_dead_records()
-    wgrads = []
-    for t, w in enumerate(weights):
-        g = torch.sparse_coo_tensor(rows[t].unsqueeze(0), values[t], tuple(w.shape), is_coalesced=False)
-        _note_capacity_grad(w, rows[t], values[t], counts[t: t + 1])
-        wgrads.append(g)
+            grads[f] = torch.zeros((rows_f, int(w.size(1))), dtype=w.dtype, device=w.device)
+    # Row-strided gradients (column slices of one [B, sum(D)] gradient, as a
+    # concatenation of the outputs hands back) are read in place.
+    if _eager(keys):
+        # the sparse gradients of every table from one call
+        wgrads = torch.ops.mdl_hip.grouped_lookup_weight_grads(
+            weights, ids, ctx.lengths, table, pooling, exclude, padding_idx, grads, keys, payload, bag_count,
+            offsets, _grad_mode == "coalesced",
+        )
+    else:
+        # traced (fake or functional tensors): the public op and capacity-sized
+        # COO tensors, which need no data
+        rows_all, vbuf, counts = torch.ops.mdl_hip.grouped_lookup_backward(
+            weights, ids, ctx.lengths, table, pooling, exclude, padding_idx, grads, keys, payload, bag_count,
+            offsets,
+        )
+        rows, values = ops.split_coalesced(weights, rows_all, vbuf,
+                                           ops.coalesced_layout(weights, _capacities(weights, ids, table)))
+        wgrads = [torch.sparse_coo_tensor(r.unsqueeze(0), v, tuple(w.shape), is_coalesced=False)
+                  for w, r, v in zip(weights, rows, values)]
     # Same structure as the inputs: a list of tensors gets a list back; a
     # list holding a None (unpooled features' lengths) is one leaf.
     lengths_grad = [None] * ctx.nf if all(ln is not None for ln in ctx.lengths) else None
-    return wgrads, [None] * ctx.nf, lengths_grad, None, None, None, None, None
+    return list(wgrads), [None] * ctx.nf, lengths_grad, None, None, None, None, None
 
 
 torch.library.register_autograd("mdl_hip::grouped_lookup", _lookup_backward, setup_context=_lookup_setup)
 
 
 # ------------------------------------------------------------- sequences --
-
-
-@torch.library.custom_op("mdl_hip::sequence_lookup", mutates_args=(), device_types=_CUDA)
-def sequence_lookup(weight: Tensor, ids: Tensor, lengths: Tensor, out_len: int, newest_first: bool,
-                    padding_idx: int, need_backward: bool) -> tuple[Tensor, Tensor, Tensor, Tensor, Tensor]:
-    """Right-aligned window ``[B, out_len, dim]``, its mask, the backward's
-    sort keys/payloads (empty without ``need_backward``) and the count of ids
-    outside the table."""
-
-    res = ops.sequence_lookup(weight, ids, lengths, out_len=out_len,
-                              order="newest_to_oldest" if newest_first else "oldest_to_newest",
-                              padding_idx=padding_idx, with_backward=need_backward)
-    empty = torch.empty(0, dtype=torch.int32, device=weight.device)
-    keys = res.keys if need_backward else empty
-    payload = res.payload if need_backward else empty.clone()
-    return res.outputs[0], res.keep[0], keys, payload, res.error_count
 
 
 def _window_cpu(ids: Tensor, lengths: Tensor, out_len: int, newest_first: bool):
@@ -561,7 +493,7 @@ def _window_cpu(ids: Tensor, lengths: Tensor, out_len: int, newest_first: bool):
     return mask, torch.where(mask, src, 0)
 
 
-@sequence_lookup.register_kernel("cpu")
+@_cpu_kernel("sequence_lookup")
 def _sequence_lookup_cpu(weight, ids, lengths, out_len, newest_first, padding_idx, need_backward):
     mask, src = _window_cpu(ids, lengths, out_len, newest_first)
     rows = torch.gather(ids, 1, src) if ids.size(1) else torch.zeros_like(src)
@@ -574,7 +506,7 @@ def _sequence_lookup_cpu(weight, ids, lengths, out_len, newest_first, padding_id
     return out, mask, empty, empty.clone(), torch.tensor([bad], dtype=torch.int32)
 
 
-@sequence_lookup.register_fake
+@_fake_kernel("sequence_lookup")
 def _sequence_lookup_fake(weight, ids, lengths, out_len, newest_first, padding_idx, need_backward):
     batch = ids.size(0)
     nk = max(int(batch * out_len), 1) if (need_backward and _is_rocm(weight)) else 0
@@ -583,34 +515,7 @@ def _sequence_lookup_fake(weight, ids, lengths, out_len, newest_first, padding_i
             ids.new_empty(1, dtype=torch.int32))
 
 
-@torch.library.custom_op("mdl_hip::sequence_lookup_backward", mutates_args=(), device_types=_CUDA)
-def sequence_lookup_backward(weight: Tensor, ids: Tensor, lengths: Tensor, out_len: int, newest_first: bool,
-                             padding_idx: int, grad: Tensor, keys: Tensor, payload: Tensor
-                             ) -> tuple[Tensor, Tensor, Tensor]:
-    """Capacity-sized coalesced gradient of the window gather (capacity: the
-    window positions, ``batch * out_len``) and its device row count (int64
-    [1]).  The sort works on copies of the keys and payloads."""
-
-    n = int(ids.size(0)) * int(out_len)
-    if keys.numel() < n or payload.numel() < n:
-        raise ValueError("sequence sort keys hold one entry per window position (batch * out_len)")
-    keys = keys.clone()
-    payload = payload.clone()
-    plan = ops.GroupPlan()
-    plan.add_feature(weight, pooling="none", padding_idx=padding_idx)
-    feats = ops.sequence_feature(weight, padding_idx=padding_idx)
-    feats["num_ids"] = n
-    res = ops.ForwardResult(
-        plan=plan, device=weight.device, ids=ids, offsets=None, outputs=[grad], feats=feats, keys=keys,
-        payload=payload, bag_count=None, error_count=torch.empty(0), count=n,
-    )
-    rows_all, vbuf, counts, layout = ops.backward_coalesce_padded(res, [grad.reshape(-1, int(weight.size(1)))])
-    rows, values = ops.split_coalesced([weight], rows_all, vbuf, layout)
-    # views of two different buffers that are not returned: no output aliases another
-    return rows[0], values[0], counts
-
-
-@sequence_lookup_backward.register_kernel("cpu")
+@_cpu_kernel("sequence_lookup_backward")
 def _sequence_backward_cpu(weight, ids, lengths, out_len, newest_first, padding_idx, grad, keys, payload):
     mask, src = _window_cpu(ids, lengths, out_len, newest_first)
     rows = torch.gather(ids, 1, src) if ids.size(1) else torch.zeros_like(src)
@@ -621,7 +526,7 @@ def _sequence_backward_cpu(weight, ids, lengths, out_len, newest_first, padding_
     return r, v, torch.tensor([u], dtype=torch.int64)
 
 
-@sequence_lookup_backward.register_fake
+@_fake_kernel("sequence_lookup_backward")
 def _sequence_backward_fake(weight, ids, lengths, out_len, newest_first, padding_idx, grad, keys, payload):
     n = int(ids.size(0)) * int(out_len)
     return (weight.new_empty(n, dtype=torch.int64), weight.new_empty((n, weight.size(1))),
@@ -644,8 +549,10 @@ def _sequence_backward(ctx, grad_out, *_unused):
     rows, values, count = torch.ops.mdl_hip.sequence_lookup_backward(
         weight, ids, lengths, out_len, newest_first, padding_idx, grad_out.contiguous(), keys, payload,
     )
-    _note_capacity_grad(weight, rows, values, count)
-    g = torch.sparse_coo_tensor(rows.unsqueeze(0), values, tuple(weight.shape), is_coalesced=False)
+    if _eager(rows):
+        g = torch.ops.mdl_hip.capacity_sparse_grad(weight, rows, values, count, _grad_mode == "coalesced")
+    else:
+        g = torch.sparse_coo_tensor(rows.unsqueeze(0), values, tuple(weight.shape), is_coalesced=False)
     return g, None, None, None, None, None, None
 
 
@@ -655,37 +562,20 @@ torch.library.register_autograd("mdl_hip::sequence_lookup", _sequence_backward, 
 # ----------------------------------------------------------- coalescing --
 
 
-@torch.library.custom_op("mdl_hip::sparse_coalesce", mutates_args=(), device_types=_CUDA)
-def sparse_coalesce(indices: Tensor, values: Tensor, num_rows: int) -> tuple[Tensor, Tensor]:
-    """Rows ascending and unique with their summed values (one host read to
-    size them, like Tensor.coalesce())."""
-
-    return ops.coalesce_rows(indices, values, num_rows)
-
-
-@sparse_coalesce.register_kernel("cpu")
+@_cpu_kernel("sparse_coalesce")
 def _sparse_coalesce_cpu(indices, values, num_rows):
     g = torch.sparse_coo_tensor(indices.reshape(1, -1), values, (num_rows, values.size(1))).coalesce()
     return g.indices()[0].clone(), g.values().clone()
 
 
-@sparse_coalesce.register_fake
+@_fake_kernel("sparse_coalesce")
 def _sparse_coalesce_fake(indices, values, num_rows):
     ctx = torch.library.get_ctx()
     u = ctx.new_dynamic_size()
     return indices.new_empty(u), values.new_empty((u, values.size(1)))
 
 
-@torch.library.custom_op("mdl_hip::sparse_coalesce_padded", mutates_args=(), device_types=_CUDA)
-def sparse_coalesce_padded(indices: Tensor, values: Tensor, num_rows: int) -> tuple[Tensor, Tensor, Tensor]:
-    """Capacity-sized coalesce (no host read): ``(rows [n], values [n, dim],
-    count)``, the first ``count`` rows ascending and unique, the rest
-    repeating the last row with zero values."""
-
-    return ops.coalesce_rows_padded(indices, values, num_rows)
-
-
-@sparse_coalesce_padded.register_kernel("cpu")
+@_cpu_kernel("sparse_coalesce_padded")
 def _sparse_coalesce_padded_cpu(indices, values, num_rows):
     keep = (indices >= 0) & (indices < num_rows)
     dim = int(values.size(1))
@@ -693,7 +583,7 @@ def _sparse_coalesce_padded_cpu(indices, values, num_rows):
     return r, v, torch.tensor([u], dtype=torch.int64)
 
 
-@sparse_coalesce_padded.register_fake
+@_fake_kernel("sparse_coalesce_padded")
 def _sparse_coalesce_padded_fake(indices, values, num_rows):
     n = int(indices.numel())
     return indices.new_empty(n, dtype=torch.int64), values.new_empty((n, values.size(1))), \
@@ -703,13 +593,7 @@ def _sparse_coalesce_padded_fake(indices, values, num_rows):
 # --------------------------------------------------------------- update --
 
 
-@torch.library.custom_op("mdl_hip::rowwise_adagrad_", mutates_args=("weight", "accumulator"), device_types=_CUDA)
-def rowwise_adagrad_(weight: Tensor, accumulator: Tensor, rows: Tensor, values: Tensor, lr: float,
-                     eps: float) -> None:
-    ops.rowwise_adagrad_(weight, accumulator, rows, values, lr=lr, eps=eps)
-
-
-@rowwise_adagrad_.register_kernel("cpu")
+@_cpu_kernel("rowwise_adagrad_")
 def _rowwise_adagrad_cpu(weight, accumulator, rows, values, lr, eps):
     """The CPU branch of ShardedRowWiseAdagrad.step (src/optim.py:359-376):
     the update is rounded to the weight dtype, then added."""
@@ -725,70 +609,33 @@ def _rowwise_adagrad_cpu(weight, accumulator, rows, values, lr, eps):
     weight.index_add_(0, rows, update, alpha=-lr)
 
 
-@rowwise_adagrad_.register_fake
+@_fake_kernel("rowwise_adagrad_")
 def _rowwise_adagrad_fake(weight, accumulator, rows, values, lr, eps):
     return None
 
 
-@torch.library.custom_op("mdl_hip::grouped_rowwise_adagrad_", mutates_args=("weights", "accumulators"),
-                         device_types=_CUDA)
-def grouped_rowwise_adagrad_(weights: list[Tensor], accumulators: list[Tensor], rows: list[Tensor],
-                             values: list[Tensor], counts: list[Optional[Tensor]], lrs: list[float],
-                             eps: float) -> None:
-    """Row-wise Adagrad of every table in one launch; table i updates
-    ``rows[i][:counts[i]]`` (the count read on the device; None: all)."""
-
-    ops.grouped_rowwise_adagrad_(weights, accumulators, rows, values, counts, lrs, eps=eps)
-
-
-@grouped_rowwise_adagrad_.register_kernel("cpu")
+@_cpu_kernel("grouped_rowwise_adagrad_")
 def _grouped_adagrad_cpu(weights, accumulators, rows, values, counts, lrs, eps):
     for w, a, r, v, c, lr in zip(weights, accumulators, rows, values, counts, lrs):
         n = int(r.numel()) if c is None else int(c.reshape(-1)[0])
         _rowwise_adagrad_cpu(w, a, r[:n], v[:n], lr, eps)
 
 
-@grouped_rowwise_adagrad_.register_fake
+@_fake_kernel("grouped_rowwise_adagrad_")
 def _grouped_adagrad_fake(weights, accumulators, rows, values, counts, lrs, eps):
     return None
 
 
 # ------------------------------------------- gradients the optimizer knows --
 
-# Capacity-sized gradients this module emitted, by parameter: the optimizer
-# finds their device row count here instead of coalescing them again.
-# Autograd's AccumulateGrad may re-wrap a sparse gradient around the same
-# index and value storage; the record is matched by storage.  A gradient
-# accumulated over several backward passes has new storage and is coalesced
-# normally.
-_CAPACITY_GRADS: dict[int, tuple] = {}
-
-
-def _note_capacity_grad(parameter: Tensor, rows: Tensor, values: Tensor, count: Tensor) -> None:
-    _CAPACITY_GRADS[id(parameter)] = (weakref.ref(parameter), rows, values, count)
-
-
-def _drop_dead_records() -> None:
-    """Forget records of parameters that no longer exist (once per backward)."""
-
-    for key in [k for k, rec in _CAPACITY_GRADS.items() if rec[0]() is None]:
-        del _CAPACITY_GRADS[key]
-
 
 def capacity_grad(parameter: Tensor, grad: Tensor) -> Optional[tuple[Tensor, Tensor, Tensor]]:
     """``(rows, values, count)`` when ``grad`` is the capacity-sized gradient
-    last emitted for ``parameter``, else None."""
+    last emitted for ``parameter`` (the extension's record), else None."""
 
-    entry = _CAPACITY_GRADS.get(id(parameter))
-    if entry is None or entry[0]() is not parameter:
-        return None
-    _, rows, values, count = entry
-    idx, val = grad._indices(), grad._values()
-    if (idx.data_ptr() == rows.data_ptr() and val.data_ptr() == values.data_ptr()
-            and idx.size(-1) == rows.numel() and tuple(val.shape) == tuple(values.shape)):
-        return rows, values, count
-    return None
+    rec = torch.ops.mdl_hip.capacity_grad_record(parameter, grad)
+    return (rec[0], rec[1], rec[2]) if rec else None
 
 
 def forget_capacity_grad(parameter: Tensor) -> None:
-    _CAPACITY_GRADS.pop(id(parameter), None)
+    torch.ops.mdl_hip.forget_capacity_grad(parameter)

@@ -3,12 +3,14 @@
 Same constructor, state layout (``step``: 0-d float64 on CPU, ``sum``: one
 fp32 accumulator per row) and ``load_state_dict`` behaviour as
 src/optim.py:212-377, so checkpoints move between the two unchanged.
-Gradients must be sparse COO.  ``step`` updates every parameter of a device
-with one ``mdl_hip::grouped_rowwise_adagrad_`` launch: a gradient emitted by
-the grouped lookup is capacity-sized with its row count on the device, so
-the step needs no host read; any other gradient is coalesced by the
-library's sort/segment-reduce first.  Parameters on the CPU take the
-reference's CPU branch (src/optim.py:359-376) through the same ops.
+Gradients must be sparse COO.  ``step`` is one ``mdl_hip::rowwise_adagrad_step_``
+call per parameter group: the C++ extension checks the gradients, advances
+the step counts and updates every parameter of a device with one grouped
+launch.  A coalesced gradient is used as it is; a capacity-sized gradient of
+the grouped lookup is updated up to its row count, read on the device; any
+other gradient is coalesced by the library's sort/segment-reduce first, with
+no host read.  Parameters on the CPU take the reference's CPU branch
+(src/optim.py:359-376).
 """
 
 from __future__ import annotations
@@ -150,19 +152,6 @@ class ShardedRowWiseAdagrad(torch.optim.Optimizer):
                 if isinstance(step, Tensor):
                     state["step"] = step.to(device="cpu", dtype=torch.float64)
 
-    def _advance(self, parameter: Tensor, group: dict[str, Any]) -> float:
-        """Bump the CPU step counter; return the decayed learning rate."""
-
-        step_tensor = self.state[parameter]["step"]
-        lr = float(group["lr"])
-        lr_decay = float(group["lr_decay"])
-        if lr_decay == 0.0:
-            step_tensor.add_(1.0)  # the rate does not read the count
-            return lr
-        step = float(step_tensor) + 1.0
-        step_tensor.fill_(step)
-        return lr / (1.0 + (step - 1.0) * lr_decay)
-
     @torch.no_grad()
     def step(self, closure: Callable[[], Tensor] | None = None) -> Tensor | None:
         loss = None
@@ -171,33 +160,15 @@ class ShardedRowWiseAdagrad(torch.optim.Optimizer):
                 loss = closure()
         if embeddings.deferred_index_checks():
             embeddings.check_index_errors()
-        # every parameter of one device (and eps) in one launch
-        batches: dict[tuple, list] = {}
+        # One call per parameter group: the extension checks every gradient,
+        # advances the CPU step counts, decays the learning rates and updates
+        # every device parameter with one grouped launch per device (CPU
+        # parameters take the reference's CPU branch, src/optim.py:359-376).
         for group in self.param_groups:
-            eps = float(group["eps"])
-            for parameter in group["params"]:
-                grad = parameter.grad
-                if grad is None:
-                    continue
-                if not grad.is_sparse or grad.layout != torch.sparse_coo:
-                    raise RuntimeError(
-                        "ShardedRowWiseAdagrad expects one-dimensional row-sparse COO gradients"
-                    )
-                if grad.sparse_dim() != 1 or grad.dense_dim() != 1:
-                    raise RuntimeError(
-                        "ShardedRowWiseAdagrad expects one sparse row dimension and one dense dimension"
-                    )
-                rows, values, count = update_rows(parameter)
-                clear_lr = self._advance(parameter, group)
-                accumulator: Tensor = self.state[parameter]["sum"]
-                batches.setdefault((parameter.device, eps), []).append(
-                    (parameter, accumulator, rows, values, count, clear_lr)
-                )
-        for (_, eps), items in batches.items():
-            torch.ops.mdl_hip.grouped_rowwise_adagrad_(
-                [i[0] for i in items], [i[1] for i in items], [i[2] for i in items], [i[3] for i in items],
-                [i[4] for i in items], [i[5] for i in items], eps,
+            params = group["params"]
+            states = [self.state[p] for p in params]
+            torch.ops.mdl_hip.rowwise_adagrad_step_(
+                params, [st["sum"] for st in states], [st["step"] for st in states], [p.grad for p in params],
+                float(group["lr"]), float(group["lr_decay"]), float(group["eps"]),
             )
-            for item in items:
-                library.forget_capacity_grad(item[0])
         return loss

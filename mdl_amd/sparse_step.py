@@ -235,9 +235,14 @@ class SparseStep:
             self._positions = torch.arange(cap, dtype=torch.int64, device=self.device)
             sentinel = int(plan.sentinel)
             self._sentinel = sentinel - (1 << 32) if sentinel >= (1 << 31) else sentinel
+        self._empty_ids = torch.zeros(1, dtype=torch.int64, device=self.device)
         self.sumsq = torch.zeros(G, dtype=torch.float32, device=self.device)
         self.norm = torch.zeros(1, dtype=torch.float32, device=self.device)
         self.coef = torch.ones(1, dtype=torch.float32, device=self.device)
+        # what the update mutates, named in the ops' schemas
+        self._weights = [t.weight for t in plan.tables]
+        self._states = [t.state for t in plan.tables]
+        self._outs = [o for outs in outputs for o in outs]
 
     # ----------------------------------------------------------- batches --
 
@@ -272,12 +277,13 @@ class SparseStep:
     def _stream(self) -> int:
         return torch.cuda.current_stream(self.device).cuda_stream
 
-    def _count_ptr(self, g: int):
-        """Device address of group g's entry count (None: all of the capacity)."""
+    def _count(self, g: int) -> tuple[Tensor | None, int]:
+        """Group g's entry count on the device: (tensor, element offset);
+        (None, 0) when the sort takes all of its capacity."""
 
         if len(self.groups) > 1:
-            return self._gcount.data_ptr() + 8 * g
-        return None if self.offsets is None else self.offsets.data_ptr() + 8 * (self.offsets.numel() - 1)
+            return self._gcount, g
+        return (None, 0) if self.offsets is None else (self.offsets, int(self.offsets.numel()) - 1)
 
     def _n(self) -> int:
         if self.k > 1:
@@ -307,18 +313,13 @@ class SparseStep:
         if G > 1 and self.dynamic:
             torch.index_select(self.offsets, 0, self._gidx, out=self._gsel)
             torch.sub(self._gsel[G:], self._gsel[:G], out=self._gcount)
-        ids = self.ids if self.ids.numel() else self.groups[0].keys  # any valid address; nothing is read
+        ids = self.ids if self.ids.numel() else self._empty_ids  # any valid address; nothing is read
         region = m * max(self.capacity, 1)
         for g, gs in enumerate(self.groups):
-            origin = None if G == 1 else self._gsel.data_ptr() + 8 * g
-            check(
-                lib().mdl_forward(
-                    gs.feats_fwd_dev.data_ptr() + m * gs.F * FEATURE_DTYPE.itemsize, gs.F, gs.chunks_dev.data_ptr(),
-                    gs.n_chunks, ids.data_ptr(), int(self.ids.numel()), ops._ptr(self.offsets),
-                    gs.keys.data_ptr() + 4 * region, gs.payload.data_ptr() + 4 * region, origin, self.plan.sentinel,
-                    ops._ptr(self.bag_count), self.error_count.data_ptr(), gs.fwd_classes, s,
-                ),
-                "mdl_forward",
+            torch.ops.mdl_hip.packed_forward_(
+                gs.feats_fwd_dev, m * gs.F, gs.F, gs.chunks_dev, gs.n_chunks, ids, int(self.ids.numel()),
+                self.offsets, gs.keys, gs.payload, region, None if G == 1 else self._gsel, g, self.plan.sentinel,
+                self.bag_count, self.error_count, self._outs, gs.fwd_classes,
             )
             if self.k > 1:
                 # entries of the region past this micro-batch's ids sort last
@@ -343,33 +344,19 @@ class SparseStep:
 
         self._check_micro_batches()
         for g, gs in enumerate(self.groups):
-            check(
-                lib().mdl_backward_sort(
-                    gs.tables_dev.data_ptr(), len(gs.tables), self.plan.max_dim, gs.keys.data_ptr(),
-                    gs.payload.data_ptr(), self._n(), self._count_ptr(g) if self.k == 1 else None,
-                    self.plan.key_bits, gs.ws.data_ptr(), gs.ws.numel(), self._stream(),
-                ),
-                "mdl_backward_sort",
-            )
-
-    def _bwd_args(self, gs: "_KeyGroup") -> tuple:
-        return (
-            gs.feats_bwd_dev.data_ptr(), len(gs.feats_bwd), gs.tables_dev.data_ptr(), len(gs.tables),
-            self.plan.max_dim, gs.keys.data_ptr(), gs.payload.data_ptr(), self._n(), self.plan.key_bits,
-            ops._ptr(self.bag_count),
-        )
+            count, at = self._count(g) if self.k == 1 else (None, 0)
+            torch.ops.mdl_hip.backward_sort_(gs.tables_dev, len(gs.tables), gs.keys, gs.payload, self._n(), count, at,
+                                             self.plan.max_dim, self.plan.key_bits, gs.ws)
 
     def apply(self, lr: float, eps: float, grad_scale: Tensor | None = None) -> None:
         """Segment reduction of duplicate rows + fused row-wise Adagrad
         (gradients times ``grad_scale``, a device fp32 [1], when given)."""
 
         for gs in self.groups:
-            check(
-                lib().mdl_backward_apply(
-                    *self._bwd_args(gs), float(lr), float(eps), ops._ptr(grad_scale), gs.ws.data_ptr(),
-                    gs.ws.numel(), gs.bwd_classes, self._stream(),
-                ),
-                "mdl_backward_apply",
+            torch.ops.mdl_hip.backward_apply_(
+                self._weights, self._states, gs.feats_bwd_dev, len(gs.feats_bwd), gs.tables_dev, len(gs.tables),
+                gs.keys, gs.payload, self._n(), self.bag_count, grad_scale, gs.ws, self.plan.max_dim,
+                self.plan.key_bits, gs.bwd_classes, float(lr), float(eps),
             )
 
     def clip(self, max_norm: float) -> tuple[Tensor, Tensor]:
@@ -379,31 +366,32 @@ class SparseStep:
         trainer's sparse clip computes it (src/train.py:5788-5826)."""
 
         for g, gs in enumerate(self.groups):
-            check(
-                lib().mdl_backward_sumsq(
-                    *self._bwd_args(gs), self.sumsq.data_ptr() + 4 * g, gs.ws.data_ptr(), gs.ws.numel(),
-                    gs.bwd_classes, self._stream(),
-                ),
-                "mdl_backward_sumsq",
+            torch.ops.mdl_hip.backward_sumsq_(
+                gs.feats_bwd_dev, len(gs.feats_bwd), gs.tables_dev, len(gs.tables), gs.keys, gs.payload, self._n(),
+                self.bag_count, self.sumsq, g, gs.ws, self.plan.max_dim, self.plan.key_bits, gs.bwd_classes,
             )
-        check(
-            lib().mdl_clip_coef(self.sumsq.data_ptr(), len(self.groups), float(max_norm), self.norm.data_ptr(),
-                                self.coef.data_ptr(), self._stream()),
-            "mdl_clip_coef",
-        )
+        torch.ops.mdl_hip.clip_coefficient_(self.sumsq, len(self.groups), float(max_norm), self.norm, self.coef)
         return self.norm, self.coef
 
     def step(self, lr: float, eps: float, clip_norm: float | None = None) -> None:
-        """Forward, sort and update of the bound batch (one micro-batch)."""
+        """Forward, sort and update of the bound batch (one micro-batch):
+        without a clip the sort and the update are one fused op,
+        ``mdl_hip::fused_backward_rowwise_adagrad_``."""
 
         if self.k > 1:
             raise ValueError("a step of several micro-batches is forward(micro_batch=m) for each m, then "
                              "sort() and apply()")
         self.forward()
-        self.sort()
         if clip_norm is None:
-            self.apply(lr, eps)
+            for g, gs in enumerate(self.groups):
+                count, at = self._count(g)
+                torch.ops.mdl_hip.fused_backward_rowwise_adagrad_(
+                    self._weights, self._states, gs.feats_bwd_dev, len(gs.feats_bwd), gs.tables_dev, len(gs.tables),
+                    gs.keys, gs.payload, self._n(), count, at, self.bag_count, None, gs.ws, self.plan.max_dim,
+                    self.plan.key_bits, gs.bwd_classes, float(lr), float(eps),
+                )
         else:
+            self.sort()
             _, coef = self.clip(clip_norm)
             self.apply(lr, eps, coef)
 
@@ -452,10 +440,11 @@ class SequenceStep:
     feature; backward: one sort and one segment-reduce + row-wise Adagrad over
     all features together.
 
-    Sort keys are packed: row b of feature f keeps min(len, L_in, L_out)
-    entries (the positions that reach the window), placed each step by one
-    scan of those clamped lengths on the device, so the backward sorts no
-    padding and any lengths of a later batch are honoured.
+    Sort keys are packed: row b of feature f keeps min(len, L_out) entries
+    (its window positions; none for an empty input, and a length past the
+    input repeats its last id as the reference's window does), placed each
+    step by one scan of those clamped lengths on the device, so the backward
+    sorts no padding and any lengths of a later batch are honoured.
 
     A plan of 2^32 - 1 rows or more is cut into key groups
     (``GroupPlan.groups``): each group's features pack their entries into a
@@ -570,6 +559,9 @@ class SequenceStep:
                 lib().mdl_backward_workspace_bytes(self._n(gs), len(gs.tables), plan.max_dim), self.device
             )
             self.groups.append(gs)
+        # what the update mutates, named in the ops' schemas
+        self._weights = [t.weight for t in plan.tables]
+        self._states = [t.state for t in plan.tables]
 
     def _n(self, gs: _SeqGroup) -> int:
         return max(gs.cap, 1) * self.k if self.k > 1 else gs.cap
@@ -647,26 +639,17 @@ class SequenceStep:
     def sort(self) -> None:
         self._check_micro_batches()
         for gs in self.groups:
-            check(
-                lib().mdl_backward_sort(
-                    gs.tables_dev.data_ptr(), len(gs.tables), self.plan.max_dim, gs.keys.data_ptr(),
-                    gs.payload.data_ptr(), self._n(gs),
-                    gs.offsets.data_ptr() + 8 * (gs.r1 - gs.r0) if self.k == 1 else None,
-                    self.plan.key_bits, gs.ws.data_ptr(), gs.ws.numel(), self._stream(),
-                ),
-                "mdl_backward_sort",
+            torch.ops.mdl_hip.backward_sort_(
+                gs.tables_dev, len(gs.tables), gs.keys, gs.payload, self._n(gs),
+                gs.offsets if self.k == 1 else None, gs.r1 - gs.r0, self.plan.max_dim, self.plan.key_bits, gs.ws,
             )
 
     def apply(self, lr: float, eps: float) -> None:
         for gs in self.groups:
-            check(
-                lib().mdl_backward_apply(
-                    gs.feats_bwd_dev.data_ptr(), len(gs.feats_bwd), gs.tables_dev.data_ptr(), len(gs.tables),
-                    self.plan.max_dim, gs.keys.data_ptr(), gs.payload.data_ptr(), self._n(gs), self.plan.key_bits,
-                    None, float(lr), float(eps), None, gs.ws.data_ptr(), gs.ws.numel(), gs.bwd_classes,
-                    self._stream(),
-                ),
-                "mdl_backward_apply",
+            torch.ops.mdl_hip.backward_apply_(
+                self._weights, self._states, gs.feats_bwd_dev, len(gs.feats_bwd), gs.tables_dev, len(gs.tables),
+                gs.keys, gs.payload, self._n(gs), None, None, gs.ws, self.plan.max_dim, self.plan.key_bits,
+                gs.bwd_classes, float(lr), float(eps),
             )
 
     def capture(self, lr: float, eps: float) -> None:

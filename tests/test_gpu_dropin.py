@@ -21,6 +21,7 @@ from mdl_amd.embeddings import (
 )
 from mdl_amd.optim import ShardedRowWiseAdagrad
 from oracle import oracle as O
+from parity_helpers import _check_update
 
 pytestmark = pytest.mark.gpu
 GOLD = json.loads((pathlib.Path(__file__).parent / "golden" / "reference_vectors.json").read_text())
@@ -48,8 +49,20 @@ def _modules(device, specs):
     return out
 
 
-def test_single_rank_grouped_lookup_matches_native_embedding(device):
-    announce("grouped_lookup_native")
+@pytest.fixture(params=["coalesced", "capacity"])
+def grad_mode(request):
+    """Both sparse-gradient modes of the lookups' backward."""
+
+    import mdl_amd.library as L
+
+    mode = L.sparse_grad_mode()
+    L.set_sparse_grad_mode(request.param)
+    yield request.param
+    L.set_sparse_grad_mode(mode)
+
+
+def test_single_rank_grouped_lookup_matches_native_embedding(device, grad_mode):
+    announce("grouped_lookup_native", grad_mode)
     emb_a, emb_b = _modules(device, [("a", 16, 4), ("b", 16, 4)])
     full_a = torch.randn(16, 4)
     full_b = torch.randn(16, 4)
@@ -66,14 +79,19 @@ def test_single_rank_grouped_lookup_matches_native_embedding(device):
     loss.backward()
     ga = emb_a.weight.grad
     assert ga is not None and ga.is_sparse
-    # capacity-sized (4 ids): the coalesced rows first, then zero-valued
-    # repeats of the last row; the optimizer finds its device row count
-    from mdl_amd.library import capacity_grad
+    if grad_mode == "coalesced":
+        # exact and flagged: the trainer's coalesce() returns the same tensor
+        assert ga.is_coalesced() and ga.coalesce() is ga
+        assert ga._indices()[0].tolist() == [3, 7]  # padding row 0 gets no gradient
+    else:
+        # capacity-sized (4 ids): the coalesced rows first, then zero-valued
+        # repeats of the last row; the optimizer finds its device row count
+        from mdl_amd.library import capacity_grad
 
-    rows, values, count = capacity_grad(emb_a.weight, ga)
-    assert int(count.item()) == 2 and ga._indices().size(1) == 4
-    assert rows[:2].tolist() == [3, 7]  # padding row 0 gets no gradient
-    assert rows[2:].tolist() == [7, 7] and not values[2:].any()
+        rows, values, count = capacity_grad(emb_a.weight, ga)
+        assert int(count.item()) == 2 and ga._indices().size(1) == 4
+        assert rows[:2].tolist() == [3, 7]  # padding row 0 gets no gradient
+        assert rows[2:].tolist() == [7, 7] and not values[2:].any()
     c = ga.coalesce()
     assert c.indices()[0].tolist() == [3, 7]
     torch.testing.assert_close(c.values().cpu(), torch.stack([4 * full_a[3], 2 * full_a[7]]))
@@ -421,3 +439,101 @@ def test_concatenated_outputs_train_like_separate_ones(device, dtype):
         results.append([m.weight.detach().clone() for m in mods] + [opt.state[m.weight]["sum"].clone() for m in mods])
     for a, b in zip(*results):
         assert torch.equal(a, b)
+
+
+def _reference_clip(parameters, max_norm):
+    """The trainer's sparse clip written with torch ops the way
+    src/train.py:5730-5826 writes it (_gradient_values: coalesce and store
+    back; fp32 vector_norm of each; min(max_norm / (norm + 1e-6), 1);
+    _foreach_mul_ of every value tensor), for a test that keeps the
+    reference's own clip in the loop.  Returns the pre-clip norm and whether
+    every coalesce() returned its input."""
+
+    grads, untouched = [], True
+    for p in parameters:
+        g = p.grad
+        c = g.coalesce()
+        untouched = untouched and c is g
+        p.grad = c
+        grads.append(c._values())
+    total = torch.zeros((), dtype=torch.float32, device=grads[0].device)
+    for v in grads:
+        total.add_(torch.linalg.vector_norm(v.float(), 2.0).square())
+    norm = total.sqrt()
+    coef = (max_norm / (norm + 1e-6)).clamp(max=1.0)
+    for v in grads:
+        v.mul_(coef.to(v.dtype))
+    return norm, untouched
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+def test_reference_shaped_step_in_both_gradient_modes(device, grad_mode, dtype):
+    """backward -> sparse clip -> ShardedRowWiseAdagrad.step, as the
+    reference's trainer sequences them (src/train.py:5730-5826,
+    src/optim.py:299-377), against the oracle's coalesce + clip + update.
+
+    coalesced mode: the reference's clip as written, whose coalesce() calls
+    must return the gradients as they are (no ATen coalesce);
+    capacity mode: the ``mdl_amd.clip`` swap, the whole checked step under
+    ``torch.cuda.set_sync_debug_mode("error")`` (no host synchronisation)."""
+
+    from mdl_amd.clip import _clip_sparse_grad_norm
+
+    announce("reference_shaped_step", grad_mode, dtype)
+    rng = np.random.default_rng(131)
+    specs = [("bag", 400, 16), ("single", 900, 8), ("wide", 300, 130)]
+    mods = _modules(device, specs)
+    for m in mods:
+        m.weight.data = m.weight.data.to(dtype)
+    opt = ShardedRowWiseAdagrad([m.weight for m in mods], lr=0.05, eps=1e-8)
+    B, max_norm = 64, 0.5
+
+    def batch():
+        lb = rng.integers(0, 9, size=B)
+        return (torch.from_numpy(rng.zipf(1.2, size=int(lb.sum())) % 400).to(device), torch.from_numpy(lb).to(device),
+                torch.from_numpy(rng.integers(0, 900, size=B)).to(device),
+                torch.from_numpy(rng.integers(0, 300, size=B)).to(device),
+                torch.from_numpy(rng.standard_normal((B, 16 + 8 + 130)).astype(np.float32)).to(device, dtype))
+
+    def step(b):
+        xb, lb, xs, xw, g = b
+        opt.zero_grad(set_to_none=True)
+        pooled = pooled_embedding_lookup([(mods[0], xb, lb, "mean", "exclude")])
+        singles = grouped_sharded_embedding_lookup([(mods[1], xs), (mods[2], xw)])
+        slots = torch.cat([pooled[0], *singles], dim=1)
+        slots.backward(g)
+        if grad_mode == "coalesced":
+            norm, untouched = _reference_clip([m.weight for m in mods], max_norm)
+            assert untouched
+        else:
+            norm = _clip_sparse_grad_norm([], [m.weight for m in mods], max_norm)
+        opt.step()
+        return norm
+
+    step(batch())  # kernels loaded, caches warm
+    torch.cuda.synchronize()
+    W0 = [m.weight.detach().float().cpu().numpy() for m in mods]
+    A0 = [opt.state[m.weight]["sum"].cpu().numpy() for m in mods]
+    b = batch()
+    if grad_mode == "capacity":
+        torch.cuda.set_sync_debug_mode("error")
+    try:
+        norm = step(b)
+    finally:
+        torch.cuda.set_sync_debug_mode("default")
+    xb, lb, xs, xw, g = [t.cpu() for t in b]
+    g = g.float().numpy().astype(np.float64)
+    parts = [O.per_id_grads(xb.numpy(), lb.numpy(), g[:, :16], "mean", "exclude"),
+             O.per_id_grads(xs.numpy(), None, g[:, 16:24], "none", "exclude"),
+             O.per_id_grads(xw.numpy(), None, g[:, 24:], "none", "exclude")]
+    coalesced = [O.coalesce(r, v) for r, v in parts]
+    scaled, total, coef = O.clip_grad_norm([v for _, v in coalesced], max_norm)
+    bf16 = dtype == torch.bfloat16
+    rtol = 1e-2 if bf16 else 1e-5  # bf16: the sparse gradients are stored in the table dtype
+    assert abs(float(norm) - total) <= rtol * total + 1e-6
+    absparts = [O.coalesce(r, np.abs(v)) for r, v in parts]
+    for t, (m, (r, _), v, (_, s), w0, a0) in enumerate(zip(mods, coalesced, scaled, absparts, W0, A0)):
+        # the clipped gradient and its |terms| bound, scaled by the coefficient
+        _check_update(f"{grad_mode} table {t}", m.weight.detach().float().cpu().numpy(),
+                      opt.state[m.weight]["sum"].cpu().numpy(), w0, a0, r, v, s * coef, 0.05, 1e-8, rtol,
+                      1e-6 if bf16 else 1e-7, bf16, acc_rtol=rtol)

@@ -33,6 +33,18 @@ pytestmark = pytest.mark.gpu
 OPS = torch.ops.mdl_hip
 
 
+@pytest.fixture
+def capacity_grads():
+    """Traced backward graphs hold capacity-sized sparse gradients (an exact
+    coalesced gradient's size is data); opcheck compares the eager gradient
+    with the traced one, so it runs in that mode."""
+
+    mode = mdl_amd.library.sparse_grad_mode()
+    mdl_amd.library.set_sparse_grad_mode("capacity")
+    yield
+    mdl_amd.library.set_sparse_grad_mode(mode)
+
+
 def announce(*parts):
     print("CASE", *parts, flush=True)
     sys.stdout.flush()
@@ -49,7 +61,7 @@ def _to(args, device):
     return args
 
 
-def test_opcheck_rocm(device):
+def test_opcheck_rocm(device, capacity_grads):
     from tests.test_library import _lookup_args
 
     announce("opcheck_rocm")
@@ -146,10 +158,11 @@ def test_cpu_and_rocm_modules_train_alike(device):
                                    atol=1e-6)
 
 
-def test_training_loop_makes_no_host_sync(device):
+def test_training_loop_makes_no_host_sync(device, capacity_grads):
     """Lookups (pooled, single, sequence), loss.backward() and
     optimizer.step() under the sync debug mode that raises on any
-    device-to-host synchronisation; the result matches the CPU run."""
+    device-to-host synchronisation (the capacity-sized gradient mode, which
+    reads no row count on the host); the result matches the CPU run."""
 
     announce("sync_free_loop")
     specs = [("bag_a", 300, 8), ("bag_b", 80, 4), ("single", 500, 16)]

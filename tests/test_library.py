@@ -32,6 +32,18 @@ GOLD = json.loads((pathlib.Path(__file__).parent / "golden" / "reference_vectors
 OPS = torch.ops.mdl_hip
 
 
+@pytest.fixture
+def capacity_grads():
+    """Traced backward graphs hold capacity-sized sparse gradients (an exact
+    coalesced gradient's size is data); opcheck compares the eager gradient
+    with the traced one, so it runs in that mode."""
+
+    mode = mdl_amd.library.sparse_grad_mode()
+    mdl_amd.library.set_sparse_grad_mode("capacity")
+    yield
+    mdl_amd.library.set_sparse_grad_mode(mode)
+
+
 def _lookup_args(requires_grad=True):
     torch.manual_seed(0)
     W = [torch.randn(20, 4, requires_grad=requires_grad), torch.randn(9, 8, requires_grad=requires_grad)]
@@ -44,7 +56,7 @@ def _lookup_args(requires_grad=True):
                                   "bucketize", "lengths_to_offsets", "sparse_coalesce", "sparse_coalesce_padded",
                                   "grouped_lookup_backward",
                                   "sequence_lookup_backward"])
-def test_opcheck_cpu(name):
+def test_opcheck_cpu(name, capacity_grads):
     if name == "grouped_lookup":
         args = _lookup_args()
     elif name == "grouped_lookup_backward":
@@ -236,7 +248,30 @@ def test_cpu_errors_follow_the_reference():
         opt.step()
 
 
-def test_capacity_gradient_is_a_valid_coo_of_the_coalesced_sum():
+def test_coalesced_gradient_is_exact_and_marked_coalesced():
+    """The default sparse-gradient mode: the lookup's gradient arrives
+    coalesced (rows ascending and unique, is_coalesced() true), so the
+    trainer's grad.coalesce() (src/train.py:5738, src/optim.py:323-324)
+    returns the same tensor; its values are the per-row sums."""
+
+    assert mdl_amd.library.sparse_grad_mode() == "coalesced"
+    (m,) = _modules([("t", 50, 4)])
+    ids = torch.tensor([7, 3, 7, 0, 9, 3])
+    out = m(ids)
+    g = torch.randn(out.shape)
+    out.backward(g)
+    grad = m.weight.grad
+    assert grad.is_coalesced()
+    assert grad._indices()[0].tolist() == [3, 7, 9]
+    assert grad.coalesce() is grad
+    dense = torch.zeros(50, 4)
+    dense.index_add_(0, ids, g)
+    dense[0] = 0  # padding_idx gets no gradient
+    torch.testing.assert_close(grad.to_dense(), dense)
+    torch.testing.assert_close(grad._values(), dense[[3, 7, 9]])
+
+
+def test_capacity_gradient_is_a_valid_coo_of_the_coalesced_sum(capacity_grads):
     """The lookup's gradient has one entry per id (a bound known without a
     device read); coalescing it gives the exact coalesced gradient."""
 
