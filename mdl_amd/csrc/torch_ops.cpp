@@ -17,6 +17,8 @@
 // with its fused update (:68-108).
 
 #include <ATen/ATen.h>
+#include <ATen/SparseTensorImpl.h>
+#include <ATen/native/SparseTensorUtils.h>
 #include <ATen/core/dispatch/Dispatcher.h>
 #include <c10/core/DeviceGuard.h>
 #include <c10/hip/HIPStream.h>
@@ -91,6 +93,21 @@ Tensor workspace(size_t bytes, const at::Device& dev) {
   return at::empty({(int64_t)std::max<size_t>(bytes, 1)}, at::TensorOptions().dtype(at::kByte).device(dev));
 }
 
+// A dense tensor over `base`'s storage (same device and key set) at a byte
+// offset, built without a dispatcher call: the per-table rows and values of
+// a backward are 200-odd such tensors per step.
+Tensor raw_view(const Tensor& base, at::ScalarType dtype, int64_t byte_offset, at::IntArrayRef sizes,
+                at::IntArrayRef strides) {
+  const auto meta = c10::scalarTypeToTypeMeta(dtype);
+  TORCH_CHECK(byte_offset % (int64_t)meta.itemsize() == 0, "view offset must be a multiple of the element size");
+  auto impl = c10::make_intrusive<c10::TensorImpl>(c10::TensorImpl::VIEW, c10::Storage(base.storage()),
+                                                   base.key_set(), meta);
+  impl->set_sizes_and_strides(sizes, strides,
+                              base.storage_offset() * (int64_t)base.element_size() / (int64_t)meta.itemsize() +
+                                  byte_offset / (int64_t)meta.itemsize());
+  return Tensor(std::move(impl));
+}
+
 int64_t bit_length(int64_t v) {
   int64_t b = 0;
   while (v > 0) {
@@ -130,8 +147,9 @@ struct Layout {
 
 struct LayoutCache {
   std::mutex mu;
-  std::list<std::pair<std::string, std::shared_ptr<const Layout>>> lru;  // most recent first
-  std::unordered_map<std::string, decltype(lru)::iterator> index;
+  using Key = std::vector<int64_t>;
+  std::list<std::pair<Key, std::shared_ptr<const Layout>>> lru;  // most recent first
+  std::unordered_multimap<uint64_t, decltype(lru)::iterator> index;
   static constexpr size_t kMax = 16;
 };
 LayoutCache g_layouts;
@@ -148,8 +166,6 @@ void validate_weights(TensorList weights) {
     TORCH_CHECK_VALUE(w.size(0) < kKeySpace, "a table of a grouped lookup holds fewer than 2^32 - 1 rows");
   }
 }
-
-void append_bytes(std::string& k, const void* p, size_t n) { k.append(static_cast<const char*>(p), n); }
 
 // Feature order of a device call: the caller's order (empty), except that a
 // call over 2^32 - 1 table rows or more looks its features up sorted by
@@ -283,37 +299,61 @@ std::shared_ptr<const Layout> build_layout(TensorList weights, at::IntArrayRef t
   return L;
 }
 
+uint64_t hash_key(const std::vector<int64_t>& k) {
+  uint64_t h = 1469598103934665603ull;
+  for (int64_t v : k) {
+    h ^= (uint64_t)v + 0x9e3779b97f4a7c15ull + (h << 6) + (h >> 2);
+    h *= 1099511628211ull;
+  }
+  return h;
+}
+
+// The cached layout of these tables and feature codes; the tables are
+// validated when their layout is first built (the key holds everything the
+// validation reads: address, shape, strides, dtype, device).
 std::shared_ptr<const Layout> layout_for(TensorList weights, at::IntArrayRef table, at::IntArrayRef pooling,
                                          at::IntArrayRef exclude, at::IntArrayRef padding_idx) {
-  std::string key;
-  key.reserve(weights.size() * 40 + table.size() * 32 + 8);
-  const int64_t dev = weights[0].device().index();
-  append_bytes(key, &dev, 8);
+  LayoutCache::Key key;
+  key.reserve(2 + weights.size() * 7 + 4 * (table.size() + 1));
+  key.push_back((int64_t)weights.size());
   for (const Tensor& w : weights) {
-    const int64_t rec[5] = {(int64_t)addr(w), w.size(0), w.size(1), w.stride(0), (int64_t)w.scalar_type()};
-    append_bytes(key, rec, sizeof(rec));
+    key.push_back((int64_t)addr(w));
+    key.push_back(w.dim());
+    key.push_back(w.dim() == 2 ? w.size(0) : -1);
+    key.push_back(w.dim() == 2 ? w.size(1) : -1);
+    key.push_back(w.dim() == 2 ? w.stride(0) : -1);
+    key.push_back(w.dim() == 2 ? w.stride(1) : -1);
+    key.push_back(((int64_t)w.scalar_type() << 16) | ((int64_t)w.device().type() << 8) | (w.device().index() & 0xff));
   }
-  const int64_t sep = -7;
   for (auto arr : {table, pooling, exclude, padding_idx}) {
-    append_bytes(key, &sep, 8);
-    append_bytes(key, arr.data(), arr.size() * 8);
+    key.push_back(-7);
+    key.insert(key.end(), arr.begin(), arr.end());
   }
+  const uint64_t h = hash_key(key);
   {
     std::lock_guard<std::mutex> lock(g_layouts.mu);
-    auto it = g_layouts.index.find(key);
-    if (it != g_layouts.index.end()) {
-      g_layouts.lru.splice(g_layouts.lru.begin(), g_layouts.lru, it->second);
-      return it->second->second;
+    auto range = g_layouts.index.equal_range(h);
+    for (auto it = range.first; it != range.second; ++it) {
+      if (it->second->first == key) {
+        g_layouts.lru.splice(g_layouts.lru.begin(), g_layouts.lru, it->second);
+        return it->second->second;
+      }
     }
   }
+  validate_weights(weights);
   auto L = build_layout(weights, table, pooling, exclude, padding_idx);
   std::lock_guard<std::mutex> lock(g_layouts.mu);
-  auto it = g_layouts.index.find(key);
-  if (it != g_layouts.index.end()) return it->second->second;
-  g_layouts.lru.emplace_front(key, L);
-  g_layouts.index[key] = g_layouts.lru.begin();
+  g_layouts.lru.emplace_front(std::move(key), L);
+  g_layouts.index.emplace(h, g_layouts.lru.begin());
   if (g_layouts.lru.size() > LayoutCache::kMax) {
-    g_layouts.index.erase(g_layouts.lru.back().first);
+    const uint64_t old = hash_key(g_layouts.lru.back().first);
+    auto range = g_layouts.index.equal_range(old);
+    for (auto it = range.first; it != range.second; ++it) {
+      if (it->second == std::prev(g_layouts.lru.end())) {
+        g_layouts.index.erase(it);
+        break;
+      }
+    }
     g_layouts.lru.pop_back();
   }
   return L;
@@ -382,7 +422,7 @@ std::tuple<std::vector<Tensor>, Tensor, Tensor, Tensor, Tensor, Tensor> grouped_
     TensorList weights, TensorList ids_in, const c10::List<std::optional<Tensor>>& lengths_in,
     at::IntArrayRef table, at::IntArrayRef pooling, at::IntArrayRef exclude, at::IntArrayRef padding_idx,
     bool need_backward) {
-  validate_weights(weights);
+  TORCH_CHECK_VALUE(!weights.empty(), "a grouped lookup needs at least one table");
   check_features(weights, ids_in, lengths_in, table, pooling, exclude, padding_idx);
   const at::Device dev = weights[0].device();
   const c10::DeviceGuard guard(dev);
@@ -409,7 +449,8 @@ std::tuple<std::vector<Tensor>, Tensor, Tensor, Tensor, Tensor, Tensor> grouped_
   // its id count).
   std::vector<Tensor> flat;
   flat.reserve(F);
-  for (const Tensor& t : ids) flat.push_back(t.reshape({-1}));
+  for (const Tensor& t : ids)
+    flat.push_back(t.is_contiguous() ? raw_view(t, at::kLong, 0, {t.numel()}, {1}) : t.reshape({-1}));
   Tensor all_ids = F == 1 ? flat[0].contiguous() : at::cat(flat).contiguous();
   Tensor ids_arg = n ? all_ids : at::zeros({1}, all_ids.options());
   Tensor offsets;
@@ -441,20 +482,22 @@ std::tuple<std::vector<Tensor>, Tensor, Tensor, Tensor, Tensor, Tensor> grouped_
   }
   std::vector<int64_t> rows_out;
   std::vector<mdl_feature> feats = call_features(*L, n_ids, n_bags, &rows_out);
+  // One tensor per output (a functional op's outputs may not share storage).
   std::vector<Tensor> outputs(F);
   int64_t total_rows = 0;
   for (int f = 0; f < F; ++f) {
     const Tensor& w = weights[L->feats[f].table];
+    const int64_t dim = w.size(1);
     std::vector<int64_t> shape;
     if (L->feats[f].pooling == MDL_POOL_NONE) {
       shape = ids[f].sizes().vec();
-      shape.push_back(w.size(1));
+      shape.push_back(dim);
     } else {
-      shape = {n_bags[f], w.size(1)};
+      shape = {n_bags[f], dim};
     }
     outputs[f] = at::empty(shape, w.options());
     feats[f].out = addr(outputs[f]);
-    feats[f].out_stride = w.size(1);
+    feats[f].out_stride = dim;
     total_rows += rows_out[f];
   }
   const int target = forward_target_ids(n);
@@ -632,7 +675,7 @@ std::tuple<Tensor, Tensor, Tensor> grouped_lookup_backward_cuda(
     at::IntArrayRef table, at::IntArrayRef pooling, at::IntArrayRef exclude, at::IntArrayRef padding_idx,
     TensorList grads_in, const Tensor& keys_in, const Tensor& payload_in, const Tensor& bag_count,
     const Tensor& offsets) {
-  validate_weights(weights);
+  TORCH_CHECK_VALUE(!weights.empty(), "a grouped lookup needs at least one table");
   check_features(weights, ids_in, lengths_in, table, pooling, exclude, padding_idx);
   TORCH_CHECK_VALUE(grads_in.size() == ids_in.size(), "one gradient per feature");
   const at::Device dev = weights[0].device();
@@ -706,7 +749,9 @@ std::optional<std::tuple<Tensor, Tensor, Tensor>> find_capacity_grad(const Tenso
   if (it == g_cap.end() || it->second.param.expired()) return std::nullopt;
   const CapRecord& r = it->second;
   if (!grad.is_sparse()) return std::nullopt;
-  const Tensor idx = grad._indices(), val = grad._values();
+  const auto* sp = at::sparse::get_sparse_impl(grad);
+  const Tensor& idx = sp->indices();
+  const Tensor& val = sp->values();
   if (idx.data_ptr() == r.rows.data_ptr() && val.data_ptr() == r.values.data_ptr() && idx.size(-1) == r.rows.numel() &&
       val.sizes() == r.values.sizes())
     return std::make_tuple(r.rows, r.values, r.count);
@@ -736,8 +781,9 @@ struct MarkCoalesced final : torch::autograd::PostAccumulateGradHook {
     if (it == g_exact.end()) return;
     const ExactRecord r = it->second;
     g_exact.erase(it);
-    if (g.defined() && g.is_sparse() && g._nnz() == r.nnz && (r.nnz == 0 || g._values().data_ptr() == r.values))
-      g._coalesced_(true);
+    if (!g.defined() || !g.is_sparse()) return;
+    auto* sp = at::sparse::get_sparse_impl(g);
+    if (sp->nnz() == r.nnz && (r.nnz == 0 || sp->values().data_ptr() == r.values)) sp->set_coalesced(true);
   }
 };
 
@@ -762,9 +808,18 @@ void note_exact_grad(const Tensor& param, const Tensor& values) {
   if (!hook) torch::autograd::impl::set_post_acc_grad_hooks(param, std::make_unique<MarkCoalesced>());
 }
 
+// A [num_rows, dim] sparse COO tensor (sparse_dim 1, dense_dim 1) over
+// `rows` (as a [1, n] index view) and `values`, built as ATen's own
+// constructors build one but without their dispatcher round trips.
 Tensor sparse_grad(const Tensor& weight, const Tensor& rows, const Tensor& values, bool coalesced) {
-  return at::_sparse_coo_tensor_with_dims_and_tensors(1, 1, weight.sizes(), rows.unsqueeze(0), values,
-                                                      values.options().layout(at::kSparse), coalesced);
+  const auto key = values.is_cuda() ? c10::DispatchKey::SparseCUDA : c10::DispatchKey::SparseCPU;
+  Tensor t = at::detail::make_tensor<at::SparseTensorImpl>(c10::DispatchKeySet(key), values.dtype());
+  auto* impl = at::sparse::get_sparse_impl(t);
+  impl->resize_(1, 1, weight.sizes());
+  const int64_t n = rows.numel();
+  impl->set_indices_and_values_unsafe(raw_view(rows, at::kLong, 0, {1, n}, {n, 1}), values);
+  impl->set_coalesced(coalesced);
+  return t;
 }
 
 // Per-table gradients from the two flat buffers: capacity-sized and recorded
@@ -785,17 +840,14 @@ std::vector<Tensor> weight_grads(TensorList weights, const Tensor& rows_all, con
   drop_dead_records();
   for (int t = 0; t < T; ++t) {
     const Tensor& w = weights[t];
-    const int64_t cap = lay.cap[t];
-    Tensor rows = rows_all.narrow(0, lay.rows_off[t], cap);
-    Tensor vals = vbuf.narrow(0, lay.val_off[t], lay.nbytes[t]).view(w.scalar_type()).view({cap, w.size(1)});
-    if (coalesced) {
-      TORCH_CHECK(u[t] >= 0 && u[t] <= cap, "coalesced row count outside its capacity");
-      out[t] = sparse_grad(w, rows.narrow(0, 0, u[t]), vals.narrow(0, 0, u[t]), true);
-      note_exact_grad(w, out[t]._values());
-    } else {
-      out[t] = sparse_grad(w, rows, vals, false);
-      note_capacity_grad(w, rows, vals, counts.narrow(0, t, 1));
-    }
+    const int64_t dim = w.size(1);
+    const int64_t n = coalesced ? u[t] : lay.cap[t];
+    TORCH_CHECK(n >= 0 && n <= lay.cap[t], "coalesced row count outside its capacity");
+    Tensor rows = raw_view(rows_all, at::kLong, 8 * lay.rows_off[t], {n}, {1});
+    Tensor vals = raw_view(vbuf, w.scalar_type(), lay.val_off[t], {n, dim}, {dim, 1});
+    out[t] = sparse_grad(w, rows, vals, coalesced);
+    if (coalesced) note_exact_grad(w, vals);
+    else note_capacity_grad(w, rows, vals, raw_view(counts, at::kLong, 8 * t, {1}, {1}));
   }
   return out;
 }
@@ -873,52 +925,49 @@ Tensor row_major_aligned(Tensor t) {
   return t;
 }
 
-void grouped_rowwise_adagrad_cuda(TensorList weights, TensorList accumulators, TensorList rows_in,
-                                  TensorList values_in, const c10::List<std::optional<Tensor>>& counts,
-                                  at::ArrayRef<double> lrs, double eps) {
-  const size_t P = weights.size();
-  TORCH_CHECK_VALUE(accumulators.size() == P && rows_in.size() == P && values_in.size() == P && counts.size() == P &&
-                        lrs.size() == P,
-                    "one accumulator, rows, values, count and learning rate per weight");
+// One table's share of a grouped update: rows[:count] (count on the device;
+// undefined: all rows) of `values` into `w` and its accumulator `a`.
+struct UpdateItem {
+  const Tensor* w;
+  const Tensor* a;
+  Tensor rows, values, count;
+  double lr;
+};
+
+void launch_updates(const at::Device& dev, std::vector<UpdateItem>& items, double eps) {
+  const size_t P = items.size();
   if (!P) return;
-  const at::Device dev = weights[0].device();
   const c10::DeviceGuard guard(dev);
-  std::vector<Tensor> keep;
-  keep.reserve(2 * P);
   std::vector<mdl_update> ups(P);
   int64_t units = 0;
   for (size_t i = 0; i < P; ++i) {
-    const Tensor& w = weights[i];
-    const Tensor& a = accumulators[i];
+    UpdateItem& it = items[i];
+    const Tensor& w = *it.w;
+    const Tensor& a = *it.a;
     require_device(w, "weight");
     TORCH_CHECK_VALUE(w.device() == dev, "one device per grouped update");
     TORCH_CHECK_VALUE(w.dim() == 2 && w.stride(1) == 1, "row-wise Adagrad expects 2D weights with contiguous rows");
     TORCH_CHECK_TYPE(a.scalar_type() == at::kFloat && a.is_contiguous(),
                      "row-wise Adagrad accumulator must be a contiguous float32 tensor");
-    Tensor r = rows_in[i];
-    if (r.scalar_type() != at::kLong || !r.is_contiguous()) r = r.to(at::kLong).contiguous();
-    Tensor v = values_in[i];
-    if ((w.scalar_type() == at::kFloat && v.scalar_type() != at::kFloat) ||
-        (v.scalar_type() != at::kFloat && v.scalar_type() != at::kBFloat16))
-      v = v.to(at::kFloat);
-    if (!v.is_contiguous() || addr(v) % 16) v = row_major_aligned(v);
-    keep.push_back(r);
-    keep.push_back(v);
+    if (it.rows.scalar_type() != at::kLong || !it.rows.is_contiguous()) it.rows = it.rows.to(at::kLong).contiguous();
+    const auto vt = it.values.scalar_type();
+    if ((w.scalar_type() == at::kFloat && vt != at::kFloat) || (vt != at::kFloat && vt != at::kBFloat16))
+      it.values = it.values.to(at::kFloat);
+    if (!it.values.is_contiguous() || addr(it.values) % 16) it.values = row_major_aligned(it.values);
     mdl_update& u = ups[i];
     u.weight = addr(w);
     u.state = addr(a);
-    u.rows = addr(r);
-    u.values = addr(v);
-    const std::optional<Tensor> c = counts.get(i);
-    u.count = c.has_value() && c->defined() ? addr(*c) : 0;
+    u.rows = addr(it.rows);
+    u.values = addr(it.values);
+    u.count = it.count.defined() ? addr(it.count) : 0;
     u.num_rows = w.size(0);
     u.dim = (int32_t)w.size(1);
-    u.capacity = r.numel();
+    u.capacity = it.rows.numel();
     u.weight_stride = w.stride(0);
-    u.values_stride = v.dim() == 2 && v.size(0) ? v.stride(0) : w.size(1);
+    u.values_stride = it.values.dim() == 2 && it.values.size(0) ? it.values.stride(0) : w.size(1);
     u.wdtype = dtype_code(w.scalar_type());
-    u.vdtype = dtype_code(v.scalar_type());
-    u.lr = (float)lrs[i];
+    u.vdtype = dtype_code(it.values.scalar_type());
+    u.lr = (float)it.lr;
     u.unit_first = units;
     units += (u.capacity + MDL_UPDATE_UNIT - 1) / MDL_UPDATE_UNIT;
   }
@@ -927,6 +976,23 @@ void grouped_rowwise_adagrad_cuda(TensorList weights, TensorList accumulators, T
   check(mdl_grouped_rowwise_adagrad(reinterpret_cast<const mdl_update*>(dev_ups.data_ptr()), ups.data(), (int32_t)P,
                                     (float)eps, nullptr, stream_of(dev)),
         "mdl_grouped_rowwise_adagrad");
+}
+
+void grouped_rowwise_adagrad_cuda(TensorList weights, TensorList accumulators, TensorList rows_in,
+                                  TensorList values_in, const c10::List<std::optional<Tensor>>& counts,
+                                  at::ArrayRef<double> lrs, double eps) {
+  const size_t P = weights.size();
+  TORCH_CHECK_VALUE(accumulators.size() == P && rows_in.size() == P && values_in.size() == P && counts.size() == P &&
+                        lrs.size() == P,
+                    "one accumulator, rows, values, count and learning rate per weight");
+  if (!P) return;
+  std::vector<UpdateItem> items(P);
+  for (size_t i = 0; i < P; ++i) {
+    const std::optional<Tensor> c = counts.get(i);
+    items[i] = UpdateItem{&weights[i], &accumulators[i], rows_in[i], values_in[i],
+                          c.has_value() && c->defined() ? *c : Tensor(), lrs[i]};
+  }
+  launch_updates(weights[0].device(), items, eps);
 }
 
 void rowwise_adagrad_cuda(const Tensor& weight, const Tensor& accumulator, const Tensor& rows_in,
@@ -1102,72 +1168,65 @@ void rowwise_adagrad_step(TensorList params, TensorList sums, TensorList steps,
   const size_t P = params.size();
   TORCH_CHECK_VALUE(sums.size() == P && steps.size() == P && grads.size() == P,
                     "one accumulator, step count and gradient per parameter");
-  struct Item {
+  std::vector<std::pair<at::Device, std::vector<UpdateItem>>> batches;
+  struct HostItem {
     size_t i;
-    Tensor rows, values, count;
+    Tensor grad;
     double lr;
   };
-  std::vector<std::pair<at::Device, std::vector<Item>>> batches;
-  std::vector<Item> host_items;
+  std::vector<HostItem> host_items;
+  std::unique_lock<std::mutex> lock(g_cap_mu);
   for (size_t i = 0; i < P; ++i) {
     const std::optional<Tensor> og = grads.get(i);
     if (!og.has_value() || !og->defined()) continue;  // skipped before the step count, as the reference does
     const Tensor& grad = *og;
     TORCH_CHECK(grad.is_sparse() && grad.layout() == at::kSparse,
                 "ShardedRowWiseAdagrad expects one-dimensional row-sparse COO gradients");
-    TORCH_CHECK(grad.sparse_dim() == 1 && grad.dense_dim() == 1,
+    const auto* sp = at::sparse::get_sparse_impl(grad);
+    TORCH_CHECK(sp->sparse_dim() == 1 && sp->dense_dim() == 1,
                 "ShardedRowWiseAdagrad expects one sparse row dimension and one dense dimension");
     const Tensor& step = steps[i];
     TORCH_CHECK(step.device().is_cpu() && step.scalar_type() == at::kDouble && step.numel() == 1,
                 "ShardedRowWiseAdagrad step counts are 0-d float64 CPU tensors");
-    double* sp = step.data_ptr<double>();
-    const double k = *sp + 1.0;
-    *sp = k;
+    double* stp = step.data_ptr<double>();
+    const double k = *stp + 1.0;
+    *stp = k;
     const double clr = lr_decay == 0.0 ? lr : lr / (1.0 + (k - 1.0) * lr_decay);
     const Tensor& p = params[i];
-    if (p.is_cuda()) {
-      Item it{i, Tensor(), Tensor(), Tensor(), clr};
-      std::optional<std::tuple<Tensor, Tensor, Tensor>> rec;
-      {
-        std::lock_guard<std::mutex> lock(g_cap_mu);
-        rec = find_capacity_grad(p, grad);
-      }
-      if (rec) {
-        std::tie(it.rows, it.values, it.count) = *rec;
-      } else if (grad.is_coalesced()) {
-        it.rows = grad._indices()[0];
-        it.values = grad._values();
-      } else {
-        std::tie(it.rows, it.values, it.count) = sparse_coalesce_padded_cuda(grad._indices()[0], grad._values(), p.size(0));
-      }
-      auto b = std::find_if(batches.begin(), batches.end(), [&](const auto& e) { return e.first == p.device(); });
-      if (b == batches.end()) {
-        batches.emplace_back(p.device(), std::vector<Item>());
-        b = batches.end() - 1;
-      }
-      b->second.push_back(std::move(it));
+    if (!p.is_cuda()) {
+      host_items.push_back(HostItem{i, grad, clr});
+      continue;
+    }
+    UpdateItem it{&p, &sums[i], Tensor(), Tensor(), Tensor(), clr};
+    auto rec = find_capacity_grad(p, grad);
+    if (rec) {
+      std::tie(it.rows, it.values, it.count) = *rec;
+      g_cap.erase(p.unsafeGetTensorImpl());
     } else {
-      Tensor g = grad.coalesce();
-      host_items.push_back(Item{i, g._indices()[0], g._values(), Tensor(), clr});
+      const Tensor& idx = sp->indices();
+      const int64_t nnz = sp->nnz();
+      Tensor rows = raw_view(idx, at::kLong, 0, {nnz}, {idx.stride(1)});
+      if (sp->coalesced()) {
+        it.rows = rows;
+        it.values = sp->values();
+      } else {
+        std::tie(it.rows, it.values, it.count) = sparse_coalesce_padded_cuda(rows, sp->values(), p.size(0));
+      }
     }
-  }
-  for (auto& [dev, items] : batches) {
-    std::vector<Tensor> w, a, r, v;
-    c10::List<std::optional<Tensor>> c;
-    std::vector<double> lrs;
-    for (const Item& it : items) {
-      w.push_back(params[it.i]);
-      a.push_back(sums[it.i]);
-      r.push_back(it.rows);
-      v.push_back(it.values);
-      c.push_back(it.count.defined() ? std::optional<Tensor>(it.count) : std::nullopt);
-      lrs.push_back(it.lr);
+    auto b = std::find_if(batches.begin(), batches.end(), [&](const auto& e) { return e.first == p.device(); });
+    if (b == batches.end()) {
+      batches.emplace_back(p.device(), std::vector<UpdateItem>());
+      b = batches.end() - 1;
+      b->second.reserve(P);
     }
-    grouped_rowwise_adagrad_cuda(w, a, r, v, c, lrs, eps);
-    std::lock_guard<std::mutex> lock(g_cap_mu);
-    for (const Item& it : items) g_cap.erase(params[it.i].unsafeGetTensorImpl());
+    b->second.push_back(std::move(it));
   }
-  for (const Item& it : host_items) cpu_branch(params[it.i], sums[it.i], it.rows, it.values, it.lr, eps);
+  lock.unlock();
+  for (auto& [dev, items] : batches) launch_updates(dev, items, eps);
+  for (const HostItem& h : host_items) {
+    Tensor g = h.grad.coalesce();
+    cpu_branch(params[h.i], sums[h.i], g._indices()[0], g._values(), h.lr, eps);
+  }
 }
 
 // ------------------------------------------------------------- bucketing --

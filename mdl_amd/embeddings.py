@@ -413,16 +413,20 @@ class _GroupedLookup(torch.autograd.Function):
 
     @staticmethod
     def forward(ctx, spec, ids, lengths, *weights):
+        weights = list(weights)
         outputs, keys, payload, bag_count, offsets, err = torch.ops.mdl_hip.grouped_lookup(
-            list(weights), ids, lengths, *spec, True)
-        library._lookup_setup(ctx, (list(weights), ids, lengths, *spec, True),
-                              (outputs, keys, payload, bag_count, offsets, err))
+            weights, ids, lengths, *spec, True)
+        # Inputs and the forward's bookkeeping kept as they are: none of them
+        # is an output of this node, so no reference cycle; the hundreds of
+        # tables and id tensors skip the saved-tensor packing.
+        ctx.lookup = (weights, ids, lengths, spec, (keys, payload, bag_count, offsets))
         ctx.mark_non_differentiable(err)
         return (*outputs, err)
 
     @staticmethod
     def backward(ctx, *grad_outputs):
-        weight_grads = library._lookup_backward(ctx, list(grad_outputs[:-1]))[0]
+        weights, ids, lengths, spec, aux = ctx.lookup
+        weight_grads = library.lookup_weight_grads(weights, ids, lengths, spec, aux, grad_outputs[:-1])
         return (None, None, None, *weight_grads)
 
 

@@ -431,41 +431,48 @@ def _lookup_setup(ctx, inputs, output):
     ctx.spec = (list(table), list(pooling), list(exclude), list(padding_idx))
 
 
-def _lookup_backward(ctx, grad_outputs, *_unused):
-    saved = ctx.saved_tensors
-    weights = list(saved[: ctx.nw])
-    ids = list(saved[ctx.nw: ctx.nw + ctx.nf])
-    keys, payload, bag_count, offsets = saved[ctx.nw + ctx.nf:]
-    table, pooling, exclude, padding_idx = ctx.spec
+def lookup_weight_grads(weights, ids, lengths, spec, aux, grad_outputs) -> list[Tensor]:
+    """Sparse gradients of every table of a grouped lookup from the upstream
+    gradients of its outputs (None: zeros).  ``spec`` is (table, pooling,
+    exclude, padding_idx) and ``aux`` the forward's (keys, payload,
+    bag_count, offsets)."""
+
+    keys, payload, bag_count, offsets = aux
+    table, pooling, exclude, padding_idx = spec
     grads = list(grad_outputs)
     for f, g in enumerate(grads):
         if g is None:
             w = weights[table[f]]
-            rows_f = int(ctx.lengths[f].numel()) if pooling[f] != 0 else int(ids[f].numel())
+            rows_f = int(lengths[f].numel()) if pooling[f] != 0 else int(ids[f].numel())
             grads[f] = torch.zeros((rows_f, int(w.size(1))), dtype=w.dtype, device=w.device)
     # Row-strided gradients (column slices of one [B, sum(D)] gradient, as a
     # concatenation of the outputs hands back) are read in place.
     if _eager(keys):
         # the sparse gradients of every table from one call
-        wgrads = torch.ops.mdl_hip.grouped_lookup_weight_grads(
-            weights, ids, ctx.lengths, table, pooling, exclude, padding_idx, grads, keys, payload, bag_count,
+        return list(torch.ops.mdl_hip.grouped_lookup_weight_grads(
+            weights, ids, lengths, table, pooling, exclude, padding_idx, grads, keys, payload, bag_count,
             offsets, _grad_mode == "coalesced",
-        )
-    else:
-        # traced (fake or functional tensors): the public op and capacity-sized
-        # COO tensors, which need no data
-        rows_all, vbuf, counts = torch.ops.mdl_hip.grouped_lookup_backward(
-            weights, ids, ctx.lengths, table, pooling, exclude, padding_idx, grads, keys, payload, bag_count,
-            offsets,
-        )
-        rows, values = ops.split_coalesced(weights, rows_all, vbuf,
-                                           ops.coalesced_layout(weights, _capacities(weights, ids, table)))
-        wgrads = [torch.sparse_coo_tensor(r.unsqueeze(0), v, tuple(w.shape), is_coalesced=False)
-                  for w, r, v in zip(weights, rows, values)]
+        ))
+    # traced (fake or functional tensors): the public op and capacity-sized
+    # COO tensors, which need no data
+    rows_all, vbuf, counts = torch.ops.mdl_hip.grouped_lookup_backward(
+        weights, ids, lengths, table, pooling, exclude, padding_idx, grads, keys, payload, bag_count, offsets,
+    )
+    rows, values = ops.split_coalesced(weights, rows_all, vbuf,
+                                       ops.coalesced_layout(weights, _capacities(weights, ids, table)))
+    return [torch.sparse_coo_tensor(r.unsqueeze(0), v, tuple(w.shape), is_coalesced=False)
+            for w, r, v in zip(weights, rows, values)]
+
+
+def _lookup_backward(ctx, grad_outputs, *_unused):
+    saved = ctx.saved_tensors
+    weights = list(saved[: ctx.nw])
+    ids = list(saved[ctx.nw: ctx.nw + ctx.nf])
+    wgrads = lookup_weight_grads(weights, ids, ctx.lengths, ctx.spec, saved[ctx.nw + ctx.nf:], grad_outputs)
     # Same structure as the inputs: a list of tensors gets a list back; a
     # list holding a None (unpooled features' lengths) is one leaf.
     lengths_grad = [None] * ctx.nf if all(ln is not None for ln in ctx.lengths) else None
-    return list(wgrads), [None] * ctx.nf, lengths_grad, None, None, None, None, None
+    return wgrads, [None] * ctx.nf, lengths_grad, None, None, None, None, None
 
 
 torch.library.register_autograd("mdl_hip::grouped_lookup", _lookup_backward, setup_context=_lookup_setup)
