@@ -61,18 +61,14 @@ def _clip_sparse_grad_norm(
     sharded_parameters: list[nn.Parameter],
     max_norm: float,
 ) -> Tensor:
-    """Clip one logical sparse group to ``max_norm``; returns the pre-clip norm."""
+    """Clip one logical sparse group to ``max_norm``; returns the pre-clip norm.
 
-    replicated_grads = _gradient_values(replicated_parameters)
-    sharded_grads = _gradient_values(sharded_parameters)
-    all_grads = [*replicated_grads, *sharded_grads]
-    parameter = next(
-        (item for item in [*replicated_parameters, *sharded_parameters] if item.device is not None),
-        None,
-    )
-    if parameter is None:
-        return torch.tensor(0.0)
-    device = parameter.device
+    One ``mdl_hip::clip_sparse_grad_norm_`` call: the C++ extension takes
+    every parameter's gradient values (coalescing and storing back a sparse
+    gradient that is neither coalesced nor the lookup's capacity-sized one),
+    sums their squares per list, forms min(max_norm / (norm + 1e-6), 1) and
+    scales every gradient in place, all on the device."""
+
     if (
         sharded_parameters
         and torch_dist.is_available()
@@ -80,13 +76,8 @@ def _clip_sparse_grad_norm(
         and torch_dist.get_world_size() > 1
     ):
         raise NotImplementedError("sparse clipping across ranks is outside this single-GPU build")
-    squared = torch.cat(
-        [
-            ops.grad_sumsq([g.detach() for g in replicated_grads], device),
-            ops.grad_sumsq([g.detach() for g in sharded_grads], device),
-        ]
-    )
-    total_norm, coef = ops.clip_coefficient(squared, max_norm)
-    if all_grads:
-        ops.scale_(all_grads, coef)
-    return total_norm.reshape(())
+    params = [p for p in [*replicated_parameters, *sharded_parameters] if p.device is not None]
+    if not params:
+        return torch.tensor(0.0)
+    return torch.ops.mdl_hip.clip_sparse_grad_norm_(list(replicated_parameters), list(sharded_parameters),
+                                                    float(max_norm))

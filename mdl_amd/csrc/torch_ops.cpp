@@ -1229,6 +1229,95 @@ void rowwise_adagrad_step(TensorList params, TensorList sums, TensorList steps,
   }
 }
 
+// ------------------------------------------------------------------ clip --
+//
+// The trainer's sparse clip (src/train.py:5730-5826) over parameter lists in
+// one call: every gradient's values -- a capacity-sized gradient's values as
+// they are (its padding rows hold zeros), a coalesced one's as they are,
+// any other sparse gradient coalesced exactly (one host read) and stored
+// back as the parameter's gradient, a dense gradient as it is -- then one
+// multi-tensor sum of squares per list, min(max_norm / (norm + 1e-6), 1) on
+// the device and one multi-tensor scale of every gradient in its own dtype.
+// Returns the pre-clip norm (0-d fp32 on the device).
+
+std::vector<Tensor> clip_values(TensorList params) {
+  std::vector<Tensor> out;
+  out.reserve(params.size());
+  for (const Tensor& p : params) {
+    const Tensor& g = p.grad();
+    if (!g.defined()) continue;
+    require_device(g, "gradient");
+    if (!g.is_sparse()) {
+      out.push_back(g);
+      continue;
+    }
+    std::optional<std::tuple<Tensor, Tensor, Tensor>> rec;
+    {
+      std::lock_guard<std::mutex> lock(g_cap_mu);
+      rec = find_capacity_grad(p, g);
+    }
+    const auto* sp = at::sparse::get_sparse_impl(g);
+    if (rec) {
+      out.push_back(std::get<1>(*rec));
+    } else if (sp->coalesced()) {
+      out.push_back(sp->values());
+    } else {
+      const Tensor& idx = sp->indices();
+      Tensor rows = raw_view(idx, at::kLong, 0, {sp->nnz()}, {idx.stride(1)});
+      auto [urows, vals] = sparse_coalesce_cuda(rows, sp->values(), p.size(0));
+      p.mutable_grad() = sparse_grad(p, urows, vals, true);
+      out.push_back(vals);
+    }
+  }
+  return out;
+}
+
+std::vector<mdl_span> spans_of(const std::vector<Tensor>& ts) {
+  std::vector<mdl_span> spans;
+  spans.reserve(ts.size());
+  for (const Tensor& t : ts) {
+    if (!t.numel()) continue;
+    TORCH_CHECK_VALUE(t.is_contiguous(), "gradients to clip must be contiguous");
+    mdl_span sp{};
+    sp.data = addr(t);
+    sp.numel = t.numel();
+    sp.dtype = dtype_code(t.scalar_type());
+    spans.push_back(sp);
+  }
+  return spans;
+}
+
+Tensor clip_sparse_grad_norm_(TensorList replicated, TensorList sharded, double max_norm) {
+  const Tensor* first = nullptr;
+  for (TensorList l : {replicated, sharded})
+    if (!first && !l.empty()) first = &l[0];
+  if (!first) return at::zeros({}, at::TensorOptions().dtype(at::kFloat));
+  const at::Device dev = first->device();
+  require_device(*first, "parameter");
+  const c10::DeviceGuard guard(dev);
+  void* s = stream_of(dev);
+  const std::vector<Tensor> rv = clip_values(replicated), sv = clip_values(sharded);
+  const std::vector<mdl_span> rs = spans_of(rv), ss = spans_of(sv);
+  // one upload: both lists' spans
+  std::vector<mdl_span> all(rs);
+  all.insert(all.end(), ss.begin(), ss.end());
+  Tensor spans_dev = upload_vec(all, dev);
+  const auto* sd = reinterpret_cast<const mdl_span*>(spans_dev.data_ptr());
+  auto f32 = at::TensorOptions().dtype(at::kFloat).device(dev);
+  Tensor sumsq = at::empty({2}, f32), norm = at::empty({1}, f32), coef = at::empty({1}, f32);
+  const size_t wsb = mdl_sumsq_workspace_bytes((int32_t)std::max(rs.size(), ss.size()));
+  Tensor ws = workspace(wsb, dev);
+  check(mdl_sumsq(rs.empty() ? nullptr : sd, (int32_t)rs.size(), sumsq.data_ptr<float>(), ws.data_ptr(), wsb, s),
+        "mdl_sumsq");
+  check(mdl_sumsq(ss.empty() ? nullptr : sd + rs.size(), (int32_t)ss.size(), sumsq.data_ptr<float>() + 1,
+                  ws.data_ptr(), wsb, s),
+        "mdl_sumsq");
+  check(mdl_clip_coef(sumsq.data_ptr<float>(), 2, (float)max_norm, norm.data_ptr<float>(), coef.data_ptr<float>(), s),
+        "mdl_clip_coef");
+  if (!all.empty()) check(mdl_scale(sd, (int32_t)all.size(), coef.data_ptr<float>(), s), "mdl_scale");
+  return norm.reshape({});
+}
+
 // ------------------------------------------------------------- bucketing --
 
 std::tuple<Tensor, Tensor> bucketize_cuda(const Tensor& raw_in, const std::optional<Tensor>& valid_in,
@@ -1563,6 +1652,10 @@ TORCH_LIBRARY(mdl_hip, m) {
         &backward_sumsq_);
   m.def("clip_coefficient_(Tensor sumsq, int count, float max_norm, Tensor(a!) total_norm, Tensor(b!) coef) -> ()",
         &clip_coefficient_);
+  // The trainer's sparse clip over parameter lists (their gradients scaled
+  // in place, some coalesced and stored back).
+  m.def("clip_sparse_grad_norm_(Tensor(a!)[] replicated, Tensor(b!)[] sharded, float max_norm) -> Tensor",
+        &clip_sparse_grad_norm_);
 }
 
 TORCH_LIBRARY_IMPL(mdl_hip, CUDA, m) {
