@@ -21,9 +21,12 @@
 #include <ATen/native/SparseTensorUtils.h>
 #include <ATen/core/dispatch/Dispatcher.h>
 #include <c10/core/DeviceGuard.h>
+#include <c10/core/impl/DeviceGuardImplInterface.h>
 #include <c10/hip/HIPStream.h>
 #include <c10/util/intrusive_ptr.h>
+#include <torch/csrc/autograd/function.h>
 #include <torch/csrc/autograd/function_hook.h>
+#include <torch/csrc/autograd/graph_task.h>
 #include <torch/csrc/autograd/variable.h>
 #include <torch/library.h>
 
@@ -822,20 +825,56 @@ Tensor sparse_grad(const Tensor& weight, const Tensor& rows, const Tensor& value
   return t;
 }
 
+// Autograd's AccumulateGrad stores a parameter's first sparse gradient as a
+// new COO tensor around the same indices and values (torch's
+// accumulate_grad.h, "Case 1.2"): a dispatcher call and a tensor per table,
+// the largest host cost left in a training step over hundreds of tables.
+// The backward stores such a first gradient on the parameter itself, and
+// hands autograd none for it, only where nothing can tell the two apart:
+// grad mode off (no create_graph) in a backward() that runs every
+// accumulator (not autograd.grad or backward(inputs=...), which select or
+// capture gradients), a leaf that has no gradient yet, no hook of any kind
+// on the leaf or its accumulator (the library's own post-accumulate hook
+// aside), and an accumulator that runs on the current stream, so the
+// gradient is ready where AccumulateGrad would have put it.  Anything else
+// takes autograd's path.
+bool plain_backward() {
+  if (at::GradMode::is_enabled()) return false;
+  const auto* info = torch::autograd::get_current_graph_task_exec_info();
+  return info != nullptr && info->empty();
+}
+
+bool stores_first_grad(const Tensor& w) {
+  if (!w.is_leaf() || !w.requires_grad() || w.grad().defined()) return false;
+  std::shared_ptr<torch::autograd::Node> acc = torch::autograd::impl::try_get_grad_accumulator(w);
+  if (!acc || !acc->pre_hooks().empty() || !acc->post_hooks().empty() || !acc->tensor_pre_hooks().empty() ||
+      !acc->retains_grad_hooks().empty())
+    return false;
+  const auto& post = torch::autograd::impl::post_acc_grad_hooks(w);
+  if (post && !dynamic_cast<const MarkCoalesced*>(post.get())) return false;
+  // the current stream as autograd records streams (a ROCm stream under the
+  // CUDA device type, which HIPStream::unwrap does not give)
+  std::optional<c10::Stream> current;
+  if (!w.is_cpu()) current = c10::impl::getDeviceGuardImpl(w.device().type())->getStream(w.device());
+  return acc->stream() == current;
+}
+
 // Per-table gradients from the two flat buffers: capacity-sized and recorded
 // (no host read), or -- `coalesced` -- cut to their row counts after one
 // batched read of the counts and marked coalesced, so coalesce() returns them
-// as they are (src/optim.py:321-324, src/train.py:5730-5742).
-std::vector<Tensor> weight_grads(TensorList weights, const Tensor& rows_all, const Tensor& vbuf, const Tensor& counts,
-                                 const CoalescedLayout& lay, bool coalesced) {
+// as they are (src/optim.py:321-324, src/train.py:5730-5742).  A gradient
+// stored on its parameter (stores_first_grad) comes back undefined.
+std::vector<std::optional<Tensor>> weight_grads(TensorList weights, const Tensor& rows_all, const Tensor& vbuf,
+                                                const Tensor& counts, const CoalescedLayout& lay, bool coalesced) {
   const int T = (int)weights.size();
-  std::vector<Tensor> out(T);
+  std::vector<std::optional<Tensor>> out(T);
   std::vector<int64_t> u(T, 0);
   if (coalesced) {
     Tensor host = counts.to(at::kCPU);
     const int64_t* h = host.data_ptr<int64_t>();
     for (int t = 0; t < T; ++t) u[t] = h[t];
   }
+  const bool plain = plain_backward();
   std::lock_guard<std::mutex> lock(g_cap_mu);
   drop_dead_records();
   for (int t = 0; t < T; ++t) {
@@ -845,9 +884,15 @@ std::vector<Tensor> weight_grads(TensorList weights, const Tensor& rows_all, con
     TORCH_CHECK(n >= 0 && n <= lay.cap[t], "coalesced row count outside its capacity");
     Tensor rows = raw_view(rows_all, at::kLong, 8 * lay.rows_off[t], {n}, {1});
     Tensor vals = raw_view(vbuf, w.scalar_type(), lay.val_off[t], {n, dim}, {dim, 1});
-    out[t] = sparse_grad(w, rows, vals, coalesced);
+    Tensor g = sparse_grad(w, rows, vals, coalesced);
+    if (!coalesced) note_capacity_grad(w, rows, vals, raw_view(counts, at::kLong, 8 * t, {1}, {1}));
+    if (plain && stores_first_grad(w)) {
+      w.mutable_grad() = g;
+      g_exact.erase(w.unsafeGetTensorImpl());
+      continue;
+    }
     if (coalesced) note_exact_grad(w, vals);
-    else note_capacity_grad(w, rows, vals, raw_view(counts, at::kLong, 8 * t, {1}, {1}));
+    out[t] = std::move(g);
   }
   return out;
 }
@@ -860,7 +905,7 @@ std::vector<int64_t> table_capacities(int T, TensorList ids, at::IntArrayRef tab
 
 // The lookup's backward as the modules' autograd runs it: coalesced
 // gradients of every table, as sparse COO tensors.
-std::vector<Tensor> grouped_lookup_weight_grads(TensorList weights, TensorList ids,
+std::vector<std::optional<Tensor>> grouped_lookup_weight_grads(TensorList weights, TensorList ids,
                                                 const c10::List<std::optional<Tensor>>& lengths, at::IntArrayRef table,
                                                 at::IntArrayRef pooling, at::IntArrayRef exclude,
                                                 at::IntArrayRef padding_idx, TensorList grads, const Tensor& keys,
@@ -915,6 +960,12 @@ std::vector<Tensor> capacity_grad_record(const Tensor& param, const Tensor& grad
 void forget_capacity_grad(const Tensor& param) {
   std::lock_guard<std::mutex> lock(g_cap_mu);
   g_cap.erase(param.unsafeGetTensorImpl());
+}
+
+// optimizer.zero_grad(set_to_none=True) in one call: each parameter's
+// gradient reset, as assigning None to .grad does.
+void clear_grads_(TensorList params) {
+  for (const Tensor& p : params) p.mutable_grad().reset();
 }
 
 // ------------------------------------------------------------- row-wise Adagrad --
@@ -1617,13 +1668,14 @@ TORCH_LIBRARY(mdl_hip, m) {
   // (registered for every backend; CPU tensors take the reference's CPU paths).
   m.def("grouped_lookup_weight_grads(Tensor[] weights, Tensor[] ids, Tensor?[] lengths, int[] table, "
         "int[] pooling, int[] exclude, int[] padding_idx, Tensor[] grads, Tensor keys, Tensor payload, "
-        "Tensor bag_count, Tensor offsets, bool coalesced) -> Tensor[]",
+        "Tensor bag_count, Tensor offsets, bool coalesced) -> Tensor?[]",
         &grouped_lookup_weight_grads);
   m.def("capacity_sparse_grad(Tensor weight, Tensor rows, Tensor values, Tensor count, bool coalesced) -> Tensor",
         &capacity_sparse_grad);
   m.def("capacity_grad_record(Tensor param, Tensor grad) -> Tensor[]", &capacity_grad_record);
   m.def("lookup_order(Tensor[] weights, int[] table) -> int[]", &lookup_order);
   m.def("forget_capacity_grad(Tensor param) -> ()", &forget_capacity_grad);
+  m.def("clear_grads_(Tensor[] params) -> ()", &clear_grads_);
   m.def("rowwise_adagrad_step_(Tensor(a!)[] params, Tensor(b!)[] sums, Tensor(c!)[] steps, Tensor?[] grads, "
         "float lr, float lr_decay, float eps) -> ()",
         &rowwise_adagrad_step);

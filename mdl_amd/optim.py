@@ -152,6 +152,17 @@ class ShardedRowWiseAdagrad(torch.optim.Optimizer):
                 if isinstance(step, Tensor):
                     state["step"] = step.to(device="cpu", dtype=torch.float64)
 
+    def zero_grad(self, set_to_none: bool = True) -> None:
+        """``torch.optim.Optimizer.zero_grad``; with ``set_to_none`` (the
+        trainer's call, src/train.py:6955,7005) one call of the extension per
+        parameter group resets every gradient."""
+
+        if not set_to_none:
+            super().zero_grad(set_to_none=False)
+            return
+        for group in self.param_groups:
+            torch.ops.mdl_hip.clear_grads_(group["params"])
+
     @torch.no_grad()
     def step(self, closure: Callable[[], Tensor] | None = None) -> Tensor | None:
         loss = None

@@ -290,6 +290,98 @@ def test_capacity_gradient_is_a_valid_coo_of_the_coalesced_sum(capacity_grads):
     assert c.indices()[0].tolist() == [3, 7, 9]
 
 
+def _dense_grad(rows, dim, x, ln, g, mode):
+    r, v = O.per_id_grads(x, ln, g.double().numpy(), mode, "exclude")
+    dense = np.zeros((rows, dim))
+    np.add.at(dense, r, v)
+    return torch.from_numpy(dense).float()
+
+
+@pytest.mark.parametrize("device", ["cpu", pytest.param("cuda", marks=pytest.mark.gpu)])
+@pytest.mark.parametrize("grad_mode", ["coalesced", "capacity"])
+def test_gradients_reach_parameters_as_autograd_delivers_them(grad_mode, device):
+    """The backward stores a first gradient on its parameter itself only
+    where autograd's AccumulateGrad would store the same tensor unobserved;
+    hooks, autograd.grad, backward(inputs=...), a second backward and a
+    table used by two lookups all see what autograd gives them."""
+
+    mode = mdl_amd.library.sparse_grad_mode()
+    mdl_amd.library.set_sparse_grad_mode(grad_mode)
+    try:
+        rng = np.random.default_rng(5)
+        a, b, c = (m.to(device) for m in _modules([("a", 40, 4), ("b", 30, 8), ("c", 25, 4)]))
+        B = 6
+        la = rng.integers(0, 5, size=B)
+        xa = rng.integers(0, 40, size=int(la.sum()))
+        xb = rng.integers(0, 30, size=B)
+        xc1 = rng.integers(0, 25, size=B)
+        xc2 = rng.integers(0, 25, size=B)
+        ga, gb, gc1, gc2 = (torch.randn(B, d) for d in (4, 8, 4, 4))
+
+        def t(x):
+            return torch.from_numpy(x).to(device)
+
+        want = {
+            "a": _dense_grad(40, 4, xa, la, ga, "sum"),
+            "b": _dense_grad(30, 8, xb, None, gb, "none"),
+            "c": _dense_grad(25, 4, xc1, la * 0 + 1, gc1, "sum") + _dense_grad(25, 4, xc2, None, gc2, "none"),
+        }
+
+        def run():
+            pooled = pooled_embedding_lookup([(a, t(xa), t(la), "sum", "exclude"),
+                                              (c, t(xc1), t(np.ones(B, np.int64)), "sum", "exclude")])
+            single = grouped_sharded_embedding_lookup([(b, t(xb)), (c, t(xc2))])
+            return ((pooled[0].cpu() * ga).sum() + (pooled[1].cpu() * gc1).sum() + (single[0].cpu() * gb).sum()
+                    + (single[1].cpu() * gc2).sum())
+
+        mods = {"a": a, "b": b, "c": c}
+
+        def check(name, grad, scale=1.0):
+            assert grad is not None and grad.is_sparse and grad.device.type == device
+            torch.testing.assert_close(grad.to_dense().cpu(), want[name] * scale)
+            if grad_mode == "coalesced" and name != "c" and scale == 1.0:
+                assert grad.is_coalesced() and grad.coalesce() is grad
+
+        # plain backward: every table gets its gradient (c: summed over its two
+        # lookups), the first ones stored without AccumulateGrad's re-wrap
+        with torch.profiler.profile(activities=[torch.profiler.ProfilerActivity.CPU]) as prof:
+            run().backward()
+        names = [e.name for e in prof.events()]
+        assert names.count("aten::_sparse_coo_tensor_unsafe") == 0
+        for k, m in mods.items():
+            check(k, m.weight.grad)
+        # a second backward accumulates into the existing gradients
+        run().backward()
+        for k, m in mods.items():
+            check(k, m.weight.grad.coalesce(), 2.0)
+        # torch.autograd.grad returns the gradients and leaves .grad alone
+        for m in mods.values():
+            m.weight.grad = None
+        got = torch.autograd.grad(run(), [m.weight for m in mods.values()])
+        for (k, m), g in zip(mods.items(), got):
+            check(k, g.coalesce())
+            assert m.weight.grad is None
+        # backward(inputs=...) fills only the named parameter
+        run().backward(inputs=[b.weight])
+        check("b", b.weight.grad)
+        assert a.weight.grad is None and c.weight.grad is None
+        b.weight.grad = None
+        # a tensor hook sees the gradient, a post-accumulate hook runs after it lands
+        seen, landed = [], []
+        h1 = a.weight.register_hook(lambda g: seen.append(g))
+        h2 = b.weight.register_post_accumulate_grad_hook(lambda p: landed.append(p.grad))
+        run().backward()
+        assert len(seen) == 1 and len(landed) == 1
+        check("a", seen[0].coalesce())
+        check("a", a.weight.grad)
+        check("b", landed[0].coalesce())
+        assert landed[0] is b.weight.grad
+        h1.remove()
+        h2.remove()
+    finally:
+        mdl_amd.library.set_sparse_grad_mode(mode)
+
+
 def test_cpu_fused_rowwise_adagrad_update_public_function():
     """``fused_rowwise_adagrad_update`` on CPU tensors (the op's CPU kernel,
     the reference's CPU update rule src/optim.py:359-376) on the golden case of
