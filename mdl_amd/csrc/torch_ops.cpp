@@ -17,6 +17,7 @@
 // with its fused update (:68-108).
 
 #include <ATen/ATen.h>
+#include <ATen/core/LegacyTypeDispatch.h>
 #include <ATen/SparseTensorImpl.h>
 #include <ATen/native/SparseTensorUtils.h>
 #include <ATen/core/dispatch/Dispatcher.h>
@@ -539,6 +540,23 @@ std::tuple<std::vector<Tensor>, Tensor, Tensor, Tensor, Tensor, Tensor> grouped_
   return {outputs, keys, payload, bag_count, offsets, err};
 }
 
+// The modules' forward: mdl_hip::grouped_lookup called below the autograd
+// keys, for callers that record the autograd graph themselves (the modules
+// keep one node per call over the tables).  Through the op's own autograd
+// registration, a Python wrapper that flattens every list argument, a call
+// of 150 features cost about 0.2 ms more.
+std::tuple<std::vector<Tensor>, Tensor, Tensor, Tensor, Tensor, Tensor> grouped_lookup_untracked(
+    TensorList weights, TensorList ids, const c10::List<std::optional<Tensor>>& lengths, at::IntArrayRef table,
+    at::IntArrayRef pooling, at::IntArrayRef exclude, at::IntArrayRef padding_idx, bool need_backward) {
+  static auto op = c10::Dispatcher::singleton()
+                       .findSchemaOrThrow("mdl_hip::grouped_lookup", "")
+                       .typed<std::tuple<std::vector<Tensor>, Tensor, Tensor, Tensor, Tensor, Tensor>(
+                           TensorList, TensorList, const c10::List<std::optional<Tensor>>&, at::IntArrayRef,
+                           at::IntArrayRef, at::IntArrayRef, at::IntArrayRef, bool)>();
+  at::AutoDispatchBelowAutograd below;
+  return op.call(weights, ids, lengths, table, pooling, exclude, padding_idx, need_backward);
+}
+
 // --------------------------------------------------- coalesced gradients --
 //
 // Capacity-sized coalesced gradients of every table in two flat buffers:
@@ -593,9 +611,16 @@ struct CoalesceResult {
   CoalescedLayout layout;
 };
 
+// Sort, count and coalesce every key group of a call.  The counting kernels
+// of all groups go first (each group keeps its own workspace, which its
+// coalescing reduce reads), so a caller that needs the row counts on the host
+// (`host_counts`) reads them before the reduces are queued: it waits for the
+// sort and the count only, and builds its tensors while the reduces run.
+// `pad` fills entries [U_t, cap_t) of every table (capacity-sized
+// gradients); exact gradients do not view them.
 CoalesceResult coalesce_groups(const Layout& L, std::vector<mdl_feature>& feats, const Tensor& keys,
                                const Tensor& payload, const Tensor& bag_count, const std::vector<int64_t>& cap,
-                               const at::Device& dev) {
+                               const at::Device& dev, bool pad = true, std::vector<int64_t>* host_counts = nullptr) {
   void* s = stream_of(dev);
   const int T = (int)L.esz.size();
   CoalesceResult r;
@@ -606,10 +631,20 @@ CoalesceResult coalesce_groups(const Layout& L, std::vector<mdl_feature>& feats,
   int64_t n_ranges = 0;
   for (const auto& g : L.groups) n_ranges += 2 * (int64_t)g.tables.size();
   Tensor urange = at::zeros({n_ranges}, at::TensorOptions().dtype(at::kLong).device(dev));
-  Tensor ws;
-  std::vector<Tensor> keep;
-  int64_t u0 = 0;
   const uint64_t rows_base = addr(r.rows_all), vals_base = addr(r.vbuf);
+  struct Launch {
+    const mdl_feature* fd;
+    const mdl_table* td;
+    const int64_t* md;
+    int Tg, nf;
+    int64_t n, units;
+    int64_t* ur;
+    uint32_t *k, *p;
+    Tensor dmeta, ws;
+    uint32_t classes;
+  };
+  std::vector<Launch> launches;
+  int64_t u0 = 0;
   for (const auto& g : L.groups) {
     const int Tg = (int)g.tables.size();
     int64_t* ur = urange.data_ptr<int64_t>() + u0;
@@ -628,7 +663,6 @@ CoalesceResult coalesce_groups(const Layout& L, std::vector<mdl_feature>& feats,
       meta[2 * Tg + j] = c;
       meta[3 * Tg + j + 1] = meta[3 * Tg + j] + (c + 63) / 64;
     }
-    const int64_t units = meta[4 * Tg];
     const size_t fbytes = (size_t)(g.hi - g.lo) * sizeof(mdl_feature);
     const size_t tbytes = (size_t)Tg * sizeof(mdl_table);
     const size_t mbytes = meta.size() * 8;
@@ -636,29 +670,25 @@ CoalesceResult coalesce_groups(const Layout& L, std::vector<mdl_feature>& feats,
     std::memcpy(host.data(), feats.data() + g.lo, fbytes);
     std::memcpy(host.data() + fbytes, g.recs.data(), tbytes);
     std::memcpy(host.data() + fbytes + tbytes, meta.data(), mbytes);
-    Tensor dmeta = upload(host.data(), host.size(), dev);
-    keep.push_back(dmeta);
-    const uint8_t* b = static_cast<const uint8_t*>(dmeta.data_ptr());
-    const auto* fd = reinterpret_cast<const mdl_feature*>(b);
-    const auto* td = reinterpret_cast<const mdl_table*>(b + fbytes);
-    const auto* md = reinterpret_cast<const int64_t*>(b + fbytes + tbytes);
-    const size_t need = mdl_backward_workspace_bytes(n, Tg, L.max_dim);
-    if (!ws.defined() || (size_t)ws.numel() < need) {
-      ws = workspace(need, dev);
-      keep.push_back(ws);
-    }
-    uint32_t* k = reinterpret_cast<uint32_t*>(keys.data_ptr()) + first;
-    uint32_t* p = reinterpret_cast<uint32_t*>(payload.data_ptr()) + first;
-    check(mdl_backward_count(td, Tg, L.max_dim, k, p, n, nullptr, L.key_bits, ur, ws.data_ptr(), (size_t)ws.numel(), s),
+    Launch l;
+    l.dmeta = upload(host.data(), host.size(), dev);
+    const uint8_t* b = static_cast<const uint8_t*>(l.dmeta.data_ptr());
+    l.fd = reinterpret_cast<const mdl_feature*>(b);
+    l.td = reinterpret_cast<const mdl_table*>(b + fbytes);
+    l.md = reinterpret_cast<const int64_t*>(b + fbytes + tbytes);
+    l.Tg = Tg;
+    l.nf = g.hi - g.lo;
+    l.n = n;
+    l.units = meta[4 * Tg];
+    l.ur = ur;
+    l.k = reinterpret_cast<uint32_t*>(keys.data_ptr()) + first;
+    l.p = reinterpret_cast<uint32_t*>(payload.data_ptr()) + first;
+    l.ws = workspace(mdl_backward_workspace_bytes(n, Tg, L.max_dim), dev);
+    l.classes = g.classes;
+    check(mdl_backward_count(l.td, Tg, L.max_dim, l.k, l.p, n, nullptr, L.key_bits, ur, l.ws.data_ptr(),
+                             (size_t)l.ws.numel(), s),
           "mdl_backward_count");
-    check(mdl_backward_coalesce(fd, g.hi - g.lo, td, Tg, L.max_dim, k, p, n, L.key_bits,
-                                bag_count.defined() && bag_count.numel() ? bag_count.data_ptr<float>() : nullptr, ur,
-                                reinterpret_cast<const uint64_t*>(md), reinterpret_cast<const uint64_t*>(md + Tg),
-                                ws.data_ptr(), (size_t)ws.numel(), g.classes, s),
-          "mdl_backward_coalesce");
-    check(mdl_backward_pad(td, Tg, ur, reinterpret_cast<const uint64_t*>(md), reinterpret_cast<const uint64_t*>(md + Tg),
-                           md + 2 * Tg, md + 3 * Tg, units, s),
-          "mdl_backward_pad");
+    launches.push_back(std::move(l));
   }
   Tensor diff = urange.slice(0, 1, n_ranges, 2) - urange.slice(0, 0, n_ranges, 2);
   if (L.groups.size() == 1) {
@@ -670,14 +700,35 @@ CoalesceResult coalesce_groups(const Layout& L, std::vector<mdl_feature>& feats,
     r.counts = at::zeros({T}, urange.options());
     r.counts.index_copy_(0, upload_vec(order, dev).view(at::kLong).narrow(0, 0, (int64_t)order.size()), diff);
   }
+  if (host_counts) {
+    Tensor h = r.counts.to(at::kCPU);
+    host_counts->assign(h.data_ptr<int64_t>(), h.data_ptr<int64_t>() + T);
+  }
+  for (const Launch& l : launches) {
+    check(mdl_backward_coalesce(l.fd, l.nf, l.td, l.Tg, L.max_dim, l.k, l.p, l.n, L.key_bits,
+                                bag_count.defined() && bag_count.numel() ? bag_count.data_ptr<float>() : nullptr, l.ur,
+                                reinterpret_cast<const uint64_t*>(l.md), reinterpret_cast<const uint64_t*>(l.md + l.Tg),
+                                l.ws.data_ptr(), (size_t)l.ws.numel(), l.classes, s),
+          "mdl_backward_coalesce");
+    if (pad)
+      check(mdl_backward_pad(l.td, l.Tg, l.ur, reinterpret_cast<const uint64_t*>(l.md),
+                             reinterpret_cast<const uint64_t*>(l.md + l.Tg), l.md + 2 * l.Tg, l.md + 3 * l.Tg, l.units,
+                             s),
+            "mdl_backward_pad");
+  }
   return r;
 }
 
-std::tuple<Tensor, Tensor, Tensor> grouped_lookup_backward_cuda(
-    TensorList weights, TensorList ids_in, const c10::List<std::optional<Tensor>>& lengths_in,
-    at::IntArrayRef table, at::IntArrayRef pooling, at::IntArrayRef exclude, at::IntArrayRef padding_idx,
-    TensorList grads_in, const Tensor& keys_in, const Tensor& payload_in, const Tensor& bag_count,
-    const Tensor& offsets) {
+// The grouped lookup's backward on the device.  `sort_in_place` sorts the
+// forward's keys and payloads where they are (the modules' own backward: a
+// second backward over a retained graph sorts the sorted pairs again, to the
+// same order); the public op sorts copies and leaves its inputs as they are.
+CoalesceResult lookup_backward(TensorList weights, TensorList ids_in,
+                               const c10::List<std::optional<Tensor>>& lengths_in, at::IntArrayRef table,
+                               at::IntArrayRef pooling, at::IntArrayRef exclude, at::IntArrayRef padding_idx,
+                               TensorList grads_in, const Tensor& keys_in, const Tensor& payload_in,
+                               const Tensor& bag_count, bool sort_in_place, bool pad,
+                               std::vector<int64_t>* host_counts) {
   TORCH_CHECK_VALUE(!weights.empty(), "a grouped lookup needs at least one table");
   check_features(weights, ids_in, lengths_in, table, pooling, exclude, padding_idx);
   TORCH_CHECK_VALUE(grads_in.size() == ids_in.size(), "one gradient per feature");
@@ -697,9 +748,8 @@ std::tuple<Tensor, Tensor, Tensor> grouped_lookup_backward_cuda(
   }
   TORCH_CHECK_VALUE(keys_in.numel() >= n && payload_in.numel() >= n,
                     "sort keys and payloads hold one entry per looked-up id");
-  // The sort works on copies: the op leaves its inputs as they are.
-  Tensor keys = keys_in.clone();
-  Tensor payload = payload_in.clone();
+  Tensor keys = sort_in_place ? keys_in : keys_in.clone();
+  Tensor payload = sort_in_place ? payload_in : payload_in.clone();
   std::vector<int64_t> rows_out;
   std::vector<mdl_feature> feats = call_features(*L, n_ids, n_bags, &rows_out);
   std::vector<Tensor> grads(F);
@@ -710,7 +760,16 @@ std::tuple<Tensor, Tensor, Tensor> grouped_lookup_backward_cuda(
     feats[f].out = addr(grads[f]);
     feats[f].out_stride = grads[f].stride(0);
   }
-  CoalesceResult r = coalesce_groups(*L, feats, keys, payload, bag_count, cap, dev);
+  return coalesce_groups(*L, feats, keys, payload, bag_count, cap, dev, pad, host_counts);
+}
+
+std::tuple<Tensor, Tensor, Tensor> grouped_lookup_backward_cuda(
+    TensorList weights, TensorList ids_in, const c10::List<std::optional<Tensor>>& lengths_in,
+    at::IntArrayRef table, at::IntArrayRef pooling, at::IntArrayRef exclude, at::IntArrayRef padding_idx,
+    TensorList grads_in, const Tensor& keys_in, const Tensor& payload_in, const Tensor& bag_count,
+    const Tensor& offsets) {
+  CoalesceResult r = lookup_backward(weights, ids_in, lengths_in, table, pooling, exclude, padding_idx, grads_in,
+                                     keys_in, payload_in, bag_count, false, true, nullptr);
   return {r.rows_all, r.vbuf, r.counts};
 }
 
@@ -865,11 +924,14 @@ bool stores_first_grad(const Tensor& w) {
 // as they are (src/optim.py:321-324, src/train.py:5730-5742).  A gradient
 // stored on its parameter (stores_first_grad) comes back undefined.
 std::vector<std::optional<Tensor>> weight_grads(TensorList weights, const Tensor& rows_all, const Tensor& vbuf,
-                                                const Tensor& counts, const CoalescedLayout& lay, bool coalesced) {
+                                                const Tensor& counts, const CoalescedLayout& lay, bool coalesced,
+                                                const std::vector<int64_t>* host_counts = nullptr) {
   const int T = (int)weights.size();
   std::vector<std::optional<Tensor>> out(T);
   std::vector<int64_t> u(T, 0);
-  if (coalesced) {
+  if (coalesced && host_counts) {
+    u = *host_counts;
+  } else if (coalesced) {
     Tensor host = counts.to(at::kCPU);
     const int64_t* h = host.data_ptr<int64_t>();
     for (int t = 0; t < T; ++t) u[t] = h[t];
@@ -911,8 +973,17 @@ std::vector<std::optional<Tensor>> grouped_lookup_weight_grads(TensorList weight
                                                 at::IntArrayRef padding_idx, TensorList grads, const Tensor& keys,
                                                 const Tensor& payload, const Tensor& bag_count, const Tensor& offsets,
                                                 bool coalesced) {
-  // through the dispatcher: ROCm tables take the kernels above, CPU tables
-  // the reference's CPU path registered on the same schema
+  if (!weights.empty() && weights[0].is_cuda()) {
+    // ROCm tables: the backward above, called directly (the sort in place,
+    // no padding for exact gradients, their counts read before the
+    // coalescing reduce is queued)
+    std::vector<int64_t> host_counts;
+    CoalesceResult r = lookup_backward(weights, ids, lengths, table, pooling, exclude, padding_idx, grads, keys,
+                                       payload, bag_count, true, !coalesced, coalesced ? &host_counts : nullptr);
+    return weight_grads(weights, r.rows_all, r.vbuf, r.counts, r.layout, coalesced,
+                        coalesced ? &host_counts : nullptr);
+  }
+  // CPU tables: the reference's CPU path registered on the same schema
   static auto op =
       c10::Dispatcher::singleton()
           .findSchemaOrThrow("mdl_hip::grouped_lookup_backward", "")
@@ -1651,6 +1722,9 @@ TORCH_LIBRARY(mdl_hip, m) {
   m.def("lengths_to_offsets(Tensor lengths) -> Tensor");
   m.def("grouped_lookup(Tensor[] weights, Tensor[] ids, Tensor?[] lengths, int[] table, int[] pooling, "
         "int[] exclude, int[] padding_idx, bool need_backward) -> (Tensor[], Tensor, Tensor, Tensor, Tensor, Tensor)");
+  m.def("grouped_lookup_untracked(Tensor[] weights, Tensor[] ids, Tensor?[] lengths, int[] table, int[] pooling, "
+        "int[] exclude, int[] padding_idx, bool need_backward) -> (Tensor[], Tensor, Tensor, Tensor, Tensor, Tensor)",
+        &grouped_lookup_untracked);
   m.def("grouped_lookup_backward(Tensor[] weights, Tensor[] ids, Tensor?[] lengths, int[] table, int[] pooling, "
         "int[] exclude, int[] padding_idx, Tensor[] grads, Tensor keys, Tensor payload, Tensor bag_count, "
         "Tensor offsets) -> (Tensor, Tensor, Tensor)");

@@ -398,23 +398,26 @@ def _grouped_lookup(
     if need_backward:
         *outputs, err = _GroupedLookup.apply(spec, ids, list(lengths), *weights)
     else:
-        outputs, _, _, _, _, err = torch.ops.mdl_hip.grouped_lookup(weights, ids, list(lengths), *spec, False)
+        outputs, _, _, _, _, err = torch.ops.mdl_hip.grouped_lookup_untracked(weights, ids, list(lengths), *spec,
+                                                                              False)
     _check_ids(modules, ids, err)
     return list(outputs)
 
 
 class _GroupedLookup(torch.autograd.Function):
-    """``mdl_hip::grouped_lookup`` with its registered backward
-    (``library._lookup_backward``), as one autograd node whose inputs are the
-    tables themselves.  The op's own autograd registration flattens its list
-    arguments (every id tensor, length and per-feature code) on each call; for
-    the modules' calls over hundreds of features that costs more host time
-    than the rest of the forward (about 0.35 ms per call at 200 features)."""
+    """``mdl_hip::grouped_lookup`` with its backward
+    (``library.lookup_weight_grads``), as one autograd node whose inputs are
+    the tables themselves.  The op's own autograd registration flattens its
+    list arguments (every id tensor, length and per-feature code) on each
+    call; for the modules' calls over hundreds of features that costs more
+    host time than the rest of the forward (about 0.35 ms per call at 200
+    features), so the node calls the op below autograd
+    (``grouped_lookup_untracked``)."""
 
     @staticmethod
     def forward(ctx, spec, ids, lengths, *weights):
         weights = list(weights)
-        outputs, keys, payload, bag_count, offsets, err = torch.ops.mdl_hip.grouped_lookup(
+        outputs, keys, payload, bag_count, offsets, err = torch.ops.mdl_hip.grouped_lookup_untracked(
             weights, ids, lengths, *spec, True)
         # Inputs and the forward's bookkeeping kept as they are: none of them
         # is an output of this node, so no reference cycle; the hundreds of
