@@ -25,6 +25,7 @@
 #include <c10/core/impl/DeviceGuardImplInterface.h>
 #include <c10/hip/HIPStream.h>
 #include <c10/util/intrusive_ptr.h>
+#include <torch/csrc/autograd/custom_function.h>
 #include <torch/csrc/autograd/function.h>
 #include <torch/csrc/autograd/function_hook.h>
 #include <torch/csrc/autograd/graph_task.h>
@@ -32,6 +33,7 @@
 #include <torch/library.h>
 
 #include <algorithm>
+#include <atomic>
 #include <cstring>
 #include <list>
 #include <memory>
@@ -877,7 +879,8 @@ Tensor sparse_grad(const Tensor& weight, const Tensor& rows, const Tensor& value
   const auto key = values.is_cuda() ? c10::DispatchKey::SparseCUDA : c10::DispatchKey::SparseCPU;
   Tensor t = at::detail::make_tensor<at::SparseTensorImpl>(c10::DispatchKeySet(key), values.dtype());
   auto* impl = at::sparse::get_sparse_impl(t);
-  impl->resize_(1, 1, weight.sizes());
+  // sizes and dims only: the indices and values set next fit them
+  impl->raw_resize_(1, 1, weight.sizes());
   const int64_t n = rows.numel();
   impl->set_indices_and_values_unsafe(raw_view(rows, at::kLong, 0, {1, n}, {n, 1}), values);
   impl->set_coalesced(coalesced);
@@ -1001,6 +1004,90 @@ std::vector<std::optional<Tensor>> grouped_lookup_weight_grads(TensorList weight
   }
   auto lay = coalesced_layout(esz, dims, table_capacities(T, ids, table));
   return weight_grads(weights, rows_all, vbuf, counts, lay, coalesced);
+}
+
+// The sparse-gradient mode of the modules' backward, set from Python
+// (mdl_amd.library.set_sparse_grad_mode): exact coalesced gradients, or
+// capacity-sized ones that need no host read.
+std::atomic<bool> g_exact_grads{true};
+
+void set_exact_sparse_grads(bool exact) { g_exact_grads = exact; }
+
+// The modules' grouped lookup as one autograd node in C++ over the tables
+// (their only differentiable inputs): the forward calls the lookup below
+// autograd, the backward builds every table's sparse gradient with
+// grouped_lookup_weight_grads.  No Python runs in the backward, so autograd's
+// device thread needs no interpreter lock for it, and the node's state is
+// freed without one.
+struct GroupedLookupFn : public torch::autograd::Function<GroupedLookupFn> {
+  static torch::autograd::variable_list forward(torch::autograd::AutogradContext* ctx, TensorList weights,
+                                                const std::vector<Tensor>& ids,
+                                                const c10::List<std::optional<Tensor>>& lengths,
+                                                at::IntArrayRef table, at::IntArrayRef pooling,
+                                                at::IntArrayRef exclude, at::IntArrayRef padding_idx) {
+    auto [outputs, keys, payload, bag_count, offsets, err] =
+        grouped_lookup_untracked(weights, ids, lengths, table, pooling, exclude, padding_idx, true);
+    auto& sd = ctx->saved_data;
+    sd["weights"] = weights;
+    sd["ids"] = ids;
+    sd["lengths"] = lengths;
+    sd["table"] = table;
+    sd["pooling"] = pooling;
+    sd["exclude"] = exclude;
+    sd["padding_idx"] = padding_idx;
+    sd["keys"] = keys;
+    sd["payload"] = payload;
+    sd["bag_count"] = bag_count;
+    sd["offsets"] = offsets;
+    ctx->mark_non_differentiable({err});
+    outputs.push_back(err);
+    return outputs;
+  }
+
+  // One gradient per forward argument: the tables', then none for the ids,
+  // lengths and the four per-feature lists.
+  static torch::autograd::variable_list backward(torch::autograd::AutogradContext* ctx,
+                                                 torch::autograd::variable_list grads) {
+    auto& sd = ctx->saved_data;
+    const std::vector<Tensor> weights = sd["weights"].toTensorVector();
+    const std::vector<Tensor> ids = sd["ids"].toTensorVector();
+    grads.pop_back();  // err
+    const std::vector<std::optional<Tensor>> wg = grouped_lookup_weight_grads(
+        weights, ids, sd["lengths"].toOptionalTensorList(), sd["table"].toIntVector(), sd["pooling"].toIntVector(),
+        sd["exclude"].toIntVector(), sd["padding_idx"].toIntVector(), grads, sd["keys"].toTensor(),
+        sd["payload"].toTensor(), sd["bag_count"].toTensor(), sd["offsets"].toTensor(), g_exact_grads.load());
+    torch::autograd::variable_list out(weights.size() + 6);
+    for (size_t t = 0; t < wg.size(); ++t)
+      if (wg[t]) out[t] = *wg[t];
+    return out;
+  }
+};
+
+// A tensor without data of its own: fake or functional (a tracer's), or meta.
+bool traced(const Tensor& t) {
+  const auto ks = t.key_set();
+  return t.is_meta() || ks.has(c10::DispatchKey::Python) || ks.has(c10::DispatchKey::Functionalize);
+}
+
+std::vector<Tensor> grouped_lookup_autograd(TensorList weights, TensorList ids,
+                                            const c10::List<std::optional<Tensor>>& lengths, at::IntArrayRef table,
+                                            at::IntArrayRef pooling, at::IntArrayRef exclude,
+                                            at::IntArrayRef padding_idx) {
+  TORCH_CHECK_VALUE(!weights.empty() && !ids.empty(), "a grouped lookup needs at least one table and feature");
+  if (traced(weights[0]) || traced(ids[0])) {
+    // tracers take the public op and its registered autograd, which builds
+    // capacity-sized gradients from shapes alone
+    static auto op = c10::Dispatcher::singleton()
+                         .findSchemaOrThrow("mdl_hip::grouped_lookup", "")
+                         .typed<std::tuple<std::vector<Tensor>, Tensor, Tensor, Tensor, Tensor, Tensor>(
+                             TensorList, TensorList, const c10::List<std::optional<Tensor>>&, at::IntArrayRef,
+                             at::IntArrayRef, at::IntArrayRef, at::IntArrayRef, bool)>();
+    auto res = op.call(weights, ids, lengths, table, pooling, exclude, padding_idx, true);
+    std::vector<Tensor> out = std::get<0>(res);
+    out.push_back(std::get<5>(res));
+    return out;
+  }
+  return GroupedLookupFn::apply(weights, ids.vec(), lengths, table, pooling, exclude, padding_idx);
 }
 
 // One parameter's gradient from (rows, values, count): the sequence lookup's.
@@ -1725,6 +1812,10 @@ TORCH_LIBRARY(mdl_hip, m) {
   m.def("grouped_lookup_untracked(Tensor[] weights, Tensor[] ids, Tensor?[] lengths, int[] table, int[] pooling, "
         "int[] exclude, int[] padding_idx, bool need_backward) -> (Tensor[], Tensor, Tensor, Tensor, Tensor, Tensor)",
         &grouped_lookup_untracked);
+  m.def("grouped_lookup_autograd(Tensor[] weights, Tensor[] ids, Tensor?[] lengths, int[] table, int[] pooling, "
+        "int[] exclude, int[] padding_idx) -> Tensor[]",
+        &grouped_lookup_autograd);
+  m.def("set_exact_sparse_grads(bool exact) -> ()", &set_exact_sparse_grads);
   m.def("grouped_lookup_backward(Tensor[] weights, Tensor[] ids, Tensor?[] lengths, int[] table, int[] pooling, "
         "int[] exclude, int[] padding_idx, Tensor[] grads, Tensor keys, Tensor payload, Tensor bag_count, "
         "Tensor offsets) -> (Tensor, Tensor, Tensor)");

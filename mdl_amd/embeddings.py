@@ -383,11 +383,12 @@ def _grouped_lookup(
     index: dict[int, int] = {}
     table = []
     for module in modules:
-        key = id(module.weight)
-        if key not in index:
-            index[key] = len(weights)
-            weights.append(module.weight)
-        table.append(index[key])
+        w = module.weight
+        t = index.get(id(w))
+        if t is None:
+            t = index[id(w)] = len(weights)
+            weights.append(w)
+        table.append(t)
     for policy in null_policies:
         if policy not in ("exclude", "include_as_padding"):
             raise ValueError(f"unsupported categorical bag null policy {policy!r}")
@@ -396,41 +397,14 @@ def _grouped_lookup(
             [int(m.padding_idx) for m in modules])
     ids = list(ids)
     if need_backward:
-        *outputs, err = _GroupedLookup.apply(spec, ids, list(lengths), *weights)
+        # one autograd node in C++ over the tables (no Python in the
+        # backward); tracers get the op's registered autograd instead
+        *outputs, err = torch.ops.mdl_hip.grouped_lookup_autograd(weights, ids, list(lengths), *spec)
     else:
         outputs, _, _, _, _, err = torch.ops.mdl_hip.grouped_lookup_untracked(weights, ids, list(lengths), *spec,
                                                                               False)
     _check_ids(modules, ids, err)
     return list(outputs)
-
-
-class _GroupedLookup(torch.autograd.Function):
-    """``mdl_hip::grouped_lookup`` with its backward
-    (``library.lookup_weight_grads``), as one autograd node whose inputs are
-    the tables themselves.  The op's own autograd registration flattens its
-    list arguments (every id tensor, length and per-feature code) on each
-    call; for the modules' calls over hundreds of features that costs more
-    host time than the rest of the forward (about 0.35 ms per call at 200
-    features), so the node calls the op below autograd
-    (``grouped_lookup_untracked``)."""
-
-    @staticmethod
-    def forward(ctx, spec, ids, lengths, *weights):
-        weights = list(weights)
-        outputs, keys, payload, bag_count, offsets, err = torch.ops.mdl_hip.grouped_lookup_untracked(
-            weights, ids, lengths, *spec, True)
-        # Inputs and the forward's bookkeeping kept as they are: none of them
-        # is an output of this node, so no reference cycle; the hundreds of
-        # tables and id tensors skip the saved-tensor packing.
-        ctx.lookup = (weights, ids, lengths, spec, (keys, payload, bag_count, offsets))
-        ctx.mark_non_differentiable(err)
-        return (*outputs, err)
-
-    @staticmethod
-    def backward(ctx, *grad_outputs):
-        weights, ids, lengths, spec, aux = ctx.lookup
-        weight_grads = library.lookup_weight_grads(weights, ids, lengths, spec, aux, grad_outputs[:-1])
-        return (None, None, None, *weight_grads)
 
 
 # ----------------------------------------------------------------- module --

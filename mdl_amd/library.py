@@ -81,6 +81,8 @@ _GRAD_MODES = ("coalesced", "capacity")
 _grad_mode = os.environ.get("MDL_SPARSE_GRADS", "coalesced")
 if _grad_mode not in _GRAD_MODES:
     raise ValueError(f"MDL_SPARSE_GRADS must be one of {_GRAD_MODES}, got {_grad_mode!r}")
+# the modules' backward in C++ reads the mode from the extension
+torch.ops.mdl_hip.set_exact_sparse_grads(_grad_mode == "coalesced")
 
 
 def set_sparse_grad_mode(mode: str) -> None:
@@ -92,6 +94,7 @@ def set_sparse_grad_mode(mode: str) -> None:
     if mode not in _GRAD_MODES:
         raise ValueError(f"sparse gradient mode must be one of {_GRAD_MODES}")
     _grad_mode = mode
+    torch.ops.mdl_hip.set_exact_sparse_grads(mode == "coalesced")
 
 
 def sparse_grad_mode() -> str:

@@ -382,6 +382,29 @@ def test_gradients_reach_parameters_as_autograd_delivers_them(grad_mode, device)
         mdl_amd.library.set_sparse_grad_mode(mode)
 
 
+def test_modules_compile_with_their_gradients(capacity_grads):
+    """torch.compile (full graph, AOT autograd) traces the modules' lookups:
+    fake tensors take the op's registered autograd, and the compiled step's
+    gradients equal the eager ones."""
+
+    a, b = _modules([("a", 30, 4), ("b", 20, 8)])
+    for m in (a, b):
+        m.validate_indices = False  # the host-side check reads a device count
+
+    def fn(x, y, ln):
+        o = pooled_embedding_lookup([(a, x, ln, "mean", "exclude")])[0]
+        s = grouped_sharded_embedding_lookup([(b, y)])[0]
+        return (o * 2).sum() + (s * 3).sum()
+
+    x, ln, y = torch.tensor([1, 2, 3, 4, 5]), torch.tensor([2, 3]), torch.tensor([3, 3, 7])
+    fn(x, y, ln).backward()
+    want = [m.weight.grad.coalesce().to_dense() for m in (a, b)]
+    a.weight.grad = b.weight.grad = None
+    torch.compile(fn, backend="aot_eager", fullgraph=True)(x, y, ln).backward()
+    for m, w in zip((a, b), want):
+        torch.testing.assert_close(m.weight.grad.coalesce().to_dense(), w)
+
+
 def test_cpu_fused_rowwise_adagrad_update_public_function():
     """``fused_rowwise_adagrad_update`` on CPU tensors (the op's CPU kernel,
     the reference's CPU update rule src/optim.py:359-376) on the golden case of
