@@ -635,20 +635,25 @@ def aux_measurements(torch, dev, wl, n_ids: float, steps: int, device, batches=N
     # reference's modules runs (src/model.py:3782-3890, src/train.py:7060-7188),
     # timed under the sync debug mode that raises on any host synchronisation
     if batches is not None:
-        out["dropin_step"] = dropin_loop(torch, dev, wl, device, steps=min(steps, 10), mode="capacity")
-        out["dropin_step_clipped"] = dropin_loop(torch, dev, wl, device, steps=min(steps, 10), mode="capacity",
-                                                 clip_norm=1.0)
-        out["dropin_step_coalesced"] = dropin_loop(torch, dev, wl, device, steps=min(steps, 10), mode="coalesced")
+        k = min(steps, 20)
+        out["dropin_step"] = dropin_loop(torch, dev, wl, device, steps=k, mode="capacity")
+        out["dropin_step_clipped"] = dropin_loop(torch, dev, wl, device, steps=k, mode="capacity", clip_norm=1.0)
+        out["dropin_step_coalesced"] = dropin_loop(torch, dev, wl, device, steps=k, mode="coalesced")
+        out["dropin_step_single_thread_autograd"] = dropin_loop(torch, dev, wl, device, steps=k, mode="capacity",
+                                                                autograd_threads=False)
     return out
 
 
 def dropin_loop(torch, dev, wl, device, steps: int = 10, mode: str = "capacity",
-                clip_norm: float | None = None) -> dict:
+                clip_norm: float | None = None, autograd_threads: bool = True) -> dict:
     """The modules' training loop over the bench's tables, in one of the
     sparse-gradient modes: "capacity" (no host read; timed under the sync
     debug mode that raises on any), "coalesced" (exact coalesced gradients,
     one batched read of the row counts per backward).  ``clip_norm`` adds the
-    trainer's sparse clip through ``mdl_amd.clip`` between backward and step."""
+    trainer's sparse clip through ``mdl_amd.clip`` between backward and step.
+    ``autograd_threads=False`` runs the loop under
+    ``torch.autograd.set_multithreading_enabled(False)``: the backward on the
+    calling thread instead of autograd's device thread."""
 
     from torch import nn
 
@@ -709,6 +714,8 @@ def dropin_loop(torch, dev, wl, device, steps: int = 10, mode: str = "capacity",
             _clip_sparse_grad_norm([], weights, clip_norm)
         opt.step()
 
+    threads = torch.autograd.set_multithreading_enabled(autograd_threads)
+    threads.__enter__()
     try:
         for i in range(2):
             one(i)
@@ -733,6 +740,7 @@ def dropin_loop(torch, dev, wl, device, steps: int = 10, mode: str = "capacity",
             torch.cuda.synchronize()
             ms = (time.perf_counter() - t0) * 1e3 / steps
     finally:
+        threads.__exit__(None, None, None)
         L.set_sparse_grad_mode(prev_mode)
     grads_what = ("capacity-sized coalesced sparse grads (no host read)" if mode == "capacity" else
                   "exact coalesced sparse grads (is_coalesced, one batched read of the row counts per backward)")
@@ -742,7 +750,9 @@ def dropin_loop(torch, dev, wl, device, steps: int = 10, mode: str = "capacity",
                     f"gradient -> {grads_what}, "
                     + ("mdl_amd.clip._clip_sparse_grad_norm, " if clip_norm is not None else "")
                     + "ShardedRowWiseAdagrad.step() (one call, one grouped launch)"
-                    + ("; timed steps under torch.cuda.set_sync_debug_mode('error')" if mode == "capacity" else "")}
+                    + ("; timed steps under torch.cuda.set_sync_debug_mode('error')" if mode == "capacity" else "")
+                    + ("" if autograd_threads else
+                       "; under torch.autograd.set_multithreading_enabled(False) (backward on the calling thread)")}
 
 
 # ------------------------------------------------------------ cpu baseline --
