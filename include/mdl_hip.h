@@ -150,7 +150,7 @@ typedef struct mdl_table {
 /* ---------------------------------------------------------------- misc --- */
 
 const char* mdl_last_error(void);
-int32_t mdl_abi_version(void);
+int32_t mdl_abi_version(void);   /* 6 */
 
 /* ------------------------------------------------------------ bucketing --- */
 
@@ -506,13 +506,19 @@ int mdl_backward_pad(const mdl_table* tables, int32_t num_tables, const int64_t*
 
 /* ------------------------------------------------------------ clipping --- */
 
-/* A contiguous gradient tensor (dense, or the values of a coalesced COO). */
+/* A contiguous gradient tensor (dense, or the values of a coalesced COO).
+ * With live_rows set, only the first min(numel, *live_rows * row_elems)
+ * elements count: the live rows of a capacity-sized sparse gradient, whose
+ * row count is known on the device only.  The sum of squares cuts a span
+ * into slices by that live element count, so a capacity-sized gradient and
+ * its exact coalesced counterpart give the same bits. */
 typedef struct mdl_span {
   uint64_t data;          /* device address */
   int64_t numel;
   int32_t dtype;          /* MDL_F32 / MDL_BF16 */
-  int32_t reserved;
-} mdl_span;               /* 24 bytes */
+  int32_t row_elems;      /* elements per row (with live_rows) */
+  const int64_t* live_rows; /* device int64, or NULL: all numel elements */
+} mdl_span;               /* 32 bytes */
 
 /*
  * Sparse gradient clipping of the trainer (_clip_sparse_grad_norm,

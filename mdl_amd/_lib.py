@@ -26,7 +26,7 @@ MDL_FLAG_EXCLUDE_NULL = 1
 MDL_FLAG_ROWS_BY_POSITION = 2
 MDL_FLAG_IDS_FROM_OFFSETS = 4
 MDL_CLASSES_UNSUPPORTED = 0x80000000
-ABI_VERSION = 5
+ABI_VERSION = 6
 MDL_BUCKET_PRE_HASHED = 0
 MDL_BUCKET_MOD = 1
 MDL_BUCKET_NONE = 2
@@ -61,7 +61,8 @@ FEATURE_DTYPE = np.dtype(
     ]
 )
 CHUNK_DTYPE = np.dtype([("feature", "<i4"), ("count", "<i4"), ("first", "<i8")])
-SPAN_DTYPE = np.dtype([("data", "<u8"), ("numel", "<i8"), ("dtype", "<i4"), ("reserved", "<i4")])
+SPAN_DTYPE = np.dtype([("data", "<u8"), ("numel", "<i8"), ("dtype", "<i4"), ("row_elems", "<i4"),
+                       ("live_rows", "<u8")])
 TABLE_DTYPE = np.dtype(
     [
         ("weight", "<u8"),
@@ -96,7 +97,7 @@ MDL_UPDATE_UNIT = 256
 assert UPDATE_DTYPE.itemsize == 96
 assert FEATURE_DTYPE.itemsize == 128
 assert CHUNK_DTYPE.itemsize == 16
-assert SPAN_DTYPE.itemsize == 24
+assert SPAN_DTYPE.itemsize == 32
 assert TABLE_DTYPE.itemsize == 48
 
 _P = ctypes.c_void_p
@@ -186,7 +187,7 @@ def lib() -> ctypes.CDLL:
     if not os.path.exists(path):
         raise RuntimeError(
             f"libmdl_hip.so not found at {path}; build it with "
-            "`python -m mdl_amd.build` (hipcc, gfx950)"
+            "`python mdl_amd/build.py` (hipcc, gfx950)"
         )
     handle = ctypes.CDLL(path)
     for name, (restype, argtypes) in SIGNATURES.items():
@@ -197,7 +198,7 @@ def lib() -> ctypes.CDLL:
     if found != ABI_VERSION:
         raise RuntimeError(
             f"{path} implements C ABI version {found}, this package binds version {ABI_VERSION}; "
-            "rebuild it with `python -m mdl_amd.build`"
+            "rebuild it with `python mdl_amd/build.py`"
         )
     _LIB = handle
     return handle

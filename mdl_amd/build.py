@@ -1,4 +1,6 @@
-"""Build the package's native libraries in-tree (``python -m mdl_amd.build``):
+"""Build the package's native libraries in-tree (``python mdl_amd/build.py``;
+run as a script, so that importing the package, which loads the libraries,
+is not needed to build them):
 
 * ``libmdl_hip.so``: the gfx950 HIP kernels and their C ABI (hipcc,
   ``mdl_amd/csrc/Makefile``);

@@ -25,6 +25,13 @@ __device__ __forceinline__ float block_sum(float v, float* smem) {
   return t;
 }
 
+// The span's element count: all numel, or its live rows' elements.
+__device__ __forceinline__ int64_t span_elems(const mdl_span& s) {
+  if (!s.live_rows) return s.numel;
+  const int64_t live = *s.live_rows * (int64_t)s.row_elems;
+  return live < 0 ? 0 : (live < s.numel ? live : s.numel);
+}
+
 // Elements [lo, hi) of a span, as this block's slice.
 __device__ __forceinline__ void slice_of(int64_t n, int64_t* lo, int64_t* hi) {
   const int64_t per = ((n + kNormParts - 1) / kNormParts + 7) & ~int64_t(7);
@@ -38,7 +45,7 @@ __global__ __launch_bounds__(kNormThreads) void span_sumsq_kernel(const mdl_span
   __shared__ float smem[kNormThreads / kWave];
   const mdl_span s = spans[blockIdx.y];
   int64_t lo, hi;
-  slice_of(s.numel, &lo, &hi);
+  slice_of(span_elems(s), &lo, &hi);
   float acc = 0.f;
   if (s.dtype == MDL_F32) {
     const float* p = reinterpret_cast<const float*>(s.data);
@@ -115,7 +122,7 @@ __global__ __launch_bounds__(kNormThreads) void span_scale_kernel(const mdl_span
                                                                    const float* __restrict__ coef_p) {
   const mdl_span s = spans[blockIdx.y];
   int64_t lo, hi;
-  slice_of(s.numel, &lo, &hi);
+  slice_of(span_elems(s), &lo, &hi);
   const float coef = coef_p[0];
   if (s.dtype == MDL_F32) {
     float* p = reinterpret_cast<float*>(s.data);

@@ -1449,15 +1449,22 @@ void rowwise_adagrad_step(TensorList params, TensorList sums, TensorList steps,
 // the device and one multi-tensor scale of every gradient in its own dtype.
 // Returns the pre-clip norm (0-d fp32 on the device).
 
-std::vector<Tensor> clip_values(TensorList params) {
-  std::vector<Tensor> out;
+// A gradient's values for the clip, and for a capacity-sized gradient the
+// device count of its live rows (the clip then stops at them).
+struct ClipValues {
+  Tensor values;
+  Tensor live_rows;  // undefined: all rows count
+};
+
+std::vector<ClipValues> clip_values(TensorList params) {
+  std::vector<ClipValues> out;
   out.reserve(params.size());
   for (const Tensor& p : params) {
     const Tensor& g = p.grad();
     if (!g.defined()) continue;
     require_device(g, "gradient");
     if (!g.is_sparse()) {
-      out.push_back(g);
+      out.push_back({g, Tensor()});
       continue;
     }
     std::optional<std::tuple<Tensor, Tensor, Tensor>> rec;
@@ -1467,30 +1474,35 @@ std::vector<Tensor> clip_values(TensorList params) {
     }
     const auto* sp = at::sparse::get_sparse_impl(g);
     if (rec) {
-      out.push_back(std::get<1>(*rec));
+      out.push_back({std::get<1>(*rec), std::get<2>(*rec)});
     } else if (sp->coalesced()) {
-      out.push_back(sp->values());
+      out.push_back({sp->values(), Tensor()});
     } else {
       const Tensor& idx = sp->indices();
       Tensor rows = raw_view(idx, at::kLong, 0, {sp->nnz()}, {idx.stride(1)});
       auto [urows, vals] = sparse_coalesce_cuda(rows, sp->values(), p.size(0));
       p.mutable_grad() = sparse_grad(p, urows, vals, true);
-      out.push_back(vals);
+      out.push_back({vals, Tensor()});
     }
   }
   return out;
 }
 
-std::vector<mdl_span> spans_of(const std::vector<Tensor>& ts) {
+std::vector<mdl_span> spans_of(const std::vector<ClipValues>& vs) {
   std::vector<mdl_span> spans;
-  spans.reserve(ts.size());
-  for (const Tensor& t : ts) {
+  spans.reserve(vs.size());
+  for (const ClipValues& v : vs) {
+    const Tensor& t = v.values;
     if (!t.numel()) continue;
     TORCH_CHECK_VALUE(t.is_contiguous(), "gradients to clip must be contiguous");
     mdl_span sp{};
     sp.data = addr(t);
     sp.numel = t.numel();
     sp.dtype = dtype_code(t.scalar_type());
+    if (v.live_rows.defined()) {
+      sp.row_elems = (int32_t)(t.dim() > 1 ? t.size(1) : 1);
+      sp.live_rows = v.live_rows.data_ptr<int64_t>();
+    }
     spans.push_back(sp);
   }
   return spans;
@@ -1505,7 +1517,7 @@ Tensor clip_sparse_grad_norm_(TensorList replicated, TensorList sharded, double 
   require_device(*first, "parameter");
   const c10::DeviceGuard guard(dev);
   void* s = stream_of(dev);
-  const std::vector<Tensor> rv = clip_values(replicated), sv = clip_values(sharded);
+  const std::vector<ClipValues> rv = clip_values(replicated), sv = clip_values(sharded);
   const std::vector<mdl_span> rs = spans_of(rv), ss = spans_of(sv);
   // one upload: both lists' spans
   std::vector<mdl_span> all(rs);

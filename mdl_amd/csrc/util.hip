@@ -263,7 +263,7 @@ extern "C" {
 
 const char* mdl_last_error(void) { return g_last_error.c_str(); }
 
-int32_t mdl_abi_version(void) { return 5; }
+int32_t mdl_abi_version(void) { return 6; }
 
 int mdl_bucketize(const int64_t* raw, const uint8_t* valid, int64_t n, int64_t num_buckets,
                   int32_t mode, int32_t validate_nonzero, int64_t* out, int32_t* error_count,

@@ -69,7 +69,7 @@ def _load() -> None:
     _lib.lib()  # the C ABI and its version check
     if not TORCH_LIB_PATH.exists():
         raise RuntimeError(
-            f"{TORCH_LIB_PATH.name} not found at {TORCH_LIB_PATH}; build it with `python -m mdl_amd.build` "
+            f"{TORCH_LIB_PATH.name} not found at {TORCH_LIB_PATH}; build it with `python mdl_amd/build.py` "
             "(the torch.library extension of the mdl_hip operators)"
         )
     torch.ops.load_library(str(TORCH_LIB_PATH))

@@ -537,3 +537,49 @@ def test_reference_shaped_step_in_both_gradient_modes(device, grad_mode, dtype):
         _check_update(f"{grad_mode} table {t}", m.weight.detach().float().cpu().numpy(),
                       opt.state[m.weight]["sum"].cpu().numpy(), w0, a0, r, v, s * coef, 0.05, 1e-8, rtol,
                       1e-6 if bf16 else 1e-7, bf16, acc_rtol=rtol)
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+def test_clip_gives_the_same_bits_in_both_gradient_modes(device, dtype):
+    """``mdl_amd.clip._clip_sparse_grad_norm`` over capacity-sized gradients
+    stops at each table's live rows (a device count in the span) and cuts the
+    norm's slices by them, so the norm, the clipped gradients and the update
+    equal those of exact coalesced gradients bit for bit."""
+
+    import mdl_amd.library as L
+    from mdl_amd.clip import _clip_sparse_grad_norm
+
+    announce("clip_both_modes", dtype)
+    specs = [("bag", 400, 16), ("single", 900, 8), ("wide", 300, 130)]
+    rng = np.random.default_rng(7)
+    B = 96
+    lb = rng.integers(0, 9, size=B)
+    xb = torch.from_numpy(rng.zipf(1.2, size=int(lb.sum())) % 400).to(device)
+    xs = torch.from_numpy(rng.integers(0, 900, size=B)).to(device)
+    xw = torch.from_numpy(rng.zipf(1.3, size=B) % 300).to(device)
+    lb = torch.from_numpy(lb).to(device)
+    g = torch.from_numpy(rng.standard_normal((B, 16 + 8 + 130)).astype(np.float32)).to(device, dtype)
+    results = {}
+    prev = L.sparse_grad_mode()
+    try:
+        for mode in ("coalesced", "capacity"):
+            L.set_sparse_grad_mode(mode)
+            torch.manual_seed(3)
+            mods = _modules(device, specs)
+            for m in mods:
+                m.weight.data = m.weight.data.to(dtype)
+            opt = ShardedRowWiseAdagrad([m.weight for m in mods], lr=0.05, eps=1e-8)
+            pooled = pooled_embedding_lookup([(mods[0], xb, lb, "mean", "exclude")])
+            singles = grouped_sharded_embedding_lookup([(mods[1], xs), (mods[2], xw)])
+            torch.cat([pooled[0], *singles], dim=1).backward(g)
+            for max_norm in (1e9, 0.25):  # no clipping, then clipping
+                norm = _clip_sparse_grad_norm([], [m.weight for m in mods], max_norm)
+            opt.step()
+            results[mode] = (norm.cpu(), [m.weight.detach().cpu() for m in mods],
+                             [opt.state[m.weight]["sum"].cpu() for m in mods])
+    finally:
+        L.set_sparse_grad_mode(prev)
+    (n0, w0, a0), (n1, w1, a1) = results["coalesced"], results["capacity"]
+    assert torch.equal(n0, n1)
+    for x, y in zip(w0 + a0, w1 + a1):
+        assert torch.equal(x, y)
