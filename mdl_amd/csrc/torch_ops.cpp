@@ -453,11 +453,26 @@ std::tuple<std::vector<Tensor>, Tensor, Tensor, Tensor, Tensor, Tensor> grouped_
   // Every feature's ids back to back; the offsets of all features from one
   // scan of the concatenated lengths (an unpooled feature's pseudo-length is
   // its id count).
-  std::vector<Tensor> flat;
-  flat.reserve(F);
-  for (const Tensor& t : ids)
-    flat.push_back(t.is_contiguous() ? raw_view(t, at::kLong, 0, {t.numel()}, {1}) : t.reshape({-1}));
-  Tensor all_ids = F == 1 ? flat[0].contiguous() : at::cat(flat).contiguous();
+  // Id tensors that lie back to back in one buffer (a packed loader batch)
+  // are used where they are; others are concatenated.
+  bool packed = true;
+  for (int f = 0; f < F && packed; ++f) {
+    const Tensor& t = ids[f];
+    packed = t.is_contiguous() && t.scalar_type() == at::kLong &&
+             (f == 0 || (t.numel() == 0 && n_ids[f] == 0) ||
+              (ids[f - 1].storage().is_alias_of(t.storage()) &&
+               addr(t) == addr(ids[f - 1]) + 8 * (uint64_t)n_ids[f - 1]));
+  }
+  Tensor all_ids;
+  if (packed) {
+    all_ids = raw_view(ids[0], at::kLong, 0, {n}, {1});
+  } else {
+    std::vector<Tensor> flat;
+    flat.reserve(F);
+    for (const Tensor& t : ids)
+      flat.push_back(t.is_contiguous() ? raw_view(t, at::kLong, 0, {t.numel()}, {1}) : t.reshape({-1}));
+    all_ids = F == 1 ? flat[0].contiguous() : at::cat(flat).contiguous();
+  }
   Tensor ids_arg = n ? all_ids : at::zeros({1}, all_ids.options());
   Tensor offsets;
   if (L->pooled_any) {

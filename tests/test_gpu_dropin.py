@@ -583,3 +583,29 @@ def test_clip_gives_the_same_bits_in_both_gradient_modes(device, dtype):
     assert torch.equal(n0, n1)
     for x, y in zip(w0 + a0, w1 + a1):
         assert torch.equal(x, y)
+
+
+def test_packed_and_separate_ids_look_up_the_same(device):
+    """Id tensors that lie back to back in one buffer are read in place (no
+    concatenation); separate tensors are concatenated.  Both give the same
+    outputs and gradients, bit for bit."""
+
+    announce("packed_ids")
+    specs = [("a", 500, 16), ("b", 300, 8), ("c", 700, 32)]
+    rng = np.random.default_rng(17)
+    B = 40
+    la = rng.integers(0, 6, size=B)
+    n = [int(la.sum()), B, B]
+    packed = torch.from_numpy(rng.integers(0, 300, size=sum(n))).to(device)
+    parts = torch.split(packed, n)
+    results = []
+    for ids in (parts, [p.clone() for p in parts]):
+        torch.manual_seed(1)
+        mods = _modules(device, specs)
+        pooled = pooled_embedding_lookup([(mods[0], ids[0], torch.from_numpy(la).to(device), "mean", "exclude")])
+        singles = grouped_sharded_embedding_lookup([(mods[1], ids[1]), (mods[2], ids[2])])
+        outs = [pooled[0], *singles]
+        torch.autograd.backward(outs, [torch.ones_like(o) for o in outs])
+        results.append(([o.detach().cpu() for o in outs], [m.weight.grad.coalesce().to_dense().cpu() for m in mods]))
+    for x, y in zip(results[0][0] + results[0][1], results[1][0] + results[1][1]):
+        assert torch.equal(x, y)
