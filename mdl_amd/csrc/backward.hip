@@ -460,8 +460,9 @@ __device__ __forceinline__ void zero(float (&v)[C]) {
 template <int kMode, bool kOne, typename TW, typename TG, int C>
 __device__ __forceinline__ void reduce_chunk_body(const BwdArgs& a, int64_t c, const ChunkDesc& d,
                                                   const Reducer<kMode, TW, TG, C>& R, const ChunkStage& st) {
-  // Entries per slot per iteration: about 32 elements of loads in flight per lane.
-  constexpr int U = unroll_for<C>();
+  // Entries per slot per iteration: about MDL_ELEMS_IN_FLIGHT row elements of
+  // loads in flight per lane (bf16 weight rows: MDL_BF16_ELEMS_IN_FLIGHT).
+  constexpr int U = sizeof(TW) == 2 ? unroll_for<C, MDL_BF16_ELEMS_IN_FLIGHT>() : unroll_for<C>();
   constexpr bool adagrad = kMode == kModeAdagrad;
   constexpr bool coalesce = kMode == kModeCoalesce;
   const uint32_t kNone = 0xffffffffu;
