@@ -22,13 +22,17 @@ constexpr int kSortWaves = kSortThreads / kWave;
 // per CU, else 8 or 4, so a small sort (c0, c4: ~0.5 M keys) still spreads
 // over every CU.  (At c1, 8 M keys, 16 per thread sorts in 0.180 ms, 8 in
 // 0.195, 4 in 0.248: the larger tiles' longer digit runs win once the chip
-// is full.)
+// is full; 32, 8192-key tiles whose 64 KB stage leaves two blocks per CU,
+// in 0.214, its downsweep 37.7 us per pass against 30.3.)
 #ifndef MDL_SORT_MIN_TILES
 #define MDL_SORT_MIN_TILES 512
 #endif
 constexpr int kMinTiles = MDL_SORT_MIN_TILES;
+#ifndef MDL_SORT_MAX_ITEMS
+#define MDL_SORT_MAX_ITEMS 16
+#endif
 static inline int sort_items(int64_t n) {
-  for (int items = 16; items > 4; items >>= 1)
+  for (int items = MDL_SORT_MAX_ITEMS; items > 4; items >>= 1)
     if ((n + kSortThreads * items - 1) / (kSortThreads * items) >= kMinTiles) return items;
   return 4;
 }
@@ -316,6 +320,10 @@ int sort_pairs(uint32_t* keys, uint32_t* vals, uint32_t* keys_alt, uint32_t* val
   int passes = 0;
   for (int shift = 0; shift < key_bits; shift += kDigitBits) {
     const int bits = key_bits - shift < kDigitBits ? key_bits - shift : kDigitBits;
+#if MDL_SORT_MAX_ITEMS >= 32
+    if (items == 32) radix_pass<32>(ki, vi, ko, vo, n, n_dev, shift, bits, counts, digit_total, ntiles, s);
+    else
+#endif
     if (items == 16) radix_pass<16>(ki, vi, ko, vo, n, n_dev, shift, bits, counts, digit_total, ntiles, s);
     else if (items == 8) radix_pass<8>(ki, vi, ko, vo, n, n_dev, shift, bits, counts, digit_total, ntiles, s);
     else radix_pass<4>(ki, vi, ko, vo, n, n_dev, shift, bits, counts, digit_total, ntiles, s);
