@@ -48,7 +48,7 @@ def torch_extension_command(out: Path) -> list[str]:
     cmd += [f"-I{p}" for p in include_paths()] + [f"-I{ROCM / 'include'}"]
     cmd += [str(CSRC / "torch_ops.cpp"), "-o", str(out)]
     cmd += [f"-L{p}" for p in library_paths()] + [f"-L{PKG}"]
-    cmd += ["-ltorch", "-ltorch_cpu", "-lc10", "-lc10_hip", "-lmdl_hip", "-Wl,-rpath,$ORIGIN"]
+    cmd += ["-ltorch", "-ltorch_cpu", "-ltorch_hip", "-lc10", "-lc10_hip", "-lmdl_hip", "-Wl,-rpath,$ORIGIN"]
     cmd += [f"-Wl,-rpath,{p}" for p in library_paths()]
     return cmd
 

@@ -18,6 +18,7 @@
 
 #include <ATen/ATen.h>
 #include <ATen/core/LegacyTypeDispatch.h>
+#include <ATen/hip/EmptyTensor.h>
 #include <ATen/SparseTensorImpl.h>
 #include <ATen/native/SparseTensorUtils.h>
 #include <ATen/core/dispatch/Dispatcher.h>
@@ -516,7 +517,10 @@ std::tuple<std::vector<Tensor>, Tensor, Tensor, Tensor, Tensor, Tensor> grouped_
     } else {
       shape = {n_bags[f], dim};
     }
-    outputs[f] = at::empty(shape, w.options());
+    // every element is written by the lookup: allocated without a dispatcher
+    // round trip per output
+    outputs[f] = w.is_cuda() ? Tensor(at::detail::empty_cuda(shape, w.scalar_type(), dev, std::nullopt))
+                             : at::empty(shape, w.options());
     feats[f].out = addr(outputs[f]);
     feats[f].out_stride = dim;
     total_rows += rows_out[f];
