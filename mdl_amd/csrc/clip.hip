@@ -86,16 +86,31 @@ __global__ __launch_bounds__(kNormThreads) void span_sumsq_kernel(const mdl_span
   if (threadIdx.x == 0) partial[(int64_t)blockIdx.y * kNormParts + blockIdx.x] = t;
 }
 
-// out[0] = sum of m partials, added in a fixed order in fp64.
-__global__ __launch_bounds__(kNormThreads) void sum_partials_kernel(const float* __restrict__ partial, int64_t m,
-                                                                     const int64_t* m_dev, float* out) {
-  __shared__ double smem[kNormThreads];
+// out[0] = sum of m partials, added in a fixed order in fp64: thread t adds
+// partials t, t + kSumThreads, ... in index order (eight loads issued before
+// their additions), then a fixed tree joins the threads.  One block of 1024
+// threads: the per-chunk partials of a c1 backward (17-42 K of them) take
+// about five memory round trips instead of twenty (22.6 us with 256 threads).
+constexpr int kSumThreads = 1024;
+__global__ __launch_bounds__(kSumThreads) void sum_partials_kernel(const float* __restrict__ partial, int64_t m,
+                                                                    const int64_t* m_dev, float* out) {
+  __shared__ double smem[kSumThreads];
   if (m_dev) m = *m_dev;
+  constexpr int kBatch = 8;
   double acc = 0.0;
-  for (int64_t i = threadIdx.x; i < m; i += kNormThreads) acc += (double)partial[i];
+  for (int64_t base = 0; base < m; base += (int64_t)kSumThreads * kBatch) {
+    float v[kBatch];
+#pragma unroll
+    for (int j = 0; j < kBatch; ++j) {
+      const int64_t i = base + (int64_t)j * kSumThreads + threadIdx.x;
+      v[j] = i < m ? partial[i] : 0.f;
+    }
+#pragma unroll
+    for (int j = 0; j < kBatch; ++j) acc += (double)v[j];
+  }
   smem[threadIdx.x] = acc;
   __syncthreads();
-  for (int d = kNormThreads / 2; d >= 1; d >>= 1) {
+  for (int d = kSumThreads / 2; d >= 1; d >>= 1) {
     if (threadIdx.x < d) smem[threadIdx.x] += smem[threadIdx.x + d];
     __syncthreads();
   }
@@ -159,7 +174,7 @@ __global__ __launch_bounds__(kNormThreads) void span_scale_kernel(const mdl_span
 }
 
 int launch_sum_partials(const float* partial, int64_t m, const int64_t* m_dev, float* out, hipStream_t s) {
-  hipLaunchKernelGGL(sum_partials_kernel, dim3(1), dim3(kNormThreads), 0, s, partial, m, m_dev, out);
+  hipLaunchKernelGGL(sum_partials_kernel, dim3(1), dim3(kSumThreads), 0, s, partial, m, m_dev, out);
   MDL_CHECK_LAUNCH("sum_partials_kernel");
   return MDL_OK;
 }
