@@ -1359,53 +1359,6 @@ def grouped_rowwise_adagrad_(
     del keep
 
 
-def coalesce_rows_padded(
-    indices: Tensor, values: Tensor, num_rows: int, *, error_count: Tensor | None = None
-) -> tuple[Tensor, Tensor, Tensor]:
-    """Sort + unique + segment-sum of an uncoalesced COO gradient without a
-    host read: ``(rows [n], summed [n, dim], count)`` where the first
-    ``count`` (device int64 [1]) rows are ascending and unique and the rest
-    repeat the last row with zero values.  Indices outside ``[0, num_rows)``
-    are dropped and counted in ``error_count`` when given."""
-
-    _require_device(values, "values")
-    device = values.device
-    n = int(indices.numel())
-    dim = int(values.size(1))
-    indices = indices.to(torch.int64).contiguous()
-    values = _row_major_aligned(values)
-    plan = GroupPlan()
-    # A stand-in table of the right shape (a stride-0 view of one row): only
-    # its row count, dim and dtype are read, never its rows.
-    stand_in = torch.empty((1, dim), dtype=values.dtype, device=device).expand(int(num_rows), dim)
-    plan.tables.append(TableSpec(weight=stand_in, state=None, row_base=0))
-    plan.total_rows = int(num_rows)
-    plan.features.append(FeatureSpec(table=0, pooling=MDL_POOL_NONE, exclude_null=False, padding_idx=-1,
-                                     out_dtype=values.dtype))
-    keys = torch.empty(max(n, 1), dtype=torch.int32, device=device)
-    payload = torch.empty(max(n, 1), dtype=torch.int32, device=device)
-    err = error_count if error_count is not None else torch.zeros(1, dtype=torch.int32, device=device)
-    if n:
-        check(
-            lib().mdl_sparse_keys(indices.data_ptr(), n, int(num_rows), 0, 0, -1, keys.data_ptr(), payload.data_ptr(),
-                                  plan.sentinel, err.data_ptr(), _stream(device)),
-            "mdl_sparse_keys",
-        )
-    feats = np.zeros(1, dtype=FEATURE_DTYPE)
-    feats[0]["num_rows"] = int(num_rows)
-    feats[0]["num_ids"] = n
-    feats[0]["dim"] = dim
-    feats[0]["wdtype"] = dtype_code(values.dtype)
-    feats[0]["odtype"] = dtype_code(values.dtype)
-    feats[0]["pooling"] = MDL_POOL_NONE
-    feats[0]["padding_idx"] = -1
-    res = ForwardResult(plan=plan, device=device, ids=indices, offsets=None, outputs=[values], feats=feats, keys=keys,
-                        payload=payload, bag_count=None, error_count=err)
-    rows_all, vbuf, counts, layout = backward_coalesce_padded(res, [values])
-    rows, vals = split_coalesced([plan.tables[0].weight], rows_all, vbuf, layout)
-    return rows[0], vals[0], counts
-
-
 def coalesce_rows(
     indices: Tensor, values: Tensor, num_rows: int, *, padding_idx: int = -1
 ) -> tuple[Tensor, Tensor]:

@@ -25,23 +25,6 @@ from torch import Tensor, nn
 from . import embeddings, library
 
 
-def update_rows(parameter: Tensor) -> tuple[Tensor, Tensor, Tensor | None]:
-    """``(rows, values, count)`` of the parameter's sparse gradient for the
-    update, rows unique and ascending in the first ``count`` entries (a device
-    int64; None: all): a gradient the lookup emitted as it is, a coalesced one
-    as it is, any other coalesced locally by ``mdl_hip::sparse_coalesce_padded``
-    (like ``grad = grad.coalesce()`` in src/optim.py:321-324, without the host
-    read that sizes an exact coalesce)."""
-
-    grad = parameter.grad
-    known = library.capacity_grad(parameter, grad)
-    if known is not None:
-        return known
-    if grad.is_coalesced():
-        return grad._indices()[0], grad._values(), None
-    return torch.ops.mdl_hip.sparse_coalesce_padded(grad._indices()[0], grad._values(), int(parameter.shape[0]))
-
-
 def coalesced_grad(parameter: Tensor) -> Tensor:
     """The parameter's sparse gradient with every row's summed value once,
     stored back as ``parameter.grad`` (src/train.py:5730-5742).
