@@ -38,28 +38,38 @@ def _checksum(t: torch.Tensor) -> tuple[int, int]:
 
 class ErrorStats:
     """Observed error against |ref|, per category (e.g. "c1 weights"): the
-    worst relative error |got - ref| / |ref| over elements with ref != 0,
-    how many elements exceed the plain relative tolerance, and the worst
-    ratio of the error to the bound the check applies (<= 1 passes).  The
-    full-size tests print one line per category, so each run records how
+    worst relative error |got - ref| / |ref| over elements with ref != 0, the
+    same over the well-conditioned elements (|ref| at least half the
+    magnitude the bound uses, the sum of |terms| where the check has one: a
+    condition number of at most 2, where fp32 summation's error stays near
+    the unit roundoff times the term count),
+    how many elements of each exceed the plain relative tolerance, and the
+    worst ratio of the error to the bound the check applies (<= 1 passes).
+    The full-size tests print one line per category, so each run records how
     close the results come to the plain 1e-5 / 1e-2 relative figures, beside
     the first-order bounds over |terms| that they are checked against."""
 
     def __init__(self):
         self.cats: dict[str, dict] = {}
 
-    def add(self, what: str, err, ref, bound, rtol: float):
+    def add(self, what: str, err, ref, bound, rtol: float, scale=None):
         cat = " ".join(what.split()[:1] + [w for w in what.split()[1:] if not w.isdigit()][-1:])
-        c = self.cats.setdefault(cat, {"n": 0, "nonzero": 0, "over_rtol": 0, "worst_rel": 0.0,
-                                       "worst_bound_ratio": 0.0, "rtol": rtol})
+        c = self.cats.setdefault(cat, {"n": 0, "nonzero": 0, "over_rtol": 0, "worst_rel": 0.0, "kept": 0,
+                                       "kept_over_rtol": 0, "kept_worst_rel": 0.0, "worst_bound_ratio": 0.0,
+                                       "rtol": rtol})
         mag = np.abs(ref)
         nz = mag > 0
         rel = np.where(nz, err / np.where(nz, mag, 1.0), 0.0)
+        kept = nz & (mag >= 0.5 * (mag if scale is None else scale))
         c["n"] += int(err.size)
         c["nonzero"] += int(nz.sum())
         c["over_rtol"] += int((rel > rtol).sum())
+        c["kept"] += int(kept.sum())
+        c["kept_over_rtol"] += int((kept & (rel > rtol)).sum())
         if err.size:
             c["worst_rel"] = max(c["worst_rel"], float(rel.max()))
+            if kept.any():
+                c["kept_worst_rel"] = max(c["kept_worst_rel"], float(rel[kept].max()))
             c["worst_bound_ratio"] = max(c["worst_bound_ratio"], float((err / bound).max()))
 
     def report(self, prefix: str = ""):
@@ -67,8 +77,9 @@ class ErrorStats:
             if prefix and not cat.startswith(prefix):
                 continue
             say("ERR", cat, f"elements {c['n']}", f"worst |err|/|ref| {c['worst_rel']:.3e}",
-                f"over {c['rtol']:g} relative: {c['over_rtol']} of {c['nonzero']}",
-                f"worst err/bound {c['worst_bound_ratio']:.3f}")
+                f"over {c['rtol']:g} relative: {c['over_rtol']} of {c['nonzero']};",
+                f"well-conditioned: worst {c['kept_worst_rel']:.3e}, over {c['rtol']:g}: {c['kept_over_rtol']} of "
+                f"{c['kept']};", f"worst err/bound {c['worst_bound_ratio']:.3f}")
 
 
 STATS = ErrorStats()
@@ -81,7 +92,7 @@ def assert_close(got, ref, rtol, atol, scale=None, what=""):
     err = np.abs(got - ref)
     mag = np.abs(ref) if scale is None else np.maximum(np.abs(ref), np.asarray(scale, dtype=np.float64))
     bound = atol + rtol * mag
-    STATS.add(what, err, ref, bound, rtol)
+    STATS.add(what, err, ref, bound, rtol, None if scale is None else mag)
     bad = err > bound
     assert not bad.any(), f"{what}: {int(bad.sum())} mismatches, worst excess {float((err - bound).max())}"
 
