@@ -609,3 +609,33 @@ def test_packed_and_separate_ids_look_up_the_same(device):
         results.append(([o.detach().cpu() for o in outs], [m.weight.grad.coalesce().to_dense().cpu() for m in mods]))
     for x, y in zip(results[0][0] + results[0][1], results[1][0] + results[1][1]):
         assert torch.equal(x, y)
+
+
+@pytest.mark.parametrize("grad_mode", ["coalesced", "capacity"])
+def test_backward_over_a_retained_graph_repeats_its_gradient(device, grad_mode):
+    """The modules' backward sorts the forward's keys in place; a second
+    backward over the retained graph sorts the sorted pairs again and gives
+    the same gradient, so the accumulated one is exactly twice the first."""
+
+    import mdl_amd.library as L
+
+    announce("retained_graph", grad_mode)
+    prev = L.sparse_grad_mode()
+    L.set_sparse_grad_mode(grad_mode)
+    try:
+        rng = np.random.default_rng(23)
+        mods = _modules(device, [("bag", 300, 16), ("single", 200, 8)])
+        B = 64
+        lb = rng.integers(0, 7, size=B)
+        xb = torch.from_numpy(rng.zipf(1.2, size=int(lb.sum())) % 300).to(device)
+        xs = torch.from_numpy(rng.zipf(1.2, size=B) % 200).to(device)
+        pooled = pooled_embedding_lookup([(mods[0], xb, torch.from_numpy(lb).to(device), "mean", "exclude")])
+        single = grouped_sharded_embedding_lookup([(mods[1], xs)])
+        g = [torch.randn(B, 16, device=device), torch.randn(B, 8, device=device)]
+        torch.autograd.backward([pooled[0], single[0]], g, retain_graph=True)
+        first = [m.weight.grad.coalesce().to_dense().clone() for m in mods]
+        torch.autograd.backward([pooled[0], single[0]], g)
+        for m, f in zip(mods, first):
+            assert torch.equal(m.weight.grad.coalesce().to_dense(), 2 * f)
+    finally:
+        L.set_sparse_grad_mode(prev)
