@@ -350,9 +350,9 @@ def _raise_for_errors(modules: list["ShardedEmbedding"], ids: list[Tensor], err:
 
 
 def _check_ids(modules: list["ShardedEmbedding"], ids: list[Tensor], err: Tensor) -> None:
-    if not any(m.validate_indices for m in modules):
-        return
     checked = [m for m in modules if m.validate_indices]
+    if not checked:
+        return
     if err.device.type != "cuda":
         _raise_for_errors(modules, ids, err)
         return
@@ -363,7 +363,7 @@ def _check_ids(modules: list["ShardedEmbedding"], ids: list[Tensor], err: Tensor
         _deferred_counter(err.device).add_(err.reshape(-1)[:1])
     else:
         names = ", ".join(repr(m.table_name) for m in checked[:4])
-        torch._assert_async(err.reshape(-1)[0] == 0, f"embedding {names} received an out-of-range ID")
+        torch._assert_async(err == 0, f"embedding {names} received an out-of-range ID")
 
 
 _POOLING_CODES = {"none": 0, "sum": 1, "mean": 2}
@@ -381,20 +381,25 @@ def _grouped_lookup(
 
     weights: list[Tensor] = []
     index: dict[int, int] = {}
-    table = []
-    for module in modules:
+    table, codes, exclude, padding = [], [], [], []
+    # one pass over the requests: each table once, and the per-feature codes
+    for module, pooling, policy in zip(modules, poolings, null_policies):
         w = module.weight
         t = index.get(id(w))
         if t is None:
             t = index[id(w)] = len(weights)
             weights.append(w)
         table.append(t)
-    for policy in null_policies:
-        if policy not in ("exclude", "include_as_padding"):
+        codes.append(_POOLING_CODES[pooling])
+        if policy == "exclude":
+            exclude.append(1)
+        elif policy == "include_as_padding":
+            exclude.append(0)
+        else:
             raise ValueError(f"unsupported categorical bag null policy {policy!r}")
+        padding.append(int(module.padding_idx))
     need_backward = torch.is_grad_enabled() and any(w.requires_grad for w in weights)
-    spec = (table, [_POOLING_CODES[p] for p in poolings], [1 if p == "exclude" else 0 for p in null_policies],
-            [int(m.padding_idx) for m in modules])
+    spec = (table, codes, exclude, padding)
     ids = list(ids)
     if need_backward:
         # one autograd node in C++ over the tables (no Python in the
@@ -527,12 +532,14 @@ def grouped_sharded_embedding_lookup(
         return []
     if max_output_bytes is not None and int(max_output_bytes) <= 0:
         raise ValueError("grouped embedding max output bytes must be positive")
-    modules = [m for m, _ in request_list]
-    ids = [t for _, t in request_list]
+    modules, ids = [], []
     for module, t in request_list:
-        module._require_single_rank()
+        if module.world_size != 1:
+            module._require_single_rank()
         if t.dtype != torch.long:
             raise TypeError("sharded embedding indices must be torch.long")
+        modules.append(module)
+        ids.append(t)
     outputs = _grouped_lookup(
         modules, ids, [None] * len(ids), ["none"] * len(ids), ["include_as_padding"] * len(ids)
     )
@@ -559,7 +566,8 @@ def pooled_embedding_lookup(
     if not request_list:
         return []
     for module, values, lengths, pooling, policy in request_list:
-        module._require_single_rank()
+        if module.world_size != 1:
+            module._require_single_rank()
         if pooling not in ("mean", "sum"):
             raise ValueError("pooled lookups use mean or sum pooling")
         if lengths.ndim != 1:
