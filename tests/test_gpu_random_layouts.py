@@ -164,18 +164,40 @@ def test_random_dropin_training_matches_oracle(device, seed):
     per-id gradients of every request
     (src/model.py:564-570), coalesced per table (src/optim.py:321-324), the
     row-wise update (src/optim.py:31-62); a bf16 table's gradient is stored
-    in bf16 as the reference's is."""
+    in bf16 as the reference's is.  Odd seeds run with capacity-sized
+    gradients, even ones with exact coalesced ones; every third seed
+    accumulates two backward passes before each step
+    (src/train.py:5388-5396), and seeds 1, 5 and 9 clip the gradients
+    through ``mdl_amd.clip._clip_sparse_grad_norm`` first (src/train.py:5788-5826)."""
 
+    import mdl_amd.library as L
+    from mdl_amd.clip import _clip_sparse_grad_norm
     from mdl_amd.embeddings import (EmbeddingTableSpec, ShardedEmbedding, grouped_sharded_embedding_lookup,
                                     plan_embedding_shards, pooled_embedding_lookup)
     from mdl_amd.optim import ShardedRowWiseAdagrad
 
+    grad_mode = "capacity" if seed % 2 else "coalesced"
+    passes = 2 if seed % 3 == 0 else 1
+    clip = 0.5 if seed % 4 == 1 else None
+    prev_mode = L.sparse_grad_mode()
+    L.set_sparse_grad_mode(grad_mode)
+    try:
+        _random_dropin(device, seed, passes, clip, _clip_sparse_grad_norm, EmbeddingTableSpec, ShardedEmbedding,
+                       grouped_sharded_embedding_lookup, plan_embedding_shards, pooled_embedding_lookup,
+                       ShardedRowWiseAdagrad)
+    finally:
+        L.set_sparse_grad_mode(prev_mode)
+
+
+def _random_dropin(device, seed, passes, clip, _clip_sparse_grad_norm, EmbeddingTableSpec, ShardedEmbedding,
+                   grouped_sharded_embedding_lookup, plan_embedding_shards, pooled_embedding_lookup,
+                   ShardedRowWiseAdagrad):
     rng = np.random.default_rng(5000 + seed)
     T = int(rng.integers(3, 8))
     rows = [int(np.exp(rng.uniform(np.log(3), np.log(100_000)))) for _ in range(T)]
     dims = [int(rng.choice(WIDTHS)) for _ in range(T)]
     bf16 = [bool(rng.random() < 0.4) for _ in range(T)]
-    announce("random_dropin", seed, rows, dims, bf16)
+    announce("random_dropin", seed, rows, dims, bf16, passes, clip)
     specs = [(f"t{t}", rows[t], dims[t]) for t in range(T)]
     plan = plan_embedding_shards([EmbeddingTableSpec(n, r, d) for n, r, d in specs], world_size=1,
                                  strategy="row_wise", table_wise_max_rows=32)
@@ -189,36 +211,38 @@ def test_random_dropin_training_matches_oracle(device, seed):
     for step in range(2):
         W = [m.weight.detach().float().cpu().numpy().copy() for m in mods]
         A = [opt.state[m.weight]["sum"].cpu().numpy().copy() for m in mods]
-        pooled_req, single_req, ref_req = [], [], []
-        for _ in range(int(rng.integers(2, 9))):
-            t = int(rng.integers(0, T))
-            if rng.random() < 0.6:
-                ln = rng.integers(0, 9, size=B)
-                x = np.minimum(rng.zipf(1.2, size=int(ln.sum())) - 1, rows[t] - 1)
-                mode = "mean" if rng.random() < 0.5 else "sum"
-                pol = "exclude" if rng.random() < 0.5 else "include_as_padding"
-                pooled_req.append((mods[t], torch.from_numpy(x).to(device), torch.from_numpy(ln).to(device), mode, pol))
-                ref_req.append(("p", t, x, ln, mode, pol))
-            else:
-                x = rng.integers(0, rows[t], size=B)
-                single_req.append((mods[t], torch.from_numpy(x).to(device)))
-                ref_req.append(("s", t, x, None, "none", "exclude"))
         opt.zero_grad(set_to_none=True)
-        outs = (pooled_embedding_lookup(pooled_req) if pooled_req else []) + \
-               (grouped_sharded_embedding_lookup(single_req) if single_req else [])
-        order = [r for r in ref_req if r[0] == "p"] + [r for r in ref_req if r[0] == "s"]
-        grads = [torch.from_numpy(rng.standard_normal(tuple(o.shape)).astype(np.float32)).to(o.dtype).to(device)
-                 for o in outs]
-        torch.autograd.backward(outs, grads)
-        opt.step()
         per_table = {t: ([], [], []) for t in range(T)}
-        for (kind, t, x, ln, mode, pol), g in zip(order, grads):
-            gh = g.float().cpu().numpy()
-            r, v = O.per_id_grads(x, ln, gh, mode, pol)
-            _, va = O.per_id_grads(x, ln, np.abs(gh), mode, pol)
-            per_table[t][0].append(r)
-            per_table[t][1].append(v.reshape(-1, dims[t]))
-            per_table[t][2].append(va.reshape(-1, dims[t]))
+        for _ in range(passes):
+            pooled_req, single_req, ref_req = [], [], []
+            for _ in range(int(rng.integers(2, 9))):
+                t = int(rng.integers(0, T))
+                if rng.random() < 0.6:
+                    ln = rng.integers(0, 9, size=B)
+                    x = np.minimum(rng.zipf(1.2, size=int(ln.sum())) - 1, rows[t] - 1)
+                    mode = "mean" if rng.random() < 0.5 else "sum"
+                    pol = "exclude" if rng.random() < 0.5 else "include_as_padding"
+                    pooled_req.append((mods[t], torch.from_numpy(x).to(device), torch.from_numpy(ln).to(device),
+                                       mode, pol))
+                    ref_req.append(("p", t, x, ln, mode, pol))
+                else:
+                    x = rng.integers(0, rows[t], size=B)
+                    single_req.append((mods[t], torch.from_numpy(x).to(device)))
+                    ref_req.append(("s", t, x, None, "none", "exclude"))
+            outs = (pooled_embedding_lookup(pooled_req) if pooled_req else []) + \
+                   (grouped_sharded_embedding_lookup(single_req) if single_req else [])
+            order = [r for r in ref_req if r[0] == "p"] + [r for r in ref_req if r[0] == "s"]
+            grads = [torch.from_numpy(rng.standard_normal(tuple(o.shape)).astype(np.float32)).to(o.dtype).to(device)
+                     for o in outs]
+            torch.autograd.backward(outs, grads)
+            for (kind, t, x, ln, mode, pol), g in zip(order, grads):
+                gh = g.float().cpu().numpy()
+                r, v = O.per_id_grads(x, ln, gh, mode, pol)
+                _, va = O.per_id_grads(x, ln, np.abs(gh), mode, pol)
+                per_table[t][0].append(r)
+                per_table[t][1].append(v.reshape(-1, dims[t]))
+                per_table[t][2].append(va.reshape(-1, dims[t]))
+        coalesced = {}
         for t in range(T):
             if per_table[t][0]:
                 r, v = O.coalesce(np.concatenate(per_table[t][0]), np.concatenate(per_table[t][1]))
@@ -227,10 +251,23 @@ def test_random_dropin_training_matches_oracle(device, seed):
                 r, v, va = np.zeros(0, np.int64), np.zeros((0, dims[t])), np.zeros((0, dims[t]))
             if bf16[t]:
                 v = torch.from_numpy(v).to(torch.bfloat16).double().numpy()
-            rt = 1e-2 if bf16[t] else 1e-5
+            coalesced[t] = (r, v, va)
+        coef = 1.0
+        if clip is not None:
+            norm = _clip_sparse_grad_norm([], [m.weight for m in mods], clip)
+            _, total, coef = O.clip_grad_norm([coalesced[t][1] for t in range(T)], clip)
+            rt = 1e-2 if any(bf16) else 1e-5
+            assert abs(float(norm) - total) <= rt * total + 1e-6, (float(norm), total)
+        opt.step()
+        for t in range(T):
+            r, v, va = coalesced[t]
+            # a bf16 table's gradient is rounded to bf16 once per backward
+            # pass, and accumulated passes once more when the optimizer
+            # coalesces them: up to three roundings of 2^-9 each
+            rt = (1e-2 if passes == 1 else 2e-2) if bf16[t] else 1e-5
             _check_update(f"step {step} table {t}", mods[t].weight.detach().float().cpu().numpy(),
-                          opt.state[mods[t].weight]["sum"].cpu().numpy(), W[t], A[t], r, v, va, 0.05, 1e-8,
-                          rt, 1e-6 if bf16[t] else 1e-7, bf16[t], acc_rtol=rt)
+                          opt.state[mods[t].weight]["sum"].cpu().numpy(), W[t], A[t], r, v * coef, va * coef,
+                          0.05, 1e-8, rt, 1e-6 if bf16[t] else 1e-7, bf16[t], acc_rtol=rt)
 
 
 @pytest.mark.parametrize("seed", range(12))
