@@ -1023,8 +1023,13 @@ def backward_adagrad(
 # ------------------------------------------------------------- clipping --
 
 
-def _spans(tensors: Sequence[Tensor]) -> tuple[np.ndarray, list[Tensor]]:
+def _spans(tensors: Sequence[Tensor], live_rows: Sequence[Tensor | None] | None = None
+           ) -> tuple[np.ndarray, list[Tensor]]:
+    """Span descriptors of contiguous gradients; ``live_rows[i]`` (a device
+    int64 [1], or None) limits span i to its first rows."""
+
     spans = np.zeros(len(tensors), dtype=_lib.SPAN_DTYPE)
+    keep = list(tensors)
     for i, t in enumerate(tensors):
         _require_device(t, "gradient")
         if not t.is_contiguous():
@@ -1032,15 +1037,24 @@ def _spans(tensors: Sequence[Tensor]) -> tuple[np.ndarray, list[Tensor]]:
         spans[i]["data"] = t.data_ptr()
         spans[i]["numel"] = t.numel()
         spans[i]["dtype"] = dtype_code(t.dtype)
-    return spans, list(tensors)
+        live = live_rows[i] if live_rows is not None else None
+        if live is not None:
+            if live.dtype != torch.int64 or live.device != t.device:
+                raise ValueError("live row counts are int64 tensors on the gradient's device")
+            spans[i]["row_elems"] = int(t[0].numel()) if t.dim() > 1 else 1
+            spans[i]["live_rows"] = live.data_ptr()
+            keep.append(live)
+    return spans, keep
 
 
-def grad_sumsq(tensors: Sequence[Tensor], device: torch.device) -> Tensor:
-    """Sum of squares of every element of every tensor: fp32 [1] on device."""
+def grad_sumsq(tensors: Sequence[Tensor], device: torch.device,
+               live_rows: Sequence[Tensor | None] | None = None) -> Tensor:
+    """Sum of squares of every element of every tensor: fp32 [1] on device
+    (of tensor i's first ``live_rows[i]`` rows only, when given)."""
 
     out = torch.empty(1, dtype=torch.float32, device=device)
-    tensors = [t for t in tensors if t.numel()]
-    spans, _ = _spans(tensors)
+    pairs = [(t, None if live_rows is None else live_rows[i]) for i, t in enumerate(tensors) if t.numel()]
+    spans, _ = _spans([t for t, _ in pairs], [c for _, c in pairs])
     ws = _workspace(lib().mdl_sumsq_workspace_bytes(len(spans)), device)
     spans_dev = upload(spans, device) if len(spans) else None
     check(
@@ -1064,14 +1078,15 @@ def clip_coefficient(sumsq: Tensor, max_norm: float) -> tuple[Tensor, Tensor]:
     return norm, coef
 
 
-def scale_(tensors: Sequence[Tensor], coef: Tensor) -> None:
-    """In-place ``t *= coef`` in each tensor's dtype (coef: device fp32 [1])."""
+def scale_(tensors: Sequence[Tensor], coef: Tensor, live_rows: Sequence[Tensor | None] | None = None) -> None:
+    """In-place ``t *= coef`` in each tensor's dtype (coef: device fp32 [1]);
+    of tensor i's first ``live_rows[i]`` rows only, when given."""
 
-    tensors = [t for t in tensors if t.numel()]
-    if not tensors:
+    pairs = [(t, None if live_rows is None else live_rows[i]) for i, t in enumerate(tensors) if t.numel()]
+    if not pairs:
         return
-    spans, _ = _spans(tensors)
-    device = tensors[0].device
+    spans, _ = _spans([t for t, _ in pairs], [c for _, c in pairs])
+    device = pairs[0][0].device
     spans_dev = upload(spans, device)
     check(lib().mdl_scale(spans_dev.data_ptr(), len(spans), coef.data_ptr(), _stream(device)), "mdl_scale")
 

@@ -184,3 +184,30 @@ def test_fused_clip_step_matches_oracle(device, max_norm):
     st.sort()
     norm2, _ = st.clip(max_norm)
     assert torch.equal(first, norm2)
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+def test_live_row_spans_cover_only_their_live_rows(device, dtype):
+    """A span with a device row count (mdl_span.live_rows, C ABI 6) sums and
+    scales only its first rows, clamped to [0, rows]; its sum of squares has
+    the bits of a span of exactly those rows (the slices follow the live
+    element count), and rows past the count keep their bits."""
+
+    from mdl_amd import ops
+
+    torch.manual_seed(11)
+    rows, dim = 1000, 24
+    x = torch.randn(rows, dim, device=device).to(dtype)
+    for live in (0, 1, 377, rows, rows + 5, -3):
+        count = torch.tensor([live], dtype=torch.int64, device=device)
+        k = min(max(live, 0), rows)
+        got = ops.grad_sumsq([x], device, live_rows=[count])
+        want = ops.grad_sumsq([x[:k].contiguous()], device) if k else torch.zeros(1, device=device)
+        assert torch.equal(got, want), (live, float(got), float(want))
+        y = x.clone()
+        coef = torch.tensor([0.37], dtype=torch.float32, device=device)
+        ops.scale_([y], coef, live_rows=[count])
+        z = x[:k].clone()
+        if k:
+            ops.scale_([z], coef)
+        assert torch.equal(y[:k], z) and torch.equal(y[k:], x[k:]), live
