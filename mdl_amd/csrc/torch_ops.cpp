@@ -989,19 +989,23 @@ std::vector<int64_t> table_capacities(int T, TensorList ids, at::IntArrayRef tab
 
 // The lookup's backward as the modules' autograd runs it: coalesced
 // gradients of every table, as sparse COO tensors.
-std::vector<std::optional<Tensor>> grouped_lookup_weight_grads(TensorList weights, TensorList ids,
-                                                const c10::List<std::optional<Tensor>>& lengths, at::IntArrayRef table,
-                                                at::IntArrayRef pooling, at::IntArrayRef exclude,
-                                                at::IntArrayRef padding_idx, TensorList grads, const Tensor& keys,
-                                                const Tensor& payload, const Tensor& bag_count, const Tensor& offsets,
-                                                bool coalesced) {
+// `sort_in_place`: the keys and payloads are the caller's own (the modules'
+// autograd node keeps them private) and may be sorted where they are; the
+// operator leaves them as they are, as the forward's outputs they are.
+std::vector<std::optional<Tensor>> weight_grads_for(TensorList weights, TensorList ids,
+                                                    const c10::List<std::optional<Tensor>>& lengths,
+                                                    at::IntArrayRef table, at::IntArrayRef pooling,
+                                                    at::IntArrayRef exclude, at::IntArrayRef padding_idx,
+                                                    TensorList grads, const Tensor& keys, const Tensor& payload,
+                                                    const Tensor& bag_count, const Tensor& offsets, bool coalesced,
+                                                    bool sort_in_place) {
   if (!weights.empty() && weights[0].is_cuda()) {
-    // ROCm tables: the backward above, called directly (the sort in place,
-    // no padding for exact gradients, their counts read before the
-    // coalescing reduce is queued)
+    // ROCm tables: the backward above, called directly (no padding for exact
+    // gradients, their counts read before the coalescing reduce is queued)
     std::vector<int64_t> host_counts;
     CoalesceResult r = lookup_backward(weights, ids, lengths, table, pooling, exclude, padding_idx, grads, keys,
-                                       payload, bag_count, true, !coalesced, coalesced ? &host_counts : nullptr);
+                                       payload, bag_count, sort_in_place, !coalesced,
+                                       coalesced ? &host_counts : nullptr);
     return weight_grads(weights, r.rows_all, r.vbuf, r.counts, r.layout, coalesced,
                         coalesced ? &host_counts : nullptr);
   }
@@ -1023,6 +1027,16 @@ std::vector<std::optional<Tensor>> grouped_lookup_weight_grads(TensorList weight
   }
   auto lay = coalesced_layout(esz, dims, table_capacities(T, ids, table));
   return weight_grads(weights, rows_all, vbuf, counts, lay, coalesced);
+}
+
+std::vector<std::optional<Tensor>> grouped_lookup_weight_grads(TensorList weights, TensorList ids,
+                                                const c10::List<std::optional<Tensor>>& lengths, at::IntArrayRef table,
+                                                at::IntArrayRef pooling, at::IntArrayRef exclude,
+                                                at::IntArrayRef padding_idx, TensorList grads, const Tensor& keys,
+                                                const Tensor& payload, const Tensor& bag_count, const Tensor& offsets,
+                                                bool coalesced) {
+  return weight_grads_for(weights, ids, lengths, table, pooling, exclude, padding_idx, grads, keys, payload,
+                          bag_count, offsets, coalesced, false);
 }
 
 // The sparse-gradient mode of the modules' backward, set from Python
@@ -1071,10 +1085,10 @@ struct GroupedLookupFn : public torch::autograd::Function<GroupedLookupFn> {
     const std::vector<Tensor> weights = sd["weights"].toTensorVector();
     const std::vector<Tensor> ids = sd["ids"].toTensorVector();
     grads.pop_back();  // err
-    const std::vector<std::optional<Tensor>> wg = grouped_lookup_weight_grads(
+    const std::vector<std::optional<Tensor>> wg = weight_grads_for(
         weights, ids, sd["lengths"].toOptionalTensorList(), sd["table"].toIntVector(), sd["pooling"].toIntVector(),
         sd["exclude"].toIntVector(), sd["padding_idx"].toIntVector(), grads, sd["keys"].toTensor(),
-        sd["payload"].toTensor(), sd["bag_count"].toTensor(), sd["offsets"].toTensor(), g_exact_grads.load());
+        sd["payload"].toTensor(), sd["bag_count"].toTensor(), sd["offsets"].toTensor(), g_exact_grads.load(), true);
     torch::autograd::variable_list out(weights.size() + 6);
     for (size_t t = 0; t < wg.size(); ++t)
       if (wg[t]) out[t] = *wg[t];

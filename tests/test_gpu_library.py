@@ -260,3 +260,28 @@ def test_padded_coalesce_matches_oracle(device):
         got_v = v[t].cpu().numpy()
         np.testing.assert_allclose(got_v[:u], ev, rtol=1e-5, atol=1e-5)
         assert not got_v[u:].any()
+
+
+@pytest.mark.parametrize("grad_mode", ["coalesced", "capacity"])
+def test_public_lookup_backward_leaves_its_outputs_alone(device, grad_mode):
+    """The grouped_lookup op returns its sort keys and payloads; the backward
+    registered on it sorts copies, so the tensors a caller holds keep the
+    forward's values (the modules' own node, whose keys nobody else sees,
+    sorts in place)."""
+
+    prev = mdl_amd.library.sparse_grad_mode()
+    mdl_amd.library.set_sparse_grad_mode(grad_mode)
+    try:
+        torch.manual_seed(4)
+        W = [torch.randn(50, 8, device=device, requires_grad=True), torch.randn(40, 4, device=device,
+                                                                                requires_grad=True)]
+        ids = [torch.randint(0, 50, (30,), device=device), torch.randint(0, 40, (12,), device=device)]
+        lengths = [torch.tensor([3, 0, 9, 18], device=device), None]
+        outs, keys, payload, bag_count, offsets, err = OPS.grouped_lookup(W, ids, lengths, [0, 1], [2, 0], [1, 0],
+                                                                          [0, 0], True)
+        held = (keys.clone(), payload.clone())
+        torch.autograd.backward(outs, [torch.randn_like(o) for o in outs])
+        assert torch.equal(keys, held[0]) and torch.equal(payload, held[1])
+        assert all(w.grad is not None for w in W)
+    finally:
+        mdl_amd.library.set_sparse_grad_mode(prev)
