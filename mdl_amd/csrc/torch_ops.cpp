@@ -963,6 +963,7 @@ std::vector<std::optional<Tensor>> weight_grads(TensorList weights, const Tensor
   drop_dead_records();
   for (int t = 0; t < T; ++t) {
     const Tensor& w = weights[t];
+    if (!w.requires_grad()) continue;  // a frozen table gets no gradient
     const int64_t dim = w.size(1);
     const int64_t n = coalesced ? u[t] : lay.cap[t];
     TORCH_CHECK(n >= 0 && n <= lay.cap[t], "coalesced row count outside its capacity");

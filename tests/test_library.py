@@ -382,6 +382,21 @@ def test_gradients_reach_parameters_as_autograd_delivers_them(grad_mode, device)
         mdl_amd.library.set_sparse_grad_mode(mode)
 
 
+@pytest.mark.parametrize("device", ["cpu", pytest.param("cuda", marks=pytest.mark.gpu)])
+def test_frozen_table_in_a_grouped_lookup_gets_no_gradient(device):
+    """A table with requires_grad=False looked up beside trainable ones gets
+    no gradient; the trainable ones get theirs."""
+
+    a, b = (m.to(device) for m in _modules([("a", 20, 4), ("b", 20, 4)]))
+    b.weight.requires_grad_(False)
+    outs = grouped_sharded_embedding_lookup([(a, torch.tensor([1, 2, 2], device=device)),
+                                             (b, torch.tensor([3, 3], device=device))])
+    torch.autograd.backward(outs, [torch.ones_like(o) for o in outs])
+    assert b.weight.grad is None
+    dense = a.weight.grad.coalesce().to_dense().cpu()
+    assert dense[1].tolist() == [1.0] * 4 and dense[2].tolist() == [2.0] * 4 and float(dense.abs().sum()) == 12.0
+
+
 def test_modules_compile_with_their_gradients(capacity_grads):
     """torch.compile (full graph, AOT autograd) traces the modules' lookups:
     fake tensors take the op's registered autograd, and the compiled step's
